@@ -1,0 +1,361 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-inference hot path on one MI355X.
+
+Headline (`value`): ternary GEMV GB/s on the 6912x2560 I2 layer (2-bit
+weights, int8 per-token-absmax activations, fp32 output).  One step is one
+grouped launch over 64 distinct weight matrices (283 MB, more than the
+256 MB MALL), inputs resident in HBM.  Also measured, reported under
+"secondary": gated delta-net decode (B=32, Hk=16, Hv=32, d=128, fp32 state,
+8 rotating state sets = 512 MiB) in tokens/s, and the 512x4096 bf16
+Walsh-Hadamard rotation in GB/s.
+
+Every kernel time comes from HIP events recorded on the stream the kernels
+run on.  The CPU baseline is the oracle (a C restatement of the reference's
+threaded CPU kernels) on a bounded sample, rank 0 only.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+METRIC = "ternary GEMV GB/s (% HBM peak); gated delta-net decode tokens/sec, 1 GPU"
+
+# Algorithmic bytes per unit (weights + int8 x + x scale + w scale + fp32 y).
+GEMV_OUT, GEMV_IN, GEMV_MATS = 6912, 2560, 64
+GEMV_BYTES = GEMV_OUT * GEMV_IN // 4 + GEMV_IN + 4 + 4 + GEMV_OUT * 4  # 4,453,896
+# GDN decode step: state read+write, q,k bf16, v bf16, gate+beta f32, out f32.
+GDN_B, GDN_HK, GDN_HV, GDN_D, GDN_SETS = 32, 16, 32, 128, 8
+GDN_BYTES = (2 * GDN_B * GDN_HV * GDN_D * GDN_D * 4 + 2 * GDN_B * GDN_HK * GDN_D * 2
+             + GDN_B * GDN_HV * GDN_D * 2 + 2 * GDN_B * GDN_HV * 4 + GDN_B * GDN_HV * GDN_D * 4)
+# FWHT 512 x 4096 bf16 in and out.
+FW_ROWS, FW_N, FW_BUFS = 512, 4096, 32
+FW_BYTES = 2 * FW_ROWS * FW_N * 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    env = os.environ.get("OURO_N_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return min(os.cpu_count() or 1, 16)
+
+
+def time_events(stream, fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn() on `stream`, HIP events around `steps` calls."""
+    from ouroboros_amd.device import Event, synchronize
+
+    for i in range(warmup):
+        fn(i)
+    synchronize(stream)
+    from ouroboros_amd._lib import call
+    call("ouro_device_synchronize")
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    for i in range(steps):
+        fn(warmup + i)
+    e1.record(stream)
+    call("ouro_device_synchronize")
+    return e0.elapsed_ms(e1) / steps
+
+
+def bench_gemv(stream, steps, warmup, orc):
+    from ouroboros_amd import ops
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(1234)
+    tb = ops.i2_tiled_bytes(GEMV_OUT, GEMV_IN)
+    stride = (tb + 4 + 255) // 256 * 256
+    w_all = DeviceBuffer((GEMV_MATS * stride,), np.uint8)
+    n_distinct = 4  # distinct contents, copied to 64 distinct addresses
+    canons, scales = [], []
+    for m in range(n_distinct):
+        codes = rng.integers(0, 3, size=(GEMV_OUT, GEMV_IN), dtype=np.uint8)
+        canon = (codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
+        canons.append(np.ascontiguousarray(canon))
+        scales.append(np.float32(rng.uniform(0.5, 2.0)))
+    payloads = [ops.i2_payload(c, GEMV_OUT, GEMV_IN, float(s)) for c, s in zip(canons, scales)]
+    for m in range(GEMV_MATS):
+        call("ouro_memcpy_dtod", w_all.ptr + m * stride, payloads[m % n_distinct].ptr, tb + 4, None)
+    x = rng.standard_normal((GEMV_MATS, GEMV_IN)).astype(np.float32)
+    xd = DeviceBuffer.from_host(x)
+    xq = DeviceBuffer((GEMV_MATS, GEMV_IN), np.int8)
+    ds = DeviceBuffer((GEMV_MATS,), np.float32)
+    ops.act_quant_i8(xd, GEMV_MATS, GEMV_IN, xq, ds, stream)
+    wsc = DeviceBuffer.from_host(np.array([scales[m % n_distinct] for m in range(GEMV_MATS)], np.float32))
+    y = DeviceBuffer((GEMV_MATS, GEMV_OUT), np.float32)
+    call("ouro_device_synchronize")
+
+    def grouped(_i):
+        call("ouro_gemv_i2_grouped", w_all.ptr, stride, wsc.ptr, xq.ptr, GEMV_IN, ds.ptr, y.ptr,
+             GEMV_OUT, GEMV_OUT, GEMV_IN, GEMV_MATS, stream)
+
+    ms = time_events(stream, grouped, steps, warmup)
+
+    # parity spot check of the timed output (not timed): matrix 0 and 5
+    got = y.download()
+    if orc is not None:
+        xq_h, ds_h = xq.download(), ds.download()
+        for m in (0, 5):
+            _, want = orc.gemm_i2(canons[m % n_distinct], GEMV_OUT, GEMV_IN, xq_h[m:m + 1], ds_h[m:m + 1],
+                                  scales[m % n_distinct])
+            if not np.array_equal(got[m].view(np.uint32), want.view(np.uint32)):
+                raise SystemExit(f"GEMV parity failure on matrix {m}")
+
+    # single-matrix launches back to back (each a different matrix)
+    def single(i):
+        m = i % GEMV_MATS
+        call("ouro_gemm_i2", w_all.ptr + m * stride, GEMV_OUT, GEMV_IN, wsc.ptr + 4 * m,
+             xq.ptr + m * GEMV_IN, ds.ptr + 4 * m, 1, y.ptr + 4 * m * GEMV_OUT, None, stream)
+
+    ms_single = time_events(stream, single, 4 * GEMV_MATS, GEMV_MATS)
+    return ms, ms_single
+
+
+def bench_gdn(stream, steps, warmup):
+    from ouroboros_amd import quant, qwen35
+    from ouroboros_amd._lib import GDN_L2NORM_QK, GDN_SCALE_Q, call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(99)
+    B, Hk, Hv, d = GDN_B, GDN_HK, GDN_HV, GDN_D
+    per = B * Hv * d * d
+    states = DeviceBuffer((GDN_SETS, per), np.float32)
+    init = (0.02 * rng.standard_normal(per)).astype(np.float32)
+    for s in range(GDN_SETS):
+        call("ouro_memcpy_htod", states.ptr + 4 * s * per, init.ctypes.data, 4 * per)
+    q = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((B, Hk, d)).astype(np.float32)))
+    k = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((B, Hk, d)).astype(np.float32)))
+    v = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((B, Hv, d)).astype(np.float32)))
+    beta = DeviceBuffer.from_host((1 / (1 + np.exp(-rng.standard_normal((B, Hv))))).astype(np.float32))
+    gate = DeviceBuffer.from_host((-np.log1p(np.exp(rng.standard_normal((B, Hv))))).astype(np.float32))
+    out = DeviceBuffer((B, Hv, d), np.float32)
+    fl = GDN_L2NORM_QK | GDN_SCALE_Q
+
+    def step(i):
+        s = i % GDN_SETS
+        call("ouro_gdn_decode", states.ptr + 4 * s * per, q.ptr, k.ptr, 1, v.ptr, 1, gate.ptr, beta.ptr,
+             out.ptr, B, Hk, Hv, d, fl, 1e-6, stream)
+
+    return time_events(stream, step, max(steps, 2 * GDN_SETS), warmup)
+
+
+def bench_fwht(stream, steps, warmup):
+    from ouroboros_amd import quant
+    from ouroboros_amd._lib import DT_BF16, call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(7)
+    per = FW_ROWS * FW_N
+    x = rng.standard_normal(per).astype(np.float32)
+    x[rng.random(per) < 0.01] *= 50.0
+    xb = quant.f32_to_bf16_bits(x)
+    src = DeviceBuffer((FW_BUFS, per), np.uint16)
+    dst = DeviceBuffer((FW_BUFS, per), np.uint16)
+    for b in range(FW_BUFS):
+        call("ouro_memcpy_htod", src.ptr + 2 * b * per, xb.ctypes.data, 2 * per)
+
+    def step(i):
+        b = i % FW_BUFS
+        call("ouro_fwht_rows", src.ptr + 2 * b * per, DT_BF16, dst.ptr + 2 * b * per, DT_BF16, FW_ROWS,
+             FW_N, FW_N, None, 0, None, None, stream)
+
+    ms = time_events(stream, step, max(steps, 2 * FW_BUFS), warmup)
+
+    def whole(_i):  # all 32 buffers as one launch of 16384 rows
+        call("ouro_fwht_rows", src.ptr, DT_BF16, dst.ptr, DT_BF16, FW_ROWS * FW_BUFS, FW_N, FW_N, None, 0,
+             None, None, stream)
+
+    ms_all = time_events(stream, whole, max(2, steps // 4), 2)
+    return ms, ms_all
+
+
+def cpu_baseline(orc, budget_s: float = 12.0) -> dict:
+    """The reference's own CPU GEMV (matvec_tl1, SSE4.1 order, row-split
+    threads) on the same 6912x2560 shape in its PTQ1_0 format."""
+    nt = cpu_threads()
+    rng = np.random.default_rng(5)
+    rb = GEMV_IN // 128 * 28
+    payload = rng.integers(0, 256, GEMV_OUT * rb, dtype=np.uint8)
+    g = payload.reshape(-1, 28)
+    d = rng.uniform(0.01, 0.1, g.shape[0]).astype(np.float16).view(np.uint16)
+    g[:, 26], g[:, 27] = d & 0xFF, d >> 8
+    x = rng.standard_normal(GEMV_IN).astype(np.float32)
+    orc.matvec_tl1(payload, GEMV_OUT, GEMV_IN, x, simd=1, nthreads=nt)  # warm
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s and n < 2000:
+        orc.matvec_tl1(payload, GEMV_OUT, GEMV_IN, x, simd=1, nthreads=nt)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    tl1_bytes = payload.nbytes + GEMV_IN * 4 + GEMV_OUT * 4
+    # I2 oracle on the headline format, for reference (scalar C, same threads)
+    codes = rng.integers(0, 3, size=(GEMV_OUT, GEMV_IN), dtype=np.uint8)
+    canon = np.ascontiguousarray(codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
+    xq, ds = orc.act_quant_i8(x[None])
+    t1 = time.perf_counter()
+    m = 0
+    while time.perf_counter() - t1 < budget_s / 4 and m < 200:
+        orc.gemm_i2(canon, GEMV_OUT, GEMV_IN, xq, ds, 1.0, nthreads=nt)
+        m += 1
+    dt_i2 = (time.perf_counter() - t1) / m
+    return {
+        "value": round(tl1_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": nt,
+        "kind": "port",
+        "sample": (f"{n} calls of the oracle's matvec_tl1 (SSE4.1 order, {nt} row-split threads) on one "
+                   f"6912x2560 PTQ1_0 matrix ({tl1_bytes} B per call), {dt * 1e3:.2f} ms/call; the int8 x 2-bit "
+                   f"oracle (scalar C) ran {GEMV_BYTES / dt_i2 / 1e9:.3f} GB/s ({dt_i2 * 1e3:.2f} ms/call, {m} calls)"),
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def gdn_cpu_baseline(orc, budget_s: float = 6.0) -> dict:
+    nt = cpu_threads()
+    rng = np.random.default_rng(3)
+    B, Hk, Hv, d = GDN_B, GDN_HK, GDN_HV, GDN_D
+    state = (0.02 * rng.standard_normal((B, Hv, d * d))).astype(np.float32)
+    q = rng.standard_normal((B, Hk, d)).astype(np.float32)
+    k = rng.standard_normal((B, Hk, d)).astype(np.float32)
+    v = rng.standard_normal((B, Hv, d)).astype(np.float32)
+    gate = -np.log1p(np.exp(rng.standard_normal((B, Hv)))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, Hv))))).astype(np.float32)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s and n < 500:
+        orc.gdn_decode(state, q, k, v, gate, beta, B, Hk, Hv, d, orc.L2NORM_QK | orc.SCALE_Q, 1e-6, nt)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(B / dt, 1), "unit": "tokens/s", "cores": nt, "kind": "port",
+            "sample": f"{n} decode steps of the oracle's delta_head_dim loop over 32x32 heads, {dt * 1e3:.2f} ms/step"}
+
+
+def load_traffic() -> dict:
+    f = ROOT / "profiles" / "pmc_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text())
+        except (OSError, ValueError):
+            return {}
+    return {}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["gemv", "gdn", "fwht"], default=None,
+                    help="run one workload (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the workloads would shard by output rows / heads with no exchange).", file=sys.stderr)
+        return 2
+
+    from ouroboros_amd import _lib
+    from ouroboros_amd.device import Stream
+
+    _lib.init()
+    stream = Stream().handle
+    orc = None
+    if not args.no_cpu:
+        import oracle as orc  # the CPU baseline / parity checker only
+
+    res = {}
+    if args.only in (None, "gemv"):
+        log("GEMV 6912x2560 x 64 matrices")
+        ms, ms_single = bench_gemv(stream, args.steps, args.warmup, orc)
+        res["gemv"] = (ms, ms_single)
+    if args.only in (None, "gdn"):
+        log("GDN decode B=32")
+        res["gdn"] = bench_gdn(stream, args.steps, args.warmup)
+    if args.only in (None, "fwht"):
+        log("FWHT 512x4096 bf16")
+        res["fwht"] = bench_fwht(stream, args.steps, args.warmup)
+
+    traffic = load_traffic()
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+    sec = {}
+    if "gemv" in res:
+        ms, ms_single = res["gemv"]
+        bytes_launch = GEMV_BYTES * GEMV_MATS
+        gbs = bytes_launch / (ms * 1e-3) / 1e9
+        out.update({
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4), "dtype": "int8",
+            "config": {"workload": "ternary GEMV 6912x2560, 2-bit weights x int8 absmax activations -> fp32, "
+                                   "64 distinct matrices per step (one grouped launch)",
+                       "out_len": GEMV_OUT, "in_len": GEMV_IN, "matrices_per_step": GEMV_MATS,
+                       "bytes_per_matrix": GEMV_BYTES},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("i2_gemv_kernel")},
+            "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "single_matrix_launch_us": round(ms_single * 1e3, 2),
+            "single_matrix_GBs": round(GEMV_BYTES / (ms_single * 1e-3) / 1e9, 1),
+        })
+    else:
+        out.update({"value": None, "unit": "GB/s"})
+    if "gdn" in res:
+        ms = res["gdn"]
+        gbs = GDN_BYTES / (ms * 1e-3) / 1e9
+        sec["gdn_decode"] = {
+            "value": round(GDN_B / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "config": "B=32 seqs, Hk=16, Hv=32, d=128, fp32 state, bf16 q/k/v, 8 rotating state sets",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("gdn_decode_kernel")},
+            "bytes_per_step": GDN_BYTES,
+        }
+    if "fwht" in res:
+        ms, ms_all = res["fwht"]
+        gbs = FW_BYTES / (ms * 1e-3) / 1e9
+        gbs_all = FW_BYTES * FW_BUFS / (ms_all * 1e-3) / 1e9
+        sec["fwht"] = {
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4),
+            "config": "512x4096 bf16 in/out, block 4096, scale 1/64, 32 rotating buffers",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("fwht_row_kernel")},
+            "streaming_16384_rows_GBs": round(gbs_all, 1),
+            "bytes_per_call": FW_BYTES,
+        }
+    if orc is not None:
+        log("CPU baseline")
+        if "gemv" in res:
+            out["cpu_baseline"] = cpu_baseline(orc)
+        if "gdn" in res:
+            sec.setdefault("gdn_decode", {})["cpu_baseline"] = gdn_cpu_baseline(orc)
+    out["secondary"] = sec
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

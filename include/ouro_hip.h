@@ -1,0 +1,263 @@
+/*
+ * ouro_hip.h - C ABI of the MI355X (gfx950) quantized-inference hot path.
+ *
+ * This is the drop-in boundary for the kernel-call surface of OuroborOS's
+ * Rust engine (cluster/src/infer/).  Every entry point below names the
+ * reference function it replaces (file:line in the reference tree).  All
+ * compute entry points work on DEVICE buffers owned by the caller, are
+ * stream-ordered (asynchronous w.r.t. the host) and never allocate device
+ * memory, except the documented workspace users (ouro_matvec_q /
+ * ouro_matmul_q for the I2 kind), which take memory from a per-device
+ * library workspace that is grown on first use and kept until
+ * ouro_shutdown().
+ *
+ * Conventions
+ *  - Return value: OURO_OK (0) or an ouro_status code.  The failing call's
+ *    message is kept in a thread-local buffer, read with ouro_last_error().
+ *    No entry point aborts the process (the reference's assert!/bail! paths,
+ *    e.g. infer/mod.rs:139-145, hadamard.rs:33-37, become status codes).
+ *  - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *  - Shapes are checked on the host before any launch; a kernel is never
+ *    launched on a shape it does not handle.
+ *  - Element (i, j) of a delta-net state head is at i + j*d, i.e. the k
+ *    dimension is contiguous (qwen35.rs:19-20).
+ *  - Matrices are row-major W[out_len][in_len], y = W x (ops.rs:1-4).
+ */
+#ifndef OURO_HIP_H
+#define OURO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OURO_ABI_VERSION 1
+
+typedef enum ouro_status {
+    OURO_OK = 0,
+    OURO_ERR_INVALID_ARG = 1, /* NULL pointer, zero size, bad flag */
+    OURO_ERR_SHAPE = 2,       /* shape the entry point does not support */
+    OURO_ERR_ALIGN = 3,       /* pointer not aligned as documented */
+    OURO_ERR_KIND = 4,        /* quant kind not supported by this entry */
+    OURO_ERR_NO_DEVICE = 5,   /* no HIP device, or init failed */
+    OURO_ERR_HIP = 6,         /* a HIP runtime call failed */
+    OURO_ERR_NOT_INIT = 7,    /* ouro_init() was not called */
+} ouro_status;
+
+/* Quant kinds.  The ggml dtype ids of QuantKind::from_dtype
+ * (dequant.rs:334-348) are kept as the numeric values. */
+enum {
+    OURO_KIND_F32 = 0,
+    OURO_KIND_F16 = 1,
+    OURO_KIND_BF16 = 30,
+    OURO_KIND_TQ1_0 = 34,  /* 54 B / 256 weights, base-3 (dequant.rs:49-105) */
+    OURO_KIND_TL1 = 143,   /* PTQ1_0, 28 B / 128 weights (dequant.rs:124-195) */
+    /* 2-bit ternary codes in the device-tiled layout below, followed by one
+     * little-endian fp32 per-tensor scale (the BitNet convention of a scale
+     * appended at the end of the tensor, dequant.rs:8-11).  No reference
+     * kind: this is the int8-activation x 2-bit format of bitnet.cpp. */
+    OURO_KIND_I2 = 0x4932,
+};
+
+/* Element dtypes for activation buffers. */
+enum { OURO_DT_F32 = 0, OURO_DT_BF16 = 1 };
+
+/* ------------------------------------------------------------------ */
+/* Runtime                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Select and initialise a device.  device < 0 picks OURO_GPU_INDEX from the
+ * environment, else 0 (the reference's GPU pick, ouro-wgpu/src/lib.rs:219-248).
+ * Safe to call again; it re-selects the device. */
+int ouro_init(int device);
+/* Releases the library workspaces.  Caller buffers are never touched. */
+int ouro_shutdown(void);
+const char *ouro_last_error(void);
+int ouro_abi_version(void);
+int ouro_device_count(int *count);
+/* Device name of the initialised device (e.g. "gfx950"). */
+int ouro_device_arch(char *buf, size_t len);
+
+/* Device memory and stream plumbing for callers that have no other HIP
+ * runtime at hand (tests, benches, FFI hosts).  Thin wrappers over HIP. */
+int ouro_malloc(void **ptr, size_t bytes);
+int ouro_free(void *ptr);
+int ouro_memcpy_htod(void *dst, const void *src, size_t bytes);
+int ouro_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int ouro_memcpy_dtod(void *dst, const void *src, size_t bytes, void *stream);
+int ouro_memset(void *dst, int value, size_t bytes, void *stream);
+int ouro_stream_create(void **stream);
+int ouro_stream_destroy(void *stream);
+int ouro_stream_synchronize(void *stream);
+int ouro_device_synchronize(void);
+int ouro_event_create(void **event);
+int ouro_event_destroy(void *event);
+int ouro_event_record(void *event, void *stream);
+int ouro_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* ------------------------------------------------------------------ */
+/* Ternary GEMV / GEMM: int8 per-token-absmax activations x 2-bit      */
+/* ternary weights (the I2 format), exact int32 accumulation.          */
+/* ------------------------------------------------------------------ */
+/*
+ * Canonical I2 bytes (host / on disk): row r is in_len/4 bytes; weight k of
+ * the row sits in byte k/4 at bits 2*(k%4)..2*(k%4)+1 as code = w + 1,
+ * w in {-1, 0, +1}.  Decoding is w = code - 1.
+ *
+ * Device-tiled I2 (what the kernels read; ouro_i2_tile() produces it):
+ *   G = in_len / 256 four-weight groups per lane per row (in_len % 256 == 0),
+ *   R = 16 / gcd(G, 16) rows per tile, tiles = ceil(out_len / R) (rows past
+ *   out_len hold code 1, i.e. w = 0, and are never written out).  Tile t
+ *   starts at byte
+ *   t * R * in_len / 4.  Inside a tile, lane l (0..63) owns the k-range
+ *   [4*G*l, 4*G*(l+1)) of all R rows; its 32-bit word d (0 .. R*G/4 - 1)
+ *   sits at byte (d/4)*1024 + l*16 + (d%4)*4, so every 16-byte load of a
+ *   64-lane wavefront is one contiguous 1 KiB segment.  Word d carries four
+ *   groups gi = 4d + f (f = 0..3); group gi is row r = gi / G, k-group
+ *   g = gi % G, i.e. weights k = 4*G*l + 4*g + b (b = 0..3), whose codes sit
+ *   at bits 8*b + 2*f of the word.
+ *
+ * Activation quantisation (per row of n values, one row per token):
+ *   amax = max|x|; if amax == 0: q = 0, dscale = 0;
+ *   else s = 127.0f / amax, q = clamp(rintf(x * s), -127, 127),
+ *        dscale = amax / 127.0f.
+ * Output: y = ((float)acc * dscale) * w_scale, acc = sum_k w*q (int32), with
+ * both products rounded separately (no fused multiply-add).
+ */
+
+/* Size in bytes of the device-tiled codes (without the trailing scale). */
+size_t ouro_i2_tiled_bytes(size_t out_len, size_t in_len);
+/* canonical (device) -> tiled (device).  in_len % 256 == 0.  When
+ * w_scale_or_null is given, the fp32 scale is written right after the
+ * tiled codes, making `tiled` a complete OURO_KIND_I2 payload. */
+int ouro_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
+                 uint8_t *tiled, const float *w_scale_or_null, void *stream);
+/* Per-row absmax int8 quantisation of rows x n activations (f32 or bf16). */
+int ouro_act_quant_i8(const void *x, int x_dtype, size_t rows, size_t n,
+                      int8_t *xq, float *dscale, void *stream);
+/* y[c*out_len + r] for ncols activation columns (xq row-major [ncols][in]),
+ * column-major output like matmul_q (ops.rs:160-161).  acc_or_null, when
+ * given, receives the exact int32 accumulators in the same layout.
+ * w_scale is read from the device (4 bytes), e.g. the payload tail. */
+int ouro_gemm_i2(const uint8_t *w_tiled, size_t out_len, size_t in_len,
+                 const float *w_scale, const int8_t *xq, const float *dscale,
+                 size_t ncols, float *y, int32_t *acc_or_null, void *stream);
+/* Grouped launch over `count` independent (weight, activation, output)
+ * triples of one shape, laid out at fixed strides (bytes / elements):
+ * matrix m uses w_tiled + m*w_stride, w_scale[m], xq + m*x_stride,
+ * dscale[m], y + m*y_stride.  One column each.  This is the shape of the
+ * projections that share a step but not a matrix (e.g. all layers' weight
+ * streams of one decode step handed to the GPU at once). */
+int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride,
+                         const float *w_scale, const int8_t *xq,
+                         size_t x_stride, const float *dscale, float *y,
+                         size_t y_stride, size_t out_len, size_t in_len,
+                         size_t count, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Reference matvec surface                                             */
+/* ------------------------------------------------------------------ */
+
+/* matvec_q (ops.rs:76-84): y = W x, x f32[in_len], y f32[out_len], W the
+ * device payload of `kind`:
+ *   OURO_KIND_TL1   - PTQ1_0 groups (fused decode + dot, ops.rs:294-363)
+ *   OURO_KIND_TQ1_0 - TQ1_0 blocks (matvec_qblock, ops.rs:101-128)
+ *   OURO_KIND_F32 / F16 / BF16 - dense rows (ops.rs:87-98,131-154,600-623)
+ *   OURO_KIND_I2    - tiled I2 + scale; x is quantised per call into the
+ *                     library workspace (int8 absmax, see above).
+ * Floating-point sums are not in the reference's order; results agree to
+ * float32 rounding (the reference's own fused-vs-scalar bar is rel 1e-5,
+ * ops.rs:800-838). */
+int ouro_matvec_q(const void *payload, int kind, size_t out_len,
+                  size_t in_len, const float *x, float *y, void *stream);
+/* matmul_q (ops.rs:219-230): x row-major [k][in_len], y column-major
+ * y[c*out_len + r] (ops.rs:160-161). */
+int ouro_matmul_q(const void *payload, int kind, size_t out_len,
+                  size_t in_len, const float *x, size_t k, float *y,
+                  void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Walsh-Hadamard rotation                                              */
+/* ------------------------------------------------------------------ */
+
+#define OURO_FWHT_INVERSE 1u /* rotate_inv: h = s o (H z)/sqrt(N) */
+
+/* Row-batched rotate_fwd / rotate_inv (hadamard.rs:41-66): each of `rows`
+ * rows of n elements is rotated in blocks of `block` (power of two,
+ * 2..8192, n % block == 0).  signs: NULL (all +1) or f32[n], +-1 each.
+ * The fp32 result is bit-identical to the reference: same butterfly stages
+ * in the same order (hadamard.rs:15-31), same scale 1/sqrtf(block).
+ * x and y may alias.  Either dtype on either side; bf16 output is rounded
+ * to nearest-even.  When xq/dscale are non-NULL, each row of the output
+ * (as stored, i.e. after bf16 rounding) is also int8-absmax-quantised as
+ * ouro_act_quant_i8 does (the fused FWHT -> quantisation epilogue);
+ * y may then be NULL to skip storing the rotated activations. */
+int ouro_fwht_rows(const void *x, int x_dtype, void *y, int y_dtype,
+                   size_t rows, size_t n, size_t block, const float *signs,
+                   unsigned flags, int8_t *xq, float *dscale, void *stream);
+/* Exact mirrors of hadamard::rotate_fwd / rotate_inv (hadamard.rs:41,57)
+ * on one f32 device vector, in place. */
+int ouro_rotate_fwd(float *x, const float *signs, size_t n, size_t block,
+                    void *stream);
+int ouro_rotate_inv(float *x, const float *signs, size_t n, size_t block,
+                    void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Gated delta-net                                                      */
+/* ------------------------------------------------------------------ */
+
+#define OURO_GDN_L2NORM_QK 1u /* l2_norm q,k per head (qwen35.rs:73-79,1101-1102) */
+#define OURO_GDN_SCALE_Q   2u /* q *= 1/sqrt(d) after the norm (qwen35.rs:1095,1107) */
+#define OURO_GDN_KHEAD_DIV 4u /* k-head = v/(Hv/Hk); default v % Hk (qwen35.rs:1098) */
+
+/* delta_head_dim (qwen35.rs:27-57) for one head, in place on the device:
+ * decay = exp(gate); sk = decay * S^T k; dv = beta (v - sk);
+ * S = decay S + k dv^T; out = S^T q.  sdim == 128; q is pre-scaled. */
+int ouro_delta_head_dim(float *state, size_t sdim, const float *q,
+                        const float *k, const float *v, float gate,
+                        float beta, float *out, void *stream);
+
+/* One decode step for B sequences x Hv v-heads (run_delta's per-head loop,
+ * qwen35.rs:1096-1112, with the recurrence of qwen35.rs:27-57).
+ *   q, k   : [B][Hk][d], dtype qk_dtype (raw; normalised per flags)
+ *   v      : [B][Hv][d], dtype v_dtype
+ *   gate   : [B][Hv] f32 log-decay (decay = exp(gate)); beta: [B][Hv] f32
+ *   state  : [B][Hv][d][d] f32, element (i,j) of a head at i + j*d; updated
+ *   out    : [B][Hv][d] f32
+ * d == 128, Hv % Hk == 0.  eps is the l2_norm epsilon (outside the sqrt). */
+int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype,
+                    const void *v, int v_dtype, const float *gate,
+                    const float *beta, float *out, size_t B, size_t Hk,
+                    size_t Hv, size_t d, unsigned flags, float eps,
+                    void *stream);
+
+/* ------------------------------------------------------------------ */
+/* Resident weights (GpuPool::upload_q6k / matvec, ouro-wgpu/src/lib.rs:   */
+/* 251-356): upload once, repacking on upload, then matvec by handle.    */
+/* ------------------------------------------------------------------ */
+
+typedef struct ouro_weight *ouro_weight_t;
+
+/* Upload `bytes` host bytes of a `kind` tensor [out_len][in_len].  For
+ * OURO_KIND_I2, `host` holds canonical I2 codes (out_len*in_len/4 bytes)
+ * and w_scale is the per-tensor scale; the upload tiles them.  For the
+ * other kinds host holds the reference payload (row_bytes*out_len bytes)
+ * and w_scale is ignored.  max_cols sizes the handle's own activation
+ * scratch (for matmul up to max_cols columns). */
+int ouro_weight_upload(int kind, const void *host, size_t bytes,
+                       size_t out_len, size_t in_len, float w_scale,
+                       size_t max_cols, ouro_weight_t *out);
+int ouro_weight_free(ouro_weight_t w);
+/* Device payload of a handle (what ouro_matvec_q takes for its kind). */
+const void *ouro_weight_payload(ouro_weight_t w);
+int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y,
+                       void *stream);
+int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y,
+                       void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OURO_HIP_H */

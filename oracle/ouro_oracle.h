@@ -1,0 +1,172 @@
+/*
+ * ouro_oracle.h - CPU oracle for the quantized-inference hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
+ * CPU arithmetic (Rust, cluster/src/infer/{dequant,ops,hadamard,qwen35}.rs)
+ * used as the parity checker by tests/, by __graft_entry__.smoke() and by the
+ * cpu_baseline leg of bench.py.  The shipped product (libouro_hip.so) never
+ * links, loads or calls anything in this directory.
+ *
+ * Every function cites the reference file:line it follows.  Functions that
+ * implement the int8-activation x 2-bit ternary ("I2") format have no
+ * counterpart in the reference tree (that format lives only in the absent
+ * bitnet-cpp submodule); they implement the closed-form definition written in
+ * ouro_hip.h and are pinned by closed forms and brute force in tests/.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; Rust never contracts
+ * a*b+c, so neither may the oracle).
+ */
+#ifndef OURO_ORACLE_H
+#define OURO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- dequant.rs ------------------------------------------------------- */
+
+/* Quant kinds, same set and ggml dtype ids as QuantKind (dequant.rs:315-348). */
+enum {
+    ORC_KIND_F32 = 0,
+    ORC_KIND_F16 = 1,
+    ORC_KIND_BF16 = 30,
+    ORC_KIND_Q8_0 = 8,
+    ORC_KIND_Q3K = 11,
+    ORC_KIND_Q4K = 12,
+    ORC_KIND_Q5K = 13,
+    ORC_KIND_Q6K = 14,
+    ORC_KIND_TQ1_0 = 34,
+    ORC_KIND_TL1 = 143,
+    /* not a reference kind: 2-bit ternary codes, per-tensor scale */
+    ORC_KIND_I2 = 0x4932,
+};
+
+float orc_f16_to_f32(uint16_t bits);                  /* dequant.rs:21-47 */
+float orc_bf16_to_f32(uint16_t bits);                 /* dequant.rs:197-199 */
+uint16_t orc_f32_to_bf16_rne(float x);                /* round-to-nearest-even */
+void orc_tl1_group(const uint8_t *g28, float *out128); /* dequant.rs:146-171 */
+void orc_dequant_tl1_row(const uint8_t *payload, size_t row, size_t row_elems,
+                         float *out);                  /* dequant.rs:185-195 */
+void orc_tq1_block(const uint8_t *b54, float *out256); /* dequant.rs:50-80 */
+void orc_dequant_tq1_row(const uint8_t *payload, size_t row, size_t row_bytes,
+                         float *out);                  /* dequant.rs:96-105 */
+/* QuantKind::row_bytes (dequant.rs:376-387); 0 for an unknown kind. */
+size_t orc_row_bytes(int kind, size_t k);
+/* QuantKind::from_dtype (dequant.rs:334-348): 1 if supported, else 0. */
+int orc_kind_supported(uint32_t dtype);
+
+/* ---- ops.rs ------------------------------------------------------------ */
+
+float orc_dot(const float *a, const float *b, size_t n); /* ops.rs:53-60 */
+
+/* matvec_tl1 (ops.rs:294-321).  simd=0 follows tl1_rows_scalar
+ * (ops.rs:324-363), simd=1 follows the SSE4.1 tl1_rows_avx2 summation order
+ * (ops.rs:499-584).  nthreads<=0 means OURO_N_THREADS or all cores
+ * (mt_threads, ops.rs:62-73). */
+void orc_matvec_tl1(const uint8_t *payload, size_t out_len, size_t in_len,
+                    const float *x, float *y, int simd, int nthreads);
+/* matmul_tl1 (ops.rs:162-215): x row-major [k][in_len], y column-major
+ * y[c*out_len + r].  simd selects tl1_rows_scalar_k (ops.rs:244-286) or
+ * tl1_rows_avx2_k (ops.rs:381-473). */
+void orc_matmul_tl1(const uint8_t *payload, size_t out_len, size_t in_len,
+                    const float *x, size_t k, float *y, int simd, int nthreads);
+/* matvec_qblock for TQ1_0 (ops.rs:101-128): dequant row, then dot. */
+void orc_matvec_tq1(const uint8_t *payload, size_t out_len, size_t in_len,
+                    const float *x, float *y, int nthreads);
+/* matvec_f32raw / matvec_f16 / matvec_bf16 (ops.rs:87-98,131-154,600-623). */
+void orc_matvec_dense(const uint8_t *payload, int kind, size_t out_len,
+                      size_t in_len, const float *x, float *y);
+/* matvec_q dispatch (ops.rs:76-84) over the kinds above.  Returns 0, or -1
+ * for a kind this oracle does not restate. */
+int orc_matvec_q(const uint8_t *payload, int kind, size_t out_len,
+                 size_t in_len, const float *x, float *y, int nthreads);
+/* matmul_q (ops.rs:219-230): TL1 fused K-column, else K matvecs. */
+int orc_matmul_q(const uint8_t *payload, int kind, size_t out_len,
+                 size_t in_len, const float *x, size_t k, float *y,
+                 int nthreads);
+
+/* ---- I2: int8 per-token absmax activations x 2-bit ternary ------------- */
+
+/* Canonical I2 packing: row r is in_len/4 bytes; element k sits in byte k/4
+ * at bits 2*(k%4)..2*(k%4)+1 as code = w + 1.  w in {-1,0,1}.
+ * Returns -1 if a weight is outside {-1,0,1} or in_len % 4 != 0. */
+int orc_i2_pack(const int8_t *w, size_t out_len, size_t in_len, uint8_t *packed);
+/* Decode: w = code - 1 (code 3, never produced by the packer, decodes to 2). */
+void orc_i2_unpack(const uint8_t *packed, size_t out_len, size_t in_len,
+                   int8_t *w);
+/* Device-tiled I2 layout (ouro_hip.h): G = in_len/256, R = 16/gcd(G,16),
+ * tiles = ceil(out_len/R); padding rows hold code 1.  Returns the byte count
+ * written (0 if in_len % 256 != 0).  `tiled` must hold that many bytes. */
+size_t orc_i2_tiled_bytes(size_t out_len, size_t in_len);
+size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
+                   uint8_t *tiled);
+/* Per-row absmax int8 quantization of `rows` rows of n floats:
+ *   amax = max|x|; amax == 0 -> q = 0, dscale = 0;
+ *   s = 127.0f / amax; q = clamp(rintf(x*s), -127, 127); dscale = amax/127.0f */
+void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
+                      float *dscale);
+/* y[c*out_len + r] = ((float)acc * dscale[c]) * w_scale,
+ * acc = sum_k w[r][k] * xq[c][k] (exact int32).  acc may be NULL. */
+void orc_gemm_i2(const uint8_t *packed, size_t out_len, size_t in_len,
+                 const int8_t *xq, const float *dscale, size_t ncols,
+                 float w_scale, int32_t *acc, float *y, int nthreads);
+
+/* ---- hadamard.rs ------------------------------------------------------- */
+
+void orc_wht_inplace(float *x, size_t n);              /* hadamard.rs:15-31 */
+/* rotate_fwd / rotate_inv (hadamard.rs:41-66); check_args (33-37) failures
+ * return -1 instead of panicking. */
+int orc_rotate_fwd(float *x, const float *signs, size_t n, size_t block);
+int orc_rotate_inv(float *x, const float *signs, size_t n, size_t block);
+/* rows x n helper, rows split across threads (one rotate call per row). */
+int orc_rotate_rows(float *x, const float *signs, size_t rows, size_t n,
+                    size_t block, int inverse, int nthreads);
+
+/* ---- qwen35.rs --------------------------------------------------------- */
+
+/* delta_head_dim (qwen35.rs:27-57); state element (i,j) at i + j*sdim. */
+void orc_delta_head_dim(float *state, size_t sdim, const float *q,
+                        const float *k, const float *v, float gate, float beta,
+                        float *out);
+void orc_l2_norm(float *v, size_t n, float eps);       /* qwen35.rs:73-79 */
+float orc_softplus(float x);                           /* qwen35.rs:1241-1243 */
+float orc_sigmoid(float x);                            /* qwen35.rs:1067 */
+float orc_silu(float x);                               /* ops.rs:34-36 */
+float orc_conv_step(float ring[3], const float w[4], float x); /* qwen35.rs:64-70 */
+void orc_gated_norm_rms(const float *x, const float *w, const float *gate,
+                        size_t n, float eps, float *y); /* qwen35.rs:82-92 */
+float orc_delta_q_scale(size_t d);                     /* qwen35.rs:108-110 */
+
+/* Flags shared with ouro_hip.h (same values). */
+#define ORC_GDN_L2NORM_QK   1u  /* l2_norm q and k per head (qwen35.rs:1101-1102) */
+#define ORC_GDN_SCALE_Q     2u  /* q *= 1/sqrt(d) after the norm (qwen35.rs:1107) */
+#define ORC_GDN_KHEAD_DIV   4u  /* k-head = v / (Hv/Hk) instead of v % Hk (qwen35.rs:1098) */
+
+/* Batched decode step: the per-v-head loop of run_delta
+ * (qwen35.rs:1096-1112) over B sequences.  Layouts:
+ *   q,k [B][Hk][d] f32 (raw, e.g. bf16-decoded); v [B][Hv][d];
+ *   gate, beta [B][Hv] (gate is the log-decay: decay = exp(gate));
+ *   state [B][Hv][d*d] (element (i,j) at i + j*d); out [B][Hv][d]. */
+void orc_gdn_decode(float *state, const float *q, const float *k,
+                    const float *v, const float *gate, const float *beta,
+                    float *out, size_t B, size_t Hk, size_t Hv, size_t d,
+                    unsigned flags, float eps, int nthreads);
+/* Token-by-token prefill (the reference prefill, shell/src/bonsai.rs:48-52
+ * driving run_delta): T tokens of one sequence, q,k [T][Hk][d], v [T][Hv][d],
+ * gate, beta [T][Hv], out [T][Hv][d]; state [Hv][d*d] updated in place. */
+void orc_gdn_prefill_tokens(float *state, const float *q, const float *k,
+                            const float *v, const float *gate,
+                            const float *beta, float *out, size_t T,
+                            size_t Hk, size_t Hv, size_t d, unsigned flags,
+                            float eps, int nthreads);
+
+/* OURO_N_THREADS or all logical cores (ops.rs:62-73). */
+int orc_mt_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,202 @@
+// gdn_decode.hip - gated delta-net recurrent decode step on the GPU.
+//
+// Follows delta_head_dim (qwen35.rs:27-57) per (sequence, v-head) with the
+// per-head preprocessing of run_delta (qwen35.rs:1096-1112):
+//   decay = exp(gate); sk = decay * S^T k; dv = beta * (v - sk);
+//   S' = decay * S + k dv^T; out = S'^T q.
+// With S(i, j) at i + j*d, output column j touches only column j of S, so
+// the state is split by columns: a 64-lane wavefront owns 16 columns, lanes
+// 0-31 walking one column of each pair and lanes 32-63 the other, four k
+// values per lane.  Each wavefront issues all of its state loads up front
+// (16 columns x 512 B), reduces S^T k across its 32-lane halves with a
+// reduce-scatter, broadcasts dv, updates the columns in registers, writes
+// them back and reduces S'^T q.  The state makes exactly one HBM round trip.
+#include "common.hpp"
+
+namespace ouro {
+namespace {
+
+constexpr int kD = 128;          // d_state of the qwen35 family (qwen35.rs:8)
+constexpr int kColsPerWave = 16;
+constexpr int kWavesPerBlock = 4;
+constexpr int kColsPerBlock = kColsPerWave * kWavesPerBlock;
+constexpr int kPairs = kColsPerWave / 2;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct DecodeArgs {
+    float *state;
+    const void *q, *k, *v;
+    const float *gate, *beta;  // NULL: use gate_s / beta_s for every head
+    float gate_s, beta_s;
+    float *out;
+    int B, Hk, Hv;
+    unsigned flags;
+    float eps;
+};
+
+template <typename T>
+__device__ __forceinline__ float4 ld4(const T *p);
+template <>
+__device__ __forceinline__ float4 ld4<float>(const float *p) {
+    return *reinterpret_cast<const float4 *>(p);
+}
+template <>
+__device__ __forceinline__ float4 ld4<uint16_t>(const uint16_t *p) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                       __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+template <typename T>
+__device__ __forceinline__ float ld1(const T *p);
+template <>
+__device__ __forceinline__ float ld1<float>(const float *p) { return *p; }
+template <>
+__device__ __forceinline__ float ld1<uint16_t>(const uint16_t *p) { return bf16_bits_to_f32(*p); }
+
+__device__ __forceinline__ float sum_half(float v) {  // over the 32 lanes of a half
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) v += xor_shfl(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
+    return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+template <typename TQK, typename TV>
+__global__ __launch_bounds__(64 * kWavesPerBlock) void gdn_decode_kernel(DecodeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int half = lane >> 5;
+    const int i0 = 4 * (lane & 31);
+    const int bh = blockIdx.x;  // b * Hv + h
+    const int b = bh / a.Hv, h = bh % a.Hv;
+    const int kh = (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
+    const int col0 = blockIdx.y * kColsPerBlock + wave * kColsPerWave;
+
+    float *S = a.state + static_cast<long long>(bh) * kD * kD;
+    // State columns first: they are the bytes that matter.
+    float4 s[kPairs];
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+        const f32x4 t = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4 *>(S + (col0 + 2 * p + half) * kD + i0));
+        s[p] = make_float4(t[0], t[1], t[2], t[3]);
+    }
+
+    const long long qk_off = (static_cast<long long>(b) * a.Hk + kh) * kD + i0;
+    float4 k = ld4(static_cast<const TQK *>(a.k) + qk_off);
+    float4 q = ld4(static_cast<const TQK *>(a.q) + qk_off);
+    const float gate = a.gate ? a.gate[bh] : a.gate_s;
+    const float beta = a.beta ? a.beta[bh] : a.beta_s;
+    if (a.flags & OURO_GDN_L2NORM_QK) {  // l2_norm: 1 / (sqrt(sum) + eps)
+        const float ik = 1.0f / (sqrtf(sum_half(dot4(k, k))) + a.eps);
+        const float iq = 1.0f / (sqrtf(sum_half(dot4(q, q))) + a.eps);
+        k = make_float4(k.x * ik, k.y * ik, k.z * ik, k.w * ik);
+        q = make_float4(q.x * iq, q.y * iq, q.z * iq, q.w * iq);
+    }
+    if (a.flags & OURO_GDN_SCALE_Q) {
+        const float sc = 1.0f / sqrtf(static_cast<float>(kD));
+        q = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
+    }
+    const float decay = expf(gate);
+
+    // sk for the 16 columns: reduce-scatter over each 32-lane half.
+    float part[kPairs];
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) part[p] = dot4(s[p], k);
+    const float skj = reduce_scatter<kPairs, 32>(part, lane) * decay;
+    // This lane now holds column pair (lane & 31) / 4 of its half.
+    const int myp = (lane & 31) >> 2;
+    const int myj = col0 + 2 * myp + half;
+    const float vj = ld1(static_cast<const TV *>(a.v) + static_cast<long long>(bh) * kD + myj);
+    const float dj = beta * (vj - skj);
+
+    float o[kPairs];
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+        const float dp = __shfl(dj, (half << 5) + 4 * p, 64);
+        float4 t;
+        t.x = s[p].x * decay + k.x * dp;
+        t.y = s[p].y * decay + k.y * dp;
+        t.z = s[p].z * decay + k.z * dp;
+        t.w = s[p].w * decay + k.w * dp;
+        const f32x4 tv = {t.x, t.y, t.z, t.w};
+        __builtin_nontemporal_store(tv, reinterpret_cast<f32x4 *>(S + (col0 + 2 * p + half) * kD + i0));
+        o[p] = dot4(t, q);
+    }
+    const float oj = reduce_scatter<kPairs, 32>(o, lane);
+    if ((lane & 3) == 0) a.out[static_cast<long long>(bh) * kD + myj] = oj;
+}
+
+template <typename TQK, typename TV>
+int launch(const DecodeArgs &a, hipStream_t s) {
+    dim3 grid(static_cast<unsigned>(a.B * a.Hv), kD / kColsPerBlock);
+    hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV>), grid, dim3(64 * kWavesPerBlock), 0, s, a);
+    return check_launch("gdn_decode_kernel");
+}
+
+}  // namespace
+
+int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+               const float *gate, const float *beta, float gate_s, float beta_s, float *out,
+               size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream) {
+    if (!state || !q || !k || !v || !out) return fail(OURO_ERR_INVALID_ARG, "gdn decode: NULL argument");
+    if (d != static_cast<size_t>(kD)) return fail(OURO_ERR_SHAPE, "gdn decode: d = %zu, only 128 is supported", d);
+    if (!B || !Hk || !Hv || Hv % Hk) return fail(OURO_ERR_SHAPE, "gdn decode: bad heads B=%zu Hk=%zu Hv=%zu", B, Hk, Hv);
+    if (B * Hv > 0x7fffffffULL) return fail(OURO_ERR_SHAPE, "gdn decode: too many heads");
+    if (flags & ~(OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | OURO_GDN_KHEAD_DIV))
+        return fail(OURO_ERR_INVALID_ARG, "gdn decode: bad flags 0x%x", flags);
+    if (reinterpret_cast<uintptr_t>(state) % 16) return fail(OURO_ERR_ALIGN, "gdn decode: state needs 16-byte alignment");
+    const size_t qa = qk_dtype == OURO_DT_F32 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(q) % qa || reinterpret_cast<uintptr_t>(k) % qa)
+        return fail(OURO_ERR_ALIGN, "gdn decode: q/k need %zu-byte alignment", qa);
+    DecodeArgs a{};
+    a.state = state;
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.gate = gate;
+    a.beta = beta;
+    a.gate_s = gate_s;
+    a.beta_s = beta_s;
+    a.out = out;
+    a.B = static_cast<int>(B);
+    a.Hk = static_cast<int>(Hk);
+    a.Hv = static_cast<int>(Hv);
+    a.flags = flags;
+    a.eps = eps;
+    hipStream_t s = as_stream(stream);
+    const bool qf = qk_dtype == OURO_DT_F32, vf = v_dtype == OURO_DT_F32;
+    if ((qk_dtype != OURO_DT_F32 && qk_dtype != OURO_DT_BF16) || (v_dtype != OURO_DT_F32 && v_dtype != OURO_DT_BF16))
+        return fail(OURO_ERR_INVALID_ARG, "gdn decode: bad dtype");
+    if (qf && vf) return launch<float, float>(a, s);
+    if (qf) return launch<float, uint16_t>(a, s);
+    if (vf) return launch<uint16_t, float>(a, s);
+    return launch<uint16_t, uint16_t>(a, s);
+}
+
+}  // namespace ouro
+
+using namespace ouro;
+
+extern "C" {
+
+int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+                    const float *gate, const float *beta, float *out, size_t B, size_t Hk, size_t Hv,
+                    size_t d, unsigned flags, float eps, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (!gate || !beta) return fail(OURO_ERR_INVALID_ARG, "ouro_gdn_decode: gate/beta NULL");
+    return gdn_decode(state, q, k, qk_dtype, v, v_dtype, gate, beta, 0.f, 0.f, out, B, Hk, Hv, d,
+                      flags, eps, stream);
+}
+
+int ouro_delta_head_dim(float *state, size_t sdim, const float *q, const float *k, const float *v,
+                        float gate, float beta, float *out, void *stream) {
+    OURO_REQUIRE_INIT();
+    return gdn_decode(state, q, k, OURO_DT_F32, v, OURO_DT_F32, nullptr, nullptr, gate, beta, out, 1,
+                      1, 1, sdim, 0u, 0.f, stream);
+}
+
+}  // extern "C"

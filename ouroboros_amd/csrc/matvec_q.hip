@@ -1,0 +1,284 @@
+// matvec_q.hip - the reference kernel-call surface matvec_q / matmul_q
+// (ops.rs:76-84, 219-230) on device payloads of every ternary and dense kind.
+//
+// TL1 (PTQ1_0) and TQ1_0 are decoded in registers exactly as the reference
+// does (digit of byte b at stage n: q = b * 3^n mod 256, digit = (q*3) >> 8,
+// trit = digit - 1; dequant.rs:55-59, 134-138), one packed byte per lane
+// task, and multiplied straight into fp32 accumulators: trits never touch
+// memory (ops.rs:288-293).  One wavefront per output row; a task is one
+// payload byte with its 4 or 5 trits, so consecutive lanes read consecutive
+// payload bytes.  matmul_q decodes each byte once for up to 8 columns.
+#include "common.hpp"
+
+namespace ouro {
+
+int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *w_scale,
+            const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc,
+            void *stream);
+int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale,
+              void *stream);
+size_t i2_tiled_bytes(size_t out_len, size_t in_len);
+
+namespace {
+
+constexpr int kWaves = 4;
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+__device__ __forceinline__ int trit(uint32_t byte, uint32_t pow3) {
+    const uint32_t q = (byte * pow3) & 0xffu;  // u8 wrapping_mul
+    return static_cast<int>((q * 3u) >> 8) - 1;
+}
+
+struct MvArgs {
+    const uint8_t *w;
+    const float *x;  // [k][in_len]
+    float *y;        // column-major [k][out_len]
+    int out_len, in_len, k;
+};
+
+template <int NC>
+__device__ __forceinline__ void wave_store(float (&acc)[NC], const MvArgs &a, int row, int c0, int lane) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float v = acc[c];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
+        if (lane == 0 && c0 + c < a.k) a.y[static_cast<long long>(c0 + c) * a.out_len + row] = v;
+    }
+}
+
+// PTQ1_0 group (dequant.rs:140-171): qs[0..16] hold elements n*16 + m,
+// qs[16..24] elements 80 + n*8 + m, qh[0..2] elements 120 + n*2 + h.
+template <int NC>
+__global__ __launch_bounds__(64 * kWaves) void tl1_kernel(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int c0 = blockIdx.y * NC;
+    if (row >= a.out_len) return;
+    const int gpr = a.in_len / 128;
+    const uint8_t *rw = a.w + static_cast<long long>(row) * gpr * 28;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    const int tasks = gpr * 26;
+    for (int t = lane; t < tasks; t += 64) {
+        const int g = t / 26, b = t % 26;
+        const uint8_t *gp = rw + g * 28;
+        const uint32_t byte = gp[b];
+        const float d = f16_bits_to_f32(gp[26] | (static_cast<uint32_t>(gp[27]) << 8));
+        const int xg = g * 128;
+        int base, stride, cnt;
+        if (b < 16) {
+            base = xg + b, stride = 16, cnt = 5;
+        } else if (b < 24) {
+            base = xg + 80 + (b - 16), stride = 8, cnt = 5;
+        } else {
+            base = xg + 120 + (b - 24), stride = 2, cnt = 4;
+        }
+        uint32_t pow3 = 1;
+#pragma unroll
+        for (int n = 0; n < 5; ++n) {
+            if (n < cnt) {
+                const float w = static_cast<float>(trit(byte, pow3)) * d;
+                const int xi = base + n * stride;
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    if (c0 + c < a.k) acc[c] += w * a.x[static_cast<long long>(c0 + c) * a.in_len + xi];
+            }
+            pow3 *= 3;
+        }
+    }
+    wave_store<NC>(acc, a, row, c0, lane);
+}
+
+// TQ1_0 block (dequant.rs:49-80): qs[0..32] hold elements n*32 + m,
+// qs[32..48] elements 160 + n*16 + m, qh[0..4] elements 240 + n*4 + m;
+// f16 scale at bytes 52..53.
+template <int NC>
+__global__ __launch_bounds__(64 * kWaves) void tq1_kernel(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int c0 = blockIdx.y * NC;
+    if (row >= a.out_len) return;
+    const int bpr = a.in_len / 256;
+    const uint8_t *rw = a.w + static_cast<long long>(row) * bpr * 54;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    const int tasks = bpr * 52;
+    for (int t = lane; t < tasks; t += 64) {
+        const int blk = t / 52, b = t % 52;
+        const uint8_t *bp = rw + blk * 54;
+        const uint32_t byte = bp[b];
+        const float d = f16_bits_to_f32(bp[52] | (static_cast<uint32_t>(bp[53]) << 8));
+        const int xb = blk * 256;
+        int base, stride, cnt;
+        if (b < 32) {
+            base = xb + b, stride = 32, cnt = 5;
+        } else if (b < 48) {
+            base = xb + 160 + (b - 32), stride = 16, cnt = 5;
+        } else {
+            base = xb + 240 + (b - 48), stride = 4, cnt = 4;
+        }
+        uint32_t pow3 = 1;
+#pragma unroll
+        for (int n = 0; n < 5; ++n) {
+            if (n < cnt) {
+                const float w = static_cast<float>(trit(byte, pow3)) * d;
+                const int xi = base + n * stride;
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+                    if (c0 + c < a.k) acc[c] += w * a.x[static_cast<long long>(c0 + c) * a.in_len + xi];
+            }
+            pow3 *= 3;
+        }
+    }
+    wave_store<NC>(acc, a, row, c0, lane);
+}
+
+template <int KIND>
+__device__ __forceinline__ float dense_w(const uint8_t *w, long long i);
+template <>
+__device__ __forceinline__ float dense_w<OURO_KIND_F32>(const uint8_t *w, long long i) {
+    return reinterpret_cast<const float *>(w)[i];
+}
+template <>
+__device__ __forceinline__ float dense_w<OURO_KIND_F16>(const uint8_t *w, long long i) {
+    return f16_bits_to_f32(reinterpret_cast<const uint16_t *>(w)[i]);
+}
+template <>
+__device__ __forceinline__ float dense_w<OURO_KIND_BF16>(const uint8_t *w, long long i) {
+    return bf16_bits_to_f32(reinterpret_cast<const uint16_t *>(w)[i]);
+}
+
+template <int KIND, int NC>
+__global__ __launch_bounds__(64 * kWaves) void dense_kernel(MvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int c0 = blockIdx.y * NC;
+    if (row >= a.out_len) return;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    const long long rb = static_cast<long long>(row) * a.in_len;
+    for (int i = lane; i < a.in_len; i += 64) {
+        const float w = dense_w<KIND>(a.w, rb + i);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (c0 + c < a.k) acc[c] += w * a.x[static_cast<long long>(c0 + c) * a.in_len + i];
+    }
+    wave_store<NC>(acc, a, row, c0, lane);
+}
+
+int launch_mv(int kind, const MvArgs &a, hipStream_t s) {
+    const int nc = a.k >= 8 ? 8 : (a.k >= 4 ? 4 : (a.k >= 2 ? 2 : 1));
+    dim3 grid((a.out_len + kWaves - 1) / kWaves, (a.k + nc - 1) / nc), block(64 * kWaves);
+    if (grid.y > 65535) return fail(OURO_ERR_SHAPE, "matmul_q: too many columns");
+#define OURO_MV_LAUNCH(KERNEL)                                                        \
+    do {                                                                              \
+        if (nc == 8) hipLaunchKernelGGL(KERNEL<8>, grid, block, 0, s, a);             \
+        else if (nc == 4) hipLaunchKernelGGL(KERNEL<4>, grid, block, 0, s, a);        \
+        else if (nc == 2) hipLaunchKernelGGL(KERNEL<2>, grid, block, 0, s, a);        \
+        else hipLaunchKernelGGL(KERNEL<1>, grid, block, 0, s, a);                     \
+    } while (0)
+    switch (kind) {
+    case OURO_KIND_TL1: OURO_MV_LAUNCH(tl1_kernel); break;
+    case OURO_KIND_TQ1_0: OURO_MV_LAUNCH(tq1_kernel); break;
+    case OURO_KIND_F32:
+        if (nc == 8) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F32, 8>), grid, block, 0, s, a);
+        else if (nc == 4) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F32, 4>), grid, block, 0, s, a);
+        else if (nc == 2) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F32, 2>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((dense_kernel<OURO_KIND_F32, 1>), grid, block, 0, s, a);
+        break;
+    case OURO_KIND_F16:
+        if (nc == 8) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F16, 8>), grid, block, 0, s, a);
+        else if (nc == 4) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F16, 4>), grid, block, 0, s, a);
+        else if (nc == 2) hipLaunchKernelGGL((dense_kernel<OURO_KIND_F16, 2>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((dense_kernel<OURO_KIND_F16, 1>), grid, block, 0, s, a);
+        break;
+    case OURO_KIND_BF16:
+        if (nc == 8) hipLaunchKernelGGL((dense_kernel<OURO_KIND_BF16, 8>), grid, block, 0, s, a);
+        else if (nc == 4) hipLaunchKernelGGL((dense_kernel<OURO_KIND_BF16, 4>), grid, block, 0, s, a);
+        else if (nc == 2) hipLaunchKernelGGL((dense_kernel<OURO_KIND_BF16, 2>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((dense_kernel<OURO_KIND_BF16, 1>), grid, block, 0, s, a);
+        break;
+    default:
+        return fail(OURO_ERR_KIND, "matvec_q: kind %d not supported", kind);
+    }
+#undef OURO_MV_LAUNCH
+    return check_launch("matvec_q kernel");
+}
+
+}  // namespace
+
+// Shape rules of the reference decoders: TL1 rows are whole 128-groups
+// (ops.rs:296), TQ1_0 rows whole 256-blocks (QuantKind::row_bytes,
+// dequant.rs:376-387).
+int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
+             float *y, int8_t *xq_scratch, float *dscale_scratch, void *stream) {
+    if (!payload || !x || !y) return fail(OURO_ERR_INVALID_ARG, "matvec_q: NULL argument");
+    if (!out_len || !in_len || !k) return fail(OURO_ERR_SHAPE, "matvec_q: empty shape");
+    if (out_len > 0x7fffffffULL || in_len > 0x7fffffffULL || k > 0x7fffffffULL)
+        return fail(OURO_ERR_SHAPE, "matvec_q: shape too large");
+    switch (kind) {
+    case OURO_KIND_TL1:
+        if (in_len % 128) return fail(OURO_ERR_SHAPE, "matvec_q TL1: in_len %zu not a multiple of 128", in_len);
+        break;
+    case OURO_KIND_TQ1_0:
+        if (in_len % 256) return fail(OURO_ERR_SHAPE, "matvec_q TQ1_0: in_len %zu not a multiple of 256", in_len);
+        break;
+    case OURO_KIND_F32:
+        if (reinterpret_cast<uintptr_t>(payload) % 4) return fail(OURO_ERR_ALIGN, "matvec_q F32: payload alignment");
+        break;
+    case OURO_KIND_F16:
+    case OURO_KIND_BF16:
+        if (reinterpret_cast<uintptr_t>(payload) % 2) return fail(OURO_ERR_ALIGN, "matvec_q F16: payload alignment");
+        break;
+    case OURO_KIND_I2: {
+        const size_t tb = i2_tiled_bytes(out_len, in_len);
+        if (!tb) return fail(OURO_ERR_SHAPE, "matvec_q I2: in_len %zu not a multiple of 256", in_len);
+        int8_t *xq = xq_scratch;
+        float *ds = dscale_scratch;
+        if (!xq) {
+            const size_t xb = (k * in_len + 255) & ~size_t(255);
+            uint8_t *ws = static_cast<uint8_t *>(workspace(xb + k * sizeof(float), stream));
+            if (!ws) return OURO_ERR_HIP;
+            xq = reinterpret_cast<int8_t *>(ws);
+            ds = reinterpret_cast<float *>(ws + xb);
+        }
+        int st = act_quant(x, OURO_DT_F32, k, in_len, xq, ds, stream);
+        if (st) return st;
+        const uint8_t *w = static_cast<const uint8_t *>(payload);
+        return i2_gemm(w, out_len, in_len, reinterpret_cast<const float *>(w + tb), xq, ds, k, y,
+                       nullptr, stream);
+    }
+    default:
+        return fail(OURO_ERR_KIND, "matvec_q: kind %d not supported", kind);
+    }
+    MvArgs a{static_cast<const uint8_t *>(payload), x, y, static_cast<int>(out_len),
+             static_cast<int>(in_len), static_cast<int>(k)};
+    return launch_mv(kind, a, as_stream(stream));
+}
+
+}  // namespace ouro
+
+using namespace ouro;
+
+extern "C" {
+
+int ouro_matvec_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
+                  float *y, void *stream) {
+    OURO_REQUIRE_INIT();
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream);
+}
+
+int ouro_matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
+                  size_t k, float *y, void *stream) {
+    OURO_REQUIRE_INIT();
+    return matmul_q(payload, kind, out_len, in_len, x, k, y, nullptr, nullptr, stream);
+}
+
+}  // extern "C"

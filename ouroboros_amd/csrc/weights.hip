@@ -1,0 +1,138 @@
+// weights.hip - resident weight handles, the device analogue of the
+// reference's GpuPool (ouro-wgpu/src/lib.rs:251-356): a tensor is uploaded
+// once (and repacked on upload, as upload_q6k repacks 210 -> 212 B blocks),
+// then applied by handle.  An I2 handle also owns its activation-quantisation
+// scratch, sized at upload for max_cols columns, so its matvec allocates
+// nothing.
+#include "common.hpp"
+
+#include <new>
+
+namespace ouro {
+int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
+             float *y, int8_t *xq_scratch, float *dscale_scratch, void *stream);
+int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
+            const float *w_scale, void *stream);
+size_t i2_tiled_bytes(size_t out_len, size_t in_len);
+}  // namespace ouro
+
+struct ouro_weight {
+    int kind = 0;
+    size_t out_len = 0, in_len = 0, max_cols = 0;
+    void *payload = nullptr;
+    int8_t *xq = nullptr;
+    float *dscale = nullptr;
+};
+
+using namespace ouro;
+
+namespace {
+
+size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:376-387)
+    switch (kind) {
+    case OURO_KIND_F32: return k * 4;
+    case OURO_KIND_F16:
+    case OURO_KIND_BF16: return k * 2;
+    case OURO_KIND_TL1: return k / 128 * 28;
+    case OURO_KIND_TQ1_0: return k / 256 * 54;
+    case OURO_KIND_I2: return k / 4;
+    default: return 0;
+    }
+}
+
+void release(ouro_weight *w) {
+    if (!w) return;
+    if (w->payload) (void)hipFree(w->payload);
+    if (w->xq) (void)hipFree(w->xq);
+    delete w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len, size_t in_len,
+                       float w_scale, size_t max_cols, ouro_weight_t *out) {
+    OURO_REQUIRE_INIT();
+    if (!host || !out) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_upload: NULL argument");
+    *out = nullptr;
+    const size_t rb = ref_row_bytes(kind, in_len);
+    if (!rb) return fail(OURO_ERR_KIND, "ouro_weight_upload: kind %d / in_len %zu unsupported", kind, in_len);
+    if (!out_len || bytes != rb * out_len)
+        return fail(OURO_ERR_SHAPE, "ouro_weight_upload: %zu bytes, expected %zu", bytes, rb * out_len);
+    ouro_weight *w = new (std::nothrow) ouro_weight;
+    if (!w) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_upload: out of host memory");
+    w->kind = kind;
+    w->out_len = out_len;
+    w->in_len = in_len;
+    w->max_cols = max_cols ? max_cols : 1;
+    if (kind == OURO_KIND_I2) {
+        const size_t tb = i2_tiled_bytes(out_len, in_len);
+        if (!tb) {
+            release(w);
+            return fail(OURO_ERR_SHAPE, "ouro_weight_upload: I2 in_len %zu not a multiple of 256", in_len);
+        }
+        void *canon = nullptr;
+        if (hipMalloc(&w->payload, tb + 16) != hipSuccess || hipMalloc(&canon, bytes) != hipSuccess) {
+            if (canon) (void)hipFree(canon);
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+        }
+        int st = OURO_OK;
+        if (hipMemcpy(canon, host, bytes, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(static_cast<uint8_t *>(w->payload) + tb, &w_scale, 4, hipMemcpyHostToDevice) != hipSuccess)
+            st = fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
+        if (!st) st = i2_tile(static_cast<const uint8_t *>(canon), out_len, in_len,
+                              static_cast<uint8_t *>(w->payload), nullptr, nullptr);
+        if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
+        (void)hipFree(canon);
+        if (st) {
+            release(w);
+            return st;
+        }
+        const size_t xb = (w->max_cols * in_len + 255) & ~size_t(255);
+        void *scratch = nullptr;
+        if (hipMalloc(&scratch, xb + w->max_cols * sizeof(float)) != hipSuccess) {
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: scratch allocation failed");
+        }
+        w->xq = static_cast<int8_t *>(scratch);
+        w->dscale = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + xb);
+    } else {
+        if (hipMalloc(&w->payload, bytes) != hipSuccess) {
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+        }
+        if (hipMemcpy(w->payload, host, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
+        }
+    }
+    *out = w;
+    return OURO_OK;
+}
+
+int ouro_weight_free(ouro_weight_t w) {
+    OURO_REQUIRE_INIT();
+    if (w) {
+        (void)hipDeviceSynchronize();
+        release(w);
+    }
+    return OURO_OK;
+}
+
+const void *ouro_weight_payload(ouro_weight_t w) { return w ? w->payload : nullptr; }
+
+int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (!w) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matmul: NULL handle");
+    if (w->kind == OURO_KIND_I2 && k > w->max_cols)
+        return fail(OURO_ERR_SHAPE, "ouro_weight_matmul: k %zu > max_cols %zu of the handle", k, w->max_cols);
+    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->dscale, stream);
+}
+
+int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y, void *stream) {
+    return ouro_weight_matmul(w, x, 1, y, stream);
+}
+
+}  // extern "C"

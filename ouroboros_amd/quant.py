@@ -1,0 +1,75 @@
+"""Quant kinds and the canonical I2 packing (host side, no GPU needed).
+
+``QuantKind`` mirrors the reference enum (cluster/src/infer/dequant.rs:315-388)
+with the same ggml dtype ids; ``I2`` is the int8-activation x 2-bit ternary
+format of this library (no reference counterpart).
+"""
+from __future__ import annotations
+
+import enum
+
+import numpy as np
+
+from . import _lib
+
+
+class QuantKind(enum.IntEnum):
+    F32 = _lib.KIND_F32
+    F16 = _lib.KIND_F16
+    BF16 = _lib.KIND_BF16
+    TQ1_0 = _lib.KIND_TQ1_0
+    TL1 = _lib.KIND_TL1
+    I2 = _lib.KIND_I2
+
+    @classmethod
+    def from_dtype(cls, dtype_id: int) -> "QuantKind | None":
+        """QuantKind::from_dtype (dequant.rs:334-348) for the kinds on this path."""
+        try:
+            k = cls(dtype_id)
+        except ValueError:
+            return None
+        return None if k is cls.I2 else k
+
+    def block_bytes(self) -> int:  # dequant.rs:351-363
+        return {self.F32: 4, self.F16: 2, self.BF16: 2, self.TQ1_0: 54, self.TL1: 28, self.I2: 1}[self]
+
+    def block_elems(self) -> int:  # dequant.rs:366-373
+        return {self.F32: 1, self.F16: 1, self.BF16: 1, self.TQ1_0: 256, self.TL1: 128, self.I2: 4}[self]
+
+    def row_bytes(self, k: int) -> int:  # dequant.rs:376-387
+        return k // self.block_elems() * self.block_bytes()
+
+
+def i2_pack(w: np.ndarray) -> np.ndarray:
+    """Canonical I2 bytes of a ternary matrix w[out][in] (values -1, 0, +1).
+
+    Weight k of a row sits in byte k/4 at bits 2*(k%4) as code w+1.
+    """
+    w = np.asarray(w)
+    if w.ndim != 2 or w.shape[1] % 4:
+        raise ValueError("i2_pack: need a 2-D matrix with in_len % 4 == 0")
+    if w.size and (w.min() < -1 or w.max() > 1):
+        raise ValueError("i2_pack: weights must be in {-1, 0, +1}")
+    codes = (w.astype(np.int16) + 1).astype(np.uint8).reshape(w.shape[0], -1, 4)
+    return (codes[..., 0] | (codes[..., 1] << 2) | (codes[..., 2] << 4) | (codes[..., 3] << 6)).astype(np.uint8)
+
+
+def i2_unpack(packed: np.ndarray, in_len: int) -> np.ndarray:
+    """Inverse of :func:`i2_pack` (code 3 decodes to +2)."""
+    p = np.asarray(packed, dtype=np.uint8).reshape(-1, in_len // 4)
+    codes = np.stack([(p >> (2 * f)) & 3 for f in range(4)], axis=-1).reshape(p.shape[0], in_len)
+    return codes.astype(np.int8) - 1
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x7FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    """bf16 bit patterns -> fp32 (exact; dequant.rs:197-199)."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
