@@ -233,6 +233,27 @@ int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype,
                     size_t Hv, size_t d, unsigned flags, float eps,
                     void *stream);
 
+/* Chunked prefill of N sequences packed into one varlen buffer of T tokens
+ * (cu_seqlens_host[0..N] on the HOST, [0] = 0, [N] = T; NULL means one
+ * sequence of T tokens).  Same head layout and flags as ouro_gdn_decode,
+ * with a token axis in place of the batch axis:
+ *   q, k [T][Hk][d] bf16; v [T][Hv][d] bf16; gate, beta [T][Hv] f32;
+ *   state [N][Hv][d][d] f32 (initial state in, final state out);
+ *   out [T][Hv][d] f32.
+ * The result equals running the decode recurrence token by token (the
+ * reference prefill, shell/src/bonsai.rs:48-52 driving run_delta,
+ * qwen35.rs:1048-1158); inside each chunk of `chunk` (64) tokens it uses the
+ * WY/UT form with bf16 MFMA contractions and fp32 accumulation.  d == 128.
+ * Allocates nothing: the offsets travel as kernel arguments (launched in
+ * slices of 256 sequences). */
+int ouro_gdn_chunk_prefill(float *state, const void *q, const void *k,
+                           const void *v, const float *gate,
+                           const float *beta, float *out,
+                           const int32_t *cu_seqlens_host, size_t N,
+                           size_t T, size_t Hk, size_t Hv, size_t d,
+                           size_t chunk, unsigned flags, float eps,
+                           void *stream);
+
 /* ------------------------------------------------------------------ */
 /* Resident weights (GpuPool::upload_q6k / matvec, ouro-wgpu/src/lib.rs:   */
 /* 251-356): upload once, repacking on upload, then matvec by handle.    */

@@ -61,22 +61,16 @@ def gdn_decode(state: DeviceBuffer, q: DeviceBuffer, k: DeviceBuffer, v: DeviceB
          out.ptr, B, Hk, Hv, d, flags, eps, stream)
 
 
-def gdn_chunk_workspace_bytes(T: int, N: int, Hk: int, Hv: int, d: int = S, chunk: int = 64) -> int:
-    return int(_lib.lib().ouro_gdn_chunk_workspace_bytes(T, N, Hk, Hv, d, chunk))
-
-
 def gdn_chunk_prefill(state: DeviceBuffer, q: DeviceBuffer, k: DeviceBuffer, v: DeviceBuffer,
                       gate: DeviceBuffer, beta: DeviceBuffer, out: DeviceBuffer,
                       cu_seqlens: np.ndarray | None, T: int, Hk: int, Hv: int, d: int = S,
                       chunk: int = 64, flags: int = _lib.GDN_L2NORM_QK | _lib.GDN_SCALE_Q,
-                      eps: float = 1e-6, workspace: DeviceBuffer | None = None,
-                      stream=None) -> None:
+                      eps: float = 1e-6, stream=None) -> None:
+    """Chunked prefill of packed varlen sequences (q, k, v bf16 as uint16)."""
     if cu_seqlens is None:
-        cu = None
-        n = 1
+        cu, n = None, 1
     else:
         cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
         n = len(cu) - 1
     call("ouro_gdn_chunk_prefill", state.ptr, q.ptr, k.ptr, v.ptr, gate.ptr, beta.ptr, out.ptr,
-         cu.ctypes.data if cu is not None else None, n, T, Hk, Hv, d, chunk, flags, eps,
-         workspace.ptr if workspace is not None else None, stream)
+         cu.ctypes.data if cu is not None else None, n, T, Hk, Hv, d, chunk, flags, eps, stream)
