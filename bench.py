@@ -6,11 +6,13 @@ weights, int8 per-token-absmax activations, fp32 output).  One step is one
 grouped launch over 64 distinct weight matrices (283 MB, more than the
 256 MB MALL), inputs resident in HBM.  Also measured, reported under
 "secondary": gated delta-net decode (B=32, Hk=16, Hv=32, d=128, fp32 state,
-8 rotating state sets = 512 MiB) in tokens/s, and the 512x4096 bf16
-Walsh-Hadamard rotation in GB/s.
+8 rotating state sets = 512 MiB) in tokens/s, the 512x4096 bf16
+Walsh-Hadamard rotation in GB/s, the chunked prefill of 4 x 4096 tokens in
+tokens/s and TFLOP/s, and a 512 MiB device copy as the bandwidth reference.
 
 Every kernel time comes from HIP events recorded on the stream the kernels
-run on.  The CPU baseline is the oracle (a C restatement of the reference's
+run on: the null stream, where back-to-back launches carry no extra gap.
+The CPU baseline is the oracle (a C restatement of the reference's
 threaded CPU kernels) on a bounded sample, rank 0 only.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -42,6 +44,17 @@ GDN_BYTES = (2 * GDN_B * GDN_HV * GDN_D * GDN_D * 4 + 2 * GDN_B * GDN_HK * GDN_D
 # FWHT 512 x 4096 bf16 in and out.
 FW_ROWS, FW_N, FW_BUFS = 512, 4096, 32
 FW_BYTES = 2 * FW_ROWS * FW_N * 2
+# Chunked prefill: 4 sequences x 4096 tokens, chunk 64, same heads.
+PF_SEQ, PF_LEN, PF_C = 4, 4096, 64
+PF_T = PF_SEQ * PF_LEN
+# Each contraction counted once per (chunk, v-head): K K^T, Q K^T (64x64x128),
+# K S0, Q S0 (64x128x128), T R, Pt U (64x64x128), K^T U (128x64x128).
+PF_FLOP_CHUNK_HEAD = 2 * (64 * 64 * 128 * 4 + 64 * 128 * 128 * 2 + 128 * 64 * 128)
+PF_FLOPS = PF_FLOP_CHUNK_HEAD * (PF_LEN // PF_C) * PF_SEQ * GDN_HV
+# q,k,v bf16 in, gate+beta f32 in, out f32, state in+out.
+PF_BYTES = (2 * PF_T * GDN_HK * GDN_D * 2 + PF_T * GDN_HV * GDN_D * 2 + 2 * PF_T * GDN_HV * 4
+            + PF_T * GDN_HV * GDN_D * 4 + 2 * PF_SEQ * GDN_HV * GDN_D * GDN_D * 4)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def log(msg: str) -> None:
@@ -55,14 +68,22 @@ def cpu_threads() -> int:
     return min(os.cpu_count() or 1, 16)
 
 
-def time_events(stream, fn, steps: int, warmup: int) -> float:
-    """Average ms per call of fn() on `stream`, HIP events around `steps` calls."""
+def time_events(stream, fn, steps: int, warmup: int, min_warm_s: float = 0.15) -> float:
+    """Average ms per call of fn() on `stream`, HIP events around `steps` calls.
+
+    Untimed warm-up: `warmup` calls, then more until `min_warm_s` of wall time
+    has passed, so the GPU clocks have ramped before the timed region."""
+    from ouroboros_amd._lib import call
     from ouroboros_amd.device import Event, synchronize
 
-    for i in range(warmup):
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < min_warm_s:
         fn(i)
+        i += 1
+        if i % 16 == 0:
+            synchronize(stream)
     synchronize(stream)
-    from ouroboros_amd._lib import call
     call("ouro_device_synchronize")
     e0, e1 = Event(), Event()
     e0.record(stream)
@@ -185,6 +206,47 @@ def bench_fwht(stream, steps, warmup):
     return ms, ms_all
 
 
+def bench_prefill(stream, steps, warmup):
+    from ouroboros_amd import quant
+    from ouroboros_amd._lib import GDN_L2NORM_QK, GDN_SCALE_Q, call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(11)
+    T, Hk, Hv, d = PF_T, GDN_HK, GDN_HV, GDN_D
+    q = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((T, Hk, d)).astype(np.float32)))
+    k = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((T, Hk, d)).astype(np.float32)))
+    v = DeviceBuffer.from_host(quant.f32_to_bf16_bits(rng.standard_normal((T, Hv, d)).astype(np.float32)))
+    beta = DeviceBuffer.from_host((1 / (1 + np.exp(-rng.standard_normal((T, Hv))))).astype(np.float32))
+    gate = DeviceBuffer.from_host((-np.log1p(np.exp(rng.standard_normal((T, Hv))))).astype(np.float32))
+    state = DeviceBuffer.from_host((0.02 * rng.standard_normal((PF_SEQ, Hv, d * d))).astype(np.float32))
+    out = DeviceBuffer((T, Hv, d), np.float32)
+    cu = np.arange(PF_SEQ + 1, dtype=np.int32) * PF_LEN
+
+    def step(_i):
+        call("ouro_gdn_chunk_prefill", state.ptr, q.ptr, k.ptr, v.ptr, gate.ptr, beta.ptr, out.ptr,
+             cu.ctypes.data, PF_SEQ, T, Hk, Hv, d, PF_C, GDN_L2NORM_QK | GDN_SCALE_Q, 1e-6, stream)
+
+    return time_events(stream, step, max(3, steps // 5), 2)
+
+
+COPY_BYTES = 512 << 20
+
+
+def bench_copy(stream, steps):
+    """Device-to-device copy of 512 MiB: the achievable-bandwidth reference
+    and the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.device import DeviceBuffer
+
+    src = DeviceBuffer((COPY_BYTES,), np.uint8, zero=True)
+    dst = DeviceBuffer((COPY_BYTES,), np.uint8)
+
+    def step(_i):
+        call("ouro_memcpy_dtod", dst.ptr, src.ptr, COPY_BYTES, stream)
+
+    return time_events(stream, step, max(3, steps // 5), 2)
+
+
 def cpu_baseline(orc, budget_s: float = 12.0) -> dict:
     """The reference's own CPU GEMV (matvec_tl1, SSE4.1 order, row-split
     threads) on the same 6912x2560 shape in its PTQ1_0 format."""
@@ -257,22 +319,34 @@ def gdn_cpu_baseline(orc, budget_s: float = 6.0) -> dict:
 
 
 def load_traffic() -> dict:
+    """Calibrated HBM bytes per dispatch from the committed PMC summary
+    (profiles/pmc_traffic.json, FETCH_SIZE and WRITE_SIZE runs scaled by a
+    512 MiB device copy), keyed by kernel name and grid size."""
     f = ROOT / "profiles" / "pmc_traffic.json"
-    if f.exists():
-        try:
-            return json.loads(f.read_text())
-        except (OSError, ValueError):
-            return {}
-    return {}
+    try:
+        return json.loads(f.read_text()).get("kernels", {})
+    except (OSError, ValueError):
+        return {}
+
+
+def traffic_of(traffic: dict, prefix: str, grid: int | None = None):
+    best = None
+    for name, by_grid in traffic.items():
+        if not name.startswith(prefix):
+            continue
+        for g, b in by_grid.items():
+            if grid is None or int(g) == grid:
+                best = b if best is None else max(best, b)
+    return best
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["gemv", "gdn", "fwht"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gdn", "fwht", "prefill", "copy"], default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -281,10 +355,9 @@ def main() -> int:
         return 2
 
     from ouroboros_amd import _lib
-    from ouroboros_amd.device import Stream
-
+    
     _lib.init()
-    stream = Stream().handle
+    stream = None  # the null stream: no per-launch gap between back-to-back kernels
     orc = None
     if not args.no_cpu:
         import oracle as orc  # the CPU baseline / parity checker only
@@ -300,6 +373,12 @@ def main() -> int:
     if args.only in (None, "fwht"):
         log("FWHT 512x4096 bf16")
         res["fwht"] = bench_fwht(stream, args.steps, args.warmup)
+    if args.only in (None, "copy"):
+        log("device copy 512 MiB")
+        res["copy"] = bench_copy(stream, args.steps)
+    if args.only in (None, "prefill"):
+        log("GDN chunked prefill 4x4096")
+        res["prefill"] = bench_prefill(stream, args.steps, args.warmup)
 
     traffic = load_traffic()
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -317,7 +396,7 @@ def main() -> int:
                        "bytes_per_matrix": GEMV_BYTES},
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4),
-                         "traffic": traffic.get("i2_gemv_kernel")},
+                         "traffic": traffic_of(traffic, "i2_gemv_kernel")},
             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
             "single_matrix_launch_us": round(ms_single * 1e3, 2),
             "single_matrix_GBs": round(GEMV_BYTES / (ms_single * 1e-3) / 1e9, 1),
@@ -331,7 +410,7 @@ def main() -> int:
             "value": round(GDN_B / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
             "config": "B=32 seqs, Hk=16, Hv=32, d=128, fp32 state, bf16 q/k/v, 8 rotating state sets",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("gdn_decode_kernel")},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "gdn_decode_kernel")},
             "bytes_per_step": GDN_BYTES,
         }
     if "fwht" in res:
@@ -342,9 +421,28 @@ def main() -> int:
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4),
             "config": "512x4096 bf16 in/out, block 4096, scale 1/64, 32 rotating buffers",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("fwht_row_kernel")},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "fwht_row_kernel", FW_ROWS * 256)},
             "streaming_16384_rows_GBs": round(gbs_all, 1),
             "bytes_per_call": FW_BYTES,
+        }
+    if "copy" in res:
+        ms = res["copy"]
+        sec["device_copy"] = {"value": round(2 * COPY_BYTES / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                              "config": "hipMemcpyAsync device-to-device, 512 MiB (read + write counted)",
+                              "frac_of_peak": round(2 * COPY_BYTES / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if "prefill" in res:
+        ms = res["prefill"]
+        tf = PF_FLOPS / (ms * 1e-3) / 1e12
+        gbs = PF_BYTES / (ms * 1e-3) / 1e9
+        t_mem = PF_BYTES / (HBM_PEAK_GBS * 1e9)
+        t_mfma = PF_FLOPS / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+        sec["gdn_prefill"] = {
+            "value": round(PF_T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_call": round(ms, 4),
+            "config": "4 seqs x 4096 tokens packed varlen, chunk 64, Hk=16, Hv=32, d=128, bf16 q/k/v, fp32 state/out",
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_of(traffic, "gdn_chunk_kernel")},
+            "algorithmic_gflop": round(PF_FLOPS / 1e9, 2), "bytes": PF_BYTES, "hbm_GBs": round(gbs, 1),
+            "frac_of_min_roofline": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
         }
     if orc is not None:
         log("CPU baseline")

@@ -17,7 +17,6 @@ namespace ouro {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kWavesPerBlock = 4;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -117,9 +116,9 @@ struct GemvArgs {
 };
 
 // G: 4-weight groups per lane per row; R rows per tile; NC activation
-// columns per pass; TPW tiles per wavefront.
-template <int G, int NC, int TPW>
-__global__ __launch_bounds__(kWave *kWavesPerBlock) void i2_gemv_kernel(GemvArgs a) {
+// columns per pass; TPW tiles per wavefront; WPB wavefronts per block.
+template <int G, int NC, int TPW, int WPB>
+__global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
     constexpr int R = rows_per_tile(G);
     constexpr int CHUNK = R * G;      // bytes per lane per tile
     constexpr int NV = CHUNK / 16;    // 16-byte loads per lane per tile
@@ -129,7 +128,7 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void i2_gemv_kernel(GemvArgs
     const int wave = threadIdx.x / kWave;
     const int mat = blockIdx.z;
     const int c0 = blockIdx.y * NC;
-    const int tile0 = (blockIdx.x * kWavesPerBlock + wave) * TPW;
+    const int tile0 = (blockIdx.x * WPB + wave) * TPW;
     if (tile0 >= a.tiles) return;  // whole wavefront leaves together
 
     const uint8_t *w = a.w + mat * a.w_stride;
@@ -162,7 +161,7 @@ __global__ __launch_bounds__(kWave *kWavesPerBlock) void i2_gemv_kernel(GemvArgs
         const u32x4 *tp = reinterpret_cast<const u32x4 *>(
             w + static_cast<long long>(tile < a.tiles ? tile : tile0) * (R * 64 * G));
 #pragma unroll
-        for (int j = 0; j < NV; ++j) buf[t][j] = __builtin_nontemporal_load(tp + j * kWave + lane);
+        for (int j = 0; j < NV; ++j) buf[t][j] = tp[j * kWave + lane];
     }
 
 #pragma unroll
@@ -211,7 +210,7 @@ using GemvFn = void (*)(GemvArgs);
 
 struct GemvPick {
     GemvFn fn;
-    int nc, tpw;
+    int nc, tpw, wpb;
 };
 
 // Tiles per wavefront are capped so that the in-flight tile buffers stay
@@ -219,11 +218,13 @@ struct GemvPick {
 template <int G>
 GemvPick pick_g(int ncols, int want_tpw) {
     constexpr int NV = rows_per_tile(G) * G / 16;
-    if (ncols >= 4) return {i2_gemv_kernel<G, 4, 1>, 4, 1};
-    if (ncols >= 2) return {i2_gemv_kernel<G, 2, 1>, 2, 1};
-    if (want_tpw >= 4 && 4 * NV <= 32) return {i2_gemv_kernel<G, 1, 4>, 1, 4};
-    if (want_tpw >= 2 && 2 * NV <= 32) return {i2_gemv_kernel<G, 1, 2>, 1, 2};
-    return {i2_gemv_kernel<G, 1, 1>, 1, 1};
+    if (ncols >= 4) return {i2_gemv_kernel<G, 4, 1, 4>, 4, 1, 4};
+    if (ncols >= 2) return {i2_gemv_kernel<G, 2, 1, 4>, 2, 1, 4};
+    // Measured on the 64 x 6912x2560 stream: 2 tiles per wavefront in
+    // 8-wavefront blocks for large grouped launches, 1 tile per wavefront
+    // when a single matrix has to spread over the whole chip.
+    if (want_tpw >= 2 && 2 * NV <= 32) return {i2_gemv_kernel<G, 1, 2, 8>, 1, 2, 8};
+    return {i2_gemv_kernel<G, 1, 1, 4>, 1, 1, 4};
 }
 
 GemvPick pick_gemv(int G, int ncols, int tpw) {
@@ -249,14 +250,14 @@ int launch_gemv(const GemvArgs &base, int count, void *stream) {
     // Tiles per wavefront: enough in flight for a large grouped launch,
     // one per wavefront when a single matrix has to fill the chip alone.
     const long long total_tiles = static_cast<long long>(tiles) * count;
-    const int want = total_tiles >= 64LL * 1024 ? 4 : (total_tiles >= 8192 ? 2 : 1);
+    const int want = total_tiles >= 8192 ? 2 : 1;
     const GemvPick p = pick_gemv(G, base.ncols, want);
     if (!p.fn) return fail(OURO_ERR_SHAPE, "i2 gemv: in_len %d (G=%d) has no kernel instance", base.in_len, G);
     const int nc = p.nc;
-    const int per_block = kWavesPerBlock * p.tpw;
+    const int per_block = p.wpb * p.tpw;
     dim3 grid((tiles + per_block - 1) / per_block, (base.ncols + nc - 1) / nc, count);
     if (grid.y > 65535 || grid.z > 65535) return fail(OURO_ERR_SHAPE, "i2 gemv: grid too large");
-    hipLaunchKernelGGL(p.fn, grid, dim3(kWave * kWavesPerBlock), 0, as_stream(stream), base);
+    hipLaunchKernelGGL(p.fn, grid, dim3(kWave * p.wpb), 0, as_stream(stream), base);
     return check_launch("i2_gemv_kernel");
 }
 
