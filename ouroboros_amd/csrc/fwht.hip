@@ -22,13 +22,44 @@ constexpr int kMaxN = 32768;  // row length limit of the LDS-resident design
 
 __device__ __forceinline__ int pad_idx(int i) { return i + (i >> 4); }
 
-template <typename T>
-__device__ __forceinline__ float ld(const T *p, long long i);
-template <>
-__device__ __forceinline__ float ld<float>(const float *p, long long i) { return p[i]; }
-template <>
-__device__ __forceinline__ float ld<uint16_t>(const uint16_t *p, long long i) {
-    return bf16_bits_to_f32(p[i]);
+// 16 contiguous elements <-> registers with 16-byte global accesses.
+__device__ __forceinline__ void ld16(const float *p, float (&v)[16]) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 t = q[i];
+        v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
+    }
+}
+__device__ __forceinline__ void ld16(const uint16_t *p, float (&v)[16]) {
+    const uint4 *q = reinterpret_cast<const uint4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint4 t = q[i];
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[8 * i + 2 * e] = __uint_as_float(w[e] << 16);
+            v[8 * i + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+        }
+    }
+}
+__device__ __forceinline__ void st16(float *p, const float (&v)[16]) {
+    float4 *q = reinterpret_cast<float4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+}
+__device__ __forceinline__ void st16(uint16_t *p, const float (&v)[16]) {
+    uint4 *q = reinterpret_cast<uint4 *>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w[e] = static_cast<uint32_t>(f32_to_bf16_bits(v[8 * i + 2 * e])) |
+                   (static_cast<uint32_t>(f32_to_bf16_bits(v[8 * i + 2 * e + 1])) << 16);
+        q[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
 }
 
 // Value as it will be stored in the output dtype (bf16 rounds).
@@ -41,20 +72,11 @@ __device__ __forceinline__ float as_stored<uint16_t>(float v) {
     return bf16_bits_to_f32(f32_to_bf16_bits(v));
 }
 
-template <typename T>
-__device__ __forceinline__ void st(T *p, long long i, float v);
-template <>
-__device__ __forceinline__ void st<float>(float *p, long long i, float v) { p[i] = v; }
-template <>
-__device__ __forceinline__ void st<uint16_t>(uint16_t *p, long long i, float v) {
-    p[i] = f32_to_bf16_bits(v);
-}
-
 // In-register stages h = 1..min(8, block/2) over 16 contiguous values.
-__device__ __forceinline__ void wht16(float (&v)[16], int logb) {
+template <int LOGB>
+__device__ __forceinline__ void wht16(float (&v)[16]) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        if (s >= logb) break;
+    for (int s = 0; s < (LOGB < 4 ? LOGB : 4); ++s) {
         const int h = 1 << s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -74,11 +96,47 @@ struct FwhtArgs {
     int8_t *xq;
     float *dscale;
     long long rows;
-    int n, logb;
+    int n;
     float scale;
 };
 
-template <typename TI, typename TO, bool INV, bool QUANT, bool STORE>
+// Pass P (P >= 1) of a block of 2^LOGB: stages 2^(4P) .. over the <= 16
+// elements of one set, which differ only in index bits 4P .. 4P+NB-1.  The
+// padded LDS index of element e is e + e/16, so the set's elements sit at a
+// constant stride from its base and every access is an immediate offset.
+template <int LOGB, int P>
+__device__ __forceinline__ void wht_pass(float *lds, int n, int tid) {
+    constexpr int LO = 4 * P;
+    constexpr int NB = (LOGB - LO) < 4 ? (LOGB - LO) : 4;
+    constexpr int SPAN = 1 << NB;
+    constexpr int STRIDE = (1 << LO) + (1 << (LO - 4));  // padded distance of index bit LO
+    const int sets = n >> NB;
+    for (int s = tid; s < sets; s += kThreads) {
+        const int low = s & ((1 << LO) - 1);
+        const int high = s >> LO;
+        const int base = (high << (LO + NB)) + low;
+        float *p = lds + pad_idx(base);
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) v[j] = p[j * STRIDE];
+#pragma unroll
+        for (int st_ = 0; st_ < NB; ++st_) {
+            const int h = 1 << st_;
+#pragma unroll
+            for (int j = 0; j < SPAN; ++j) {
+                if ((j & h) == 0) {
+                    const float u = v[j], w = v[j + h];
+                    v[j] = u + w;
+                    v[j + h] = u - w;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) p[j * STRIDE] = v[j];
+    }
+}
+
+template <typename TI, typename TO, bool INV, bool QUANT, bool STORE, int LOGB>
 __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     extern __shared__ float lds[];
     __shared__ float red[kThreads / 64];
@@ -91,49 +149,31 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     // Pass 0: load 16 contiguous values, apply forward signs, stages 1..8.
     for (int c = tid; c < chunks; c += kThreads) {
         float v[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = ld(x, 16LL * c + i);
+        ld16(x + 16LL * c, v);
         if (!INV && a.signs) {
+            float sg[16];
+            ld16(a.signs + 16 * c, sg);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = v[i] * a.signs[16 * c + i];
+            for (int i = 0; i < 16; ++i) v[i] = v[i] * sg[i];
         }
-        wht16(v, a.logb);
+        wht16<LOGB>(v);
+        float *p = lds + 17 * c;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) lds[pad_idx(16 * c + i)] = v[i];
+        for (int i = 0; i < 16; ++i) p[i] = v[i];
     }
 
-    // Passes 1..: stages 16, 32, ... in order, 4 per pass.
-    for (int p = 1; 4 * p < a.logb; ++p) {
-        const int nb = min(4, a.logb - 4 * p);
-        const int span = 1 << nb;
-        const int sets = n >> nb;
-        const int lo_bits = 4 * p;
+    // Passes 1..3: stages 16, 32, ... in the reference's order, 4 per pass.
+    if constexpr (LOGB > 4) {
         __syncthreads();
-        for (int s = tid; s < sets; s += kThreads) {
-            const int low = s & ((1 << lo_bits) - 1);
-            const int high = s >> lo_bits;
-            const int base = (high << (lo_bits + nb)) + low;
-            float v[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (j < span) v[j] = lds[pad_idx(base + (j << lo_bits))];
-#pragma unroll
-            for (int st_ = 0; st_ < 4; ++st_) {
-                if (st_ >= nb) break;
-                const int h = 1 << st_;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    if ((j & h) == 0 && j + h < span) {
-                        const float u = v[j], w = v[j + h];
-                        v[j] = u + w;
-                        v[j + h] = u - w;
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (j < span) lds[pad_idx(base + (j << lo_bits))] = v[j];
-        }
+        wht_pass<LOGB, 1>(lds, n, tid);
+    }
+    if constexpr (LOGB > 8) {
+        __syncthreads();
+        wht_pass<LOGB, 2>(lds, n, tid);
+    }
+    if constexpr (LOGB > 12) {
+        __syncthreads();
+        wht_pass<LOGB, 3>(lds, n, tid);
     }
     __syncthreads();
 
@@ -141,25 +181,24 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     TO *y = STORE ? static_cast<TO *>(a.y) + row * n : nullptr;
     float amax = 0.f;
     for (int c = tid; c < chunks; c += kThreads) {
-        float v[16];
+        float v[16], sg[16];
+        if (INV && a.signs) ld16(a.signs + 16 * c, sg);
+        float *p = lds + 17 * c;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            float t = lds[pad_idx(16 * c + i)];
+            float t = p[i];
             if (INV && a.signs)
-                t = t * (a.signs[16 * c + i] * a.scale);
+                t = t * (sg[i] * a.scale);
             else
                 t = t * a.scale;
             v[i] = as_stored<TO>(t);
         }
-        if (STORE) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) st(y, 16LL * c + i, v[i]);
-        }
+        if (STORE) st16(y + 16LL * c, v);
         if (QUANT) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 amax = fmaxf(amax, fabsf(v[i]));
-                lds[pad_idx(16 * c + i)] = v[i];
+                p[i] = v[i];
             }
         }
     }
@@ -171,28 +210,53 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int8_t *q = a.xq + row * n;
     if (amax == 0.f) {
-        for (int i = tid; i < n; i += kThreads) q[i] = 0;
+        for (int c = tid; c < chunks; c += kThreads)
+            *reinterpret_cast<uint4 *>(q + 16 * c) = make_uint4(0, 0, 0, 0);
         if (tid == 0) a.dscale[row] = 0.f;
         return;
     }
     const float s = 127.0f / amax;
     for (int c = tid; c < chunks; c += kThreads) {
+        const float *p = lds + 17 * c;
+        uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            float t = rintf(lds[pad_idx(16 * c + i)] * s);
+            float t = rintf(p[i] * s);
             t = fminf(fmaxf(t, -127.f), 127.f);
-            q[16 * c + i] = static_cast<int8_t>(t);
+            w[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xffu) << (8 * (i & 3));
         }
+        *reinterpret_cast<uint4 *>(q + 16 * c) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     if (tid == 0) a.dscale[row] = amax / 127.0f;
 }
 
+template <typename TI, typename TO, bool INV, bool QUANT, bool STORE>
+void (*pick_logb(int logb))(FwhtArgs) {
+    switch (logb) {
+    case 1: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 1>;
+    case 2: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 2>;
+    case 3: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 3>;
+    case 4: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 4>;
+    case 5: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 5>;
+    case 6: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 6>;
+    case 7: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 7>;
+    case 8: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 8>;
+    case 9: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 9>;
+    case 10: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 10>;
+    case 11: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 11>;
+    case 12: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 12>;
+    case 13: return fwht_row_kernel<TI, TO, INV, QUANT, STORE, 13>;
+    default: return nullptr;
+    }
+}
+
 template <typename TI, typename TO, bool INV>
-int launch_t(const FwhtArgs &a, bool quant, bool store, hipStream_t s) {
+int launch_t(const FwhtArgs &a, int logb, bool quant, bool store, hipStream_t s) {
     const size_t lds = sizeof(float) * static_cast<size_t>(a.n + a.n / 16 + 1);
-    void (*kern)(FwhtArgs) = quant ? (store ? fwht_row_kernel<TI, TO, INV, true, true>
-                                            : fwht_row_kernel<TI, TO, INV, true, false>)
-                                   : fwht_row_kernel<TI, TO, INV, false, true>;
+    void (*kern)(FwhtArgs) = quant ? (store ? pick_logb<TI, TO, INV, true, true>(logb)
+                                            : pick_logb<TI, TO, INV, true, false>(logb))
+                                   : pick_logb<TI, TO, INV, false, true>(logb);
+    if (!kern) return fail(OURO_ERR_SHAPE, "ouro_fwht_rows: no kernel for log2(block) = %d", logb);
     if (lds > 64 * 1024) {
         // Rows longer than ~15K elements need the opt-in for >64 KiB of LDS.
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -207,8 +271,9 @@ int launch_t(const FwhtArgs &a, bool quant, bool store, hipStream_t s) {
 }
 
 template <typename TI, typename TO>
-int launch_io(const FwhtArgs &a, bool inv, bool quant, bool store, hipStream_t s) {
-    return inv ? launch_t<TI, TO, true>(a, quant, store, s) : launch_t<TI, TO, false>(a, quant, store, s);
+int launch_io(const FwhtArgs &a, int logb, bool inv, bool quant, bool store, hipStream_t s) {
+    return inv ? launch_t<TI, TO, true>(a, logb, quant, store, s)
+               : launch_t<TI, TO, false>(a, logb, quant, store, s);
 }
 
 }  // namespace
@@ -231,6 +296,8 @@ int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, siz
     if (!n || n % block) return fail(OURO_ERR_SHAPE, "ouro_fwht_rows: len %zu not multiple of block %zu", n, block);
     if (n % 16 || n > static_cast<size_t>(kMaxN))
         return fail(OURO_ERR_SHAPE, "ouro_fwht_rows: len %zu must be a multiple of 16 and <= %d", n, kMaxN);
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(signs)) % 16)
+        return fail(OURO_ERR_ALIGN, "ouro_fwht_rows: x, y and signs need 16-byte alignment");
     if (!rows) return OURO_OK;
     if (rows > 0x7fffffffULL) return fail(OURO_ERR_SHAPE, "ouro_fwht_rows: too many rows");
     FwhtArgs a{};
@@ -243,16 +310,15 @@ int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, siz
     a.n = static_cast<int>(n);
     int logb = 0;
     while ((size_t(1) << logb) < block) ++logb;
-    a.logb = logb;
     a.scale = 1.0f / sqrtf(static_cast<float>(block));  // hadamard.rs:43
     const bool inv = (flags & OURO_FWHT_INVERSE) != 0;
     const bool store = y != nullptr;
     hipStream_t s = as_stream(stream);
     const bool fi = x_dtype == OURO_DT_F32, fo = y_dtype == OURO_DT_F32;
-    if (fi && fo) return launch_io<float, float>(a, inv, quant, store, s);
-    if (fi && !fo) return launch_io<float, uint16_t>(a, inv, quant, store, s);
-    if (!fi && fo) return launch_io<uint16_t, float>(a, inv, quant, store, s);
-    return launch_io<uint16_t, uint16_t>(a, inv, quant, store, s);
+    if (fi && fo) return launch_io<float, float>(a, logb, inv, quant, store, s);
+    if (fi && !fo) return launch_io<float, uint16_t>(a, logb, inv, quant, store, s);
+    if (!fi && fo) return launch_io<uint16_t, float>(a, logb, inv, quant, store, s);
+    return launch_io<uint16_t, uint16_t>(a, logb, inv, quant, store, s);
 }
 
 }  // namespace ouro

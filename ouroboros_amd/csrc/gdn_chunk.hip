@@ -37,21 +37,24 @@ constexpr int kMaxSeq = 256;   // sequences per launch (cu_seqlens by value)
 
 constexpr int KP = kD + 8;     // bf16 row pitch of K, Q, S^T (272 B)
 constexpr int VP = kDVB + 8;   // bf16 row pitch of V (144 B)
-constexpr int FP = kC + 4;     // fp32 row pitch of 64x64 matrices (272 B)
+constexpr int FP = kC + 8;     // pitch of 64x64 matrices: fp32 (288 B) or bf16 hi/lo (144 B)
+constexpr int HL = kC * FP;    // elements of one bf16 plane (hi or lo) of a 64x64 matrix
 
 // LDS byte offsets.
+constexpr int MAT = kC * FP * 4;                  // bytes of a 64x64 fp32 (= hi+lo bf16) slot
 constexpr int OFF_K = 0;
-constexpr int OFF_Q = OFF_K + kC * KP * 2;
-constexpr int OFF_V = OFF_Q + kC * KP * 2;
-constexpr int OFF_A = OFF_V + kC * VP * 2;        // A, then R^T [j][s]
-constexpr int OFF_T = OFF_A + kC * FP * 4;
-constexpr int OFF_P = OFF_T + kC * FP * 4;        // Pt
-constexpr int OFF_SHI = OFF_P + kC * FP * 4;      // S0 hi, [j][i]
+constexpr int OFF_Q = OFF_K + kC * KP * 2;        // Q, then U~^T hi/lo
+constexpr int OFF_V = OFF_Q + MAT;
+constexpr int OFF_A = OFF_V + kC * VP * 2;        // A fp32, then R^T hi/lo
+constexpr int OFF_T = OFF_A + MAT;                // T fp32, then T hi/lo
+constexpr int OFF_P = OFF_T + MAT;                // Pt hi/lo
+constexpr int OFF_SHI = OFF_P + MAT;              // S0 hi, [j][i]
 constexpr int OFF_SLO = OFF_SHI + kDVB * KP * 2;  // S0 lo
-constexpr int OFF_U = OFF_SLO + kDVB * KP * 2;    // U^T [j][s]
-constexpr int OFF_RT = OFF_U + kDVB * FP * 4;     // 3 x 16 x 17 fp32 scratch
+constexpr int OFF_U = OFF_SLO + kDVB * KP * 2;    // U^T hi/lo
+constexpr int OFF_RT = OFF_U + MAT;               // 3 x 16 x 17 fp32 scratch
 constexpr int OFF_VEC = OFF_RT + 3 * 16 * 17 * 4; // nk, nq, g, beta
 constexpr int LDS_BYTES = OFF_VEC + 4 * kC * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a gfx950 workgroup");
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -78,31 +81,38 @@ __device__ __forceinline__ bf16x8 ld_bf8(const uint16_t *p) {
     return *reinterpret_cast<const bf16x8 *>(p);
 }
 
-// 8 fp32 from LDS, scaled per element, split into hi + lo bf16 operands.
-__device__ __forceinline__ void ld_split8(const float *p, const float *scale, bf16x8 &hi, bf16x8 &lo) {
-    const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
-    const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
-    float f[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): ~16 significant bits.
+__device__ __forceinline__ void split(float x, uint16_t &hi, uint16_t &lo) {
+    const __bf16 h = static_cast<__bf16>(x);
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x - static_cast<float>(h)));
+}
+
+// Store 4 consecutive values (along the contiguous axis) of a hi/lo matrix.
+__device__ __forceinline__ void st_split4(uint16_t *hl, int off, const f32x4 &v) {
+    uint16_t h[4], l[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float x = scale ? f[e] * scale[e] : f[e];
-        const __bf16 h = static_cast<__bf16>(x);
-        hi[e] = h;
-        lo[e] = static_cast<__bf16>(x - static_cast<float>(h));
-    }
+    for (int e = 0; e < 4; ++e) split(v[e], h[e], l[e]);
+    *reinterpret_cast<uint2 *>(hl + off) =
+        make_uint2(h[0] | (static_cast<uint32_t>(h[1]) << 16), h[2] | (static_cast<uint32_t>(h[3]) << 16));
+    *reinterpret_cast<uint2 *>(hl + HL + off) =
+        make_uint2(l[0] | (static_cast<uint32_t>(l[1]) << 16), l[2] | (static_cast<uint32_t>(l[3]) << 16));
 }
 
 __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     uint16_t *Kl = reinterpret_cast<uint16_t *>(lds + OFF_K);
     uint16_t *Ql = reinterpret_cast<uint16_t *>(lds + OFF_Q);
+    uint16_t *UWl = reinterpret_cast<uint16_t *>(lds + OFF_Q);  // U~^T hi/lo after phase 2
     uint16_t *Vl = reinterpret_cast<uint16_t *>(lds + OFF_V);
     float *Al = reinterpret_cast<float *>(lds + OFF_A);
+    uint16_t *Rl = reinterpret_cast<uint16_t *>(lds + OFF_A);   // R^T hi/lo after the solve
     float *Tl = reinterpret_cast<float *>(lds + OFF_T);
-    float *Pl = reinterpret_cast<float *>(lds + OFF_P);
+    uint16_t *Thl = reinterpret_cast<uint16_t *>(lds + OFF_T);  // T hi/lo after the solve
+    uint16_t *Pl = reinterpret_cast<uint16_t *>(lds + OFF_P);
     uint16_t *Shi = reinterpret_cast<uint16_t *>(lds + OFF_SHI);
     uint16_t *Slo = reinterpret_cast<uint16_t *>(lds + OFF_SLO);
-    float *Ul = reinterpret_cast<float *>(lds + OFF_U);
+    uint16_t *Ul = reinterpret_cast<uint16_t *>(lds + OFF_U);
     float *Rt = reinterpret_cast<float *>(lds + OFF_RT);
     float *nk = reinterpret_cast<float *>(lds + OFF_VEC);
     float *nq = nk + kC;
@@ -121,33 +131,14 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
 
     float *S = a.state + (static_cast<long long>(seq) * a.Hv + h) * kD * kD;
 
-    // Upper off-diagonal 16x16 blocks of T are never written: zero once.
-    for (int e = tid; e < kC * kC; e += kThreads) {
-        const int r = e / kC, c = e % kC;
-        if ((c >> 4) > (r >> 4)) Tl[r * FP + c] = 0.f;
-    }
-
-    // State tiles of this wave: 4 tiles of the 128 x 64 block, (ti, tj) with
-    // tile id 4*wave + u, ti = id / 4 (i rows), tj = id % 4 (j columns).
+    // State tiles of this wave: 4 tiles of the 128 x 64 block, tile id
+    // 4*wave + u, rows i from (id / 4) * 16, columns j from (id % 4) * 16.
     f32x4 st[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int id = 4 * wave + u;
         const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
         st[u] = *reinterpret_cast<const f32x4 *>(S + (jb + j) * kD + i0);
-        uint16_t hi[4], lo[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const __bf16 hb = static_cast<__bf16>(st[u][e]);
-            const __bf16 lb = static_cast<__bf16>(st[u][e] - static_cast<float>(hb));
-            hi[e] = __builtin_bit_cast(uint16_t, hb);
-            lo[e] = __builtin_bit_cast(uint16_t, lb);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            Shi[j * KP + i0 + e] = hi[e];
-            Slo[j * KP + i0 + e] = lo[e];
-        }
     }
 
     const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
@@ -155,9 +146,9 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
 
     for (int t0 = t_begin; t0 < t_end; t0 += kC) {
         const int n = min(kC, t_end - t0);
-        __syncthreads();  // previous chunk fully consumed K, Q, V, U
+        __syncthreads();  // the previous chunk is done with every LDS buffer
 
-        // ---- phase 0: chunk rows into LDS (rows >= n are zero) ----------
+        // ---- phase 0: chunk rows and S0 hi/lo into LDS -----------------
         for (int idx = tid; idx < kC * 16; idx += kThreads) {
             const int r = idx >> 4, c16 = idx & 15;
             uint4 kv = make_uint4(0, 0, 0, 0), qv = kv;
@@ -177,25 +168,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
                     a.v + (static_cast<long long>(t0 + r) * a.Hv + h) * kD + jb + 8 * c8);
             *reinterpret_cast<uint4 *>(Vl + r * VP + 8 * c8) = vv;
         }
-        float gate_l = 0.f;
-        if (wave == 2 && lane < n) gate_l = a.gate[static_cast<long long>(t0 + lane) * a.Hv + h];
-        if (wave == 3) bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
-        __syncthreads();
-
-        // ---- phase 1: row norms and cumulative log-decay -----------------
-        if (wave < 2) {
-            const uint16_t *row = (wave == 0 ? Kl : Ql) + lane * KP;
-            float ss = 0.f;
-            for (int i = 0; i < kD; ++i) {
-                const float x = bf(row[i]);
-                ss += x * x;
-            }
-            float sc = l2 ? 1.0f / (sqrtf(ss) + a.eps) : 1.0f;
-            if (wave == 1) sc *= qscale;
-            if (lane >= n) sc = 0.f;
-            (wave == 0 ? nk : nq)[lane] = sc;
-        } else if (wave == 2) {
-            float g = gate_l;  // inclusive scan over the 64 lanes
+        if (wave == 2) {  // inclusive scan of the log-decays over the chunk
+            float g = lane < n ? a.gate[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float o = __shfl_up(g, off, 64);
@@ -203,17 +177,52 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
             }
             gv[lane] = g;
         }
+        if (wave == 3) bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int id = 4 * wave + u;
+            const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) split(st[u][e], Shi[j * KP + i0 + e], Slo[j * KP + i0 + e]);
+        }
+        __syncthreads();
+
+        // ---- phase 1: row norms, 4 lanes per row ------------------------
+        {
+            const int row = tid >> 2, qq = tid & 3;  // rows 0..63 of K, 64..127 of Q
+            const uint16_t *rp = (row < kC ? Kl + row * KP : Ql + (row - kC) * KP) + 32 * qq;
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(rp + 8 * c);
+                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x0 = __uint_as_float(ws[e] << 16), x1 = __uint_as_float(ws[e] & 0xffff0000u);
+                    ss += x0 * x0 + x1 * x1;
+                }
+            }
+            ss += __shfl_xor(ss, 1, 64);
+            ss += __shfl_xor(ss, 2, 64);
+            if (qq == 0) {
+                const int r = row & (kC - 1);
+                float sc = l2 ? 1.0f / (sqrtf(ss) + a.eps) : 1.0f;
+                if (row >= kC) sc *= qscale;
+                if (r >= n) sc = 0.f;
+                (row < kC ? nk : nq)[r] = sc;
+            }
+        }
         __syncthreads();
 
         // ---- phase 2: G = K K^T, P = Q K^T, KS = K S0, QS = Q S0 ---------
-        f32x4 ks[2], qs[2];
-        f32x4 rr[2];  // R of the KS tiles, written after T is solved
+        f32x4 qs[2];
+        float *Rf = reinterpret_cast<float *>(lds + OFF_U);  // R fp32 [r][c] until phase 4
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int id = 2 * wave + u;
             const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;
             f32x4 g4 = {0, 0, 0, 0}, p4 = g4, k4 = g4, q4 = g4;
-#pragma unroll
+#pragma unroll 2
             for (int kk = 0; kk < kD / 32; ++kk) {
                 const int kc = kk * 32 + 8 * lg;
                 const bf16x8 ka = ld_bf8(Kl + (m0 + lr) * KP + kc);
@@ -228,19 +237,25 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
                 q4 = mfma(qa, sh, q4);
                 q4 = mfma(qa, sl, q4);
             }
-            ks[u] = k4;
             qs[u] = q4;
             const int c = n0 + lr;
+            const float gc = gv[c], nkc = nk[c];
+            f32x4 pt;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = m0 + 4 * lg + e;
-                float av = 0.f, pv = 0.f;
-                if (c < r) av = bv[r] * expf(gv[r] - gv[c]) * nk[r] * nk[c] * g4[e];
-                if (c <= r) pv = expf(gv[r] - gv[c]) * nq[r] * nk[c] * p4[e];
-                Al[r * FP + c] = av;
-                Pl[r * FP + c] = pv;
+                const float gr = gv[r];
+                const float dec = (c <= r) ? __expf(gr - gc) : 0.f;
+                Al[r * FP + c] = (c < r) ? bv[r] * dec * nk[r] * nkc * g4[e] : 0.f;
+                pt[e] = dec * nq[r] * nkc * p4[e];
                 // R[r][c] = beta_r V[r][c] - beta_r b_r nk_r KS[r][c]
-                rr[u][e] = bv[r] * bf(Vl[r * VP + c]) - bv[r] * expf(gv[r]) * nk[r] * k4[e];
+                Rf[r * FP + c] = bv[r] * bf(Vl[r * VP + c]) - bv[r] * __expf(gr) * nk[r] * k4[e];
+            }
+            // Pt is read row-major [r][s] as an A operand: 4 rows at column c
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = m0 + 4 * lg + e;
+                split(pt[e], Pl[r * FP + c], Pl[HL + r * FP + c]);
             }
         }
         __syncthreads();
@@ -259,6 +274,12 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
             }
 #pragma unroll
             for (int s = 0; s < 16; ++s) Tl[(16 * blk + s) * FP + 16 * blk + c] = t[s];
+        } else {
+            // upper off-diagonal blocks are zero
+            for (int e = tid - 64; e < kC * kC; e += kThreads - 64) {
+                const int r = e / kC, c = e % kC;
+                if ((c >> 4) > (r >> 4)) Tl[r * FP + c] = 0.f;
+            }
         }
         __syncthreads();
         for (int dd = 1; dd <= 3; ++dd) {
@@ -288,16 +309,32 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
             __syncthreads();
         }
 
-        // ---- phase 4: R^T into the A buffer -------------------------------
+        // ---- phase 4: T and R^T to hi/lo bf16 (each value split once) -------
+        {
+            // T: 8 values per thread, row r, columns 8*cq .. 8*cq+7
+            const int r = tid >> 3, cq = tid & 7;
+            const f32x4 t0v = *reinterpret_cast<const f32x4 *>(Tl + r * FP + 8 * cq);
+            const f32x4 t1v = *reinterpret_cast<const f32x4 *>(Tl + r * FP + 8 * cq + 4);
+            // R^T[j][s] hi/lo into the A slot (A is dead): this thread takes
+            // column j = tid / 8 and rows s = 8*(tid % 8) .. +7 of R.
+            const int j = tid >> 3, s0 = 8 * (tid & 7);
+            f32x4 r0, r1;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int id = 2 * wave + u;
-            const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;
-            *reinterpret_cast<f32x4 *>(Al + (n0 + lr) * FP + m0 + 4 * lg) = rr[u];
+            for (int e = 0; e < 4; ++e) {
+                r0[e] = Rf[(s0 + e) * FP + j];
+                r1[e] = Rf[(s0 + 4 + e) * FP + j];
+            }
+            st_split4(Rl, j * FP + s0, r0);
+            st_split4(Rl, j * FP + s0 + 4, r1);
+            __syncthreads();
+            st_split4(Thl, r * FP + 8 * cq, t0v);
+            st_split4(Thl, r * FP + 8 * cq + 4, t1v);
         }
         __syncthreads();
 
-        // ---- phase 5: U = T R ---------------------------------------------
+        // ---- phase 5: U = T R; store U^T and U~^T = (w o U)^T as hi/lo ------
+        const float gC = gv[n - 1];
+        const float bC = __expf(gC);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int id = 2 * wave + u;
@@ -306,18 +343,25 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
 #pragma unroll
             for (int kk = 0; kk < kC / 32; ++kk) {
                 const int kc = kk * 32 + 8 * lg;
-                bf16x8 ah, al, bh, bl;
-                ld_split8(Tl + (m0 + lr) * FP + kc, nullptr, ah, al);
-                ld_split8(Al + (n0 + lr) * FP + kc, nullptr, bh, bl);
+                const bf16x8 ah = ld_bf8(Thl + (m0 + lr) * FP + kc), al = ld_bf8(Thl + HL + (m0 + lr) * FP + kc);
+                const bf16x8 bh = ld_bf8(Rl + (n0 + lr) * FP + kc), bl = ld_bf8(Rl + HL + (n0 + lr) * FP + kc);
                 acc = mfma(ah, bh, acc);
                 acc = mfma(ah, bl, acc);
                 acc = mfma(al, bh, acc);
             }
-            *reinterpret_cast<f32x4 *>(Ul + (n0 + lr) * FP + m0 + 4 * lg) = acc;
+            const int off = (n0 + lr) * FP + m0 + 4 * lg;  // U^T[j][s], s = m0 + 4*lg + e
+            st_split4(Ul, off, acc);
+            f32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int sidx = m0 + 4 * lg + e;
+                w[e] = acc[e] * (nk[sidx] * __expf(gC - gv[sidx]));
+            }
+            st_split4(UWl, off, w);
         }
         __syncthreads();
 
-        // ---- phase 6: O = diag(b nq) QS + Pt U;  S = b_C S + K^T (w o U) ----
+        // ---- phase 6: O = diag(b nq) QS + Pt U;  S = b_C S + K^T U~ ----------
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int id = 2 * wave + u;
@@ -326,9 +370,8 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
 #pragma unroll
             for (int kk = 0; kk < kC / 32; ++kk) {
                 const int kc = kk * 32 + 8 * lg;
-                bf16x8 ah, al, bh, bl;
-                ld_split8(Pl + (m0 + lr) * FP + kc, nullptr, ah, al);
-                ld_split8(Ul + (n0 + lr) * FP + kc, nullptr, bh, bl);
+                const bf16x8 ah = ld_bf8(Pl + (m0 + lr) * FP + kc), al = ld_bf8(Pl + HL + (m0 + lr) * FP + kc);
+                const bf16x8 bh = ld_bf8(Ul + (n0 + lr) * FP + kc), bl = ld_bf8(Ul + HL + (n0 + lr) * FP + kc);
                 acc = mfma(ah, bh, acc);
                 acc = mfma(ah, bl, acc);
                 acc = mfma(al, bh, acc);
@@ -338,47 +381,27 @@ __global__ __launch_bounds__(kThreads) void gdn_chunk_kernel(ChunkArgs a) {
             for (int e = 0; e < 4; ++e) {
                 const int r = m0 + 4 * lg + e;
                 if (r < n) {
-                    const float o = expf(gv[r]) * nq[r] * qs[u][e] + acc[e];
+                    const float o = __expf(gv[r]) * nq[r] * qs[u][e] + acc[e];
                     a.out[(static_cast<long long>(t0 + r) * a.Hv + h) * kD + jb + c] = o;
                 }
             }
         }
-        const float gC = gv[n - 1];
-        const float bC = expf(gC);
-        float wsc[8];  // per-token weight nk_s exp(g_C - g_s) of this lane's k-run
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st[u] = st[u] * bC;
 #pragma unroll
         for (int kk = 0; kk < kC / 32; ++kk) {
             const int kc = kk * 32 + 8 * lg;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) wsc[e] = nk[kc + e] * expf(gC - gv[kc + e]);
-#pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int id = 4 * wave + u;
                 const int i0 = (id >> 2) * 16, j0 = (id & 3) * 16;
-                if (kk == 0) st[u] = st[u] * bC;
                 bf16x8 ka;  // K^T[i][s-run]: 8 strided bf16 of column i
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
                     ka[e] = __builtin_bit_cast(__bf16, Kl[(kc + e) * KP + i0 + lr]);
-                bf16x8 bh, bl;
-                ld_split8(Ul + (j0 + lr) * FP + kc, wsc, bh, bl);
+                const bf16x8 bh = ld_bf8(UWl + (j0 + lr) * FP + kc), bl = ld_bf8(UWl + HL + (j0 + lr) * FP + kc);
                 st[u] = mfma(ka, bh, st[u]);
                 st[u] = mfma(ka, bl, st[u]);
-            }
-        }
-        __syncthreads();  // everyone is done reading S hi/lo of this chunk
-
-        // new S0 hi/lo for the next chunk
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int id = 4 * wave + u;
-            const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const __bf16 hb = static_cast<__bf16>(st[u][e]);
-                const __bf16 lb = static_cast<__bf16>(st[u][e] - static_cast<float>(hb));
-                Shi[j * KP + i0 + e] = __builtin_bit_cast(uint16_t, hb);
-                Slo[j * KP + i0 + e] = __builtin_bit_cast(uint16_t, lb);
             }
         }
     }
