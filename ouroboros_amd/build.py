@@ -74,5 +74,25 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIB
 
 
+CPP_TEST_SRC = PKG.parent / "tests" / "cpp" / "reference_kats.cpp"
+CPP_TEST_BIN = PKG.parent / "tests" / "cpp" / "reference_kats"
+
+
+def build_cpp_tests(verbose: bool = False) -> Path:
+    """Compile the C++ reference-KAT program against the C++ host mirror
+    (include/ouro/infer.hpp) and libouro_hip.so; it runs on a GPU box."""
+    cxx = shutil.which("g++") or "g++"
+    cmd = [cxx, "-O2", "-std=c++17", "-Wall", f"-I{PKG.parent / 'include'}", str(CPP_TEST_SRC),
+           "-o", str(CPP_TEST_BIN), f"-L{LIB.parent}", "-louro_hip",
+           f"-Wl,-rpath,$ORIGIN/../../ouroboros_amd/lib", "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"C++ test build failed:\n{res.stdout}{res.stderr}")
+    if verbose:
+        print(f"built {CPP_TEST_BIN}")
+    return CPP_TEST_BIN
+
+
 if __name__ == "__main__":
     build_library(verbose=True)
+    build_cpp_tests(verbose=True)

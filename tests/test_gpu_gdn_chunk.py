@@ -85,7 +85,7 @@ def test_prefill_then_decode_matches_tokens(gpu, orc):
     q, k, v, gate, beta, state = inputs(rng, T, Hk, Hv, 1)
     qf, kf, vf = (quant.bf16_bits_to_f32(a) for a in (q, k, v))
     fl = GDN_L2NORM_QK | GDN_SCALE_Q
-    ref = np.ascontiguousarray(state[0])
+    ref = state[0].copy()  # the oracle updates its state in place
     want = orc.gdn_prefill_tokens(ref, qf, kf, vf, gate, beta, T, Hk, Hv, D, fl, 1e-6)
     sd = DeviceBuffer.from_host(state)
     out = DeviceBuffer((T - 1, Hv, D), np.float32)
