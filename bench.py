@@ -207,7 +207,7 @@ def bench_fwht(stream, steps, warmup):
 
 
 def bench_prefill(stream, steps, warmup):
-    from ouroboros_amd import quant
+    from ouroboros_amd import quant, qwen35
     from ouroboros_amd._lib import GDN_L2NORM_QK, GDN_SCALE_Q, call
     from ouroboros_amd.device import DeviceBuffer
 
@@ -221,10 +221,11 @@ def bench_prefill(stream, steps, warmup):
     state = DeviceBuffer.from_host((0.02 * rng.standard_normal((PF_SEQ, Hv, d * d))).astype(np.float32))
     out = DeviceBuffer((T, Hv, d), np.float32)
     cu = np.arange(PF_SEQ + 1, dtype=np.int32) * PF_LEN
+    ws = DeviceBuffer((qwen35.chunk_workspace_bytes(T, PF_SEQ, Hv, d, PF_C),), np.uint8)
 
     def step(_i):
         call("ouro_gdn_chunk_prefill", state.ptr, q.ptr, k.ptr, v.ptr, gate.ptr, beta.ptr, out.ptr,
-             cu.ctypes.data, PF_SEQ, T, Hk, Hv, d, PF_C, GDN_L2NORM_QK | GDN_SCALE_Q, 1e-6, stream)
+             cu.ctypes.data, PF_SEQ, T, Hk, Hv, d, PF_C, GDN_L2NORM_QK | GDN_SCALE_Q, 1e-6, ws.ptr, stream)
 
     return time_events(stream, step, max(3, steps // 5), 2)
 
@@ -340,6 +341,12 @@ def traffic_of(traffic: dict, prefix: str, grid: int | None = None):
     return best
 
 
+def traffic_sum(traffic: dict, prefixes: list[str]):
+    """HBM bytes of one call made of several kernels (None if any is unknown)."""
+    parts = [traffic_of(traffic, p) for p in prefixes]
+    return None if any(b is None for b in parts) else sum(parts)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -440,7 +447,7 @@ def main() -> int:
             "value": round(PF_T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_call": round(ms, 4),
             "config": "4 seqs x 4096 tokens packed varlen, chunk 64, Hk=16, Hv=32, d=128, bf16 q/k/v, fp32 state/out",
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_of(traffic, "gdn_chunk_kernel")},
+                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_sum(traffic, ["gdn_chunk_prep_kernel", "gdn_chunk_scan_kernel"])},
             "algorithmic_gflop": round(PF_FLOPS / 1e9, 2), "bytes": PF_BYTES, "hbm_GBs": round(gbs, 1),
             "frac_of_min_roofline": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
         }

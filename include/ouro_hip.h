@@ -244,15 +244,20 @@ int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype,
  * reference prefill, shell/src/bonsai.rs:48-52 driving run_delta,
  * qwen35.rs:1048-1158); inside each chunk of `chunk` (64) tokens it uses the
  * WY/UT form with bf16 MFMA contractions and fp32 accumulation.  d == 128.
- * Allocates nothing: the offsets travel as kernel arguments (launched in
- * slices of 256 sequences). */
+ * A state-independent pass over all chunks writes per-chunk records into
+ * `workspace` (device memory of ouro_gdn_chunk_workspace_bytes(T, N, Hv, d,
+ * chunk) bytes, 16-byte aligned; NULL = the library's per-device workspace,
+ * grown on demand).  Sequences are launched in slices of 256, offsets as
+ * kernel arguments. */
+size_t ouro_gdn_chunk_workspace_bytes(size_t T, size_t N, size_t Hv, size_t d,
+                                      size_t chunk);
 int ouro_gdn_chunk_prefill(float *state, const void *q, const void *k,
                            const void *v, const float *gate,
                            const float *beta, float *out,
                            const int32_t *cu_seqlens_host, size_t N,
                            size_t T, size_t Hk, size_t Hv, size_t d,
                            size_t chunk, unsigned flags, float eps,
-                           void *stream);
+                           void *workspace, void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Resident weights (GpuPool::upload_q6k / matvec, ouro-wgpu/src/lib.rs:   */

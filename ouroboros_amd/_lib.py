@@ -73,7 +73,8 @@ SIGNATURES = {
     "ouro_rotate_inv": (i32, [vp, vp, sz, sz, vp]),
     "ouro_delta_head_dim": (i32, [vp, sz, vp, vp, vp, f32, f32, vp, vp]),
     "ouro_gdn_decode": (i32, [vp, vp, vp, i32, vp, i32, vp, vp, vp, sz, sz, sz, sz, u32, f32, vp]),
-    "ouro_gdn_chunk_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, u32, f32, vp]),
+    "ouro_gdn_chunk_workspace_bytes": (sz, [sz, sz, sz, sz, sz]),
+    "ouro_gdn_chunk_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, u32, f32, vp, vp]),
     "ouro_weight_upload": (i32, [i32, vp, sz, sz, sz, f32, sz, C.POINTER(vp)]),
     "ouro_weight_free": (i32, [vp]),
     "ouro_weight_payload": (vp, [vp]),

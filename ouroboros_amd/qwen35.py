@@ -65,12 +65,22 @@ def gdn_chunk_prefill(state: DeviceBuffer, q: DeviceBuffer, k: DeviceBuffer, v: 
                       gate: DeviceBuffer, beta: DeviceBuffer, out: DeviceBuffer,
                       cu_seqlens: np.ndarray | None, T: int, Hk: int, Hv: int, d: int = S,
                       chunk: int = 64, flags: int = _lib.GDN_L2NORM_QK | _lib.GDN_SCALE_Q,
-                      eps: float = 1e-6, stream=None) -> None:
-    """Chunked prefill of packed varlen sequences (q, k, v bf16 as uint16)."""
+                      eps: float = 1e-6, workspace: DeviceBuffer | None = None, stream=None) -> None:
+    """Chunked prefill of packed varlen sequences (q, k, v bf16 as uint16).
+
+    ``workspace`` (optional) is a device buffer of at least
+    ``chunk_workspace_bytes(T, n, Hv)`` bytes; without it the library's
+    per-device workspace is used."""
     if cu_seqlens is None:
         cu, n = None, 1
     else:
         cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
         n = len(cu) - 1
     call("ouro_gdn_chunk_prefill", state.ptr, q.ptr, k.ptr, v.ptr, gate.ptr, beta.ptr, out.ptr,
-         cu.ctypes.data if cu is not None else None, n, T, Hk, Hv, d, chunk, flags, eps, stream)
+         cu.ctypes.data if cu is not None else None, n, T, Hk, Hv, d, chunk, flags, eps,
+         workspace.ptr if workspace is not None else None, stream)
+
+
+def chunk_workspace_bytes(T: int, N: int, Hv: int, d: int = S, chunk: int = 64) -> int:
+    """Bytes of the per-chunk records gdn_chunk_prefill writes (0 = unsupported shape)."""
+    return int(_lib.lib().ouro_gdn_chunk_workspace_bytes(T, N, Hv, d, chunk))

@@ -66,6 +66,16 @@ def test_i2_tiled_bytes_matches_oracle(orc):
         assert ops.i2_tiled_bytes(out_len, in_len) == want
 
 
+def test_chunk_workspace_bytes():
+    from ouroboros_amd import qwen35
+
+    rec = 17408  # T hi/lo (16 KiB) + nk, nq, g, padded to 256 B
+    assert qwen35.chunk_workspace_bytes(16384, 4, 32) == (256 + 4 + 1) * 32 * rec
+    assert qwen35.chunk_workspace_bytes(100, 1000, 2) == (1 + 256 + 1) * 2 * rec
+    assert qwen35.chunk_workspace_bytes(64, 1, 4, d=64) == 0
+    assert qwen35.chunk_workspace_bytes(64, 1, 4, chunk=32) == 0
+
+
 def test_no_oracle_in_product():
     # The product never imports, links or loads the oracle.
     for p in list((ROOT / "ouroboros_amd").rglob("*.py")) + list((ROOT / "ouroboros_amd" / "csrc").glob("*")):

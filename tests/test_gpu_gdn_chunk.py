@@ -28,7 +28,7 @@ def inputs(rng, T, Hk, Hv, N):
     return q, k, v, gate, beta, state
 
 
-def run_both(orc, cu, Hk, Hv, flags, seed=0):
+def run_both(orc, cu, Hk, Hv, flags, seed=0, workspace=False):
     rng = np.random.default_rng(seed)
     T = int(cu[-1])
     N = len(cu) - 1
@@ -45,9 +45,12 @@ def run_both(orc, cu, Hk, Hv, flags, seed=0):
             want_state[s] = st
     sd = DeviceBuffer.from_host(state)
     out = DeviceBuffer((max(T, 1), Hv, D), np.float32, zero=True)
+    ws = None
+    if workspace:
+        ws = DeviceBuffer((qwen35.chunk_workspace_bytes(T, N, Hv),), np.uint8)
     qwen35.gdn_chunk_prefill(sd, DeviceBuffer.from_host(q), DeviceBuffer.from_host(k), DeviceBuffer.from_host(v),
                              DeviceBuffer.from_host(gate), DeviceBuffer.from_host(beta), out,
-                             np.asarray(cu, np.int32), T, Hk, Hv, flags=flags, eps=1e-6)
+                             np.asarray(cu, np.int32), T, Hk, Hv, flags=flags, eps=1e-6, workspace=ws)
     return out.download()[:T], want_out, sd.download(), want_state
 
 
@@ -67,6 +70,17 @@ def test_ragged_varlen(gpu, orc, cu):
 def test_flags(gpu, orc, flags):
     got, want, gs, ws = run_both(orc, [0, 200, 333], 2, 4, flags, seed=3)
     assert rel(got, want) < TOL and rel(gs, ws) < TOL
+
+
+def test_many_sequences_caller_workspace(gpu, orc):
+    # 300 ragged sequences (two launch slices of up to 256), caller-owned
+    # workspace of exactly chunk_workspace_bytes, empty sequences included.
+    rng = np.random.default_rng(21)
+    lens = rng.integers(0, 140, 300)
+    lens[[0, 17, 255, 256]] = 0
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    got, want, gs, ws = run_both(orc, cu, 1, 2, GDN_L2NORM_QK | GDN_SCALE_Q, seed=22, workspace=True)
+    assert rel(got, want) < TOL and rel(gs, ws) < TOL, (rel(got, want), rel(gs, ws))
 
 
 def test_config4_shape(gpu, orc):
