@@ -23,12 +23,11 @@
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
 // and computes what does not depend on the state: row norms, g, A and T,
 // written to a workspace record (T as hi/lo bf16 plus the vectors).
-// gdn_chunk_scan_kernel then walks the chunks of a sequence in order: one
-// 512-thread workgroup owns (sequence, v-head, 64 of the 128 state columns)
-// -- output column j of the recurrence only touches state column j, so the
-// two column halves of a head are independent chains -- and does only the
-// state-dependent contractions, four barriers per chunk, with the next
-// chunk's rows loaded into registers while the current one computes.
+// gdn_chunk_scan_kernel then walks the chunks of a sequence in order.  Output
+// column j of the recurrence only touches state column j, so 16-column
+// stripes of the state are independent chains: a "chain" wave keeps one
+// stripe in registers and runs K S0 -> R -> U -> S update, while a paired
+// "output" wave forms Pt and O for the same stripe; two barriers per chunk.
 #include "common.hpp"
 
 namespace ouro {
@@ -36,44 +35,49 @@ namespace {
 
 constexpr int kD = 128;           // d_k = d_v (qwen35.rs:8)
 constexpr int kC = 64;            // chunk length
-constexpr int kDVB = 64;          // state columns per scan workgroup
-constexpr int kScanThreads = 512; // 8 waves
+constexpr int kDVB = 64;          // state columns per scan workgroup (16 per wave)
+constexpr int kScanThreads = 512; // 4 chain + 4 output waves
 constexpr int kPrepThreads = 256; // 4 waves
 constexpr int kMaxSeq = 256;      // sequences per launch (offsets by value)
 
-constexpr int KP = kD + 8;        // bf16 row pitch of K, Q, S^T (272 B)
-constexpr int VP = kDVB + 8;      // bf16 row pitch of V (144 B)
+constexpr int KP = kD + 8;        // bf16 row pitch of K, Q (272 B)
+constexpr int KTP = kC + 8;       // bf16 row pitch of K^T (144 B)
 constexpr int FP = kC + 8;        // pitch of 64x64 matrices: fp32 (288 B) or bf16 planes (144 B)
 constexpr int HL = kC * FP;       // elements of one bf16 plane (hi or lo) of a 64x64 matrix
-constexpr int MAT = kC * FP * 4;  // bytes of a 64x64 fp32 (= hi+lo bf16) slot
 
 // Workspace record of one (chunk, v-head): T hi [64][64] bf16, T lo, then
-// nk, nq, g [64] fp32 each, padded to a multiple of 256 B.
+// per-row coefficient vectors [64] fp32 (below), padded to 256 B.  With
+// g the in-chunk cumsum of the gate, g_C its last entry, and for row r
+// the tile reference g_{16 floor(r/16)}:
+//   beta, rk = beta e^g nk, w = nk e^(g_C - g), so = e^g nq,
+//   rho = e^(g - g_ref) nq, c_b = e^(g_16b - g) nk for rows < 16b (b = 1..3),
+//   g, nq, nk.
 constexpr int REC_T = 2 * kC * kC * 2;
-constexpr size_t kRec = 17408;
-static_assert(REC_T + 3 * kC * 4 <= static_cast<int>(kRec), "record size");
+enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_RHO = 256, V_C1 = 320, V_G = 512, V_NQ = 576,
+       V_NK = 640, kVec = 704 };
+constexpr size_t kRec = 19456;
+static_assert(REC_T + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
 
-// Scan kernel LDS byte offsets.
-constexpr int OFF_K = 0;
-constexpr int OFF_Q = OFF_K + kC * KP * 2;        // Q, then U~^T hi/lo
-constexpr int OFF_V = OFF_Q + MAT;
-constexpr int OFF_T = OFF_V + kC * VP * 2;        // T hi/lo
-constexpr int OFF_R = OFF_T + MAT;                // R^T hi/lo
-constexpr int OFF_P = OFF_R + MAT;                // Pt hi/lo
-constexpr int OFF_SHI = OFF_P + MAT;              // S0 hi, [j][i]
-constexpr int OFF_SLO = OFF_SHI + kDVB * KP * 2;  // S0 lo
-constexpr int OFF_U = OFF_SLO + kDVB * KP * 2;    // U^T hi/lo
-constexpr int OFF_VEC = OFF_U + MAT;              // nk, nq, g, beta
-constexpr int SCAN_LDS = OFF_VEC + 4 * kC * 4;
+// Scan kernel LDS byte offsets.  K and T are read in the first half of a
+// chunk only and refilled in the second; Q, K^T and the vectors are read in
+// both halves and double-buffered; X passes S0 and U (hi/lo operand
+// registers) from each chain wave to its output wave.
+constexpr int S_K = 0;                          // K [64][KP]
+constexpr int S_T = S_K + kC * KP * 2;          // T hi, T lo [64][FP]
+constexpr int S_Q = S_T + 2 * kC * FP * 2;      // Q [2][64][KP]
+constexpr int S_KT = S_Q + 2 * kC * KP * 2;     // K^T [2][128][KTP]
+constexpr int S_VEC = S_KT + 2 * kD * KTP * 2;  // vectors [2][kVec]
+constexpr int S_X = S_VEC + 2 * kVec * 4;       // [4 waves][S0 hi/lo 8 KiB, U hi/lo 4 KiB]
+constexpr int X_WAVE = 12288;
+constexpr int SCAN_LDS = S_X + 4 * X_WAVE;
 static_assert(SCAN_LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
 
-// Prep kernel LDS byte offsets.
-constexpr int PO_K = 0;
-constexpr int PO_A = PO_K + kC * KP * 2;
-constexpr int PO_T = PO_A + MAT;
-constexpr int PO_RT = PO_T + MAT;                 // 3 x 16 x 17 fp32
-constexpr int PO_VEC = PO_RT + 3 * 16 * 17 * 4;   // nk, nq, g, beta
-constexpr int PREP_LDS = PO_VEC + 4 * kC * 4;
+// Prep kernel: one wave per (chunk, v-head), four per workgroup; each wave
+// has A (then T) [64][AP] fp32 and its vectors in LDS.
+constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int AP = kC + 4;                         // fp32 row pitch of A / T
+constexpr int PW_BYTES = kC * AP * 4 + 4 * kC * 4; // per-wave LDS
+constexpr int PREP_LDS = kPrepWaves * PW_BYTES;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -113,15 +117,6 @@ __device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
     return a | (static_cast<uint32_t>(b) << 16);
 }
 
-// Store 4 consecutive values (along the contiguous axis) of a hi/lo matrix.
-__device__ __forceinline__ void st_split4(uint16_t *hl, int off, const f32x4 &v) {
-    uint16_t h[4], l[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) split(v[e], h[e], l[e]);
-    *reinterpret_cast<uint2 *>(hl + off) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-    *reinterpret_cast<uint2 *>(hl + HL + off) = make_uint2(pack2(l[0], l[1]), pack2(l[2], l[3]));
-}
-
 __device__ __forceinline__ int khead(const ChunkArgs &a, int h) {
     return (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
 }
@@ -142,24 +137,76 @@ __device__ __forceinline__ float sumsq32(const uint4 (&w)[4]) {
 }
 
 // ---------------------------------------------------------------------------
-// Prep: one 256-thread workgroup per (chunk, v-head).
+// Scan: one 512-thread workgroup per (sequence, v-head, 64 state columns).
+// Chain wave w (0..3) owns state columns jb + 16w .. +15, all 128 rows, in
+// registers and runs the recurrence for them: K S0, R, U = T R, and
+// S = b_C S0 + K^T U~, every contraction an MFMA whose operands are its own
+// accumulators or chunk rows in LDS.  Output wave 4 + w forms Pt (its own
+// copy, in registers) while the chain computes U, then takes S0 and U from
+// chain wave w through LDS and computes O = so (Q S0) + Pt U.  The chunk's
+// rows are loaded into registers one chunk ahead and staged into LDS in the
+// second half of the chunk before.
+//
+// Operand layout.  v_mfma_f32_16x16x32_bf16 lane l (r = l % 16, g = l / 16)
+// holds A[r][8g..8g+7], B[8g..8g+7][r] and D[4g..4g+3][r].  A 64-row D
+// result (four 16-row tiles) is used directly as the B operand of the next
+// contraction over those 64 rows: for the 32-row slab of tiles 2q, 2q+1 the
+// lane's eight k values are rows 32q + 4g + {0..3} and 32q + 16 + 4g + {0..3}
+// (tile 2q, then tile 2q+1).  The LDS operand on the other side is read
+// with the same row order (ld_perm), so the sum runs over the same k set.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a) {
+
+// A operand row[base + 4g .. +3] ++ row[base + 16 + 4g .. +3].
+__device__ __forceinline__ bf16x8 ld_perm(const uint16_t *row, int base, int lg) {
+    const uint2 x = *reinterpret_cast<const uint2 *>(row + base + 4 * lg);
+    const uint2 y = *reinterpret_cast<const uint2 *>(row + base + 16 + 4 * lg);
+    return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// x = hi + lo for two values at once: hi = bf16(x) (round to nearest even),
+// lo = bf16(x - hi); packed as bf16 pairs.
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+    const float ha = __uint_as_float(h << 16), hb = __uint_as_float(h & 0xffff0000u);
+    hi = h;
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a - ha, b - hb}, bf16x2));
+}
+
+// Two D tiles (rows 32q + 4g + e and 32q + 16 + 4g + e) as hi and lo B operands.
+__device__ __forceinline__ void split8(const f32x4 &t0, const f32x4 &t1, bf16x8 &hi, bf16x8 &lo) {
+    uint4 h, l;
+    split2(t0[0], t0[1], h.x, l.x);
+    split2(t0[2], t0[3], h.y, l.y);
+    split2(t1[0], t1[1], h.z, l.z);
+    split2(t1[2], t1[3], h.w, l.w);
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+// ---------------------------------------------------------------------------
+// Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K stays
+// in registers in MFMA operand layout (lane r + 16 g holds
+// K[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so G = K K^T
+// needs no LDS; A^T goes to the wave's LDS and T = (I + A)^-1 is solved with
+// one column of T per lane.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    uint16_t *Kl = reinterpret_cast<uint16_t *>(lds + PO_K);
-    float *Al = reinterpret_cast<float *>(lds + PO_A);
-    float *Tl = reinterpret_cast<float *>(lds + PO_T);
-    float *Rt = reinterpret_cast<float *>(lds + PO_RT);
-    float *nk = reinterpret_cast<float *>(lds + PO_VEC);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int item = blockIdx.x * kPrepWaves + wave;
+    if (item >= items) return;  // whole wave
+    float *Al = reinterpret_cast<float *>(lds + wave * PW_BYTES);
+    float *nk = Al + kC * AP;
     float *nq = nk + kC;
     float *gv = nq + kC;
     float *bv = gv + kC;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int lr = lane & 15, lg = lane >> 4;
-    const int cg = blockIdx.x, h = blockIdx.y;
-    int lo = 0, hi = a.nseq;  // sequence of chunk cg: largest s with coff[s] <= cg
+    const int cg = item / a.Hv, h = item % a.Hv;
+    int lo = 0, hi = a.nseq;  // sequence of chunk cg: coff[lo] <= cg < coff[lo + 1]
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
         if (a.coff[mid] <= cg) lo = mid; else hi = mid;
@@ -171,27 +218,32 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
     const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
 
-    // K rows to LDS (zero beyond n); row norms of K and Q, 4 lanes per row.
-    for (int idx = tid; idx < kC * 16; idx += kPrepThreads) {
-        const int r = idx >> 4, c16 = idx & 15;
-        uint4 kv = make_uint4(0, 0, 0, 0);
-        if (r < n) kv = *reinterpret_cast<const uint4 *>(a.k + (static_cast<long long>(t0 + r) * a.Hk + kh) * kD + 8 * c16);
-        *reinterpret_cast<uint4 *>(Kl + r * KP + 8 * c16) = kv;
-    }
-    {
-        const int r = tid >> 2, qq = tid & 3;
-        uint4 w[4] = {};
-        if (r < n) {
-            const uint4 *qp = reinterpret_cast<const uint4 *>(a.q + (static_cast<long long>(t0 + r) * a.Hk + kh) * kD + 32 * qq);
+    // K (kept) and Q (norms only) rows 16aa + lr, columns 32kk + 8lg .. +7
+    uint4 kr[4][4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) w[c] = qp[c];
+    for (int aa = 0; aa < 4; ++aa) {
+        const int row = 16 * aa + lr;
+        uint4 qv[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            kr[aa][kk] = qv[kk] = make_uint4(0, 0, 0, 0);
+            if (row < n) {
+                const long long off = (static_cast<long long>(t0 + row) * a.Hk + kh) * kD + 32 * kk + 8 * lg;
+                kr[aa][kk] = *reinterpret_cast<const uint4 *>(a.k + off);
+                qv[kk] = *reinterpret_cast<const uint4 *>(a.q + off);
+            }
         }
-        float ss = sumsq32(w);
-        ss += __shfl_xor(ss, 1, 64);
-        ss += __shfl_xor(ss, 2, 64);
-        if (qq == 0) nq[r] = r < n ? (l2 ? 1.0f / (sqrtf(ss) + a.eps) : 1.0f) * qscale : 0.f;
+        float sk = sumsq32(kr[aa]), sq = sumsq32(qv);
+        sk += __shfl_xor(sk, 16, 64);
+        sk += __shfl_xor(sk, 32, 64);
+        sq += __shfl_xor(sq, 16, 64);
+        sq += __shfl_xor(sq, 32, 64);
+        if (lg == 0) {
+            nk[row] = row < n ? (l2 ? 1.0f / (sqrtf(sk) + a.eps) : 1.0f) : 0.f;
+            nq[row] = row < n ? (l2 ? 1.0f / (sqrtf(sq) + a.eps) : 1.0f) * qscale : 0.f;
+        }
     }
-    if (wave == 0) {  // inclusive scan of the log-decays
+    {  // inclusive scan of the log-decays, one token per lane
         float g = lane < n ? a.gate[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -199,344 +251,485 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
             if (lane >= off) g += o;
         }
         gv[lane] = g;
+        bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
     }
-    if (wave == 1) bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
-    __syncthreads();
-    {
-        const int r = tid >> 2, qq = tid & 3;
-        uint4 w[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) w[c] = *reinterpret_cast<const uint4 *>(Kl + r * KP + 32 * qq + 8 * c);
-        float ss = sumsq32(w);
-        ss += __shfl_xor(ss, 1, 64);
-        ss += __shfl_xor(ss, 2, 64);
-        if (qq == 0) nk[r] = r < n ? (l2 ? 1.0f / (sqrtf(ss) + a.eps) : 1.0f) : 0.f;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
 
-    // A = strictly lower (beta_s exp(g_s - g_j) nk_s nk_j K K^T); 4 tiles per wave.
+    // A[r][c] = beta_r exp(g_r - g_c) nk_r nk_c (K K^T)[r][c], c < r, stored
+    // transposed (Al[c][r]); tiles on and below the diagonal only (the solve
+    // never reads r <= c).
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int id = 4 * wave + u;
-        const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;
-        f32x4 g4 = {0, 0, 0, 0};
-        if (n0 <= m0) {  // tiles above the diagonal are zero (uniform per wave)
+    for (int aa = 0; aa < 4; ++aa) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bv + 16 * aa + 4 * lg);
+        const f32x4 g4r = *reinterpret_cast<const f32x4 *>(gv + 16 * aa + 4 * lg);
+        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(nk + 16 * aa + 4 * lg);
 #pragma unroll
-            for (int kk = 0; kk < kD / 32; ++kk) {
-                const int kc = kk * 32 + 8 * lg;
-                g4 = mfma(ld_bf8(Kl + (m0 + lr) * KP + kc), ld_bf8(Kl + (n0 + lr) * KP + kc), g4);
+        for (int bb = 0; bb <= aa; ++bb) {
+            f32x4 g4 = {0, 0, 0, 0};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+                g4 = mfma(__builtin_bit_cast(bf16x8, kr[aa][kk]), __builtin_bit_cast(bf16x8, kr[bb][kk]), g4);
+            const int c = 16 * bb + lr;
+            const float gc = gv[c], kc = nk[c];
+            f32x4 av;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 16 * aa + 4 * lg + e;
+                av[e] = (c < r) ? b4[e] * __expf(g4r[e] - gc) * k4[e] * kc * g4[e] : 0.f;
             }
-        }
-        const int c = n0 + lr;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int r = m0 + 4 * lg + e;
-            Al[r * FP + c] = (c < r) ? bv[r] * __expf(gv[r] - gv[c]) * nk[r] * nk[c] * g4[e] : 0.f;
+            *reinterpret_cast<f32x4 *>(Al + c * AP + 16 * aa + 4 * lg) = av;
         }
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
 
-    // T = (I + A)^-1: 16x16 diagonal blocks by forward substitution, then
-    // T_ij = -T_ii sum_{k=j..i-1} A_ik T_kj in order of i - j.
-    if (wave == 0) {
-        const int blk = lg, c = lr;
-        float t[16];
+    // Column `lane` of T = (I + A)^-1 by right-looking substitution: once
+    // t_j is final, t_s -= A[s][j] t_j for every s > j (independent FMAs).
+    float t[kC];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-            float acc = (s == c) ? 1.f : 0.f;
-            const float *arow = Al + (16 * blk + s) * FP + 16 * blk;
+    for (int s2 = 0; s2 < kC; ++s2) t[s2] = (s2 == lane) ? 1.f : 0.f;
 #pragma unroll
-            for (int j = 0; j < s; ++j) acc -= arow[j] * t[j];
-            t[s] = acc;
-        }
+    for (int j = 0; j < kC - 1; ++j) {
+        const float tj = t[j];
+        const float *acol = Al + j * AP;  // A[.][j]
 #pragma unroll
-        for (int s = 0; s < 16; ++s) Tl[(16 * blk + s) * FP + 16 * blk + c] = t[s];
-    } else {
-        for (int e = tid - 64; e < kC * kC; e += kPrepThreads - 64) {
-            const int r = e / kC, c = e % kC;
-            if ((c >> 4) > (r >> 4)) Tl[r * FP + c] = 0.f;
+        for (int s4 = (j + 1) & ~3; s4 < kC; s4 += 4) {
+            const f32x4 a4 = *reinterpret_cast<const f32x4 *>(acol + s4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (s4 + e > j) t[s4 + e] -= a4[e] * tj;
         }
     }
-    __syncthreads();
-    for (int dd = 1; dd <= 3; ++dd) {
-        const int nblk = 4 - dd;
-        for (int e = tid; e < nblk * 256; e += kPrepThreads) {
-            const int bi = e >> 8, ar = (e >> 4) & 15, bc = e & 15;
-            const int i = dd + bi, j = bi;
-            float acc = 0.f;
-            for (int kb = j; kb < i; ++kb) {
-                const float *arow = Al + (16 * i + ar) * FP + 16 * kb;
-                const float *tcol = Tl + (16 * kb) * FP + 16 * j + bc;
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int m = 0; m < 16; ++m) acc += arow[m] * tcol[m * FP];
-            }
-            Rt[bi * 272 + ar * 17 + bc] = acc;
-        }
-        __syncthreads();
-        for (int e = tid; e < nblk * 256; e += kPrepThreads) {
-            const int bi = e >> 8, ar = (e >> 4) & 15, bc = e & 15;
-            const int i = dd + bi, j = bi;
-            const float *trow = Tl + (16 * i + ar) * FP + 16 * i;
-            float acc = 0.f;
-#pragma unroll
-            for (int m = 0; m < 16; ++m) acc += trow[m] * Rt[bi * 272 + m * 17 + bc];
-            Tl[(16 * i + ar) * FP + 16 * j + bc] = -acc;
-        }
-        __syncthreads();
-    }
+    for (int s2 = 0; s2 < kC; ++s2) Al[s2 * AP + lane] = t[s2];
+    __builtin_amdgcn_wave_barrier();
 
     // Record: T hi/lo row-major [64][64], then nk, nq, g.
-    unsigned char *rec = a.ws + (static_cast<size_t>(cg) * a.Hv + h) * kRec;
-    {
-        const int r = tid >> 2, c0 = 16 * (tid & 3);
-        uint32_t hw[8], lw[8];
+    unsigned char *rec = a.ws + static_cast<size_t>(item) * kRec;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            uint16_t h0, l0, h1, l1;
-            split(Tl[r * FP + c0 + 2 * e], h0, l0);
-            split(Tl[r * FP + c0 + 2 * e + 1], h1, l1);
-            hw[e] = pack2(h0, h1);
-            lw[e] = pack2(l0, l1);
-        }
-        uint4 *th = reinterpret_cast<uint4 *>(rec + (r * kC + c0) * 2);
-        uint4 *tlo = reinterpret_cast<uint4 *>(rec + kC * kC * 2 + (r * kC + c0) * 2);
-        th[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        th[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
-        tlo[0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-        tlo[1] = make_uint4(lw[4], lw[5], lw[6], lw[7]);
+    for (int i = 0; i < 8; ++i) {
+        const int id = lane + 64 * i;
+        const int r = id >> 3, c0 = 8 * (id & 7);
+        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(Al + r * AP + c0);
+        const f32x4 x1 = *reinterpret_cast<const f32x4 *>(Al + r * AP + c0 + 4);
+        bf16x8 th, tl;
+        split8(x0, x1, th, tl);
+        reinterpret_cast<bf16x8 *>(rec)[id] = th;
+        reinterpret_cast<bf16x8 *>(rec + kC * kC * 2)[id] = tl;
     }
-    if (tid < 3 * kC) reinterpret_cast<float *>(rec + REC_T)[tid] = nk[tid];  // nk, nq, g are contiguous
+    {
+        float *rv = reinterpret_cast<float *>(rec + REC_T);
+        const float g = gv[lane], b = bv[lane], kn = nk[lane], qn = nq[lane];
+        const float gC = gv[n - 1], eg = __expf(g);
+        rv[V_BETA + lane] = b;
+        rv[V_RK + lane] = b * eg * kn;
+        rv[V_W + lane] = kn * __expf(gC - g);
+        rv[V_SO + lane] = eg * qn;
+        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]) * qn;
+#pragma unroll
+        for (int bb = 1; bb < 4; ++bb)
+            rv[V_C1 + 64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
+        rv[V_G + lane] = g;
+        rv[V_NQ + lane] = qn;
+        rv[V_NK + lane] = kn;
+    }
 }
 
-// ---------------------------------------------------------------------------
-// Scan: one 512-thread workgroup per (sequence, v-head, 64 state columns).
-// ---------------------------------------------------------------------------
-
-// The rows of one chunk, in registers between their load and their LDS store.
-struct ChunkRegs {
-    uint4 k[2], q[2], v, t[2];
-    float vec;
+// Chain-wave prefetch: K rows (as pairs, for the K^T store) and T of the
+// next chunk.  Chain thread tc, item it (0, 1): id = tc + 256 it covers rows
+// 2p, 2p+1 (p = id % 32) and bf16 columns 8c .. 8c+7 (c = id / 32).
+struct ChainRegs {
+    uint4 k[2][2], t[4];
+    uint16_t v[16];  // V of this wave's stripe in D layout: v[4a + e] = V[16a + 4g + e][jw + r]
 };
 
-__device__ __forceinline__ void load_chunk(const ChunkArgs &a, ChunkRegs &r, int tid, int t0, int n, int kh,
-                                           int h, int jb, const unsigned char *rec) {
+// Output-wave prefetch: Q rows and the coefficient vectors of the next chunk.
+struct OutRegs {
+    uint4 q[4], vec;
+};
+
+// base + a 32-bit byte offset (lets the loads use a uniform base address)
+template <typename T>
+__device__ __forceinline__ const T &at(const void *base, unsigned byte_off) {
+    return *reinterpret_cast<const T *>(static_cast<const char *>(base) + byte_off);
+}
+
+// Rows at or past n load row n - 1 (always valid, n >= 1) and are zeroed
+// when staged into LDS (or used), so the loads carry no branches and nothing
+// waits for them before the stage.
+__device__ __forceinline__ uint4 zero_if(bool z, uint4 v) {
+    return z ? make_uint4(0, 0, 0, 0) : v;
+}
+
+__device__ __forceinline__ void load_chain(const ChunkArgs &a, ChainRegs &r, int tc, int t0, int n, int kh, int h,
+                                           int jw, int lr, int lg, const unsigned char *rec) {
+    // uniform chunk bases, 32-bit lane offsets
+    const uint16_t *kb = a.k + (static_cast<long long>(t0) * a.Hk + kh) * kD;
+    const unsigned ks = static_cast<unsigned>(a.Hk) * kD;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int idx = tid + kScanThreads * p;
-        const int row = idx >> 4, c16 = idx & 15;
-        r.k[p] = r.q[p] = make_uint4(0, 0, 0, 0);
-        if (row < n) {
-            const long long off = (static_cast<long long>(t0 + row) * a.Hk + kh) * kD + 8 * c16;
-            r.k[p] = *reinterpret_cast<const uint4 *>(a.k + off);
-            r.q[p] = *reinterpret_cast<const uint4 *>(a.q + off);
+    for (int it = 0; it < 2; ++it) {
+        const int id = tc + 256 * it;
+        const int p = id & 31, c = id >> 5;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const unsigned row = static_cast<unsigned>(min(2 * p + w, n - 1));
+            r.k[it][w] = at<uint4>(kb, 2u * (row * ks + 8u * c));
         }
-        r.t[p] = reinterpret_cast<const uint4 *>(rec)[idx];
     }
-    {
-        const int row = tid >> 3, c8 = tid & 7;
-        r.v = make_uint4(0, 0, 0, 0);
-        if (row < n) r.v = *reinterpret_cast<const uint4 *>(a.v + (static_cast<long long>(t0 + row) * a.Hv + h) * kD + jb + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec)[tc + 256 * i];
+    const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
+    const unsigned vs = static_cast<unsigned>(a.Hv) * kD;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const unsigned row = static_cast<unsigned>(min(16 * (i >> 2) + 4 * lg + (i & 3), n - 1));
+        r.v[i] = at<uint16_t>(vb, 2u * (row * vs + static_cast<unsigned>(lr)));
     }
-    r.vec = 0.f;
-    if (tid < 3 * kC) {
-        r.vec = reinterpret_cast<const float *>(rec + REC_T)[tid];
-    } else if (tid < 4 * kC) {
-        const int row = tid - 3 * kC;
-        if (row < n) r.vec = a.beta[static_cast<long long>(t0 + row) * a.Hv + h];
+}
+
+__device__ __forceinline__ void store_chain(const ChainRegs &r, unsigned char *lds, int kt_buf, int tc, int n) {
+    uint16_t *K = reinterpret_cast<uint16_t *>(lds + S_K);
+    uint32_t *KT = reinterpret_cast<uint32_t *>(lds + S_KT + kt_buf * kD * KTP * 2);
+    uint16_t *T = reinterpret_cast<uint16_t *>(lds + S_T);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int id = tc + 256 * it;
+        const int p = id & 31, c = id >> 5;
+        const uint4 k0 = zero_if(2 * p >= n, r.k[it][0]), k1 = zero_if(2 * p + 1 >= n, r.k[it][1]);
+        *reinterpret_cast<uint4 *>(K + (2 * p) * KP + 8 * c) = k0;
+        *reinterpret_cast<uint4 *>(K + (2 * p + 1) * KP + 8 * c) = k1;
+        // K^T[8c + e][2p .. 2p+1]: one 32-bit store per column e
+        const uint32_t x0[4] = {k0.x, k0.y, k0.z, k0.w};
+        const uint32_t x1[4] = {k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            KT[((8 * c + 2 * e) * KTP + 2 * p) >> 1] = (x0[e] & 0xffffu) | (x1[e] << 16);
+            KT[((8 * c + 2 * e + 1) * KTP + 2 * p) >> 1] = (x0[e] >> 16) | (x1[e] & 0xffff0000u);
+        }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = tc + 256 * i;
+        const int plane = idx >> 9, e = idx & 511;  // T hi then lo, 8 bf16 per uint4
+        *reinterpret_cast<uint4 *>(T + plane * HL + (e >> 3) * FP + 8 * (e & 7)) = r.t[i];
+    }
+}
+
+__device__ __forceinline__ void load_out(const ChunkArgs &a, OutRegs &r, int to, int t0, int n, int kh,
+                                         const unsigned char *rec) {
+    const uint16_t *qb = a.q + (static_cast<long long>(t0) * a.Hk + kh) * kD;
+    const unsigned qs = static_cast<unsigned>(a.Hk) * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = to + 256 * i;
+        const unsigned row = static_cast<unsigned>(min(idx >> 4, n - 1));
+        r.q[i] = at<uint4>(qb, 2u * (row * qs + 8u * (idx & 15)));
+    }
+    r.vec = reinterpret_cast<const uint4 *>(rec + REC_T)[min(to, kVec / 4 - 1)];
+}
+
+__device__ __forceinline__ void store_out(const OutRegs &r, unsigned char *lds, int buf, int to, int n) {
+    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q + buf * kC * KP * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = to + 256 * i;
+        *reinterpret_cast<uint4 *>(Q + (idx >> 4) * KP + 8 * (idx & 15)) = zero_if((idx >> 4) >= n, r.q[i]);
+    }
+    if (to < kVec / 4) reinterpret_cast<uint4 *>(lds + S_VEC + buf * kVec * 4)[to] = r.vec;
+}
+
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+
+// Materialise a value at this point of the program (no code).
+__device__ __forceinline__ void pin(bf16x8 &x) {
+    uint4 u = __builtin_bit_cast(uint4, x);
+    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
+    x = __builtin_bit_cast(bf16x8, u);
 }
 
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    uint16_t *Kl = reinterpret_cast<uint16_t *>(lds + OFF_K);
-    uint16_t *Ql = reinterpret_cast<uint16_t *>(lds + OFF_Q);
-    uint16_t *UWl = reinterpret_cast<uint16_t *>(lds + OFF_Q);  // U~^T hi/lo once Q is consumed
-    uint16_t *Vl = reinterpret_cast<uint16_t *>(lds + OFF_V);
-    uint16_t *Tl = reinterpret_cast<uint16_t *>(lds + OFF_T);
-    uint16_t *Rl = reinterpret_cast<uint16_t *>(lds + OFF_R);
-    uint16_t *Pl = reinterpret_cast<uint16_t *>(lds + OFF_P);
-    uint16_t *Shi = reinterpret_cast<uint16_t *>(lds + OFF_SHI);
-    uint16_t *Slo = reinterpret_cast<uint16_t *>(lds + OFF_SLO);
-    uint16_t *Ul = reinterpret_cast<uint16_t *>(lds + OFF_U);
-    float *vec = reinterpret_cast<float *>(lds + OFF_VEC);
-    const float *nk = vec, *nq = vec + kC, *gv = vec + 2 * kC, *bv = vec + 3 * kC;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int lr = lane & 15, lg = lane >> 4;  // MFMA row/col and k-group of this lane
+    const int lr = lane & 15, lg = lane >> 4;
+    const bool chain = wave < 4;                      // wave-uniform role
+    const int tr = tid & 255;                         // thread index within the role
     const int seq = blockIdx.x / (a.Hv * 2);
     const int h = (blockIdx.x / 2) % a.Hv;
-    const int jb = (blockIdx.x % 2) * kDVB;
+    const int jw = (blockIdx.x % 2) * kDVB + 16 * (wave & 3);  // first state column of this stripe
     const int kh = khead(a, h);
     const int t_begin = a.cu[seq], t_end = a.cu[seq + 1];
     if (t_end <= t_begin) return;  // empty sequence: state unchanged (uniform per block)
     const int nchunks = (t_end - t_begin + kC - 1) / kC;
     auto record = [&](int c) { return a.ws + (static_cast<size_t>(a.coff[seq] + c) * a.Hv + h) * kRec; };
+    uint4 *X = reinterpret_cast<uint4 *>(lds + S_X + (wave & 3) * X_WAVE);  // [slot][lane]
 
-    float *S = a.state + (static_cast<long long>(seq) * a.Hv + h) * kD * kD;
-
-    // State tiles of this wave: 4 tiles of the 128 x 64 block, tile id
-    // 4*wave + u, rows i from (id / 4) * 16, columns j from (id % 4) * 16.
-    f32x4 st[4];
+    // Both roles run the same number of chunks and barriers (two per chunk);
+    // their registers are disjoint because each role has its own loop.
+    if (chain) {
+        // state tile t holds S[16t + 4g + e][jw + r]
+        float *S = a.state + (static_cast<long long>(seq) * a.Hv + h) * kD * kD + static_cast<long long>(jw + lr) * kD;
+        f32x4 st[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int id = 4 * wave + u;
-        const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
-        st[u] = *reinterpret_cast<const f32x4 *>(S + (jb + j) * kD + i0);
-    }
+        for (int t = 0; t < 8; ++t) st[t] = ld4(S + 16 * t + 4 * lg);
+        ChainRegs cr;
+        load_chain(a, cr, tr, t_begin, min(kC, t_end - t_begin), kh, h, jw, lr, lg, record(0));
+        store_chain(cr, lds, 0, tr, min(kC, t_end - t_begin));
 
-    ChunkRegs cr;
-    load_chunk(a, cr, tid, t_begin, min(kC, t_end - t_begin), kh, h, jb, record(0));
+        for (int c = 0; c < nchunks; ++c) {
+            const int t0 = t_begin + c * kC;
+            const int n = min(kC, t_end - t0);
+            const int b = c & 1;
+            const bool more = c + 1 < nchunks;
+            const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
+            const uint16_t *T = reinterpret_cast<const uint16_t *>(lds + S_T);
+            const uint16_t *KT = reinterpret_cast<const uint16_t *>(lds + S_KT + b * kD * KTP * 2);
+            const float *cv = reinterpret_cast<const float *>(lds + S_VEC + b * kVec * 4);
+            __syncthreads();  // chunk c is in K, T and buffer b; X is free
 
-    for (int c = 0; c < nchunks; ++c) {
-        const int t0 = t_begin + c * kC;
-        const int n = min(kC, t_end - t0);
-        __syncthreads();  // the previous chunk is done with every LDS buffer
-
-        // ---- rows of this chunk and S0 hi/lo into LDS ---------------------
+            // ---- first half: S0 -> X, KS, R, U -> X, U~ ---------------------
+            uint16_t vcur[16];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int idx = tid + kScanThreads * p;
-            const int row = idx >> 4, c16 = idx & 15;
-            *reinterpret_cast<uint4 *>(Kl + row * KP + 8 * c16) = cr.k[p];
-            *reinterpret_cast<uint4 *>(Ql + row * KP + 8 * c16) = cr.q[p];
-            const int plane = idx >> 9, e = idx & 511;  // T hi then lo, 8 bf16 per uint4
-            *reinterpret_cast<uint4 *>(Tl + plane * HL + (e >> 3) * FP + 8 * (e & 7)) = cr.t[p];
+            for (int i = 0; i < 16; ++i) vcur[i] = (16 * (i >> 2) + 4 * lg + (i & 3)) < n ? cr.v[i] : 0;
+            if (more) load_chain(a, cr, tr, t0 + kC, min(kC, t_end - t0 - kC), kh, h, jw, lr, lg, record(c + 1));
+            const float bC = __expf(cv[V_G + n - 1]);
+
+            bf16x8 sh[4], sl[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
+                X[(2 * q) * 64 + lane] = __builtin_bit_cast(uint4, sh[q]);
+                X[(2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, sl[q]);
+            }
+            f32x4 ks[4], rr[4];
+#pragma unroll
+            for (int aa = 0; aa < 4; ++aa) ks[aa] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                bf16x8 ka[4];
+#pragma unroll
+                for (int aa = 0; aa < 4; ++aa) ka[aa] = ld_perm(K + (16 * aa + lr) * KP, 32 * q, lg);
+#pragma unroll
+                for (int aa = 0; aa < 4; ++aa) ks[aa] = mfma(ka[aa], sh[q], ks[aa]);
+#pragma unroll
+                for (int aa = 0; aa < 4; ++aa) ks[aa] = mfma(ka[aa], sl[q], ks[aa]);
+            }
+#pragma unroll
+            for (int aa = 0; aa < 4; ++aa) {
+                const f32x4 b4 = ld4(cv + V_BETA + 16 * aa + 4 * lg);
+                const f32x4 r4 = ld4(cv + V_RK + 16 * aa + 4 * lg);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rr[aa][e] = b4[e] * bf(vcur[4 * aa + e]) - r4[e] * ks[aa][e];
+            }
+            bf16x8 rh[2], rl[2];
+            split8(rr[0], rr[1], rh[0], rl[0]);
+            split8(rr[2], rr[3], rh[1], rl[1]);
+            f32x4 u[4];
+#pragma unroll
+            for (int aa = 0; aa < 4; ++aa) u[aa] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {  // T is lower triangular: s-tile aa needs slabs q <= aa / 2
+                bf16x8 th[4], tl[4];
+#pragma unroll
+                for (int aa = 2 * q; aa < 4; ++aa) {
+                    th[aa] = ld_perm(T + (16 * aa + lr) * FP, 32 * q, lg);
+                    tl[aa] = ld_perm(T + HL + (16 * aa + lr) * FP, 32 * q, lg);
+                }
+#pragma unroll
+                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(th[aa], rh[q], u[aa]);
+#pragma unroll
+                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(th[aa], rl[q], u[aa]);
+#pragma unroll
+                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(tl[aa], rh[q], u[aa]);
+            }
+            bf16x8 wh[2], wl[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                bf16x8 uh, ul;
+                split8(u[2 * q], u[2 * q + 1], uh, ul);
+                X[512 + (2 * q) * 64 + lane] = __builtin_bit_cast(uint4, uh);
+                X[512 + (2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, ul);
+                f32x4 w0 = u[2 * q], w1 = u[2 * q + 1];
+                const f32x4 c0 = ld4(cv + V_W + 32 * q + 4 * lg), c1 = ld4(cv + V_W + 32 * q + 16 + 4 * lg);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    w0[e] *= c0[e];
+                    w1[e] *= c1[e];
+                }
+                split8(w0, w1, wh[q], wl[q]);
+            }
+
+            __syncthreads();  // X holds S0 and U of chunk c; K and T may be refilled
+
+            // ---- second half: S = b_C S0 + K^T U~, then stage chunk c + 1 ----
+#pragma unroll
+            for (int t = 0; t < 8; ++t) st[t] = st[t] * bC;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                bf16x8 kt[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) kt[t] = ld_perm(KT + (16 * t + lr) * KTP, 32 * q, lg);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) st[t] = mfma(kt[t], wh[q], st[t]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) st[t] = mfma(kt[t], wl[q], st[t]);
+            }
+            if (more) store_chain(cr, lds, b ^ 1, tr, min(kC, t_end - t0 - kC));
         }
-        *reinterpret_cast<uint4 *>(Vl + (tid >> 3) * VP + 8 * (tid & 7)) = cr.v;
-        if (tid < 4 * kC) vec[tid] = cr.vec;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int id = 4 * wave + u;
-            const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
-            uint16_t hh[4], ll[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) split(st[u][e], hh[e], ll[e]);
-            *reinterpret_cast<uint2 *>(Shi + j * KP + i0) = make_uint2(pack2(hh[0], hh[1]), pack2(hh[2], hh[3]));
-            *reinterpret_cast<uint2 *>(Slo + j * KP + i0) = make_uint2(pack2(ll[0], ll[1]), pack2(ll[2], ll[3]));
-        }
-        __syncthreads();
+        for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4 *>(S + 16 * t + 4 * lg) = st[t];
+    } else {
+        OutRegs orr;
+        load_out(a, orr, tr, t_begin, min(kC, t_end - t_begin), kh, record(0));
+        store_out(orr, lds, 0, tr, min(kC, t_end - t_begin));
 
-        // next chunk's rows: the loads fly while this chunk computes
-        if (c + 1 < nchunks)
-            load_chunk(a, cr, tid, t0 + kC, min(kC, t_end - t0 - kC), kh, h, jb, record(c + 1));
+        for (int c = 0; c < nchunks; ++c) {
+            const int t0 = t_begin + c * kC;
+            const int n = min(kC, t_end - t0);
+            const int b = c & 1;
+            const bool more = c + 1 < nchunks;
+            const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
+            const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q + b * kC * KP * 2);
+            const float *cv = reinterpret_cast<const float *>(lds + S_VEC + b * kVec * 4);
+            __syncthreads();  // chunk c is in K, T and buffer b
 
-        // ---- phase A: P^T = K Q^T, KS = K S0, QS^T = S0^T Q^T -------------
-        f32x4 qs[2];
+            // ---- first half: Pt operands (r-tile b, s-slab q), slots in order
+            // (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) -------------------------------
+            // P^T = K Q^T tiles (s-tile aa <= r-tile bb), tile (aa, bb) at
+            // pt[bb (bb + 1) / 2 + aa]; every K and Q operand loaded once.
+            f32x4 pt[10];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int id = 2 * wave + u;
-            const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;
-            f32x4 p4 = {0, 0, 0, 0}, k4 = p4, q4 = p4;
-#pragma unroll 2
+            for (int i = 0; i < 10; ++i) pt[i] = f32x4{0, 0, 0, 0};
+#pragma unroll
             for (int kk = 0; kk < kD / 32; ++kk) {
                 const int kc = kk * 32 + 8 * lg;
-                const bf16x8 ka = ld_bf8(Kl + (m0 + lr) * KP + kc);
-                const bf16x8 qb = ld_bf8(Ql + (n0 + lr) * KP + kc);
-                const bf16x8 sh = ld_bf8(Shi + (n0 + lr) * KP + kc), sl = ld_bf8(Slo + (n0 + lr) * KP + kc);
-                const bf16x8 sha = ld_bf8(Shi + (m0 + lr) * KP + kc), sla = ld_bf8(Slo + (m0 + lr) * KP + kc);
-                p4 = mfma(ka, qb, p4);
-                k4 = mfma(ka, sh, k4);
-                k4 = mfma(ka, sl, k4);
-                q4 = mfma(sha, qb, q4);
-                q4 = mfma(sla, qb, q4);
-            }
-            qs[u] = q4;
-            // lane holds rows s = m0 + 4*lg + e of column n0 + lr
-            const int col = n0 + lr;
-            f32x4 pt, rv;
+                bf16x8 kv[4], qv[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int sr = m0 + 4 * lg + e;
-                // Pt[r][s] with r = col: exp(g_r - g_s) nq_r nk_s P[r][s], s <= r
-                pt[e] = (sr <= col) ? __expf(gv[col] - gv[sr]) * nq[col] * nk[sr] * p4[e] : 0.f;
-                // R[s][j] with j = col: beta_s V[s][j] - beta_s b_s nk_s KS[s][j]
-                rv[e] = bv[sr] * bf(Vl[sr * VP + col]) - bv[sr] * __expf(gv[sr]) * nk[sr] * k4[e];
+                for (int x = 0; x < 4; ++x) {
+                    kv[x] = ld_bf8(K + (16 * x + lr) * KP + kc);
+                    qv[x] = ld_bf8(Q + (16 * x + lr) * KP + kc);
+                }
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                    for (int aa = 0; aa <= bb; ++aa) pt[bb * (bb + 1) / 2 + aa] = mfma(kv[aa], qv[bb], pt[bb * (bb + 1) / 2 + aa]);
             }
-            st_split4(Pl, col * FP + m0 + 4 * lg, pt);  // Pt row-major [r][s]
-            st_split4(Rl, col * FP + m0 + 4 * lg, rv);  // R^T [j][s]
-        }
-        __syncthreads();
+            bf16x8 ph[6], pl[6];
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const int r = 16 * bb + lr;  // this lane's r in the P^T tiles
+                const float rho = cv[V_RHO + r], gr = cv[V_G + r], nqr = cv[V_NQ + r];
+                f32x4 ps[4];
+#pragma unroll
+                for (int aa = 0; aa < 4; ++aa) {
+                    if (aa > bb) {
+                        ps[aa] = f32x4{0, 0, 0, 0};
+                        continue;
+                    }
+                    ps[aa] = pt[bb * (bb + 1) / 2 + aa];
+                    if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
+                        const f32x4 cb = ld4(cv + V_C1 + 64 * (bb - 1) + 16 * aa + 4 * lg);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ps[aa][e] *= rho * cb[e];
+                    } else {  // diagonal tile: s <= r only
+                        const f32x4 gs = ld4(cv + V_G + 16 * aa + 4 * lg), ks = ld4(cv + V_NK + 16 * aa + 4 * lg);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int sr = 16 * aa + 4 * lg + e;
+                            const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
+                            ps[aa][e] = sr <= r ? ev * nqr * ks[e] * ps[aa][e] : 0.f;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q <= bb / 2; ++q) {
+                    const int slot = (bb < 2) ? bb : 2 * (bb - 1) + q;
+                    split8(ps[2 * q], ps[2 * q + 1], ph[slot], pl[slot]);
+                }
+            }
 
-        // ---- phase B: U = T R; store U^T and U~^T = (w o U)^T as hi/lo ------
-        const float gC = gv[n - 1];
-        const float bC = __expf(gC);
+            // keep the Pt scaling and split in this half (ahead of the barrier)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int id = 2 * wave + u;
-            const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;
-            f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-            for (int kk = 0; kk < kC / 32; ++kk) {
-                const int kc = kk * 32 + 8 * lg;
-                const bf16x8 ah = ld_bf8(Tl + (m0 + lr) * FP + kc), al = ld_bf8(Tl + HL + (m0 + lr) * FP + kc);
-                const bf16x8 bh = ld_bf8(Rl + (n0 + lr) * FP + kc), bl = ld_bf8(Rl + HL + (n0 + lr) * FP + kc);
-                acc = mfma(ah, bh, acc);
-                acc = mfma(ah, bl, acc);
-                acc = mfma(al, bh, acc);
+            for (int i = 0; i < 6; ++i) {
+                pin(ph[i]);
+                pin(pl[i]);
             }
-            const int off = (n0 + lr) * FP + m0 + 4 * lg;  // U^T[j][s], s = m0 + 4*lg + e
-            st_split4(Ul, off, acc);
-            f32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int sr = m0 + 4 * lg + e;
-                w[e] = acc[e] * (nk[sr] * __expf(gC - gv[sr]));
-            }
-            st_split4(UWl, off, w);
-        }
-        __syncthreads();
+            __syncthreads();  // X holds S0 and U of chunk c
 
-        // ---- phase C: O^T = U^T Pt^T + diag-scaled QS^T;  S = b_C S + K^T U~ --
+            // next chunk's Q and vectors: loaded here, after this wave's O
+            // stores of the chunk before have had a half chunk to drain
+            if (more) load_out(a, orr, tr, t0 + kC, min(kC, t_end - t0 - kC), kh, record(c + 1));
+            // ---- second half: O = so (Q S0) + Pt U, then stage chunk c + 1 ----
+            bf16x8 sh[4], sl[4], uh[2], ul[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int id = 2 * wave + u;
-            const int m0 = (id >> 2) * 16, n0 = (id & 3) * 16;  // m0: j block, n0: r block
-            f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-            for (int kk = 0; kk < kC / 32; ++kk) {
-                const int kc = kk * 32 + 8 * lg;
-                const bf16x8 ah = ld_bf8(Ul + (m0 + lr) * FP + kc), al = ld_bf8(Ul + HL + (m0 + lr) * FP + kc);
-                const bf16x8 bh = ld_bf8(Pl + (n0 + lr) * FP + kc), bl = ld_bf8(Pl + HL + (n0 + lr) * FP + kc);
-                acc = mfma(ah, bh, acc);
-                acc = mfma(ah, bl, acc);
-                acc = mfma(al, bh, acc);
+            for (int q = 0; q < 4; ++q) {
+                sh[q] = __builtin_bit_cast(bf16x8, X[(2 * q) * 64 + lane]);
+                sl[q] = __builtin_bit_cast(bf16x8, X[(2 * q + 1) * 64 + lane]);
             }
-            const int r = n0 + lr;
-            if (r < n) {
-                const float sc = __expf(gv[r]) * nq[r];
-                f32x4 o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = sc * qs[u][e] + acc[e];
-                *reinterpret_cast<f32x4 *>(a.out + (static_cast<long long>(t0 + r) * a.Hv + h) * kD + jb + m0 + 4 * lg) = o;
+            for (int q = 0; q < 2; ++q) {
+                uh[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q) * 64 + lane]);
+                ul[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q + 1) * 64 + lane]);
             }
+            f32x4 o[4];
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) o[bb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                bf16x8 qa[4];
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) qa[bb] = ld_perm(Q + (16 * bb + lr) * KP, 32 * q, lg);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sh[q], o[bb]);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sl[q], o[bb]);
+            }
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const f32x4 so = ld4(cv + V_SO + 16 * bb + 4 * lg);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[bb][e] *= so[e];
+            }
+            // Pt U over s-slab q for r-tiles bb with q <= bb / 2; slot of (bb, q)
+            // in (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) order
+#pragma unroll
+            for (int pass = 0; pass < 3; ++pass) {
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) {
+#pragma unroll
+                    for (int q = 0; q <= bb / 2; ++q) {
+                        const int slot = (bb < 2) ? bb : 2 * (bb - 1) + q;
+                        if (pass == 0) o[bb] = mfma(ph[slot], uh[q], o[bb]);
+                        if (pass == 1) o[bb] = mfma(ph[slot], ul[q], o[bb]);
+                        if (pass == 2) o[bb] = mfma(pl[slot], uh[q], o[bb]);
+                    }
+                }
+            }
+            {
+                float *ob = a.out + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
+                const unsigned os = static_cast<unsigned>(a.Hv) * kD;
+                if (n == kC) {
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
+                                4u * (static_cast<unsigned>(16 * bb + 4 * lg + e) * os + static_cast<unsigned>(lr))) = o[bb][e];
+                } else {
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int row = 16 * bb + 4 * lg + e;
+                            if (row < n)
+                                *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
+                                    4u * (static_cast<unsigned>(row) * os + static_cast<unsigned>(lr))) = o[bb][e];
+                        }
+                }
+            }
+            if (more) store_out(orr, lds, b ^ 1, tr, min(kC, t_end - t0 - kC));
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) st[u] = st[u] * bC;
-#pragma unroll
-        for (int kk = 0; kk < kC / 32; ++kk) {
-            const int kc = kk * 32 + 8 * lg;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int id = 4 * wave + u;
-                const int i0 = (id >> 2) * 16, j0 = (id & 3) * 16;
-                bf16x8 ka;  // K^T[i][s-run]: 8 strided bf16 of column i
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    ka[e] = __builtin_bit_cast(__bf16, Kl[(kc + e) * KP + i0 + lr]);
-                const bf16x8 bh = ld_bf8(UWl + (j0 + lr) * FP + kc), bl = ld_bf8(UWl + HL + (j0 + lr) * FP + kc);
-                st[u] = mfma(ka, bh, st[u]);
-                st[u] = mfma(ka, bl, st[u]);
-            }
-        }
-    }
-
-    // final state back to HBM
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int id = 4 * wave + u;
-        const int i0 = (id >> 2) * 16 + 4 * lg, j = (id & 3) * 16 + lr;
-        *reinterpret_cast<f32x4 *>(S + (jb + j) * kD + i0) = st[u];
     }
 }
 
@@ -617,8 +810,9 @@ int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v,
         }
         const int chunks = a.coff[ns];
         if (chunks == 0) continue;
-        hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(Hv)),
-                           dim3(kPrepThreads), PREP_LDS, as_stream(stream), a);
+        const int items = chunks * static_cast<int>(Hv);
+        hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(static_cast<unsigned>((items + kPrepWaves - 1) / kPrepWaves)),
+                           dim3(kPrepThreads), PREP_LDS, as_stream(stream), a, items);
         int st = check_launch("gdn_chunk_prep_kernel");
         if (st) return st;
         hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(static_cast<unsigned>(ns * Hv * 2)), dim3(kScanThreads),
