@@ -21,13 +21,13 @@
 // products carry ~16 mantissa bits.  T is solved in fp32 on the VALU.
 //
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
-// and computes what does not depend on the state: row norms, g, A and T,
-// written to a workspace record (T as hi/lo bf16 plus the vectors).
-// gdn_chunk_scan_kernel then walks the chunks of a sequence in order.  Output
-// column j of the recurrence only touches state column j, so 16-column
-// stripes of the state are independent chains: a "chain" wave keeps one
-// stripe in registers and runs K S0 -> R -> U -> S update, while a paired
-// "output" wave forms Pt and O for the same stripe; two barriers per chunk.
+// and computes what does not depend on the state: row norms, g, T and Pt,
+// written to a workspace record.  gdn_chunk_scan_kernel then walks the chunks
+// of a sequence in order.  Output column j of the recurrence only touches
+// state column j, so 16-column stripes of the state are independent chains:
+// a "chain" wave keeps one stripe in registers and runs K S0 -> R -> U ->
+// S update, while a paired "output" wave forms O for the same stripe; two
+// barriers per chunk.
 #include "common.hpp"
 
 namespace ouro {
@@ -41,46 +41,51 @@ constexpr int kPrepThreads = 256; // 4 waves
 constexpr int kMaxSeq = 256;      // sequences per launch (offsets by value)
 
 constexpr int KP = kD + 8;        // bf16 row pitch of K, Q (272 B)
-constexpr int KTP = kC + 8;       // bf16 row pitch of K^T (144 B)
-constexpr int FP = kC + 8;        // pitch of 64x64 matrices: fp32 (288 B) or bf16 planes (144 B)
-constexpr int HL = kC * FP;       // elements of one bf16 plane (hi or lo) of a 64x64 matrix
+constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free 8-byte reads)
 
-// Workspace record of one (chunk, v-head): T hi [64][64] bf16, T lo, then
-// per-row coefficient vectors [64] fp32 (below), padded to 256 B.  With
-// g the in-chunk cumsum of the gate, g_C its last entry, and for row r
-// the tile reference g_{16 floor(r/16)}:
-//   beta, rk = beta e^g nk, w = nk e^(g_C - g), so = e^g nq,
-//   rho = e^(g - g_ref) nq, c_b = e^(g_16b - g) nk for rows < 16b (b = 1..3),
-//   g, nq, nk.
-constexpr int REC_T = 2 * kC * kC * 2;
-enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_RHO = 256, V_C1 = 320, V_G = 512, V_NQ = 576,
-       V_NK = 640, kVec = 704 };
-constexpr size_t kRec = 19456;
-static_assert(REC_T + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
+// Workspace record of one (chunk, v-head), 256-byte aligned, everything the
+// scan reads in the lane order of its MFMA operands:
+//   T as A operands [slot][hi, lo][64 lanes] x 16 B                  12 KiB
+//   Pt as A operands [slot][hi, lo][64 lanes] x 16 B                 12 KiB
+//   vectors [64] fp32: beta, rk = beta e^g nk, w = nk e^(g_C - g),
+//   so = e^g nq, g                                                 1280 B
+// T slots are (s-tile a, t-slab q) = (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
+// (T is lower triangular: slab q is zero for a < 2q); Pt slots are
+// (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
+constexpr int REC_T = 0;
+constexpr int REC_P = 12 * 64 * 16;
+constexpr int REC_V = REC_P + 12 * 64 * 16;
+enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_G = 256, kVec = 320 };
+constexpr size_t kRec = 26112;
+static_assert(REC_V + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
 
-// Scan kernel LDS byte offsets.  K and T are read in the first half of a
-// chunk only and refilled in the second; Q, K^T and the vectors are read in
-// both halves and double-buffered; X passes S0 and U (hi/lo operand
-// registers) from each chain wave to its output wave.
+// Scan kernel LDS byte offsets.  K and the T operands are read in the first
+// half of a chunk only and refilled in the second; the Pt operands (of the
+// chunk before, read in the first half) likewise; K^T, Q and the vectors are
+// double-buffered; X passes S0 and U (hi/lo operand registers) from each
+// chain wave to its output wave.
 constexpr int S_K = 0;                          // K [64][KP]
-constexpr int S_T = S_K + kC * KP * 2;          // T hi, T lo [64][FP]
-constexpr int S_Q = S_T + 2 * kC * FP * 2;      // Q [2][64][KP]
+constexpr int S_Q = S_K + kC * KP * 2;          // Q [2][64][KP]
 constexpr int S_KT = S_Q + 2 * kC * KP * 2;     // K^T [2][128][KTP]
 constexpr int S_VEC = S_KT + 2 * kD * KTP * 2;  // vectors [2][kVec]
-constexpr int S_X = S_VEC + 2 * kVec * 4;       // [4 waves][S0 hi/lo 8 KiB, U hi/lo 4 KiB]
+constexpr int S_T = S_VEC + 2 * kVec * 4;       // T operands [12][64] x 16 B
+constexpr int S_P = S_T + 12 * 64 * 16;         // Pt operands [12][64] x 16 B
+constexpr int S_X = S_P + 12 * 64 * 16;         // [4 waves][S0 hi/lo 8 KiB, U hi/lo 4 KiB]
 constexpr int X_WAVE = 12288;
 constexpr int SCAN_LDS = S_X + 4 * X_WAVE;
 static_assert(SCAN_LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
 
 // Prep kernel: one wave per (chunk, v-head), four per workgroup; each wave
-// has A (then T) [64][AP] fp32 and its vectors in LDS.
+// has A (then T) [64][AP] fp32 and eight vectors [64] in LDS.
 constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int AP = kC + 4;                         // fp32 row pitch of A / T
-constexpr int PW_BYTES = kC * AP * 4 + 4 * kC * 4; // per-wave LDS
+constexpr int PW_BYTES = kC * AP * 4 + 8 * kC * 4; // per-wave LDS
 constexpr int PREP_LDS = kPrepWaves * PW_BYTES;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 struct ChunkArgs {
     float *state;
@@ -101,27 +106,13 @@ __device__ __forceinline__ f32x4 mfma(const bf16x8 &a, const bf16x8 &b, const f3
 
 __device__ __forceinline__ float bf(uint16_t u) { return bf16_bits_to_f32(u); }
 
-// 8 bf16 from LDS (16-byte aligned) as an MFMA operand.
-__device__ __forceinline__ bf16x8 ld_bf8(const uint16_t *p) {
-    return *reinterpret_cast<const bf16x8 *>(p);
-}
-
-// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): ~16 significant bits.
-__device__ __forceinline__ void split(float x, uint16_t &hi, uint16_t &lo) {
-    const __bf16 h = static_cast<__bf16>(x);
-    hi = __builtin_bit_cast(uint16_t, h);
-    lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x - static_cast<float>(h)));
-}
-
-__device__ __forceinline__ uint32_t pack2(uint16_t a, uint16_t b) {
-    return a | (static_cast<uint32_t>(b) << 16);
-}
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
 
 __device__ __forceinline__ int khead(const ChunkArgs &a, int h) {
     return (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
 }
 
-// Sum of squares of 32 bf16 (4 x 16 B) at p.
+// Sum of squares of 32 bf16 (4 x 16 B).
 __device__ __forceinline__ float sumsq32(const uint4 (&w)[4]) {
     float ss = 0.f;
 #pragma unroll
@@ -136,36 +127,6 @@ __device__ __forceinline__ float sumsq32(const uint4 (&w)[4]) {
     return ss;
 }
 
-// ---------------------------------------------------------------------------
-// Scan: one 512-thread workgroup per (sequence, v-head, 64 state columns).
-// Chain wave w (0..3) owns state columns jb + 16w .. +15, all 128 rows, in
-// registers and runs the recurrence for them: K S0, R, U = T R, and
-// S = b_C S0 + K^T U~, every contraction an MFMA whose operands are its own
-// accumulators or chunk rows in LDS.  Output wave 4 + w forms Pt (its own
-// copy, in registers) while the chain computes U, then takes S0 and U from
-// chain wave w through LDS and computes O = so (Q S0) + Pt U.  The chunk's
-// rows are loaded into registers one chunk ahead and staged into LDS in the
-// second half of the chunk before.
-//
-// Operand layout.  v_mfma_f32_16x16x32_bf16 lane l (r = l % 16, g = l / 16)
-// holds A[r][8g..8g+7], B[8g..8g+7][r] and D[4g..4g+3][r].  A 64-row D
-// result (four 16-row tiles) is used directly as the B operand of the next
-// contraction over those 64 rows: for the 32-row slab of tiles 2q, 2q+1 the
-// lane's eight k values are rows 32q + 4g + {0..3} and 32q + 16 + 4g + {0..3}
-// (tile 2q, then tile 2q+1).  The LDS operand on the other side is read
-// with the same row order (ld_perm), so the sum runs over the same k set.
-// ---------------------------------------------------------------------------
-
-// A operand row[base + 4g .. +3] ++ row[base + 16 + 4g .. +3].
-__device__ __forceinline__ bf16x8 ld_perm(const uint16_t *row, int base, int lg) {
-    const uint2 x = *reinterpret_cast<const uint2 *>(row + base + 4 * lg);
-    const uint2 y = *reinterpret_cast<const uint2 *>(row + base + 16 + 4 * lg);
-    return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
-}
-
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
 // x = hi + lo for two values at once: hi = bf16(x) (round to nearest even),
 // lo = bf16(x - hi); packed as bf16 pairs.
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
@@ -175,7 +136,19 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
     lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a - ha, b - hb}, bf16x2));
 }
 
-// Two D tiles (rows 32q + 4g + e and 32q + 16 + 4g + e) as hi and lo B operands.
+// ---------------------------------------------------------------------------
+// Operand layout.  v_mfma_f32_16x16x32_bf16 lane l (r = l % 16, g = l / 16)
+// holds A[r][8g..8g+7], B[8g..8g+7][r] and D[4g..4g+3][r].  A 64-row D
+// result (four 16-row tiles) is used directly as the B operand of the next
+// contraction over those 64 rows: for the 32-row slab of tiles 2q, 2q+1 the
+// lane's eight k values are rows 32q + 4g + {0..3} and 32q + 16 + 4g + {0..3}
+// (tile 2q, then tile 2q+1).  The operand on the other side is read with the
+// same row order (ld_perm), so the sum runs over the same k set.  The same
+// pair of D tiles of a transposed product (lane index = the other matrix
+// dimension) is an A operand in that order.
+// ---------------------------------------------------------------------------
+
+// Two D tiles (rows 32q + 4g + e and 32q + 16 + 4g + e) as hi and lo operands.
 __device__ __forceinline__ void split8(const f32x4 &t0, const f32x4 &t1, bf16x8 &hi, bf16x8 &lo) {
     uint4 h, l;
     split2(t0[0], t0[1], h.x, l.x);
@@ -186,12 +159,25 @@ __device__ __forceinline__ void split8(const f32x4 &t0, const f32x4 &t1, bf16x8 
     lo = __builtin_bit_cast(bf16x8, l);
 }
 
+// A operand row[base + 4g .. +3] ++ row[base + 16 + 4g .. +3].
+__device__ __forceinline__ bf16x8 ld_perm(const uint16_t *row, int base, int lg) {
+    const uint2 x = *reinterpret_cast<const uint2 *>(row + base + 4 * lg);
+    const uint2 y = *reinterpret_cast<const uint2 *>(row + base + 16 + 4 * lg);
+    return __builtin_bit_cast(bf16x8, make_uint4(x.x, x.y, y.x, y.y));
+}
+
+// Pt slot of (r-tile bb, s-slab q), q <= bb / 2.
+__host__ __device__ constexpr int pslot(int bb, int q) { return bb < 2 ? bb : 2 * (bb - 1) + q; }
+// T slot of (s-tile aa, t-slab q), q <= aa / 2.
+__host__ __device__ constexpr int tslot(int aa, int q) { return q == 0 ? aa : 2 + aa; }
+
 // ---------------------------------------------------------------------------
-// Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K stays
-// in registers in MFMA operand layout (lane r + 16 g holds
-// K[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so G = K K^T
-// needs no LDS; A^T goes to the wave's LDS and T = (I + A)^-1 is solved with
-// one column of T per lane.
+// Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K and Q
+// stay in registers in MFMA operand layout (lane r + 16 g holds
+// X[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so K K^T and
+// K Q^T need no LDS.  Pt is scaled, split and written in the operand order
+// of the scan's output lanes; A^T goes to the wave's LDS and T = (I + A)^-1
+// is solved with one column of T per lane.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -204,6 +190,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     float *nq = nk + kC;
     float *gv = nq + kC;
     float *bv = gv + kC;
+    float *rho = bv + kC;   // e^(g - g_16floor(r/16)) nq
+    float *cb = rho + kC;   // [3][64]: e^(g_16b - g) nk for rows < 16b, b = 1..3
 
     const int cg = item / a.Hv, h = item % a.Hv;
     int lo = 0, hi = a.nseq;  // sequence of chunk cg: coff[lo] <= cg < coff[lo + 1]
@@ -217,23 +205,23 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     const int kh = khead(a, h);
     const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
     const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
+    unsigned char *rec = a.ws + static_cast<size_t>(item) * kRec;
 
-    // K (kept) and Q (norms only) rows 16aa + lr, columns 32kk + 8lg .. +7
-    uint4 kr[4][4];
+    // K and Q rows 16aa + lr, columns 32kk + 8lg .. +7 (zero past n)
+    uint4 kr[4][4], qr[4][4];
 #pragma unroll
     for (int aa = 0; aa < 4; ++aa) {
         const int row = 16 * aa + lr;
-        uint4 qv[4];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            kr[aa][kk] = qv[kk] = make_uint4(0, 0, 0, 0);
+            kr[aa][kk] = qr[aa][kk] = make_uint4(0, 0, 0, 0);
             if (row < n) {
                 const long long off = (static_cast<long long>(t0 + row) * a.Hk + kh) * kD + 32 * kk + 8 * lg;
                 kr[aa][kk] = *reinterpret_cast<const uint4 *>(a.k + off);
-                qv[kk] = *reinterpret_cast<const uint4 *>(a.q + off);
+                qr[aa][kk] = *reinterpret_cast<const uint4 *>(a.q + off);
             }
         }
-        float sk = sumsq32(kr[aa]), sq = sumsq32(qv);
+        float sk = sumsq32(kr[aa]), sq = sumsq32(qr[aa]);
         sk += __shfl_xor(sk, 16, 64);
         sk += __shfl_xor(sk, 32, 64);
         sq += __shfl_xor(sq, 16, 64);
@@ -254,15 +242,79 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
     }
     __builtin_amdgcn_wave_barrier();
+    {  // per-row coefficients, row = lane (zero past n: nk = nq = beta = 0)
+        float *rv = reinterpret_cast<float *>(rec + REC_V);
+        const float g = gv[lane], b = bv[lane], kn = nk[lane], qn = nq[lane];
+        const float gC = gv[n - 1], eg = __expf(g);
+        rv[V_BETA + lane] = b;
+        rv[V_RK + lane] = b * eg * kn;
+        rv[V_W + lane] = kn * __expf(gC - g);
+        rv[V_SO + lane] = eg * qn;
+        rv[V_G + lane] = g;
+        rho[lane] = __expf(g - gv[lane & ~15]) * qn;
+#pragma unroll
+        for (int bb = 1; bb < 4; ++bb) cb[64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
+    }
+    __builtin_amdgcn_wave_barrier();
+
+    // Pt: P^T = K Q^T tiles (s-tile aa <= r-tile bb) at pt[bb (bb + 1) / 2 + aa]
+    {
+        f32x4 pt[10];
+#pragma unroll
+        for (int i = 0; i < 10; ++i) pt[i] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+                for (int aa = 0; aa <= bb; ++aa)
+                    pt[bb * (bb + 1) / 2 + aa] = mfma(__builtin_bit_cast(bf16x8, kr[aa][kk]),
+                                                      __builtin_bit_cast(bf16x8, qr[bb][kk]), pt[bb * (bb + 1) / 2 + aa]);
+        uint4 *rp = reinterpret_cast<uint4 *>(rec + REC_P);
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+            const int r = 16 * bb + lr;  // this lane's r in the P^T tiles
+            const float rr = rho[r], gr = gv[r], nqr = nq[r];
+            f32x4 ps[4];
+#pragma unroll
+            for (int aa = 0; aa < 4; ++aa) {
+                if (aa > bb) {
+                    ps[aa] = f32x4{0, 0, 0, 0};
+                    continue;
+                }
+                ps[aa] = pt[bb * (bb + 1) / 2 + aa];
+                if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
+                    const f32x4 c4 = ld4(cb + 64 * (bb - 1) + 16 * aa + 4 * lg);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ps[aa][e] *= rr * c4[e];
+                } else {  // diagonal tile: s <= r only
+                    const f32x4 gs = ld4(gv + 16 * aa + 4 * lg), ks = ld4(nk + 16 * aa + 4 * lg);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int sr = 16 * aa + 4 * lg + e;
+                        const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
+                        ps[aa][e] = sr <= r ? ev * nqr * ks[e] * ps[aa][e] : 0.f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int q = 0; q <= bb / 2; ++q) {
+                bf16x8 ph, pl;
+                split8(ps[2 * q], ps[2 * q + 1], ph, pl);
+                rp[(2 * pslot(bb, q)) * 64 + lane] = __builtin_bit_cast(uint4, ph);
+                rp[(2 * pslot(bb, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, pl);
+            }
+        }
+    }
 
     // A[r][c] = beta_r exp(g_r - g_c) nk_r nk_c (K K^T)[r][c], c < r, stored
     // transposed (Al[c][r]); tiles on and below the diagonal only (the solve
     // never reads r <= c).
 #pragma unroll
     for (int aa = 0; aa < 4; ++aa) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bv + 16 * aa + 4 * lg);
-        const f32x4 g4r = *reinterpret_cast<const f32x4 *>(gv + 16 * aa + 4 * lg);
-        const f32x4 k4 = *reinterpret_cast<const f32x4 *>(nk + 16 * aa + 4 * lg);
+        const f32x4 b4 = ld4(bv + 16 * aa + 4 * lg);
+        const f32x4 g4r = ld4(gv + 16 * aa + 4 * lg);
+        const f32x4 k4 = ld4(nk + 16 * aa + 4 * lg);
 #pragma unroll
         for (int bb = 0; bb <= aa; ++bb) {
             f32x4 g4 = {0, 0, 0, 0};
@@ -293,7 +345,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         const float *acol = Al + j * AP;  // A[.][j]
 #pragma unroll
         for (int s4 = (j + 1) & ~3; s4 < kC; s4 += 4) {
-            const f32x4 a4 = *reinterpret_cast<const f32x4 *>(acol + s4);
+            const f32x4 a4 = ld4(acol + s4);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (s4 + e > j) t[s4 + e] -= a4[e] * tj;
@@ -304,48 +356,43 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     for (int s2 = 0; s2 < kC; ++s2) Al[s2 * AP + lane] = t[s2];
     __builtin_amdgcn_wave_barrier();
 
-    // Record: T hi/lo row-major [64][64], then nk, nq, g.
-    unsigned char *rec = a.ws + static_cast<size_t>(item) * kRec;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int id = lane + 64 * i;
-        const int r = id >> 3, c0 = 8 * (id & 7);
-        const f32x4 x0 = *reinterpret_cast<const f32x4 *>(Al + r * AP + c0);
-        const f32x4 x1 = *reinterpret_cast<const f32x4 *>(Al + r * AP + c0 + 4);
-        bf16x8 th, tl;
-        split8(x0, x1, th, tl);
-        reinterpret_cast<bf16x8 *>(rec)[id] = th;
-        reinterpret_cast<bf16x8 *>(rec + kC * kC * 2)[id] = tl;
-    }
+    // T operands: slot (aa, q) of lane (lr, lg) is T[16aa + lr][32q + 4lg .. +3]
+    // ++ T[16aa + lr][32q + 16 + 4lg .. +3], split hi/lo
     {
-        float *rv = reinterpret_cast<float *>(rec + REC_T);
-        const float g = gv[lane], b = bv[lane], kn = nk[lane], qn = nq[lane];
-        const float gC = gv[n - 1], eg = __expf(g);
-        rv[V_BETA + lane] = b;
-        rv[V_RK + lane] = b * eg * kn;
-        rv[V_W + lane] = kn * __expf(gC - g);
-        rv[V_SO + lane] = eg * qn;
-        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]) * qn;
+        uint4 *rt = reinterpret_cast<uint4 *>(rec + REC_T);
 #pragma unroll
-        for (int bb = 1; bb < 4; ++bb)
-            rv[V_C1 + 64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
-        rv[V_G + lane] = g;
-        rv[V_NQ + lane] = qn;
-        rv[V_NK + lane] = kn;
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int aa = 2 * q; aa < 4; ++aa) {
+                const float *row = Al + (16 * aa + lr) * AP + 32 * q + 4 * lg;
+                bf16x8 th, tl;
+                split8(ld4(row), ld4(row + 16), th, tl);
+                rt[(2 * tslot(aa, q)) * 64 + lane] = __builtin_bit_cast(uint4, th);
+                rt[(2 * tslot(aa, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, tl);
+            }
     }
 }
 
-// Chain-wave prefetch: K rows (as pairs, for the K^T store) and T of the
-// next chunk.  Chain thread tc, item it (0, 1): id = tc + 256 it covers rows
-// 2p, 2p+1 (p = id % 32) and bf16 columns 8c .. 8c+7 (c = id / 32).
-struct ChainRegs {
-    uint4 k[2][2], t[4];
-    uint16_t v[16];  // V of this wave's stripe in D layout: v[4a + e] = V[16a + 4g + e][jw + r]
-};
+// ---------------------------------------------------------------------------
+// Scan: one 512-thread workgroup per (sequence, v-head, 64 state columns).
+// Chain wave w (0..3) owns state columns jb + 16w .. +15, all 128 rows, in
+// registers and runs the recurrence for them: K S0, R, U = T R, and
+// S = b_C S0 + K^T U~, every contraction an MFMA whose operands are its own
+// accumulators or chunk rows in LDS.  Output wave 4 + w takes S0 and U from
+// chain wave w through LDS and computes O = so (Q S0) + Pt U with Pt from
+// the record, one chunk behind the chain.  The output waves load the next
+// chunk's K, Q and vectors in the first half and stage them into LDS at the
+// start of the second; the chain waves load their T operands and V values
+// for the next chunk in the second half.
+// ---------------------------------------------------------------------------
 
-// Output-wave prefetch: Q rows and the coefficient vectors of the next chunk.
-struct OutRegs {
-    uint4 q[4], vec;
+// Output-wave prefetch of the next chunk: K rows (as pairs, for the K^T
+// store), Q, the vectors and the T operands.  Output thread to, item it (0, 1):
+// id = to + 256 it covers K rows 2p, 2p+1 (p = id % 32) and bf16 columns
+// 8c .. 8c+7 (c = id / 32).
+struct NextRegs {
+    uint4 k[2][2], q[4], vec, t[3];
+    uint4 p0, p1, p2;  // this thread's share of the Pt operands of the current chunk
 };
 
 // base + a 32-bit byte offset (lets the loads use a uniform base address)
@@ -361,14 +408,15 @@ __device__ __forceinline__ uint4 zero_if(bool z, uint4 v) {
     return z ? make_uint4(0, 0, 0, 0) : v;
 }
 
-__device__ __forceinline__ void load_chain(const ChunkArgs &a, ChainRegs &r, int tc, int t0, int n, int kh, int h,
-                                           int jw, int lr, int lg, const unsigned char *rec) {
+__device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int to, int t0, int n, int kh,
+                                          const unsigned char *rec) {
     // uniform chunk bases, 32-bit lane offsets
     const uint16_t *kb = a.k + (static_cast<long long>(t0) * a.Hk + kh) * kD;
+    const uint16_t *qb = a.q + (static_cast<long long>(t0) * a.Hk + kh) * kD;
     const unsigned ks = static_cast<unsigned>(a.Hk) * kD;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const int id = tc + 256 * it;
+        const int id = to + 256 * it;
         const int p = id & 31, c = id >> 5;
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
@@ -377,23 +425,25 @@ __device__ __forceinline__ void load_chain(const ChunkArgs &a, ChainRegs &r, int
         }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec)[tc + 256 * i];
-    const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
-    const unsigned vs = static_cast<unsigned>(a.Hv) * kD;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const unsigned row = static_cast<unsigned>(min(16 * (i >> 2) + 4 * lg + (i & 3), n - 1));
-        r.v[i] = at<uint16_t>(vb, 2u * (row * vs + static_cast<unsigned>(lr)));
+    for (int i = 0; i < 4; ++i) {
+        const int idx = to + 256 * i;
+        const unsigned row = static_cast<unsigned>(min(idx >> 4, n - 1));
+        r.q[i] = at<uint4>(qb, 2u * (row * ks + 8u * (idx & 15)));
     }
+    r.vec = reinterpret_cast<const uint4 *>(rec + REC_V)[min(to, kVec / 4 - 1)];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec + REC_T)[to + 256 * i];
 }
 
-__device__ __forceinline__ void store_chain(const ChainRegs &r, unsigned char *lds, int kt_buf, int tc, int n) {
+// Stage the next chunk: K and the T operands (read in the first half of a
+// chunk) and K^T, Q, vectors into buffer `buf`.
+__device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds, int buf, int to, int n) {
     uint16_t *K = reinterpret_cast<uint16_t *>(lds + S_K);
-    uint32_t *KT = reinterpret_cast<uint32_t *>(lds + S_KT + kt_buf * kD * KTP * 2);
-    uint16_t *T = reinterpret_cast<uint16_t *>(lds + S_T);
+    uint32_t *KT = reinterpret_cast<uint32_t *>(lds + S_KT + buf * kD * KTP * 2);
+    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q + buf * kC * KP * 2);
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-        const int id = tc + 256 * it;
+        const int id = to + 256 * it;
         const int p = id & 31, c = id >> 5;
         const uint4 k0 = zero_if(2 * p >= n, r.k[it][0]), k1 = zero_if(2 * p + 1 >= n, r.k[it][1]);
         *reinterpret_cast<uint4 *>(K + (2 * p) * KP + 8 * c) = k0;
@@ -409,42 +459,89 @@ __device__ __forceinline__ void store_chain(const ChainRegs &r, unsigned char *l
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int idx = tc + 256 * i;
-        const int plane = idx >> 9, e = idx & 511;  // T hi then lo, 8 bf16 per uint4
-        *reinterpret_cast<uint4 *>(T + plane * HL + (e >> 3) * FP + 8 * (e & 7)) = r.t[i];
-    }
-}
-
-__device__ __forceinline__ void load_out(const ChunkArgs &a, OutRegs &r, int to, int t0, int n, int kh,
-                                         const unsigned char *rec) {
-    const uint16_t *qb = a.q + (static_cast<long long>(t0) * a.Hk + kh) * kD;
-    const unsigned qs = static_cast<unsigned>(a.Hk) * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int idx = to + 256 * i;
-        const unsigned row = static_cast<unsigned>(min(idx >> 4, n - 1));
-        r.q[i] = at<uint4>(qb, 2u * (row * qs + 8u * (idx & 15)));
-    }
-    r.vec = reinterpret_cast<const uint4 *>(rec + REC_T)[min(to, kVec / 4 - 1)];
-}
-
-__device__ __forceinline__ void store_out(const OutRegs &r, unsigned char *lds, int buf, int to, int n) {
-    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q + buf * kC * KP * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
         const int idx = to + 256 * i;
         *reinterpret_cast<uint4 *>(Q + (idx >> 4) * KP + 8 * (idx & 15)) = zero_if((idx >> 4) >= n, r.q[i]);
     }
     if (to < kVec / 4) reinterpret_cast<uint4 *>(lds + S_VEC + buf * kVec * 4)[to] = r.vec;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) reinterpret_cast<uint4 *>(lds + S_T)[to + 256 * i] = r.t[i];
 }
 
-__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+// V of a chain wave's stripe in D layout: v[4a + e] = V[16a + 4g + e][jw + r]
+// (row clamped to n - 1; zeroed when used).
+__device__ __forceinline__ void load_v(const ChunkArgs &a, uint16_t (&v)[16], int t0, int n, int h, int jw, int lr,
+                                       int lg) {
+    const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
+    const unsigned vs = static_cast<unsigned>(a.Hv) * kD;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const unsigned row = static_cast<unsigned>(min(16 * (i >> 2) + 4 * lg + (i & 3), n - 1));
+        v[i] = at<uint16_t>(vb, 2u * (row * vs + static_cast<unsigned>(lr)));
+    }
+}
 
-// Materialise a value at this point of the program (no code).
-__device__ __forceinline__ void pin(bf16x8 &x) {
-    uint4 u = __builtin_bit_cast(uint4, x);
-    asm volatile("" : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w));
-    x = __builtin_bit_cast(bf16x8, u);
+// O = so (Q S0) + Pt U for one output stripe of the chunk at t0 (n rows),
+// with Q and the vectors in buffer buf and Pt in the Pt slot.
+__device__ __forceinline__ void out_chunk(const ChunkArgs &a, const unsigned char *lds, int buf, const bf16x8 (&sh)[4],
+                                          const bf16x8 (&sl)[4], const bf16x8 (&uh)[2], const bf16x8 (&ul)[2],
+                                          int t0, int n, int h, int jw, int lane, int lr, int lg) {
+    const uint4 *P = reinterpret_cast<const uint4 *>(lds + S_P);  // [slot][lane]
+    const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q + buf * kC * KP * 2);
+    const float *cv = reinterpret_cast<const float *>(lds + S_VEC + buf * kVec * 4);
+    f32x4 o[4];
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) o[bb] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        bf16x8 qa[4];
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) qa[bb] = ld_perm(Q + (16 * bb + lr) * KP, 32 * q, lg);
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sh[q], o[bb]);
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sl[q], o[bb]);
+    }
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+        const f32x4 so = ld4(cv + V_SO + 16 * bb + 4 * lg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[bb][e] *= so[e];
+    }
+    // Pt U over s-slab q for r-tiles bb with q <= bb / 2
+#pragma unroll
+    for (int pass = 0; pass < 3; ++pass) {
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+#pragma unroll
+            for (int q = 0; q <= bb / 2; ++q) {
+                const bf16x8 ph = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q)) * 64 + lane]);
+                const bf16x8 pl = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q) + 1) * 64 + lane]);
+                if (pass == 0) o[bb] = mfma(ph, uh[q], o[bb]);
+                if (pass == 1) o[bb] = mfma(ph, ul[q], o[bb]);
+                if (pass == 2) o[bb] = mfma(pl, uh[q], o[bb]);
+            }
+        }
+    }
+    float *ob = a.out + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
+    const unsigned os = static_cast<unsigned>(a.Hv) * kD;
+    if (n == kC) {
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
+                    4u * (static_cast<unsigned>(16 * bb + 4 * lg + e) * os + static_cast<unsigned>(lr))) = o[bb][e];
+    } else {
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = 16 * bb + 4 * lg + e;
+                if (row < n)
+                    *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
+                        4u * (static_cast<unsigned>(row) * os + static_cast<unsigned>(lr))) = o[bb][e];
+            }
+    }
 }
 
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs a) {
@@ -465,17 +562,20 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
     auto record = [&](int c) { return a.ws + (static_cast<size_t>(a.coff[seq] + c) * a.Hv + h) * kRec; };
     uint4 *X = reinterpret_cast<uint4 *>(lds + S_X + (wave & 3) * X_WAVE);  // [slot][lane]
 
-    // Both roles run the same number of chunks and barriers (two per chunk);
-    // their registers are disjoint because each role has its own loop.
+    // Both roles run the same number of barriers (two per chunk and one
+    // after the loop); their registers are disjoint because each role has
+    // its own loop.
     if (chain) {
         // state tile t holds S[16t + 4g + e][jw + r]
         float *S = a.state + (static_cast<long long>(seq) * a.Hv + h) * kD * kD + static_cast<long long>(jw + lr) * kD;
         f32x4 st[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) st[t] = ld4(S + 16 * t + 4 * lg);
-        ChainRegs cr;
-        load_chain(a, cr, tr, t_begin, min(kC, t_end - t_begin), kh, h, jw, lr, lg, record(0));
-        store_chain(cr, lds, 0, tr, min(kC, t_end - t_begin));
+        bf16x8 sh[4], sl[4];  // S0 of the next chunk as hi/lo B operands, slab q = tiles 2q, 2q+1
+#pragma unroll
+        for (int q = 0; q < 4; ++q) split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
+        uint16_t vn[16];
+        load_v(a, vn, t_begin, min(kC, t_end - t_begin), h, jw, lr, lg);
 
         for (int c = 0; c < nchunks; ++c) {
             const int t0 = t_begin + c * kC;
@@ -483,25 +583,22 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
             const int b = c & 1;
             const bool more = c + 1 < nchunks;
             const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
-            const uint16_t *T = reinterpret_cast<const uint16_t *>(lds + S_T);
             const uint16_t *KT = reinterpret_cast<const uint16_t *>(lds + S_KT + b * kD * KTP * 2);
             const float *cv = reinterpret_cast<const float *>(lds + S_VEC + b * kVec * 4);
-            __syncthreads();  // chunk c is in K, T and buffer b; X is free
+            __syncthreads();  // chunk c is in K, the T slot and buffer b; X is free
 
             // ---- first half: S0 -> X, KS, R, U -> X, U~ ---------------------
-            uint16_t vcur[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) vcur[i] = (16 * (i >> 2) + 4 * lg + (i & 3)) < n ? cr.v[i] : 0;
-            if (more) load_chain(a, cr, tr, t0 + kC, min(kC, t_end - t0 - kC), kh, h, jw, lr, lg, record(c + 1));
-            const float bC = __expf(cv[V_G + n - 1]);
-
-            bf16x8 sh[4], sl[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
                 X[(2 * q) * 64 + lane] = __builtin_bit_cast(uint4, sh[q]);
                 X[(2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, sl[q]);
             }
+            uint16_t vcur[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) vcur[i] = (16 * (i >> 2) + 4 * lg + (i & 3)) < n ? vn[i] : 0;
+            const uint4 *Tl = reinterpret_cast<const uint4 *>(lds + S_T);  // [slot][lane]
+            const float bC = __expf(cv[V_G + n - 1]);
+
             f32x4 ks[4], rr[4];
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) ks[aa] = f32x4{0, 0, 0, 0};
@@ -530,18 +627,15 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
             for (int aa = 0; aa < 4; ++aa) u[aa] = f32x4{0, 0, 0, 0};
 #pragma unroll
             for (int q = 0; q < 2; ++q) {  // T is lower triangular: s-tile aa needs slabs q <= aa / 2
-                bf16x8 th[4], tl[4];
 #pragma unroll
-                for (int aa = 2 * q; aa < 4; ++aa) {
-                    th[aa] = ld_perm(T + (16 * aa + lr) * FP, 32 * q, lg);
-                    tl[aa] = ld_perm(T + HL + (16 * aa + lr) * FP, 32 * q, lg);
-                }
+                for (int aa = 2 * q; aa < 4; ++aa)
+                    u[aa] = mfma(__builtin_bit_cast(bf16x8, Tl[(2 * tslot(aa, q)) * 64 + lane]), rh[q], u[aa]);
 #pragma unroll
-                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(th[aa], rh[q], u[aa]);
+                for (int aa = 2 * q; aa < 4; ++aa)
+                    u[aa] = mfma(__builtin_bit_cast(bf16x8, Tl[(2 * tslot(aa, q)) * 64 + lane]), rl[q], u[aa]);
 #pragma unroll
-                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(th[aa], rl[q], u[aa]);
-#pragma unroll
-                for (int aa = 2 * q; aa < 4; ++aa) u[aa] = mfma(tl[aa], rh[q], u[aa]);
+                for (int aa = 2 * q; aa < 4; ++aa)
+                    u[aa] = mfma(__builtin_bit_cast(bf16x8, Tl[(2 * tslot(aa, q) + 1) * 64 + lane]), rh[q], u[aa]);
             }
             bf16x8 wh[2], wl[2];
 #pragma unroll
@@ -562,7 +656,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
 
             __syncthreads();  // X holds S0 and U of chunk c; K and T may be refilled
 
-            // ---- second half: S = b_C S0 + K^T U~, then stage chunk c + 1 ----
+            // ---- second half: next chunk's V, S = b_C S0 + K^T U~ -----------
+            if (more) load_v(a, vn, t0 + kC, min(kC, t_end - t0 - kC), h, jw, lr, lg);
 #pragma unroll
             for (int t = 0; t < 8; ++t) st[t] = st[t] * bC;
 #pragma unroll
@@ -575,93 +670,52 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
 #pragma unroll
                 for (int t = 0; t < 8; ++t) st[t] = mfma(kt[t], wl[q], st[t]);
             }
-            if (more) store_chain(cr, lds, b ^ 1, tr, min(kC, t_end - t0 - kC));
+            if (more) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
+            }
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4 *>(S + 16 * t + 4 * lg) = st[t];
+        __syncthreads();  // pairs with the output waves' last barrier
     } else {
-        OutRegs orr;
-        load_out(a, orr, tr, t_begin, min(kC, t_end - t_begin), kh, record(0));
-        store_out(orr, lds, 0, tr, min(kC, t_end - t_begin));
+        // Output waves trail the chain by one chunk: O of chunk c - 1 is
+        // formed in the first half of chunk c, beside the chain's K S0 -> U.
+        NextRegs nx;
+        {
+            const int n0 = min(kC, t_end - t_begin);
+            load_next(a, nx, tr, t_begin, n0, kh, record(0));
+            store_next(nx, lds, 0, tr, n0);
+        }
+        bf16x8 sh[4], sl[4], uh[2], ul[2];  // S0 and U of the chunk before, from X
 
         for (int c = 0; c < nchunks; ++c) {
             const int t0 = t_begin + c * kC;
-            const int n = min(kC, t_end - t0);
             const int b = c & 1;
             const bool more = c + 1 < nchunks;
-            const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
-            const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q + b * kC * KP * 2);
-            const float *cv = reinterpret_cast<const float *>(lds + S_VEC + b * kVec * 4);
-            __syncthreads();  // chunk c is in K, T and buffer b
+            const int n1 = more ? min(kC, t_end - t0 - kC) : 0;
+            __syncthreads();  // chunk c is in buffer b; Pt of chunk c - 1 in the Pt slot
 
-            // ---- first half: Pt operands (r-tile b, s-slab q), slots in order
-            // (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) -------------------------------
-            // P^T = K Q^T tiles (s-tile aa <= r-tile bb), tile (aa, bb) at
-            // pt[bb (bb + 1) / 2 + aa]; every K and Q operand loaded once.
-            f32x4 pt[10];
-#pragma unroll
-            for (int i = 0; i < 10; ++i) pt[i] = f32x4{0, 0, 0, 0};
-#pragma unroll
-            for (int kk = 0; kk < kD / 32; ++kk) {
-                const int kc = kk * 32 + 8 * lg;
-                bf16x8 kv[4], qv[4];
-#pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    kv[x] = ld_bf8(K + (16 * x + lr) * KP + kc);
-                    qv[x] = ld_bf8(Q + (16 * x + lr) * KP + kc);
-                }
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-                    for (int aa = 0; aa <= bb; ++aa) pt[bb * (bb + 1) / 2 + aa] = mfma(kv[aa], qv[bb], pt[bb * (bb + 1) / 2 + aa]);
+            // ---- first half: loads (chunk c + 1, Pt of c), O of chunk c - 1 --
+            {
+                const uint4 *rp = reinterpret_cast<const uint4 *>(record(c) + REC_P) + tr;
+                nx.p0 = rp[0];
+                nx.p1 = rp[256];
+                nx.p2 = rp[512];
             }
-            bf16x8 ph[6], pl[6];
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                const int r = 16 * bb + lr;  // this lane's r in the P^T tiles
-                const float rho = cv[V_RHO + r], gr = cv[V_G + r], nqr = cv[V_NQ + r];
-                f32x4 ps[4];
-#pragma unroll
-                for (int aa = 0; aa < 4; ++aa) {
-                    if (aa > bb) {
-                        ps[aa] = f32x4{0, 0, 0, 0};
-                        continue;
-                    }
-                    ps[aa] = pt[bb * (bb + 1) / 2 + aa];
-                    if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
-                        const f32x4 cb = ld4(cv + V_C1 + 64 * (bb - 1) + 16 * aa + 4 * lg);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) ps[aa][e] *= rho * cb[e];
-                    } else {  // diagonal tile: s <= r only
-                        const f32x4 gs = ld4(cv + V_G + 16 * aa + 4 * lg), ks = ld4(cv + V_NK + 16 * aa + 4 * lg);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int sr = 16 * aa + 4 * lg + e;
-                            const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
-                            ps[aa][e] = sr <= r ? ev * nqr * ks[e] * ps[aa][e] : 0.f;
-                        }
-                    }
-                }
-#pragma unroll
-                for (int q = 0; q <= bb / 2; ++q) {
-                    const int slot = (bb < 2) ? bb : 2 * (bb - 1) + q;
-                    split8(ps[2 * q], ps[2 * q + 1], ph[slot], pl[slot]);
-                }
-            }
+            if (more) load_next(a, nx, tr, t0 + kC, n1, kh, record(c + 1));
+            if (c > 0) out_chunk(a, lds, b ^ 1, sh, sl, uh, ul, t0 - kC, kC, h, jw, lane, lr, lg);
 
-            // keep the Pt scaling and split in this half (ahead of the barrier)
-#pragma unroll
-            for (int i = 0; i < 6; ++i) {
-                pin(ph[i]);
-                pin(pl[i]);
-            }
-            __syncthreads();  // X holds S0 and U of chunk c
+            __syncthreads();  // X holds S0 and U of chunk c; K, T and Pt are free
 
-            // next chunk's Q and vectors: loaded here, after this wave's O
-            // stores of the chunk before have had a half chunk to drain
-            if (more) load_out(a, orr, tr, t0 + kC, min(kC, t_end - t0 - kC), kh, record(c + 1));
-            // ---- second half: O = so (Q S0) + Pt U, then stage chunk c + 1 ----
-            bf16x8 sh[4], sl[4], uh[2], ul[2];
+            // ---- second half: stage chunk c + 1 and Pt of c, take S0, U of c -
+            if (more) store_next(nx, lds, b ^ 1, tr, n1);
+            {
+                uint4 *sp = reinterpret_cast<uint4 *>(lds + S_P) + tr;
+                sp[0] = nx.p0;
+                sp[256] = nx.p1;
+                sp[512] = nx.p2;
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 sh[q] = __builtin_bit_cast(bf16x8, X[(2 * q) * 64 + lane]);
@@ -672,64 +726,10 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                 uh[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q) * 64 + lane]);
                 ul[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q + 1) * 64 + lane]);
             }
-            f32x4 o[4];
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) o[bb] = f32x4{0, 0, 0, 0};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                bf16x8 qa[4];
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb) qa[bb] = ld_perm(Q + (16 * bb + lr) * KP, 32 * q, lg);
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sh[q], o[bb]);
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sl[q], o[bb]);
-            }
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-                const f32x4 so = ld4(cv + V_SO + 16 * bb + 4 * lg);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[bb][e] *= so[e];
-            }
-            // Pt U over s-slab q for r-tiles bb with q <= bb / 2; slot of (bb, q)
-            // in (0,0) (1,0) (2,0) (2,1) (3,0) (3,1) order
-#pragma unroll
-            for (int pass = 0; pass < 3; ++pass) {
-#pragma unroll
-                for (int bb = 0; bb < 4; ++bb) {
-#pragma unroll
-                    for (int q = 0; q <= bb / 2; ++q) {
-                        const int slot = (bb < 2) ? bb : 2 * (bb - 1) + q;
-                        if (pass == 0) o[bb] = mfma(ph[slot], uh[q], o[bb]);
-                        if (pass == 1) o[bb] = mfma(ph[slot], ul[q], o[bb]);
-                        if (pass == 2) o[bb] = mfma(pl[slot], uh[q], o[bb]);
-                    }
-                }
-            }
-            {
-                float *ob = a.out + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
-                const unsigned os = static_cast<unsigned>(a.Hv) * kD;
-                if (n == kC) {
-#pragma unroll
-                    for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
-                                4u * (static_cast<unsigned>(16 * bb + 4 * lg + e) * os + static_cast<unsigned>(lr))) = o[bb][e];
-                } else {
-#pragma unroll
-                    for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int row = 16 * bb + 4 * lg + e;
-                            if (row < n)
-                                *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
-                                    4u * (static_cast<unsigned>(row) * os + static_cast<unsigned>(lr))) = o[bb][e];
-                        }
-                }
-            }
-            if (more) store_out(orr, lds, b ^ 1, tr, min(kC, t_end - t0 - kC));
         }
+        __syncthreads();  // Pt of the last chunk is staged (its buffers are not overwritten)
+        const int tl = t_begin + (nchunks - 1) * kC;
+        out_chunk(a, lds, (nchunks - 1) & 1, sh, sl, uh, ul, tl, t_end - tl, h, jw, lane, lr, lg);
     }
 }
 
