@@ -112,6 +112,11 @@ __device__ __forceinline__ int khead(const ChunkArgs &a, int h) {
     return (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
 }
 
+// The j-th of the Hv / Hk v-heads that read k-head kh.
+__device__ __forceinline__ int vhead(const ChunkArgs &a, int kh, int j) {
+    return (a.flags & OURO_GDN_KHEAD_DIV) ? kh * (a.Hv / a.Hk) + j : kh + a.Hk * j;
+}
+
 // Sum of squares of 32 bf16 (4 x 16 B).
 __device__ __forceinline__ float sumsq32(const uint4 (&w)[4]) {
     float ss = 0.f;
@@ -193,7 +198,10 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     float *rho = bv + kC;   // e^(g - g_16floor(r/16)) nq
     float *cb = rho + kC;   // [3][64]: e^(g_16b - g) nk for rows < 16b, b = 1..3
 
-    const int cg = item / a.Hv, h = item % a.Hv;
+    // items of one chunk in k-head order, so that the v-heads reading the
+    // same K and Q rows sit in the same workgroup
+    const int cg = item / a.Hv;
+    const int h = vhead(a, (item % a.Hv) / (a.Hv / a.Hk), (item % a.Hv) % (a.Hv / a.Hk));
     int lo = 0, hi = a.nseq;  // sequence of chunk cg: coff[lo] <= cg < coff[lo + 1]
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -205,7 +213,7 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     const int kh = khead(a, h);
     const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
     const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
-    unsigned char *rec = a.ws + static_cast<size_t>(item) * kRec;
+    unsigned char *rec = a.ws + (static_cast<size_t>(cg) * a.Hv + h) * kRec;
 
     // K and Q rows 16aa + lr, columns 32kk + 8lg .. +7 (zero past n)
     uint4 kr[4][4], qr[4][4];
@@ -552,10 +560,24 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
     const int lr = lane & 15, lg = lane >> 4;
     const bool chain = wave < 4;                      // wave-uniform role
     const int tr = tid & 255;                         // thread index within the role
-    const int seq = blockIdx.x / (a.Hv * 2);
-    const int h = (blockIdx.x / 2) % a.Hv;
-    const int jw = (blockIdx.x % 2) * kDVB + 16 * (wave & 3);  // first state column of this stripe
-    const int kh = khead(a, h);
+    // Workgroups that read the same K, Q rows (the column halves of the
+    // v-heads of one k-head: G = 2 Hv / Hk of them) form a group, and a
+    // group is placed on one XCD (workgroup i runs on XCD i % 8) so that
+    // they share its L2.
+    const int G = 2 * (a.Hv / a.Hk);
+    const int groups = a.nseq * a.Hk;
+    int grp, mem;
+    if (groups % 8 == 0) {
+        const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+        grp = (slot / G) * 8 + xcd;
+        mem = slot % G;
+    } else {
+        grp = blockIdx.x / G;
+        mem = blockIdx.x % G;
+    }
+    const int seq = grp / a.Hk, kh = grp % a.Hk;
+    const int h = vhead(a, kh, mem >> 1);
+    const int jw = (mem & 1) * kDVB + 16 * (wave & 3);  // first state column of this stripe
     const int t_begin = a.cu[seq], t_end = a.cu[seq + 1];
     if (t_end <= t_begin) return;  // empty sequence: state unchanged (uniform per block)
     const int nchunks = (t_end - t_begin + kC - 1) / kC;
