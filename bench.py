@@ -176,6 +176,41 @@ def bench_gdn(stream, steps, warmup):
     return time_events(stream, step, max(steps, 2 * GDN_SETS), warmup)
 
 
+LY_CH = 2 * GDN_HK * GDN_D + GDN_HV * GDN_D
+# state R+W, conv ring R+W (3 f32 per channel), qkv in, z in, gates in, out; conv and norm weights
+LY_BYTES = (2 * GDN_B * GDN_HV * GDN_D * GDN_D * 4 + 2 * GDN_B * LY_CH * 12 + GDN_B * LY_CH * 4
+            + 2 * GDN_B * GDN_HV * GDN_D * 4 + 2 * GDN_B * GDN_HV * 4 + LY_CH * 16 + GDN_D * 4 + 2 * GDN_HV * 4)
+
+
+def bench_layer(stream, steps, warmup):
+    """The whole delta-net layer block of a decode step (gates, conv + SiLU,
+    recurrence, gated RMS norm) at the decode shape, 8 rotating state sets."""
+    from ouroboros_amd import qwen35
+    from ouroboros_amd._lib import GDN_V_GROUPED, call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(17)
+    B, Hk, Hv, d = GDN_B, GDN_HK, GDN_HV, GDN_D
+    per = B * Hv * d * d
+    states = DeviceBuffer((GDN_SETS, per), np.float32)
+    init = (0.02 * rng.standard_normal(per)).astype(np.float32)
+    for s in range(GDN_SETS):
+        call("ouro_memcpy_htod", states.ptr + 4 * s * per, init.ctypes.data, 4 * per)
+    f = lambda *sh: DeviceBuffer.from_host(rng.standard_normal(sh).astype(np.float32))  # noqa: E731
+    qkv, z, br, ar, dt, nw, conv = f(B, LY_CH), f(B, Hv * d), f(B, Hv), f(B, Hv), f(Hv), f(d), f(B, LY_CH, 3)
+    al = DeviceBuffer.from_host((-np.exp(rng.standard_normal(Hv))).astype(np.float32))
+    cw = DeviceBuffer.from_host((0.5 * rng.standard_normal((LY_CH, 4))).astype(np.float32))
+    out = DeviceBuffer((B, Hv * d), np.float32)
+    ws = DeviceBuffer((qwen35.layer_workspace_bytes(B, Hk, Hv, d),), np.uint8)
+
+    def step(i):
+        s = i % GDN_SETS
+        call("ouro_gdn_layer_decode", qkv.ptr, z.ptr, br.ptr, ar.ptr, dt.ptr, al.ptr, cw.ptr, nw.ptr, conv.ptr,
+             states.ptr + 4 * s * per, out.ptr, B, Hk, Hv, d, GDN_V_GROUPED, 1e-6, ws.ptr, stream)
+
+    return time_events(stream, step, max(steps, 2 * GDN_SETS), warmup)
+
+
 def bench_fwht(stream, steps, warmup):
     from ouroboros_amd import quant
     from ouroboros_amd._lib import DT_BF16, call
@@ -353,7 +388,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["gemv", "gdn", "fwht", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gdn", "layer", "fwht", "prefill", "copy"], default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -377,6 +412,9 @@ def main() -> int:
     if args.only in (None, "gdn"):
         log("GDN decode B=32")
         res["gdn"] = bench_gdn(stream, args.steps, args.warmup)
+    if args.only in (None, "layer"):
+        log("GDN layer block B=32")
+        res["layer"] = bench_layer(stream, args.steps, args.warmup)
     if args.only in (None, "fwht"):
         log("FWHT 512x4096 bf16")
         res["fwht"] = bench_fwht(stream, args.steps, args.warmup)
@@ -419,6 +457,17 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "gdn_decode_kernel")},
             "bytes_per_step": GDN_BYTES,
+        }
+    if "layer" in res:
+        ms = res["layer"]
+        gbs = LY_BYTES / (ms * 1e-3) / 1e9
+        sec["gdn_layer_block"] = {
+            "value": round(GDN_B / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "config": "run_delta's block between the projections: gates, conv+SiLU, normed recurrence, gated RMS "
+                      "norm, V-grouped; B=32, Hk=16, Hv=32, d=128, f32, 8 rotating state sets (3 launches)",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "bytes_per_step": LY_BYTES,
         }
     if "fwht" in res:
         ms, ms_all = res["fwht"]

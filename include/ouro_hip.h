@@ -211,6 +211,7 @@ int ouro_rotate_inv(float *x, const float *signs, size_t n, size_t block,
 #define OURO_GDN_L2NORM_QK 1u /* l2_norm q,k per head (qwen35.rs:73-79,1101-1102) */
 #define OURO_GDN_SCALE_Q   2u /* q *= 1/sqrt(d) after the norm (qwen35.rs:1095,1107) */
 #define OURO_GDN_KHEAD_DIV 4u /* k-head = v/(Hv/Hk); default v % Hk (qwen35.rs:1098) */
+#define OURO_GDN_V_GROUPED 8u /* layer output in V-grouped head order (qwen35.rs:1122-1138) */
 
 /* delta_head_dim (qwen35.rs:27-57) for one head, in place on the device:
  * decay = exp(gate); sk = decay * S^T k; dv = beta (v - sk);
@@ -258,6 +259,33 @@ int ouro_gdn_chunk_prefill(float *state, const void *q, const void *k,
                            size_t T, size_t Hk, size_t Hv, size_t d,
                            size_t chunk, unsigned flags, float eps,
                            void *workspace, void *stream);
+
+/* The delta-net layer block of one decode step, replacing the middle of
+ * Qwen35Stage::run_delta (qwen35.rs:1066-1140) between its input
+ * projections and ssm_out, for B sequences:
+ *   beta = sigmoid(beta_raw), gate = a_log * softplus(alpha_raw + dt_bias)
+ *     (qwen35.rs:1066-1070, 1241-1243);
+ *   conv_out = silu(conv_step(ring, conv_w, qkv)) per channel, ring updated
+ *     (qwen35.rs:1080-1088, 64-70);
+ *   per v-head: q, k of its k-head l2-normed, q scaled by 1/sqrt(d), one
+ *     delta_head_dim step on its state (qwen35.rs:1096-1112);
+ *   out = gated_norm_rms(o, norm_w, z) per head (qwen35.rs:1119-1121,
+ *     82-92), in V-grouped head order with OURO_GDN_V_GROUPED.
+ * Layouts (f32): qkv [B][ch] with ch = 2*Hk*d + Hv*d (q | k | v), z
+ * [B][Hv*d], beta_raw/alpha_raw [B][Hv], dt_bias/a_log [Hv], conv_w
+ * [ch][4], norm_w [d], conv_state [B][ch][3] (oldest first) and state
+ * [B][Hv][d][d] updated in place, out [B][Hv*d].  d == 128; flags:
+ * OURO_GDN_KHEAD_DIV, OURO_GDN_V_GROUPED.  `workspace` holds conv_out,
+ * beta, gate and o: ouro_gdn_layer_workspace_bytes(B, Hk, Hv, d) bytes,
+ * 16-byte aligned, or NULL for the library workspace. */
+size_t ouro_gdn_layer_workspace_bytes(size_t B, size_t Hk, size_t Hv, size_t d);
+int ouro_gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw,
+                          const float *alpha_raw, const float *dt_bias,
+                          const float *a_log, const float *conv_w,
+                          const float *norm_w, float *conv_state, float *state,
+                          float *out, size_t B, size_t Hk, size_t Hv, size_t d,
+                          unsigned flags, float eps, void *workspace,
+                          void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Resident weights (GpuPool::upload_q6k / matvec, ouro-wgpu/src/lib.rs:   */

@@ -84,6 +84,7 @@ def lib() -> C.CDLL:
             "orc_gated_norm_rms": (None, [vp, vp, vp, sz, f32, vp]),
             "orc_delta_q_scale": (f32, [sz]),
             "orc_gdn_decode": (None, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
+            "orc_gdn_layer_decode": (None, [vp] * 11 + [sz, sz, sz, sz, u32, f32, i32]),
             "orc_gdn_prefill_tokens": (None, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
             "orc_mt_threads": (i32, []),
         }
@@ -307,6 +308,21 @@ def gdn_prefill_tokens(state, q, k, v, gate, beta, T, Hk, Hv, d, flags, eps, nth
     out = np.empty((T, Hv, d), np.float32)
     lib().orc_gdn_prefill_tokens(_p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(out), T, Hk,
                                  Hv, d, flags, eps, nthreads)
+    return out
+
+
+GDN_V_GROUPED = 8
+
+
+def gdn_layer_decode(qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w, conv, state, B, Hk, Hv, d,
+                     flags, eps, nthreads=0) -> np.ndarray:
+    """run_delta's layer block (qwen35.rs:1066-1140); conv and state are updated in place."""
+    for a in (conv, state):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    args = [_f32(x) for x in (qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w)]
+    out = np.empty((B, Hv * d), np.float32)
+    lib().orc_gdn_layer_decode(*(_p(x) for x in args), _p(conv), _p(state), _p(out), B, Hk, Hv, d, flags, eps,
+                               nthreads)
     return out
 
 

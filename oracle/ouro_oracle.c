@@ -878,3 +878,62 @@ void orc_gdn_prefill_tokens(float *state, const float *q, const float *k,
     struct gdn_ctx c = {state, q, k, v, gate, beta, out, 1, Hk, Hv, d, T, flags, eps};
     orc_parallel_for(Hv, nthreads, gdn_prefill_range, &c);
 }
+
+/* ---- run_delta's layer block (qwen35.rs:1066-1140) ---------------------- */
+
+struct layer_ctx {
+    const float *qkv, *z, *beta_raw, *alpha_raw, *dt_bias, *a_log, *conv_w, *norm_w;
+    float *conv, *state, *out;
+    size_t Hk, Hv, d;
+    unsigned flags;
+    float eps;
+};
+
+static void layer_range(void *p, size_t lo, size_t hi)
+{
+    struct layer_ctx *c = (struct layer_ctx *)p;
+    const size_t d = c->d, Hk = c->Hk, Hv = c->Hv;
+    const size_t di = Hk * d, ch = 2 * di + Hv * d;
+    float *conv_out = (float *)malloc(sizeof(float) * ch);
+    float *o = (float *)malloc(sizeof(float) * Hv * d);
+    float *y = (float *)malloc(sizeof(float) * d);
+    for (size_t b = lo; b < hi; ++b) {
+        const float *qkv = c->qkv + b * ch;
+        float *ring = c->conv + b * ch * 3;
+        for (size_t i = 0; i < ch; ++i) /* qwen35.rs:1080-1088 */
+            conv_out[i] = orc_silu(orc_conv_step(ring + 3 * i, c->conv_w + 4 * i, qkv[i]));
+        for (size_t h = 0; h < Hv; ++h) { /* qwen35.rs:1096-1112 */
+            const float beta = orc_sigmoid(c->beta_raw[b * Hv + h]);
+            const float gate = c->a_log[h] * orc_softplus(c->alpha_raw[b * Hv + h] + c->dt_bias[h]);
+            const size_t kh = gdn_khead(h, Hk, Hv, c->flags);
+            gdn_one_head(c->state + (b * Hv + h) * d * d, conv_out + kh * d, conv_out + di + kh * d,
+                         conv_out + 2 * di + h * d, gate, beta, o + h * d, d,
+                         ORC_GDN_L2NORM_QK | ORC_GDN_SCALE_Q, c->eps);
+        }
+        for (size_t h = 0; h < Hv; ++h) { /* qwen35.rs:1119-1138 */
+            orc_gated_norm_rms(o + h * d, c->norm_w, c->z + b * Hv * d + h * d, d, c->eps, y);
+            size_t dst = h;
+            if (c->flags & ORC_GDN_V_GROUPED) {
+                const size_t rep = Hv / Hk, k = h % Hk, r = h / Hk;
+                dst = k * rep + r;
+            }
+            memcpy(c->out + b * Hv * d + dst * d, y, sizeof(float) * d);
+        }
+    }
+    free(conv_out);
+    free(o);
+    free(y);
+}
+
+void orc_gdn_layer_decode(const float *qkv, const float *z,
+                          const float *beta_raw, const float *alpha_raw,
+                          const float *dt_bias, const float *a_log,
+                          const float *conv_w, const float *norm_w,
+                          float *conv, float *state, float *out, size_t B,
+                          size_t Hk, size_t Hv, size_t d, unsigned flags,
+                          float eps, int nthreads)
+{
+    struct layer_ctx c = {qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w,
+                          conv, state, out, Hk, Hv, d, flags, eps};
+    orc_parallel_for(B, nthreads, layer_range, &c);
+}

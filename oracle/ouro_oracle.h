@@ -163,6 +163,28 @@ void orc_gdn_prefill_tokens(float *state, const float *q, const float *k,
                             size_t Hk, size_t Hv, size_t d, unsigned flags,
                             float eps, int nthreads);
 
+#define ORC_GDN_V_GROUPED   8u  /* gated output in V-grouped order (qwen35.rs:1122-1138) */
+
+/* The delta-net layer block of run_delta (qwen35.rs:1066-1140) for B
+ * sequences, one token each: beta = sigmoid(beta_raw), gate =
+ * a_log * softplus(alpha_raw + dt_bias); causal conv step + SiLU on every
+ * channel; per v-head l2-normed q, k (q scaled by 1/sqrt(d)) through
+ * delta_head_dim; gated_norm_rms(o, norm_w, z) per head; with
+ * ORC_GDN_V_GROUPED the heads are written in the grouped order (v-head
+ * r*Hk + k to position k*(Hv/Hk) + r).  flags: ORC_GDN_KHEAD_DIV,
+ * ORC_GDN_V_GROUPED.  Layouts:
+ *   qkv [B][ch], ch = 2*Hk*d + Hv*d (q | k | v); z [B][Hv*d];
+ *   beta_raw, alpha_raw [B][Hv]; dt_bias, a_log [Hv]; conv_w [ch][4];
+ *   norm_w [d]; conv [B][ch][3] and state [B][Hv][d*d] updated in place;
+ *   out [B][Hv*d]. */
+void orc_gdn_layer_decode(const float *qkv, const float *z,
+                          const float *beta_raw, const float *alpha_raw,
+                          const float *dt_bias, const float *a_log,
+                          const float *conv_w, const float *norm_w,
+                          float *conv, float *state, float *out, size_t B,
+                          size_t Hk, size_t Hv, size_t d, unsigned flags,
+                          float eps, int nthreads);
+
 /* OURO_N_THREADS or all logical cores (ops.rs:62-73). */
 int orc_mt_threads(void);
 

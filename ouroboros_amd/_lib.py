@@ -25,7 +25,7 @@ STATUS_NAMES = {
 KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2 = 0, 1, 30, 34, 143, 0x4932
 DT_F32, DT_BF16 = 0, 1
 FWHT_INVERSE = 1
-GDN_L2NORM_QK, GDN_SCALE_Q, GDN_KHEAD_DIV = 1, 2, 4
+GDN_L2NORM_QK, GDN_SCALE_Q, GDN_KHEAD_DIV, GDN_V_GROUPED = 1, 2, 4, 8
 
 
 class OuroError(RuntimeError):
@@ -74,6 +74,8 @@ SIGNATURES = {
     "ouro_delta_head_dim": (i32, [vp, sz, vp, vp, vp, f32, f32, vp, vp]),
     "ouro_gdn_decode": (i32, [vp, vp, vp, i32, vp, i32, vp, vp, vp, sz, sz, sz, sz, u32, f32, vp]),
     "ouro_gdn_chunk_workspace_bytes": (sz, [sz, sz, sz, sz, sz]),
+    "ouro_gdn_layer_workspace_bytes": (sz, [sz, sz, sz, sz]),
+    "ouro_gdn_layer_decode": (i32, [vp] * 11 + [sz, sz, sz, sz, u32, f32, vp, vp]),
     "ouro_gdn_chunk_prefill": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, u32, f32, vp, vp]),
     "ouro_weight_upload": (i32, [i32, vp, sz, sz, sz, f32, sz, C.POINTER(vp)]),
     "ouro_weight_free": (i32, [vp]),

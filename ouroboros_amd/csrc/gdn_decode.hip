@@ -27,6 +27,7 @@ struct DecodeArgs {
     const float *gate, *beta;  // NULL: use gate_s / beta_s for every head
     float gate_s, beta_s;
     float *out;
+    long long qk_bs, v_bs;  // elements between consecutive sequences of q/k and of v
     int B, Hk, Hv;
     unsigned flags;
     float eps;
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
         s[p] = make_float4(t[0], t[1], t[2], t[3]);
     }
 
-    const long long qk_off = (static_cast<long long>(b) * a.Hk + kh) * kD + i0;
+    const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * kD + i0;
     float4 k = ld4(static_cast<const TQK *>(a.k) + qk_off);
     float4 q = ld4(static_cast<const TQK *>(a.q) + qk_off);
     const float gate = a.gate ? a.gate[bh] : a.gate_s;
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     // This lane now holds column pair (lane & 31) / kSpan of its half.
     const int myp = (lane & 31) / kSpan;
     const int myj = col0 + 2 * myp + half;
-    const float vj = ld1(static_cast<const TV *>(a.v) + static_cast<long long>(bh) * kD + myj);
+    const float vj = ld1(static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD + myj);
     const float dj = beta * (vj - skj);
 
     float o[kPairs];
@@ -146,7 +147,8 @@ int launch(const DecodeArgs &a, hipStream_t s) {
 
 int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
                const float *gate, const float *beta, float gate_s, float beta_s, float *out,
-               size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream) {
+               size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream,
+               size_t qk_bs, size_t v_bs) {
     if (!state || !q || !k || !v || !out) return fail(OURO_ERR_INVALID_ARG, "gdn decode: NULL argument");
     if (d != static_cast<size_t>(kD)) return fail(OURO_ERR_SHAPE, "gdn decode: d = %zu, only 128 is supported", d);
     if (!B || !Hk || !Hv || Hv % Hk) return fail(OURO_ERR_SHAPE, "gdn decode: bad heads B=%zu Hk=%zu Hv=%zu", B, Hk, Hv);
@@ -157,6 +159,8 @@ int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const v
     const size_t qa = qk_dtype == OURO_DT_F32 ? 16 : 8;
     if (reinterpret_cast<uintptr_t>(q) % qa || reinterpret_cast<uintptr_t>(k) % qa)
         return fail(OURO_ERR_ALIGN, "gdn decode: q/k need %zu-byte alignment", qa);
+    if ((qk_bs * (qk_dtype == OURO_DT_F32 ? 4 : 2)) % qa)
+        return fail(OURO_ERR_ALIGN, "gdn decode: q/k sequence stride breaks %zu-byte alignment", qa);
     DecodeArgs a{};
     a.state = state;
     a.q = q;
@@ -167,6 +171,8 @@ int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const v
     a.gate_s = gate_s;
     a.beta_s = beta_s;
     a.out = out;
+    a.qk_bs = static_cast<long long>(qk_bs ? qk_bs : Hk * d);
+    a.v_bs = static_cast<long long>(v_bs ? v_bs : Hv * d);
     a.B = static_cast<int>(B);
     a.Hk = static_cast<int>(Hk);
     a.Hv = static_cast<int>(Hv);
@@ -194,14 +200,14 @@ int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype, co
     OURO_REQUIRE_INIT();
     if (!gate || !beta) return fail(OURO_ERR_INVALID_ARG, "ouro_gdn_decode: gate/beta NULL");
     return gdn_decode(state, q, k, qk_dtype, v, v_dtype, gate, beta, 0.f, 0.f, out, B, Hk, Hv, d,
-                      flags, eps, stream);
+                      flags, eps, stream, 0, 0);
 }
 
 int ouro_delta_head_dim(float *state, size_t sdim, const float *q, const float *k, const float *v,
                         float gate, float beta, float *out, void *stream) {
     OURO_REQUIRE_INIT();
     return gdn_decode(state, q, k, OURO_DT_F32, v, OURO_DT_F32, nullptr, nullptr, gate, beta, out, 1,
-                      1, 1, sdim, 0u, 0.f, stream);
+                      1, 1, sdim, 0u, 0.f, stream, 0, 0);
 }
 
 }  // extern "C"

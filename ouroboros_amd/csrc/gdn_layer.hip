@@ -1,0 +1,154 @@
+// gdn_layer.hip - the delta-net layer block of run_delta on the GPU.
+//
+// Between its input projections (qkv, z, beta, alpha) and its output
+// projection (ssm_out), run_delta (qwen35.rs:1048-1151) does, per token:
+//   beta = sigmoid(beta_raw); gate = a_log * softplus(alpha + dt_bias)
+//   conv_out = silu(conv_step(ring, w, qkv)) on every channel (ring updated)
+//   per v-head: l2-normed q, k of its k-head (q scaled by 1/sqrt(d)) through
+//   the recurrence (delta_head_dim), giving o
+//   gated = gated_norm_rms(o, norm_w, z) per head, optionally permuted to
+//   the V-grouped head order.
+// Here that is three launches on the caller's stream with no host round
+// trip: gdn_conv_gate_kernel (elementwise, writes conv_out, beta, gate into
+// the workspace), the decode kernel reading q, k, v in place from conv_out
+// (sequence stride = channels), and gdn_gated_norm_kernel.  The state
+// update dominates the bytes (2 x 64 KiB per head); the other two kernels
+// move about B * (channels * 28 + Hv * d * 16) bytes.
+#include "common.hpp"
+
+namespace ouro {
+
+int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+               const float *gate, const float *beta, float gate_s, float beta_s, float *out,
+               size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream,
+               size_t qk_bs, size_t v_bs);
+
+namespace {
+
+constexpr int kD = 128;
+
+// conv_step + SiLU per (sequence, channel) (qwen35.rs:64-70, 1080-1088; ops.rs:34-36),
+// then beta and gate per (sequence, v-head) (qwen35.rs:1066-1070, 1241-1243).
+__global__ __launch_bounds__(256) void gdn_conv_gate_kernel(const float *qkv, float *ring, const float *conv_w,
+                                                            const float *beta_raw, const float *alpha_raw,
+                                                            const float *dt_bias, const float *a_log,
+                                                            float *conv_out, float *beta, float *gate, int B,
+                                                            int ch, int Hv) {
+#pragma clang fp contract(off)
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < static_cast<long long>(B) * ch) {
+        const int c = static_cast<int>(i % ch);
+        float *r = ring + i * 3;
+        const float4 w = *reinterpret_cast<const float4 *>(conv_w + 4LL * c);
+        const float x = qkv[i], r0 = r[0], r1 = r[1], r2 = r[2];
+        const float y = w.x * r0 + w.y * r1 + w.z * r2 + w.w * x;
+        r[0] = r1;
+        r[1] = r2;
+        r[2] = x;
+        conv_out[i] = y / (1.0f + expf(-y));
+    }
+    if (i < static_cast<long long>(B) * Hv) {
+        const int h = static_cast<int>(i % Hv);
+        beta[i] = 1.0f / (1.0f + expf(-beta_raw[i]));
+        const float x = alpha_raw[i] + dt_bias[h];
+        gate[i] = a_log[h] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+    }
+}
+
+// gated_norm_rms (qwen35.rs:82-92) per (sequence, v-head), one wavefront
+// each, written at the head's V-grouped position when asked
+// (qwen35.rs:1122-1138: v-head r*Hk + k goes to k*(Hv/Hk) + r).
+__global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const float *o, const float *z, const float *norm_w,
+                                                             float *out, int B, int Hk, int Hv, unsigned flags,
+                                                             float eps) {
+#pragma clang fp contract(off)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long bh = static_cast<long long>(blockIdx.x) * 4 + wave;
+    if (bh >= static_cast<long long>(B) * Hv) return;  // whole wavefront
+    const long long b = bh / Hv;
+    const int h = static_cast<int>(bh % Hv);
+    const float2 x = *reinterpret_cast<const float2 *>(o + bh * kD + 2 * lane);
+    float ss = x.x * x.x + x.y * x.y;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + eps);
+    const float2 zz = *reinterpret_cast<const float2 *>(z + bh * kD + 2 * lane);
+    const float2 w = *reinterpret_cast<const float2 *>(norm_w + 2 * lane);
+    const float g0 = zz.x / (1.0f + expf(-zz.x)), g1 = zz.y / (1.0f + expf(-zz.y));
+    const int dst = (flags & OURO_GDN_V_GROUPED) ? (h % Hk) * (Hv / Hk) + h / Hk : h;
+    *reinterpret_cast<float2 *>(out + (b * Hv + dst) * kD + 2 * lane) =
+        make_float2(x.x * inv * w.x * g0, x.y * inv * w.y * g1);
+}
+
+constexpr size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv) {
+    const size_t ch = 2 * Hk * kD + Hv * kD;
+    return align256(B * ch * 4) + 2 * align256(B * Hv * 4) + align256(B * Hv * kD * 4);
+}
+
+int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,
+                     const float *dt_bias, const float *a_log, const float *conv_w, const float *norm_w,
+                     float *conv, float *state, float *out, size_t B, size_t Hk, size_t Hv, size_t d,
+                     unsigned flags, float eps, void *workspace, void *stream) {
+    if (!qkv || !z || !beta_raw || !alpha_raw || !dt_bias || !a_log || !conv_w || !norm_w || !conv || !state ||
+        !out)
+        return fail(OURO_ERR_INVALID_ARG, "gdn layer: NULL argument");
+    if (d != static_cast<size_t>(kD)) return fail(OURO_ERR_SHAPE, "gdn layer: d = %zu, only 128", d);
+    if (!B || !Hk || !Hv || Hv % Hk) return fail(OURO_ERR_SHAPE, "gdn layer: bad heads B=%zu Hk=%zu Hv=%zu", B, Hk, Hv);
+    if (flags & ~(OURO_GDN_KHEAD_DIV | OURO_GDN_V_GROUPED))
+        return fail(OURO_ERR_INVALID_ARG, "gdn layer: bad flags 0x%x", flags);
+    const size_t ch = 2 * Hk * kD + Hv * kD;
+    if (B * ch > 0x7fffffffULL) return fail(OURO_ERR_SHAPE, "gdn layer: too many channels");
+    if ((reinterpret_cast<uintptr_t>(conv_w) | reinterpret_cast<uintptr_t>(workspace)) % 16 ||
+        (reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(out)) % 8)
+        return fail(OURO_ERR_ALIGN, "gdn layer: conv_w and workspace need 16-byte, z, norm_w, out 8-byte alignment");
+    unsigned char *ws = static_cast<unsigned char *>(workspace);
+    if (!ws) {
+        ws = static_cast<unsigned char *>(ouro::workspace(gdn_layer_ws_bytes(B, Hk, Hv), stream));
+        if (!ws) return OURO_ERR_HIP;
+    }
+    float *conv_out = reinterpret_cast<float *>(ws);
+    float *beta = reinterpret_cast<float *>(ws + align256(B * ch * 4));
+    float *gate = reinterpret_cast<float *>(ws + align256(B * ch * 4) + align256(B * Hv * 4));
+    float *o = reinterpret_cast<float *>(ws + align256(B * ch * 4) + 2 * align256(B * Hv * 4));
+    hipStream_t s = as_stream(stream);
+    const size_t n = B * ch > B * Hv ? B * ch : B * Hv;
+    hipLaunchKernelGGL(gdn_conv_gate_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, qkv,
+                       conv, conv_w, beta_raw, alpha_raw, dt_bias, a_log, conv_out, beta, gate, static_cast<int>(B),
+                       static_cast<int>(ch), static_cast<int>(Hv));
+    int st = check_launch("gdn_conv_gate_kernel");
+    if (st) return st;
+    const size_t di = Hk * kD;
+    st = gdn_decode(state, conv_out, conv_out + di, OURO_DT_F32, conv_out + 2 * di, OURO_DT_F32, gate, beta, 0.f,
+                    0.f, o, B, Hk, Hv, d, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | (flags & OURO_GDN_KHEAD_DIV), eps,
+                    stream, ch, ch);
+    if (st) return st;
+    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((B * Hv + 3) / 4)), dim3(256), 0, s, o, z,
+                       norm_w, out, static_cast<int>(B), static_cast<int>(Hk), static_cast<int>(Hv), flags, eps);
+    return check_launch("gdn_gated_norm_kernel");
+}
+
+}  // namespace ouro
+
+using namespace ouro;
+
+extern "C" {
+
+size_t ouro_gdn_layer_workspace_bytes(size_t B, size_t Hk, size_t Hv, size_t d) {
+    if (d != static_cast<size_t>(kD) || !Hk) return 0;
+    return gdn_layer_ws_bytes(B, Hk, Hv);
+}
+
+int ouro_gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,
+                          const float *dt_bias, const float *a_log, const float *conv_w, const float *norm_w,
+                          float *conv_state, float *state, float *out, size_t B, size_t Hk, size_t Hv, size_t d,
+                          unsigned flags, float eps, void *workspace, void *stream) {
+    OURO_REQUIRE_INIT();
+    return gdn_layer_decode(qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w, conv_state, state, out,
+                            B, Hk, Hv, d, flags, eps, workspace, stream);
+}
+
+}  // extern "C"

@@ -4,7 +4,9 @@
 place).  ``gdn_decode`` is the batched decode step over sequences and
 v-heads with run_delta's per-head preprocessing (qwen35.rs:1096-1112);
 ``gdn_chunk_prefill`` runs a packed varlen prefill in chunks and equals the
-token-by-token recurrence.
+token-by-token recurrence.  ``gdn_layer_decode`` is the whole layer block
+of run_delta around the recurrence (gates, conv + SiLU, gated RMS norm;
+qwen35.rs:1066-1140).
 """
 from __future__ import annotations
 
@@ -84,3 +86,21 @@ def gdn_chunk_prefill(state: DeviceBuffer, q: DeviceBuffer, k: DeviceBuffer, v: 
 def chunk_workspace_bytes(T: int, N: int, Hv: int, d: int = S, chunk: int = 64) -> int:
     """Bytes of the per-chunk records gdn_chunk_prefill writes (0 = unsupported shape)."""
     return int(_lib.lib().ouro_gdn_chunk_workspace_bytes(T, N, Hv, d, chunk))
+
+
+def layer_workspace_bytes(B: int, Hk: int, Hv: int, d: int = S) -> int:
+    """Bytes of the scratch gdn_layer_decode uses (0 = unsupported shape)."""
+    return int(_lib.lib().ouro_gdn_layer_workspace_bytes(B, Hk, Hv, d))
+
+
+def gdn_layer_decode(qkv: DeviceBuffer, z: DeviceBuffer, beta_raw: DeviceBuffer, alpha_raw: DeviceBuffer,
+                     dt_bias: DeviceBuffer, a_log: DeviceBuffer, conv_w: DeviceBuffer, norm_w: DeviceBuffer,
+                     conv_state: DeviceBuffer, state: DeviceBuffer, out: DeviceBuffer, B: int, Hk: int, Hv: int,
+                     d: int = S, flags: int = 0, eps: float = 1e-6, workspace: DeviceBuffer | None = None,
+                     stream=None) -> None:
+    """The delta-net layer block of one decode step (run_delta, qwen35.rs:1066-1140):
+    gates, conv + SiLU, normed recurrence and gated RMS norm for B sequences.
+    conv_state and state are updated in place; all buffers f32."""
+    call("ouro_gdn_layer_decode", qkv.ptr, z.ptr, beta_raw.ptr, alpha_raw.ptr, dt_bias.ptr, a_log.ptr,
+         conv_w.ptr, norm_w.ptr, conv_state.ptr, state.ptr, out.ptr, B, Hk, Hv, d, flags, eps,
+         workspace.ptr if workspace is not None else None, stream)

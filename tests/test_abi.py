@@ -81,3 +81,13 @@ def test_no_oracle_in_product():
     for p in list((ROOT / "ouroboros_amd").rglob("*.py")) + list((ROOT / "ouroboros_amd" / "csrc").glob("*")):
         text = p.read_text(errors="ignore")
         assert "import oracle" not in text and "ouro_oracle" not in text and "orc_" not in text, p
+
+
+def test_layer_workspace_bytes():
+    from ouroboros_amd import qwen35
+
+    a = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    B, Hk, Hv, d = 32, 16, 32, 128
+    ch = 2 * Hk * d + Hv * d
+    assert qwen35.layer_workspace_bytes(B, Hk, Hv) == a(B * ch * 4) + 2 * a(B * Hv * 4) + a(B * Hv * d * 4)
+    assert qwen35.layer_workspace_bytes(B, Hk, Hv, d=64) == 0

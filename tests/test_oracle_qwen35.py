@@ -168,3 +168,77 @@ def test_prefill_tokens_equals_repeated_decode(orc):
         o = orc.gdn_decode(b, q[t:t + 1], k[t:t + 1], v[t:t + 1], gate[t:t + 1], beta[t:t + 1], 1, Hk, Hv, d, fl, 1e-6)
         assert np.array_equal(o[0], out[t])
     assert np.array_equal(a, b[0])
+
+
+def layer_inputs(rng, B, Hk, Hv, d=S):
+    ch = 2 * Hk * d + Hv * d
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    return dict(qkv=f(B, ch), z=f(B, Hv * d), beta_raw=f(B, Hv), alpha_raw=f(B, Hv), dt_bias=f(Hv),
+                a_log=(-np.exp(f(Hv))).astype(np.float32), conv_w=(0.5 * f(ch, 4)).astype(np.float32),
+                norm_w=f(d), conv=f(B, ch, 3), state=(0.02 * f(B, Hv, d * d)).astype(np.float32))
+
+
+def layer_f64(x, B, Hk, Hv, d, flags, eps):
+    """run_delta's block in float64 numpy: conv over the ring, matrix-form
+    recurrence per head, gated RMS norm, optional V-grouped permutation."""
+    qkv, ring = x["qkv"].astype(np.float64), x["conv"].astype(np.float64)
+    w = x["conv_w"].astype(np.float64)
+    y = (ring * w[None, :, :3]).sum(-1) + w[None, :, 3] * qkv
+    co = y / (1 + np.exp(-y))
+    new_ring = np.concatenate([ring[:, :, 1:], qkv[:, :, None]], axis=2)
+    beta = 1 / (1 + np.exp(-x["beta_raw"].astype(np.float64)))
+    sp = x["alpha_raw"].astype(np.float64) + x["dt_bias"].astype(np.float64)
+    sp = np.where(sp > 20, sp, np.log1p(np.exp(np.minimum(sp, 20))))
+    gate = x["a_log"].astype(np.float64) * sp
+    di = Hk * d
+    st = x["state"].astype(np.float64).reshape(B, Hv, d, d)  # [b][h][j][i]: S(i, j) at i + j d
+    out = np.zeros((B, Hv * d))
+    for b in range(B):
+        for h in range(Hv):
+            kh = h // (Hv // Hk) if flags & 4 else h % Hk
+            q = co[b, kh * d:(kh + 1) * d]
+            k = co[b, di + kh * d:di + (kh + 1) * d]
+            v = co[b, 2 * di + h * d:2 * di + (h + 1) * d]
+            q = q / (np.sqrt((q * q).sum()) + eps) / np.sqrt(d)
+            k = k / (np.sqrt((k * k).sum()) + eps)
+            Sm = st[b, h].T  # Sm[i][j]
+            dec = np.exp(gate[b, h])
+            dv = beta[b, h] * (v - dec * Sm.T @ k)
+            Sm = dec * Sm + np.outer(k, dv)
+            st[b, h] = Sm.T
+            o = Sm.T @ q
+            zz = x["z"][b, h * d:(h + 1) * d].astype(np.float64)
+            g = o / np.sqrt((o * o).mean() + eps) * x["norm_w"] * (zz / (1 + np.exp(-zz)))
+            dst = (h % Hk) * (Hv // Hk) + h // Hk if flags & 8 else h
+            out[b, dst * d:(dst + 1) * d] = g
+    return out, new_ring, st.reshape(B, Hv, d * d)
+
+
+@pytest.mark.parametrize("flags", [0, 4, 8, 12])
+def test_layer_block_matches_float64(orc, flags):
+    rng = np.random.default_rng(40 + flags)
+    B, Hk, Hv = 2, 2, 4
+    x = layer_inputs(rng, B, Hk, Hv)
+    want, ring, st = layer_f64(x, B, Hk, Hv, S, flags, 1e-6)
+    conv, state = x["conv"].copy(), x["state"].copy()
+    got = orc.gdn_layer_decode(x["qkv"], x["z"], x["beta_raw"], x["alpha_raw"], x["dt_bias"], x["a_log"],
+                               x["conv_w"], x["norm_w"], conv, state, B, Hk, Hv, S, flags, 1e-6)
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-5
+    assert np.array_equal(conv, ring.astype(np.float32))  # the ring shifts exactly
+    assert np.abs(state - st).max() / np.abs(st).max() < 1e-5
+
+
+def test_layer_block_v_grouped_is_a_head_permutation(orc):
+    # qwen35.rs:1126-1135: v-head r*nk + k lands at k*rep + r.
+    rng = np.random.default_rng(7)
+    B, Hk, Hv = 1, 2, 6
+    x = layer_inputs(rng, B, Hk, Hv)
+    args = lambda: [x[n] for n in ("qkv", "z", "beta_raw", "alpha_raw", "dt_bias", "a_log", "conv_w", "norm_w")]  # noqa: E731
+    plain = orc.gdn_layer_decode(*args(), x["conv"].copy(), x["state"].copy(), B, Hk, Hv, S, 0, 1e-6)
+    grouped = orc.gdn_layer_decode(*args(), x["conv"].copy(), x["state"].copy(), B, Hk, Hv, S,
+                                   orc.GDN_V_GROUPED, 1e-6)
+    rep = Hv // Hk
+    for k in range(Hk):
+        for r in range(rep):
+            src, dst = (r * Hk + k) * S, (k * rep + r) * S
+            assert np.array_equal(grouped[0, dst:dst + S], plain[0, src:src + S])
