@@ -211,6 +211,49 @@ def bench_layer(stream, steps, warmup):
     return time_events(stream, step, max(steps, 2 * GDN_SETS), warmup)
 
 
+TL1_OUT, TL1_IN = 248320, 5120
+TL1_ROW = TL1_IN // 128 * 28
+TL1_BYTES = TL1_OUT * TL1_ROW + TL1_IN * 4 + TL1_OUT * 4
+
+
+def tl1_lmhead_payload():
+    """The reference's own lm_head probe input (ops.rs:694-717): bytes
+    (i ^ (i >> 13)) * 0x9E, fp16 scale 1.0 in every 28-byte group, x[i] = ((i % 13) - 6) / 10."""
+    i = np.arange(TL1_OUT * TL1_ROW, dtype=np.uint32)
+    payload = ((i ^ (i >> 13)) * 0x9E).astype(np.uint8)
+    g = payload.reshape(-1, 28)
+    g[:, 26], g[:, 27] = 0x00, 0x3C
+    x = (((np.arange(TL1_IN) % 13) - 6.0) * 0.1).astype(np.float32)
+    return payload, x
+
+
+def bench_tl1(stream, steps, warmup):
+    """TL1 (PTQ1_0) matvec at the reference's lm_head probe shape 248320x5120:
+    a resident weight handle (repacked on upload for the table-lookup GEMV),
+    the same with the fused finite_argmax (greedy sample), and the raw-payload
+    ouro_matvec_q path."""
+    import ctypes as C
+
+    from ouroboros_amd._lib import KIND_TL1, call
+    from ouroboros_amd.device import DeviceBuffer
+
+    payload, x = tl1_lmhead_payload()
+    h = C.c_void_p()
+    call("ouro_weight_upload", KIND_TL1, payload.ctypes.data, payload.nbytes, TL1_OUT, TL1_IN, 1.0, 1, C.byref(h))
+    xd = DeviceBuffer.from_host(x)
+    y = DeviceBuffer((TL1_OUT,), np.float32)
+    idx = DeviceBuffer((1,), np.int32)
+    n = max(3, steps // 5)
+    ms = time_events(stream, lambda _i: call("ouro_weight_matvec", h.value, xd.ptr, y.ptr, stream), n, 2)
+    ms_am = time_events(stream, lambda _i: call("ouro_weight_matvec_argmax", h.value, xd.ptr, None, idx.ptr, stream),
+                        n, 2)
+    call("ouro_weight_free", h.value)
+    w = DeviceBuffer.from_host(payload)
+    ms_raw = time_events(stream, lambda _i: call("ouro_matvec_q", w.ptr, KIND_TL1, TL1_OUT, TL1_IN, xd.ptr, y.ptr,
+                                                 stream), 3, 1)
+    return ms, ms_am, ms_raw
+
+
 def bench_fwht(stream, steps, warmup):
     from ouroboros_amd import quant
     from ouroboros_amd._lib import DT_BF16, call
@@ -388,7 +431,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["gemv", "gdn", "layer", "fwht", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gdn", "layer", "tl1", "fwht", "prefill", "copy"], default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -415,6 +458,9 @@ def main() -> int:
     if args.only in (None, "layer"):
         log("GDN layer block B=32")
         res["layer"] = bench_layer(stream, args.steps, args.warmup)
+    if args.only in (None, "tl1"):
+        log("TL1 matvec 248320x5120 (lm_head probe)")
+        res["tl1"] = bench_tl1(stream, args.steps, args.warmup)
     if args.only in (None, "fwht"):
         log("FWHT 512x4096 bf16")
         res["fwht"] = bench_fwht(stream, args.steps, args.warmup)
@@ -468,6 +514,20 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
             "bytes_per_step": LY_BYTES,
+        }
+    if "tl1" in res:
+        ms, ms_am, ms_raw = res["tl1"]
+        gbs = TL1_BYTES / (ms * 1e-3) / 1e9
+        sec["tl1_matvec_lmhead"] = {
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4),
+            "config": "TL1 (PTQ1_0) 248320x5120 resident weight (table-lookup GEMV), fp32 x and y, the reference's "
+                      "lm_head probe payload (ops.rs:694-717; its CPU figure is 1.75 GB/s on an i7-3770)",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "tl1_lut_kernel")},
+            "bytes_per_call": TL1_BYTES,
+            "greedy_sample_ms": round(ms_am, 4),
+            "greedy_sample_tokens_per_s": round(1e3 / ms_am, 1),
+            "raw_payload_matvec_q_ms": round(ms_raw, 4),
         }
     if "fwht" in res:
         ms, ms_all = res["fwht"]

@@ -304,12 +304,25 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes,
                        size_t out_len, size_t in_len, float w_scale,
                        size_t max_cols, ouro_weight_t *out);
 int ouro_weight_free(ouro_weight_t w);
-/* Device payload of a handle (what ouro_matvec_q takes for its kind). */
+/* Device payload of a handle (what ouro_matvec_q takes for its kind); NULL
+ * for OURO_KIND_TL1, whose handle holds the payload repacked for the
+ * table-lookup GEMV (ouro_weight_matvec/matmul) instead of the raw groups. */
 const void *ouro_weight_payload(ouro_weight_t w);
 int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y,
                        void *stream);
 int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y,
                        void *stream);
+/* Greedy token of a head (Qwen35Stage::sample, qwen35.rs:746-757:
+ * finite_argmax(W x)): y = W x for one column, then *idx = finite_argmax(y)
+ * as a device int32.  y may be NULL (the handle's own logits scratch is
+ * used).  Nothing is allocated. */
+int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y,
+                              int32_t *idx, void *stream);
+/* finite_argmax (infer/mod.rs:70-83) of n device floats: the first index of
+ * the largest non-NaN value (-0 and +0 compare equal), 0 if every value is
+ * NaN; *idx is a device int32.  Uses 8 KiB of per-device scratch allocated
+ * on the first call. */
+int ouro_finite_argmax(const float *y, size_t n, int32_t *idx, void *stream);
 
 #ifdef __cplusplus
 }

@@ -85,6 +85,7 @@ def lib() -> C.CDLL:
             "orc_delta_q_scale": (f32, [sz]),
             "orc_gdn_decode": (None, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
             "orc_gdn_layer_decode": (None, [vp] * 11 + [sz, sz, sz, sz, u32, f32, i32]),
+            "orc_finite_argmax": (sz, [vp, sz]),
             "orc_gdn_prefill_tokens": (None, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
             "orc_mt_threads": (i32, []),
         }
@@ -324,6 +325,12 @@ def gdn_layer_decode(qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w
     lib().orc_gdn_layer_decode(*(_p(x) for x in args), _p(conv), _p(state), _p(out), B, Hk, Hv, d, flags, eps,
                                nthreads)
     return out
+
+
+def finite_argmax(l) -> int:
+    """infer/mod.rs:70-83."""
+    a = _f32(l)
+    return int(lib().orc_finite_argmax(_p(a), a.size))
 
 
 def mt_threads() -> int:

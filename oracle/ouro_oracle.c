@@ -937,3 +937,18 @@ void orc_gdn_layer_decode(const float *qkv, const float *z,
                           conv, state, out, Hk, Hv, d, flags, eps};
     orc_parallel_for(B, nthreads, layer_range, &c);
 }
+
+size_t orc_finite_argmax(const float *l, size_t n) /* infer/mod.rs:70-83 */
+{
+    size_t best = 0;
+    int found = 0;
+    for (size_t i = 0; i < n; ++i) {
+        float v = l[i];
+        if (v != v) continue;
+        if (!found || v > l[best]) {
+            best = i;
+            found = 1;
+        }
+    }
+    return best;
+}

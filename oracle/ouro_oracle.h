@@ -185,6 +185,10 @@ void orc_gdn_layer_decode(const float *qkv, const float *z,
                           size_t Hk, size_t Hv, size_t d, unsigned flags,
                           float eps, int nthreads);
 
+/* finite_argmax (infer/mod.rs:70-83): first index of the largest non-NaN
+ * value under `>`, 0 when every value is NaN. */
+size_t orc_finite_argmax(const float *l, size_t n);
+
 /* OURO_N_THREADS or all logical cores (ops.rs:62-73). */
 int orc_mt_threads(void);
 

@@ -80,6 +80,8 @@ SIGNATURES = {
     "ouro_weight_upload": (i32, [i32, vp, sz, sz, sz, f32, sz, C.POINTER(vp)]),
     "ouro_weight_free": (i32, [vp]),
     "ouro_weight_payload": (vp, [vp]),
+    "ouro_weight_matvec_argmax": (i32, [vp, vp, vp, vp, vp]),
+    "ouro_finite_argmax": (i32, [vp, sz, vp, vp]),
     "ouro_weight_matvec": (i32, [vp, vp, vp, vp]),
     "ouro_weight_matmul": (i32, [vp, vp, sz, vp, vp]),
 }

@@ -98,4 +98,45 @@ __device__ __forceinline__ T reduce_scatter(T (&v)[N], int lane) {
     return v[0];
 }
 
+// Most workgroups of an argmax (slots of 64-bit keys in its scratch).
+constexpr int kArgmaxBlocks = 1024;
+int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *stream);
+
+// finite_argmax keys (infer/mod.rs:70-83): the value's bits in an
+// order-preserving form (-0 taken as +0, as `>` does) in the high word, the
+// complement of the index in the low word (the lowest index wins a tie), 0
+// for NaN, so the largest key is the answer and key 0 means "nothing found".
+__device__ __forceinline__ unsigned long long argmax_key(float v, unsigned i) {
+    if (v != v) return 0ull;
+    uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(u) << 32) | (0xffffffffu - i);
+}
+
+__device__ __forceinline__ unsigned long long argmax_key_max(unsigned long long a, unsigned long long b) {
+    return a > b ? a : b;
+}
+
+// Reduce a thread's key over the workgroup (blockDim.x a multiple of 64, at
+// most 1024 threads); thread 0 gets the workgroup's key.
+__device__ __forceinline__ unsigned long long argmax_block_key(unsigned long long k) {
+    __shared__ unsigned long long part[16];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(k), off, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(k >> 32), off, 64);
+        k = argmax_key_max(k, (static_cast<unsigned long long>(hi) << 32) | lo);
+    }
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (unsigned w = 1; w < blockDim.x / 64; ++w) k = argmax_key_max(k, part[w]);
+    return k;
+}
+
+// The key of an argmax over per-workgroup keys, as the index it stands for.
+__device__ __forceinline__ int32_t argmax_index(unsigned long long best) {
+    return best ? static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best)) : 0;
+}
+
 }  // namespace ouro

@@ -1,0 +1,215 @@
+// tl1_lut.hip - TL1 (PTQ1_0) matvec by table lookup, for resident weights.
+//
+// A PTQ1_0 group (dequant.rs:140-171) is 28 bytes: qs[0..16] carry the
+// elements n*16 + m, qs[16..24] the elements 80 + n*8 + m, qh[0..2] the
+// elements 120 + n*2 + h (5, 5 and 4 trits per byte, digit of byte v at
+// stage n = ((v * 3^n mod 256) * 3) >> 8, trit = digit - 1), then an f16
+// scale d.  matvec_tl1 (ops.rs:294-363) computes y[r] = sum over groups of
+// sum over elements (trit * d) * x.
+//
+// Here every payload byte is one lookup: for a block of 4 groups the
+// workgroup builds, in LDS, the partial dot of each of the 256 byte values
+// of each of the 26 byte positions with its 4 or 5 x values
+// (T[g][b][v] = sum_n trit_n(v) x[...]); a row then costs 26 lookups and
+// adds per group and one multiply by d.  Weights are repacked on upload so
+// that the 112 bytes of a row's group block sit in 7 x 16 B lane-interleaved
+// chunks ([block][row tile of 64][chunk][lane]): every load instruction
+// reads 1 KiB contiguously.  Each group block writes a partial sum per row;
+// a second kernel adds the blocks (and can take the finite_argmax of the
+// result on the way, for a greedy sample).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace ouro {
+namespace {
+
+constexpr int kGB = 4;                 // groups per block
+constexpr int kChunks = kGB * 28 / 16; // 7 x 16 B per row per block
+constexpr int kThreads = 1024;
+constexpr int kTable = kGB * 26 * 256; // floats
+constexpr int LUT_LDS = kTable * 4 + kGB * 128 * 4;
+
+__device__ __forceinline__ int tl1_trit(uint32_t v, uint32_t pow3) {
+    const uint32_t q = (v * pow3) & 0xffu;  // u8 wrapping_mul
+    return static_cast<int>((q * 3u) >> 8) - 1;
+}
+
+// Raw row-major payload [rows][groups][28] -> [block][tile][chunk][lane] x 16 B,
+// zero-padded (a padded group has d = 0).  One thread per (row, block, 16 B chunk).
+__global__ void tl1_repack_kernel(const uint8_t *raw, uint4 *dst, int out_len, int groups, int nb, int ntiles) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    const long long total = static_cast<long long>(nb) * ntiles * 64 * kChunks;
+    if (i >= total) return;
+    const int lane = static_cast<int>(i % 64);
+    const int c = static_cast<int>((i / 64) % kChunks);
+    const long long bt = i / (64 * kChunks);
+    const int tile = static_cast<int>(bt % ntiles), b = static_cast<int>(bt / ntiles);
+    const int row = tile * 64 + lane;
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (row < out_len) {
+        const long long rb = static_cast<long long>(groups) * 28;
+        for (int k = 0; k < 16; ++k) {
+            const int off = c * 16 + k;          // byte within the block's 112
+            const int g = b * kGB + off / 28;   // group
+            if (g < groups) {
+                const uint32_t v = raw[row * rb + static_cast<long long>(g) * 28 + off % 28];
+                w[k / 4] |= v << (8 * (k % 4));
+            }
+        }
+    }
+    dst[i] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One group block per blockIdx.y; waves walk row tiles.
+__global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const float *x, float *partial,
+                                                           int out_len, int groups, int ntiles) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    float *T = lds;               // [g][b][256]
+    float *xs = lds + kTable;     // [g * 128]
+    const int b = blockIdx.y;
+    const int gcnt = min(kGB, groups - b * kGB);
+    const int tid = threadIdx.x;
+    for (int i = tid; i < gcnt * 128; i += kThreads) xs[i] = x[b * kGB * 128 + i];
+    __syncthreads();
+    for (int e = tid; e < gcnt * 26 * 256; e += kThreads) {
+        const int v = e & 255, bb = (e >> 8) % 26, g = e / (26 * 256);
+        int base, stride, cnt;
+        if (bb < 16) {
+            base = bb, stride = 16, cnt = 5;
+        } else if (bb < 24) {
+            base = 80 + (bb - 16), stride = 8, cnt = 5;
+        } else {
+            base = 120 + (bb - 24), stride = 2, cnt = 4;
+        }
+        const float *xg = xs + g * 128 + base;
+        float s = 0.f;
+        uint32_t p3 = 1;
+#pragma unroll
+        for (int n = 0; n < 5; ++n) {
+            if (n < cnt) s += static_cast<float>(tl1_trit(v, p3)) * xg[n * stride];
+            p3 *= 3;
+        }
+        T[e] = s;
+    }
+    __syncthreads();
+
+    const int lane = tid & 63;
+    const int wglobal = blockIdx.x * (kThreads / 64) + (tid >> 6);
+    const int wstride = gridDim.x * (kThreads / 64);
+    const uint4 *wb = w + static_cast<long long>(b) * ntiles * kChunks * 64;
+    float *pb = partial + static_cast<long long>(b) * out_len;
+    // the next tile's 112 bytes are loaded while the current one is looked up
+    uint4 nx[kChunks];
+    auto load_tile = [&](int tile) {
+        const uint4 *src = wb + static_cast<long long>(tile) * kChunks * 64 + lane;
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) nx[c] = src[c * 64];
+    };
+    if (wglobal < ntiles) load_tile(wglobal);
+    for (int tile = wglobal; tile < ntiles; tile += wstride) {
+        uint32_t u[kChunks * 4];
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            u[4 * c] = nx[c].x, u[4 * c + 1] = nx[c].y, u[4 * c + 2] = nx[c].z, u[4 * c + 3] = nx[c].w;
+        }
+        if (tile + wstride < ntiles) load_tile(tile + wstride);
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < kGB; ++g) {
+            if (g < gcnt) {
+                const float *Tg = T + g * 26 * 256;
+                float gs = 0.f;
+#pragma unroll
+                for (int bb = 0; bb < 26; ++bb) {
+                    const int by = g * 28 + bb;  // byte within the row's 112
+                    const uint32_t v = (u[by >> 2] >> (8 * (by & 3))) & 0xffu;
+                    gs += Tg[bb * 256 + v];
+                }
+                const uint32_t dw = u[(g * 28 + 24) >> 2] >> 16;  // bytes 26, 27 of the group
+                const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dw)));
+                acc += d * gs;
+            }
+        }
+        const int row = tile * 64 + lane;
+        if (row < out_len) pb[row] = acc;
+    }
+}
+
+// y[r] = sum over blocks of partial[b][r], blocks in order; with ARGMAX the
+// finite_argmax of y is reduced on the way (few workgroups: one atomic each).
+template <bool ARGMAX>
+__global__ __launch_bounds__(256) void tl1_sum_kernel(const float *partial, float *y, int out_len, int nb,
+                                                      unsigned long long *keys) {
+    unsigned long long k = 0;
+    for (int r = blockIdx.x * 256 + threadIdx.x; r < out_len; r += gridDim.x * 256) {
+        float s = 0.f;
+        for (int b = 0; b < nb; ++b) s += partial[static_cast<long long>(b) * out_len + r];
+        y[r] = s;
+        if (ARGMAX) k = argmax_key_max(k, argmax_key(s, static_cast<unsigned>(r)));
+    }
+    if (ARGMAX) {
+        k = argmax_block_key(k);
+        if (threadIdx.x == 0) keys[blockIdx.x] = k;
+    }
+}
+
+}  // namespace
+
+size_t tl1_lut_bytes(size_t out_len, size_t in_len) {
+    const size_t groups = in_len / 128, nb = (groups + kGB - 1) / kGB, ntiles = (out_len + 63) / 64;
+    return nb * ntiles * 64 * kChunks * 16;
+}
+
+size_t tl1_lut_partial_floats(size_t out_len, size_t in_len) {
+    const size_t groups = in_len / 128, nb = (groups + kGB - 1) / kGB;
+    return nb * out_len;
+}
+
+int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream) {
+    const size_t groups = in_len / 128, nb = (groups + kGB - 1) / kGB, ntiles = (out_len + 63) / 64;
+    const size_t total = nb * ntiles * 64 * kChunks;
+    hipLaunchKernelGGL(tl1_repack_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), raw, static_cast<uint4 *>(dst), static_cast<int>(out_len),
+                       static_cast<int>(groups), static_cast<int>(nb), static_cast<int>(ntiles));
+    return check_launch("tl1_repack_kernel");
+}
+
+int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream) {
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(tl1_lut_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LUT_LDS) != hipSuccess)
+            return fail(OURO_ERR_HIP, "tl1 lut: %d B of LDS refused", LUT_LDS);
+        attr = true;
+    }
+    const int groups = static_cast<int>(in_len / 128), nb = (groups + kGB - 1) / kGB;
+    const int ntiles = static_cast<int>((out_len + 63) / 64);
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    // at most one workgroup per CU in all (LDS holds one): a grid larger than
+    // the CU count would run a second round on a few CUs
+    int gx = cus / nb;
+    gx = std::max(1, std::min(gx, (ntiles + kThreads / 64 - 1) / (kThreads / 64)));
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(tl1_lut_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(nb)), dim3(kThreads),
+                       LUT_LDS, s, static_cast<const uint4 *>(packed), x, partial, static_cast<int>(out_len), groups,
+                       ntiles);
+    int st = check_launch("tl1_lut_kernel");
+    if (st) return st;
+    if (!idx) {
+        hipLaunchKernelGGL(tl1_sum_kernel<false>, dim3(static_cast<unsigned>((out_len + 255) / 256)), dim3(256), 0, s,
+                           partial, y, static_cast<int>(out_len), nb, nullptr);
+        return check_launch("tl1_sum_kernel");
+    }
+    auto *keys = static_cast<unsigned long long *>(amax_scratch);
+    const int blocks = static_cast<int>(std::min<size_t>((out_len + 255) / 256, kArgmaxBlocks));
+    hipLaunchKernelGGL(tl1_sum_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, partial, y,
+                       static_cast<int>(out_len), nb, keys);
+    st = check_launch("tl1_sum_kernel");
+    if (st) return st;
+    return argmax_final(keys, blocks, idx, stream);
+}
+
+}  // namespace ouro

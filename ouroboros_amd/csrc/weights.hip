@@ -1,8 +1,10 @@
 // weights.hip - resident weight handles, the device analogue of the
 // reference's GpuPool (ouro-wgpu/src/lib.rs:251-356): a tensor is uploaded
 // once (and repacked on upload, as upload_q6k repacks 210 -> 212 B blocks),
-// then applied by handle.  An I2 handle also owns its activation-quantisation
-// scratch, sized at upload for max_cols columns, so its matvec allocates
+// then applied by handle.  I2 codes are tiled for the int8 GEMV; TL1 payloads
+// are repacked for the table-lookup GEMV.  Every handle owns the scratch its
+// calls need (activation quantisation for up to max_cols columns, TL1
+// partial sums, a logits vector and the argmax key), so its calls allocate
 // nothing.
 #include "common.hpp"
 
@@ -14,14 +16,24 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
             const float *w_scale, void *stream);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
+size_t tl1_lut_bytes(size_t out_len, size_t in_len);
+size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
+int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream);
+int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream);
+int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream);
 }  // namespace ouro
 
 struct ouro_weight {
     int kind = 0;
     size_t out_len = 0, in_len = 0, max_cols = 0;
-    void *payload = nullptr;
-    int8_t *xq = nullptr;
+    void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
+    int8_t *xq = nullptr;     // I2: activation scratch
     float *dscale = nullptr;
+    float *partial = nullptr; // TL1: per-group-block partial sums
+    void *aux = nullptr;      // one allocation: y scratch [out_len] f32, then the argmax key slots
+    float *y = nullptr;
+    void *amax = nullptr;
 };
 
 using namespace ouro;
@@ -44,6 +56,8 @@ void release(ouro_weight *w) {
     if (!w) return;
     if (w->payload) (void)hipFree(w->payload);
     if (w->xq) (void)hipFree(w->xq);
+    if (w->partial) (void)hipFree(w->partial);
+    if (w->aux) (void)hipFree(w->aux);
     delete w;
 }
 
@@ -98,6 +112,27 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
         }
         w->xq = static_cast<int8_t *>(scratch);
         w->dscale = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + xb);
+    } else if (kind == OURO_KIND_TL1) {
+        // repack for the lookup kernel; the raw payload lives only during the upload
+        void *raw = nullptr;
+        const size_t pf = tl1_lut_partial_floats(out_len, in_len);
+        if (hipMalloc(&w->payload, tl1_lut_bytes(out_len, in_len)) != hipSuccess ||
+            hipMalloc(reinterpret_cast<void **>(&w->partial), pf * sizeof(float)) != hipSuccess ||
+            hipMalloc(&raw, bytes) != hipSuccess) {
+            if (raw) (void)hipFree(raw);
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+        }
+        int st = OURO_OK;
+        if (hipMemcpy(raw, host, bytes, hipMemcpyHostToDevice) != hipSuccess)
+            st = fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
+        if (!st) st = tl1_repack(static_cast<const uint8_t *>(raw), out_len, in_len, w->payload, nullptr);
+        if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
+        (void)hipFree(raw);
+        if (st) {
+            release(w);
+            return st;
+        }
     } else {
         if (hipMalloc(&w->payload, bytes) != hipSuccess) {
             release(w);
@@ -108,6 +143,14 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             return fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         }
     }
+    // y scratch (for argmax without a caller y) and the argmax key slots
+    const size_t yb = (out_len * sizeof(float) + 255) & ~size_t(255);
+    if (hipMalloc(&w->aux, yb + kArgmaxBlocks * 8) != hipSuccess) {
+        release(w);
+        return fail(OURO_ERR_HIP, "ouro_weight_upload: scratch allocation failed");
+    }
+    w->y = static_cast<float *>(w->aux);
+    w->amax = static_cast<uint8_t *>(w->aux) + yb;
     *out = w;
     return OURO_OK;
 }
@@ -121,14 +164,36 @@ int ouro_weight_free(ouro_weight_t w) {
     return OURO_OK;
 }
 
-const void *ouro_weight_payload(ouro_weight_t w) { return w ? w->payload : nullptr; }
+const void *ouro_weight_payload(ouro_weight_t w) {
+    return (w && w->kind != OURO_KIND_TL1) ? w->payload : nullptr;
+}
 
 int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void *stream) {
     OURO_REQUIRE_INIT();
     if (!w) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matmul: NULL handle");
+    if (!x || !y || !k) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matmul: NULL argument or k = 0");
     if (w->kind == OURO_KIND_I2 && k > w->max_cols)
         return fail(OURO_ERR_SHAPE, "ouro_weight_matmul: k %zu > max_cols %zu of the handle", k, w->max_cols);
+    if (w->kind == OURO_KIND_TL1) {  // one lookup pass per column, y column-major as matmul_q
+        for (size_t c = 0; c < k; ++c) {
+            const int st = tl1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,
+                                          w->partial, nullptr, nullptr, stream);
+            if (st) return st;
+        }
+        return OURO_OK;
+    }
     return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->dscale, stream);
+}
+
+int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t *idx, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (!w || !x || !idx) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matvec_argmax: NULL argument");
+    float *yy = y ? y : w->y;
+    if (w->kind == OURO_KIND_TL1)  // the argmax rides on the partial-sum kernel
+        return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream);
+    const int st = ouro_weight_matmul(w, x, 1, yy, stream);
+    if (st) return st;
+    return argmax_f32(yy, w->out_len, w->amax, idx, stream);
 }
 
 int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y, void *stream) {

@@ -96,6 +96,13 @@ class Weight:
         call("ouro_weight_matmul", self.handle, xb.ptr, k, y.ptr, stream)
         return y.download() if host_out else y
 
+    def matvec_argmax(self, x, y: DeviceBuffer | None = None, stream=None) -> int:
+        """finite_argmax(W x) (Qwen35Stage::sample, qwen35.rs:746-757); y optionally keeps the logits."""
+        xb, _ = _dev(x, np.float32)
+        idx = DeviceBuffer((1,), np.int32)
+        call("ouro_weight_matvec_argmax", self.handle, xb.ptr, y.ptr if y is not None else None, idx.ptr, stream)
+        return int(idx.download()[0])
+
     def free(self) -> None:
         if self.handle is not None:
             call("ouro_weight_free", self.handle)
@@ -108,3 +115,11 @@ class Weight:
                 self.handle = None
         except Exception:
             pass
+
+
+def finite_argmax(y) -> int:
+    """finite_argmax (infer/mod.rs:70-83) of a device (or host) float vector, on the GPU."""
+    yb, _ = _dev(y, np.float32)
+    idx = DeviceBuffer((1,), np.int32)
+    call("ouro_finite_argmax", yb.ptr, yb.nbytes // yb.dtype.itemsize, idx.ptr, None)
+    return int(idx.download()[0])

@@ -116,3 +116,20 @@ def test_dense_kinds_match_float64(orc):
         y = orc.matvec_q(payload.reshape(-1), kind, out_len, in_len, x)
         ref = wf.astype(np.float64) @ x.astype(np.float64)
         assert np.allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_finite_argmax(orc):  # infer/mod.rs:70-83
+    nan, inf = float("nan"), float("inf")
+    assert orc.finite_argmax([1.0, 3.0, 2.0]) == 1
+    assert orc.finite_argmax([nan, 1.0, nan, 5.0, nan]) == 3   # NaN skipped
+    assert orc.finite_argmax([2.0, 7.0, 7.0, 1.0]) == 1        # strict >: first maximum wins
+    assert orc.finite_argmax([nan, nan]) == 0                  # nothing found
+    assert orc.finite_argmax([-0.0, 0.0]) == 0                 # -0 and +0 compare equal
+    assert orc.finite_argmax([-inf, -inf]) == 0
+    assert orc.finite_argmax([nan, -inf, -5.0]) == 2
+    assert orc.finite_argmax([1.0, inf, nan, inf]) == 1
+    rng = np.random.default_rng(3)
+    for _ in range(20):  # against numpy's nanargmax (first occurrence) on NaN-sprinkled vectors
+        x = rng.standard_normal(1000).astype(np.float32)
+        x[rng.random(1000) < 0.1] = nan
+        assert orc.finite_argmax(x) == int(np.nanargmax(x))
