@@ -108,15 +108,22 @@ int ouro_event_elapsed_ms(float *ms, void *start, void *stop);
  *
  * Device-tiled I2 (what the kernels read; ouro_i2_tile() produces it):
  *   G = in_len / 256 four-weight groups per lane per row (in_len % 256 == 0),
- *   R = 16 / gcd(G, 16) rows per tile, tiles = ceil(out_len / R) (rows past
- *   out_len hold code 1, i.e. w = 0, and are never written out).  Tile t
- *   starts at byte
- *   t * R * in_len / 4.  Inside a tile, lane l (0..63) owns the k-range
- *   [4*G*l, 4*G*(l+1)) of all R rows; its 32-bit word d (0 .. R*G/4 - 1)
- *   sits at byte (d/4)*1024 + l*16 + (d%4)*4, so every 16-byte load of a
- *   64-lane wavefront is one contiguous 1 KiB segment.  Word d carries four
- *   groups gi = 4d + f (f = 0..3); group gi is row r = gi / G, k-group
- *   g = gi % G, i.e. weights k = 4*G*l + 4*g + b (b = 0..3), whose codes sit
+ *   R = 8 rows per tile, tiles = ceil(out_len / 8) (rows past out_len hold
+ *   code 1, i.e. w = 0, and are never written out).  Tile t starts at byte
+ *   t * 8 * in_len / 4.  Inside a tile, lane l (0..63) owns G k-groups
+ *   (four weights each) of all 8 rows: lane-local group g (0..G-1) is the
+ *   canonical byte column
+ *     kg(l, g) = 64*o + s*l + (g - o),
+ *   where the G local groups are cut into chunks of s = 4 groups, then one
+ *   of s = 2 (if G % 4 >= 2), then one of s = 1 (if G is odd), and o is the
+ *   first local group of g's chunk; so each chunk's activations are one
+ *   contiguous segment (4*s bytes per lane, lanes in order).  A lane's 2*G
+ *   32-bit words are stored in units of U = 16 bytes (G even) or U = 8 bytes
+ *   (G odd), W = U/4 words each; its word d (0 .. 2*G - 1) sits at byte
+ *   (d/W)*64*U + l*U + (d%W)*4, so every U-byte load of a 64-lane wavefront
+ *   is one contiguous 64*U-byte segment.  Word d carries four groups
+ *   gi = 4d + f (f = 0..3); group gi is row r = gi / G, local group
+ *   g = gi % G, i.e. weights k = 4*kg(l, g) + b (b = 0..3), whose codes sit
  *   at bits 8*b + 2*f of the word.
  *
  * Activation quantisation (per row of n values, one row per token):
@@ -140,14 +147,16 @@ int ouro_act_quant_i8(const void *x, int x_dtype, size_t rows, size_t n,
 /* y[c*out_len + r] for ncols activation columns (xq row-major [ncols][in]),
  * column-major output like matmul_q (ops.rs:160-161).  acc_or_null, when
  * given, receives the exact int32 accumulators in the same layout.
- * w_scale is read from the device (4 bytes), e.g. the payload tail. */
+ * w_scale is read from the device (4 bytes), e.g. the payload tail.
+ * w_tiled and xq need 16-byte alignment. */
 int ouro_gemm_i2(const uint8_t *w_tiled, size_t out_len, size_t in_len,
                  const float *w_scale, const int8_t *xq, const float *dscale,
                  size_t ncols, float *y, int32_t *acc_or_null, void *stream);
 /* Grouped launch over `count` independent (weight, activation, output)
  * triples of one shape, laid out at fixed strides (bytes / elements):
  * matrix m uses w_tiled + m*w_stride, w_scale[m], xq + m*x_stride,
- * dscale[m], y + m*y_stride.  One column each.  This is the shape of the
+ * dscale[m], y + m*y_stride (w_stride and x_stride multiples of 16, both
+ * bases 16-byte aligned).  One column each.  This is the shape of the
  * projections that share a step but not a matrix (e.g. all layers' weight
  * streams of one decode step handed to the GPU at once). */
 int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride,

@@ -553,13 +553,10 @@ void orc_i2_unpack(const uint8_t *packed, size_t out_len, size_t in_len,
                 (int8_t)(((packed[r * rb + k / 4] >> (2 * (k % 4))) & 3) - 1);
 }
 
-static size_t gcd_sz(size_t a, size_t b) { return b ? gcd_sz(b, a % b) : a; }
-
 size_t orc_i2_tiled_bytes(size_t out_len, size_t in_len)
 {
     if (in_len == 0 || in_len % 256) return 0;
-    size_t G = in_len / 256, R = 16 / gcd_sz(G, 16);
-    return (out_len + R - 1) / R * R * (in_len / 4);
+    return (out_len + 7) / 8 * 8 * (in_len / 4);
 }
 
 size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
@@ -567,7 +564,9 @@ size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
 {
     size_t bytes = orc_i2_tiled_bytes(out_len, in_len);
     if (!bytes) return 0;
-    size_t G = in_len / 256, R = 16 / gcd_sz(G, 16), rb = in_len / 4;
+    const size_t R = 8, G = in_len / 256, rb = in_len / 4;
+    const size_t unit = G % 2 ? 8 : 16, wu = unit / 4;
+    const size_t n4 = G / 4 * 4, n2 = n4 + (G % 4 >= 2 ? 2 : 0);
     size_t tiles = (out_len + R - 1) / R, tile_bytes = R * rb;
     for (size_t t = 0; t < tiles; ++t)
         for (size_t lane = 0; lane < 64; ++lane)
@@ -576,11 +575,15 @@ size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
                 for (int f = 0; f < 4; ++f) {
                     size_t gi = 4 * d + (size_t)f, r = gi / G, g = gi % G;
                     size_t row = t * R + r;
-                    uint8_t byte = row < out_len ? canonical[row * rb + G * lane + g] : 0x55;
+                    /* chunk of local group g: start o, size sz */
+                    size_t o = g < n4 ? g / 4 * 4 : (g < n2 ? n4 : G - 1);
+                    size_t sz = g < n4 ? 4 : (g < n2 ? 2 : 1);
+                    size_t kg = 64 * o + sz * lane + (g - o);
+                    uint8_t byte = row < out_len ? canonical[row * rb + kg] : 0x55;
                     for (int b = 0; b < 4; ++b)
                         word |= (uint32_t)((byte >> (2 * b)) & 3u) << (8 * b + 2 * f);
                 }
-                size_t off = t * tile_bytes + (d / 4) * 1024 + lane * 16 + (d % 4) * 4;
+                size_t off = t * tile_bytes + (d / wu) * 64 * unit + lane * unit + (d % wu) * 4;
                 memcpy(tiled + off, &word, 4);
             }
     return bytes;

@@ -97,9 +97,12 @@ int orc_i2_pack(const int8_t *w, size_t out_len, size_t in_len, uint8_t *packed)
 /* Decode: w = code - 1 (code 3, never produced by the packer, decodes to 2). */
 void orc_i2_unpack(const uint8_t *packed, size_t out_len, size_t in_len,
                    int8_t *w);
-/* Device-tiled I2 layout (ouro_hip.h): G = in_len/256, R = 16/gcd(G,16),
- * tiles = ceil(out_len/R); padding rows hold code 1.  Returns the byte count
- * written (0 if in_len % 256 != 0).  `tiled` must hold that many bytes. */
+/* Device-tiled I2 layout (ouro_hip.h): G = in_len/256, 8-row tiles,
+ * tiles = ceil(out_len/8), lane-local group g of lane l is canonical byte
+ * column 64*o + s*l + (g - o) (chunks of 4, 2, 1 groups), a lane's share
+ * stored in 16-byte units (G even) or 8-byte units (G odd); padding rows
+ * hold code 1.  Returns the byte count written (0 if in_len % 256 != 0).
+ * `tiled` must hold that many bytes. */
 size_t orc_i2_tiled_bytes(size_t out_len, size_t in_len);
 size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
                    uint8_t *tiled);

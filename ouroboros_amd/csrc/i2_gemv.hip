@@ -11,6 +11,8 @@
 // separately rounded products, so results are bit-identical to the oracle.
 #include "common.hpp"
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace ouro {
@@ -20,21 +22,43 @@ constexpr int kWave = 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__host__ __device__ constexpr int gcd_i(int a, int b) { return b == 0 ? a : gcd_i(b, a % b); }
-__host__ __device__ constexpr int rows_per_tile(int G) { return 16 / gcd_i(G, 16); }
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Tiles are 8 rows.  A lane's share of a tile (8 * G bytes) is stored, and
+// read, in units of 16 bytes when G is even and of 8 bytes when G is odd.
+constexpr int kTileRows = 8;
+__host__ __device__ constexpr int unit_bytes(int G) { return G % 2 ? 8 : 16; }
+
+// The G groups a lane owns in each row are split into chunks of 4 groups,
+// then one of 2 (if G % 4 >= 2), then one of 1 (if G is odd).  Chunk c of
+// size s starting at lane-local group o covers, for lane l, the k-groups
+// 64*o + s*l + (g - o), so the activations of one chunk are a contiguous
+// 64*s*4-byte segment read by one coalesced load of s*4 bytes per lane.
+__host__ __device__ constexpr int chunk_start(int G, int g) {
+    return g < G / 4 * 4 ? g / 4 * 4 : (g < G / 4 * 4 + (G % 4 >= 2 ? 2 : 0) ? G / 4 * 4 : G - 1);
+}
+__host__ __device__ constexpr int chunk_size(int G, int g) {
+    return g < G / 4 * 4 ? 4 : (g < G / 4 * 4 + (G % 4 >= 2 ? 2 : 0) ? 2 : 1);
+}
+// k-group (canonical byte column) of lane-local group g of lane l.
+__host__ __device__ constexpr int kgroup(int G, int l, int g) {
+    return 64 * chunk_start(G, g) + chunk_size(G, g) * l + (g - chunk_start(G, g));
+}
 
 // ------------------------------------------------------------ tiling --
 
 // One thread per 32-bit word of the tiled layout.
 __global__ void i2_tile_kernel(const uint8_t *__restrict__ canon, uint32_t *__restrict__ tiled,
-                               int out_len, int G, int R, long long total_words) {
+                               int out_len, int G, long long total_words) {
     long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (id >= total_words) return;
+    constexpr int R = kTileRows;
+    const int wu = unit_bytes(G) / 4;           // words per unit
     const long long tile_words = 16LL * R * G;  // 64 lanes * R*G bytes / 4
     const long long t = id / tile_words;
     const int w = static_cast<int>(id % tile_words);
-    const int lane = (w % 256) / 4;
-    const int d = 4 * (w / 256) + (w % 4);
+    const int lane = (w % (64 * wu)) / wu;
+    const int d = wu * (w / (64 * wu)) + (w % wu);
     const long long row_bytes = 64LL * G;
     uint32_t word = 0;
 #pragma unroll
@@ -43,7 +67,7 @@ __global__ void i2_tile_kernel(const uint8_t *__restrict__ canon, uint32_t *__re
         const int r = gi / G, g = gi % G;
         const long long row = t * R + r;
         uint32_t byte = 0x55;  // padding rows: code 1 (w = 0) everywhere
-        if (row < out_len) byte = canon[row * row_bytes + static_cast<long long>(G) * lane + g];
+        if (row < out_len) byte = canon[row * row_bytes + kgroup(G, lane, g)];
 #pragma unroll
         for (int b = 0; b < 4; ++b) word |= ((byte >> (2 * b)) & 3u) << (8 * b + 2 * f);
     }
@@ -115,14 +139,98 @@ struct GemvArgs {
     int out_len, in_len, ncols, tiles;
 };
 
+// Row totals of a tile: each lane holds R partial sums (one per row of the
+// tile); row r's total is the sum over the span = 64 / R lanes of group r.
+// The first log2(R) lane stages halve the value count (lanes whose stage bit
+// is set keep the upper half), the rest add within the span.  Offsets 32 and
+// 16 use v_permlane32_swap / v_permlane16_swap (upper 32 lanes of the first
+// operand <-> lower 32 of the second; odd 16-lane rows of the first <-> even
+// rows of the second), offset 8 a DPP row rotation by 8 (lane L ^ 8), the
+// fourth halving (R = 16) a DPP half-row mirror and the in-span tail a DPP
+// shift-right scan, so no stage goes through LDS.  On
+// return lane L with L % span == span - 1 holds the total of row L / span.
+template <int R>
+__device__ __forceinline__ int row_totals(int (&v)[R], int lane) {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "R is a power of two <= 16");
+    constexpr int span = kWave / R;
+    // offset 32
+    if constexpr (R > 1) {
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i) {
+            const auto p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v[i]),
+                                                            static_cast<unsigned>(v[i + R / 2]), false, false);
+            v[i] = static_cast<int>(p[0] + p[1]);
+        }
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v[0]), static_cast<unsigned>(v[0]),
+                                                        false, false);
+        v[0] = static_cast<int>(p[0] + p[1]);
+    }
+    // offset 16
+    if constexpr (R > 2) {
+#pragma unroll
+        for (int i = 0; i < R / 4; ++i) {
+            const auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v[i]),
+                                                            static_cast<unsigned>(v[i + R / 4]), false, false);
+            v[i] = static_cast<int>(p[0] + p[1]);
+        }
+    } else {
+        const auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v[0]), static_cast<unsigned>(v[0]),
+                                                        false, false);
+        v[0] = static_cast<int>(p[0] + p[1]);
+    }
+    // offset 8 (row_ror:8 = dpp_ctrl 0x128)
+    if constexpr (R > 4) {
+        const bool upper = (lane & 8) != 0;
+#pragma unroll
+        for (int i = 0; i < R / 8; ++i) {
+            const int keep = upper ? v[i + R / 8] : v[i];
+            const int send = upper ? v[i] : v[i + R / 8];
+            v[i] = keep + __builtin_amdgcn_update_dpp(0, send, 0x128, 0xf, 0xf, false);
+        }
+    }
+    // Last halving stage of R = 16: row_half_mirror (0x141) pairs lane L
+    // with L ^ 7, whose bit 2 is the opposite one; the partial sums then
+    // cover {l, l ^ 7}, and the tail below over each aligned group of four
+    // lanes adds up all eight lanes of the half-row.
+    if constexpr (R > 8) {
+        const bool upper = (lane & 4) != 0;
+        const int keep = upper ? v[1] : v[0];
+        const int send = upper ? v[0] : v[1];
+        v[0] = keep + __builtin_amdgcn_update_dpp(0, send, 0x141, 0xf, 0xf, false);
+    }
+    // In-span tail: after shift-right steps 1, 2, .., lane L holds the sum
+    // of lanes L - s + 1 .. L of its 16-lane row (row_shr:k = 0x110 + k).
+    constexpr int tail = span < 16 ? span : 16;
+    if constexpr (tail > 1) v[0] += __builtin_amdgcn_update_dpp(0, v[0], 0x111, 0xf, 0xf, false);
+    if constexpr (tail > 2) v[0] += __builtin_amdgcn_update_dpp(0, v[0], 0x112, 0xf, 0xf, false);
+    if constexpr (tail > 4) v[0] += __builtin_amdgcn_update_dpp(0, v[0], 0x114, 0xf, 0xf, false);
+    if constexpr (tail > 8) v[0] += __builtin_amdgcn_update_dpp(0, v[0], 0x118, 0xf, 0xf, false);
+    return v[0];
+}
+
 // G: 4-weight groups per lane per row; R rows per tile; NC activation
-// columns per pass; TPW tiles per wavefront; WPB wavefronts per block.
-template <int G, int NC, int TPW, int WPB>
+// columns per pass; TPW tiles per wavefront, taken in order with DEPTH of
+// them in flight (the load of tile t + DEPTH is issued as soon as tile t
+// has been consumed); WPB wavefronts per block.  SPLIT selects how the four
+// 2-bit fields of a code byte reach v_dot4_i32_i8:
+//   SPLIT = 1: each field shifted down and masked (7 operations per word),
+//              one accumulator per row;
+//   SPLIT = 2: fields 0 and 2 at scale 1 (w & 0x03.., (w >> 4) & 0x03..),
+//              fields 1 and 3 at scale 4 (w & 0x0c.., (w >> 4) & 0x0c..),
+//              5 operations per word and two accumulators per row,
+//              recombined exactly as s1 + (s4 >> 2) (s4 is a multiple of 4).
+template <int G, int NC, int TPW, int DEPTH, int WPB, int SPLIT>
 __global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
-    constexpr int R = rows_per_tile(G);
+    constexpr int R = kTileRows;
+    constexpr int U = unit_bytes(G);  // bytes per load
+    constexpr int WU = U / 4;         // words per load
     constexpr int CHUNK = R * G;      // bytes per lane per tile
-    constexpr int NV = CHUNK / 16;    // 16-byte loads per lane per tile
-    static_assert(CHUNK % 16 == 0, "tile chunk must be whole 16-byte loads");
+    constexpr int NV = CHUNK / U;     // loads per lane per tile
+    using unit_t = typename std::conditional<U == 16, u32x4, u32x2>::type;
+    static_assert(CHUNK % U == 0, "tile chunk must be whole loads");
+    static_assert(DEPTH >= 1 && DEPTH <= TPW, "1 <= DEPTH <= TPW");
+    static_assert(SPLIT == 1 || SPLIT == 2, "SPLIT is 1 or 2");
 
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
@@ -137,66 +245,100 @@ __global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
     float *y = a.y + mat * a.y_stride;
     const float wscale = a.w_scale[mat];
 
-    // Activation slice of this lane: k in [4*G*lane, 4*G*(lane+1)).
+    // Tiles past the end are loaded from tile0 (in bounds) and never used.
+    unit_t buf[DEPTH][NV];
+    auto load_tile = [&](int t, unit_t(&dst)[NV]) {
+        const int tile = tile0 + t;
+        const unit_t *tp = reinterpret_cast<const unit_t *>(
+            w + static_cast<long long>(tile < a.tiles ? tile : tile0) * (R * 64 * G));
+#pragma unroll
+        for (int j = 0; j < NV; ++j) dst[j] = tp[j * kWave + lane];
+    };
+#pragma unroll
+    for (int t = 0; t < DEPTH; ++t) load_tile(t, buf[t]);
+
+    // Activation groups of this lane (kgroup order): one 16-, 8- or 4-byte
+    // load per chunk.
     uint32_t xw[NC][G];
     int sx[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         sx[c] = 0;
         const bool live = c0 + c < a.ncols;
-        const uint32_t *xp = reinterpret_cast<const uint32_t *>(
-            xq + static_cast<long long>(c0 + c) * a.in_len + 4 * G * lane);
+        const uint32_t *xr = reinterpret_cast<const uint32_t *>(xq + static_cast<long long>(c0 + c) * a.in_len);
+        constexpr int N4 = G / 4 * 4;  // groups in chunks of 4
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            xw[c][g] = live ? xp[g] : 0u;
-            sx[c] = __builtin_amdgcn_sdot4(static_cast<int>(xw[c][g]), 0x01010101, sx[c], false);
+        for (int g = 0; g < N4; g += 4) {
+            const u32x4 v = live ? *reinterpret_cast<const u32x4 *>(xr + kgroup(G, lane, g)) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xw[c][g + i] = v[i];
         }
-    }
-
-    // Issue every load of this wavefront's tiles before any arithmetic.
-    u32x4 buf[TPW][NV];
+        if constexpr (G % 4 >= 2) {
+            const u32x2 v = live ? *reinterpret_cast<const u32x2 *>(xr + kgroup(G, lane, N4)) : u32x2{0u, 0u};
+            xw[c][N4] = v[0];
+            xw[c][N4 + 1] = v[1];
+        }
+        if constexpr (G % 2) xw[c][G - 1] = live ? xr[kgroup(G, lane, G - 1)] : 0u;
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        const int tile = tile0 + t;
-        const u32x4 *tp = reinterpret_cast<const u32x4 *>(
-            w + static_cast<long long>(tile < a.tiles ? tile : tile0) * (R * 64 * G));
-#pragma unroll
-        for (int j = 0; j < NV; ++j) buf[t][j] = tp[j * kWave + lane];
+        for (int g = 0; g < G; ++g)
+            sx[c] = __builtin_amdgcn_sdot4(static_cast<int>(xw[c][g]), 0x01010101, sx[c], false);
     }
 
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
         const int tile = tile0 + t;
         if (tile >= a.tiles) break;  // uniform across the wavefront
-        int acc[NC][R];
+        unit_t(&cur)[NV] = buf[t % DEPTH];
+        int s1[NC][R], s4[NC][R];
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[c][r] = -sx[c];  // codes are w + 1
+            for (int r = 0; r < R; ++r) {
+                s1[c][r] = -sx[c];  // codes are w + 1
+                s4[c][r] = 0;
+            }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const uint32_t words[4] = {buf[t][j].x, buf[t][j].y, buf[t][j].z, buf[t][j].w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int d = 4 * j + q;
+            for (int q = 0; q < WU; ++q) {
+                const int d = WU * j + q;
+                const uint32_t word = cur[j][q];
+                const uint32_t hi = word >> 4;
+                int fields[4];
+                if constexpr (SPLIT == 2) {
+                    fields[0] = static_cast<int>(word & 0x03030303u);
+                    fields[1] = static_cast<int>(word & 0x0c0c0c0cu);
+                    fields[2] = static_cast<int>(hi & 0x03030303u);
+                    fields[3] = static_cast<int>(hi & 0x0c0c0c0cu);
+                } else {
+#pragma unroll
+                    for (int f = 0; f < 4; ++f) fields[f] = static_cast<int>((word >> (2 * f)) & 0x03030303u);
+                }
 #pragma unroll
                 for (int f = 0; f < 4; ++f) {
                     const int gi = 4 * d + f;
                     const int r = gi / G, g = gi % G;
-                    const int codes = static_cast<int>((words[q] >> (2 * f)) & 0x03030303u);
 #pragma unroll
-                    for (int c = 0; c < NC; ++c)
-                        acc[c][r] = __builtin_amdgcn_sdot4(codes, static_cast<int>(xw[c][g]),
-                                                           acc[c][r], false);
+                    for (int c = 0; c < NC; ++c) {
+                        const int xv = static_cast<int>(xw[c][g]);
+                        if (SPLIT == 2 && (f & 1))
+                            s4[c][r] = __builtin_amdgcn_sdot4(fields[f], xv, s4[c][r], false);
+                        else
+                            s1[c][r] = __builtin_amdgcn_sdot4(fields[f], xv, s1[c][r], false);
+                    }
                 }
             }
         }
+        if (t + DEPTH < TPW) load_tile(t + DEPTH, cur);  // the slot is free again
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int total = reduce_scatter<R, kWave>(acc[c], lane);
+            int acc[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = SPLIT == 2 ? s1[c][r] + (s4[c][r] >> 2) : s1[c][r];
+            const int total = row_totals<R>(acc, lane);
             constexpr int span = kWave / R;
             const int row = tile * R + lane / span;
-            if (lane % span == 0 && row < a.out_len && c0 + c < a.ncols) {
+            if (lane % span == span - 1 && row < a.out_len && c0 + c < a.ncols) {
                 const long long o = static_cast<long long>(c0 + c) * a.out_len + row;
                 const float v = (static_cast<float>(total) * dscale[c0 + c]) * wscale;
                 y[o] = v;
@@ -213,45 +355,53 @@ struct GemvPick {
     int nc, tpw, wpb;
 };
 
-// Tiles per wavefront are capped so that the in-flight tile buffers stay
-// within about 32 VGPRs (NV 16-byte loads per tile).
+constexpr int kGemvWpb = 4;
+// Enough wavefronts to keep every CU's load pipes busy (256 CUs x 8).
+constexpr long long kGemvWaves = 2048;
+
+// One activation column.  Measured on streams of 6912x2560, 2560x6912,
+// 4096x4096, 8192x8192 and 248320x5120 matrices: one 8-row tile per
+// wavefront in 4-wavefront blocks is the fastest shape, or within 2 % of
+// it, for every in_len >= 2048, and clearly the fastest once the stream is
+// larger than the last-level cache.  For in_len <= 1024 a tile is at most
+// 8 KiB per wavefront and two tiles (both in flight) pay for the fixed
+// per-tile cost, when that still leaves kGemvWaves wavefronts.
+// Several columns: NC = 4 or 2 with the single-accumulator unpack, NC = 4
+// only while 4 * G words of activations fit in 40 registers, NC = 2 while
+// 2 * G fit in 64.
 template <int G>
-GemvPick pick_g(int ncols, int want_tpw) {
-    constexpr int NV = rows_per_tile(G) * G / 16;
-    if (ncols >= 4) return {i2_gemv_kernel<G, 4, 1, 4>, 4, 1, 4};
-    if (ncols >= 2) return {i2_gemv_kernel<G, 2, 1, 4>, 2, 1, 4};
-    // Measured on the 64 x 6912x2560 stream: 2 tiles per wavefront in
-    // 8-wavefront blocks for large grouped launches, 1 tile per wavefront
-    // when a single matrix has to spread over the whole chip.
-    if (want_tpw >= 2 && 2 * NV <= 32) return {i2_gemv_kernel<G, 1, 2, 8>, 1, 2, 8};
-    return {i2_gemv_kernel<G, 1, 1, 4>, 1, 1, 4};
+GemvPick pick_g(int ncols, long long total_tiles) {
+    if constexpr (4 * G <= 40)
+        if (ncols >= 4) return {i2_gemv_kernel<G, 4, 1, 1, kGemvWpb, 1>, 4, 1, kGemvWpb};
+    if constexpr (2 * G <= 64)
+        if (ncols >= 2) return {i2_gemv_kernel<G, 2, 1, 1, kGemvWpb, 1>, 2, 1, kGemvWpb};
+    if constexpr (G <= 4)
+        if (total_tiles >= 2 * kGemvWaves) return {i2_gemv_kernel<G, 1, 2, 2, kGemvWpb, 2>, 1, 2, kGemvWpb};
+    return {i2_gemv_kernel<G, 1, 1, 1, kGemvWpb, 2>, 1, 1, kGemvWpb};
 }
 
-GemvPick pick_gemv(int G, int ncols, int tpw) {
+GemvPick pick_gemv(int G, int ncols, long long total_tiles) {
     switch (G) {
-    case 1: return pick_g<1>(ncols, tpw);
-    case 2: return pick_g<2>(ncols, tpw);
-    case 4: return pick_g<4>(ncols, tpw);
-    case 8: return pick_g<8>(ncols, tpw);
-    case 10: return pick_g<10>(ncols, tpw);
-    case 12: return pick_g<12>(ncols, tpw);
-    case 16: return pick_g<16>(ncols, tpw);
-    case 20: return pick_g<20>(ncols, tpw);
-    case 24: return pick_g<24>(ncols, tpw);
-    case 27: return pick_g<27>(ncols, tpw);
-    case 32: return pick_g<32>(ncols, tpw);
-    default: return {nullptr, 0, 0};
+    case 1: return pick_g<1>(ncols, total_tiles);
+    case 2: return pick_g<2>(ncols, total_tiles);
+    case 4: return pick_g<4>(ncols, total_tiles);
+    case 8: return pick_g<8>(ncols, total_tiles);
+    case 10: return pick_g<10>(ncols, total_tiles);
+    case 12: return pick_g<12>(ncols, total_tiles);
+    case 16: return pick_g<16>(ncols, total_tiles);
+    case 20: return pick_g<20>(ncols, total_tiles);
+    case 24: return pick_g<24>(ncols, total_tiles);
+    case 27: return pick_g<27>(ncols, total_tiles);
+    case 32: return pick_g<32>(ncols, total_tiles);
+    default: return {nullptr, 0, 0, 0};
     }
 }
 
 int launch_gemv(const GemvArgs &base, int count, void *stream) {
     const int G = base.in_len / 256;
     const int tiles = base.tiles;
-    // Tiles per wavefront: enough in flight for a large grouped launch,
-    // one per wavefront when a single matrix has to fill the chip alone.
     const long long total_tiles = static_cast<long long>(tiles) * count;
-    const int want = total_tiles >= 8192 ? 2 : 1;
-    const GemvPick p = pick_gemv(G, base.ncols, want);
+    const GemvPick p = pick_gemv(G, base.ncols, total_tiles);
     if (!p.fn) return fail(OURO_ERR_SHAPE, "i2 gemv: in_len %d (G=%d) has no kernel instance", base.in_len, G);
     const int nc = p.nc;
     const int per_block = p.wpb * p.tpw;
@@ -278,10 +428,9 @@ int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *
     if (st) return st;
     if (!w_tiled || !w_scale || !xq || !dscale || !y || !ncols)
         return fail(OURO_ERR_INVALID_ARG, "ouro_gemm_i2: NULL argument or ncols == 0");
-    if (reinterpret_cast<uintptr_t>(w_tiled) % 16 || reinterpret_cast<uintptr_t>(xq) % 4)
-        return fail(OURO_ERR_ALIGN, "ouro_gemm_i2: weights need 16-byte, xq 4-byte alignment");
-    const int G = static_cast<int>(in_len / 256);
-    const int R = rows_per_tile(G);
+    if (reinterpret_cast<uintptr_t>(w_tiled) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
+        return fail(OURO_ERR_ALIGN, "ouro_gemm_i2: weights and xq need 16-byte alignment");
+    constexpr int R = kTileRows;
     GemvArgs a{};
     a.w = w_tiled;
     a.w_stride = 0;
@@ -318,8 +467,7 @@ int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, flo
 
 size_t i2_tiled_bytes(size_t out_len, size_t in_len) {
     if (!in_len || in_len % 256) return 0;
-    const size_t G = in_len / 256;
-    const size_t R = static_cast<size_t>(rows_per_tile(static_cast<int>(G)));
+    const size_t R = kTileRows;
     const size_t tiles = (out_len + R - 1) / R;
     return tiles * R * (in_len / 4);
 }
@@ -331,12 +479,11 @@ int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *ti
     if (!canonical || !tiled) return fail(OURO_ERR_INVALID_ARG, "ouro_i2_tile: NULL argument");
     if (reinterpret_cast<uintptr_t>(tiled) % 16) return fail(OURO_ERR_ALIGN, "ouro_i2_tile: tiled needs 16-byte alignment");
     const int G = static_cast<int>(in_len / 256);
-    const int R = rows_per_tile(G);
     const size_t bytes = i2_tiled_bytes(out_len, in_len);
     const long long words = static_cast<long long>(bytes / 4);
     const unsigned blocks = static_cast<unsigned>((words + 255) / 256);
     hipLaunchKernelGGL(i2_tile_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), canonical,
-                       reinterpret_cast<uint32_t *>(tiled), static_cast<int>(out_len), G, R, words);
+                       reinterpret_cast<uint32_t *>(tiled), static_cast<int>(out_len), G, words);
     st = check_launch("i2_tile_kernel");
     if (st) return st;
     if (w_scale) {
@@ -385,12 +532,11 @@ int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride, const float *w
         return fail(OURO_ERR_INVALID_ARG, "ouro_gemv_i2_grouped: NULL argument or count == 0");
     if (count > 65535) return fail(OURO_ERR_SHAPE, "ouro_gemv_i2_grouped: count > 65535");
     if (w_stride < i2_tiled_bytes(out_len, in_len) || w_stride % 16 || x_stride < in_len ||
-        x_stride % 4 || y_stride < out_len)
+        x_stride % 16 || y_stride < out_len)
         return fail(OURO_ERR_SHAPE, "ouro_gemv_i2_grouped: strides overlap or misaligned");
-    if (reinterpret_cast<uintptr_t>(w_tiled) % 16 || reinterpret_cast<uintptr_t>(xq) % 4)
-        return fail(OURO_ERR_ALIGN, "ouro_gemv_i2_grouped: weights need 16-byte, xq 4-byte alignment");
-    const int G = static_cast<int>(in_len / 256);
-    const int R = rows_per_tile(G);
+    if (reinterpret_cast<uintptr_t>(w_tiled) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
+        return fail(OURO_ERR_ALIGN, "ouro_gemv_i2_grouped: weights and xq need 16-byte alignment");
+    constexpr int R = kTileRows;
     GemvArgs a{};
     a.w = w_tiled;
     a.w_stride = static_cast<long long>(w_stride);

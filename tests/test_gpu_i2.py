@@ -86,11 +86,15 @@ def test_gemm_extremes(gpu, orc):
         assert (acc.download() == wv * 127 * in_len).all()
 
 
-def test_grouped_gemv_matches_single(gpu, orc):
+# (4096, 1024, 8) and (40001, 256, 1) reach 4096 tiles, where in_len <= 1024
+# takes two tiles per wavefront; 40001 rows end in a wavefront whose second
+# tile lies past the last one.
+@pytest.mark.parametrize("out_len,in_len,count", [(6912, 2560, 4), (2560, 6912, 3), (4096, 1024, 8),
+                                                  (40001, 256, 1), (1000, 512, 2)])
+def test_grouped_gemv_bit_exact(gpu, orc, out_len, in_len, count):
     from ouroboros_amd._lib import call
 
-    rng = np.random.default_rng(5)
-    out_len, in_len, count = 6912, 2560, 4
+    rng = np.random.default_rng(5 + out_len + count)
     tb = ops.i2_tiled_bytes(out_len, in_len)
     stride = tb + 256
     wbuf = DeviceBuffer((count * stride,), np.uint8)
@@ -144,3 +148,6 @@ def test_shape_errors_are_status_codes(gpu):
     with pytest.raises(OuroError) as e:
         call("ouro_gemm_i2", buf.ptr + 1, 8, 256, buf.ptr, buf.ptr, buf.ptr, 1, buf.ptr, None, None)
     assert e.value.code == 3  # misaligned weights
+    with pytest.raises(OuroError) as e:
+        call("ouro_gemm_i2", buf.ptr, 8, 256, buf.ptr, buf.ptr + 4, buf.ptr, 1, buf.ptr, None, None)
+    assert e.value.code == 3  # activations must be 16-byte aligned

@@ -97,18 +97,37 @@ def test_gemm_invariants(orc):
     assert np.array_equal(a1, -a2)
 
 
+def kgroup(G, lane, g):
+    """Canonical byte column of lane-local group g (chunks of 4, then 2, then 1 groups)."""
+    sizes = [4] * (G // 4) + ([2] if G % 4 >= 2 else []) + ([1] if G % 2 else [])
+    o = 0
+    for s in sizes:
+        if g < o + s:
+            return 64 * o + s * lane + (g - o)
+        o += s
+    raise ValueError(g)
+
+
+def test_kgroup_is_a_permutation():
+    for G in range(1, 33):
+        cols = sorted(kgroup(G, lane, g) for lane in range(64) for g in range(G))
+        assert cols == list(range(64 * G))
+
+
 def untile(tiled, out_len, in_len):
     """Inverse of the documented tiled layout (written from the layout text)."""
     G = in_len // 256
-    R = 16 // np.gcd(G, 16)
+    R = 8
+    U = 8 if G % 2 else 16
+    W = U // 4
     rb = in_len // 4
     tiles = -(-out_len // R)
     canon = np.zeros((tiles * R, rb), np.uint8)
     words = tiled.view(np.uint32)
     for t in range(tiles):
         for lane in range(64):
-            for d in range(R * G // 4):
-                off = t * R * rb + (d // 4) * 1024 + lane * 16 + (d % 4) * 4
+            for d in range(2 * G):
+                off = t * R * rb + (d // W) * 64 * U + lane * U + (d % W) * 4
                 word = int(words[off // 4])
                 for f in range(4):
                     gi = 4 * d + f
@@ -116,11 +135,11 @@ def untile(tiled, out_len, in_len):
                     byte = 0
                     for b in range(4):
                         byte |= ((word >> (8 * b + 2 * f)) & 3) << (2 * b)
-                    canon[t * R + r, G * lane + g] = byte
+                    canon[t * R + r, kgroup(G, lane, g)] = byte
     return canon
 
 
-@pytest.mark.parametrize("out_len,in_len", [(16, 256), (13, 512), (9, 2560), (20, 1024)])
+@pytest.mark.parametrize("out_len,in_len", [(16, 256), (13, 512), (9, 2560), (20, 1024), (11, 768)])
 def test_tile_roundtrip(orc, out_len, in_len):
     rng = np.random.default_rng(out_len)
     canon = orc.i2_pack(rand_w(rng, out_len, in_len))
