@@ -57,6 +57,10 @@ PF_FLOPS = PF_FLOP_CHUNK_HEAD * (PF_LEN // PF_C) * PF_SEQ * GDN_HV
 PF_BYTES = (2 * PF_T * GDN_HK * GDN_D * 2 + PF_T * GDN_HV * GDN_D * 2 + 2 * PF_T * GDN_HV * 4
             + PF_T * GDN_HV * GDN_D * 4 + 2 * PF_SEQ * GDN_HV * GDN_D * GDN_D * 4)
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# Ternary x int8 GEMM (K-column matmul) on the 6912x2560 layer.
+GM_OUT, GM_IN, GM_COLS_MAIN = 6912, 2560, 2048
+GM_COLS = (4, 8, 16, 64, 512, GM_COLS_MAIN)
+INT8_MFMA_PEAK_TOPS = 5000.0
 
 
 def log(msg: str) -> None:
@@ -257,6 +261,50 @@ def bench_tl1(stream, steps, warmup):
     return ms, ms_am, ms_raw
 
 
+def bench_gemm(stream, steps, warmup, orc):
+    """Ternary x int8 GEMM (the K-column matmul_q, ops.rs:156-230) on the
+    6912x2560 layer: the int8 MFMA GEMM (ouro_gemm_i2_mfma) for 4 .. 2048
+    columns, and the multi-column GEMV (ouro_gemm_i2) for few columns."""
+    from ouroboros_amd import ops
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(21)
+    codes = rng.integers(0, 3, size=(GM_OUT, GM_IN), dtype=np.uint8)
+    canon = np.ascontiguousarray(codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
+    w_scale = 1.5
+    p_gemv = ops.i2_payload(canon, GM_OUT, GM_IN, w_scale)
+    p_mfma = ops.i2_mfma_payload(canon, GM_OUT, GM_IN, w_scale)
+    tb_g, tb_m = ops.i2_tiled_bytes(GM_OUT, GM_IN), ops.i2_mfma_bytes(GM_OUT, GM_IN)
+    nmax = max(GM_COLS)
+    x = DeviceBuffer.from_host(rng.standard_normal((nmax, GM_IN)).astype(np.float32))
+    xq = DeviceBuffer((nmax, GM_IN), np.int8)
+    ds = DeviceBuffer((nmax,), np.float32)
+    ops.act_quant_i8(x, nmax, GM_IN, xq, ds, stream)
+    y = DeviceBuffer((nmax * GM_OUT,), np.float32)
+    call("ouro_device_synchronize")
+    rows = []
+    for n in GM_COLS:
+        reps = max(5, min(steps, int(2e5 / (GM_OUT * n / 1e3 + 50))))
+        ms_m = time_events(stream, lambda _i: call("ouro_gemm_i2_mfma", p_mfma.ptr, GM_OUT, GM_IN, p_mfma.ptr + tb_m,
+                                                   xq.ptr, ds.ptr, n, y.ptr, None, stream), reps, 2)
+        row = {"cols": n, "mfma_us": round(ms_m * 1e3, 2),
+               "mfma_tops": round(2.0 * GM_OUT * GM_IN * n / (ms_m * 1e-3) / 1e12, 1)}
+        if n <= 16:
+            ms_v = time_events(stream, lambda _i: call("ouro_gemm_i2", p_gemv.ptr, GM_OUT, GM_IN, p_gemv.ptr + tb_g,
+                                                       xq.ptr, ds.ptr, n, y.ptr, None, stream), reps, 2)
+            row["gemv_us"] = round(ms_v * 1e3, 2)
+        rows.append(row)
+    # parity spot check of the MFMA path (not timed): 64 columns against the oracle
+    if orc is not None:
+        call("ouro_gemm_i2_mfma", p_mfma.ptr, GM_OUT, GM_IN, p_mfma.ptr + tb_m, xq.ptr, ds.ptr, 64, y.ptr, None, stream)
+        got = y.download()[:64 * GM_OUT]
+        _, want = orc.gemm_i2(canon, GM_OUT, GM_IN, xq.download()[:64], ds.download()[:64], w_scale)
+        if not np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)):
+            raise SystemExit("ternary GEMM parity failure")
+    return rows
+
+
 def bench_fwht(stream, steps, warmup):
     from ouroboros_amd import quant
     from ouroboros_amd._lib import DT_BF16, call
@@ -434,7 +482,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["gemv", "gdn", "layer", "tl1", "fwht", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "fwht", "prefill", "copy"], default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -463,6 +511,9 @@ def main() -> int:
     if args.only in (None, "tl1"):
         log("TL1 matvec 248320x5120 (lm_head probe)")
         res["tl1"] = bench_tl1(stream, args.steps, args.warmup)
+    if args.only in (None, "gemm"):
+        log("ternary GEMM 6912x2560, 4..2048 columns")
+        res["gemm"] = bench_gemm(stream, args.steps, args.warmup, orc)
     if args.only in (None, "fwht"):
         log("FWHT 512x4096 bf16")
         res["fwht"] = bench_fwht(stream, args.steps, args.warmup)
@@ -532,6 +583,17 @@ def main() -> int:
             "greedy_sample_ms": round(ms_am, 4),
             "greedy_sample_tokens_per_s": round(1e3 / ms_am, 1),
             "raw_payload_matvec_q_ms": round(ms_raw, 4),
+        }
+    if "gemm" in res:
+        rows = res["gemm"]
+        main = next(r for r in rows if r["cols"] == GM_COLS_MAIN)
+        sec["ternary_gemm"] = {
+            "value": main["mfma_tops"], "unit": "TOP/s", "us_per_call": main["mfma_us"],
+            "config": f"I2 6912x2560 x int8 [{GM_COLS_MAIN} columns] -> fp32, int8 MFMA (the K-column matmul_q)",
+            "roofline": {"bound": "mfma", "achieved": main["mfma_tops"], "peak": INT8_MFMA_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": round(main["mfma_tops"] / INT8_MFMA_PEAK_TOPS, 4),
+                         "traffic": None},
+            "by_columns": rows,
         }
     if "fwht" in res:
         ms, ms_all = res["fwht"]

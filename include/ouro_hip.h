@@ -165,6 +165,35 @@ int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride,
                          size_t y_stride, size_t out_len, size_t in_len,
                          size_t count, void *stream);
 
+/*
+ * Ternary x int8 GEMM on int8 MFMA for many activation columns: the
+ * K-column product of matmul_q / matmul_tl1 (ops.rs:156-230; col-major
+ * output as ops.rs:160-161), which decodes the weights once for all K
+ * columns; for batched verify and prefill projections.
+ *
+ * MFMA-tiled I2 (ouro_i2_tile_mfma() produces it): 1 KiB units, one per
+ * (row tile rt of 16 rows, k block kb of 256), unit at byte
+ * (rt * in_len/256 + kb) * 1024; tiles = ceil(out_len / 16), rows past
+ * out_len hold w = 0.  Lane l (0..63) of a unit has 16 bytes; its 32-bit
+ * word s (0..3) holds row 16*rt + l%16, weights
+ * k = 256*kb + 64*s + 16*(l/16) + 4*j + i (i, j = 0..3) at bits
+ * 8*i + 2*j, each as the 2-bit two's complement of v = 1 - code (= -w).
+ * Results are bit-identical to ouro_gemm_i2 for any ncols.
+ */
+size_t ouro_i2_mfma_bytes(size_t out_len, size_t in_len);
+/* canonical (device) -> MFMA-tiled (device); in_len % 256 == 0, dst 16-byte
+ * aligned.  When w_scale_or_null is given, the fp32 scale is written right
+ * after the codes. */
+int ouro_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
+                      uint8_t *dst, const float *w_scale_or_null, void *stream);
+/* y[c*out_len + r] = (acc * dscale[c]) * w_scale for ncols int8 columns
+ * (xq row-major [ncols][in_len], 16-byte aligned); acc_or_null receives
+ * the exact int32 sums.  Same semantics as ouro_gemm_i2. */
+int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len,
+                      const float *w_scale, const int8_t *xq,
+                      const float *dscale, size_t ncols, float *y,
+                      int32_t *acc_or_null, void *stream);
+
 /* ------------------------------------------------------------------ */
 /* Reference matvec surface                                             */
 /* ------------------------------------------------------------------ */
@@ -308,7 +337,9 @@ typedef struct ouro_weight *ouro_weight_t;
  * and w_scale is the per-tensor scale; the upload tiles them.  For the
  * other kinds host holds the reference payload (row_bytes*out_len bytes)
  * and w_scale is ignored.  max_cols sizes the handle's own activation
- * scratch (for matmul up to max_cols columns). */
+ * scratch (for matmul up to max_cols columns); an I2 handle with
+ * max_cols >= 8 also keeps the codes in the MFMA layout, and its matmuls
+ * of 8 or more columns run on the int8 MFMA GEMM (same results). */
 int ouro_weight_upload(int kind, const void *host, size_t bytes,
                        size_t out_len, size_t in_len, float w_scale,
                        size_t max_cols, ouro_weight_t *out);

@@ -70,6 +70,8 @@ def lib() -> C.CDLL:
             "orc_act_quant_i8": (None, [vp, sz, sz, vp, vp]),
             "orc_i2_tiled_bytes": (sz, [sz, sz]),
             "orc_i2_tile": (sz, [vp, sz, sz, vp]),
+            "orc_i2_mfma_bytes": (sz, [sz, sz]),
+            "orc_i2_tile_mfma": (sz, [vp, sz, sz, vp]),
             "orc_gemm_i2": (None, [vp, sz, sz, vp, vp, sz, f32, vp, vp, i32]),
             "orc_wht_inplace": (None, [vp, sz]),
             "orc_rotate_fwd": (i32, [vp, vp, sz, sz]),
@@ -201,6 +203,16 @@ def i2_tile(canonical: np.ndarray, out_len: int, in_len: int) -> np.ndarray:
         raise ValueError("i2_tile: in_len must be a multiple of 256")
     out = np.empty(n, np.uint8)
     lib().orc_i2_tile(_p(c), out_len, in_len, _p(out))
+    return out
+
+
+def i2_tile_mfma(canonical: np.ndarray, out_len: int, in_len: int) -> np.ndarray:
+    c = np.ascontiguousarray(canonical, dtype=np.uint8)
+    n = int(lib().orc_i2_mfma_bytes(out_len, in_len))
+    if n == 0:
+        raise ValueError("i2_tile_mfma: in_len must be a multiple of 256")
+    out = np.empty(n, np.uint8)
+    lib().orc_i2_tile_mfma(_p(c), out_len, in_len, _p(out))
     return out
 
 

@@ -589,6 +589,35 @@ size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
     return bytes;
 }
 
+size_t orc_i2_mfma_bytes(size_t out_len, size_t in_len)
+{
+    if (in_len == 0 || in_len % 256) return 0;
+    return (out_len + 15) / 16 * (in_len / 256) * 1024;
+}
+
+size_t orc_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
+                        uint8_t *dst)
+{
+    size_t bytes = orc_i2_mfma_bytes(out_len, in_len);
+    if (!bytes) return 0;
+    const size_t nkb = in_len / 256, rb = in_len / 4, tiles = (out_len + 15) / 16;
+    for (size_t rt = 0; rt < tiles; ++rt)
+        for (size_t kb = 0; kb < nkb; ++kb)
+            for (size_t l = 0; l < 64; ++l)
+                for (size_t s = 0; s < 4; ++s) {
+                    uint32_t word = 0;
+                    size_t row = rt * 16 + l % 16;
+                    for (size_t j = 0; j < 4; ++j)
+                        for (size_t i = 0; i < 4; ++i) {
+                            size_t k = 256 * kb + 64 * s + 16 * (l / 16) + 4 * j + i;
+                            uint32_t code = row < out_len ? (canonical[row * rb + k / 4] >> (2 * (k % 4))) & 3u : 1u;
+                            word |= ((1u - code) & 3u) << (8 * i + 2 * j);
+                        }
+                    memcpy(dst + ((rt * nkb + kb) * 64 + l) * 16 + 4 * s, &word, 4);
+                }
+    return bytes;
+}
+
 void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
                       float *dscale)
 {

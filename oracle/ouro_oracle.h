@@ -106,6 +106,13 @@ void orc_i2_unpack(const uint8_t *packed, size_t out_len, size_t in_len,
 size_t orc_i2_tiled_bytes(size_t out_len, size_t in_len);
 size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
                    uint8_t *tiled);
+/* MFMA-tiled I2 layout (ouro_hip.h): 1 KiB unit per (16-row tile, 256-k
+ * block); lane l's word s holds row 16*rt + l%16, k = 256*kb + 64*s +
+ * 16*(l/16) + 4j + i at bits 8i + 2j as the 2-bit two's complement of
+ * 1 - code.  Padding rows hold code 1 (w = 0).  Returns the byte count. */
+size_t orc_i2_mfma_bytes(size_t out_len, size_t in_len);
+size_t orc_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
+                        uint8_t *dst);
 /* Per-row absmax int8 quantization of `rows` rows of n floats:
  *   amax = max|x|; amax == 0 -> q = 0, dscale = 0;
  *   s = 127.0f / amax; q = clamp(rintf(x*s), -127, 127); dscale = amax/127.0f */

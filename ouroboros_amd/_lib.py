@@ -66,6 +66,9 @@ SIGNATURES = {
     "ouro_act_quant_i8": (i32, [vp, i32, sz, sz, vp, vp, vp]),
     "ouro_gemm_i2": (i32, [vp, sz, sz, vp, vp, vp, sz, vp, vp, vp]),
     "ouro_gemv_i2_grouped": (i32, [vp, sz, vp, vp, sz, vp, vp, sz, sz, sz, sz, vp]),
+    "ouro_i2_mfma_bytes": (sz, [sz, sz]),
+    "ouro_i2_tile_mfma": (i32, [vp, sz, sz, vp, vp, vp]),
+    "ouro_gemm_i2_mfma": (i32, [vp, sz, sz, vp, vp, vp, sz, vp, vp, vp]),
     "ouro_matvec_q": (i32, [vp, i32, sz, sz, vp, vp, vp]),
     "ouro_matmul_q": (i32, [vp, i32, sz, sz, vp, sz, vp, vp]),
     "ouro_fwht_rows": (i32, [vp, i32, vp, i32, sz, sz, sz, vp, u32, vp, vp, vp]),

@@ -80,7 +80,7 @@ CPP_TEST_BIN = PKG.parent / "tests" / "cpp" / "reference_kats"
 
 def build_cpp_tests(verbose: bool = False) -> Path:
     """Compile the C++ reference-KAT program against the C++ host mirror
-    (include/ouro/infer.hpp) and libouro_hip.so; it runs on a GPU box."""
+    (include/ouro/infer.hpp) and libouro_hip.so; it runs where a GPU is present."""
     cxx = shutil.which("g++") or "g++"
     cmd = [cxx, "-O2", "-std=c++17", "-Wall", f"-I{PKG.parent / 'include'}", str(CPP_TEST_SRC),
            "-o", str(CPP_TEST_BIN), f"-L{LIB.parent}", "-louro_hip",

@@ -1,0 +1,286 @@
+// i2_gemm.hip - ternary x int8 GEMM for many activation columns on int8 MFMA.
+//
+// matmul_q (ops.rs:156-230) amortises one decode of the weights over K input
+// columns; at K in the tens to thousands (batched verify, prefill
+// projections) the product is compute-bound, so it runs on
+// v_mfma_i32_16x16x64_i8 with the 2-bit weights expanded to int8 MFMA A
+// fragments in registers and the int8 activations staged through LDS as B
+// fragments.  Accumulation is exact int32 and the fp32 epilogue is the same
+// two separately rounded products as the GEMV, so every output is
+// bit-identical to the oracle for any K.
+//
+// MFMA layout of the codes (ouro_i2_tile_mfma): 1 KiB units, one per
+// (row tile of 16 rows, k block of 256); unit (rt, kb) at byte
+// (rt * in_len/256 + kb) * 1024.  Lane l's 16 bytes of a unit are its A
+// fragments for the block's four 64-deep MFMA steps: 32-bit word s holds
+// row 16*rt + l%16, k = 256*kb + 64*s + 16*(l/16) + 4*j + i at bits
+// 8*i + 2*j as the 2-bit two's complement of v = 1 - code = -w (so every
+// 2-bit code, including the never-produced 3, is representable).  One
+// shift and one mask, (word << (6 - 2j)) & 0xC0C0C0C0, turn field j of all
+// four bytes into the int8 values 64*v for k = 4j + i; the MFMA sum is
+// -64 * sum(w*x), and acc = -(D >> 6) exactly.
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ouro {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kGemmWaves = 4;
+constexpr int kXPitch = 272;  // LDS bytes per activation row of a 256-k block
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// One thread per 32-bit word of the MFMA layout.
+__global__ void i2_tile_mfma_kernel(const uint8_t *__restrict__ canon, uint32_t *__restrict__ dst,
+                                    int out_len, int in_len, long long total_words) {
+    const long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= total_words) return;
+    const int nkb = in_len / 256;
+    const long long unit = id / 256;
+    const int rem = static_cast<int>(id % 256);
+    const int l = rem / 4, s = rem % 4;
+    const long long rt = unit / nkb;
+    const int kb = static_cast<int>(unit % nkb);
+    const long long row = rt * 16 + (l % 16);
+    const int kbase = 256 * kb + 64 * s + 16 * (l / 16);
+    uint32_t word = 0;
+    if (row < out_len) {
+        const uint8_t *cr = canon + row * (in_len / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = kbase + 4 * j + i;
+                const uint32_t code = (cr[k / 4] >> (2 * (k % 4))) & 3u;
+                word |= ((1u - code) & 3u) << (8 * i + 2 * j);
+            }
+    }
+    dst[id] = word;
+}
+
+__global__ void copy_scale_mfma_kernel(const float *src, float *dst) { *dst = *src; }
+
+struct GemmArgs {
+    const uint4 *w;        // MFMA-layout units
+    const float *w_scale;  // device scalar
+    const int8_t *xq;      // [N][K] int8
+    const float *dscale;   // [N]
+    float *y;              // [N][M]
+    int32_t *acc;          // optional, same layout as y
+    int M, K, N, nkb, nrb;
+};
+
+// Block: 4 wavefronts stacked along rows; wavefront w owns row tiles
+// (4*rb + w)*WR .. +WR-1 and the block's WC column tiles of 16 columns.
+// Per 256-deep k block: the block copies its WC*16 activation rows into
+// one of two LDS buffers (prefetched a block ahead in registers), every
+// wavefront loads its WR 1 KiB weight units (also a block ahead), and runs
+// 4 steps x WR x WC MFMAs.
+template <int WR, int WC>
+__global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][WC * 16 * kXPitch];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rb = blockIdx.x % a.nrb, cb = blockIdx.x / a.nrb;
+    const int n0 = cb * WC * 16;
+    const int rt0 = (rb * kGemmWaves + wave) * WR;
+    const int nrt = (a.M + 15) / 16;
+
+    uint4 xr[WC];
+    auto load_x = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < WC; ++i) {
+            const int c = tid + kWave * kGemmWaves * i;
+            const int n = n0 + c / 16;
+            xr[i] = n < a.N ? *reinterpret_cast<const uint4 *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb +
+                                                               16 * (c % 16))
+                            : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < WC; ++i) {
+            const int c = tid + kWave * kGemmWaves * i;
+            *reinterpret_cast<uint4 *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
+        }
+    };
+    uint4 wr[WR];
+    auto load_w = [&](int kb) {
+#pragma unroll
+        for (int r = 0; r < WR; ++r) {
+            const int rt = rt0 + r;
+            wr[r] = rt < nrt ? a.w[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane]
+                             : make_uint4(0u, 0u, 0u, 0u);
+        }
+    };
+
+    v4i acc[WR][WC];
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+#pragma unroll
+        for (int c = 0; c < WC; ++c) acc[r][c] = v4i{0, 0, 0, 0};
+
+    load_x(0);
+    load_w(0);
+    store_x(0);
+    __syncthreads();
+    for (int kb = 0; kb < a.nkb; ++kb) {
+        uint4 wc[WR];
+#pragma unroll
+        for (int r = 0; r < WR; ++r) wc[r] = wr[r];
+        const bool more = kb + 1 < a.nkb;
+        if (more) {
+            load_x(kb + 1);
+            load_w(kb + 1);
+        }
+        const uint8_t *xb = xs[kb & 1] + (lane & 15) * kXPitch + 16 * (lane >> 4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v4i A[WR];
+#pragma unroll
+            for (int r = 0; r < WR; ++r) {
+                const uint32_t wd = s == 0 ? wc[r].x : s == 1 ? wc[r].y : s == 2 ? wc[r].z : wc[r].w;
+                A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
+                           static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+            }
+#pragma unroll
+            for (int c = 0; c < WC; ++c) {
+                const v4i B = *reinterpret_cast<const v4i *>(xb + c * 16 * kXPitch + 64 * s);
+#pragma unroll
+                for (int r = 0; r < WR; ++r)
+                    acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B, acc[r][c], 0, 0, 0);
+            }
+        }
+        if (more) store_x((kb + 1) & 1);
+        __syncthreads();
+    }
+
+    // D lane l: rows 4*(l/16) + e of the row tile, column l % 16.
+    const float wscale = *a.w_scale;
+#pragma unroll
+    for (int c = 0; c < WC; ++c) {
+        const int n = n0 + 16 * c + (lane & 15);
+        if (n >= a.N) continue;
+        const float ds = a.dscale[n];
+#pragma unroll
+        for (int r = 0; r < WR; ++r) {
+            const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (row + e >= a.M) break;
+                const int total = -(acc[r][c][e] >> 6);
+                const long long o = static_cast<long long>(n) * a.M + row + e;
+                a.y[o] = (static_cast<float>(total) * ds) * wscale;
+                if (a.acc) a.acc[o] = total;
+            }
+        }
+    }
+}
+
+using GemmFn = void (*)(GemmArgs);
+
+struct GemmPick {
+    GemmFn fn;
+    int wr, wc;
+};
+
+// Row tiles per wavefront WR and column tiles per block WC, from sweeps on
+// MI355X (6912x2560, 2560x6912 and 2560x2560 at 4 .. 8192 columns): the
+// largest wavefront tile (2x4: 32 rows x 64 columns, 8 MFMAs per pair of
+// fragment loads) while it still gives >= 1024 workgroups, then 2x2 while
+// >= 512, else 1x1 (16x16 per wavefront, the most workgroups, which is what
+// few columns need).
+GemmPick pick_gemm(int M, int N) {
+    const int nrt = (M + 15) / 16;
+    const auto blocks = [&](int wr, int wc) {
+        const long long nrb = (nrt + kGemmWaves * wr - 1) / (kGemmWaves * wr);
+        return nrb * ((N + 16 * wc - 1) / (16 * wc));
+    };
+    if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4>, 2, 4};
+    if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2>, 2, 2};
+    return {i2_gemm_mfma_kernel<1, 1>, 1, 1};
+}
+
+int check_mfma_shape(size_t out_len, size_t in_len) {
+    if (!out_len || !in_len) return fail(OURO_ERR_SHAPE, "i2 mfma: empty shape");
+    if (in_len % 256) return fail(OURO_ERR_SHAPE, "i2 mfma: in_len %zu is not a multiple of 256", in_len);
+    if (out_len > (1u << 30) || in_len > (1u << 18)) return fail(OURO_ERR_SHAPE, "i2 mfma: shape too large");
+    return OURO_OK;
+}
+
+}  // namespace
+
+size_t i2_mfma_bytes(size_t out_len, size_t in_len) {
+    if (!in_len || in_len % 256) return 0;
+    return (out_len + 15) / 16 * (in_len / 256) * 1024;
+}
+
+int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst,
+                 const float *w_scale, void *stream) {
+    int st = check_mfma_shape(out_len, in_len);
+    if (st) return st;
+    if (!canonical || !dst) return fail(OURO_ERR_INVALID_ARG, "ouro_i2_tile_mfma: NULL argument");
+    if (reinterpret_cast<uintptr_t>(dst) % 16) return fail(OURO_ERR_ALIGN, "ouro_i2_tile_mfma: dst needs 16-byte alignment");
+    const size_t bytes = i2_mfma_bytes(out_len, in_len);
+    const long long words = static_cast<long long>(bytes / 4);
+    hipLaunchKernelGGL(i2_tile_mfma_kernel, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), canonical, reinterpret_cast<uint32_t *>(dst), static_cast<int>(out_len),
+                       static_cast<int>(in_len), words);
+    st = check_launch("i2_tile_mfma_kernel");
+    if (st || !w_scale) return st;
+    hipLaunchKernelGGL(copy_scale_mfma_kernel, dim3(1), dim3(1), 0, as_stream(stream), w_scale,
+                       reinterpret_cast<float *>(dst + bytes));
+    return check_launch("copy_scale_mfma_kernel");
+}
+
+int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream) {
+    int st = check_mfma_shape(out_len, in_len);
+    if (st) return st;
+    if (!w_mfma || !w_scale || !xq || !dscale || !y || !ncols)
+        return fail(OURO_ERR_INVALID_ARG, "ouro_gemm_i2_mfma: NULL argument or ncols == 0");
+    if (ncols > (1u << 24)) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: ncols %zu too large", ncols);
+    if (reinterpret_cast<uintptr_t>(w_mfma) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
+        return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
+    GemmArgs a{};
+    a.w = reinterpret_cast<const uint4 *>(w_mfma);
+    a.w_scale = w_scale;
+    a.xq = xq;
+    a.dscale = dscale;
+    a.y = y;
+    a.acc = acc;
+    a.M = static_cast<int>(out_len);
+    a.K = static_cast<int>(in_len);
+    a.N = static_cast<int>(ncols);
+    a.nkb = a.K / 256;
+    const GemmPick p = pick_gemm(a.M, a.N);
+    const int nrt = (a.M + 15) / 16;
+    a.nrb = (nrt + kGemmWaves * p.wr - 1) / (kGemmWaves * p.wr);
+    const long long ncb = (a.N + 16LL * p.wc - 1) / (16LL * p.wc);
+    const long long grid = static_cast<long long>(a.nrb) * ncb;
+    if (grid > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: grid too large");
+    hipLaunchKernelGGL(p.fn, dim3(static_cast<unsigned>(grid)), dim3(kWave * kGemmWaves), 0, as_stream(stream), a);
+    return check_launch("i2_gemm_mfma_kernel");
+}
+
+}  // namespace ouro
+
+extern "C" {
+
+size_t ouro_i2_mfma_bytes(size_t out_len, size_t in_len) { return ouro::i2_mfma_bytes(out_len, in_len); }
+
+int ouro_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst,
+                      const float *w_scale_or_null, void *stream) {
+    OURO_REQUIRE_INIT();
+    return ouro::i2_tile_mfma(canonical, out_len, in_len, dst, w_scale_or_null, stream);
+}
+
+int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale,
+                      const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc_or_null,
+                      void *stream) {
+    OURO_REQUIRE_INIT();
+    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream);
+}
+
+}  // extern "C"

@@ -1,8 +1,9 @@
 // weights.hip - resident weight handles, the device analogue of the
 // reference's GpuPool (ouro-wgpu/src/lib.rs:251-356): a tensor is uploaded
 // once (and repacked on upload, as upload_q6k repacks 210 -> 212 B blocks),
-// then applied by handle.  I2 codes are tiled for the int8 GEMV; TL1 payloads
-// are repacked for the table-lookup GEMV.  Every handle owns the scratch its
+// then applied by handle.  I2 codes are tiled for the int8 GEMV (and, for
+// handles that expect many columns, also for the int8 MFMA GEMM); TL1
+// payloads are repacked for the table-lookup GEMV.  Every handle owns the scratch its
 // calls need (activation quantisation for up to max_cols columns, TL1
 // partial sums, a logits vector and the argmax key), so its calls allocate
 // nothing.
@@ -16,6 +17,12 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
             const float *w_scale, void *stream);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
+size_t i2_mfma_bytes(size_t out_len, size_t in_len);
+int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
+                 void *stream);
+int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream);
+int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale, void *stream);
 size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream);
@@ -28,6 +35,7 @@ struct ouro_weight {
     int kind = 0;
     size_t out_len = 0, in_len = 0, max_cols = 0;
     void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
+    void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes
     int8_t *xq = nullptr;     // I2: activation scratch
     float *dscale = nullptr;
     float *partial = nullptr; // TL1: per-group-block partial sums
@@ -39,6 +47,10 @@ struct ouro_weight {
 using namespace ouro;
 
 namespace {
+
+// Columns from which an I2 matmul runs on the int8 MFMA GEMM instead of the
+// multi-column GEMV (measured crossover on the 6912x2560 layer).
+constexpr size_t kMfmaCols = 8;
 
 size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:376-387)
     switch (kind) {
@@ -55,6 +67,7 @@ size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:
 void release(ouro_weight *w) {
     if (!w) return;
     if (w->payload) (void)hipFree(w->payload);
+    if (w->mfma) (void)hipFree(w->mfma);
     if (w->xq) (void)hipFree(w->xq);
     if (w->partial) (void)hipFree(w->partial);
     if (w->aux) (void)hipFree(w->aux);
@@ -98,6 +111,13 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             st = fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         if (!st) st = i2_tile(static_cast<const uint8_t *>(canon), out_len, in_len,
                               static_cast<uint8_t *>(w->payload), nullptr, nullptr);
+        if (!st && w->max_cols >= kMfmaCols) {  // second layout for many-column matmuls
+            if (hipMalloc(&w->mfma, i2_mfma_bytes(out_len, in_len)) != hipSuccess)
+                st = fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+            else
+                st = i2_tile_mfma(static_cast<const uint8_t *>(canon), out_len, in_len,
+                                  static_cast<uint8_t *>(w->mfma), nullptr, nullptr);
+        }
         if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
         (void)hipFree(canon);
         if (st) {
@@ -181,6 +201,14 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
             if (st) return st;
         }
         return OURO_OK;
+    }
+    if (w->kind == OURO_KIND_I2 && w->mfma && k >= kMfmaCols) {
+        int st = act_quant(x, OURO_DT_F32, k, w->in_len, w->xq, w->dscale, stream);
+        if (st) return st;
+        const float *w_scale =
+            reinterpret_cast<const float *>(static_cast<const uint8_t *>(w->payload) + i2_tiled_bytes(w->out_len, w->in_len));
+        return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->dscale,
+                            k, y, nullptr, stream);
     }
     return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->dscale, stream);
 }

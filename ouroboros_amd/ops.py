@@ -57,6 +57,32 @@ def i2_payload(canonical: np.ndarray | DeviceBuffer, out_len: int, in_len: int, 
     return out
 
 
+def i2_mfma_bytes(out_len: int, in_len: int) -> int:
+    return int(_lib.lib().ouro_i2_mfma_bytes(out_len, in_len))
+
+
+def i2_mfma_payload(canonical: np.ndarray | DeviceBuffer, out_len: int, in_len: int, w_scale: float,
+                    stream=None) -> DeviceBuffer:
+    """Device MFMA-tiled I2 codes + fp32 scale (for gemm_i2_mfma) from canonical bytes."""
+    cb, _ = _dev(canonical, np.uint8)
+    tb = i2_mfma_bytes(out_len, in_len)
+    if tb == 0:
+        raise ValueError(f"I2 needs in_len % 256 == 0 (got {in_len})")
+    out = DeviceBuffer((tb + 16,), np.uint8)
+    sc = DeviceBuffer.from_host(np.array([w_scale], dtype=np.float32))
+    call("ouro_i2_tile_mfma", cb.ptr, out_len, in_len, out.ptr, sc.ptr, stream)
+    return out
+
+
+def gemm_i2_mfma(w_payload: DeviceBuffer, out_len: int, in_len: int, xq: DeviceBuffer,
+                 dscale: DeviceBuffer, ncols: int, y: DeviceBuffer, acc: DeviceBuffer | None = None,
+                 stream=None) -> None:
+    """MFMA-tiled I2 x int8 columns -> fp32 (and optionally the exact int32 sums)."""
+    tb = i2_mfma_bytes(out_len, in_len)
+    call("ouro_gemm_i2_mfma", w_payload.ptr, out_len, in_len, w_payload.ptr + tb, xq.ptr, dscale.ptr,
+         ncols, y.ptr, acc.ptr if acc is not None else None, stream)
+
+
 def act_quant_i8(x: DeviceBuffer, rows: int, n: int, xq: DeviceBuffer, dscale: DeviceBuffer,
                  stream=None) -> None:
     dt = _lib.DT_BF16 if x.dtype == np.uint16 else _lib.DT_F32

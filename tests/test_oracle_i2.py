@@ -147,3 +147,40 @@ def test_tile_roundtrip(orc, out_len, in_len):
     back = untile(tiled, out_len, in_len)
     assert np.array_equal(back[:out_len], canon)
     assert (back[out_len:] == 0x55).all()  # padding rows are w = 0
+
+
+def untile_mfma(units, out_len, in_len):
+    """Weights w = -v recovered from the documented MFMA layout (written from the layout text)."""
+    nkb, tiles = in_len // 256, -(-out_len // 16)
+    words = units.view(np.uint32).reshape(tiles, nkb, 64, 4)
+    w = np.zeros((tiles * 16, in_len), np.int8)
+    for rt in range(tiles):
+        for kb in range(nkb):
+            for lane in range(64):
+                for s in range(4):
+                    word = int(words[rt, kb, lane, s])
+                    for j in range(4):
+                        for i in range(4):
+                            v = (word >> (8 * i + 2 * j)) & 3
+                            v = v - 4 if v >= 2 else v  # 2-bit two's complement
+                            w[rt * 16 + lane % 16, 256 * kb + 64 * s + 16 * (lane // 16) + 4 * j + i] = -v
+    return w
+
+
+@pytest.mark.parametrize("out_len,in_len", [(16, 256), (5, 512), (33, 768)])
+def test_tile_mfma_roundtrip(orc, out_len, in_len):
+    rng = np.random.default_rng(out_len + in_len)
+    w = rand_w(rng, out_len, in_len)
+    units = orc.i2_tile_mfma(orc.i2_pack(w), out_len, in_len)
+    back = untile_mfma(units, out_len, in_len)
+    assert np.array_equal(back[:out_len], w)
+    assert (back[out_len:] == 0).all()  # padding rows are w = 0
+
+
+def test_tile_mfma_keeps_code_3(orc):
+    # code 3 (never produced by the packer) decodes to w = 2 (orc_i2_unpack); the
+    # MFMA layout stores v = 1 - code = -2, which two bits still hold
+    canon = np.full((1, 64), 0x55, np.uint8)
+    canon[0, 0] = 0x57  # k = 0 has code 3
+    back = untile_mfma(orc.i2_tile_mfma(canon, 1, 256), 1, 256)
+    assert back[0, 0] == 2 and (back[0, 1:] == 0).all()
