@@ -295,6 +295,26 @@ def bench_gemm(stream, steps, warmup, orc):
                                                        xq.ptr, ds.ptr, n, y.ptr, None, stream), reps, 2)
             row["gemv_us"] = round(ms_v * 1e3, 2)
         rows.append(row)
+    # The vendor's dense int8 GEMM (hipBLASLt through torch._int_mm, 8-bit
+    # weights) on the same product, as a reference point for the MFMA rate.
+    vendor = None
+    try:
+        import torch
+        if torch.cuda.is_available():
+            a8 = torch.randint(-127, 128, (GM_COLS_MAIN, GM_IN), dtype=torch.int8, device="cuda")
+            b8 = torch.randint(-127, 128, (GM_IN, GM_OUT), dtype=torch.int8, device="cuda")
+            for _ in range(5):
+                torch._int_mm(a8, b8)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(20):
+                torch._int_mm(a8, b8)
+            e1.record()
+            torch.cuda.synchronize()
+            vendor = e0.elapsed_time(e1) / 20
+    except Exception as exc:  # the reference point is optional
+        log(f"vendor int8 GEMM reference skipped: {exc}")
     # parity spot check of the MFMA path (not timed): 64 columns against the oracle
     if orc is not None:
         call("ouro_gemm_i2_mfma", p_mfma.ptr, GM_OUT, GM_IN, p_mfma.ptr + tb_m, xq.ptr, ds.ptr, 64, y.ptr, None, stream)
@@ -302,7 +322,7 @@ def bench_gemm(stream, steps, warmup, orc):
         _, want = orc.gemm_i2(canon, GM_OUT, GM_IN, xq.download()[:64], ds.download()[:64], w_scale)
         if not np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)):
             raise SystemExit("ternary GEMM parity failure")
-    return rows
+    return rows, vendor
 
 
 def bench_fwht(stream, steps, warmup):
@@ -585,7 +605,7 @@ def main() -> int:
             "raw_payload_matvec_q_ms": round(ms_raw, 4),
         }
     if "gemm" in res:
-        rows = res["gemm"]
+        rows, vendor = res["gemm"]
         main = next(r for r in rows if r["cols"] == GM_COLS_MAIN)
         sec["ternary_gemm"] = {
             "value": main["mfma_tops"], "unit": "TOP/s", "us_per_call": main["mfma_us"],
@@ -594,6 +614,7 @@ def main() -> int:
                          "unit": "TOP/s", "frac": round(main["mfma_tops"] / INT8_MFMA_PEAK_TOPS, 4),
                          "traffic": None},
             "by_columns": rows,
+            "vendor_int8_gemm_8bit_weights_us": round(vendor * 1e3, 2) if vendor else None,
         }
     if "fwht" in res:
         ms, ms_all = res["fwht"]
