@@ -9,8 +9,8 @@
 // 0-31 walking one column of each pair and lanes 32-63 the other, four k
 // values per lane.  Each wavefront issues all of its state loads up front
 // (non-temporal: the state is touched once per step), reduces S^T k across
-// its 32-lane halves with a reduce-scatter, broadcasts dv, updates the
-// columns in registers, writes them back and reduces S'^T q.  The state
+// its 32-lane halves (permlane16 swaps and DPP, no LDS), broadcasts dv,
+// updates the columns in registers, writes them back and reduces S'^T q.  The state
 // makes exactly one HBM round trip.
 #include "common.hpp"
 
@@ -52,10 +52,28 @@ __device__ __forceinline__ float ld1<float>(const float *p) { return *p; }
 template <>
 __device__ __forceinline__ float ld1<uint16_t>(const uint16_t *p) { return bf16_bits_to_f32(*p); }
 
-__device__ __forceinline__ float sum_half(float v) {  // over the 32 lanes of a half
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) v += xor_shfl(v, off);
+// Cross-lane float sums without LDS.  dpp(v, ctrl) moves v across lanes
+// of a 16-lane row: 0x128 row_ror:8 (lane ^ 8), 0x141 row_half_mirror
+// (lane ^ 7 within 8), 0x4E quad_perm [2,3,0,1] (lane ^ 2), 0xB1 quad_perm
+// [1,0,3,2] (lane ^ 1); the four steps make every lane of a row hold the
+// row's sum (the lane sets {l, l^8}, {.., ^7}, {.., ^2}, {.., ^1} cover the
+// 16 lanes once).
+#define OURO_DPP(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false))
+__device__ __forceinline__ float sum_row16(float v) {
+    v += OURO_DPP(v, 0x128);
+    v += OURO_DPP(v, 0x141);
+    v += OURO_DPP(v, 0x4E);
+    v += OURO_DPP(v, 0xB1);
     return v;
+}
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even
+// rows of b; adding the two results sums rows 0+1 and 2+3.
+__device__ __forceinline__ float sum_rows_pair(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float sum_half(float v) {  // over the 32 lanes of a half, every lane
+    return sum_row16(sum_rows_pair(v, v));
 }
 
 __device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
@@ -65,6 +83,7 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
 // CPW state columns per wavefront, WPB wavefronts per block.
 template <typename TQK, typename TV, int CPW, int WPB>
 __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
+    static_assert(CPW == 4, "two column pairs per wavefront: one per 16-lane row of each half");
     constexpr int kPairs = CPW / 2;
     constexpr int kSpan = 32 / kPairs;  // lanes of a half that end up holding one pair
     const int lane = threadIdx.x & 63;
@@ -103,21 +122,29 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     }
     const float decay = expf(gate);
 
-    // sk for the 16 columns: reduce-scatter over each 32-lane half.
+    // sk for the column pairs: over each 32-lane half, row r of the half
+    // (16 lanes) ends up holding pair r.
     float part[kPairs];
 #pragma unroll
     for (int p = 0; p < kPairs; ++p) part[p] = dot4(s[p], k);
-    const float skj = reduce_scatter<kPairs, 32>(part, lane) * decay;
+    const float skj = sum_row16(sum_rows_pair(part[0], part[1])) * decay;
     // This lane now holds column pair (lane & 31) / kSpan of its half.
     const int myp = (lane & 31) / kSpan;
     const int myj = col0 + 2 * myp + half;
     const float vj = ld1(static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD + myj);
     const float dj = beta * (vj - skj);
+    // dv of pair p in half hh sits in every lane of row 2*hh + p (named
+    // scalars: an array indexed by the half would be placed in memory).
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dj), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dj), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dj), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dj), 48));
+    const float dv0 = half ? r2 : r0, dv1 = half ? r3 : r1;
 
     float o[kPairs];
 #pragma unroll
     for (int p = 0; p < kPairs; ++p) {
-        const float dp = __shfl(dj, (half << 5) + kSpan * p, 64);
+        const float dp = p == 0 ? dv0 : dv1;
         float4 t;
         t.x = s[p].x * decay + k.x * dp;
         t.y = s[p].y * decay + k.y * dp;
@@ -127,7 +154,7 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
         __builtin_nontemporal_store(tv, reinterpret_cast<f32x4 *>(S + (col0 + 2 * p + half) * kD + i0));
         o[p] = dot4(t, q);
     }
-    const float oj = reduce_scatter<kPairs, 32>(o, lane);
+    const float oj = sum_row16(sum_rows_pair(o[0], o[1]));
     if ((lane & (kSpan - 1)) == 0) a.out[static_cast<long long>(bh) * kD + myj] = oj;
 }
 
