@@ -39,8 +39,21 @@ class OuroError(RuntimeError):
 
 vp, sz, i32, u32, f32 = C.c_void_p, C.c_size_t, C.c_int, C.c_uint, C.c_float
 
+
+class StackCard(C.Structure):
+    """ouro_stack_card (include/ouro_stack.h)."""
+    _fields_ = [(n, C.c_int32) for n in ("n_layer", "n_embd", "n_ff", "n_vocab", "full_attention_interval",
+                                          "n_head", "n_head_kv", "head_dim", "n_rot", "ssm_n_k_heads",
+                                          "ssm_n_v_heads", "ssm_d_state")] + [("eps", C.c_float),
+                                                                              ("rope_base", C.c_float)]
+
 # name -> (restype, argtypes); every function of include/ouro_hip.h.
 SIGNATURES = {
+    "ouro_stack_create": (i32, [C.POINTER(StackCard), u32, sz, sz, sz, vp]),
+    "ouro_stack_free": (i32, [vp]),
+    "ouro_stack_device_bytes": (sz, [vp]),
+    "ouro_stack_prefill": (i32, [vp, vp, vp, sz, vp, vp, vp]),
+    "ouro_stack_decode": (i32, [vp, vp, vp, vp, vp]),
     "ouro_init": (i32, [i32]),
     "ouro_shutdown": (i32, []),
     "ouro_last_error": (C.c_char_p, []),

@@ -84,6 +84,18 @@ constexpr size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(25
 
 }  // namespace
 
+// gated_norm_rms per (row, v-head) of rows x Hv heads of d = 128 (the
+// prefill's token rows, or the decode's sequences).
+int gdn_gated_norm(const float *o, const float *z, const float *norm_w, float *out, size_t rows, size_t Hk,
+                   size_t Hv, unsigned flags, float eps, void *stream) {
+    const long long items = static_cast<long long>(rows * Hv);
+    if (!items) return OURO_OK;
+    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
+                       as_stream(stream), o, z, norm_w, out, static_cast<int>(rows), static_cast<int>(Hk),
+                       static_cast<int>(Hv), flags, eps);
+    return check_launch("gdn_gated_norm_kernel");
+}
+
 size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv) {
     const size_t ch = 2 * Hk * kD + Hv * kD;
     return align256(B * ch * 4) + 2 * align256(B * Hv * 4) + align256(B * Hv * kD * 4);

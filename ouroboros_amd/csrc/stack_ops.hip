@@ -1,0 +1,648 @@
+// stack_ops.hip - the device operations of a Qwen3.5-style hybrid decoder
+// stack that the hot-path kernels do not already cover: RMS norm with the
+// residual add, SwiGLU, the attention block's per-head norm + partial NEOX
+// rope + KV append, causal attention over a packed varlen batch (prefill)
+// and over each sequence's cache (decode), the delta-net block's causal
+// conv + gates over a packed varlen batch, embedding lookup, per-row
+// finite_argmax and the seeded synthetic weights.
+//
+// Reference semantics followed: run_layer (qwen35.rs:776-795), run_ffn
+// (798-805), run_attn (1160-1215) with attn_head (1227-1240), run_delta's
+// conv and gates (1066-1088), rmsnorm/silu/softmax (ops.rs:12-17, 34-48),
+// rope_partial_neox (qwen35.rs:96-106).
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ouro {
+namespace {
+
+constexpr int kHd = 128;  // attention head dim and delta-net d handled here
+
+// ------------------------------------------------------- synthetic weights --
+
+// 32-bit mix of (seed, tensor, index); the same arithmetic is restated in
+// the oracle so synthetic weights are reproducible on the host.
+__device__ __forceinline__ uint32_t mix3(uint32_t seed, uint32_t tensor, uint32_t idx) {
+    uint32_t x = seed ^ (tensor * 0x9E3779B9u) ^ (idx * 0x85EBCA6Bu);
+    x ^= x >> 16;
+    x *= 0x7FEB352Du;
+    x ^= x >> 15;
+    x *= 0x846CA68Bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// Canonical I2 bytes of a rows x cols ternary tensor: code(k) = mix3 % 3.
+__global__ void gen_codes_kernel(uint32_t seed, uint32_t tensor, long long rows, int cols, uint8_t *dst) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const long long bytes = rows * (cols / 4);
+    if (i >= bytes) return;
+    const long long row = i / (cols / 4);
+    const int j = static_cast<int>(i % (cols / 4));
+    uint32_t b = 0;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+        const uint32_t idx = static_cast<uint32_t>(row * cols + 4 * j + f);
+        b |= (mix3(seed, tensor, idx) % 3u) << (2 * f);
+    }
+    dst[i] = static_cast<uint8_t>(b);
+}
+
+// dst[i] = lo + span * u, u = (mix3 >> 8) * 2^-24 in [0, 1); signs (span
+// == 0): +1 or -1 from the low bit.
+__global__ void gen_floats_kernel(uint32_t seed, uint32_t tensor, long long n, float lo, float span, float *dst) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t h = mix3(seed, tensor, static_cast<uint32_t>(i));
+    if (span == 0.f) {
+        dst[i] = (h & 1u) ? 1.0f : -1.0f;
+        return;
+    }
+    const float u = static_cast<float>(h >> 8) * 5.9604644775390625e-8f;
+    dst[i] = lo + span * u;
+}
+
+// ----------------------------------------------------------------- norms --
+
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return t;
+}
+
+// One 256-thread block per row: s = a (+ b), optionally stored, then
+// out = s * inv * w with inv = 1 / sqrt(mean(s^2) + eps) (ops.rs:12-17).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *a, const float *b, const float *w, float *sum_out,
+                                                      float *out, int n, float eps) {
+    __shared__ float red[4];
+    const long long row = blockIdx.x;
+    const float *ar = a + row * n;
+    const float *br = b ? b + row * n : nullptr;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float s = br ? ar[i] + br[i] : ar[i];
+        ss += s * s;
+    }
+    const float ms = block_sum_256(ss, red) / static_cast<float>(n);
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float s = br ? ar[i] + br[i] : ar[i];
+        if (sum_out) sum_out[row * n + i] = s;
+        out[row * n + i] = s * inv * w[i];
+    }
+}
+
+// act = silu(gate) * up (run_ffn, qwen35.rs:802).
+__global__ void swiglu_kernel(const float *gate, const float *up, float *out, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float g = gate[i];
+    out[i] = g / (1.0f + expf(-g)) * up[i];
+}
+
+// Token rows -> embedding rows (ids clamped into the table).
+__global__ void embed_kernel(const int32_t *tokens, const float *table, float *x, int n_tok, int n_vocab, int n_embd) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<long long>(n_tok) * n_embd) return;
+    const int t = static_cast<int>(i / n_embd), c = static_cast<int>(i % n_embd);
+    int id = tokens[t];
+    id = id < 0 ? 0 : (id >= n_vocab ? n_vocab - 1 : id);
+    x[i] = table[static_cast<long long>(id) * n_embd + c];
+}
+
+// Rows src_rows[i] of src -> row i of dst (the last token of each sequence).
+__global__ void gather_rows_kernel(const float *src, const int32_t *src_rows, float *dst, int n, int width) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<long long>(n) * width) return;
+    const int r = static_cast<int>(i / width), c = static_cast<int>(i % width);
+    dst[i] = src[static_cast<long long>(src_rows[r]) * width + c];
+}
+
+// --------------------------------------------------------- attention prep --
+
+struct AttnPrepArgs {
+    const float *qfull;       // [T][nh][2*hd]: q | gate per head (qwen35.rs:1174)
+    const float *k, *v;       // [T][nkv][hd]
+    const float *qn, *kn;     // [hd] head-norm gains
+    const int32_t *pos;       // [T] position of the token in its sequence
+    const int32_t *seq;       // [T] sequence of the token
+    const long long *base;    // [N] first cache row of each sequence
+    float *q_out, *gate_out;  // [T][nh][hd]
+    float *kc, *vc;           // cache [rows][nkv][hd]
+    int T, nh, nkv, n_rot;
+    float rope_base, eps;
+};
+
+// One wavefront per (token, head of q or k); lane l holds dims 2l, 2l+1.
+__global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
+    const int lane = threadIdx.x & 63;
+    const long long item = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int heads = a.nh + a.nkv;
+    if (item >= static_cast<long long>(a.T) * heads) return;  // whole wavefront
+    const int t = static_cast<int>(item / heads), hh = static_cast<int>(item % heads);
+    const bool isq = hh < a.nh;
+    const int h = isq ? hh : hh - a.nh;
+    const float *src = isq ? a.qfull + (static_cast<long long>(t) * a.nh + h) * (2 * kHd)
+                           : a.k + (static_cast<long long>(t) * a.nkv + h) * kHd;
+    float2 x = *reinterpret_cast<const float2 *>(src + 2 * lane);
+    // rmsnorm_head (qwen35.rs:1246-1248)
+    float ss = x.x * x.x + x.y * x.y;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + a.eps);
+    const float2 g = *reinterpret_cast<const float2 *>((isq ? a.qn : a.kn) + 2 * lane);
+    x.x = x.x * inv * g.x;
+    x.y = x.y * inv * g.y;
+    // rope_partial_neox on the first n_rot dims: pair (i, i + n_rot/2)
+    const int half = a.n_rot / 2;
+    const int p = a.pos[t];
+    const int partner = lane < half / 2 ? lane + half / 2 : lane - half / 2;
+    const float px = __shfl(x.x, partner, 64), py = __shfl(x.y, partner, 64);
+    if (2 * lane < a.n_rot) {
+        float r[2] = {x.x, x.y};
+        const float pr[2] = {px, py};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int d = 2 * lane + e;
+            const int i = d < half ? d : d - half;
+            const float theta = 1.0f / powf(a.rope_base, static_cast<float>(2 * i) / static_cast<float>(a.n_rot));
+            const float ang = static_cast<float>(p) * theta;
+            const float c = cosf(ang), s = sinf(ang);
+            r[e] = d < half ? r[e] * c - pr[e] * s : r[e] * c + pr[e] * s;
+        }
+        x.x = r[0];
+        x.y = r[1];
+    }
+    if (isq) {
+        const long long o = (static_cast<long long>(t) * a.nh + h) * kHd + 2 * lane;
+        *reinterpret_cast<float2 *>(a.q_out + o) = x;
+        *reinterpret_cast<float2 *>(a.gate_out + o) = *reinterpret_cast<const float2 *>(src + kHd + 2 * lane);
+    } else {
+        const long long row = a.base[a.seq[t]] + p;
+        const long long o = (row * a.nkv + h) * kHd + 2 * lane;
+        *reinterpret_cast<float2 *>(a.kc + o) = x;
+        *reinterpret_cast<float2 *>(a.vc + o) =
+            *reinterpret_cast<const float2 *>(a.v + (static_cast<long long>(t) * a.nkv + h) * kHd + 2 * lane);
+    }
+}
+
+// ---------------------------------------------------- attention (prefill) --
+
+constexpr int kQT = 64;        // query rows per tile
+constexpr int kKT = 64;        // keys per tile
+constexpr int kQP = kHd + 4;   // LDS row pitch (floats) of Q, K, V tiles
+constexpr int kPP = kKT + 4;   // LDS row pitch of P
+constexpr int kAttnLds = (kQT * kQP + 2 * kKT * kQP + kQT * kPP) * 4;
+
+struct AttnArgs {
+    const float *q, *gate;    // [T][nh][hd]
+    const float *kc, *vc;     // cache [rows][nkv][hd]
+    const long long *base;    // [N] first cache row of each sequence
+    const int32_t *cu;        // [N+1] token offsets (prefill); NULL for decode
+    const int32_t *lens;      // [N] keys per sequence (decode)
+    const int32_t *tile_seq, *tile_p0;  // prefill query tiles
+    float *out;               // [T][nh][hd]
+    int nh, nkv;
+    float scale;
+};
+
+// Causal attention over a packed varlen batch, one workgroup per (query
+// tile of 64 tokens of one sequence, q head), online softmax over key
+// tiles of 64 up to the diagonal, fp32 throughout.  Thread (tr, tc) =
+// (tid / 16, tid % 16) owns rows 4tr..4tr+3 of the tile: scores of keys
+// 4tc..4tc+3 and outputs of dims 8tc..8tc+7.  The 16 threads of a row
+// group are one 16-lane row of a wavefront, reduced with DPP.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+    return v;
+}
+
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
+    extern __shared__ float lds[];
+    float *Qs = lds, *Ks = Qs + kQT * kQP, *Vs = Ks + kKT * kQP, *Ps = Vs + kKT * kQP;
+    const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+    const int s = a.tile_seq[blockIdx.x], p0 = a.tile_p0[blockIdx.x];
+    const int h = blockIdx.y;
+    const int kvh = h / (a.nh / a.nkv);
+    const int t0 = a.cu[s], L = a.cu[s + 1] - t0;
+    const long long kbase = a.base[s];
+
+    // Q tile (rows past the sequence's end are zero and never stored)
+    for (int i = tid; i < kQT * (kHd / 4); i += 256) {
+        const int r = i / (kHd / 4), c4 = i % (kHd / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p0 + r < L)
+            v = *reinterpret_cast<const float4 *>(a.q + ((static_cast<long long>(t0) + p0 + r) * a.nh + h) * kHd + 4 * c4);
+        *reinterpret_cast<float4 *>(Qs + r * kQP + 4 * c4) = v;
+    }
+    float m[4], l[4], o[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[r][d] = 0.f;
+    }
+    const int last = min(p0 + kQT, L) - 1;  // last query position in the tile
+    for (int k0 = 0; k0 <= last; k0 += kKT) {
+        __syncthreads();  // previous tile's K, V, P are consumed
+        for (int i = tid; i < kKT * (kHd / 4); i += 256) {
+            const int r = i / (kHd / 4), c4 = i % (kHd / 4);
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (k0 + r < L) {
+                const long long off = ((kbase + k0 + r) * a.nkv + kvh) * kHd + 4 * c4;
+                kv = *reinterpret_cast<const float4 *>(a.kc + off);
+                vv = *reinterpret_cast<const float4 *>(a.vc + off);
+            }
+            *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
+            *reinterpret_cast<float4 *>(Vs + r * kQP + 4 * c4) = vv;
+        }
+        __syncthreads();
+        float sc[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sc[r][c] = 0.f;
+        for (int d = 0; d < kHd; d += 4) {
+            float4 qv[4], kv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) qv[r] = *reinterpret_cast<const float4 *>(Qs + (4 * tr + r) * kQP + d);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kv[c] = *reinterpret_cast<const float4 *>(Ks + (4 * tc + c) * kQP + d);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    sc[r][c] += qv[r].x * kv[c].x + qv[r].y * kv[c].y + qv[r].z * kv[c].z + qv[r].w * kv[c].w;
+        }
+        float corr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int qp = p0 + 4 * tr + r;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int kp = k0 + 4 * tc + c;
+                sc[r][c] = (kp <= qp && kp < L) ? sc[r][c] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sc[r][c]);
+            }
+            mx = row16_max(mx);
+            const float mn = fmaxf(m[r], mx);
+            // rows with no visible key yet keep m = -inf; use 0 to avoid inf - inf
+            const float mref = mn == -INFINITY ? 0.f : mn;
+            corr[r] = expf(m[r] - mref);
+            float ps = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float pv = expf(sc[r][c] - mref);
+                Ps[(4 * tr + r) * kPP + 4 * tc + c] = pv;
+                ps += pv;
+            }
+            l[r] = l[r] * corr[r] + row16_sum(ps);
+            m[r] = mn;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int d = 0; d < 8; ++d) o[r][d] *= corr[r];
+        for (int j = 0; j < kKT; j += 4) {
+            float4 pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pr[r] = *reinterpret_cast<const float4 *>(Ps + (4 * tr + r) * kPP + j);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const float4 v0 = *reinterpret_cast<const float4 *>(Vs + (j + jj) * kQP + 8 * tc);
+                const float4 v1 = *reinterpret_cast<const float4 *>(Vs + (j + jj) * kQP + 8 * tc + 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float pw = jj == 0 ? pr[r].x : jj == 1 ? pr[r].y : jj == 2 ? pr[r].z : pr[r].w;
+                    o[r][0] += pw * v0.x;
+                    o[r][1] += pw * v0.y;
+                    o[r][2] += pw * v0.z;
+                    o[r][3] += pw * v0.w;
+                    o[r][4] += pw * v1.x;
+                    o[r][5] += pw * v1.y;
+                    o[r][6] += pw * v1.z;
+                    o[r][7] += pw * v1.w;
+                }
+            }
+        }
+    }
+    // o / l, times sigmoid(gate) (qwen35.rs:1208-1210)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int qp = p0 + 4 * tr + r;
+        if (qp >= L) continue;
+        const long long base = ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + 8 * tc;
+        const float il = 1.0f / l[r];
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const float g = a.gate[base + d];
+            a.out[base + d] = (o[r][d] * il) * (1.0f / (1.0f + expf(-g)));
+        }
+    }
+}
+
+// ----------------------------------------------------- attention (decode) --
+
+constexpr int kMaxCtx = 16384;  // keys per sequence the decode kernel holds
+
+// One 256-thread workgroup per (sequence, q head): scores of all keys into
+// LDS (a 16-lane group per key, 8 dims per lane), softmax, then each of 256
+// threads accumulates one (dim, key half) of p V.
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
+    extern __shared__ float sc[];
+    __shared__ float red[8];
+    __shared__ float half_o[kHd];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.x, h = blockIdx.y;
+    const int kvh = h / (a.nh / a.nkv);
+    const int L = a.lens[b];
+    const long long kbase = a.base[b];
+    const long long qo = (static_cast<long long>(b) * a.nh + h) * kHd;
+    const int g = lane >> 4, gl = lane & 15;  // key group of the wavefront, lane in group
+    const float4 q0 = *reinterpret_cast<const float4 *>(a.q + qo + 8 * gl);
+    const float4 q1 = *reinterpret_cast<const float4 *>(a.q + qo + 8 * gl + 4);
+    for (int j0 = 0; j0 < L; j0 += 16) {
+        const int j = j0 + 4 * wave + g;
+        float part = 0.f;
+        if (j < L) {
+            const long long off = ((kbase + j) * a.nkv + kvh) * kHd + 8 * gl;
+            const float4 k0 = *reinterpret_cast<const float4 *>(a.kc + off);
+            const float4 k1 = *reinterpret_cast<const float4 *>(a.kc + off + 4);
+            part = q0.x * k0.x + q0.y * k0.y + q0.z * k0.z + q0.w * k0.w + q1.x * k1.x + q1.y * k1.y +
+                   q1.z * k1.z + q1.w * k1.w;
+        }
+        part = row16_sum(part);
+        if (gl == 0 && j < L) sc[j] = part * a.scale;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = tid; j < L; j += 256) mx = fmaxf(mx, sc[j]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sum = 0.f;
+    for (int j = tid; j < L; j += 256) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    __syncthreads();  // red[] reuse and sc[] writes
+    if (lane == 0) red[4 + wave] = sum;
+    __syncthreads();
+    sum = red[4] + red[5] + red[6] + red[7];
+    const int d = tid & (kHd - 1), hf = tid >> 7;
+    float acc = 0.f;
+    for (int j = hf; j < L; j += 2) acc += sc[j] * a.vc[((kbase + j) * a.nkv + kvh) * kHd + d];
+    if (hf == 1) half_o[d] = acc;
+    __syncthreads();
+    if (hf == 0) {
+        const float g2 = a.gate[qo + d];
+        a.out[qo + d] = ((acc + half_o[d]) / sum) * (1.0f / (1.0f + expf(-g2)));
+    }
+}
+
+// ------------------------------------------------ delta-net prefill inputs --
+
+struct ConvArgs {
+    const float *qkv;          // [T][ch]
+    const float *ring;         // [N][ch][3] conv state before the batch
+    const float *conv_w;       // [ch][4]
+    const int32_t *seq, *pos;  // [T]
+    const float *beta_raw, *alpha_raw, *dt_bias, *a_log;  // [T][Hv], [Hv]
+    uint16_t *qb, *kb, *vb;    // bf16 [T][di], [T][di], [T][Hv*d]
+    float *beta, *gate;        // [T][Hv]
+    int T, ch, di, Hv;
+};
+
+__device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x); }
+
+// conv_step + SiLU per (token, channel) with the causal window inside the
+// token's sequence (inputs before the sequence come from its ring), then
+// beta and gate per (token, v-head) (qwen35.rs:1066-1088).
+__global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < static_cast<long long>(a.T) * a.ch) {
+        const int t = static_cast<int>(i / a.ch), c = static_cast<int>(i % a.ch);
+        const int p = a.pos[t];
+        const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
+        float xin[3];
+#pragma unroll
+        for (int o = 1; o <= 3; ++o)
+            xin[3 - o] = p - o >= 0 ? a.qkv[(static_cast<long long>(t) - o) * a.ch + c] : r[3 + p - o];
+        const float4 w = *reinterpret_cast<const float4 *>(a.conv_w + 4LL * c);
+        const float y = w.x * xin[0] + w.y * xin[1] + w.z * xin[2] + w.w * a.qkv[i];
+        const float sy = y / (1.0f + expf(-y));
+        if (c < a.di)
+            a.qb[static_cast<long long>(t) * a.di + c] = to_bf16(sy);
+        else if (c < 2 * a.di)
+            a.kb[static_cast<long long>(t) * a.di + c - a.di] = to_bf16(sy);
+        else
+            a.vb[static_cast<long long>(t) * (a.ch - 2 * a.di) + c - 2 * a.di] = to_bf16(sy);
+    }
+    if (i < static_cast<long long>(a.T) * a.Hv) {
+        const int hv = static_cast<int>(i % a.Hv);
+        a.beta[i] = 1.0f / (1.0f + expf(-a.beta_raw[i]));
+        const float x = a.alpha_raw[i] + a.dt_bias[hv];
+        a.gate[i] = a.a_log[hv] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+    }
+}
+
+// The conv ring after a sequence: its last three inputs (older ring values
+// for sequences shorter than three), one thread per (sequence, channel).
+__global__ void ring_update_kernel(const float *qkv, float *ring, const int32_t *cu, int N, int ch) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<long long>(N) * ch) return;
+    const int s = static_cast<int>(i / ch), c = static_cast<int>(i % ch);
+    const int t0 = cu[s], L = cu[s + 1] - t0;
+    float *r = ring + i * 3;
+    float nr[3];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) {
+        const int j = L - 3 + e;  // input index within the sequence
+        nr[e] = j >= 0 ? qkv[(static_cast<long long>(t0) + j) * ch + c] : r[3 + j];
+    }
+    r[0] = nr[0];
+    r[1] = nr[1];
+    r[2] = nr[2];
+}
+
+// finite_argmax (infer/mod.rs:70-83) of each row, one 1024-thread block per row.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *y, long long n, int32_t *idx) {
+    const long long row = blockIdx.x;
+    const float *yr = y + row * n;
+    unsigned long long best = 0;
+    for (long long i = threadIdx.x; i < n; i += 1024) best = argmax_key_max(best, argmax_key(yr[i], static_cast<unsigned>(i)));
+    best = argmax_block_key(best);
+    if (threadIdx.x == 0) idx[row] = argmax_index(best);
+}
+
+__global__ void fill_zero_kernel(float *p, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+// Start of a decode step: the new token of sequence b sits at position
+// lens[b], its attention sees lens[b] + 1 keys, and the cache grows by one.
+__global__ void lens_step_kernel(int32_t *lens, int32_t *pos, int32_t *klen, int B) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const int l = lens[b];
+    pos[b] = l;
+    klen[b] = l + 1;
+    lens[b] = l + 1;
+}
+
+unsigned blocks_for(long long n, int per) { return static_cast<unsigned>((n + per - 1) / per); }
+
+}  // namespace
+
+// ------------------------------------------------------- host launchers --
+
+int fill_zero(float *p, size_t n, void *stream) {
+    if (!n) return OURO_OK;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks_for(static_cast<long long>(n), 256)), dim3(256), 0,
+                       as_stream(stream), p, static_cast<long long>(n));
+    return check_launch("fill_zero_kernel");
+}
+
+int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, void *stream) {
+    hipLaunchKernelGGL(lens_step_kernel, dim3(blocks_for(static_cast<long long>(B), 256)), dim3(256), 0,
+                       as_stream(stream), lens, pos, klen, static_cast<int>(B));
+    return check_launch("lens_step_kernel");
+}
+
+int gen_codes(uint32_t seed, uint32_t tensor, size_t rows, size_t cols, uint8_t *dst, void *stream) {
+    if (cols % 4 || rows * cols >= (1ull << 32)) return fail(OURO_ERR_SHAPE, "gen_codes: %zu x %zu", rows, cols);
+    const long long bytes = static_cast<long long>(rows * cols / 4);
+    hipLaunchKernelGGL(gen_codes_kernel, dim3(blocks_for(bytes, 256)), dim3(256), 0, as_stream(stream), seed, tensor,
+                       static_cast<long long>(rows), static_cast<int>(cols), dst);
+    return check_launch("gen_codes_kernel");
+}
+
+int gen_floats(uint32_t seed, uint32_t tensor, size_t n, float lo, float span, float *dst, void *stream) {
+    if (n >= (1ull << 32)) return fail(OURO_ERR_SHAPE, "gen_floats: %zu values", n);
+    hipLaunchKernelGGL(gen_floats_kernel, dim3(blocks_for(static_cast<long long>(n), 256)), dim3(256), 0,
+                       as_stream(stream), seed, tensor, static_cast<long long>(n), lo, span, dst);
+    return check_launch("gen_floats_kernel");
+}
+
+int rmsnorm_rows(const float *a, const float *b, const float *w, float *sum_out, float *out, size_t rows, size_t n,
+                 float eps, void *stream) {
+    if (!rows) return OURO_OK;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, as_stream(stream), a, b, w,
+                       sum_out, out, static_cast<int>(n), eps);
+    return check_launch("rmsnorm_kernel");
+}
+
+int swiglu(const float *gate, const float *up, float *out, size_t n, void *stream) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(static_cast<long long>(n), 256)), dim3(256), 0,
+                       as_stream(stream), gate, up, out, static_cast<long long>(n));
+    return check_launch("swiglu_kernel");
+}
+
+int embed_rows(const int32_t *tokens, const float *table, float *x, size_t n_tok, size_t n_vocab, size_t n_embd,
+               void *stream) {
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks_for(static_cast<long long>(n_tok * n_embd), 256)), dim3(256), 0,
+                       as_stream(stream), tokens, table, x, static_cast<int>(n_tok), static_cast<int>(n_vocab),
+                       static_cast<int>(n_embd));
+    return check_launch("embed_kernel");
+}
+
+int gather_rows(const float *src, const int32_t *rows_idx, float *dst, size_t n, size_t width, void *stream) {
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_for(static_cast<long long>(n * width), 256)), dim3(256), 0,
+                       as_stream(stream), src, rows_idx, dst, static_cast<int>(n), static_cast<int>(width));
+    return check_launch("gather_rows_kernel");
+}
+
+int attn_prep(const float *qfull, const float *k, const float *v, const float *qn, const float *kn,
+              const int32_t *pos, const int32_t *seq, const long long *base, float *q_out, float *gate_out,
+              float *kc, float *vc, size_t T, int nh, int nkv, int n_rot, float rope_base, float eps,
+              void *stream) {
+    if (n_rot < 0 || n_rot > kHd || n_rot % 4) return fail(OURO_ERR_SHAPE, "attn_prep: n_rot %d", n_rot);
+    AttnPrepArgs a{qfull, k, v, qn, kn, pos, seq, base, q_out, gate_out, kc, vc,
+                   static_cast<int>(T), nh, nkv, n_rot, rope_base, eps};
+    const long long items = static_cast<long long>(T) * (nh + nkv);
+    hipLaunchKernelGGL(attn_prep_kernel, dim3(blocks_for(items, 4)), dim3(256), 0, as_stream(stream), a);
+    return check_launch("attn_prep_kernel");
+}
+
+int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+                 const int32_t *cu, const int32_t *tile_seq, const int32_t *tile_p0, size_t n_tiles, float *out,
+                 int nh, int nkv, void *stream) {
+    if (!n_tiles) return OURO_OK;
+    static bool lds_set = false;  // one opt-in per process for > 64 KiB of dynamic LDS
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kAttnLds);
+        if (e != hipSuccess) return fail(OURO_ERR_HIP, "attn_prefill: LDS opt-in: %s", hipGetErrorString(e));
+        lds_set = true;
+    }
+    AttnArgs a{q, gate, kc, vc, base, cu, nullptr, tile_seq, tile_p0, out, nh, nkv, 1.0f / sqrtf(static_cast<float>(kHd))};
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<unsigned>(n_tiles), nh), dim3(256), kAttnLds,
+                       as_stream(stream), a);
+    return check_launch("attn_prefill_kernel");
+}
+
+int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+                const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, void *stream) {
+    if (max_len > kMaxCtx) return fail(OURO_ERR_SHAPE, "attn_decode: context %d > %d", max_len, kMaxCtx);
+    static bool lds_set = false;
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_decode_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
+        if (e != hipSuccess) return fail(OURO_ERR_HIP, "attn_decode: LDS opt-in: %s", hipGetErrorString(e));
+        lds_set = true;
+    }
+    AttnArgs a{q, gate, kc, vc, base, nullptr, lens, nullptr, nullptr, out, nh, nkv,
+               1.0f / sqrtf(static_cast<float>(kHd))};
+    hipLaunchKernelGGL(attn_decode_kernel, dim3(static_cast<unsigned>(B), nh), dim3(256),
+                       static_cast<size_t>(max_len) * 4, as_stream(stream), a);
+    return check_launch("attn_decode_kernel");
+}
+
+int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, const int32_t *seq,
+                      const int32_t *pos, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
+                      const float *a_log, uint16_t *qb, uint16_t *kb, uint16_t *vb, float *beta, float *gate,
+                      size_t T, int ch, int di, int Hv, void *stream) {
+    ConvArgs a{qkv, ring, conv_w, seq, pos, beta_raw, alpha_raw, dt_bias, a_log, qb, kb, vb, beta, gate,
+               static_cast<int>(T), ch, di, Hv};
+    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(blocks_for(static_cast<long long>(T) * ch, 256)), dim3(256), 0,
+                       as_stream(stream), a);
+    return check_launch("prefill_conv_gate_kernel");
+}
+
+int ring_update(const float *qkv, float *ring, const int32_t *cu, size_t N, int ch, void *stream) {
+    hipLaunchKernelGGL(ring_update_kernel, dim3(blocks_for(static_cast<long long>(N) * ch, 256)), dim3(256), 0,
+                       as_stream(stream), qkv, ring, cu, static_cast<int>(N), ch);
+    return check_launch("ring_update_kernel");
+}
+
+int argmax_rows(const float *y, size_t rows, size_t n, int32_t *idx, void *stream) {
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, as_stream(stream), y,
+                       static_cast<long long>(n), idx);
+    return check_launch("argmax_rows_kernel");
+}
+
+}  // namespace ouro

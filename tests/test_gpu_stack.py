@@ -1,0 +1,116 @@
+"""Hybrid decoder stack (include/ouro_stack.h) against the CPU oracle of the
+reference's per-token stage (oracle/stack_oracle.py) on small cards: a
+ragged packed prefill of several prompts, then decode steps fed the fp32
+oracle's greedy tokens (teacher forcing, so every step compares the same
+history).
+
+Every ternary product requantises its input to int8, so a perturbation of
+any size flips a few roundings and moves the logits by about one int8 step:
+on these cards a relative change of 1e-6 in the delta-net conv outputs
+already moves the logits by up to 1.5% of their largest magnitude (two
+oracle runs on the CPU).  The GPU prefill feeds the delta-net recurrence
+bf16 q, k, v (the MFMA operands of the chunked prefill) and computes the
+chunk algebra to ~16 bits; the oracle run with the same bf16 rounding
+(bf16_prefill=True) is matched to TOL_BF16, a few int8 steps, and the fp32
+token-by-token oracle (the reference's own arithmetic; bf16 alone moves the
+logits by up to ~5%) to TOL_F32.  A wiring mistake (a wrong operand, head
+order or state hand-off) moves them by tens of percent."""
+import numpy as np
+import pytest
+
+from ouroboros_amd._lib import OuroError
+from ouroboros_amd.device import DeviceBuffer
+from ouroboros_amd.stack import Card, Stack
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 5e-2
+TOL_F32 = 0.1
+
+SMALL = Card(n_layer=4, n_embd=256, n_ff=512, n_vocab=512, full_attention_interval=2, n_head=2, n_head_kv=1,
+             n_rot=64, ssm_n_k_heads=1, ssm_n_v_heads=2, eps=1e-6, rope_base=1e7)
+# wider heads: GQA 4:2, Hk=2 Hv=4 (V-grouped order matters), 3 delta + 1 attention layer
+WIDE = Card(n_layer=4, n_embd=512, n_ff=768, n_vocab=1000, full_attention_interval=4, n_head=4, n_head_kv=2,
+            n_rot=32, ssm_n_k_heads=2, ssm_n_v_heads=4, eps=1e-6, rope_base=1e6)
+
+
+def rel(a, b):
+    return float(np.abs(a - b).max() / np.abs(b).max())
+
+
+def oracle_runs(card, prompts, steps):
+    from oracle.stack_oracle import StackOracle
+
+    l32, t32 = StackOracle(card, seed=7).run(prompts, steps)
+    l16, t16 = StackOracle(card, seed=7, bf16_prefill=True).run(prompts, steps, feed=t32[:-1])
+    return l32, t32, l16, t16
+
+
+def gpu_run(card, prompts, feed, max_seqs=4, max_tokens=64, max_ctx=32):
+    N, V = len(prompts), card.n_vocab
+    st = Stack(card, 7, max_seqs=max_seqs, max_tokens=max_tokens, max_ctx=max_ctx)
+    try:
+        cu = np.concatenate([[0], np.cumsum([len(p) for p in prompts])]).astype(np.int32)
+        toks = DeviceBuffer.from_host(np.concatenate(prompts).astype(np.int32))
+        nxt = DeviceBuffer((N,), np.int32)
+        lg = DeviceBuffer((N * V,), np.float32)
+        st.prefill(toks, cu, nxt, lg)
+        logits, tokens = [lg.download().reshape(N, V)], [nxt.download()]
+        for f in feed:
+            st.decode(DeviceBuffer.from_host(np.array(f, np.int32)), nxt, lg)
+            logits.append(lg.download().reshape(N, V))
+            tokens.append(nxt.download())
+    finally:
+        st.free()
+    return logits, tokens
+
+
+def check(card, prompts, steps, **kw):
+    l32, t32, l16, t16 = oracle_runs(card, prompts, steps)
+    got, gtok = gpu_run(card, prompts, t32[:-1], **kw)
+    e16 = [rel(g, w) for g, w in zip(got, l16)]
+    e32 = [rel(g, w) for g, w in zip(got, l32)]
+    print("vs bf16-prefill oracle", e16, "vs fp32 oracle", e32)
+    assert max(e16) < TOL_BF16, e16
+    assert max(e32) < TOL_F32, e32
+    # greedy tokens agree with the matching oracle wherever its top two logits are apart
+    for g, w, lg in zip(gtok, t16, l16):
+        top2 = np.sort(lg, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2 * TOL_BF16 * np.abs(lg).max(axis=1)
+        assert np.array_equal(np.asarray(g)[clear], np.asarray(w)[clear])
+
+
+def test_stack_matches_oracle(gpu):
+    rng = np.random.default_rng(3)
+    prompts = [list(rng.integers(0, SMALL.n_vocab, n)) for n in (5, 9, 2)]
+    check(SMALL, prompts, 3)
+
+
+def test_stack_single_token_prompts(gpu):
+    check(SMALL, [[5], [511], [0]], 2)
+
+
+def test_stack_long_ragged_prompts_wide_heads(gpu):
+    # prompts across the 64-token chunk and attention-tile edges, one of length 1
+    rng = np.random.default_rng(4)
+    prompts = [list(rng.integers(0, WIDE.n_vocab, n)) for n in (70, 1, 64, 129)]
+    check(WIDE, prompts, 2, max_seqs=4, max_tokens=300, max_ctx=160)
+
+
+def test_stack_rejects_bad_calls(gpu):
+    st = Stack(SMALL, 7, max_seqs=2, max_tokens=10, max_ctx=8)
+    try:
+        nxt = DeviceBuffer((4,), np.int32)
+        toks = DeviceBuffer.from_host(np.zeros(32, np.int32))
+        with pytest.raises(OuroError):  # decode before any prefill
+            st.decode(toks, nxt)
+        for cu in ([0, 1, 2, 3], [0, 8], [0, 0, 3], [1, 3], [0, 6, 12]):
+            # too many sequences, prompt >= max_ctx, empty prompt, bad start, > max_tokens
+            with pytest.raises(OuroError):
+                st.prefill(toks, np.array(cu, np.int32), nxt)
+        st.prefill(toks, np.array([0, 7], np.int32), nxt)  # 7 tokens fill max_ctx - 1
+        st.decode(toks, nxt)  # 8th position
+        with pytest.raises(OuroError):  # the context is full
+            st.decode(toks, nxt)
+    finally:
+        st.free()
