@@ -379,6 +379,84 @@ def bench_prefill(stream, steps, warmup):
     return time_events(stream, step, max(3, steps // 5), 2)
 
 
+# Hybrid stack: 64 prompts of 16..2048 tokens packed varlen, then 128
+# greedy decode steps of all 64 sequences (24 layers, 3 delta : 1 attention).
+ST_SEQS, ST_MIN, ST_MAX, ST_STEPS = 64, 16, 2048, 128
+
+
+def stack_lens() -> np.ndarray:
+    return np.random.default_rng(5).integers(ST_MIN, ST_MAX + 1, ST_SEQS)
+
+
+def stack_algorithmic(card, lens) -> dict:
+    """Algorithmic HBM bytes of one decode step (every weight byte once,
+    delta-net state read + written, the KV cache of every attention layer
+    read once, averaged over the steps) and int8 ops of the prefill's
+    ternary products (2 x rows x weights, lm_head on the last rows only)."""
+    E, F, V, L = card.n_embd, card.n_ff, card.n_vocab, card.n_layer
+    d = card.head_dim
+    di, dv = card.ssm_n_k_heads * d, card.ssm_n_v_heads * d
+    qdim, kvdim = card.n_head * d, card.n_head_kv * d
+    n_attn = L // card.full_attention_interval
+    n_delta = L - n_attn
+    ffn = 3 * E * F
+    w_delta = (2 * di + dv) * E + dv * E + 2 * card.ssm_n_v_heads * E + E * dv
+    w_attn = 2 * qdim * E + 2 * kvdim * E + E * qdim
+    weights = n_delta * (w_delta + ffn) + n_attn * (w_attn + ffn)
+    B = len(lens)
+    state = n_delta * B * card.ssm_n_v_heads * d * d * 4 * 2
+    mean_ctx = float(np.mean(lens)) + (ST_STEPS + 1) / 2
+    kv = n_attn * B * mean_ctx * kvdim * 4 * 2
+    dec_bytes = weights // 4 + V * E // 4 + state + kv + B * E * 4
+    T = int(np.sum(lens))
+    pf_ops = 2 * T * weights + 2 * B * V * E
+    return {"decode_step_bytes": int(dec_bytes), "weight_bytes": int(weights // 4 + V * E // 4),
+            "state_bytes": int(state), "kv_bytes": int(kv), "prefill_int8_ops": int(pf_ops)}
+
+
+def bench_stack(stream, steps, warmup):
+    """One step = a packed prefill of the 64 prompts + 128 decode steps, the
+    greedy tokens fed back on the device.  Returns (prefill ms, decode ms
+    for all steps, device bytes, prompt tokens)."""
+    from ouroboros_amd.device import DeviceBuffer, Event, synchronize
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.stack import Card, Stack
+
+    card = Card()
+    lens = stack_lens()
+    T = int(lens.sum())
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    rng = np.random.default_rng(6)
+    st = Stack(card, 1234, max_seqs=ST_SEQS, max_tokens=T, max_ctx=ST_MAX + ST_STEPS + 1)
+    toks = DeviceBuffer.from_host(rng.integers(0, card.n_vocab, T).astype(np.int32))
+    a, b = DeviceBuffer((ST_SEQS,), np.int32), DeviceBuffer((ST_SEQS,), np.int32)
+    try:
+        def run():
+            e0, e1, e2 = Event(), Event(), Event()
+            e0.record(stream)
+            st.prefill(toks, cu, a, None, stream)
+            e1.record(stream)
+            cur, nxt = a, b
+            for _ in range(ST_STEPS):
+                st.decode(cur, nxt, None, stream)
+                cur, nxt = nxt, cur
+            e2.record(stream)
+            call("ouro_device_synchronize")
+            return e0.elapsed_ms(e1), e1.elapsed_ms(e2)
+
+        for _ in range(max(1, min(warmup, 2))):
+            run()
+        synchronize(stream)
+        pf, dec = [], []
+        for _ in range(max(1, min(steps, 3))):
+            p, d_ = run()
+            pf.append(p)
+            dec.append(d_)
+        return float(np.mean(pf)), float(np.mean(dec)), st.device_bytes, T, card, lens
+    finally:
+        st.free()
+
+
 COPY_BYTES = 512 << 20
 
 
@@ -502,7 +580,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "fwht", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "fwht", "prefill", "copy", "stack"],
+                    default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -543,6 +622,9 @@ def main() -> int:
     if args.only in (None, "prefill"):
         log("GDN chunked prefill 4x4096")
         res["prefill"] = bench_prefill(stream, args.steps, args.warmup)
+    if args.only in (None, "stack"):
+        log(f"hybrid stack: {ST_SEQS} prompts of {ST_MIN}..{ST_MAX} tokens + {ST_STEPS} decode steps")
+        res["stack"] = bench_stack(stream, args.steps, args.warmup)
 
     traffic = load_traffic()
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -647,6 +729,27 @@ def main() -> int:
                          "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_sum(traffic, ["gdn_chunk_prep_kernel", "gdn_chunk_scan_kernel"])},
             "algorithmic_gflop": round(PF_FLOPS / 1e9, 2), "bytes": PF_BYTES, "hbm_GBs": round(gbs, 1),
             "frac_of_min_roofline": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
+        }
+    if "stack" in res:
+        pf_ms, dec_ms, dev_bytes, T, card, lens = res["stack"]
+        alg = stack_algorithmic(card, lens)
+        step_ms = dec_ms / ST_STEPS
+        dec_gbs = alg["decode_step_bytes"] / (step_ms * 1e-3) / 1e9
+        pf_tops = alg["prefill_int8_ops"] / (pf_ms * 1e-3) / 1e12
+        gen = ST_SEQS * ST_STEPS
+        sec["hybrid_stack"] = {
+            "value": round((T + gen) / ((pf_ms + dec_ms) * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_step": round(pf_ms + dec_ms, 3),
+            "config": f"24 layers (18 gated delta-net, 6 full attention), hidden 2560, FFN 6912, vocab 248320, "
+                      f"I2 ternary projections on Hadamard-rotated int8 activations; {ST_SEQS} prompts of "
+                      f"{ST_MIN}..{ST_MAX} tokens ({T} total) packed varlen, then {ST_STEPS} greedy decode steps "
+                      f"of all {ST_SEQS} sequences; synthetic seeded weights",
+            "prefill_tokens_per_s": round(T / (pf_ms * 1e-3), 1), "prefill_ms": round(pf_ms, 3),
+            "decode_tokens_per_s": round(gen / (dec_ms * 1e-3), 1), "decode_step_ms": round(step_ms, 4),
+            "decode_roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
+            "prefill_ternary_TOPs": round(pf_tops, 1),
+            "algorithmic": alg, "device_bytes": int(dev_bytes),
         }
     if orc is not None:
         log("CPU baseline")
