@@ -52,8 +52,9 @@ int attn_prep(const float *qfull, const float *k, const float *v, const float *q
 int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
                  const int32_t *cu, const int32_t *tile_seq, const int32_t *tile_p0, size_t n_tiles, float *out,
                  int nh, int nkv, void *stream);
+size_t attn_decode_ws_bytes(size_t B, int nh, size_t max_ctx);
 int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
-                const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, void *stream);
+                const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, float *part, void *stream);
 int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, const int32_t *seq,
                       const int32_t *pos, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
                       const float *a_log, uint16_t *qb, uint16_t *kb, uint16_t *vb, float *beta, float *gate,
@@ -119,7 +120,7 @@ struct ouro_stack {
     float *x = nullptr, *h = nullptr, *pre = nullptr, *f = nullptr, *mix = nullptr;
     float *big = nullptr, *big2 = nullptr, *zb = nullptr, *braw = nullptr, *araw = nullptr;
     float *o = nullptr, *g = nullptr, *qbuf = nullptr, *gbuf = nullptr, *kbuf = nullptr, *vbuf = nullptr;
-    float *attn_o = nullptr, *lp = nullptr, *lmx = nullptr, *hl = nullptr, *logits = nullptr;
+    float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *lmx = nullptr, *hl = nullptr, *logits = nullptr;
     int8_t *xq = nullptr;
     float *ds = nullptr;
     uint16_t *qb = nullptr, *kb = nullptr, *vb = nullptr;
@@ -238,7 +239,7 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
                              s->attn_o, c.n_head, c.n_head_kv, stream));
         else
             TRY(attn_decode(s->qbuf, s->gbuf, L.kc, L.vc, s->base, s->klen, rows, s->max_len, s->attn_o, c.n_head,
-                            c.n_head_kv, stream));
+                            c.n_head_kv, s->attn_part, stream));
         TRY(rq(s, s->attn_o, rows, s->qdim, s->sign_q, stream));
         TRY(lin(s, L.o, rows, s->mix, stream));
     }
@@ -269,8 +270,8 @@ int check_card(const ouro_stack_card &c) {
         c.full_attention_interval < 1)
         return fail(OURO_ERR_SHAPE, "ouro_stack: bad sizes (n_embd and n_ff multiples of 256)");
     if (c.head_dim != kHd || c.ssm_d_state != kHd) return fail(OURO_ERR_SHAPE, "ouro_stack: head_dim and d_state must be 128");
-    if (c.n_head < 2 || c.n_head % 2 || c.n_head_kv < 1 || c.n_head % c.n_head_kv)
-        return fail(OURO_ERR_SHAPE, "ouro_stack: n_head even and a multiple of n_head_kv");
+    if (c.n_head < 2 || c.n_head % 2 || c.n_head_kv < 1 || c.n_head % c.n_head_kv || c.n_head / c.n_head_kv > 8)
+        return fail(OURO_ERR_SHAPE, "ouro_stack: n_head even, a multiple of n_head_kv, at most 8 per kv head");
     if (c.n_rot < 0 || c.n_rot > kHd || c.n_rot % 4) return fail(OURO_ERR_SHAPE, "ouro_stack: n_rot");
     if (c.ssm_n_k_heads < 1 || c.ssm_n_v_heads % 2 || c.ssm_n_v_heads % c.ssm_n_k_heads)
         return fail(OURO_ERR_SHAPE, "ouro_stack: ssm heads (n_v_heads even, a multiple of n_k_heads)");
@@ -390,7 +391,9 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         return done(st);
     const size_t wsb = std::max(gdn_chunk_ws_bytes(max_tokens, max_seqs, c.ssm_n_v_heads),
                                 gdn_layer_ws_bytes(max_seqs, c.ssm_n_k_heads, c.ssm_n_v_heads));
-    if ((st = dalloc(s, reinterpret_cast<uint8_t **>(&s->ws), wsb))) return done(st);
+    if ((st = dalloc(s, reinterpret_cast<uint8_t **>(&s->ws), wsb)) ||
+        (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->attn_part), attn_decode_ws_bytes(max_seqs, c.n_head, max_ctx))))
+        return done(st);
     // constant per-sequence data: cache bases and the decode row -> sequence map
     s->host_i32_n = 3 * rows + 2 * tiles + 4 * max_seqs + 8;
     if (hipHostMalloc(reinterpret_cast<void **>(&s->host_i32), s->host_i32_n * 4, hipHostMallocDefault) != hipSuccess)

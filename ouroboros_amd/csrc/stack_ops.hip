@@ -361,66 +361,129 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
 
 // ----------------------------------------------------- attention (decode) --
 
-constexpr int kMaxCtx = 16384;  // keys per sequence the decode kernel holds
 
 // One 256-thread workgroup per (sequence, q head): scores of all keys into
 // LDS (a 16-lane group per key, 8 dims per lane), softmax, then each of 256
 // threads accumulates one (dim, key half) of p V.
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnArgs a) {
-    extern __shared__ float sc[];
-    __shared__ float red[8];
-    __shared__ float half_o[kHd];
+// Decode attention, split over the context (flash-decoding): workgroup
+// (sequence b, kv head, split sp) takes keys sp*kDecKeys .. +kDecKeys of b
+// for all G = nh/nkv query heads of that kv head, so each K and V row is
+// read once per step.  Scores: 16 lanes per key (8 dims each, G dot
+// products, DPP row sums), 4 keys per wavefront per step, into LDS; per-head
+// max and exp-sum over the split; P V with lane = 2 dims and the 4
+// wavefronts on interleaved keys, reduced through LDS.  The split's
+// unnormalised output, max and sum go to `part`; attn_combine_kernel merges
+// the splits of each (b, head) and applies the sigmoid output gate.
+constexpr int kDecKeys = 256;
+constexpr int kPartStride = kHd + 4;  // floats per (b, head, split) record: o[128], m, l
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, float *part, int nsplit) {
+    __shared__ float sc[G][kDecKeys];
+    __shared__ float red[4][G][kHd];
+    __shared__ float ml[G][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int b = blockIdx.x, h = blockIdx.y;
-    const int kvh = h / (a.nh / a.nkv);
+    const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
     const int L = a.lens[b];
-    const long long kbase = a.base[b];
-    const long long qo = (static_cast<long long>(b) * a.nh + h) * kHd;
-    const int g = lane >> 4, gl = lane & 15;  // key group of the wavefront, lane in group
-    const float4 q0 = *reinterpret_cast<const float4 *>(a.q + qo + 8 * gl);
-    const float4 q1 = *reinterpret_cast<const float4 *>(a.q + qo + 8 * gl + 4);
-    for (int j0 = 0; j0 < L; j0 += 16) {
-        const int j = j0 + 4 * wave + g;
-        float part = 0.f;
-        if (j < L) {
-            const long long off = ((kbase + j) * a.nkv + kvh) * kHd + 8 * gl;
-            const float4 k0 = *reinterpret_cast<const float4 *>(a.kc + off);
-            const float4 k1 = *reinterpret_cast<const float4 *>(a.kc + off + 4);
-            part = q0.x * k0.x + q0.y * k0.y + q0.z * k0.z + q0.w * k0.w + q1.x * k1.x + q1.y * k1.y +
-                   q1.z * k1.z + q1.w * k1.w;
+    const int j0 = sp * kDecKeys;
+    if (j0 >= L) return;  // whole workgroup
+    const int n = min(kDecKeys, L - j0);
+    const long long row0 = a.base[b] + j0;
+    const int g4 = lane >> 4, gl = lane & 15;
+    float4 q[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float *qp = a.q + (static_cast<long long>(b) * a.nh + kvh * G + g) * kHd + 8 * gl;
+        q[g][0] = *reinterpret_cast<const float4 *>(qp);
+        q[g][1] = *reinterpret_cast<const float4 *>(qp + 4);
+    }
+    // scores: wave w, step it -> key w*64 + 4*it + g4
+#pragma unroll 4
+    for (int it = 0; it < 16; ++it) {
+        const int j = wave * 64 + 4 * it + g4;
+        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0;
+        if (j < n) {
+            const float *kp = a.kc + ((row0 + j) * a.nkv + kvh) * kHd + 8 * gl;
+            k0 = *reinterpret_cast<const float4 *>(kp);
+            k1 = *reinterpret_cast<const float4 *>(kp + 4);
         }
-        part = row16_sum(part);
-        if (gl == 0 && j < L) sc[j] = part * a.scale;
-    }
-    __syncthreads();
-    float mx = -INFINITY;
-    for (int j = tid; j < L; j += 256) mx = fmaxf(mx, sc[j]);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) red[wave] = mx;
+        for (int g = 0; g < G; ++g) {
+            float d = q[g][0].x * k0.x + q[g][0].y * k0.y + q[g][0].z * k0.z + q[g][0].w * k0.w +
+                      q[g][1].x * k1.x + q[g][1].y * k1.y + q[g][1].z * k1.z + q[g][1].w * k1.w;
+            d = row16_sum(d);
+            if (gl == 0 && j < n) sc[g][j] = d * a.scale;
+        }
+    }
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float sum = 0.f;
-    for (int j = tid; j < L; j += 256) {
-        const float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
+    // per-head max and exp-sum over the split (wave w takes heads w, w+4, ...)
+    for (int g = wave; g < G; g += 4) {
+        float mx = -INFINITY;
+        for (int j = lane; j < n; j += 64) mx = fmaxf(mx, sc[g][j]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        float sum = 0.f;
+        for (int j = lane; j < n; j += 64) {
+            const float e = expf(sc[g][j] - mx);
+            sc[g][j] = e;
+            sum += e;
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) {
+            ml[g][0] = mx;
+            ml[g][1] = sum;
+        }
+    }
+    __syncthreads();
+    // P V: wave w takes keys w, w+4, ...; lane owns dims 2*lane, 2*lane+1
+    float2 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = make_float2(0.f, 0.f);
+    const float *vp = a.vc + (row0 * a.nkv + kvh) * kHd + 2 * lane;
+    const long long vstride = static_cast<long long>(a.nkv) * kHd;
+#pragma unroll 4
+    for (int j = wave; j < n; j += 4) {
+        const float2 v = *reinterpret_cast<const float2 *>(vp + j * vstride);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float pj = sc[g][j];
+            acc[g].x += pj * v.x;
+            acc[g].y += pj * v.y;
+        }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    __syncthreads();  // red[] reuse and sc[] writes
-    if (lane == 0) red[4 + wave] = sum;
+    for (int g = 0; g < G; ++g) *reinterpret_cast<float2 *>(&red[wave][g][2 * lane]) = acc[g];
     __syncthreads();
-    sum = red[4] + red[5] + red[6] + red[7];
-    const int d = tid & (kHd - 1), hf = tid >> 7;
-    float acc = 0.f;
-    for (int j = hf; j < L; j += 2) acc += sc[j] * a.vc[((kbase + j) * a.nkv + kvh) * kHd + d];
-    if (hf == 1) half_o[d] = acc;
-    __syncthreads();
-    if (hf == 0) {
-        const float g2 = a.gate[qo + d];
-        a.out[qo + d] = ((acc + half_o[d]) / sum) * (1.0f / (1.0f + expf(-g2)));
+    for (int i = tid; i < G * kHd; i += 256) {
+        const int g = i / kHd, d = i % kHd;
+        const float o = red[0][g][d] + red[1][g][d] + red[2][g][d] + red[3][g][d];
+        float *rec = part + ((static_cast<long long>(b) * a.nh + kvh * G + g) * nsplit + sp) * kPartStride;
+        rec[d] = o;
+        if (d == 0) {
+            rec[kHd] = ml[g][0];
+            rec[kHd + 1] = ml[g][1];
+        }
     }
+}
+
+// Merge the splits of (b, head): o = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s,
+// times sigmoid(gate) (qwen35.rs:1205-1210).  One 128-thread workgroup per (b, head).
+__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, const float *part, int nsplit) {
+    const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    const int ns = (a.lens[b] + kDecKeys - 1) / kDecKeys;
+    const float *rec = part + (static_cast<long long>(b) * a.nh + h) * nsplit * kPartStride;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, rec[s * kPartStride + kHd]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < ns; ++s) {
+        const float w = expf(rec[s * kPartStride + kHd] - M);
+        num += w * rec[s * kPartStride + d];
+        den += w * rec[s * kPartStride + kHd + 1];
+    }
+    const long long qo = (static_cast<long long>(b) * a.nh + h) * kHd + d;
+    const float g2 = a.gate[qo];
+    a.out[qo] = (num / den) * (1.0f / (1.0f + expf(-g2)));
 }
 
 // ------------------------------------------------ delta-net prefill inputs --
@@ -605,21 +668,35 @@ int attn_prefill(const float *q, const float *gate, const float *kc, const float
     return check_launch("attn_prefill_kernel");
 }
 
+size_t attn_decode_ws_bytes(size_t B, int nh, size_t max_ctx) {
+    return B * static_cast<size_t>(nh) * ((max_ctx + kDecKeys - 1) / kDecKeys) * kPartStride * sizeof(float);
+}
+
 int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
-                const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, void *stream) {
-    if (max_len > kMaxCtx) return fail(OURO_ERR_SHAPE, "attn_decode: context %d > %d", max_len, kMaxCtx);
-    static bool lds_set = false;
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_decode_kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
-        if (e != hipSuccess) return fail(OURO_ERR_HIP, "attn_decode: LDS opt-in: %s", hipGetErrorString(e));
-        lds_set = true;
-    }
+                const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, float *part, void *stream) {
+    const int G = nh / nkv;
+    if (G < 1 || G > 8 || nh % nkv) return fail(OURO_ERR_SHAPE, "attn_decode: %d heads over %d kv heads", nh, nkv);
+    if (max_len < 1 || !B) return OURO_OK;
+    const int nsplit = (max_len + kDecKeys - 1) / kDecKeys;
     AttnArgs a{q, gate, kc, vc, base, nullptr, lens, nullptr, nullptr, out, nh, nkv,
                1.0f / sqrtf(static_cast<float>(kHd))};
-    hipLaunchKernelGGL(attn_decode_kernel, dim3(static_cast<unsigned>(B), nh), dim3(256),
-                       static_cast<size_t>(max_len) * 4, as_stream(stream), a);
-    return check_launch("attn_decode_kernel");
+    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(nkv), static_cast<unsigned>(nsplit));
+    hipStream_t s = as_stream(stream);
+    switch (G) {
+    case 1: hipLaunchKernelGGL(attn_decode_split_kernel<1>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 2: hipLaunchKernelGGL(attn_decode_split_kernel<2>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 3: hipLaunchKernelGGL(attn_decode_split_kernel<3>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 4: hipLaunchKernelGGL(attn_decode_split_kernel<4>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 5: hipLaunchKernelGGL(attn_decode_split_kernel<5>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 6: hipLaunchKernelGGL(attn_decode_split_kernel<6>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    case 7: hipLaunchKernelGGL(attn_decode_split_kernel<7>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    default: hipLaunchKernelGGL(attn_decode_split_kernel<8>, grid, dim3(256), 0, s, a, part, nsplit); break;
+    }
+    int st = check_launch("attn_decode_split_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(static_cast<unsigned>(B), static_cast<unsigned>(nh)), dim3(kHd), 0, s,
+                       a, part, nsplit);
+    return check_launch("attn_combine_kernel");
 }
 
 int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, const int32_t *seq,
