@@ -28,14 +28,14 @@ extern "C" {
 
 typedef struct {
     int32_t n_layer;                 /* decoder layers */
-    int32_t n_embd;                  /* hidden width, a multiple of 256 */
-    int32_t n_ff;                    /* FFN width, a multiple of 256 */
+    int32_t n_embd;                  /* hidden width, a multiple of 256, <= 6144 */
+    int32_t n_ff;                    /* FFN width, a multiple of 256, <= 12288 */
     int32_t n_vocab;
     int32_t full_attention_interval; /* layer il is attention iff (il+1) % interval == 0 (qwen35.rs:421-423) */
     int32_t n_head, n_head_kv;       /* attention heads (n_head even, 1..8 x n_head_kv) */
     int32_t head_dim;                /* 128 */
     int32_t n_rot;                   /* rotated dims of rope_partial_neox, a multiple of 4, <= 128 */
-    int32_t ssm_n_k_heads, ssm_n_v_heads, ssm_d_state; /* delta-net heads (n_v_heads even); d_state 128 */
+    int32_t ssm_n_k_heads, ssm_n_v_heads, ssm_d_state; /* delta-net heads (n_v_heads even, <= 96); d_state 128 */
     float eps, rope_base;
 } ouro_stack_card;
 

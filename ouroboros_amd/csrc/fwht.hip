@@ -230,6 +230,204 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     if (tid == 0) a.dscale[row] = amax / 127.0f;
 }
 
+// ------------------------------------------------------------------------
+// Fused row kernels: a prologue that produces the row to be rotated, then
+// the same butterfly passes and int8 absmax epilogue as fwht_row_kernel.
+//   RQ_COPY    v = a
+//   RQ_NORM    s = a (+ b) (optionally stored), v = s * inv * w with
+//              inv = 1 / sqrt(mean(s^2) + eps) (rmsnorm, ops.rs:12-17);
+//              Q2 also quantises the unrotated v (no rotation) into xq2
+//   RQ_SWIGLU  v = silu(a) * b (run_ffn, qwen35.rs:802)
+//   RQ_GNORM   per 128-wide head of a: v = a * inv_h * w * silu(b)
+//              (gated_norm_rms, qwen35.rs:82-92), heads optionally placed in
+//              the V-grouped order (qwen35.rs:1122-1138)
+// then v * signs -> WHT blocks -> * 1/sqrt(block) -> int8 absmax.  The int8
+// rows go out row-major, or (tiles > 0) in the B-fragment order of the
+// few-column ternary GEMM: 16-byte chunk k/16 of row r at
+// (((k/256)*4 + (k%256)/64) * tiles + r/16) * 1024 + (16*((k%64)/16) + r%16) * 16.
+enum { RQ_COPY = 0, RQ_NORM = 1, RQ_SWIGLU = 2, RQ_GNORM = 3 };
+
+struct RowRqArgs {
+    const float *a, *b, *w;
+    float *sum_out;
+    const float *signs;
+    int8_t *xq, *xq2;
+    float *ds, *ds2;
+    int n, tiles, Hk, Hv;
+    unsigned flags;
+    float eps, scale;
+};
+
+__device__ __forceinline__ long long rq_offset(long long row, int c16, int n, int tiles) {
+    if (!tiles) return row * n + 16LL * c16;
+    const int kb = c16 >> 4, s = (c16 >> 2) & 3, g = c16 & 3;
+    return ((static_cast<long long>(kb * 4 + s) * tiles + (row >> 4)) * 64 + 16 * g + (row & 15)) * 16;
+}
+
+__device__ __forceinline__ void quant16_store(const float *p, float s, int8_t *dst) {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float t = rintf(p[i] * s);
+        t = fminf(fmaxf(t, -127.f), 127.f);
+        w[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xffu) << (8 * (i & 3));
+    }
+    *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <int LOGB, int PRO, bool Q2>
+__global__ __launch_bounds__(kThreads) void row_rq_kernel(RowRqArgs a) {
+    extern __shared__ float lds[];
+    __shared__ float red[8];
+    const long long row = blockIdx.x;
+    const int n = a.n, tid = threadIdx.x, chunks = n / 16;
+    float *hl = lds + 17 * chunks + 16;  // Q2: the unrotated row, same padded layout
+    const float *ar = a.a + row * n;
+    float inv = 0.f;
+    if constexpr (PRO == RQ_NORM) {
+        const float *br = a.b ? a.b + row * n : nullptr;
+        float ss = 0.f;
+        for (int c = tid; c < chunks; c += kThreads) {
+            float v[16];
+            ld16(ar + 16 * c, v);
+            if (br) {
+                float u[16];
+                ld16(br + 16 * c, u);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = v[i] + u[i];
+            }
+            if (a.sum_out) st16(a.sum_out + row * n + 16 * c, v);
+            float *p = lds + 17 * c;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                ss += v[i] * v[i];
+                p[i] = v[i];
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = red[0] + red[1] + red[2] + red[3];
+        inv = 1.0f / sqrtf(ss / static_cast<float>(n) + a.eps);
+    }
+    float amax2 = 0.f;
+    for (int c = tid; c < chunks; c += kThreads) {
+        float v[16];
+        int dc = c;
+        if constexpr (PRO == RQ_NORM) {
+            const float *p = lds + 17 * c;
+            float wv[16];
+            ld16(a.w + 16 * c, wv);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = p[i] * inv * wv[i];
+            if constexpr (Q2) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    hl[17 * c + i] = v[i];
+                    amax2 = fmaxf(amax2, fabsf(v[i]));
+                }
+            }
+        } else if constexpr (PRO == RQ_SWIGLU) {
+            float u[16];
+            ld16(ar + 16 * c, v);
+            ld16(a.b + row * n + 16 * c, u);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = v[i] / (1.0f + expf(-v[i])) * u[i];
+        } else if constexpr (PRO == RQ_GNORM) {
+            // the 8 chunks of a head sit on 8 consecutive lanes (n = Hv * 128)
+            ld16(ar + 16 * c, v);
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) ss += v[i] * v[i];
+            ss += xor_shfl(ss, 1);
+            ss += xor_shfl(ss, 2);
+            ss += xor_shfl(ss, 4);
+            const float invh = 1.0f / sqrtf(ss / 128.0f + a.eps);
+            float z[16], wv[16];
+            ld16(a.b + row * n + 16 * c, z);
+            ld16(a.w + 16 * (c & 7), wv);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float g = z[i] / (1.0f + expf(-z[i]));
+                v[i] = v[i] * invh * wv[i] * g;
+            }
+            if (a.flags & OURO_GDN_V_GROUPED) {
+                const int h = c >> 3;
+                dc = ((h % a.Hk) * (a.Hv / a.Hk) + h / a.Hk) * 8 + (c & 7);
+            }
+        } else {
+            ld16(ar + 16 * c, v);
+        }
+        if (a.signs) {
+            float sg[16];
+            ld16(a.signs + 16 * dc, sg);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = v[i] * sg[i];
+        }
+        wht16<LOGB>(v);
+        float *p = lds + 17 * dc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) p[i] = v[i];
+    }
+    if constexpr (LOGB > 4) {
+        __syncthreads();
+        wht_pass<LOGB, 1>(lds, n, tid);
+    }
+    if constexpr (LOGB > 8) {
+        __syncthreads();
+        wht_pass<LOGB, 2>(lds, n, tid);
+    }
+    if constexpr (LOGB > 12) {
+        __syncthreads();
+        wht_pass<LOGB, 3>(lds, n, tid);
+    }
+    __syncthreads();
+    float amax = 0.f;
+    for (int c = tid; c < chunks; c += kThreads) {
+        float *p = lds + 17 * c;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float t = p[i] * a.scale;
+            p[i] = t;
+            amax = fmaxf(amax, fabsf(t));
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        amax = fmaxf(amax, xor_shfl(amax, off));
+        if constexpr (Q2) amax2 = fmaxf(amax2, xor_shfl(amax2, off));
+    }
+    if ((tid & 63) == 0) {
+        red[4 + (tid >> 6)] = amax;
+        if constexpr (Q2) red[tid >> 6] = amax2;
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
+    {
+        const float s = amax == 0.f ? 0.f : 127.0f / amax;
+        for (int c = tid; c < chunks; c += kThreads) quant16_store(lds + 17 * c, s, a.xq + rq_offset(row, c, n, a.tiles));
+        if (tid == 0) a.ds[row] = amax == 0.f ? 0.f : amax / 127.0f;
+    }
+    if constexpr (Q2) {
+        amax2 = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        const float s = amax2 == 0.f ? 0.f : 127.0f / amax2;
+        for (int c = tid; c < chunks; c += kThreads) quant16_store(hl + 17 * c, s, a.xq2 + rq_offset(row, c, n, a.tiles));
+        if (tid == 0) a.ds2[row] = amax2 == 0.f ? 0.f : amax2 / 127.0f;
+    }
+}
+
+template <int PRO, bool Q2>
+void (*pick_rq(int logb))(RowRqArgs) {
+    switch (logb) {
+    case 8: return row_rq_kernel<8, PRO, Q2>;
+    case 9: return row_rq_kernel<9, PRO, Q2>;
+    case 10: return row_rq_kernel<10, PRO, Q2>;
+    case 11: return row_rq_kernel<11, PRO, Q2>;
+    case 12: return row_rq_kernel<12, PRO, Q2>;
+    case 13: return row_rq_kernel<13, PRO, Q2>;
+    default: return nullptr;
+    }
+}
+
 template <typename TI, typename TO, bool INV, bool QUANT, bool STORE>
 void (*pick_logb(int logb))(FwhtArgs) {
     switch (logb) {
@@ -319,6 +517,43 @@ int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, siz
     if (fi && !fo) return launch_io<float, uint16_t>(a, logb, inv, quant, store, s);
     if (!fi && fo) return launch_io<uint16_t, float>(a, logb, inv, quant, store, s);
     return launch_io<uint16_t, uint16_t>(a, logb, inv, quant, store, s);
+}
+
+// Fused prologue + rotation + int8 quantisation of rows x n (n a multiple
+// of block, block a power of two in 256..8192).  pro: RQ_COPY, RQ_NORM
+// (a + b optional, sum_out optional, w[n]; xq2/ds2 optional: the unrotated
+// row quantised too), RQ_SWIGLU (gate a, up b), RQ_GNORM (o a, z b, w[128],
+// n = Hv * 128, flags OURO_GDN_V_GROUPED).  tiles > 0 writes the int8 rows
+// in the few-column GEMM's fragment order for 16 * tiles >= rows columns.
+int row_rotate_quant(int pro, const float *a, const float *b, const float *w, float *sum_out, size_t rows,
+                     size_t n, size_t block, const float *signs, int8_t *xq, float *ds, int8_t *xq2, float *ds2,
+                     int tiles, int Hk, int Hv, unsigned flags, float eps, void *stream) {
+    if (!a || !xq || !ds) return fail(OURO_ERR_INVALID_ARG, "row_rotate_quant: NULL argument");
+    if (block < 256 || (block & (block - 1)) || block > 8192 || n % block || n > 12288)
+        return fail(OURO_ERR_SHAPE, "row_rotate_quant: len %zu, block %zu", n, block);
+    if (pro == RQ_GNORM && (n != static_cast<size_t>(Hv) * 128 || Hk < 1 || Hv % Hk))
+        return fail(OURO_ERR_SHAPE, "row_rotate_quant: gated norm over %d heads of 128 (len %zu)", Hv, n);
+    if (tiles && static_cast<size_t>(tiles) * 16 < rows)
+        return fail(OURO_ERR_SHAPE, "row_rotate_quant: %d fragment tiles for %zu rows", tiles, rows);
+    if (!rows) return OURO_OK;
+    RowRqArgs r{a, b, w, sum_out, signs, xq, xq2, ds, ds2, static_cast<int>(n), tiles, Hk, Hv, flags, eps,
+                1.0f / sqrtf(static_cast<float>(block))};
+    int logb = 0;
+    while ((size_t(1) << logb) < block) ++logb;
+    const bool q2 = pro == RQ_NORM && xq2 && ds2;
+    void (*kern)(RowRqArgs) = nullptr;
+    switch (pro) {
+    case RQ_COPY: kern = pick_rq<RQ_COPY, false>(logb); break;
+    case RQ_NORM: kern = q2 ? pick_rq<RQ_NORM, true>(logb) : pick_rq<RQ_NORM, false>(logb); break;
+    case RQ_SWIGLU: kern = pick_rq<RQ_SWIGLU, false>(logb); break;
+    case RQ_GNORM: kern = pick_rq<RQ_GNORM, false>(logb); break;
+    default: return fail(OURO_ERR_INVALID_ARG, "row_rotate_quant: prologue %d", pro);
+    }
+    if (!kern) return fail(OURO_ERR_SHAPE, "row_rotate_quant: block %zu", block);
+    const size_t lds = sizeof(float) * ((q2 ? 2 : 1) * (n + n / 16) + 16);
+    if (lds > 64 * 1024) return fail(OURO_ERR_SHAPE, "row_rotate_quant: len %zu needs %zu B of LDS", n, lds);
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(rows)), dim3(kThreads), lds, as_stream(stream), r);
+    return check_launch("row_rq_kernel");
 }
 
 }  // namespace ouro

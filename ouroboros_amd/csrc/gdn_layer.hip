@@ -101,6 +101,29 @@ size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv) {
     return align256(B * ch * 4) + 2 * align256(B * Hv * 4) + align256(B * Hv * kD * 4);
 }
 
+// run_delta's block up to the recurrence output: gates, conv + SiLU (ring
+// updated), normed recurrence into o[B][Hv][d] (no gated norm).  The
+// workspace holds conv_out, beta and gate (gdn_layer_ws_bytes).
+int gdn_decode_core(const float *qkv, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
+                    const float *a_log, const float *conv_w, float *conv, float *state, float *o, size_t B, size_t Hk,
+                    size_t Hv, unsigned flags, float eps, void *workspace, void *stream) {
+    const size_t ch = 2 * Hk * kD + Hv * kD;
+    unsigned char *ws = static_cast<unsigned char *>(workspace);
+    float *conv_out = reinterpret_cast<float *>(ws);
+    float *beta = reinterpret_cast<float *>(ws + align256(B * ch * 4));
+    float *gate = reinterpret_cast<float *>(ws + align256(B * ch * 4) + align256(B * Hv * 4));
+    const size_t n = B * ch > B * Hv ? B * ch : B * Hv;
+    hipLaunchKernelGGL(gdn_conv_gate_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), qkv, conv, conv_w, beta_raw, alpha_raw, dt_bias, a_log, conv_out, beta, gate,
+                       static_cast<int>(B), static_cast<int>(ch), static_cast<int>(Hv));
+    int st = check_launch("gdn_conv_gate_kernel");
+    if (st) return st;
+    const size_t di = Hk * kD;
+    return gdn_decode(state, conv_out, conv_out + di, OURO_DT_F32, conv_out + 2 * di, OURO_DT_F32, gate, beta, 0.f,
+                      0.f, o, B, Hk, Hv, kD, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | (flags & OURO_GDN_KHEAD_DIV), eps,
+                      stream, ch, ch);
+}
+
 int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,
                      const float *dt_bias, const float *a_log, const float *conv_w, const float *norm_w,
                      float *conv, float *state, float *out, size_t B, size_t Hk, size_t Hv, size_t d,
@@ -122,24 +145,13 @@ int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, co
         ws = static_cast<unsigned char *>(ouro::workspace(gdn_layer_ws_bytes(B, Hk, Hv), stream));
         if (!ws) return OURO_ERR_HIP;
     }
-    float *conv_out = reinterpret_cast<float *>(ws);
-    float *beta = reinterpret_cast<float *>(ws + align256(B * ch * 4));
-    float *gate = reinterpret_cast<float *>(ws + align256(B * ch * 4) + align256(B * Hv * 4));
     float *o = reinterpret_cast<float *>(ws + align256(B * ch * 4) + 2 * align256(B * Hv * 4));
-    hipStream_t s = as_stream(stream);
-    const size_t n = B * ch > B * Hv ? B * ch : B * Hv;
-    hipLaunchKernelGGL(gdn_conv_gate_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, qkv,
-                       conv, conv_w, beta_raw, alpha_raw, dt_bias, a_log, conv_out, beta, gate, static_cast<int>(B),
-                       static_cast<int>(ch), static_cast<int>(Hv));
-    int st = check_launch("gdn_conv_gate_kernel");
+    int st = gdn_decode_core(qkv, beta_raw, alpha_raw, dt_bias, a_log, conv_w, conv, state, o, B, Hk, Hv, flags, eps,
+                             ws, stream);
     if (st) return st;
-    const size_t di = Hk * kD;
-    st = gdn_decode(state, conv_out, conv_out + di, OURO_DT_F32, conv_out + 2 * di, OURO_DT_F32, gate, beta, 0.f,
-                    0.f, o, B, Hk, Hv, d, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | (flags & OURO_GDN_KHEAD_DIV), eps,
-                    stream, ch, ch);
-    if (st) return st;
-    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((B * Hv + 3) / 4)), dim3(256), 0, s, o, z,
-                       norm_w, out, static_cast<int>(B), static_cast<int>(Hk), static_cast<int>(Hv), flags, eps);
+    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((B * Hv + 3) / 4)), dim3(256), 0,
+                       as_stream(stream), o, z, norm_w, out, static_cast<int>(B), static_cast<int>(Hk),
+                       static_cast<int>(Hv), flags, eps);
     return check_launch("gdn_gated_norm_kernel");
 }
 

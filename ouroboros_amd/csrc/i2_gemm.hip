@@ -29,6 +29,8 @@ namespace {
 constexpr int kWave = 64;
 constexpr int kGemmWaves = 4;
 constexpr int kXPitch = 272;  // LDS bytes per activation row of a 256-k block
+constexpr int kSkinnyCols = 64;  // column counts up to this use the split-k kernel
+constexpr int kSkinnyWaves = 16; // its wavefronts per workgroup (one per k block; half for > 32 columns)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -70,6 +72,7 @@ struct GemmArgs {
     float *y;              // [N][M]
     int32_t *acc;          // optional, same layout as y
     int M, K, N, nkb, nrb;
+    int x_tiled;           // xq in the few-column fragment order (ceil(N/16) column tiles)
 };
 
 // Block: 4 wavefronts stacked along rows; wavefront w owns row tiles
@@ -178,6 +181,94 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
     }
 }
 
+// Few columns (N <= 64, e.g. one decode step of a batch of sequences): the
+// product is a weight stream, so every weight unit must be read once and
+// the k loop must not be a latency chain.  Workgroup = 2 row tiles (32 rows)
+// x all N columns, with one wavefront per k block (up to 16; beyond that
+// each wavefront takes every 16th block), so all of a workgroup's loads are
+// in flight at once.  Wavefronts read their activation fragments straight
+// from global memory (L2-resident: 16*WC rows of in_len bytes) and add their
+// int32 tiles into one LDS tile with integer atomics (exact, order-free).
+constexpr int skinny_waves(int wc) { return wc <= 2 ? kSkinnyWaves : kSkinnyWaves / 2; }
+
+template <int WC>
+__global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(GemmArgs a) {
+    constexpr int WR = 2, TR = 16 * WR, TC = 16 * WC + 1;
+    __shared__ int tile[TR * TC];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int rt0 = blockIdx.x * WR;
+    const int nrt = (a.M + 15) / 16;
+    for (int i = tid; i < TR * TC; i += blockDim.x) tile[i] = 0;
+    v4i acc[WR][WC];
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+#pragma unroll
+        for (int c = 0; c < WC; ++c) acc[r][c] = v4i{0, 0, 0, 0};
+    // Rows past M and columns past N are clamped to the last valid ones
+    // (unconditional loads, no branches between them); their sums land in
+    // tile rows / columns that the epilogue never stores.
+    // Row-major x: lane l of column tile c reads row 16c + l%16 (clamped),
+    // bytes 16*(l/16) of each 64-deep step.  Fragment-ordered x: one
+    // contiguous 1 KiB per (k block, step, column tile), 16 bytes per lane.
+    const int8_t *xr[WC];
+#pragma unroll
+    for (int c = 0; c < WC; ++c)
+        xr[c] = a.x_tiled ? a.xq + (static_cast<long long>(c) * kWave + lane) * 16
+                          : a.xq + static_cast<long long>(min(16 * c + (lane & 15), a.N - 1)) * a.K + 16 * (lane >> 4);
+    const long long xkb = a.x_tiled ? 4LL * WC * 1024 : 256, xs = a.x_tiled ? WC * 1024 : 64;
+    const uint4 *wp[WR];
+#pragma unroll
+    for (int r = 0; r < WR; ++r) wp[r] = a.w + static_cast<long long>(min(rt0 + r, nrt - 1)) * a.nkb * kWave + lane;
+    const int nl = lane & 15;
+    for (int kb = wave; kb < a.nkb; kb += nw) {
+        uint4 wr[WR];
+#pragma unroll
+        for (int r = 0; r < WR; ++r) wr[r] = wp[r][kb * kWave];
+        v4i B[WC][4];
+#pragma unroll
+        for (int c = 0; c < WC; ++c)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) B[c][s] = *reinterpret_cast<const v4i *>(xr[c] + xkb * kb + xs * s);
+        __builtin_amdgcn_sched_barrier(0);  // every load of the k block is issued before the first wait
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v4i A[WR];
+#pragma unroll
+            for (int r = 0; r < WR; ++r) {
+                const uint32_t wd = s == 0 ? wr[r].x : s == 1 ? wr[r].y : s == 2 ? wr[r].z : wr[r].w;
+                A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
+                           static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+            }
+#pragma unroll
+            for (int c = 0; c < WC; ++c)
+#pragma unroll
+                for (int r = 0; r < WR; ++r)
+                    acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B[c][s], acc[r][c], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // tile zeroed
+    // D lane l: rows 4*(l/16) + e of the row tile, column l % 16.
+    if (wave < a.nkb) {
+#pragma unroll
+        for (int r = 0; r < WR; ++r)
+#pragma unroll
+            for (int c = 0; c < WC; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    atomicAdd(&tile[(16 * r + 4 * (lane >> 4) + e) * TC + 16 * c + nl], acc[r][c][e]);
+    }
+    __syncthreads();
+    const float wscale = *a.w_scale;
+    for (int i = tid; i < TR * 16 * WC; i += blockDim.x) {
+        const int n = i / TR, rr = i % TR, row = rt0 * 16 + rr;
+        if (n >= a.N || row >= a.M) continue;
+        const int total = -(tile[rr * TC + n] >> 6);
+        const long long o = static_cast<long long>(n) * a.M + row;
+        a.y[o] = (static_cast<float>(total) * a.dscale[n]) * wscale;
+        if (a.acc) a.acc[o] = total;
+    }
+}
+
 using GemmFn = void (*)(GemmArgs);
 
 struct GemmPick {
@@ -200,6 +291,16 @@ GemmPick pick_gemm(int M, int N) {
     if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4>, 2, 4};
     if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2>, 2, 2};
     return {i2_gemm_mfma_kernel<1, 1>, 1, 1};
+}
+
+// Few-column launches: column tiles WC = ceil(N / 16) <= 4.
+GemmFn pick_skinny(int N) {
+    switch ((N + 15) / 16) {
+    case 1: return i2_gemm_skinny_kernel<1>;
+    case 2: return i2_gemm_skinny_kernel<2>;
+    case 3: return i2_gemm_skinny_kernel<3>;
+    default: return i2_gemm_skinny_kernel<4>;
+    }
 }
 
 int check_mfma_shape(size_t out_len, size_t in_len) {
@@ -235,7 +336,7 @@ int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_
 }
 
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream) {
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled) {
     int st = check_mfma_shape(out_len, in_len);
     if (st) return st;
     if (!w_mfma || !w_scale || !xq || !dscale || !y || !ncols)
@@ -254,6 +355,17 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     a.K = static_cast<int>(in_len);
     a.N = static_cast<int>(ncols);
     a.nkb = a.K / 256;
+    a.x_tiled = x_tiled;
+    if (x_tiled && ncols > static_cast<size_t>(kSkinnyCols))
+        return fail(OURO_ERR_SHAPE, "i2 gemm: fragment-ordered x is for <= %d columns", kSkinnyCols);
+    if (ncols <= static_cast<size_t>(kSkinnyCols)) {
+        const int maxw = skinny_waves((a.N + 15) / 16);
+        const int waves = a.nkb < maxw ? a.nkb : maxw;
+        const GemmFn fn = pick_skinny(a.N);
+        const long long blocks = ((a.M + 15) / 16 + 1) / 2;
+        hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kWave * waves), 0, as_stream(stream), a);
+        return check_launch("i2_gemm_skinny_kernel");
+    }
     const GemmPick p = pick_gemm(a.M, a.N);
     const int nrt = (a.M + 15) / 16;
     a.nrb = (nrt + kGemmWaves * p.wr - 1) / (kGemmWaves * p.wr);
@@ -280,7 +392,7 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, cons
                       const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc_or_null,
                       void *stream) {
     OURO_REQUIRE_INIT();
-    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream);
+    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0);
 }
 
 }  // extern "C"

@@ -20,29 +20,24 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
                  void *stream);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream);
-int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale, void *stream);
-int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, size_t n, size_t block,
-              const float *signs, unsigned flags, int8_t *xq, float *dscale, void *stream);
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled);
 size_t gdn_chunk_ws_bytes(size_t T, size_t N, size_t Hv);
 int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v, const float *gate,
                       const float *beta, float *out, const int32_t *cu_host, size_t N, size_t T, size_t Hk,
                       size_t Hv, size_t d, size_t chunk, unsigned flags, float eps, void *workspace, void *stream);
 size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv);
-int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,
-                     const float *dt_bias, const float *a_log, const float *conv_w, const float *norm_w,
-                     float *conv, float *state, float *out, size_t B, size_t Hk, size_t Hv, size_t d,
-                     unsigned flags, float eps, void *workspace, void *stream);
-int gdn_gated_norm(const float *o, const float *z, const float *norm_w, float *out, size_t rows, size_t Hk,
-                   size_t Hv, unsigned flags, float eps, void *stream);
+int gdn_decode_core(const float *qkv, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
+                    const float *a_log, const float *conv_w, float *conv, float *state, float *o, size_t B, size_t Hk,
+                    size_t Hv, unsigned flags, float eps, void *workspace, void *stream);
+int row_rotate_quant(int pro, const float *a, const float *b, const float *w, float *sum_out, size_t rows,
+                     size_t n, size_t block, const float *signs, int8_t *xq, float *ds, int8_t *xq2, float *ds2,
+                     int tiles, int Hk, int Hv, unsigned flags, float eps, void *stream);
+enum { RQ_COPY = 0, RQ_NORM = 1, RQ_SWIGLU = 2, RQ_GNORM = 3 };  // row_rotate_quant prologues (fwht.hip)
 // stack_ops.hip
 int fill_zero(float *p, size_t n, void *stream);
 int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, void *stream);
 int gen_codes(uint32_t seed, uint32_t tensor, size_t rows, size_t cols, uint8_t *dst, void *stream);
 int gen_floats(uint32_t seed, uint32_t tensor, size_t n, float lo, float span, float *dst, void *stream);
-int rmsnorm_rows(const float *a, const float *b, const float *w, float *sum_out, float *out, size_t rows, size_t n,
-                 float eps, void *stream);
-int swiglu(const float *gate, const float *up, float *out, size_t n, void *stream);
 int embed_rows(const int32_t *tokens, const float *table, float *x, size_t n_tok, size_t n_vocab, size_t n_embd,
                void *stream);
 int gather_rows(const float *src, const int32_t *rows_idx, float *dst, size_t n, size_t width, void *stream);
@@ -117,12 +112,12 @@ struct ouro_stack {
     Lin lm;
     float *sign_e = nullptr, *sign_ff = nullptr, *sign_di = nullptr, *sign_q = nullptr;
     // activations, rows = max(max_tokens, max_seqs)
-    float *x = nullptr, *h = nullptr, *pre = nullptr, *f = nullptr, *mix = nullptr;
+    float *x = nullptr, *pre = nullptr, *mix = nullptr;
     float *big = nullptr, *big2 = nullptr, *zb = nullptr, *braw = nullptr, *araw = nullptr;
     float *o = nullptr, *g = nullptr, *qbuf = nullptr, *gbuf = nullptr, *kbuf = nullptr, *vbuf = nullptr;
-    float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *lmx = nullptr, *hl = nullptr, *logits = nullptr;
-    int8_t *xq = nullptr;
-    float *ds = nullptr;
+    float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *lmx = nullptr, *logits = nullptr;
+    int8_t *xq = nullptr, *xq2 = nullptr;  // rotated activations; unrotated h for beta / alpha
+    float *ds = nullptr, *ds2 = nullptr;
     uint16_t *qb = nullptr, *kb = nullptr, *vb = nullptr;
     float *beta = nullptr, *gate = nullptr;
     int32_t *pos = nullptr, *seqid = nullptr, *cu = nullptr, *tile_seq = nullptr, *tile_p0 = nullptr;
@@ -178,13 +173,25 @@ int make_vec(ouro_stack *s, float **p, uint32_t tensor, size_t n, float lo, floa
     return gen_floats(s->seed, tensor, n, lo, span, *p, nullptr);
 }
 
-// Rotate rows x n (signs of that width) and quantise into s->xq / s->ds.
-int rq(ouro_stack *s, const float *x, size_t rows, size_t n, const float *signs, void *stream) {
-    return fwht_rows(x, OURO_DT_F32, nullptr, OURO_DT_F32, rows, n, rot_block(n), signs, 0u, s->xq, s->ds, stream);
+// Launches of at most this many activation rows (decode steps, heads of a
+// few sequences) pass the int8 activations in the few-column GEMM's
+// fragment order; longer ones row-major.
+constexpr size_t kFragRows = 64;
+int frag_tiles(size_t rows) { return rows <= kFragRows ? static_cast<int>((rows + 15) / 16) : 0; }
+
+// y[cols][L.out] = L x (int8 activations xq/ds of `cols` rows, as produced
+// for the same row count).
+int lin(const Lin &L, size_t cols, const int8_t *xq, const float *ds, float *y, void *stream) {
+    return i2_gemm_mfma(L.w, L.out, L.in, L.scale, xq, ds, cols, y, nullptr, stream, frag_tiles(cols) ? 1 : 0);
 }
 
-int lin(ouro_stack *s, const Lin &L, size_t cols, float *y, void *stream) {
-    return i2_gemm_mfma(L.w, L.out, L.in, L.scale, s->xq, s->ds, cols, y, nullptr, stream);
+// Prologue + Hadamard rotation (signs of width n) + int8 absmax into s->xq / s->ds.
+int rq(ouro_stack *s, int pro, const float *a, const float *b, const float *w, float *sum_out, size_t rows, size_t n,
+       const float *signs, void *stream, bool also_plain = false) {
+    const ouro_stack_card &c = s->c;
+    return row_rotate_quant(pro, a, b, w, sum_out, rows, n, rot_block(n), signs, s->xq, s->ds,
+                            also_plain ? s->xq2 : nullptr, also_plain ? s->ds2 : nullptr, frag_tiles(rows),
+                            c.ssm_n_k_heads, c.ssm_n_v_heads, OURO_GDN_V_GROUPED, c.eps, stream);
 }
 
 #define TRY(expr)              \
@@ -201,17 +208,17 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     const ouro_stack_card &c = s->c;
     const size_t Hk = c.ssm_n_k_heads, Hv = c.ssm_n_v_heads;
     // h = rmsnorm(x) * attn_norm, where x = pre + mix of the previous layer
-    if (il == 0)
-        TRY(rmsnorm_rows(s->x, nullptr, L.attn_norm, nullptr, s->h, rows, s->E, c.eps, stream));
-    else
-        TRY(rmsnorm_rows(s->pre, s->mix, L.attn_norm, s->x, s->h, rows, s->E, c.eps, stream));
+    // (stored), rotated and quantised; delta layers also quantise h itself
+    // for the beta and alpha projections (qwen35.rs:1058-1065)
+    const float *xa = il == 0 ? s->x : s->pre;
+    const float *xb = il == 0 ? nullptr : s->mix;
+    float *xsum = il == 0 ? nullptr : s->x;
+    TRY(rq(s, RQ_NORM, xa, xb, L.attn_norm, xsum, rows, s->E, s->sign_e, stream, L.delta));
     if (L.delta) {
-        TRY(rq(s, s->h, rows, s->E, s->sign_e, stream));
-        TRY(lin(s, L.qkv, rows, s->big, stream));
-        TRY(lin(s, L.z, rows, s->zb, stream));
-        TRY(act_quant(s->h, OURO_DT_F32, rows, s->E, s->xq, s->ds, stream));  // beta, alpha: unrotated h
-        TRY(lin(s, L.beta, rows, s->braw, stream));
-        TRY(lin(s, L.alpha, rows, s->araw, stream));
+        TRY(lin(L.qkv, rows, s->xq, s->ds, s->big, stream));
+        TRY(lin(L.z, rows, s->xq, s->ds, s->zb, stream));
+        TRY(lin(L.beta, rows, s->xq2, s->ds2, s->braw, stream));
+        TRY(lin(L.alpha, rows, s->xq2, s->ds2, s->araw, stream));
         if (prefill) {
             TRY(prefill_conv_gate(s->big, L.ring, L.conv_w, s->seqid, s->pos, s->braw, s->araw, L.dt_bias, L.a_log,
                                   s->qb, s->kb, s->vb, s->beta, s->gate, rows, static_cast<int>(s->ch),
@@ -219,18 +226,17 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
             TRY(ring_update(s->big, L.ring, s->cu, N, static_cast<int>(s->ch), stream));
             TRY(gdn_chunk_prefill(L.state, s->qb, s->kb, s->vb, s->gate, s->beta, s->o, cu_host, N, rows, Hk, Hv,
                                   kHd, 64, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q, c.eps, s->ws, stream));
-            TRY(gdn_gated_norm(s->o, s->zb, L.ssm_norm, s->g, rows, Hk, Hv, OURO_GDN_V_GROUPED, c.eps, stream));
         } else {
-            TRY(gdn_layer_decode(s->big, s->zb, s->braw, s->araw, L.dt_bias, L.a_log, L.conv_w, L.ssm_norm, L.ring,
-                                 L.state, s->g, rows, Hk, Hv, kHd, OURO_GDN_V_GROUPED, c.eps, s->ws, stream));
+            TRY(gdn_decode_core(s->big, s->braw, s->araw, L.dt_bias, L.a_log, L.conv_w, L.ring, L.state, s->o, rows,
+                                Hk, Hv, 0u, c.eps, s->ws, stream));
         }
-        TRY(rq(s, s->g, rows, s->dv, s->sign_di, stream));
-        TRY(lin(s, L.out, rows, s->mix, stream));
+        // gated RMS norm per head in the V-grouped order, rotated, quantised
+        TRY(rq(s, RQ_GNORM, s->o, s->zb, L.ssm_norm, nullptr, rows, s->dv, s->sign_di, stream));
+        TRY(lin(L.out, rows, s->xq, s->ds, s->mix, stream));
     } else {
-        TRY(rq(s, s->h, rows, s->E, s->sign_e, stream));
-        TRY(lin(s, L.q, rows, s->big, stream));
-        TRY(lin(s, L.k, rows, s->kbuf, stream));
-        TRY(lin(s, L.v, rows, s->vbuf, stream));
+        TRY(lin(L.q, rows, s->xq, s->ds, s->big, stream));
+        TRY(lin(L.k, rows, s->xq, s->ds, s->kbuf, stream));
+        TRY(lin(L.v, rows, s->xq, s->ds, s->vbuf, stream));
         TRY(attn_prep(s->big, s->kbuf, s->vbuf, L.qn, L.kn, s->pos, prefill ? s->seqid : s->dec_seq, s->base,
                       s->qbuf, s->gbuf, L.kc, L.vc, rows, c.n_head, c.n_head_kv, c.n_rot, c.rope_base, c.eps,
                       stream));
@@ -240,17 +246,15 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
         else
             TRY(attn_decode(s->qbuf, s->gbuf, L.kc, L.vc, s->base, s->klen, rows, s->max_len, s->attn_o, c.n_head,
                             c.n_head_kv, s->attn_part, stream));
-        TRY(rq(s, s->attn_o, rows, s->qdim, s->sign_q, stream));
-        TRY(lin(s, L.o, rows, s->mix, stream));
+        TRY(rq(s, RQ_COPY, s->attn_o, nullptr, nullptr, nullptr, rows, s->qdim, s->sign_q, stream));
+        TRY(lin(L.o, rows, s->xq, s->ds, s->mix, stream));
     }
-    // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = FFN(f)
-    TRY(rmsnorm_rows(s->x, s->mix, L.post_norm, s->pre, s->f, rows, s->E, c.eps, stream));
-    TRY(rq(s, s->f, rows, s->E, s->sign_e, stream));
-    TRY(lin(s, L.up, rows, s->big, stream));
-    TRY(lin(s, L.gate, rows, s->big2, stream));
-    TRY(swiglu(s->big2, s->big, s->big, rows * s->F, stream));
-    TRY(rq(s, s->big, rows, s->F, s->sign_ff, stream));
-    TRY(lin(s, L.down, rows, s->mix, stream));
+    // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = down(silu(gate f) * up f)
+    TRY(rq(s, RQ_NORM, s->x, s->mix, L.post_norm, s->pre, rows, s->E, s->sign_e, stream));
+    TRY(lin(L.up, rows, s->xq, s->ds, s->big, stream));
+    TRY(lin(L.gate, rows, s->xq, s->ds, s->big2, stream));
+    TRY(rq(s, RQ_SWIGLU, s->big2, s->big, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
+    TRY(lin(L.down, rows, s->xq, s->ds, s->mix, stream));
     return OURO_OK;
 }
 
@@ -258,22 +262,22 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
 int head(ouro_stack *s, const int32_t *rows_idx, size_t n, int32_t *next, float *logits_out, void *stream) {
     TRY(gather_rows(s->pre, rows_idx, s->lp, n, s->E, stream));
     TRY(gather_rows(s->mix, rows_idx, s->lmx, n, s->E, stream));
-    TRY(rmsnorm_rows(s->lp, s->lmx, s->out_norm, nullptr, s->hl, n, s->E, s->c.eps, stream));
-    TRY(rq(s, s->hl, n, s->E, s->sign_e, stream));
+    TRY(rq(s, RQ_NORM, s->lp, s->lmx, s->out_norm, nullptr, n, s->E, s->sign_e, stream));
     float *lg = logits_out ? logits_out : s->logits;
-    TRY(lin(s, s->lm, n, lg, stream));
+    TRY(lin(s->lm, n, s->xq, s->ds, lg, stream));
     return argmax_rows(lg, n, s->V, next, stream);
 }
 
 int check_card(const ouro_stack_card &c) {
-    if (c.n_layer < 1 || c.n_embd < 256 || c.n_embd % 256 || c.n_ff < 256 || c.n_ff % 256 || c.n_vocab < 1 ||
-        c.full_attention_interval < 1)
-        return fail(OURO_ERR_SHAPE, "ouro_stack: bad sizes (n_embd and n_ff multiples of 256)");
+    if (c.n_layer < 1 || c.n_embd < 256 || c.n_embd % 256 || c.n_embd > 6144 || c.n_ff < 256 || c.n_ff % 256 ||
+        c.n_ff > 12288 || c.n_vocab < 1 || c.full_attention_interval < 1)
+        return fail(OURO_ERR_SHAPE, "ouro_stack: bad sizes (n_embd <= 6144 and n_ff <= 12288, multiples of 256)");
     if (c.head_dim != kHd || c.ssm_d_state != kHd) return fail(OURO_ERR_SHAPE, "ouro_stack: head_dim and d_state must be 128");
     if (c.n_head < 2 || c.n_head % 2 || c.n_head_kv < 1 || c.n_head % c.n_head_kv || c.n_head / c.n_head_kv > 8)
         return fail(OURO_ERR_SHAPE, "ouro_stack: n_head even, a multiple of n_head_kv, at most 8 per kv head");
     if (c.n_rot < 0 || c.n_rot > kHd || c.n_rot % 4) return fail(OURO_ERR_SHAPE, "ouro_stack: n_rot");
-    if (c.ssm_n_k_heads < 1 || c.ssm_n_v_heads % 2 || c.ssm_n_v_heads % c.ssm_n_k_heads)
+    if (c.ssm_n_k_heads < 1 || c.ssm_n_v_heads % 2 || c.ssm_n_v_heads % c.ssm_n_k_heads || c.ssm_n_v_heads > 96 ||
+        c.n_head > 96)
         return fail(OURO_ERR_SHAPE, "ouro_stack: ssm heads (n_v_heads even, a multiple of n_k_heads)");
     if (static_cast<size_t>(c.n_vocab) * c.n_embd >= (1ull << 32)) return fail(OURO_ERR_SHAPE, "ouro_stack: vocab too large");
     return OURO_OK;
@@ -369,8 +373,9 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         return done(st);
     const size_t xw = std::max({E, F, s->dv, s->qdim});
     const size_t tiles = max_tokens / 64 + max_seqs + 1;
-    if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->h, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) ||
-        (st = dalloc(s, &s->f, rows * E)) || (st = dalloc(s, &s->mix, rows * E)) ||
+    // int8 activations of a few-row launch are padded to whole 16-row tiles
+    const size_t qrows = std::max(rows, (max_seqs + 15) / 16 * 16);
+    if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) || (st = dalloc(s, &s->mix, rows * E)) ||
         (st = dalloc(s, &s->big, rows * wide)) || (st = dalloc(s, &s->big2, rows * F)) ||
         (st = dalloc(s, &s->zb, rows * s->dv)) || (st = dalloc(s, &s->braw, rows * c.ssm_n_v_heads)) ||
         (st = dalloc(s, &s->araw, rows * c.ssm_n_v_heads)) || (st = dalloc(s, &s->o, rows * s->dv)) ||
@@ -378,8 +383,8 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         (st = dalloc(s, &s->gbuf, rows * s->qdim)) || (st = dalloc(s, &s->kbuf, rows * s->kvdim)) ||
         (st = dalloc(s, &s->vbuf, rows * s->kvdim)) || (st = dalloc(s, &s->attn_o, rows * s->qdim)) ||
         (st = dalloc(s, &s->lp, max_seqs * E)) || (st = dalloc(s, &s->lmx, max_seqs * E)) ||
-        (st = dalloc(s, &s->hl, max_seqs * E)) || (st = dalloc(s, &s->logits, max_seqs * V)) ||
-        (st = dalloc(s, &s->xq, rows * xw)) || (st = dalloc(s, &s->ds, rows)) ||
+        (st = dalloc(s, &s->logits, max_seqs * V)) || (st = dalloc(s, &s->xq, qrows * xw)) ||
+        (st = dalloc(s, &s->ds, qrows)) || (st = dalloc(s, &s->xq2, qrows * E)) || (st = dalloc(s, &s->ds2, qrows)) ||
         (st = dalloc(s, &s->qb, rows * s->di)) || (st = dalloc(s, &s->kb, rows * s->di)) ||
         (st = dalloc(s, &s->vb, rows * s->dv)) || (st = dalloc(s, &s->beta, rows * c.ssm_n_v_heads)) ||
         (st = dalloc(s, &s->gate, rows * c.ssm_n_v_heads)) || (st = dalloc(s, &s->pos, rows)) ||

@@ -1,14 +1,15 @@
 // stack_ops.hip - the device operations of a Qwen3.5-style hybrid decoder
-// stack that the hot-path kernels do not already cover: RMS norm with the
-// residual add, SwiGLU, the attention block's per-head norm + partial NEOX
-// rope + KV append, causal attention over a packed varlen batch (prefill)
-// and over each sequence's cache (decode), the delta-net block's causal
-// conv + gates over a packed varlen batch, embedding lookup, per-row
-// finite_argmax and the seeded synthetic weights.
+// stack that the hot-path kernels do not already cover: the attention
+// block's per-head norm + partial NEOX rope + KV append, causal attention
+// over a packed varlen batch (prefill) and over each sequence's cache
+// (decode), the delta-net block's causal conv + gates over a packed varlen
+// batch, embedding lookup, per-row finite_argmax and the seeded synthetic
+// weights.  (RMS norm, SwiGLU and the gated norm run fused ahead of the
+// activation rotation, fwht.hip.)
 //
 // Reference semantics followed: run_layer (qwen35.rs:776-795), run_ffn
 // (798-805), run_attn (1160-1215) with attn_head (1227-1240), run_delta's
-// conv and gates (1066-1088), rmsnorm/silu/softmax (ops.rs:12-17, 34-48),
+// conv and gates (1066-1088), silu/softmax (ops.rs:34-48),
 // rope_partial_neox (qwen35.rs:96-106).
 #include "common.hpp"
 
@@ -63,47 +64,7 @@ __global__ void gen_floats_kernel(uint32_t seed, uint32_t tensor, long long n, f
     dst[i] = lo + span * u;
 }
 
-// ----------------------------------------------------------------- norms --
-
-__device__ __forceinline__ float block_sum_256(float v, float *red) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float t = red[0] + red[1] + red[2] + red[3];
-    __syncthreads();
-    return t;
-}
-
-// One 256-thread block per row: s = a (+ b), optionally stored, then
-// out = s * inv * w with inv = 1 / sqrt(mean(s^2) + eps) (ops.rs:12-17).
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const float *a, const float *b, const float *w, float *sum_out,
-                                                      float *out, int n, float eps) {
-    __shared__ float red[4];
-    const long long row = blockIdx.x;
-    const float *ar = a + row * n;
-    const float *br = b ? b + row * n : nullptr;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float s = br ? ar[i] + br[i] : ar[i];
-        ss += s * s;
-    }
-    const float ms = block_sum_256(ss, red) / static_cast<float>(n);
-    const float inv = 1.0f / sqrtf(ms + eps);
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float s = br ? ar[i] + br[i] : ar[i];
-        if (sum_out) sum_out[row * n + i] = s;
-        out[row * n + i] = s * inv * w[i];
-    }
-}
-
-// act = silu(gate) * up (run_ffn, qwen35.rs:802).
-__global__ void swiglu_kernel(const float *gate, const float *up, float *out, long long n) {
-    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float g = gate[i];
-    out[i] = g / (1.0f + expf(-g)) * up[i];
-}
+// -------------------------------------------------------------- embedding --
 
 // Token rows -> embedding rows (ids clamped into the table).
 __global__ void embed_kernel(const int32_t *tokens, const float *table, float *x, int n_tok, int n_vocab, int n_embd) {
@@ -609,20 +570,6 @@ int gen_floats(uint32_t seed, uint32_t tensor, size_t n, float lo, float span, f
     hipLaunchKernelGGL(gen_floats_kernel, dim3(blocks_for(static_cast<long long>(n), 256)), dim3(256), 0,
                        as_stream(stream), seed, tensor, static_cast<long long>(n), lo, span, dst);
     return check_launch("gen_floats_kernel");
-}
-
-int rmsnorm_rows(const float *a, const float *b, const float *w, float *sum_out, float *out, size_t rows, size_t n,
-                 float eps, void *stream) {
-    if (!rows) return OURO_OK;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, as_stream(stream), a, b, w,
-                       sum_out, out, static_cast<int>(n), eps);
-    return check_launch("rmsnorm_kernel");
-}
-
-int swiglu(const float *gate, const float *up, float *out, size_t n, void *stream) {
-    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(static_cast<long long>(n), 256)), dim3(256), 0,
-                       as_stream(stream), gate, up, out, static_cast<long long>(n));
-    return check_launch("swiglu_kernel");
 }
 
 int embed_rows(const int32_t *tokens, const float *table, float *x, size_t n_tok, size_t n_vocab, size_t n_embd,

@@ -21,7 +21,7 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
                  void *stream);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream);
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled);
 int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale, void *stream);
 size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
@@ -208,7 +208,7 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         const float *w_scale =
             reinterpret_cast<const float *>(static_cast<const uint8_t *>(w->payload) + i2_tiled_bytes(w->out_len, w->in_len));
         return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->dscale,
-                            k, y, nullptr, stream);
+                            k, y, nullptr, stream, 0);
     }
     return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->dscale, stream);
 }
