@@ -102,6 +102,19 @@ __device__ __forceinline__ T reduce_scatter(T (&v)[N], int lane) {
 constexpr int kArgmaxBlocks = 1024;
 int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *stream);
 
+// One ternary x int8 product of a grouped few-column launch (i2_gemm.hip):
+// MFMA-tiled weights w with out_len rows, activations xq/dscale, y[ncols][out_len].
+struct GemmProblem {
+    const uint8_t *w;
+    size_t out_len;
+    const float *w_scale;
+    const int8_t *xq;
+    const float *dscale;
+    float *y;
+    int32_t *acc;  // optional exact int32 sums
+};
+int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream);
+
 // finite_argmax keys (infer/mod.rs:70-83): the value's bits in an
 // order-preserving form (-0 taken as +0, as `>` does) in the high word, the
 // complement of the index in the low word (the lowest index wins a tie), 0

@@ -31,6 +31,7 @@ constexpr int kGemmWaves = 4;
 constexpr int kXPitch = 272;  // LDS bytes per activation row of a 256-k block
 constexpr int kSkinnyCols = 64;  // column counts up to this use the split-k kernel
 constexpr int kSkinnyWaves = 16; // its wavefronts per workgroup (one per k block; half for > 32 columns)
+constexpr int kSkinnyGroup = 4;  // products per grouped launch
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -191,12 +192,42 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
 // int32 tiles into one LDS tile with integer atomics (exact, order-free).
 constexpr int skinny_waves(int wc) { return wc <= 2 ? kSkinnyWaves : kSkinnyWaves / 2; }
 
+// Up to kSkinnyGroup products with the same k and column count share one
+// launch (the projections of one activation): workgroups
+// bstart[p] .. bstart[p+1]-1 belong to product p.
+struct SkinnyProblem {
+    const uint4 *w;
+    const float *w_scale;
+    const int8_t *xq;
+    const float *dscale;
+    float *y;
+    int32_t *acc;
+    int M;
+};
+struct SkinnyGroup {
+    SkinnyProblem p[kSkinnyGroup];
+    int bstart[kSkinnyGroup + 1];
+    int np, K, N, nkb, x_tiled;
+};
+
 template <int WC>
-__global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(GemmArgs a) {
+__global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(SkinnyGroup g) {
     constexpr int WR = 2, TR = 16 * WR, TC = 16 * WC + 1;
     __shared__ int tile[TR * TC];
+    int pi = 0;
+    while (pi + 1 < g.np && static_cast<int>(blockIdx.x) >= g.bstart[pi + 1]) ++pi;
+    const SkinnyProblem &pb = g.p[pi];
+    struct {
+        const uint4 *w;
+        const float *w_scale;
+        const int8_t *xq;
+        const float *dscale;
+        float *y;
+        int32_t *acc;
+        int M, K, N, nkb, x_tiled;
+    } a{pb.w, pb.w_scale, pb.xq, pb.dscale, pb.y, pb.acc, pb.M, g.K, g.N, g.nkb, g.x_tiled};
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    const int rt0 = blockIdx.x * WR;
+    const int rt0 = (static_cast<int>(blockIdx.x) - g.bstart[pi]) * WR;
     const int nrt = (a.M + 15) / 16;
     for (int i = tid; i < TR * TC; i += blockDim.x) tile[i] = 0;
     v4i acc[WR][WC];
@@ -270,6 +301,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
 }
 
 using GemmFn = void (*)(GemmArgs);
+using SkinnyFn = void (*)(SkinnyGroup);
 
 struct GemmPick {
     GemmFn fn;
@@ -294,7 +326,7 @@ GemmPick pick_gemm(int M, int N) {
 }
 
 // Few-column launches: column tiles WC = ceil(N / 16) <= 4.
-GemmFn pick_skinny(int N) {
+SkinnyFn pick_skinny(int N) {
     switch ((N + 15) / 16) {
     case 1: return i2_gemm_skinny_kernel<1>;
     case 2: return i2_gemm_skinny_kernel<2>;
@@ -335,6 +367,42 @@ int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_
     return check_launch("copy_scale_mfma_kernel");
 }
 
+// Up to 4 few-column products of the same activations (k = in_len, ncols
+// <= 64 columns, each with its own weights, activations, scales and
+// output) in one launch.
+int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream) {
+    if (np < 1 || np > kSkinnyGroup) return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: %d products", np);
+    if (!ncols || ncols > static_cast<size_t>(kSkinnyCols))
+        return fail(OURO_ERR_SHAPE, "i2 gemm group: %zu columns (1..%d)", ncols, kSkinnyCols);
+    SkinnyGroup g{};
+    g.np = np;
+    g.K = static_cast<int>(in_len);
+    g.N = static_cast<int>(ncols);
+    g.nkb = g.K / 256;
+    g.x_tiled = x_tiled;
+    long long blocks = 0;
+    for (int i = 0; i < np; ++i) {
+        const GemmProblem &p = probs[i];
+        int st = check_mfma_shape(p.out_len, in_len);
+        if (st) return st;
+        if (!p.w || !p.w_scale || !p.xq || !p.dscale || !p.y)
+            return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: NULL argument in product %d", i);
+        if (reinterpret_cast<uintptr_t>(p.w) % 16 || reinterpret_cast<uintptr_t>(p.xq) % 16)
+            return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
+        g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.dscale, p.y, p.acc,
+                               static_cast<int>(p.out_len)};
+        g.bstart[i] = static_cast<int>(blocks);
+        blocks += (static_cast<long long>(p.out_len + 15) / 16 + 1) / 2;
+    }
+    g.bstart[np] = static_cast<int>(blocks);
+    if (blocks > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "i2 gemm group: grid too large");
+    const int maxw = skinny_waves((g.N + 15) / 16);
+    const int waves = g.nkb < maxw ? g.nkb : maxw;
+    hipLaunchKernelGGL(pick_skinny(g.N), dim3(static_cast<unsigned>(blocks)), dim3(kWave * waves), 0,
+                       as_stream(stream), g);
+    return check_launch("i2_gemm_skinny_kernel");
+}
+
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
                  const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled) {
     int st = check_mfma_shape(out_len, in_len);
@@ -359,12 +427,8 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     if (x_tiled && ncols > static_cast<size_t>(kSkinnyCols))
         return fail(OURO_ERR_SHAPE, "i2 gemm: fragment-ordered x is for <= %d columns", kSkinnyCols);
     if (ncols <= static_cast<size_t>(kSkinnyCols)) {
-        const int maxw = skinny_waves((a.N + 15) / 16);
-        const int waves = a.nkb < maxw ? a.nkb : maxw;
-        const GemmFn fn = pick_skinny(a.N);
-        const long long blocks = ((a.M + 15) / 16 + 1) / 2;
-        hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kWave * waves), 0, as_stream(stream), a);
-        return check_launch("i2_gemm_skinny_kernel");
+        const GemmProblem one{w_mfma, out_len, w_scale, xq, dscale, y, acc};
+        return i2_gemm_skinny_group(&one, 1, in_len, ncols, x_tiled, stream);
     }
     const GemmPick p = pick_gemm(a.M, a.N);
     const int nrt = (a.M + 15) / 16;

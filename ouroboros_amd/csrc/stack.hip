@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <initializer_list>
 #include <new>
 #include <vector>
 
@@ -55,7 +56,8 @@ int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, 
                       const float *a_log, uint16_t *qb, uint16_t *kb, uint16_t *vb, float *beta, float *gate,
                       size_t T, int ch, int di, int Hv, void *stream);
 int ring_update(const float *qkv, float *ring, const int32_t *cu, size_t N, int ch, void *stream);
-int argmax_rows(const float *y, size_t rows, size_t n, int32_t *idx, void *stream);
+size_t argmax_rows_ws_bytes(size_t rows, size_t n);
+int argmax_rows(const float *y, size_t rows, size_t n, int32_t *idx, unsigned long long *keys, void *stream);
 }  // namespace ouro
 
 using namespace ouro;
@@ -123,6 +125,7 @@ struct ouro_stack {
     int32_t *pos = nullptr, *seqid = nullptr, *cu = nullptr, *tile_seq = nullptr, *tile_p0 = nullptr;
     int32_t *lens = nullptr, *klen = nullptr, *last_rows = nullptr, *dec_seq = nullptr;
     long long *base = nullptr;
+    unsigned long long *arg_keys = nullptr;  // argmax chunk keys of the head rows
     void *ws = nullptr;
     // host staging (pinned) for the per-prefill index arrays
     int32_t *host_i32 = nullptr;
@@ -173,6 +176,12 @@ int make_vec(ouro_stack *s, float **p, uint32_t tensor, size_t n, float lo, floa
     return gen_floats(s->seed, tensor, n, lo, span, *p, nullptr);
 }
 
+#define TRY(expr)              \
+    do {                       \
+        const int st_ = (expr); \
+        if (st_) return st_;   \
+    } while (0)
+
 // Launches of at most this many activation rows (decode steps, heads of a
 // few sequences) pass the int8 activations in the few-column GEMM's
 // fragment order; longer ones row-major.
@@ -185,6 +194,25 @@ int lin(const Lin &L, size_t cols, const int8_t *xq, const float *ds, float *y, 
     return i2_gemm_mfma(L.w, L.out, L.in, L.scale, xq, ds, cols, y, nullptr, stream, frag_tiles(cols) ? 1 : 0);
 }
 
+// Several projections of the same activation rows: one grouped launch for
+// a few rows, else one launch each.
+struct LinOp {
+    const Lin *L;
+    const int8_t *xq;
+    const float *ds;
+    float *y;
+};
+int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
+    if (!frag_tiles(cols)) {
+        for (const LinOp &o : ops) TRY(lin(*o.L, cols, o.xq, o.ds, o.y, stream));
+        return OURO_OK;
+    }
+    GemmProblem p[4];
+    int np = 0;
+    for (const LinOp &o : ops) p[np++] = GemmProblem{o.L->w, o.L->out, o.L->scale, o.xq, o.ds, o.y, nullptr};
+    return i2_gemm_skinny_group(p, np, ops.begin()->L->in, cols, 1, stream);
+}
+
 // Prologue + Hadamard rotation (signs of width n) + int8 absmax into s->xq / s->ds.
 int rq(ouro_stack *s, int pro, const float *a, const float *b, const float *w, float *sum_out, size_t rows, size_t n,
        const float *signs, void *stream, bool also_plain = false) {
@@ -194,11 +222,6 @@ int rq(ouro_stack *s, int pro, const float *a, const float *b, const float *w, f
                             c.ssm_n_k_heads, c.ssm_n_v_heads, OURO_GDN_V_GROUPED, c.eps, stream);
 }
 
-#define TRY(expr)              \
-    do {                       \
-        const int st_ = (expr); \
-        if (st_) return st_;   \
-    } while (0)
 
 // Mixer + FFN of one layer over `rows` token rows; x is the layer input (the
 // residual stream), the layer's output is pre + mix.
@@ -215,10 +238,9 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     float *xsum = il == 0 ? nullptr : s->x;
     TRY(rq(s, RQ_NORM, xa, xb, L.attn_norm, xsum, rows, s->E, s->sign_e, stream, L.delta));
     if (L.delta) {
-        TRY(lin(L.qkv, rows, s->xq, s->ds, s->big, stream));
-        TRY(lin(L.z, rows, s->xq, s->ds, s->zb, stream));
-        TRY(lin(L.beta, rows, s->xq2, s->ds2, s->braw, stream));
-        TRY(lin(L.alpha, rows, s->xq2, s->ds2, s->araw, stream));
+        TRY(lin_group({{&L.qkv, s->xq, s->ds, s->big}, {&L.z, s->xq, s->ds, s->zb},
+                       {&L.beta, s->xq2, s->ds2, s->braw}, {&L.alpha, s->xq2, s->ds2, s->araw}},
+                      rows, stream));
         if (prefill) {
             TRY(prefill_conv_gate(s->big, L.ring, L.conv_w, s->seqid, s->pos, s->braw, s->araw, L.dt_bias, L.a_log,
                                   s->qb, s->kb, s->vb, s->beta, s->gate, rows, static_cast<int>(s->ch),
@@ -234,9 +256,8 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
         TRY(rq(s, RQ_GNORM, s->o, s->zb, L.ssm_norm, nullptr, rows, s->dv, s->sign_di, stream));
         TRY(lin(L.out, rows, s->xq, s->ds, s->mix, stream));
     } else {
-        TRY(lin(L.q, rows, s->xq, s->ds, s->big, stream));
-        TRY(lin(L.k, rows, s->xq, s->ds, s->kbuf, stream));
-        TRY(lin(L.v, rows, s->xq, s->ds, s->vbuf, stream));
+        TRY(lin_group({{&L.q, s->xq, s->ds, s->big}, {&L.k, s->xq, s->ds, s->kbuf}, {&L.v, s->xq, s->ds, s->vbuf}},
+                      rows, stream));
         TRY(attn_prep(s->big, s->kbuf, s->vbuf, L.qn, L.kn, s->pos, prefill ? s->seqid : s->dec_seq, s->base,
                       s->qbuf, s->gbuf, L.kc, L.vc, rows, c.n_head, c.n_head_kv, c.n_rot, c.rope_base, c.eps,
                       stream));
@@ -251,8 +272,7 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     }
     // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = down(silu(gate f) * up f)
     TRY(rq(s, RQ_NORM, s->x, s->mix, L.post_norm, s->pre, rows, s->E, s->sign_e, stream));
-    TRY(lin(L.up, rows, s->xq, s->ds, s->big, stream));
-    TRY(lin(L.gate, rows, s->xq, s->ds, s->big2, stream));
+    TRY(lin_group({{&L.up, s->xq, s->ds, s->big}, {&L.gate, s->xq, s->ds, s->big2}}, rows, stream));
     TRY(rq(s, RQ_SWIGLU, s->big2, s->big, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
     TRY(lin(L.down, rows, s->xq, s->ds, s->mix, stream));
     return OURO_OK;
@@ -265,7 +285,7 @@ int head(ouro_stack *s, const int32_t *rows_idx, size_t n, int32_t *next, float 
     TRY(rq(s, RQ_NORM, s->lp, s->lmx, s->out_norm, nullptr, n, s->E, s->sign_e, stream));
     float *lg = logits_out ? logits_out : s->logits;
     TRY(lin(s->lm, n, s->xq, s->ds, lg, stream));
-    return argmax_rows(lg, n, s->V, next, stream);
+    return argmax_rows(lg, n, s->V, next, s->arg_keys, stream);
 }
 
 int check_card(const ouro_stack_card &c) {
@@ -397,7 +417,8 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
     const size_t wsb = std::max(gdn_chunk_ws_bytes(max_tokens, max_seqs, c.ssm_n_v_heads),
                                 gdn_layer_ws_bytes(max_seqs, c.ssm_n_k_heads, c.ssm_n_v_heads));
     if ((st = dalloc(s, reinterpret_cast<uint8_t **>(&s->ws), wsb)) ||
-        (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->attn_part), attn_decode_ws_bytes(max_seqs, c.n_head, max_ctx))))
+        (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->attn_part), attn_decode_ws_bytes(max_seqs, c.n_head, max_ctx))) ||
+        (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->arg_keys), argmax_rows_ws_bytes(max_seqs, V))))
         return done(st);
     // constant per-sequence data: cache bases and the decode row -> sequence map
     s->host_i32_n = 3 * rows + 2 * tiles + 4 * max_seqs + 8;

@@ -512,12 +512,28 @@ __global__ void ring_update_kernel(const float *qkv, float *ring, const int32_t 
     r[2] = nr[2];
 }
 
-// finite_argmax (infer/mod.rs:70-83) of each row, one 1024-thread block per row.
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *y, long long n, int32_t *idx) {
-    const long long row = blockIdx.x;
+// finite_argmax (infer/mod.rs:70-83) of each row in two launches: keys of
+// kArgChunk-element chunks (grid chunks x rows), then one
+// wavefront per row over its chunk keys.  Keys order values as `>` does and
+// break ties toward the lower index, so the split gives the same answer.
+constexpr int kArgChunk = 4096;
+
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float *y, long long n, unsigned long long *keys) {
+    const long long row = blockIdx.y;
+    const long long c0 = static_cast<long long>(blockIdx.x) * kArgChunk;
     const float *yr = y + row * n;
     unsigned long long best = 0;
-    for (long long i = threadIdx.x; i < n; i += 1024) best = argmax_key_max(best, argmax_key(yr[i], static_cast<unsigned>(i)));
+    const long long end = c0 + kArgChunk < n ? c0 + kArgChunk : n;
+    for (long long i = c0 + threadIdx.x; i < end; i += 256)
+        best = argmax_key_max(best, argmax_key(yr[i], static_cast<unsigned>(i)));
+    best = argmax_block_key(best);
+    if (threadIdx.x == 0) keys[row * gridDim.x + blockIdx.x] = best;
+}
+
+__global__ __launch_bounds__(64) void argmax_final_rows_kernel(const unsigned long long *keys, int nk, int32_t *idx) {
+    const long long row = blockIdx.x;
+    unsigned long long best = 0;
+    for (int i = threadIdx.x; i < nk; i += 64) best = argmax_key_max(best, keys[row * nk + i]);
     best = argmax_block_key(best);
     if (threadIdx.x == 0) idx[row] = argmax_index(best);
 }
@@ -663,10 +679,20 @@ int ring_update(const float *qkv, float *ring, const int32_t *cu, size_t N, int 
     return check_launch("ring_update_kernel");
 }
 
-int argmax_rows(const float *y, size_t rows, size_t n, int32_t *idx, void *stream) {
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, as_stream(stream), y,
-                       static_cast<long long>(n), idx);
-    return check_launch("argmax_rows_kernel");
+size_t argmax_rows_ws_bytes(size_t rows, size_t n) {
+    return rows * ((n + kArgChunk - 1) / kArgChunk) * sizeof(unsigned long long);
+}
+
+int argmax_rows(const float *y, size_t rows, size_t n, int32_t *idx, unsigned long long *keys, void *stream) {
+    if (!rows || !n) return OURO_OK;
+    const int nk = static_cast<int>((n + kArgChunk - 1) / kArgChunk);
+    hipLaunchKernelGGL(argmax_chunk_kernel, dim3(static_cast<unsigned>(nk), static_cast<unsigned>(rows)), dim3(256), 0,
+                       as_stream(stream), y, static_cast<long long>(n), keys);
+    int st = check_launch("argmax_chunk_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(argmax_final_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, as_stream(stream),
+                       keys, nk, idx);
+    return check_launch("argmax_final_rows_kernel");
 }
 
 }  // namespace ouro
