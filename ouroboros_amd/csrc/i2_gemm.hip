@@ -208,14 +208,17 @@ struct SkinnyGroup {
     SkinnyProblem p[kSkinnyGroup];
     int bstart[kSkinnyGroup + 1];
     int np, K, N, nkb, x_tiled;
+    int tiles;  // column tiles of the whole launch, ceil(N / 16)
+    int ncg;    // column groups of WC tiles; workgroup x = row block * ncg + column group
 };
 
 template <int WC>
 __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(SkinnyGroup g) {
     constexpr int WR = 2, TR = 16 * WR, TC = 16 * WC + 1;
     __shared__ int tile[TR * TC];
+    const int bx = static_cast<int>(blockIdx.x) / g.ncg, cg = static_cast<int>(blockIdx.x) % g.ncg;
     int pi = 0;
-    while (pi + 1 < g.np && static_cast<int>(blockIdx.x) >= g.bstart[pi + 1]) ++pi;
+    while (pi + 1 < g.np && bx >= g.bstart[pi + 1]) ++pi;
     const SkinnyProblem &pb = g.p[pi];
     struct {
         const uint4 *w;
@@ -227,7 +230,8 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         int M, K, N, nkb, x_tiled;
     } a{pb.w, pb.w_scale, pb.xq, pb.dscale, pb.y, pb.acc, pb.M, g.K, g.N, g.nkb, g.x_tiled};
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    const int rt0 = (static_cast<int>(blockIdx.x) - g.bstart[pi]) * WR;
+    const int ct0 = cg * WC;  // first column tile of this workgroup
+    const int rt0 = (bx - g.bstart[pi]) * WR;
     const int nrt = (a.M + 15) / 16;
     for (int i = tid; i < TR * TC; i += blockDim.x) tile[i] = 0;
     v4i acc[WR][WC];
@@ -244,9 +248,10 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
     const int8_t *xr[WC];
 #pragma unroll
     for (int c = 0; c < WC; ++c)
-        xr[c] = a.x_tiled ? a.xq + (static_cast<long long>(c) * kWave + lane) * 16
-                          : a.xq + static_cast<long long>(min(16 * c + (lane & 15), a.N - 1)) * a.K + 16 * (lane >> 4);
-    const long long xkb = a.x_tiled ? 4LL * WC * 1024 : 256, xs = a.x_tiled ? WC * 1024 : 64;
+        xr[c] = a.x_tiled ? a.xq + (static_cast<long long>(ct0 + c) * kWave + lane) * 16
+                          : a.xq + static_cast<long long>(min(16 * (ct0 + c) + (lane & 15), a.N - 1)) * a.K +
+                                16 * (lane >> 4);
+    const long long xkb = a.x_tiled ? 4LL * g.tiles * 1024 : 256, xs = a.x_tiled ? g.tiles * 1024 : 64;
     const uint4 *wp[WR];
 #pragma unroll
     for (int r = 0; r < WR; ++r) wp[r] = a.w + static_cast<long long>(min(rt0 + r, nrt - 1)) * a.nkb * kWave + lane;
@@ -291,9 +296,9 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
     __syncthreads();
     const float wscale = *a.w_scale;
     for (int i = tid; i < TR * 16 * WC; i += blockDim.x) {
-        const int n = i / TR, rr = i % TR, row = rt0 * 16 + rr;
+        const int nt = i / TR, rr = i % TR, row = rt0 * 16 + rr, n = 16 * ct0 + nt;
         if (n >= a.N || row >= a.M) continue;
-        const int total = -(tile[rr * TC + n] >> 6);
+        const int total = -(tile[rr * TC + nt] >> 6);
         const long long o = static_cast<long long>(n) * a.M + row;
         a.y[o] = (static_cast<float>(total) * a.dscale[n]) * wscale;
         if (a.acc) a.acc[o] = total;
@@ -396,9 +401,19 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
     }
     g.bstart[np] = static_cast<int>(blocks);
     if (blocks > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "i2 gemm group: grid too large");
-    const int maxw = skinny_waves((g.N + 15) / 16);
+    // Few row blocks: split the column tiles into groups so the launch still
+    // fills the chip; a row block's column groups are adjacent workgroups,
+    // so the weights they share are read from HBM once and then from L2.
+    g.tiles = (g.N + 15) / 16;
+    int ncg = 1;
+    if (g.tiles == 4 && blocks < 96) ncg = 4;
+    else if (g.tiles % 2 == 0 && blocks < 192) ncg = 2;
+    g.ncg = ncg;
+    const int wc = g.tiles / ncg;
+    const int maxw = skinny_waves(wc);
     const int waves = g.nkb < maxw ? g.nkb : maxw;
-    hipLaunchKernelGGL(pick_skinny(g.N), dim3(static_cast<unsigned>(blocks)), dim3(kWave * waves), 0,
+    if (blocks * ncg > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "i2 gemm group: grid too large");
+    hipLaunchKernelGGL(pick_skinny(16 * wc), dim3(static_cast<unsigned>(blocks * ncg)), dim3(kWave * waves), 0,
                        as_stream(stream), g);
     return check_launch("i2_gemm_skinny_kernel");
 }
