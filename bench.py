@@ -427,7 +427,9 @@ def bench_stack(stream, steps, warmup):
     T = int(lens.sum())
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     rng = np.random.default_rng(6)
-    st = Stack(card, 1234, max_seqs=ST_SEQS, max_tokens=T, max_ctx=ST_MAX + ST_STEPS + 1)
+    # the KV pool holds exactly what the run needs: 64-token pages per sequence
+    pages = int(sum((int(l) + ST_STEPS + 63) // 64 for l in lens))
+    st = Stack(card, 1234, max_seqs=ST_SEQS, max_tokens=T, max_ctx=ST_MAX + ST_STEPS + 1, kv_pages=pages)
     toks = DeviceBuffer.from_host(rng.integers(0, card.n_vocab, T).astype(np.int32))
     a, b = DeviceBuffer((ST_SEQS,), np.int32), DeviceBuffer((ST_SEQS,), np.int32)
     try:

@@ -13,8 +13,8 @@
  * code = mix3(seed, tensor, k) % 3, per-tensor scale 1/sqrt(2/3 in_len),
  * float vectors from the same mix), so a host restatement can rebuild them.
  *
- * All pointers are device pointers unless named *_host; every call is
- * asynchronous on `stream` (NULL = default) and allocates nothing.
+ * All pointers are device pointers unless named *_host; every call after
+ * create is asynchronous on `stream` (NULL = default) and allocates nothing.
  */
 #ifndef OURO_STACK_H
 #define OURO_STACK_H
@@ -43,21 +43,30 @@ typedef struct ouro_stack *ouro_stack_t;
 
 /* Build a stack with synthetic weights.  max_seqs sequences of at most
  * max_ctx tokens each (prompt + generated), at most max_tokens prompt
- * tokens per prefill call.  Allocates everything the calls need. */
+ * tokens per prefill call.  The attention layers' KV cache is a pool of
+ * kv_pages pages of 64 tokens shared by all sequences through a page table
+ * (0 = max_seqs * ceil(max_ctx / 64), enough for every sequence at
+ * max_ctx); a sequence takes a page when it enters one.  Allocates
+ * everything the calls need. */
 int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seqs,
-                      size_t max_tokens, size_t max_ctx, ouro_stack_t *out);
+                      size_t max_tokens, size_t max_ctx, size_t kv_pages, ouro_stack_t *out);
 int ouro_stack_free(ouro_stack_t s);
 /* Device bytes the stack holds (weights, caches, activations). */
 size_t ouro_stack_device_bytes(ouro_stack_t s);
 /* Prefill N prompts packed into tokens[T] (T = cu_seqlens_host[N]), which
- * starts N fresh sequences (state, conv rings and KV caches reset), each
- * prompt token by token in the reference's sense (forward, qwen35.rs:730).
- * next_tokens[N] receives the greedy token after each prompt (sample,
- * qwen35.rs:746-757); logits_or_null[N][n_vocab] its logits. */
+ * starts N fresh sequences (state, conv rings reset, every KV page back in
+ * the pool), each prompt token by token in the reference's sense (forward,
+ * qwen35.rs:730).  next_tokens[N] receives the greedy token after each
+ * prompt (sample, qwen35.rs:746-757); logits_or_null[N][n_vocab] its
+ * logits.  Synchronises `stream` before it rewrites its pinned index
+ * staging; fails (before launching anything) when the prompts need more
+ * KV pages than the pool holds. */
 int ouro_stack_prefill(ouro_stack_t s, const int32_t *tokens, const int32_t *cu_seqlens_host,
                        size_t N, int32_t *next_tokens, float *logits_or_null, void *stream);
 /* One decode step of the N sequences of the last prefill: tokens[N] in,
- * next_tokens[N] (and logits_or_null[N][n_vocab]) out. */
+ * next_tokens[N] (and logits_or_null[N][n_vocab]) out.  Fails, before
+ * launching anything, when a sequence would pass max_ctx or the KV page
+ * pool is exhausted. */
 int ouro_stack_decode(ouro_stack_t s, const int32_t *tokens, int32_t *next_tokens,
                       float *logits_or_null, void *stream);
 

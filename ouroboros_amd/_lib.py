@@ -49,7 +49,7 @@ class StackCard(C.Structure):
 
 # name -> (restype, argtypes); every function of include/ouro_hip.h.
 SIGNATURES = {
-    "ouro_stack_create": (i32, [C.POINTER(StackCard), u32, sz, sz, sz, vp]),
+    "ouro_stack_create": (i32, [C.POINTER(StackCard), u32, sz, sz, sz, sz, vp]),
     "ouro_stack_free": (i32, [vp]),
     "ouro_stack_device_bytes": (sz, [vp]),
     "ouro_stack_prefill": (i32, [vp, vp, vp, sz, vp, vp, vp]),

@@ -115,6 +115,15 @@ struct GemmProblem {
 };
 int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream);
 
+// KV-cache pages handed out by the host for one decode step of the hybrid
+// stack: page_table[slot[i]] = page[i] (stack.hip, stack_ops.hip).
+constexpr int kMaxPageAssign = 64;
+struct PageAssign {
+    int n;
+    int slot[kMaxPageAssign];
+    int page[kMaxPageAssign];
+};
+
 // finite_argmax keys (infer/mod.rs:70-83): the value's bits in an
 // order-preserving form (-0 taken as +0, as `>` does) in the high word, the
 // complement of the index in the low word (the lowest index wins a tie), 0

@@ -36,20 +36,21 @@ int row_rotate_quant(int pro, const float *a, const float *b, const float *w, fl
 enum { RQ_COPY = 0, RQ_NORM = 1, RQ_SWIGLU = 2, RQ_GNORM = 3 };  // row_rotate_quant prologues (fwht.hip)
 // stack_ops.hip
 int fill_zero(float *p, size_t n, void *stream);
-int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, void *stream);
+int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, int32_t *pages, const PageAssign &pa,
+              void *stream);
 int gen_codes(uint32_t seed, uint32_t tensor, size_t rows, size_t cols, uint8_t *dst, void *stream);
 int gen_floats(uint32_t seed, uint32_t tensor, size_t n, float lo, float span, float *dst, void *stream);
 int embed_rows(const int32_t *tokens, const float *table, float *x, size_t n_tok, size_t n_vocab, size_t n_embd,
                void *stream);
 int gather_rows(const float *src, const int32_t *rows_idx, float *dst, size_t n, size_t width, void *stream);
 int attn_prep(const float *qfull, const float *k, const float *v, const float *qn, const float *kn,
-              const int32_t *pos, const int32_t *seq, const long long *base, float *q_out, float *gate_out,
+              const int32_t *pos, const int32_t *seq, const int32_t *pages, int maxp, float *q_out, float *gate_out,
               float *kc, float *vc, size_t T, int nh, int nkv, int n_rot, float rope_base, float eps, void *stream);
-int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const int32_t *pages, int maxp,
                  const int32_t *cu, const int32_t *tile_seq, const int32_t *tile_p0, size_t n_tiles, float *out,
                  int nh, int nkv, void *stream);
 size_t attn_decode_ws_bytes(size_t B, int nh, size_t max_ctx);
-int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const int32_t *pages, int maxp,
                 const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, float *part, void *stream);
 int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, const int32_t *seq,
                       const int32_t *pos, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
@@ -124,7 +125,7 @@ struct ouro_stack {
     float *beta = nullptr, *gate = nullptr;
     int32_t *pos = nullptr, *seqid = nullptr, *cu = nullptr, *tile_seq = nullptr, *tile_p0 = nullptr;
     int32_t *lens = nullptr, *klen = nullptr, *last_rows = nullptr, *dec_seq = nullptr;
-    long long *base = nullptr;
+    int32_t *pages = nullptr;  // KV page table [max_seqs][maxp]
     unsigned long long *arg_keys = nullptr;  // argmax chunk keys of the head rows
     void *ws = nullptr;
     // host staging (pinned) for the per-prefill index arrays
@@ -134,6 +135,11 @@ struct ouro_stack {
     size_t bytes = 0;
     size_t n_seqs = 0;
     int max_len = 0;  // longest sequence (keys) so far
+    // paged KV cache: kv_pages pages of kPage rows, handed out on the host
+    size_t kv_pages = 0;
+    int maxp = 0;                         // page-table entries per sequence
+    std::vector<int32_t> free_pages;      // stack of unused pages
+    std::vector<int32_t> lens_host;       // tokens held per sequence
 };
 
 namespace {
@@ -186,6 +192,7 @@ int make_vec(ouro_stack *s, float **p, uint32_t tensor, size_t n, float lo, floa
 // few sequences) pass the int8 activations in the few-column GEMM's
 // fragment order; longer ones row-major.
 constexpr size_t kFragRows = 64;
+constexpr int kPage = 64;  // tokens per KV cache page (stack_ops.hip)
 int frag_tiles(size_t rows) { return rows <= kFragRows ? static_cast<int>((rows + 15) / 16) : 0; }
 
 // y[cols][L.out] = L x (int8 activations xq/ds of `cols` rows, as produced
@@ -258,14 +265,14 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     } else {
         TRY(lin_group({{&L.q, s->xq, s->ds, s->big}, {&L.k, s->xq, s->ds, s->kbuf}, {&L.v, s->xq, s->ds, s->vbuf}},
                       rows, stream));
-        TRY(attn_prep(s->big, s->kbuf, s->vbuf, L.qn, L.kn, s->pos, prefill ? s->seqid : s->dec_seq, s->base,
+        TRY(attn_prep(s->big, s->kbuf, s->vbuf, L.qn, L.kn, s->pos, prefill ? s->seqid : s->dec_seq, s->pages, s->maxp,
                       s->qbuf, s->gbuf, L.kc, L.vc, rows, c.n_head, c.n_head_kv, c.n_rot, c.rope_base, c.eps,
                       stream));
         if (prefill)
-            TRY(attn_prefill(s->qbuf, s->gbuf, L.kc, L.vc, s->base, s->cu, s->tile_seq, s->tile_p0, n_tiles,
+            TRY(attn_prefill(s->qbuf, s->gbuf, L.kc, L.vc, s->pages, s->maxp, s->cu, s->tile_seq, s->tile_p0, n_tiles,
                              s->attn_o, c.n_head, c.n_head_kv, stream));
         else
-            TRY(attn_decode(s->qbuf, s->gbuf, L.kc, L.vc, s->base, s->klen, rows, s->max_len, s->attn_o, c.n_head,
+            TRY(attn_decode(s->qbuf, s->gbuf, L.kc, L.vc, s->pages, s->maxp, s->klen, rows, s->max_len, s->attn_o, c.n_head,
                             c.n_head_kv, s->attn_part, stream));
         TRY(rq(s, RQ_COPY, s->attn_o, nullptr, nullptr, nullptr, rows, s->qdim, s->sign_q, stream));
         TRY(lin(L.o, rows, s->xq, s->ds, s->mix, stream));
@@ -308,14 +315,15 @@ int check_card(const ouro_stack_card &c) {
 extern "C" {
 
 int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seqs, size_t max_tokens,
-                      size_t max_ctx, ouro_stack_t *out) {
+                      size_t max_ctx, size_t kv_pages, ouro_stack_t *out) {
     OURO_REQUIRE_INIT();
     if (!card || !out) return fail(OURO_ERR_INVALID_ARG, "ouro_stack_create: NULL argument");
     *out = nullptr;
     int st = check_card(*card);
     if (st) return st;
-    if (!max_seqs || !max_tokens || max_ctx < 2 || max_ctx > 16384 || max_tokens > (1u << 20) || max_seqs > 4096)
-        return fail(OURO_ERR_SHAPE, "ouro_stack_create: max_seqs, max_tokens, max_ctx (<= 16384) out of range");
+    if (!max_seqs || !max_tokens || max_ctx < 2 || max_ctx > 16384 || max_tokens > (1u << 20) || max_seqs > 4096 ||
+        kv_pages > (1u << 24))
+        return fail(OURO_ERR_SHAPE, "ouro_stack_create: max_seqs, max_tokens, max_ctx (<= 16384), kv_pages out of range");
     ouro_stack *s = new (std::nothrow) ouro_stack;
     if (!s) return fail(OURO_ERR_INVALID_ARG, "ouro_stack_create: out of host memory");
     s->c = *card;
@@ -323,6 +331,9 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
     s->max_seqs = max_seqs;
     s->max_tokens = max_tokens;
     s->max_ctx = max_ctx;
+    s->maxp = static_cast<int>((max_ctx + kPage - 1) / kPage);
+    s->kv_pages = kv_pages ? kv_pages : max_seqs * static_cast<size_t>(s->maxp);
+    s->lens_host.assign(max_seqs, 0);
     const ouro_stack_card &c = s->c;
     s->E = c.n_embd;
     s->F = c.n_ff;
@@ -378,8 +389,8 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
                 (st = make_lin(s, L.o, tid_layer(il, T_O), E, s->qdim, canon)) ||
                 (st = make_vec(s, &L.qn, tid_layer(il, T_QN), kHd, 0.8f, 0.4f)) ||
                 (st = make_vec(s, &L.kn, tid_layer(il, T_KN), kHd, 0.8f, 0.4f)) ||
-                (st = dalloc(s, &L.kc, max_seqs * max_ctx * s->kvdim)) ||
-                (st = dalloc(s, &L.vc, max_seqs * max_ctx * s->kvdim)))
+                (st = dalloc(s, &L.kc, s->kv_pages * kPage * s->kvdim)) ||
+                (st = dalloc(s, &L.vc, s->kv_pages * kPage * s->kvdim)))
                 return done(st);
         }
     }
@@ -412,7 +423,7 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         (st = dalloc(s, &s->tile_seq, tiles)) || (st = dalloc(s, &s->tile_p0, tiles)) ||
         (st = dalloc(s, &s->lens, max_seqs)) || (st = dalloc(s, &s->klen, max_seqs)) ||
         (st = dalloc(s, &s->last_rows, max_seqs)) || (st = dalloc(s, &s->dec_seq, max_seqs)) ||
-        (st = dalloc(s, &s->base, max_seqs)))
+        (st = dalloc(s, &s->pages, max_seqs * static_cast<size_t>(s->maxp))))
         return done(st);
     const size_t wsb = std::max(gdn_chunk_ws_bytes(max_tokens, max_seqs, c.ssm_n_v_heads),
                                 gdn_layer_ws_bytes(max_seqs, c.ssm_n_k_heads, c.ssm_n_v_heads));
@@ -420,18 +431,14 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->attn_part), attn_decode_ws_bytes(max_seqs, c.n_head, max_ctx))) ||
         (st = dalloc(s, reinterpret_cast<uint8_t **>(&s->arg_keys), argmax_rows_ws_bytes(max_seqs, V))))
         return done(st);
-    // constant per-sequence data: cache bases and the decode row -> sequence map
-    s->host_i32_n = 3 * rows + 2 * tiles + 4 * max_seqs + 8;
+    // pinned staging of the per-prefill index arrays and page table; the
+    // decode row -> sequence map is constant
+    s->host_i32_n = 3 * rows + 2 * tiles + 4 * max_seqs + max_seqs * static_cast<size_t>(s->maxp) + 8;
     if (hipHostMalloc(reinterpret_cast<void **>(&s->host_i32), s->host_i32_n * 4, hipHostMallocDefault) != hipSuccess)
         return done(fail(OURO_ERR_HIP, "ouro_stack_create: pinned host allocation failed"));
-    std::vector<long long> bases(max_seqs);
     std::vector<int32_t> ids(max_seqs);
-    for (size_t i = 0; i < max_seqs; ++i) {
-        bases[i] = static_cast<long long>(i * max_ctx);
-        ids[i] = static_cast<int32_t>(i);
-    }
-    if (hipMemcpy(s->base, bases.data(), max_seqs * 8, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(s->dec_seq, ids.data(), max_seqs * 4, hipMemcpyHostToDevice) != hipSuccess ||
+    for (size_t i = 0; i < max_seqs; ++i) ids[i] = static_cast<int32_t>(i);
+    if (hipMemcpy(s->dec_seq, ids.data(), max_seqs * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess)
         return done(fail(OURO_ERR_HIP, "ouro_stack_create: setup copy failed"));
     *out = s;
@@ -470,8 +477,15 @@ int ouro_stack_prefill(ouro_stack_t s, const int32_t *tokens, const int32_t *cu_
     size_t n_tiles = 0;
     for (size_t i = 0; i < N; ++i)
         for (int p0 = 0; p0 < cu_host[i + 1] - cu_host[i]; p0 += 64) ++n_tiles;
-    int32_t *h_tp = h_ts + n_tiles, *h_last = h_tp + n_tiles, *h_lens = h_last + N;
-    if (static_cast<size_t>(h_lens + N - hp) > s->host_i32_n) return fail(OURO_ERR_SHAPE, "ouro_stack_prefill: index staging");
+    int32_t *h_tp = h_ts + n_tiles, *h_last = h_tp + n_tiles, *h_lens = h_last + N, *h_pt = h_lens + N;
+    const size_t n_pt = N * static_cast<size_t>(s->maxp);
+    if (static_cast<size_t>(h_pt + n_pt - hp) > s->host_i32_n) return fail(OURO_ERR_SHAPE, "ouro_stack_prefill: index staging");
+    // fresh sequences: every KV page returns to the pool, each prompt takes ceil(L / kPage)
+    size_t need = 0;
+    for (size_t i = 0; i < N; ++i) need += (cu_host[i + 1] - cu_host[i] + kPage - 1) / kPage;
+    if (need > s->kv_pages)
+        return fail(OURO_ERR_SHAPE, "ouro_stack_prefill: prompts need %zu KV pages of %d tokens (pool %zu)", need, kPage,
+                    s->kv_pages);
     hipStream_t st = as_stream(stream);
     // the staging buffer is rewritten: earlier copies from it must be done
     if (hipStreamSynchronize(st) != hipSuccess) return fail(OURO_ERR_HIP, "ouro_stack_prefill: stream sync");
@@ -490,13 +504,26 @@ int ouro_stack_prefill(ouro_stack_t s, const int32_t *tokens, const int32_t *cu_
         h_lens[i] = L;
     }
     for (size_t i = 0; i <= N; ++i) h_cu[i] = cu_host[i];
+    s->free_pages.resize(s->kv_pages);
+    for (size_t i = 0; i < s->kv_pages; ++i) s->free_pages[i] = static_cast<int32_t>(s->kv_pages - 1 - i);
+    std::fill(h_pt, h_pt + n_pt, 0);
+    std::fill(s->lens_host.begin(), s->lens_host.end(), 0);
+    for (size_t i = 0; i < N; ++i) {
+        const int L = cu_host[i + 1] - cu_host[i];
+        for (int p = 0; p * kPage < L; ++p) {
+            h_pt[i * s->maxp + p] = s->free_pages.back();
+            s->free_pages.pop_back();
+        }
+        s->lens_host[i] = L;
+    }
     if (hipMemcpyAsync(s->pos, h_pos, T * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(s->seqid, h_seq, T * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(s->cu, h_cu, (N + 1) * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(s->tile_seq, h_ts, n_tiles * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(s->tile_p0, h_tp, n_tiles * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
         hipMemcpyAsync(s->last_rows, h_last, N * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipMemcpyAsync(s->lens, h_lens, N * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+        hipMemcpyAsync(s->lens, h_lens, N * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipMemcpyAsync(s->pages, h_pt, n_pt * 4, hipMemcpyHostToDevice, st) != hipSuccess)
         return fail(OURO_ERR_HIP, "ouro_stack_prefill: index upload");
     // fresh sequences: zero recurrent state and conv rings
     for (auto &L : s->layers)
@@ -519,7 +546,24 @@ int ouro_stack_decode(ouro_stack_t s, const int32_t *tokens, int32_t *next_token
     if (!B) return fail(OURO_ERR_SHAPE, "ouro_stack_decode: no sequences (prefill first)");
     if (static_cast<size_t>(s->max_len) + 1 > s->max_ctx)
         return fail(OURO_ERR_SHAPE, "ouro_stack_decode: a sequence reached max_ctx = %zu", s->max_ctx);
-    TRY(lens_step(s->lens, s->pos, s->klen, B, stream));
+    // a sequence whose new token starts a page takes one from the pool
+    size_t need = 0;
+    for (size_t b = 0; b < B; ++b) need += s->lens_host[b] % kPage == 0;
+    if (need > s->free_pages.size())
+        return fail(OURO_ERR_SHAPE, "ouro_stack_decode: KV page pool (%zu pages) exhausted", s->kv_pages);
+    PageAssign pa{};
+    for (size_t b = 0; b < B; ++b) {
+        const int l = s->lens_host[b]++;
+        if (l % kPage) continue;
+        if (pa.n == kMaxPageAssign) {  // more than one launch's worth: flush first
+            TRY(lens_step(s->lens, s->pos, s->klen, 0, s->pages, pa, stream));
+            pa.n = 0;
+        }
+        pa.slot[pa.n] = static_cast<int>(b) * s->maxp + l / kPage;
+        pa.page[pa.n++] = s->free_pages.back();
+        s->free_pages.pop_back();
+    }
+    TRY(lens_step(s->lens, s->pos, s->klen, B, s->pages, pa, stream));
     s->max_len += 1;
     TRY(embed_rows(tokens, s->embd, s->x, B, s->V, s->E, stream));
     for (int il = 0; il < s->c.n_layer; ++il) TRY(run_layer(s, il, B, false, nullptr, B, 0, stream));

@@ -19,6 +19,13 @@ namespace ouro {
 namespace {
 
 constexpr int kHd = 128;  // attention head dim and delta-net d handled here
+constexpr int kPage = 64;  // tokens per KV cache page
+
+// Cache row of (sequence, position): the KV cache is a pool of pages of
+// kPage rows; pages[seq * maxp + pos / kPage] names the page holding pos.
+__device__ __forceinline__ long long kv_row(const int32_t *pages, int maxp, int seq, int pos) {
+    return static_cast<long long>(pages[static_cast<long long>(seq) * maxp + pos / kPage]) * kPage + pos % kPage;
+}
 
 // ------------------------------------------------------- synthetic weights --
 
@@ -92,10 +99,10 @@ struct AttnPrepArgs {
     const float *qn, *kn;     // [hd] head-norm gains
     const int32_t *pos;       // [T] position of the token in its sequence
     const int32_t *seq;       // [T] sequence of the token
-    const long long *base;    // [N] first cache row of each sequence
+    const int32_t *pages;     // [N][maxp] page table
     float *q_out, *gate_out;  // [T][nh][hd]
-    float *kc, *vc;           // cache [rows][nkv][hd]
-    int T, nh, nkv, n_rot;
+    float *kc, *vc;           // cache pages [pages * kPage][nkv][hd]
+    int T, nh, nkv, n_rot, maxp;
     float rope_base, eps;
 };
 
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
         *reinterpret_cast<float2 *>(a.q_out + o) = x;
         *reinterpret_cast<float2 *>(a.gate_out + o) = *reinterpret_cast<const float2 *>(src + kHd + 2 * lane);
     } else {
-        const long long row = a.base[a.seq[t]] + p;
+        const long long row = kv_row(a.pages, a.maxp, a.seq[t], p);
         const long long o = (row * a.nkv + h) * kHd + 2 * lane;
         *reinterpret_cast<float2 *>(a.kc + o) = x;
         *reinterpret_cast<float2 *>(a.vc + o) =
@@ -162,13 +169,13 @@ constexpr int kAttnLds = (kQT * kQP + 2 * kKT * kQP + kQT * kPP) * 4;
 
 struct AttnArgs {
     const float *q, *gate;    // [T][nh][hd]
-    const float *kc, *vc;     // cache [rows][nkv][hd]
-    const long long *base;    // [N] first cache row of each sequence
+    const float *kc, *vc;     // cache pages [pages * kPage][nkv][hd]
+    const int32_t *pages;     // [N][maxp] page table
     const int32_t *cu;        // [N+1] token offsets (prefill); NULL for decode
     const int32_t *lens;      // [N] keys per sequence (decode)
     const int32_t *tile_seq, *tile_p0;  // prefill query tiles
     float *out;               // [T][nh][hd]
-    int nh, nkv;
+    int nh, nkv, maxp;
     float scale;
 };
 
@@ -201,7 +208,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     const int h = blockIdx.y;
     const int kvh = h / (a.nh / a.nkv);
     const int t0 = a.cu[s], L = a.cu[s + 1] - t0;
-    const long long kbase = a.base[s];
 
     // Q tile (rows past the sequence's end are zero and never stored)
     for (int i = tid; i < kQT * (kHd / 4); i += 256) {
@@ -225,8 +231,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
         for (int i = tid; i < kKT * (kHd / 4); i += 256) {
             const int r = i / (kHd / 4), c4 = i % (kHd / 4);
             float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (k0 + r < L) {
-                const long long off = ((kbase + k0 + r) * a.nkv + kvh) * kHd + 4 * c4;
+            if (k0 + r < L) {  // a key tile is one page
+                const long long off = ((kv_row(a.pages, a.maxp, s, k0) + r) * a.nkv + kvh) * kHd + 4 * c4;
                 kv = *reinterpret_cast<const float4 *>(a.kc + off);
                 vv = *reinterpret_cast<const float4 *>(a.vc + off);
             }
@@ -343,13 +349,15 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     __shared__ float sc[G][kDecKeys];
     __shared__ float red[4][G][kHd];
     __shared__ float ml[G][2];
+    __shared__ long long prow[kDecKeys / kPage];  // first cache row of each page of the split
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
     const int L = a.lens[b];
     const int j0 = sp * kDecKeys;
     if (j0 >= L) return;  // whole workgroup
     const int n = min(kDecKeys, L - j0);
-    const long long row0 = a.base[b] + j0;
+    if (tid < kDecKeys / kPage && j0 + tid * kPage < L) prow[tid] = kv_row(a.pages, a.maxp, b, j0 + tid * kPage);
+    __syncthreads();
     const int g4 = lane >> 4, gl = lane & 15;
     float4 q[G][2];
 #pragma unroll
@@ -358,13 +366,14 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
         q[g][0] = *reinterpret_cast<const float4 *>(qp);
         q[g][1] = *reinterpret_cast<const float4 *>(qp + 4);
     }
-    // scores: wave w, step it -> key w*64 + 4*it + g4
+    // scores: wave w, step it -> key w*64 + 4*it + g4 (wave w reads page w of the split)
+    const long long wrow = wave * kPage < n ? prow[wave] : 0;
 #pragma unroll 4
     for (int it = 0; it < 16; ++it) {
         const int j = wave * 64 + 4 * it + g4;
         float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0;
         if (j < n) {
-            const float *kp = a.kc + ((row0 + j) * a.nkv + kvh) * kHd + 8 * gl;
+            const float *kp = a.kc + ((wrow + 4 * it + g4) * a.nkv + kvh) * kHd + 8 * gl;
             k0 = *reinterpret_cast<const float4 *>(kp);
             k1 = *reinterpret_cast<const float4 *>(kp + 4);
         }
@@ -401,11 +410,11 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     float2 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] = make_float2(0.f, 0.f);
-    const float *vp = a.vc + (row0 * a.nkv + kvh) * kHd + 2 * lane;
+    const float *vp = a.vc + kvh * kHd + 2 * lane;
     const long long vstride = static_cast<long long>(a.nkv) * kHd;
 #pragma unroll 4
     for (int j = wave; j < n; j += 4) {
-        const float2 v = *reinterpret_cast<const float2 *>(vp + j * vstride);
+        const float2 v = *reinterpret_cast<const float2 *>(vp + (prow[j / kPage] + j % kPage) * vstride);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float pj = sc[g][j];
@@ -545,8 +554,11 @@ __global__ void fill_zero_kernel(float *p, long long n) {
 
 // Start of a decode step: the new token of sequence b sits at position
 // lens[b], its attention sees lens[b] + 1 keys, and the cache grows by one.
-__global__ void lens_step_kernel(int32_t *lens, int32_t *pos, int32_t *klen, int B) {
+// Pages the host assigned for this step (a sequence entering a new page)
+// arrive by value and are written into the page table first.
+__global__ void lens_step_kernel(int32_t *lens, int32_t *pos, int32_t *klen, int B, int32_t *pages, PageAssign pa) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < pa.n) pages[pa.slot[b]] = pa.page[b];
     if (b >= B) return;
     const int l = lens[b];
     pos[b] = l;
@@ -567,9 +579,11 @@ int fill_zero(float *p, size_t n, void *stream) {
     return check_launch("fill_zero_kernel");
 }
 
-int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, void *stream) {
-    hipLaunchKernelGGL(lens_step_kernel, dim3(blocks_for(static_cast<long long>(B), 256)), dim3(256), 0,
-                       as_stream(stream), lens, pos, klen, static_cast<int>(B));
+int lens_step(int32_t *lens, int32_t *pos, int32_t *klen, size_t B, int32_t *pages, const PageAssign &pa,
+              void *stream) {
+    const long long n = static_cast<long long>(B) > pa.n ? static_cast<long long>(B) : pa.n;
+    hipLaunchKernelGGL(lens_step_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream), lens, pos, klen,
+                       static_cast<int>(B), pages, pa);
     return check_launch("lens_step_kernel");
 }
 
@@ -603,18 +617,18 @@ int gather_rows(const float *src, const int32_t *rows_idx, float *dst, size_t n,
 }
 
 int attn_prep(const float *qfull, const float *k, const float *v, const float *qn, const float *kn,
-              const int32_t *pos, const int32_t *seq, const long long *base, float *q_out, float *gate_out,
+              const int32_t *pos, const int32_t *seq, const int32_t *pages, int maxp, float *q_out, float *gate_out,
               float *kc, float *vc, size_t T, int nh, int nkv, int n_rot, float rope_base, float eps,
               void *stream) {
     if (n_rot < 0 || n_rot > kHd || n_rot % 4) return fail(OURO_ERR_SHAPE, "attn_prep: n_rot %d", n_rot);
-    AttnPrepArgs a{qfull, k, v, qn, kn, pos, seq, base, q_out, gate_out, kc, vc,
-                   static_cast<int>(T), nh, nkv, n_rot, rope_base, eps};
+    AttnPrepArgs a{qfull, k, v, qn, kn, pos, seq, pages, q_out, gate_out, kc, vc,
+                   static_cast<int>(T), nh, nkv, n_rot, maxp, rope_base, eps};
     const long long items = static_cast<long long>(T) * (nh + nkv);
     hipLaunchKernelGGL(attn_prep_kernel, dim3(blocks_for(items, 4)), dim3(256), 0, as_stream(stream), a);
     return check_launch("attn_prep_kernel");
 }
 
-int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+int attn_prefill(const float *q, const float *gate, const float *kc, const float *vc, const int32_t *pages, int maxp,
                  const int32_t *cu, const int32_t *tile_seq, const int32_t *tile_p0, size_t n_tiles, float *out,
                  int nh, int nkv, void *stream) {
     if (!n_tiles) return OURO_OK;
@@ -625,7 +639,8 @@ int attn_prefill(const float *q, const float *gate, const float *kc, const float
         if (e != hipSuccess) return fail(OURO_ERR_HIP, "attn_prefill: LDS opt-in: %s", hipGetErrorString(e));
         lds_set = true;
     }
-    AttnArgs a{q, gate, kc, vc, base, cu, nullptr, tile_seq, tile_p0, out, nh, nkv, 1.0f / sqrtf(static_cast<float>(kHd))};
+    AttnArgs a{q, gate, kc, vc, pages, cu, nullptr, tile_seq, tile_p0, out, nh, nkv, maxp,
+               1.0f / sqrtf(static_cast<float>(kHd))};
     hipLaunchKernelGGL(attn_prefill_kernel, dim3(static_cast<unsigned>(n_tiles), nh), dim3(256), kAttnLds,
                        as_stream(stream), a);
     return check_launch("attn_prefill_kernel");
@@ -635,13 +650,13 @@ size_t attn_decode_ws_bytes(size_t B, int nh, size_t max_ctx) {
     return B * static_cast<size_t>(nh) * ((max_ctx + kDecKeys - 1) / kDecKeys) * kPartStride * sizeof(float);
 }
 
-int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const long long *base,
+int attn_decode(const float *q, const float *gate, const float *kc, const float *vc, const int32_t *pages, int maxp,
                 const int32_t *lens, size_t B, int max_len, float *out, int nh, int nkv, float *part, void *stream) {
     const int G = nh / nkv;
     if (G < 1 || G > 8 || nh % nkv) return fail(OURO_ERR_SHAPE, "attn_decode: %d heads over %d kv heads", nh, nkv);
     if (max_len < 1 || !B) return OURO_OK;
     const int nsplit = (max_len + kDecKeys - 1) / kDecKeys;
-    AttnArgs a{q, gate, kc, vc, base, nullptr, lens, nullptr, nullptr, out, nh, nkv,
+    AttnArgs a{q, gate, kc, vc, pages, nullptr, lens, nullptr, nullptr, out, nh, nkv, maxp,
                1.0f / sqrtf(static_cast<float>(kHd))};
     const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(nkv), static_cast<unsigned>(nsplit));
     hipStream_t s = as_stream(stream);

@@ -36,12 +36,14 @@ class Card:
 
 
 class Stack:
-    def __init__(self, card: Card, seed: int, max_seqs: int, max_tokens: int, max_ctx: int):
+    def __init__(self, card: Card, seed: int, max_seqs: int, max_tokens: int, max_ctx: int, kv_pages: int = 0):
+        """kv_pages: pages of 64 tokens in the attention layers' KV pool
+        (0 = enough for every sequence at max_ctx)."""
         _lib.init()
         self.card = card
         self._c = card.c()
         h = C.c_void_p()
-        call("ouro_stack_create", C.byref(self._c), seed, max_seqs, max_tokens, max_ctx, C.byref(h))
+        call("ouro_stack_create", C.byref(self._c), seed, max_seqs, max_tokens, max_ctx, kv_pages, C.byref(h))
         self.handle = h.value
 
     @property

@@ -114,3 +114,39 @@ def test_stack_rejects_bad_calls(gpu):
             st.decode(toks, nxt)
     finally:
         st.free()
+
+
+def test_stack_kv_page_pool(gpu):
+    # 64-token pages: two 64-token prompts take 2 pages; their first decode
+    # step enters a new page each, so a pool of 3 runs dry, a pool of 4 does not
+    rng = np.random.default_rng(5)
+    prompts = [list(rng.integers(0, SMALL.n_vocab, 64)), list(rng.integers(0, SMALL.n_vocab, 64))]
+    cu = np.array([0, 64, 128], np.int32)
+    toks = DeviceBuffer.from_host(np.concatenate(prompts).astype(np.int32))
+    nxt = DeviceBuffer((2,), np.int32)
+    small = Stack(SMALL, 7, max_seqs=2, max_tokens=128, max_ctx=200, kv_pages=1)
+    try:
+        with pytest.raises(OuroError):  # the prompts alone need 2 pages
+            small.prefill(toks, cu, nxt)
+    finally:
+        small.free()
+    st = Stack(SMALL, 7, max_seqs=2, max_tokens=128, max_ctx=200, kv_pages=3)
+    try:
+        st.prefill(toks, cu, nxt)
+        with pytest.raises(OuroError):
+            st.decode(nxt, nxt)
+    finally:
+        st.free()
+    got = []
+    for pages in (4, 0):  # exactly enough, and the default max_seqs * ceil(max_ctx / 64)
+        st = Stack(SMALL, 7, max_seqs=2, max_tokens=128, max_ctx=200, kv_pages=pages)
+        try:
+            lg = DeviceBuffer((2 * SMALL.n_vocab,), np.float32)
+            st.prefill(toks, cu, nxt, lg)
+            fed = DeviceBuffer.from_host(np.array([3, 4], np.int32))
+            for _ in range(3):
+                st.decode(fed, nxt, lg)
+            got.append(lg.download())
+        finally:
+            st.free()
+    assert np.array_equal(got[0], got[1])
