@@ -10,7 +10,10 @@ reported beside it.  Also measured, reported under
 "secondary": gated delta-net decode (B=32, Hk=16, Hv=32, d=128, fp32 state,
 8 rotating state sets = 512 MiB) in tokens/s, the 512x4096 bf16
 Walsh-Hadamard rotation in GB/s, the chunked prefill of 4 x 4096 tokens in
-tokens/s and TFLOP/s, and a 512 MiB device copy as the bandwidth reference.
+tokens/s and TFLOP/s, the ternary GEMM at 4..2048 columns, the TL1 lm_head
+GEMV, the hybrid stack (24 layers, 64 ragged prompts of 16..2048 tokens then
+128 greedy decode steps) in tokens/s with its decode step against the HBM
+roofline, and a 512 MiB device copy as the bandwidth reference.
 
 Every kernel time comes from HIP events recorded on the stream the kernels
 run on: the null stream, where back-to-back launches carry no extra gap.

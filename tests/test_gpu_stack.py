@@ -90,6 +90,20 @@ def test_stack_single_token_prompts(gpu):
     check(SMALL, [[5], [511], [0]], 2)
 
 
+def test_stack_attention_only_single_token_matches_oracle_closely(gpu):
+    # no delta layers (no bf16 anywhere) and one key per sequence: everything
+    # from the synthetic weights to the head runs the oracle's arithmetic
+    # up to summation order, so the logits agree far inside one int8 step
+    from oracle.stack_oracle import StackOracle
+
+    card = Card(n_layer=2, n_embd=256, n_ff=512, n_vocab=512, full_attention_interval=1, n_head=2, n_head_kv=1,
+                n_rot=64, ssm_n_k_heads=1, ssm_n_v_heads=2, eps=1e-6, rope_base=1e7)
+    prompts = [[5], [17], [300]]
+    want, _ = StackOracle(card, seed=7).run(prompts, 0)
+    got, _ = gpu_run(card, prompts, [])
+    assert rel(got[0], want[0]) < 1e-4, rel(got[0], want[0])
+
+
 def test_stack_long_ragged_prompts_wide_heads(gpu):
     # prompts across the 64-token chunk and attention-tile edges, one of length 1
     rng = np.random.default_rng(4)
