@@ -15,13 +15,17 @@
 #include <vector>
 
 #include "../ouro_hip.h"
+#include "bmts.hpp"
 
 namespace ouro {
 
+#ifndef OURO_ERROR_DEFINED
+#define OURO_ERROR_DEFINED
 struct Error : std::runtime_error {
     int code;
     Error(int c, const std::string &what) : std::runtime_error(what), code(c) {}
 };
+#endif
 
 inline void check(int st, const char *what) {
     if (st != OURO_OK) throw Error(st, std::string(what) + ": " + ouro_last_error());
@@ -170,6 +174,32 @@ public:
         auto it = w_.find(name);
         if (it != w_.end()) ouro_weight_free(it->second.h);
         w_[name] = Entry{h, out_len, in_len};
+    }
+
+    // Upload straight from a view (e.g. a tensor of a mapped shard), no host copy.
+    void upload_view(const std::string &name, infer::QuantKind kind, const uint8_t *bytes, size_t n, size_t out_len,
+                     size_t in_len, float w_scale = 1.0f, size_t max_cols = 8) {
+        ouro_weight_t h = nullptr;
+        check(ouro_weight_upload(static_cast<int>(kind), bytes, n, out_len, in_len, w_scale, max_cols, &h),
+              "ouro_weight_upload");
+        auto it = w_.find(name);
+        if (it != w_.end()) ouro_weight_free(it->second.h);
+        w_[name] = Entry{h, out_len, in_len};
+    }
+
+    // Stage::from_shard (mod.rs:112-135): every tensor of the shard, its
+    // ggml dtype as the kind (the kinds this path decodes; others refused).
+    void from_shard(const bmts::Shard &shard, size_t max_cols = 8) {
+        for (const bmts::Tensor &t : shard.tensors()) {
+            const int d = static_cast<int>(t.dtype);
+            if (d != OURO_KIND_F32 && d != OURO_KIND_F16 && d != OURO_KIND_BF16 && d != OURO_KIND_TQ1_0 &&
+                d != OURO_KIND_TL1)
+                throw Error(OURO_ERR_KIND, "unsupported dtype " + std::to_string(t.dtype) + " on " + t.name);
+            size_t out_len = 0, in_len = 0;
+            shard.weight_shape(t.name, &out_len, &in_len);
+            const auto v = shard.tensor_bytes(t.name);
+            upload_view(t.name, static_cast<infer::QuantKind>(d), v.first, v.second, out_len, in_len, 1.0f, max_cols);
+        }
     }
 
     std::vector<float> matvec(const std::string &name, const std::vector<float> &x) const {

@@ -2,8 +2,11 @@
 // in C++ against the C++ host mirror (include/ouro/infer.hpp), i.e. run on
 // the GPU through the C ABI.  Each test names the reference test it follows.
 // Exit status 0 when every test passes.
+#include <unistd.h>
+
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <functional>
 #include <vector>
 
@@ -299,6 +302,38 @@ static void test_pool_matvec_by_name() {  // GpuPool::upload/matvec pattern (our
     EXPECT(threw);
 }
 
+static void test_pool_from_mapped_shard() {  // Stage::from_shard (mod.rs:112-135) on a BMTS file (bmts.rs:311-324)
+    const size_t out_len = 37, in_len = 384;
+    const auto payload = tl1_payload(out_len, in_len, 11);
+    std::vector<uint8_t> data(16, 0);  // the tensor does not start the data section
+    data.insert(data.end(), payload.begin(), payload.end());
+    char path[] = "/tmp/ouro_kat_shard_XXXXXX";
+    const int fd = mkstemp(path);
+    EXPECT(fd >= 0);
+    close(fd);
+    bmts::Tensor t;
+    t.name = "blk.2.ffn_up.weight";
+    t.shape = {in_len, out_len};
+    t.dtype = 143;
+    t.offset = 16;
+    t.length = payload.size();
+    bmts::write_shard(path, 3, {t}, data);
+    std::vector<float> x(in_len);
+    // small multiples of 0.5: every partial sum is exact, so both decode orders agree bit for bit
+    for (size_t i = 0; i < in_len; ++i) x[i] = (static_cast<float>(i % 5) - 2.0f) * 0.5f;
+    std::vector<float> a;
+    {
+        bmts::Shard shard(path);
+        EXPECT(shard.node() == 3 && shard.tensors().size() == 1);
+        HipPool pool;
+        pool.from_shard(shard);  // uploaded from the mapping itself
+        a = pool.matvec("blk.2.ffn_up.weight", x);
+    }
+    std::remove(path);
+    const auto b = ops::matvec_q(payload, QuantKind::Tl1, out_len, in_len, x);
+    EXPECT(a == b);
+}
+
 int main() {
     try {
         init();
@@ -318,6 +353,7 @@ int main() {
     run("ops::test_matvec_tl1_fused_matches_reference", test_matvec_tl1_fused_matches_reference);
     run("ops::test_matmul_tl1_k_columns_matches_matvec", test_matmul_tl1_k_columns_matches_matvec);
     run("pool::matvec_by_name", test_pool_matvec_by_name);
+    run("pool::from_mapped_shard", test_pool_from_mapped_shard);
     std::printf("%d failed\n", g_failed);
     return g_failed ? 1 : 0;
 }

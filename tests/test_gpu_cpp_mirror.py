@@ -15,4 +15,4 @@ def test_reference_kats_through_cpp_mirror(gpu):
     r = subprocess.run([str(BIN)], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
-    assert r.stdout.count("PASS") == 12
+    assert r.stdout.count("PASS") == 13
