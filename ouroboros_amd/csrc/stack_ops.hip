@@ -19,6 +19,7 @@ namespace ouro {
 namespace {
 
 constexpr int kHd = 128;  // attention head dim and delta-net d handled here
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kPage = 64;  // tokens per KV cache page
 
 // Cache row of (sequence, position): the KV cache is a pool of pages of
@@ -165,7 +166,6 @@ constexpr int kQT = 64;        // query rows per tile
 constexpr int kKT = 64;        // keys per tile
 constexpr int kQP = kHd + 4;   // LDS row pitch (floats) of Q, K, V tiles
 constexpr int kPP = kKT + 4;   // LDS row pitch of P
-constexpr int kAttnLds = (kQT * kQP + 2 * kKT * kQP + kQT * kPP) * 4;
 
 struct AttnArgs {
     const float *q, *gate;    // [T][nh][hd]
@@ -179,12 +179,16 @@ struct AttnArgs {
     float scale;
 };
 
-// Causal attention over a packed varlen batch, one workgroup per (query
-// tile of 64 tokens of one sequence, q head), online softmax over key
-// tiles of 64 up to the diagonal, fp32 throughout.  Thread (tr, tc) =
-// (tid / 16, tid % 16) owns rows 4tr..4tr+3 of the tile: scores of keys
-// 4tc..4tc+3 and outputs of dims 8tc..8tc+7.  The 16 threads of a row
-// group are one 16-lane row of a wavefront, reduced with DPP.
+// Causal attention over a packed varlen batch on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: fp32 products and sums, the reference's f32
+// arithmetic up to summation order).  One workgroup per (query tile of 64
+// tokens of one sequence, q head); wavefront w owns query rows 16w..16w+15
+// and keeps their Q in registers as A operands.  Per key tile of 64 (one KV
+// page): S = Q K^T as 4 MFMA tiles of 16 keys (k = 128 dims, the dims of
+// k-step s and lane group g being 32g + s), online softmax per row with DPP
+// row reductions, P to the wavefront's LDS rows, then O += P V as 8 MFMA
+// tiles of 16 dims (k = 64 keys, key 16g + s at step s) with V staged
+// transposed.  The sigmoid output gate is applied at the end.
 __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
@@ -200,128 +204,143 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+constexpr int kVTP = kKT + 4;  // LDS row pitch of V^T (floats)
+constexpr int kAttnLds = (kKT * kQP + kHd * kVTP + kQT * kPP) * 4;
+
+__device__ __forceinline__ f32x4_t mfma_f32(float a, float b, const f32x4_t &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     extern __shared__ float lds[];
-    float *Qs = lds, *Ks = Qs + kQT * kQP, *Vs = Ks + kKT * kQP, *Ps = Vs + kKT * kQP;
-    const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+    float *Ks = lds, *Vt = Ks + kKT * kQP, *Ps = Vt + kHd * kVTP;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
     const int s = a.tile_seq[blockIdx.x], p0 = a.tile_p0[blockIdx.x];
     const int h = blockIdx.y;
     const int kvh = h / (a.nh / a.nkv);
     const int t0 = a.cu[s], L = a.cu[s + 1] - t0;
+    float *Pw = Ps + 16 * wave * kPP;  // this wavefront's 16 rows of P
 
-    // Q tile (rows past the sequence's end are zero and never stored)
-    for (int i = tid; i < kQT * (kHd / 4); i += 256) {
-        const int r = i / (kHd / 4), c4 = i % (kHd / 4);
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (p0 + r < L)
-            v = *reinterpret_cast<const float4 *>(a.q + ((static_cast<long long>(t0) + p0 + r) * a.nh + h) * kHd + 4 * c4);
-        *reinterpret_cast<float4 *>(Qs + r * kQP + 4 * c4) = v;
+    // Q row 16w + lr, dims 32g .. 32g + 31 as the A operand of k-steps 0..31
+    float qa[32];
+    {
+        const int qp = min(p0 + 16 * wave + lr, L - 1);  // rows past the end: any valid row, never stored
+        const float *qr = a.q + ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + 32 * lg;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = *reinterpret_cast<const float4 *>(qr + 4 * i);
+            qa[4 * i] = v.x, qa[4 * i + 1] = v.y, qa[4 * i + 2] = v.z, qa[4 * i + 3] = v.w;
+        }
     }
-    float m[4], l[4], o[4][8];
+    f32x4_t o[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -INFINITY;
-        l[r] = 0.f;
+    for (int t = 0; t < 8; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o[r][d] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+        m[e] = -INFINITY;
+        l[e] = 0.f;
     }
     const int last = min(p0 + kQT, L) - 1;  // last query position in the tile
     for (int k0 = 0; k0 <= last; k0 += kKT) {
-        __syncthreads();  // previous tile's K, V, P are consumed
-        for (int i = tid; i < kKT * (kHd / 4); i += 256) {
-            const int r = i / (kHd / 4), c4 = i % (kHd / 4);
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (k0 + r < L) {  // a key tile is one page
-                const long long off = ((kv_row(a.pages, a.maxp, s, k0) + r) * a.nkv + kvh) * kHd + 4 * c4;
-                kv = *reinterpret_cast<const float4 *>(a.kc + off);
-                vv = *reinterpret_cast<const float4 *>(a.vc + off);
+        __syncthreads();  // the previous tile's K and V are consumed
+        {
+            const long long row0 = kv_row(a.pages, a.maxp, s, k0);  // a key tile is one page
+            for (int i = tid; i < kKT * (kHd / 4); i += 256) {
+                const int r = i / (kHd / 4), c4 = i % (kHd / 4);
+                float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+                if (k0 + r < L) {
+                    const long long off = ((row0 + r) * a.nkv + kvh) * kHd + 4 * c4;
+                    kv = *reinterpret_cast<const float4 *>(a.kc + off);
+                    vv = *reinterpret_cast<const float4 *>(a.vc + off);
+                }
+                *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
+                Vt[(4 * c4) * kVTP + r] = vv.x;
+                Vt[(4 * c4 + 1) * kVTP + r] = vv.y;
+                Vt[(4 * c4 + 2) * kVTP + r] = vv.z;
+                Vt[(4 * c4 + 3) * kVTP + r] = vv.w;
             }
-            *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
-            *reinterpret_cast<float4 *>(Vs + r * kQP + 4 * c4) = vv;
         }
         __syncthreads();
-        float sc[4][4];
+        // S: tile t holds S[16w + 4g + e][k0 + 16t + lr]
+        f32x4_t sc[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int t = 0; t < 4; ++t) {
+            sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            const float *kr = Ks + (16 * t + lr) * kQP + 32 * lg;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) sc[r][c] = 0.f;
-        for (int d = 0; d < kHd; d += 4) {
-            float4 qv[4], kv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) qv[r] = *reinterpret_cast<const float4 *>(Qs + (4 * tr + r) * kQP + d);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) kv[c] = *reinterpret_cast<const float4 *>(Ks + (4 * tc + c) * kQP + d);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    sc[r][c] += qv[r].x * kv[c].x + qv[r].y * kv[c].y + qv[r].z * kv[c].z + qv[r].w * kv[c].w;
+            for (int i = 0; i < 8; ++i) {
+                const float4 kv = *reinterpret_cast<const float4 *>(kr + 4 * i);
+                sc[t] = mfma_f32(qa[4 * i], kv.x, sc[t]);
+                sc[t] = mfma_f32(qa[4 * i + 1], kv.y, sc[t]);
+                sc[t] = mfma_f32(qa[4 * i + 2], kv.z, sc[t]);
+                sc[t] = mfma_f32(qa[4 * i + 3], kv.w, sc[t]);
+            }
         }
         float corr[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int qp = p0 + 4 * tr + r;
+        for (int e = 0; e < 4; ++e) {
+            const int qp = p0 + 16 * wave + 4 * lg + e;
             float mx = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int kp = k0 + 4 * tc + c;
-                sc[r][c] = (kp <= qp && kp < L) ? sc[r][c] * a.scale : -INFINITY;
-                mx = fmaxf(mx, sc[r][c]);
+            for (int t = 0; t < 4; ++t) {
+                const int kp = k0 + 16 * t + lr;
+                sc[t][e] = (kp <= qp && kp < L) ? sc[t][e] * a.scale : -INFINITY;
+                mx = fmaxf(mx, sc[t][e]);
             }
             mx = row16_max(mx);
-            const float mn = fmaxf(m[r], mx);
+            const float mn = fmaxf(m[e], mx);
             // rows with no visible key yet keep m = -inf; use 0 to avoid inf - inf
             const float mref = mn == -INFINITY ? 0.f : mn;
-            corr[r] = expf(m[r] - mref);
+            corr[e] = expf(m[e] - mref);
             float ps = 0.f;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float pv = expf(sc[r][c] - mref);
-                Ps[(4 * tr + r) * kPP + 4 * tc + c] = pv;
+            for (int t = 0; t < 4; ++t) {
+                const float pv = expf(sc[t][e] - mref);
+                Pw[(4 * lg + e) * kPP + 16 * t + lr] = pv;
                 ps += pv;
             }
-            l[r] = l[r] * corr[r] + row16_sum(ps);
-            m[r] = mn;
+            l[e] = l[e] * corr[e] + row16_sum(ps);
+            m[e] = mn;
         }
-        __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int d = 0; d < 8; ++d) o[r][d] *= corr[r];
-        for (int j = 0; j < kKT; j += 4) {
-            float4 pr[4];
+            for (int e = 0; e < 4; ++e) o[t][e] *= corr[e];
+        __builtin_amdgcn_wave_barrier();  // P rows written by this wavefront only
+        // O += P V: A = P[16w + lr][16g + s], B = V[16g + s][16t + lr]
+        float pa[16];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = *reinterpret_cast<const float4 *>(Ps + (4 * tr + r) * kPP + j);
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = *reinterpret_cast<const float4 *>(Pw + lr * kPP + 16 * lg + 4 * i);
+            pa[4 * i] = v.x, pa[4 * i + 1] = v.y, pa[4 * i + 2] = v.z, pa[4 * i + 3] = v.w;
+        }
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const float4 v0 = *reinterpret_cast<const float4 *>(Vs + (j + jj) * kQP + 8 * tc);
-                const float4 v1 = *reinterpret_cast<const float4 *>(Vs + (j + jj) * kQP + 8 * tc + 4);
+        for (int t = 0; t < 8; ++t) {
+            const float *vr = Vt + (16 * t + lr) * kVTP + 16 * lg;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float pw = jj == 0 ? pr[r].x : jj == 1 ? pr[r].y : jj == 2 ? pr[r].z : pr[r].w;
-                    o[r][0] += pw * v0.x;
-                    o[r][1] += pw * v0.y;
-                    o[r][2] += pw * v0.z;
-                    o[r][3] += pw * v0.w;
-                    o[r][4] += pw * v1.x;
-                    o[r][5] += pw * v1.y;
-                    o[r][6] += pw * v1.z;
-                    o[r][7] += pw * v1.w;
-                }
+            for (int i = 0; i < 4; ++i) {
+                const float4 vv = *reinterpret_cast<const float4 *>(vr + 4 * i);
+                o[t] = mfma_f32(pa[4 * i], vv.x, o[t]);
+                o[t] = mfma_f32(pa[4 * i + 1], vv.y, o[t]);
+                o[t] = mfma_f32(pa[4 * i + 2], vv.z, o[t]);
+                o[t] = mfma_f32(pa[4 * i + 3], vv.w, o[t]);
             }
         }
+        __builtin_amdgcn_wave_barrier();  // P reads done before the next tile's writes
     }
-    // o / l, times sigmoid(gate) (qwen35.rs:1208-1210)
+    // o / l, times sigmoid(gate) (qwen35.rs:1208-1210); lane holds rows 4g + e, dims 16t + lr
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int qp = p0 + 4 * tr + r;
+    for (int e = 0; e < 4; ++e) {
+        const int qp = p0 + 16 * wave + 4 * lg + e;
         if (qp >= L) continue;
-        const long long base = ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + 8 * tc;
-        const float il = 1.0f / l[r];
+        const long long base = ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + lr;
+        const float il = 1.0f / l[e];
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            const float g = a.gate[base + d];
-            a.out[base + d] = (o[r][d] * il) * (1.0f / (1.0f + expf(-g)));
+        for (int t = 0; t < 8; ++t) {
+            const float g = a.gate[base + 16 * t];
+            a.out[base + 16 * t] = (o[t][e] * il) * (1.0f / (1.0f + expf(-g)));
         }
     }
 }
@@ -329,9 +348,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
 // ----------------------------------------------------- attention (decode) --
 
 
-// One 256-thread workgroup per (sequence, q head): scores of all keys into
-// LDS (a 16-lane group per key, 8 dims per lane), softmax, then each of 256
-// threads accumulates one (dim, key half) of p V.
 // Decode attention, split over the context (flash-decoding): workgroup
 // (sequence b, kv head, split sp) takes keys sp*kDecKeys .. +kDecKeys of b
 // for all G = nh/nkv query heads of that kv head, so each K and V row is
@@ -474,10 +490,19 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x
 // conv_step + SiLU per (token, channel) with the causal window inside the
 // token's sequence (inputs before the sequence come from its ring), then
 // beta and gate per (token, v-head) (qwen35.rs:1066-1088).
+// Grid: x = channel blocks of 256, y strides over tokens (the gates of
+// token t are written by its first channel block).
 __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a) {
-    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-    if (i < static_cast<long long>(a.T) * a.ch) {
-        const int t = static_cast<int>(i / a.ch), c = static_cast<int>(i % a.ch);
+    const int c = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
+    for (int t = blockIdx.y; t < a.T; t += gridDim.y) {
+        const long long i = static_cast<long long>(t) * a.ch + c;
+        if (c < a.Hv && blockIdx.x == 0) {
+            const long long ig = static_cast<long long>(t) * a.Hv + c;
+            a.beta[ig] = 1.0f / (1.0f + expf(-a.beta_raw[ig]));
+            const float x = a.alpha_raw[ig] + a.dt_bias[c];
+            a.gate[ig] = a.a_log[c] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+        }
+        if (c >= a.ch) continue;
         const int p = a.pos[t];
         const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
         float xin[3];
@@ -493,12 +518,6 @@ __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a) {
             a.kb[static_cast<long long>(t) * a.di + c - a.di] = to_bf16(sy);
         else
             a.vb[static_cast<long long>(t) * (a.ch - 2 * a.di) + c - 2 * a.di] = to_bf16(sy);
-    }
-    if (i < static_cast<long long>(a.T) * a.Hv) {
-        const int hv = static_cast<int>(i % a.Hv);
-        a.beta[i] = 1.0f / (1.0f + expf(-a.beta_raw[i]));
-        const float x = a.alpha_raw[i] + a.dt_bias[hv];
-        a.gate[i] = a.a_log[hv] * (x > 20.0f ? x : logf(1.0f + expf(x)));
     }
 }
 
@@ -683,8 +702,10 @@ int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, 
                       size_t T, int ch, int di, int Hv, void *stream) {
     ConvArgs a{qkv, ring, conv_w, seq, pos, beta_raw, alpha_raw, dt_bias, a_log, qb, kb, vb, beta, gate,
                static_cast<int>(T), ch, di, Hv};
-    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(blocks_for(static_cast<long long>(T) * ch, 256)), dim3(256), 0,
-                       as_stream(stream), a);
+    if (!T) return OURO_OK;
+    const int cb = (ch > Hv ? ch : Hv) + 255;
+    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(static_cast<unsigned>(cb / 256), static_cast<unsigned>(T < 65535 ? T : 65535)),
+                       dim3(256), 0, as_stream(stream), a);
     return check_launch("prefill_conv_gate_kernel");
 }
 
