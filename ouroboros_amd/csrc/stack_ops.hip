@@ -490,34 +490,53 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x
 // conv_step + SiLU per (token, channel) with the causal window inside the
 // token's sequence (inputs before the sequence come from its ring), then
 // beta and gate per (token, v-head) (qwen35.rs:1066-1088).
-// Grid: x = channel blocks of 256, y strides over tokens (the gates of
-// token t are written by its first channel block).
-__global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a) {
+// Grid: x = channel blocks of 256, y = contiguous token ranges.  A thread
+// walks its channel along its range with the last three inputs in registers
+// (each input read once), taking them from the sequence's ring at a
+// sequence start.  The gates of token t are written by channel block 0.
+__global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int per) {
     const int c = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
-    for (int t = blockIdx.y; t < a.T; t += gridDim.y) {
-        const long long i = static_cast<long long>(t) * a.ch + c;
-        if (c < a.Hv && blockIdx.x == 0) {
-            const long long ig = static_cast<long long>(t) * a.Hv + c;
+    const int ta = static_cast<int>(blockIdx.y) * per, tb = min(ta + per, a.T);
+    if (blockIdx.x == 0 && threadIdx.x < a.Hv) {
+        const int hv = threadIdx.x;
+        for (int t = ta; t < tb; ++t) {
+            const long long ig = static_cast<long long>(t) * a.Hv + hv;
             a.beta[ig] = 1.0f / (1.0f + expf(-a.beta_raw[ig]));
-            const float x = a.alpha_raw[ig] + a.dt_bias[c];
-            a.gate[ig] = a.a_log[c] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+            const float x = a.alpha_raw[ig] + a.dt_bias[hv];
+            a.gate[ig] = a.a_log[hv] * (x > 20.0f ? x : logf(1.0f + expf(x)));
         }
-        if (c >= a.ch) continue;
-        const int p = a.pos[t];
-        const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
-        float xin[3];
-#pragma unroll
-        for (int o = 1; o <= 3; ++o)
-            xin[3 - o] = p - o >= 0 ? a.qkv[(static_cast<long long>(t) - o) * a.ch + c] : r[3 + p - o];
-        const float4 w = *reinterpret_cast<const float4 *>(a.conv_w + 4LL * c);
-        const float y = w.x * xin[0] + w.y * xin[1] + w.z * xin[2] + w.w * a.qkv[i];
-        const float sy = y / (1.0f + expf(-y));
-        if (c < a.di)
-            a.qb[static_cast<long long>(t) * a.di + c] = to_bf16(sy);
-        else if (c < 2 * a.di)
-            a.kb[static_cast<long long>(t) * a.di + c - a.di] = to_bf16(sy);
+    }
+    if (c >= a.ch || ta >= tb) return;
+    const float4 w = *reinterpret_cast<const float4 *>(a.conv_w + 4LL * c);
+    const int di = a.di, dv = a.ch - 2 * a.di;
+    // window x[t-3], x[t-2], x[t-1] for the range's first token
+    float x0, x1, x2;
+    {
+        const int p = a.pos[ta];
+        const float *r = a.ring + (static_cast<long long>(a.seq[ta]) * a.ch + c) * 3;
+        x0 = p >= 3 ? a.qkv[(static_cast<long long>(ta) - 3) * a.ch + c] : r[p];
+        x1 = p >= 2 ? a.qkv[(static_cast<long long>(ta) - 2) * a.ch + c] : r[1 + p];
+        x2 = p >= 1 ? a.qkv[(static_cast<long long>(ta) - 1) * a.ch + c] : r[2];
+    }
+    for (int t = ta; t < tb; ++t) {
+        if (t > ta && a.pos[t] == 0) {  // a sequence starts: its ring is the window
+            const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
+            x0 = r[0];
+            x1 = r[1];
+            x2 = r[2];
+        }
+        const float x = a.qkv[static_cast<long long>(t) * a.ch + c];
+        const float y = w.x * x0 + w.y * x1 + w.z * x2 + w.w * x;
+        x0 = x1;
+        x1 = x2;
+        x2 = x;
+        const uint16_t sy = to_bf16(y / (1.0f + expf(-y)));
+        if (c < di)
+            a.qb[static_cast<long long>(t) * di + c] = sy;
+        else if (c < 2 * di)
+            a.kb[static_cast<long long>(t) * di + c - di] = sy;
         else
-            a.vb[static_cast<long long>(t) * (a.ch - 2 * a.di) + c - 2 * a.di] = to_bf16(sy);
+            a.vb[static_cast<long long>(t) * dv + c - 2 * di] = sy;
     }
 }
 
@@ -703,9 +722,14 @@ int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, 
     ConvArgs a{qkv, ring, conv_w, seq, pos, beta_raw, alpha_raw, dt_bias, a_log, qb, kb, vb, beta, gate,
                static_cast<int>(T), ch, di, Hv};
     if (!T) return OURO_OK;
-    const int cb = (ch > Hv ? ch : Hv) + 255;
-    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(static_cast<unsigned>(cb / 256), static_cast<unsigned>(T < 65535 ? T : 65535)),
-                       dim3(256), 0, as_stream(stream), a);
+    if (Hv > 256) return fail(OURO_ERR_SHAPE, "prefill_conv_gate: %d v-heads (<= 256)", Hv);
+    const int cb = (ch + 255) / 256;
+    // token ranges: enough workgroups to fill the chip, each range long
+    // enough that the window is refilled from memory rarely
+    const int ranges = static_cast<int>(T < 256 ? T : 256);
+    const int per = static_cast<int>((T + ranges - 1) / ranges);
+    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(static_cast<unsigned>(cb), static_cast<unsigned>((T + per - 1) / per)),
+                       dim3(256), 0, as_stream(stream), a, per);
     return check_launch("prefill_conv_gate_kernel");
 }
 
