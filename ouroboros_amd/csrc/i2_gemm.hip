@@ -32,6 +32,7 @@ constexpr int kXPitch = 272;  // LDS bytes per activation row of a 256-k block
 constexpr int kSkinnyCols = 64;  // column counts up to this use the split-k kernel
 constexpr int kSkinnyWaves = 16; // its wavefronts per workgroup (one per k block; half for > 32 columns)
 constexpr int kSkinnyGroup = 4;  // products per grouped launch
+constexpr long long kSkinnyTallTiles = 4096;  // row tiles from which a workgroup takes 4 of them
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
 
 // Few columns (N <= 64, e.g. one decode step of a batch of sequences): the
 // product is a weight stream, so every weight unit must be read once and
-// the k loop must not be a latency chain.  Workgroup = 2 row tiles (32 rows)
+// the k loop must not be a latency chain.  Workgroup = 2 (or 4) row tiles
 // x all N columns, with one wavefront per k block (up to 16; beyond that
 // each wavefront takes every 16th block), so all of a workgroup's loads are
 // in flight at once.  Wavefronts read their activation fragments straight
@@ -212,9 +213,9 @@ struct SkinnyGroup {
     int ncg;    // column groups of WC tiles; workgroup x = row block * ncg + column group
 };
 
-template <int WC>
+template <int WC, int WR>
 __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(SkinnyGroup g) {
-    constexpr int WR = 2, TR = 16 * WR, TC = 16 * WC + 1;
+    constexpr int TR = 16 * WR, TC = 16 * WC + 1;
     __shared__ int tile[TR * TC];
     const int bx = static_cast<int>(blockIdx.x) / g.ncg, cg = static_cast<int>(blockIdx.x) % g.ncg;
     int pi = 0;
@@ -330,15 +331,19 @@ GemmPick pick_gemm(int M, int N) {
     return {i2_gemm_mfma_kernel<1, 1>, 1, 1};
 }
 
-// Few-column launches: column tiles WC = ceil(N / 16) <= 4.
-SkinnyFn pick_skinny(int N) {
+// Few-column launches: column tiles WC = ceil(N / 16) <= 4; row tiles per
+// workgroup WR = 2, or 4 for very tall products, where re-reading the
+// activations once per workgroup (from L2) costs more than the weights.
+template <int WR>
+SkinnyFn pick_skinny_wr(int N) {
     switch ((N + 15) / 16) {
-    case 1: return i2_gemm_skinny_kernel<1>;
-    case 2: return i2_gemm_skinny_kernel<2>;
-    case 3: return i2_gemm_skinny_kernel<3>;
-    default: return i2_gemm_skinny_kernel<4>;
+    case 1: return i2_gemm_skinny_kernel<1, WR>;
+    case 2: return i2_gemm_skinny_kernel<2, WR>;
+    case 3: return i2_gemm_skinny_kernel<3, WR>;
+    default: return i2_gemm_skinny_kernel<4, WR>;
     }
 }
+SkinnyFn pick_skinny(int N, int wr) { return wr == 4 ? pick_skinny_wr<4>(N) : pick_skinny_wr<2>(N); }
 
 int check_mfma_shape(size_t out_len, size_t in_len) {
     if (!out_len || !in_len) return fail(OURO_ERR_SHAPE, "i2 mfma: empty shape");
@@ -396,8 +401,13 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
             return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
         g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.dscale, p.y, p.acc,
                                static_cast<int>(p.out_len)};
+    }
+    long long row_tiles = 0;
+    for (int i = 0; i < np; ++i) row_tiles += (static_cast<long long>(probs[i].out_len) + 15) / 16;
+    const int wr = row_tiles >= kSkinnyTallTiles ? 4 : 2;
+    for (int i = 0; i < np; ++i) {
         g.bstart[i] = static_cast<int>(blocks);
-        blocks += (static_cast<long long>(p.out_len + 15) / 16 + 1) / 2;
+        blocks += ((static_cast<long long>(probs[i].out_len) + 15) / 16 + wr - 1) / wr;
     }
     g.bstart[np] = static_cast<int>(blocks);
     if (blocks > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "i2 gemm group: grid too large");
@@ -413,7 +423,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
     const int maxw = skinny_waves(wc);
     const int waves = g.nkb < maxw ? g.nkb : maxw;
     if (blocks * ncg > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "i2 gemm group: grid too large");
-    hipLaunchKernelGGL(pick_skinny(16 * wc), dim3(static_cast<unsigned>(blocks * ncg)), dim3(kWave * waves), 0,
+    hipLaunchKernelGGL(pick_skinny(16 * wc, wr), dim3(static_cast<unsigned>(blocks * ncg)), dim3(kWave * waves), 0,
                        as_stream(stream), g);
     return check_launch("i2_gemm_skinny_kernel");
 }
