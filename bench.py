@@ -585,6 +585,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the hybrid-stack leg (profiling runs of the kernel legs)")
     ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "fwht", "prefill", "copy", "stack"],
                     default=None,
                     help="run one workload (for profiling)")
@@ -627,7 +629,7 @@ def main() -> int:
     if args.only in (None, "prefill"):
         log("GDN chunked prefill 4x4096")
         res["prefill"] = bench_prefill(stream, args.steps, args.warmup)
-    if args.only in (None, "stack"):
+    if args.only in (None, "stack") and not args.no_stack:
         log(f"hybrid stack: {ST_SEQS} prompts of {ST_MIN}..{ST_MAX} tokens + {ST_STEPS} decode steps")
         res["stack"] = bench_stack(stream, args.steps, args.warmup)
 
