@@ -111,6 +111,15 @@ def test_stack_long_ragged_prompts_wide_heads(gpu):
     check(WIDE, prompts, 2, max_seqs=4, max_tokens=300, max_ctx=160)
 
 
+def test_stack_many_sequences(gpu):
+    # 64 sequences: the decode step's int8 activations go out in fragment
+    # order over 4 column tiles and the few-row products split them into
+    # column groups (the configuration of the 64-sequence benchmark)
+    rng = np.random.default_rng(6)
+    prompts = [list(rng.integers(0, SMALL.n_vocab, int(n))) for n in rng.integers(1, 4, 64)]
+    check(SMALL, prompts, 2, max_seqs=64, max_tokens=256, max_ctx=16)
+
+
 def test_stack_rejects_bad_calls(gpu):
     st = Stack(SMALL, 7, max_seqs=2, max_tokens=10, max_ctx=8)
     try:
