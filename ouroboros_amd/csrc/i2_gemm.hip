@@ -35,6 +35,9 @@ constexpr int kSkinnyGroup = 4;  // products per grouped launch
 constexpr long long kSkinnyTallTiles = 4096;  // row tiles from which a workgroup takes 4 of them
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+// Register arrays of 16-byte pieces use the native vector type: arrays of
+// HIP's uint4 struct are kept in scratch memory by the compiler.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 // One thread per 32-bit word of the MFMA layout.
 __global__ void i2_tile_mfma_kernel(const uint8_t *__restrict__ canon, uint32_t *__restrict__ dst,
@@ -92,31 +95,28 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
     const int rt0 = (rb * kGemmWaves + wave) * WR;
     const int nrt = (a.M + 15) / 16;
 
-    uint4 xr[WC];
+    v4u xr[WC];
     auto load_x = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kGemmWaves * i;
-            const int n = n0 + c / 16;
-            xr[i] = n < a.N ? *reinterpret_cast<const uint4 *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb +
-                                                               16 * (c % 16))
-                            : make_uint4(0u, 0u, 0u, 0u);
+            const int n = min(n0 + c / 16, a.N - 1);  // clamped: columns past N are never stored
+            xr[i] = *reinterpret_cast<const v4u *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb + 16 * (c % 16));
         }
     };
     auto store_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kGemmWaves * i;
-            *reinterpret_cast<uint4 *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
+            *reinterpret_cast<v4u *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
         }
     };
-    uint4 wr[WR];
+    v4u wr[WR];
     auto load_w = [&](int kb) {
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
-            const int rt = rt0 + r;
-            wr[r] = rt < nrt ? a.w[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane]
-                             : make_uint4(0u, 0u, 0u, 0u);
+            const int rt = min(rt0 + r, nrt - 1);  // clamped: rows past M are never stored
+            wr[r] = reinterpret_cast<const v4u *>(a.w)[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane];
         }
     };
 
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
     store_x(0);
     __syncthreads();
     for (int kb = 0; kb < a.nkb; ++kb) {
-        uint4 wc[WR];
+        v4u wc[WR];
 #pragma unroll
         for (int r = 0; r < WR; ++r) wc[r] = wr[r];
         const bool more = kb + 1 < a.nkb;
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
             v4i A[WR];
 #pragma unroll
             for (int r = 0; r < WR; ++r) {
-                const uint32_t wd = s == 0 ? wc[r].x : s == 1 ? wc[r].y : s == 2 ? wc[r].z : wc[r].w;
+                const uint32_t wd = s == 0 ? wc[r][0] : s == 1 ? wc[r][1] : s == 2 ? wc[r][2] : wc[r][3];
                 A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
                            static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
             }
@@ -180,6 +180,154 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
                 if (a.acc) a.acc[o] = total;
             }
         }
+    }
+}
+
+// Large products (prefill projections, thousands of columns) on
+// v_mfma_i32_32x32x32_i8, which sustains ~1.4x the rate of the 16x16x64
+// form on MI355X.  Workgroup tile 256 rows x 128 columns: four wavefronts
+// stacked along the rows, each with a 64 x 128 register tile (2 x 4 MFMA
+// tiles of 32 x 32), so each decoded weight fragment feeds 4 MFMAs (the
+// 2-bit decode is the VALU work that competes with the MFMA issue) and each
+// 16-byte activation fragment from LDS feeds 2.
+//
+// The weights stay in the 16-row unit layout: the 32x32x32 A operand of
+// lane l is row l % 32 and 16 k values chosen per lane, so lane l reads
+// lane slot (l % 16) + 16 (2p + l / 32) of unit 2 RT + (l % 32) / 16 for
+// p = 0, 1; word s of that slot is MFMA step (s, p) over k = 64 s + 32 p +
+// 16 (l / 32) + 0..15, and the B operand reads the same 16 activation bytes
+// of column l % 32.  D lane l register e: column l % 32, row
+// 8 (e / 4) + 4 (l / 32) + e % 4.
+//
+// The activation tile of a 256-deep k block (32 KiB) is double-buffered in
+// LDS; activations and weights are prefetched a k block ahead in registers
+// (indices clamped, not guarded, so the loads are unconditional and the
+// waits count them exactly).  Workgroups are handed out XCD by XCD
+// (blockIdx % 8 is the XCD): each XCD takes a contiguous run of tiles, row
+// blocks fastest, so the 128 activation columns a run shares stay in that
+// XCD's L2.
+typedef int v16i __attribute__((ext_vector_type(16)));
+constexpr int kBigTM = 2, kBigTN = 4;  // 32 x 32 MFMA tiles per wavefront
+constexpr int kBigCols = kBigTN * 32;  // columns per workgroup (rows: 4 kBigTM 32)
+constexpr int kBigMinBlocks = 192;  // fewer tiles than this: the 16x16 kernel (faster there)
+
+__global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void i2_gemm_big_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][kBigCols * kXPitch];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nblk = static_cast<int>(gridDim.x), xcd = static_cast<int>(blockIdx.x) % 8;
+    const int q8 = nblk / 8, r8 = nblk % 8;
+    const int t = xcd * q8 + min(xcd, r8) + static_cast<int>(blockIdx.x) / 8;
+    const int rb = t % a.nrb, cb = t / a.nrb;
+    const int n0 = cb * kBigCols;
+    const int RT0 = (rb * kGemmWaves + wave) * kBigTM;  // the wavefront's first 32-row tile
+    const int nrt = (a.M + 15) / 16;
+    const int half = (lane & 31) >> 4, g = lane >> 5;
+
+    constexpr int XV = kBigCols * 16 / (kWave * kGemmWaves);  // 16-byte pieces per thread per k block
+    v4u xr[XV], wr[kBigTM][2];
+    auto load_x = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int c = tid + kWave * kGemmWaves * i;
+            const int n = min(n0 + c / 16, a.N - 1);  // clamped: columns past N are never stored
+            xr[i] = *reinterpret_cast<const v4u *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb + 16 * (c % 16));
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XV; ++i) {
+            const int c = tid + kWave * kGemmWaves * i;
+            *reinterpret_cast<v4u *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
+        }
+    };
+    auto load_w = [&](int kb) {
+#pragma unroll
+        for (int r = 0; r < kBigTM; ++r) {
+            const int rt = min(2 * (RT0 + r) + half, nrt - 1);  // clamped: rows past M are never stored
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+                wr[r][p] = reinterpret_cast<const v4u *>(
+                    a.w)[(static_cast<long long>(rt) * a.nkb + kb) * kWave + (lane & 15) + 16 * (2 * p + g)];
+        }
+    };
+
+    v16i acc[kBigTM][kBigTN];
+#pragma unroll
+    for (int r = 0; r < kBigTM; ++r)
+#pragma unroll
+        for (int c = 0; c < kBigTN; ++c)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[r][c][e] = 0;
+
+    load_x(0);
+    load_w(0);
+    store_x(0);
+    __syncthreads();
+    for (int kb = 0; kb < a.nkb; ++kb) {
+        v4u wc[kBigTM][2];
+#pragma unroll
+        for (int r = 0; r < kBigTM; ++r) wc[r][0] = wr[r][0], wc[r][1] = wr[r][1];
+        const bool more = kb + 1 < a.nkb;
+        if (more) {
+            load_x(kb + 1);
+            load_w(kb + 1);
+        }
+        const uint8_t *xb = xs[kb & 1] + (lane & 31) * kXPitch + 16 * g;
+#pragma unroll
+        for (int sp = 0; sp < 8; ++sp) {
+            const int s = sp / 2, p = sp % 2;  // MFMA step (s, p): k = 64 s + 32 p + 16 g
+            v4i A[kBigTM];
+#pragma unroll
+            for (int r = 0; r < kBigTM; ++r) {
+                const uint32_t wd = wc[r][p][s];
+                A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
+                           static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+            }
+#pragma unroll
+            for (int c = 0; c < kBigTN; ++c) {
+                const v4i B = *reinterpret_cast<const v4i *>(xb + c * 32 * kXPitch + 32 * sp);
+#pragma unroll
+                for (int r = 0; r < kBigTM; ++r)
+                    acc[r][c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[r], B, acc[r][c], 0, 0, 0);
+            }
+        }
+        if (more) store_x((kb + 1) & 1);
+        __syncthreads();
+    }
+
+    // registers 4q .. 4q+3 of a tile are 4 consecutive rows of one column,
+    // contiguous in y: a full quad goes out as one 16-byte store
+    const float wscale = *a.w_scale;
+    const bool quad = (a.M % 4) == 0 && !a.acc && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+#pragma unroll
+    for (int c = 0; c < kBigTN; ++c) {
+        const int n = n0 + c * 32 + (lane & 31);
+        if (n >= a.N) continue;
+        const float ds = a.dscale[n];
+#pragma unroll
+        for (int r = 0; r < kBigTM; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int row = (RT0 + r) * 32 + 8 * q + 4 * g;
+                const long long o = static_cast<long long>(n) * a.M + row;
+                if (quad && row + 3 < a.M) {
+                    float4 v;
+                    v.x = (static_cast<float>(-(acc[r][c][4 * q] >> 6)) * ds) * wscale;
+                    v.y = (static_cast<float>(-(acc[r][c][4 * q + 1] >> 6)) * ds) * wscale;
+                    v.z = (static_cast<float>(-(acc[r][c][4 * q + 2] >> 6)) * ds) * wscale;
+                    v.w = (static_cast<float>(-(acc[r][c][4 * q + 3] >> 6)) * ds) * wscale;
+                    *reinterpret_cast<float4 *>(a.y + o) = v;
+                    continue;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (row + e >= a.M) break;
+                    const int total = -(acc[r][c][4 * q + e] >> 6);
+                    a.y[o + e] = (static_cast<float>(total) * ds) * wscale;
+                    if (a.acc) a.acc[o + e] = total;
+                }
+            }
     }
 }
 
@@ -455,8 +603,19 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
         const GemmProblem one{w_mfma, out_len, w_scale, xq, dscale, y, acc};
         return i2_gemm_skinny_group(&one, 1, in_len, ncols, x_tiled, stream);
     }
-    const GemmPick p = pick_gemm(a.M, a.N);
     const int nrt = (a.M + 15) / 16;
+    {
+        const long long nrb = (nrt + 8LL * kBigTM - 1) / (8LL * kBigTM);  // 16-row tiles per workgroup: 8 kBigTM
+        const long long big = nrb * ((a.N + kBigCols - 1) / kBigCols);
+        if (big >= kBigMinBlocks) {
+            if (big > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: grid too large");
+            a.nrb = static_cast<int>(nrb);
+            hipLaunchKernelGGL(i2_gemm_big_kernel, dim3(static_cast<unsigned>(big)), dim3(kWave * kGemmWaves), 0,
+                               as_stream(stream), a);
+            return check_launch("i2_gemm_big_kernel");
+        }
+    }
+    const GemmPick p = pick_gemm(a.M, a.N);
     a.nrb = (nrt + kGemmWaves * p.wr - 1) / (kGemmWaves * p.wr);
     const long long ncb = (a.N + 16LL * p.wc - 1) / (16LL * p.wc);
     const long long grid = static_cast<long long>(a.nrb) * ncb;

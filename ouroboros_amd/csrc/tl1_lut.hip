@@ -27,6 +27,7 @@ namespace {
 constexpr int kGB = 4;                 // groups per block
 constexpr int kChunks = kGB * 28 / 16; // 7 x 16 B per row per block
 constexpr int kThreads = 1024;
+constexpr int kAhead = 1;             // tiles of weights in flight per wave (deeper is slower)
 constexpr int kTable = kGB * 26 * 256; // floats
 constexpr int LUT_LDS = kTable * 4 + kGB * 128 * 4;
 
@@ -72,25 +73,28 @@ __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const
     const int tid = threadIdx.x;
     for (int i = tid; i < gcnt * 128; i += kThreads) xs[i] = x[b * kGB * 128 + i];
     __syncthreads();
-    for (int e = tid; e < gcnt * 26 * 256; e += kThreads) {
-        const int v = e & 255, bb = (e >> 8) % 26, g = e / (26 * 256);
-        int base, stride, cnt;
-        if (bb < 16) {
-            base = bb, stride = 16, cnt = 5;
-        } else if (bb < 24) {
-            base = 80 + (bb - 16), stride = 8, cnt = 5;
-        } else {
-            base = 120 + (bb - 24), stride = 2, cnt = 4;
-        }
-        const float *xg = xs + g * 128 + base;
-        float s = 0.f;
-        uint32_t p3 = 1;
+    // thread (g = tid / 256, v = tid % 256) decodes byte value v once and
+    // fills T[g][bb][v] for the 26 byte positions (x reads are broadcasts)
+    static_assert(kThreads == kGB * 256, "one thread per (group, byte value)");
+    {
+        const int v = tid & 255, g = tid >> 8;
+        if (g < gcnt) {
+            float tr[5];
+            uint32_t p3 = 1;
 #pragma unroll
-        for (int n = 0; n < 5; ++n) {
-            if (n < cnt) s += static_cast<float>(tl1_trit(v, p3)) * xg[n * stride];
-            p3 *= 3;
+            for (int n = 0; n < 5; ++n, p3 *= 3) tr[n] = static_cast<float>(tl1_trit(static_cast<uint32_t>(v), p3));
+            const float *xg = xs + g * 128;
+            float *Tg = T + g * 26 * 256 + v;
+#pragma unroll
+            for (int bb = 0; bb < 26; ++bb) {
+                const int base = bb < 16 ? bb : bb < 24 ? 80 + (bb - 16) : 120 + (bb - 24);
+                const int stride = bb < 16 ? 16 : bb < 24 ? 8 : 2;
+                float s = 0.f;
+#pragma unroll
+                for (int n = 0; n < (bb < 24 ? 5 : 4); ++n) s += tr[n] * xg[base + n * stride];
+                Tg[bb * 256] = s;
+            }
         }
-        T[e] = s;
     }
     __syncthreads();
 
@@ -99,40 +103,49 @@ __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const
     const int wstride = gridDim.x * (kThreads / 64);
     const uint4 *wb = w + static_cast<long long>(b) * ntiles * kChunks * 64;
     float *pb = partial + static_cast<long long>(b) * out_len;
-    // the next tile's 112 bytes are loaded while the current one is looked up
-    uint4 nx[kChunks];
-    auto load_tile = [&](int tile) {
+    // a wave keeps the 112-byte rows of its next kAhead tiles in flight
+    // while it looks up the current one
+    uint4 nx[kAhead][kChunks];
+    auto load_tile = [&](uint4 (&dst)[kChunks], int tile) {
         const uint4 *src = wb + static_cast<long long>(tile) * kChunks * 64 + lane;
 #pragma unroll
-        for (int c = 0; c < kChunks; ++c) nx[c] = src[c * 64];
+        for (int c = 0; c < kChunks; ++c) dst[c] = src[c * 64];
     };
-    if (wglobal < ntiles) load_tile(wglobal);
-    for (int tile = wglobal; tile < ntiles; tile += wstride) {
-        uint32_t u[kChunks * 4];
 #pragma unroll
-        for (int c = 0; c < kChunks; ++c) {
-            u[4 * c] = nx[c].x, u[4 * c + 1] = nx[c].y, u[4 * c + 2] = nx[c].z, u[4 * c + 3] = nx[c].w;
-        }
-        if (tile + wstride < ntiles) load_tile(tile + wstride);
-        float acc = 0.f;
+    for (int a = 0; a < kAhead; ++a)
+        if (wglobal + a * wstride < ntiles) load_tile(nx[a], wglobal + a * wstride);
+    for (int tile0 = wglobal; tile0 < ntiles; tile0 += kAhead * wstride) {
 #pragma unroll
-        for (int g = 0; g < kGB; ++g) {
-            if (g < gcnt) {
-                const float *Tg = T + g * 26 * 256;
-                float gs = 0.f;
+        for (int a = 0; a < kAhead; ++a) {
+            const int tile = tile0 + a * wstride;  // wave-uniform
+            if (tile >= ntiles) break;
+            uint32_t u[kChunks * 4];
 #pragma unroll
-                for (int bb = 0; bb < 26; ++bb) {
-                    const int by = g * 28 + bb;  // byte within the row's 112
-                    const uint32_t v = (u[by >> 2] >> (8 * (by & 3))) & 0xffu;
-                    gs += Tg[bb * 256 + v];
-                }
-                const uint32_t dw = u[(g * 28 + 24) >> 2] >> 16;  // bytes 26, 27 of the group
-                const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dw)));
-                acc += d * gs;
+            for (int c = 0; c < kChunks; ++c) {
+                u[4 * c] = nx[a][c].x, u[4 * c + 1] = nx[a][c].y, u[4 * c + 2] = nx[a][c].z,
+                u[4 * c + 3] = nx[a][c].w;
             }
+            if (tile + kAhead * wstride < ntiles) load_tile(nx[a], tile + kAhead * wstride);
+            float acc = 0.f;
+#pragma unroll
+            for (int g = 0; g < kGB; ++g) {
+                if (g < gcnt) {
+                    const float *Tg = T + g * 26 * 256;
+                    float gs = 0.f;
+#pragma unroll
+                    for (int bb = 0; bb < 26; ++bb) {
+                        const int by = g * 28 + bb;  // byte within the row's 112
+                        const uint32_t v = (u[by >> 2] >> (8 * (by & 3))) & 0xffu;
+                        gs += Tg[bb * 256 + v];
+                    }
+                    const uint32_t dw = u[(g * 28 + 24) >> 2] >> 16;  // bytes 26, 27 of the group
+                    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dw)));
+                    acc += d * gs;
+                }
+            }
+            const int row = tile * 64 + lane;
+            if (row < out_len) pb[row] = acc;
         }
-        const int row = tile * 64 + lane;
-        if (row < out_len) pb[row] = acc;
     }
 }
 

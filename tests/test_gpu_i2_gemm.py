@@ -31,7 +31,7 @@ def test_tile_mfma_matches_oracle(gpu, orc, out_len, in_len):
 @pytest.mark.parametrize("out_len,in_len,ncols", [(6912, 2560, 1), (6912, 2560, 16), (6912, 2560, 100),
                                                   (2560, 6912, 33), (37, 256, 5), (1000, 1024, 64),
                                                   (130, 5120, 17), (17, 768, 300), (4096, 4096, 256),
-                                                  (8, 2048, 2)])
+                                                  (8, 2048, 2), (4000, 256, 3000), (4002, 256, 3000)])
 def test_gemm_i2_mfma_bit_exact(gpu, orc, out_len, in_len, ncols):
     rng = np.random.default_rng(out_len * 5 + in_len + ncols)
     w, x, w_scale = make_case(rng, out_len, in_len, ncols)
@@ -44,6 +44,22 @@ def test_gemm_i2_mfma_bit_exact(gpu, orc, out_len, in_len, ncols):
     acc = DeviceBuffer((ncols * out_len,), np.int32)
     ops.gemm_i2_mfma(payload, out_len, in_len, xq, ds, ncols, y, acc)
     assert np.array_equal(acc.download(), want_acc.reshape(-1))
+    assert np.array_equal(y.download().view(np.uint32), want_y.reshape(-1).view(np.uint32))
+
+
+@pytest.mark.parametrize("out_len,ncols", [(4000, 3000), (2560, 4096)])
+def test_gemm_i2_mfma_large_no_acc(gpu, orc, out_len, ncols):
+    # 256 x 128 workgroup tiles (partial row and column tiles in the first
+    # case) storing y four rows at a time, which the int32 output turns off
+    rng = np.random.default_rng(out_len + ncols)
+    in_len = 512
+    w, x, w_scale = make_case(rng, out_len, in_len, ncols)
+    canon = orc.i2_pack(w)
+    xq_h, ds_h = orc.act_quant_i8(x)
+    _, want_y = orc.gemm_i2(canon, out_len, in_len, xq_h, ds_h, w_scale)
+    payload = ops.i2_mfma_payload(canon, out_len, in_len, float(w_scale))
+    y = DeviceBuffer((ncols * out_len,), np.float32)
+    ops.gemm_i2_mfma(payload, out_len, in_len, DeviceBuffer.from_host(xq_h), DeviceBuffer.from_host(ds_h), ncols, y)
     assert np.array_equal(y.download().view(np.uint32), want_y.reshape(-1).view(np.uint32))
 
 
