@@ -80,35 +80,63 @@ struct GemmArgs {
     int x_tiled;           // xq in the few-column fragment order (ceil(N/16) column tiles)
 };
 
+// Up to four products with the same k and column count in one launch of the
+// 16x16 kernel: workgroups bstart[p] .. bstart[p+1]-1 belong to product p.
+constexpr int kMfmaGroup = 4;
+static_assert(kMfmaGroup >= kSkinnyGroup, "a few-column group fits one 16x16 launch");
+struct MfmaGroup {
+    GemmArgs p[kMfmaGroup];
+    int bstart[kMfmaGroup + 1];
+    int np;
+};
+
 // Block: 4 wavefronts stacked along rows; wavefront w owns row tiles
 // (4*rb + w)*WR .. +WR-1 and the block's WC column tiles of 16 columns.
 // Per 256-deep k block: the block copies its WC*16 activation rows into
 // one of two LDS buffers (prefetched a block ahead in registers), every
 // wavefront loads its WR 1 KiB weight units (also a block ahead), and runs
-// 4 steps x WR x WC MFMAs.
-template <int WR, int WC>
-__global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArgs a) {
+// 4 steps x WR x WC MFMAs.  XT: the activations are in the few-column
+// fragment order, whose 1 KiB pieces (k block, step, column tile) are the
+// MFMA B operands lane by lane; they are copied to LDS as they are and read
+// back at lane * 16.  A launch may hold several products (MfmaGroup).
+template <int WR, int WC, bool XT>
+__global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGroup grp) {
     __shared__ __attribute__((aligned(16))) uint8_t xs[2][WC * 16 * kXPitch];
+    static_assert(WC * 4 * 1024 <= WC * 16 * kXPitch, "fragment-ordered tile fits the LDS buffer");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rb = blockIdx.x % a.nrb, cb = blockIdx.x / a.nrb;
+    int pi = 0;
+    while (pi + 1 < grp.np && static_cast<int>(blockIdx.x) >= grp.bstart[pi + 1]) ++pi;
+    const GemmArgs &a = grp.p[pi];
+    const int local = static_cast<int>(blockIdx.x) - grp.bstart[pi];
+    const int rb = local % a.nrb, cb = local / a.nrb;
     const int n0 = cb * WC * 16;
     const int rt0 = (rb * kGemmWaves + wave) * WR;
     const int nrt = (a.M + 15) / 16;
+    const int tiles = (a.N + 15) / 16;
 
     v4u xr[WC];
     auto load_x = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kGemmWaves * i;
-            const int n = min(n0 + c / 16, a.N - 1);  // clamped: columns past N are never stored
-            xr[i] = *reinterpret_cast<const v4u *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb + 16 * (c % 16));
+            if (XT) {
+                // piece c: step c / (64 WC), column tile c / 64 % WC, lane c % 64
+                const int ct = min(n0 / 16 + (c / 64) % WC, tiles - 1);  // clamped: never stored
+                xr[i] = *reinterpret_cast<const v4u *>(
+                    a.xq + ((static_cast<long long>(kb) * 4 + c / (64 * WC)) * tiles + ct) * 1024 + (c % 64) * 16);
+            } else {
+                const int n = min(n0 + c / 16, a.N - 1);  // clamped: columns past N are never stored
+                xr[i] = *reinterpret_cast<const v4u *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb +
+                                                       16 * (c % 16));
+            }
         }
     };
     auto store_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kGemmWaves * i;
-            *reinterpret_cast<v4u *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
+            const int off = XT ? 16 * c : (c / 16) * kXPitch + 16 * (c % 16);
+            *reinterpret_cast<v4u *>(&xs[buf][off]) = xr[i];
         }
     };
     v4u wr[WR];
@@ -139,7 +167,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
             load_x(kb + 1);
             load_w(kb + 1);
         }
-        const uint8_t *xb = xs[kb & 1] + (lane & 15) * kXPitch + 16 * (lane >> 4);
+        const uint8_t *xb = XT ? xs[kb & 1] + 16 * lane : xs[kb & 1] + (lane & 15) * kXPitch + 16 * (lane >> 4);
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             v4i A[WR];
@@ -151,7 +179,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(GemmArg
             }
 #pragma unroll
             for (int c = 0; c < WC; ++c) {
-                const v4i B = *reinterpret_cast<const v4i *>(xb + c * 16 * kXPitch + 64 * s);
+                const v4i B = *reinterpret_cast<const v4i *>(XT ? xb + (s * WC + c) * 1024 : xb + c * 16 * kXPitch + 64 * s);
 #pragma unroll
                 for (int r = 0; r < WR; ++r)
                     acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B, acc[r][c], 0, 0, 0);
@@ -454,7 +482,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
     }
 }
 
-using GemmFn = void (*)(GemmArgs);
+using GemmFn = void (*)(MfmaGroup);
 using SkinnyFn = void (*)(SkinnyGroup);
 
 struct GemmPick {
@@ -467,16 +495,50 @@ struct GemmPick {
 // largest wavefront tile (2x4: 32 rows x 64 columns, 8 MFMAs per pair of
 // fragment loads) while it still gives >= 1024 workgroups, then 2x2 while
 // >= 512, else 1x1 (16x16 per wavefront, the most workgroups, which is what
-// few columns need).
-GemmPick pick_gemm(int M, int N) {
-    const int nrt = (M + 15) / 16;
+// few columns need).  nrt = row tiles of all products of the launch.
+template <bool XT>
+GemmPick pick_gemm_xt(long long nrt, int N) {
     const auto blocks = [&](int wr, int wc) {
         const long long nrb = (nrt + kGemmWaves * wr - 1) / (kGemmWaves * wr);
         return nrb * ((N + 16 * wc - 1) / (16 * wc));
     };
-    if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4>, 2, 4};
-    if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2>, 2, 2};
-    return {i2_gemm_mfma_kernel<1, 1>, 1, 1};
+    if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4, XT>, 2, 4};
+    if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2, XT>, 2, 2};
+    return {i2_gemm_mfma_kernel<1, 1, XT>, 1, 1};
+}
+
+// One launch of the 16x16 kernel over np products (shared k, column count
+// and activation layout); shapes are checked by the callers.
+int launch_mfma_group(const GemmArgs *args, int np, void *stream) {
+    long long nrt = 0;
+    for (int i = 0; i < np; ++i) nrt += (args[i].M + 15) / 16;
+    const int N = args[0].N;
+    const GemmPick p = args[0].x_tiled ? pick_gemm_xt<true>(nrt, N) : pick_gemm_xt<false>(nrt, N);
+    const long long ncb = (N + 16LL * p.wc - 1) / (16LL * p.wc);
+    MfmaGroup g{};
+    g.np = np;
+    long long grid = 0;
+    for (int i = 0; i < np; ++i) {
+        g.p[i] = args[i];
+        g.p[i].nrb = ((args[i].M + 15) / 16 + kGemmWaves * p.wr - 1) / (kGemmWaves * p.wr);
+        g.bstart[i] = static_cast<int>(grid);
+        grid += static_cast<long long>(g.p[i].nrb) * ncb;
+        if (grid > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: grid too large");
+    }
+    g.bstart[np] = static_cast<int>(grid);
+    hipLaunchKernelGGL(p.fn, dim3(static_cast<unsigned>(grid)), dim3(kWave * kGemmWaves), 0, as_stream(stream), g);
+    return check_launch("i2_gemm_mfma_kernel");
+}
+
+// Few columns: the split-k kernel below unless the launch is tall (its
+// activation re-reads grow with the rows) and has more than 32 columns (16
+// on the tallest weights); the 16x16 kernel then streams the activations
+// once per 64 rows.  Short products (2560 rows, some with 6912-deep k) keep
+// the split-k kernel, which spreads k over the waves (sweeps on MI355X at
+// 8 .. 64 columns, 2560 .. 248320 rows, singly and in the hybrid stack).
+constexpr long long kFewColsMfmaTiles = 640;
+bool few_cols_on_mfma(int N, long long row_tiles) {
+    return (N > 32 && row_tiles >= kFewColsMfmaTiles) || (N > 16 && row_tiles >= kSkinnyTallTiles);
 }
 
 // Few-column launches: column tiles WC = ceil(N / 16) <= 4; row tiles per
@@ -552,6 +614,14 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
     }
     long long row_tiles = 0;
     for (int i = 0; i < np; ++i) row_tiles += (static_cast<long long>(probs[i].out_len) + 15) / 16;
+    if (few_cols_on_mfma(g.N, row_tiles)) {
+        GemmArgs args[kMfmaGroup];
+        for (int i = 0; i < np; ++i)
+            args[i] = GemmArgs{reinterpret_cast<const uint4 *>(probs[i].w), probs[i].w_scale, probs[i].xq,
+                               probs[i].dscale, probs[i].y, probs[i].acc, static_cast<int>(probs[i].out_len),
+                               g.K, g.N, g.nkb, 0, x_tiled};
+        return launch_mfma_group(args, np, stream);
+    }
     const int wr = row_tiles >= kSkinnyTallTiles ? 4 : 2;
     for (int i = 0; i < np; ++i) {
         g.bstart[i] = static_cast<int>(blocks);
@@ -615,13 +685,7 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
             return check_launch("i2_gemm_big_kernel");
         }
     }
-    const GemmPick p = pick_gemm(a.M, a.N);
-    a.nrb = (nrt + kGemmWaves * p.wr - 1) / (kGemmWaves * p.wr);
-    const long long ncb = (a.N + 16LL * p.wc - 1) / (16LL * p.wc);
-    const long long grid = static_cast<long long>(a.nrb) * ncb;
-    if (grid > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: grid too large");
-    hipLaunchKernelGGL(p.fn, dim3(static_cast<unsigned>(grid)), dim3(kWave * kGemmWaves), 0, as_stream(stream), a);
-    return check_launch("i2_gemm_mfma_kernel");
+    return launch_mfma_group(&a, 1, stream);
 }
 
 }  // namespace ouro

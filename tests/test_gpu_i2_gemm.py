@@ -26,12 +26,13 @@ def test_tile_mfma_matches_oracle(gpu, orc, out_len, in_len):
     assert got[tb:tb + 4].view(np.float32)[0] == np.float32(1.25)
 
 
-# Column counts cover every launch shape (<= 16, <= 32, > 32 columns) and
-# partial column and row tiles.
+# Column counts cover every launch shape (<= 16, <= 32, > 32 columns; few
+# columns on tall weights; 256 x 128 tiles) and partial column and row tiles.
 @pytest.mark.parametrize("out_len,in_len,ncols", [(6912, 2560, 1), (6912, 2560, 16), (6912, 2560, 100),
                                                   (2560, 6912, 33), (37, 256, 5), (1000, 1024, 64),
                                                   (130, 5120, 17), (17, 768, 300), (4096, 4096, 256),
-                                                  (8, 2048, 2), (4000, 256, 3000), (4002, 256, 3000)])
+                                                  (8, 2048, 2), (4000, 256, 3000), (4002, 256, 3000),
+                                                  (12000, 512, 40), (66000, 256, 20)])
 def test_gemm_i2_mfma_bit_exact(gpu, orc, out_len, in_len, ncols):
     rng = np.random.default_rng(out_len * 5 + in_len + ncols)
     w, x, w_scale = make_case(rng, out_len, in_len, ncols)

@@ -111,13 +111,22 @@ def test_stack_long_ragged_prompts_wide_heads(gpu):
     check(WIDE, prompts, 2, max_seqs=4, max_tokens=300, max_ctx=160)
 
 
-def test_stack_many_sequences(gpu):
-    # 64 sequences: the decode step's int8 activations go out in fragment
-    # order over 4 column tiles and the few-row products split them into
-    # column groups (the configuration of the 64-sequence benchmark)
+# a wide FFN: its up/gate pair (10752 rows) is tall enough for the 16x16
+# MFMA kernel at more than 32 columns
+FFN_TALL = Card(n_layer=2, n_embd=256, n_ff=5376, n_vocab=512, full_attention_interval=2, n_head=2, n_head_kv=1,
+                n_rot=64, ssm_n_k_heads=1, ssm_n_v_heads=2, eps=1e-6, rope_base=1e7)
+
+
+@pytest.mark.parametrize("card,nseq", [(SMALL, 64), (FFN_TALL, 40), (FFN_TALL, 64)])
+def test_stack_many_sequences(gpu, card, nseq):
+    # more than 32 sequences: the decode step's int8 activations go out in
+    # fragment order over 3 or 4 column tiles (the last one partial for 40);
+    # the short products split k over the waves, the wide FFN's up/gate pair
+    # runs on the grouped 16x16 MFMA kernel (64 sequences is the
+    # configuration of the 64-sequence benchmark)
     rng = np.random.default_rng(6)
-    prompts = [list(rng.integers(0, SMALL.n_vocab, int(n))) for n in rng.integers(1, 4, 64)]
-    check(SMALL, prompts, 2, max_seqs=64, max_tokens=256, max_ctx=16)
+    prompts = [list(rng.integers(0, card.n_vocab, int(n))) for n in rng.integers(1, 4, nseq)]
+    check(card, prompts, 2, max_seqs=64, max_tokens=256, max_ctx=16)
 
 
 def test_stack_rejects_bad_calls(gpu):
