@@ -353,8 +353,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
 // for all G = nh/nkv query heads of that kv head, so each K and V row is
 // read once per step.  Scores: 16 lanes per key (8 dims each, G dot
 // products, DPP row sums), 4 keys per wavefront per step, into LDS; per-head
-// max and exp-sum over the split; P V with lane = 2 dims and the 4
-// wavefronts on interleaved keys, reduced through LDS.  The split's
+// max and exp-sum over the split; P V with lane = 4 dims, two keys per
+// wavefront load and the 4 wavefronts on interleaved keys, reduced through
+// LDS.  The split's
 // unnormalised output, max and sum go to `part`; attn_combine_kernel merges
 // the splits of each (b, head) and applies the sigmoid output gate.
 constexpr int kDecKeys = 256;
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     __shared__ float ml[G][2];
     __shared__ long long prow[kDecKeys / kPage];  // first cache row of each page of the split
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
+    const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int L = a.lens[b];
     const int j0 = sp * kDecKeys;
     if (j0 >= L) return;  // whole workgroup
@@ -382,23 +383,23 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
         q[g][0] = *reinterpret_cast<const float4 *>(qp);
         q[g][1] = *reinterpret_cast<const float4 *>(qp + 4);
     }
-    // scores: wave w, step it -> key w*64 + 4*it + g4 (wave w reads page w of the split)
-    const long long wrow = wave * kPage < n ? prow[wave] : 0;
-#pragma unroll 4
-    for (int it = 0; it < 16; ++it) {
-        const int j = wave * 64 + 4 * it + g4;
-        float4 k0 = make_float4(0.f, 0.f, 0.f, 0.f), k1 = k0;
-        if (j < n) {
-            const float *kp = a.kc + ((wrow + 4 * it + g4) * a.nkv + kvh) * kHd + 8 * gl;
-            k0 = *reinterpret_cast<const float4 *>(kp);
-            k1 = *reinterpret_cast<const float4 *>(kp + 4);
-        }
+    // scores: wave w, step it -> key w*64 + 4*it + g4 (wave w reads page w of
+    // the split); rows past the split are clamped to its last key, so the
+    // loads carry no branches, and their scores are not stored
+    const int wkeys = min(kPage, n - wave * kPage);  // keys of this wave's page (<= 0: none)
+    const long long wrow = wkeys > 0 ? prow[wave] : 0;
+#pragma unroll 8
+    for (int it = 0; it < (wkeys > 0 ? 16 : 0); ++it) {
+        const int jj = 4 * it + g4;
+        const float *kp = a.kc + ((wrow + min(jj, max(wkeys - 1, 0))) * a.nkv + kvh) * kHd + 8 * gl;
+        const float4 k0 = *reinterpret_cast<const float4 *>(kp);
+        const float4 k1 = *reinterpret_cast<const float4 *>(kp + 4);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float d = q[g][0].x * k0.x + q[g][0].y * k0.y + q[g][0].z * k0.z + q[g][0].w * k0.w +
                       q[g][1].x * k1.x + q[g][1].y * k1.y + q[g][1].z * k1.z + q[g][1].w * k1.w;
             d = row16_sum(d);
-            if (gl == 0 && j < n) sc[g][j] = d * a.scale;
+            if (gl == 0 && jj < wkeys) sc[g][wave * 64 + jj] = d * a.scale;
         }
     }
     __syncthreads();
@@ -422,24 +423,39 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
         }
     }
     __syncthreads();
-    // P V: wave w takes keys w, w+4, ...; lane owns dims 2*lane, 2*lane+1
-    float2 acc[G];
+    // P V: wave w, half h (lanes 32h .. 32h+31) take keys 2w + h, +8, ...;
+    // lane owns dims 4 (lane % 32) .. +3, so one load instruction reads two
+    // whole 512-byte rows; the halves are added at the end
+    const int h = lane >> 5, d4 = 4 * (lane & 31);
+    float4 acc[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[g] = make_float2(0.f, 0.f);
-    const float *vp = a.vc + kvh * kHd + 2 * lane;
+    for (int g = 0; g < G; ++g) acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float *vp = a.vc + kvh * kHd + d4;
     const long long vstride = static_cast<long long>(a.nkv) * kHd;
-#pragma unroll 4
-    for (int j = wave; j < n; j += 4) {
-        const float2 v = *reinterpret_cast<const float2 *>(vp + (prow[j / kPage] + j % kPage) * vstride);
+#pragma unroll 8
+    for (int j0 = 2 * wave; j0 < n; j0 += 8) {
+        const int j = min(j0 + h, n - 1);  // clamped; its weight is zeroed
+        const float4 v = *reinterpret_cast<const float4 *>(vp + (prow[j / kPage] + j % kPage) * vstride);
+        const bool live = j0 + h < n;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float pj = sc[g][j];
+            const float pj = live ? sc[g][j] : 0.f;
             acc[g].x += pj * v.x;
             acc[g].y += pj * v.y;
+            acc[g].z += pj * v.z;
+            acc[g].w += pj * v.w;
         }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) *reinterpret_cast<float2 *>(&red[wave][g][2 * lane]) = acc[g];
+    for (int g = 0; g < G; ++g) {
+        acc[g].x += __shfl_xor(acc[g].x, 32, 64);
+        acc[g].y += __shfl_xor(acc[g].y, 32, 64);
+        acc[g].z += __shfl_xor(acc[g].z, 32, 64);
+        acc[g].w += __shfl_xor(acc[g].w, 32, 64);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (h == 0) *reinterpret_cast<float4 *>(&red[wave][g][d4]) = acc[g];
     __syncthreads();
     for (int i = tid; i < G * kHd; i += 256) {
         const int g = i / kHd, d = i % kHd;
@@ -696,7 +712,11 @@ int attn_decode(const float *q, const float *gate, const float *kc, const float 
     const int nsplit = (max_len + kDecKeys - 1) / kDecKeys;
     AttnArgs a{q, gate, kc, vc, pages, nullptr, lens, nullptr, nullptr, out, nh, nkv, maxp,
                1.0f / sqrtf(static_cast<float>(kHd))};
-    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>(nkv), static_cast<unsigned>(nsplit));
+    // the split is the fastest grid index: workgroups are dealt to the CUs
+    // in launch order, so a long context's splits land on different CUs
+    // (with the sequence fastest, every split of one sequence would fall on
+    // the same CU and the longest context would set the step time)
+    const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(nkv), static_cast<unsigned>(B));
     hipStream_t s = as_stream(stream);
     switch (G) {
     case 1: hipLaunchKernelGGL(attn_decode_split_kernel<1>, grid, dim3(256), 0, s, a, part, nsplit); break;

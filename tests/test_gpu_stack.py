@@ -111,6 +111,14 @@ def test_stack_long_ragged_prompts_wide_heads(gpu):
     check(WIDE, prompts, 2, max_seqs=4, max_tokens=300, max_ctx=160)
 
 
+def test_stack_decode_over_several_splits(gpu):
+    # decode attention splits the keys in runs of 256 (plus a combine pass):
+    # contexts of 301 and 521 keys cover full, partial and single-page splits
+    rng = np.random.default_rng(8)
+    prompts = [list(rng.integers(0, SMALL.n_vocab, n)) for n in (300, 5, 520)]
+    check(SMALL, prompts, 2, max_seqs=4, max_tokens=900, max_ctx=600)
+
+
 # a wide FFN: its up/gate pair (10752 rows) is tall enough for the 16x16
 # MFMA kernel at more than 32 columns
 FFN_TALL = Card(n_layer=2, n_embd=256, n_ff=5376, n_vocab=512, full_attention_interval=2, n_head=2, n_head_kv=1,
