@@ -489,16 +489,22 @@ int ouro_stack_prefill(ouro_stack_t s, const int32_t *tokens, const int32_t *cu_
     hipStream_t st = as_stream(stream);
     // the staging buffer is rewritten: earlier copies from it must be done
     if (hipStreamSynchronize(st) != hipSuccess) return fail(OURO_ERR_HIP, "ouro_stack_prefill: stream sync");
+    // query tiles, the longest first (a tile at p0 reads p0 / 64 + 1 key
+    // tiles): workgroups start in launch order, so the heavy tiles of long
+    // prompts start early and the short ones fill in at the end
     size_t k = 0;
+    for (int p0 = (max_len - 1) / 64 * 64; p0 >= 0; p0 -= 64)
+        for (size_t i = 0; i < N; ++i)
+            if (p0 < cu_host[i + 1] - cu_host[i]) {
+                h_ts[k] = static_cast<int32_t>(i);
+                h_tp[k] = p0;
+                ++k;
+            }
     for (size_t i = 0; i < N; ++i) {
         const int t0 = cu_host[i], L = cu_host[i + 1] - t0;
         for (int p = 0; p < L; ++p) {
             h_pos[t0 + p] = p;
             h_seq[t0 + p] = static_cast<int32_t>(i);
-        }
-        for (int p0 = 0; p0 < L; p0 += 64, ++k) {
-            h_ts[k] = static_cast<int32_t>(i);
-            h_tp[k] = p0;
         }
         h_last[i] = t0 + L - 1;
         h_lens[i] = L;
