@@ -701,7 +701,7 @@ def main() -> int:
             "config": f"I2 6912x2560 x int8 [{GM_COLS_MAIN} columns] -> fp32, int8 MFMA (the K-column matmul_q)",
             "roofline": {"bound": "mfma", "achieved": main["mfma_tops"], "peak": INT8_MFMA_PEAK_TOPS,
                          "unit": "TOP/s", "frac": round(main["mfma_tops"] / INT8_MFMA_PEAK_TOPS, 4),
-                         "traffic": traffic_of(traffic, "i2_gemm_mfma_kernel<2, 4>")},
+                         "traffic": traffic_of(traffic, "i2_gemm_big_kernel")},
             "algorithmic_bytes": GM_OUT * GM_IN // 4 + GM_COLS_MAIN * GM_IN + GM_COLS_MAIN * GM_OUT * 4,
             "by_columns": rows,
             "vendor_int8_gemm_8bit_weights_us": round(vendor * 1e3, 2) if vendor else None,
