@@ -342,26 +342,72 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     }
     __builtin_amdgcn_wave_barrier();
 
-    // Column `lane` of T = (I + A)^-1 by right-looking substitution: once
-    // t_j is final, t_s -= A[s][j] t_j for every s > j (independent FMAs).
-    float t[kC];
+    // T = (I + A)^-1 in 16 x 16 blocks.  A sits transposed in the blocks on
+    // and above the diagonal of Al (block (j, i) holds A_ij^T, i >= j); T
+    // goes row-major: each diagonal block over A_ii, T_ij (i > j) into the
+    // free blocks below the diagonal.
+    {  // T_ii = (I + A_ii)^-1: lane (i = lg, c = lr) solves column c by
+       // substitution (once t_j is final, t_s -= A_ii[s][j] t_j for s > j)
+        float t[16];
 #pragma unroll
-    for (int s2 = 0; s2 < kC; ++s2) t[s2] = (s2 == lane) ? 1.f : 0.f;
+        for (int s2 = 0; s2 < 16; ++s2) t[s2] = (s2 == lr) ? 1.f : 0.f;
+        const float *Ad = Al + 16 * lg * AP + 16 * lg;  // Ad[j * AP + s] = A[16i + s][16i + j]
 #pragma unroll
-    for (int j = 0; j < kC - 1; ++j) {
-        const float tj = t[j];
-        const float *acol = Al + j * AP;  // A[.][j]
+        for (int j = 0; j < 15; ++j) {
+            const float tj = t[j];
 #pragma unroll
-        for (int s4 = (j + 1) & ~3; s4 < kC; s4 += 4) {
-            const f32x4 a4 = ld4(acol + s4);
+            for (int s4 = (j + 1) & ~3; s4 < 16; s4 += 4) {
+                const f32x4 a4 = ld4(Ad + j * AP + s4);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (s4 + e > j) t[s4 + e] -= a4[e] * tj;
+                for (int e = 0; e < 4; ++e)
+                    if (s4 + e > j) t[s4 + e] -= a4[e] * tj;
+            }
         }
-    }
-    __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int s2 = 0; s2 < kC; ++s2) Al[s2 * AP + lane] = t[s2];
+        for (int s2 = 0; s2 < 16; ++s2) Al[(16 * lg + s2) * AP + 16 * lg + lr] = t[s2];
+        __builtin_amdgcn_wave_barrier();
+    }
+    // T_ij = -T_ii (sum over k = j .. i-1 of A_ik T_kj) on fp32 MFMA: the sum
+    // goes through block (i, j), which the second product then overwrites
+    // (D lane l, register e: row 4 (l / 16) + e, column l % 16)
+    auto offdiag = [&](int i, int j) {
+        f32x4 y = {0.f, 0.f, 0.f, 0.f};
+        for (int k = j; k < i; ++k)
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int kk = 16 * k + 4 * s4 + lg;  // A[16i + lr][kk] T[kk][16j + lr]
+                y = __builtin_amdgcn_mfma_f32_16x16x4f32(Al[kk * AP + 16 * i + lr], Al[kk * AP + 16 * j + lr], y, 0, 0,
+                                                         0);
+            }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Al[(16 * i + 4 * lg + e) * AP + 16 * j + lr] = y[e];
+        __builtin_amdgcn_wave_barrier();
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int kk = 4 * s4 + lg;  // T_ii[lr][kk] Y[kk][lr]
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(Al[(16 * i + lr) * AP + 16 * i + kk],
+                                                     Al[(16 * i + kk) * AP + 16 * j + lr], x, 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Al[(16 * i + 4 * lg + e) * AP + 16 * j + lr] = -x[e];
+        __builtin_amdgcn_wave_barrier();
+    };
+    offdiag(1, 0);
+    offdiag(2, 1);
+    offdiag(3, 2);
+    offdiag(2, 0);
+    offdiag(3, 1);
+    offdiag(3, 0);
+    // the T operands below also read blocks (0, 1) and (2, 3) above the
+    // diagonal (A_10^T and A_32^T until now): T is zero there
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        Al[(4 * lg + e) * AP + 16 + lr] = 0.f;
+        Al[(32 + 4 * lg + e) * AP + 48 + lr] = 0.f;
+    }
     __builtin_amdgcn_wave_barrier();
 
     // T operands: slot (aa, q) of lane (lr, lg) is T[16aa + lr][32q + 4lg .. +3]
