@@ -511,15 +511,30 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x
 // (each input read once), taking them from the sequence's ring at a
 // sequence start.  The gates of token t are written by channel block 0.
 __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int per) {
+    // tokens go in batches of kB: a batch's loads are issued together (the
+    // token loop is otherwise one dependent HBM round trip per token)
+    constexpr int kB = 16;
     const int c = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
     const int ta = static_cast<int>(blockIdx.y) * per, tb = min(ta + per, a.T);
     if (blockIdx.x == 0 && threadIdx.x < a.Hv) {
         const int hv = threadIdx.x;
-        for (int t = ta; t < tb; ++t) {
-            const long long ig = static_cast<long long>(t) * a.Hv + hv;
-            a.beta[ig] = 1.0f / (1.0f + expf(-a.beta_raw[ig]));
-            const float x = a.alpha_raw[ig] + a.dt_bias[hv];
-            a.gate[ig] = a.a_log[hv] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+        const float dtb = a.dt_bias[hv], al = a.a_log[hv];
+        for (int t0 = ta; t0 < tb; t0 += kB) {
+            float br[kB], ar[kB];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                const long long ig = static_cast<long long>(min(t0 + u, tb - 1)) * a.Hv + hv;
+                br[u] = a.beta_raw[ig];
+                ar[u] = a.alpha_raw[ig];
+            }
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                if (t0 + u >= tb) break;
+                const long long ig = static_cast<long long>(t0 + u) * a.Hv + hv;
+                a.beta[ig] = 1.0f / (1.0f + expf(-br[u]));
+                const float x = ar[u] + dtb;
+                a.gate[ig] = al * (x > 20.0f ? x : logf(1.0f + expf(x)));
+            }
         }
     }
     if (c >= a.ch || ta >= tb) return;
@@ -534,25 +549,33 @@ __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int 
         x1 = p >= 2 ? a.qkv[(static_cast<long long>(ta) - 2) * a.ch + c] : r[1 + p];
         x2 = p >= 1 ? a.qkv[(static_cast<long long>(ta) - 1) * a.ch + c] : r[2];
     }
-    for (int t = ta; t < tb; ++t) {
-        if (t > ta && a.pos[t] == 0) {  // a sequence starts: its ring is the window
-            const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
-            x0 = r[0];
-            x1 = r[1];
-            x2 = r[2];
+    for (int t0 = ta; t0 < tb; t0 += kB) {
+        float xb[kB];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) xb[u] = a.qkv[static_cast<long long>(min(t0 + u, tb - 1)) * a.ch + c];
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+            const int t = t0 + u;
+            if (t >= tb) break;
+            if (t > ta && a.pos[t] == 0) {  // a sequence starts: its ring is the window
+                const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
+                x0 = r[0];
+                x1 = r[1];
+                x2 = r[2];
+            }
+            const float x = xb[u];
+            const float y = w.x * x0 + w.y * x1 + w.z * x2 + w.w * x;
+            x0 = x1;
+            x1 = x2;
+            x2 = x;
+            const uint16_t sy = to_bf16(y / (1.0f + expf(-y)));
+            if (c < di)
+                a.qb[static_cast<long long>(t) * di + c] = sy;
+            else if (c < 2 * di)
+                a.kb[static_cast<long long>(t) * di + c - di] = sy;
+            else
+                a.vb[static_cast<long long>(t) * dv + c - 2 * di] = sy;
         }
-        const float x = a.qkv[static_cast<long long>(t) * a.ch + c];
-        const float y = w.x * x0 + w.y * x1 + w.z * x2 + w.w * x;
-        x0 = x1;
-        x1 = x2;
-        x2 = x;
-        const uint16_t sy = to_bf16(y / (1.0f + expf(-y)));
-        if (c < di)
-            a.qb[static_cast<long long>(t) * di + c] = sy;
-        else if (c < 2 * di)
-            a.kb[static_cast<long long>(t) * di + c - di] = sy;
-        else
-            a.vb[static_cast<long long>(t) * dv + c - 2 * di] = sy;
     }
 }
 
