@@ -243,26 +243,38 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
         l[e] = 0.f;
     }
     const int last = min(p0 + kQT, L) - 1;  // last query position in the tile
+    // K and V of the next key tile are loaded into registers while the
+    // current one is used (a key tile is one KV page; rows past L read the
+    // page's unused rows and are zeroed)
+    constexpr int kPer = kKT * (kHd / 4) / 256;  // float4 of K (and of V) per thread
+    float4 kpre[kPer], vpre[kPer];
+    auto load_kv = [&](int k0) {
+        const long long row0 = kv_row(a.pages, a.maxp, s, k0);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = tid + 256 * j, r = i / (kHd / 4), c4 = i % (kHd / 4);
+            const long long off = ((row0 + r) * a.nkv + kvh) * kHd + 4 * c4;
+            kpre[j] = *reinterpret_cast<const float4 *>(a.kc + off);
+            vpre[j] = *reinterpret_cast<const float4 *>(a.vc + off);
+        }
+    };
+    load_kv(0);
     for (int k0 = 0; k0 <= last; k0 += kKT) {
         __syncthreads();  // the previous tile's K and V are consumed
-        {
-            const long long row0 = kv_row(a.pages, a.maxp, s, k0);  // a key tile is one page
-            for (int i = tid; i < kKT * (kHd / 4); i += 256) {
-                const int r = i / (kHd / 4), c4 = i % (kHd / 4);
-                float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-                if (k0 + r < L) {
-                    const long long off = ((row0 + r) * a.nkv + kvh) * kHd + 4 * c4;
-                    kv = *reinterpret_cast<const float4 *>(a.kc + off);
-                    vv = *reinterpret_cast<const float4 *>(a.vc + off);
-                }
-                *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
-                Vt[(4 * c4) * kVTP + r] = vv.x;
-                Vt[(4 * c4 + 1) * kVTP + r] = vv.y;
-                Vt[(4 * c4 + 2) * kVTP + r] = vv.z;
-                Vt[(4 * c4 + 3) * kVTP + r] = vv.w;
-            }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = tid + 256 * j, r = i / (kHd / 4), c4 = i % (kHd / 4);
+            const bool live = k0 + r < L;
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 kv = live ? kpre[j] : z, vv = live ? vpre[j] : z;
+            *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
+            Vt[(4 * c4) * kVTP + r] = vv.x;
+            Vt[(4 * c4 + 1) * kVTP + r] = vv.y;
+            Vt[(4 * c4 + 2) * kVTP + r] = vv.z;
+            Vt[(4 * c4 + 3) * kVTP + r] = vv.w;
         }
         __syncthreads();
+        if (k0 + kKT <= last) load_kv(k0 + kKT);
         // S: tile t holds S[16w + 4g + e][k0 + 16t + lr]
         f32x4_t sc[4];
 #pragma unroll
