@@ -395,13 +395,15 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
         q[g][0] = *reinterpret_cast<const float4 *>(qp);
         q[g][1] = *reinterpret_cast<const float4 *>(qp + 4);
     }
-    // scores: wave w, step it -> key w*64 + 4*it + g4 (wave w reads page w of
-    // the split); rows past the split are clamped to its last key, so the
+    // scores: wave w, step it -> key w*kWK + 4*it + g4 (a wave's keys lie in
+    // one page); rows past the split are clamped to its last key, so the
     // loads carry no branches, and their scores are not stored
-    const int wkeys = min(kPage, n - wave * kPage);  // keys of this wave's page (<= 0: none)
-    const long long wrow = wkeys > 0 ? prow[wave] : 0;
+    constexpr int kWK = kDecKeys / 4;  // keys per wavefront
+    static_assert(kPage % kWK == 0, "a wavefront's keys lie in one page");
+    const int wkeys = min(kWK, n - wave * kWK);  // keys of this wave (<= 0: none)
+    const long long wrow = wkeys > 0 ? prow[wave * kWK / kPage] + wave * kWK % kPage : 0;
 #pragma unroll 8
-    for (int it = 0; it < (wkeys > 0 ? 16 : 0); ++it) {
+    for (int it = 0; it < (wkeys > 0 ? kWK / 4 : 0); ++it) {
         const int jj = 4 * it + g4;
         const float *kp = a.kc + ((wrow + min(jj, max(wkeys - 1, 0))) * a.nkv + kvh) * kHd + 8 * gl;
         const float4 k0 = *reinterpret_cast<const float4 *>(kp);
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
             float d = q[g][0].x * k0.x + q[g][0].y * k0.y + q[g][0].z * k0.z + q[g][0].w * k0.w +
                       q[g][1].x * k1.x + q[g][1].y * k1.y + q[g][1].z * k1.z + q[g][1].w * k1.w;
             d = row16_sum(d);
-            if (gl == 0 && jj < wkeys) sc[g][wave * 64 + jj] = d * a.scale;
+            if (gl == 0 && jj < wkeys) sc[g][wave * kWK + jj] = d * a.scale;
         }
     }
     __syncthreads();
