@@ -78,7 +78,12 @@ struct GemmArgs {
     int32_t *acc;          // optional, same layout as y
     int M, K, N, nkb, nrb;
     int x_tiled;           // xq in the few-column fragment order (ceil(N/16) column tiles)
+    int swiglu;            // rows are (up, gate) pairs: y[N][M/2] = silu(gate) * up (no acc)
 };
+
+// The SwiGLU of an interleaved (up, gate) row pair, in the row kernel's
+// arithmetic (silu(gate) * up, run_ffn qwen35.rs:802).
+__device__ __forceinline__ float swiglu_pair(float up, float gate) { return gate / (1.0f + expf(-gate)) * up; }
 
 // Up to four products with the same k and column count in one launch of the
 // 16x16 kernel: workgroups bstart[p] .. bstart[p+1]-1 belong to product p.
@@ -199,6 +204,16 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
+            if (a.swiglu) {  // rows row .. row+3 = (up, gate) of outputs row/2, row/2 + 1
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    if (row + e + 1 >= a.M) break;
+                    const float up = (static_cast<float>(-(acc[r][c][e] >> 6)) * ds) * wscale;
+                    const float gt = (static_cast<float>(-(acc[r][c][e + 1] >> 6)) * ds) * wscale;
+                    a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
+                }
+                continue;
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (row + e >= a.M) break;
@@ -339,6 +354,16 @@ void i2_gemm_big_kernel(GemmArgs a) {
             for (int q = 0; q < 4; ++q) {
                 const int row = (RT0 + r) * 32 + 8 * q + 4 * g;
                 const long long o = static_cast<long long>(n) * a.M + row;
+                if (a.swiglu) {  // rows row .. row+3 = (up, gate) of outputs row/2, row/2 + 1
+#pragma unroll
+                    for (int e = 0; e < 4; e += 2) {
+                        if (row + e + 1 >= a.M) break;
+                        const float up = (static_cast<float>(-(acc[r][c][4 * q + e] >> 6)) * ds) * wscale;
+                        const float gt = (static_cast<float>(-(acc[r][c][4 * q + e + 1] >> 6)) * ds) * wscale;
+                        a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
+                    }
+                    continue;
+                }
                 if (quad && row + 3 < a.M) {
                     float4 v;
                     v.x = (static_cast<float>(-(acc[r][c][4 * q] >> 6)) * ds) * wscale;
@@ -647,7 +672,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
 }
 
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled) {
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu) {
     int st = check_mfma_shape(out_len, in_len);
     if (st) return st;
     if (!w_mfma || !w_scale || !xq || !dscale || !y || !ncols)
@@ -667,6 +692,10 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     a.N = static_cast<int>(ncols);
     a.nkb = a.K / 256;
     a.x_tiled = x_tiled;
+    a.swiglu = swiglu;
+    if (swiglu && (x_tiled || acc || out_len % 2 || ncols <= static_cast<size_t>(kSkinnyCols)))
+        return fail(OURO_ERR_SHAPE, "i2 gemm: the SwiGLU epilogue takes > %d row-major columns, an even row count "
+                    "and no int32 output", kSkinnyCols);
     if (x_tiled && ncols > static_cast<size_t>(kSkinnyCols))
         return fail(OURO_ERR_SHAPE, "i2 gemm: fragment-ordered x is for <= %d columns", kSkinnyCols);
     if (ncols <= static_cast<size_t>(kSkinnyCols)) {
@@ -704,7 +733,7 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, cons
                       const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc_or_null,
                       void *stream) {
     OURO_REQUIRE_INIT();
-    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0);
+    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0, 0);
 }
 
 }  // extern "C"

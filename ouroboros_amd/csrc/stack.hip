@@ -21,7 +21,7 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
                  void *stream);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled);
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0);
 size_t gdn_chunk_ws_bytes(size_t T, size_t N, size_t Hv);
 int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v, const float *gate,
                       const float *beta, float *out, const int32_t *cu_host, size_t N, size_t T, size_t Hk,
@@ -94,6 +94,7 @@ struct Layer {
     bool delta = false;
     float *attn_norm = nullptr, *post_norm = nullptr;
     Lin up, gate, down;
+    Lin upgate;  // up and gate rows interleaved, for prefill: its GEMM writes silu(gate) * up
     // delta-net
     Lin qkv, z, beta, alpha, out;
     float *conv_w = nullptr, *dt_bias = nullptr, *a_log = nullptr, *ssm_norm = nullptr;
@@ -171,6 +172,28 @@ int make_lin(ouro_stack *s, Lin &L, uint32_t tensor, size_t out, size_t in, uint
     L.scale = reinterpret_cast<float *>(L.w + tb);
     if ((st = gen_codes(s->seed, tensor, out, in, canon_scratch, nullptr))) return st;
     if ((st = i2_tile_mfma(canon_scratch, out, in, L.w, nullptr, nullptr))) return st;
+    const float sc = static_cast<float>(1.0 / std::sqrt(static_cast<double>(in) * 2.0 / 3.0));
+    if (hipMemcpy(L.scale, &sc, 4, hipMemcpyHostToDevice) != hipSuccess) return fail(OURO_ERR_HIP, "stack: scale copy");
+    return hipDeviceSynchronize() == hipSuccess ? OURO_OK : fail(OURO_ERR_HIP, "stack: weight generation");
+}
+
+// The same codes as make_lin(up) and make_lin(gate), rows interleaved
+// (up row i -> row 2i, gate row i -> row 2i + 1); both have the same scale.
+// The canonical scratch holds up, gate and the interleaved rows (4 out rows).
+int make_lin_pair(ouro_stack *s, Lin &L, uint32_t t_up, uint32_t t_gate, size_t out, size_t in, uint8_t *canon_scratch) {
+    L.out = 2 * out;
+    L.in = in;
+    const size_t tb = i2_mfma_bytes(2 * out, in), rb = in / 4;
+    int st = dalloc(s, &L.w, tb + 16);
+    if (st) return st;
+    L.scale = reinterpret_cast<float *>(L.w + tb);
+    uint8_t *up = canon_scratch, *gate = up + out * rb, *pair = gate + out * rb;
+    if ((st = gen_codes(s->seed, t_up, out, in, up, nullptr)) || (st = gen_codes(s->seed, t_gate, out, in, gate, nullptr)))
+        return st;
+    if (hipMemcpy2D(pair, 2 * rb, up, rb, rb, out, hipMemcpyDeviceToDevice) != hipSuccess ||
+        hipMemcpy2D(pair + rb, 2 * rb, gate, rb, rb, out, hipMemcpyDeviceToDevice) != hipSuccess)
+        return fail(OURO_ERR_HIP, "stack: interleaving up and gate");
+    if ((st = i2_tile_mfma(pair, 2 * out, in, L.w, nullptr, nullptr))) return st;
     const float sc = static_cast<float>(1.0 / std::sqrt(static_cast<double>(in) * 2.0 / 3.0));
     if (hipMemcpy(L.scale, &sc, 4, hipMemcpyHostToDevice) != hipSuccess) return fail(OURO_ERR_HIP, "stack: scale copy");
     return hipDeviceSynchronize() == hipSuccess ? OURO_OK : fail(OURO_ERR_HIP, "stack: weight generation");
@@ -279,8 +302,14 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     }
     // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = down(silu(gate f) * up f)
     TRY(rq(s, RQ_NORM, s->x, s->mix, L.post_norm, s->pre, rows, s->E, s->sign_e, stream));
-    TRY(lin_group({{&L.up, s->xq, s->ds, s->big}, {&L.gate, s->xq, s->ds, s->big2}}, rows, stream));
-    TRY(rq(s, RQ_SWIGLU, s->big2, s->big, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
+    if (frag_tiles(rows)) {  // few rows (decode): the up and gate products in one launch, SwiGLU in the row kernel
+        TRY(lin_group({{&L.up, s->xq, s->ds, s->big}, {&L.gate, s->xq, s->ds, s->big2}}, rows, stream));
+        TRY(rq(s, RQ_SWIGLU, s->big2, s->big, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
+    } else {  // prefill: the interleaved product writes silu(gate) * up
+        TRY(i2_gemm_mfma(L.upgate.w, L.upgate.out, L.upgate.in, L.upgate.scale, s->xq, s->ds, rows, s->big, nullptr,
+                         stream, 0, 1));
+        TRY(rq(s, RQ_COPY, s->big, nullptr, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
+    }
     TRY(lin(L.down, rows, s->xq, s->ds, s->mix, stream));
     return OURO_OK;
 }
@@ -348,7 +377,7 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
     const size_t wide = std::max({s->ch, 2 * s->qdim, F});
     // scratch for canonical codes of the largest tensor
     uint8_t *canon = nullptr;
-    const size_t canon_bytes = std::max({V * E, F * E, s->ch * E, 2 * s->qdim * E}) / 4;
+    const size_t canon_bytes = std::max({V * E, 4 * F * E, s->ch * E, 2 * s->qdim * E}) / 4;
     if (hipMalloc(reinterpret_cast<void **>(&canon), canon_bytes) != hipSuccess) {
         release(s);
         return fail(OURO_ERR_HIP, "ouro_stack_create: out of device memory");
@@ -366,6 +395,7 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
             (st = make_vec(s, &L.post_norm, tid_layer(il, T_POST_NORM), E, 0.8f, 0.4f)) ||
             (st = make_lin(s, L.up, tid_layer(il, T_UP), F, E, canon)) ||
             (st = make_lin(s, L.gate, tid_layer(il, T_GATE), F, E, canon)) ||
+            (st = make_lin_pair(s, L.upgate, tid_layer(il, T_UP), tid_layer(il, T_GATE), F, E, canon)) ||
             (st = make_lin(s, L.down, tid_layer(il, T_DOWN), E, F, canon)))
             return done(st);
         if (L.delta) {

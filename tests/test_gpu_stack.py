@@ -125,6 +125,15 @@ FFN_TALL = Card(n_layer=2, n_embd=256, n_ff=5376, n_vocab=512, full_attention_in
                 n_rot=64, ssm_n_k_heads=1, ssm_n_v_heads=2, eps=1e-6, rope_base=1e7)
 
 
+def test_stack_wide_ffn_long_prefill(gpu):
+    # 825 prompt tokens through the wide FFN: the prefill's interleaved
+    # up/gate product runs on the 256 x 128 tile kernel and writes
+    # silu(gate) * up from its epilogue
+    rng = np.random.default_rng(9)
+    prompts = [list(rng.integers(0, FFN_TALL.n_vocab, n)) for n in (300, 5, 520)]
+    check(FFN_TALL, prompts, 2, max_seqs=4, max_tokens=900, max_ctx=600)
+
+
 @pytest.mark.parametrize("card,nseq", [(SMALL, 64), (FFN_TALL, 40), (FFN_TALL, 64)])
 def test_stack_many_sequences(gpu, card, nseq):
     # more than 32 sequences: the decode step's int8 activations go out in
