@@ -104,6 +104,20 @@ int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *str
 
 // One ternary x int8 product of a grouped few-column launch (i2_gemm.hip):
 // MFMA-tiled weights w with out_len rows, activations xq/dscale, y[ncols][out_len].
+// Optional element-wise epilogue of a product (the delta-net's conv and gates
+// of one decode step, run where the projection outputs are produced):
+//   EPI_CONV     y <- silu(conv4(ring[n][row], y)), ring[n][row] shifted in
+//                (conv_step, qwen35.rs:64-70; w = conv weights [rows][4])
+//   EPI_SIGMOID  y <- 1 / (1 + e^-y)  (beta, qwen35.rs:1066-1067)
+//   EPI_GATE     y <- c[row] * softplus(y + b[row])  (qwen35.rs:1068-1070,
+//                1241-1243; b = dt_bias, c = a_log)
+enum { EPI_NONE = 0, EPI_CONV = 1, EPI_SIGMOID = 2, EPI_GATE = 3 };
+struct GemmEpilogue {
+    int op;
+    const float *w;  // EPI_CONV
+    float *ring;     // EPI_CONV: [ncols][rows][3]
+    const float *b, *c;  // EPI_GATE
+};
 struct GemmProblem {
     const uint8_t *w;
     size_t out_len;
@@ -112,7 +126,30 @@ struct GemmProblem {
     const float *dscale;
     float *y;
     int32_t *acc;  // optional exact int32 sums
+    GemmEpilogue epi;
 };
+
+// The epilogue's element-wise step for output (column n, row) of a product
+// with `rows` rows; the arithmetic of gdn_conv_gate_kernel.
+__device__ __forceinline__ float gemm_epilogue(const GemmEpilogue &e, float y, long long n, int row, int rows) {
+#pragma clang fp contract(off)
+    if (e.op == EPI_CONV) {
+        float *r = e.ring + (n * rows + row) * 3;
+        const float4 w = *reinterpret_cast<const float4 *>(e.w + 4LL * row);
+        const float r0 = r[0], r1 = r[1], r2 = r[2];
+        const float v = w.x * r0 + w.y * r1 + w.z * r2 + w.w * y;
+        r[0] = r1;
+        r[1] = r2;
+        r[2] = y;
+        return v / (1.0f + expf(-v));
+    }
+    if (e.op == EPI_SIGMOID) return 1.0f / (1.0f + expf(-y));
+    if (e.op == EPI_GATE) {
+        const float x = y + e.b[row];
+        return e.c[row] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+    }
+    return y;
+}
 int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream);
 
 // KV-cache pages handed out by the host for one decode step of the hybrid

@@ -79,6 +79,7 @@ struct GemmArgs {
     int M, K, N, nkb, nrb;
     int x_tiled;           // xq in the few-column fragment order (ceil(N/16) column tiles)
     int swiglu;            // rows are (up, gate) pairs: y[N][M/2] = silu(gate) * up (no acc)
+    GemmEpilogue epi;      // element-wise step on every stored output (not with acc or swiglu)
 };
 
 // The SwiGLU of an interleaved (up, gate) row pair, in the row kernel's
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
                 if (row + e >= a.M) break;
                 const int total = -(acc[r][c][e] >> 6);
                 const long long o = static_cast<long long>(n) * a.M + row + e;
-                a.y[o] = (static_cast<float>(total) * ds) * wscale;
+                a.y[o] = gemm_epilogue(a.epi, (static_cast<float>(total) * ds) * wscale, n, row + e, a.M);
                 if (a.acc) a.acc[o] = total;
             }
         }
@@ -405,6 +406,7 @@ struct SkinnyProblem {
     float *y;
     int32_t *acc;
     int M;
+    GemmEpilogue epi;
 };
 struct SkinnyGroup {
     SkinnyProblem p[kSkinnyGroup];
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         if (n >= a.N || row >= a.M) continue;
         const int total = -(tile[rr * TC + nt] >> 6);
         const long long o = static_cast<long long>(n) * a.M + row;
-        a.y[o] = (static_cast<float>(total) * a.dscale[n]) * wscale;
+        a.y[o] = gemm_epilogue(pb.epi, (static_cast<float>(total) * a.dscale[n]) * wscale, n, row, a.M);
         if (a.acc) a.acc[o] = total;
     }
 }
@@ -634,8 +636,10 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
             return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: NULL argument in product %d", i);
         if (reinterpret_cast<uintptr_t>(p.w) % 16 || reinterpret_cast<uintptr_t>(p.xq) % 16)
             return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
+        if (p.epi.op != EPI_NONE && p.acc)
+            return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: an epilogue with int32 output in product %d", i);
         g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.dscale, p.y, p.acc,
-                               static_cast<int>(p.out_len)};
+                               static_cast<int>(p.out_len), p.epi};
     }
     long long row_tiles = 0;
     for (int i = 0; i < np; ++i) row_tiles += (static_cast<long long>(probs[i].out_len) + 15) / 16;
@@ -644,7 +648,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
         for (int i = 0; i < np; ++i)
             args[i] = GemmArgs{reinterpret_cast<const uint4 *>(probs[i].w), probs[i].w_scale, probs[i].xq,
                                probs[i].dscale, probs[i].y, probs[i].acc, static_cast<int>(probs[i].out_len),
-                               g.K, g.N, g.nkb, 0, x_tiled};
+                               g.K, g.N, g.nkb, 0, x_tiled, 0, probs[i].epi};
         return launch_mfma_group(args, np, stream);
     }
     const int wr = row_tiles >= kSkinnyTallTiles ? 4 : 2;

@@ -27,6 +27,10 @@ int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v,
                       const float *beta, float *out, const int32_t *cu_host, size_t N, size_t T, size_t Hk,
                       size_t Hv, size_t d, size_t chunk, unsigned flags, float eps, void *workspace, void *stream);
 size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv);
+int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
+               const float *gate, const float *beta, float gate_s, float beta_s, float *out,
+               size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream,
+               size_t qk_bs, size_t v_bs);
 int gdn_decode_core(const float *qkv, const float *beta_raw, const float *alpha_raw, const float *dt_bias,
                     const float *a_log, const float *conv_w, float *conv, float *state, float *o, size_t B, size_t Hk,
                     size_t Hv, unsigned flags, float eps, void *workspace, void *stream);
@@ -231,6 +235,7 @@ struct LinOp {
     const int8_t *xq;
     const float *ds;
     float *y;
+    GemmEpilogue epi;  // few-column launches only
 };
 int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
     if (!frag_tiles(cols)) {
@@ -239,7 +244,7 @@ int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
     }
     GemmProblem p[4];
     int np = 0;
-    for (const LinOp &o : ops) p[np++] = GemmProblem{o.L->w, o.L->out, o.L->scale, o.xq, o.ds, o.y, nullptr};
+    for (const LinOp &o : ops) p[np++] = GemmProblem{o.L->w, o.L->out, o.L->scale, o.xq, o.ds, o.y, nullptr, o.epi};
     return i2_gemm_skinny_group(p, np, ops.begin()->L->in, cols, 1, stream);
 }
 
@@ -268,19 +273,34 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     float *xsum = il == 0 ? nullptr : s->x;
     TRY(rq(s, RQ_NORM, xa, xb, L.attn_norm, xsum, rows, s->E, s->sign_e, stream, L.delta));
     if (L.delta) {
-        TRY(lin_group({{&L.qkv, s->xq, s->ds, s->big}, {&L.z, s->xq, s->ds, s->zb},
-                       {&L.beta, s->xq2, s->ds2, s->braw}, {&L.alpha, s->xq2, s->ds2, s->araw}},
-                      rows, stream));
-        if (prefill) {
-            TRY(prefill_conv_gate(s->big, L.ring, L.conv_w, s->seqid, s->pos, s->braw, s->araw, L.dt_bias, L.a_log,
-                                  s->qb, s->kb, s->vb, s->beta, s->gate, rows, static_cast<int>(s->ch),
-                                  static_cast<int>(s->di), static_cast<int>(Hv), stream));
-            TRY(ring_update(s->big, L.ring, s->cu, N, static_cast<int>(s->ch), stream));
-            TRY(gdn_chunk_prefill(L.state, s->qb, s->kb, s->vb, s->gate, s->beta, s->o, cu_host, N, rows, Hk, Hv,
-                                  kHd, 64, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q, c.eps, s->ws, stream));
+        if (!prefill && frag_tiles(rows)) {
+            // decode: the conv + SiLU (ring shifted in place) and the gates run
+            // in the projections' epilogue; the recurrence reads them directly
+            const GemmEpilogue conv{EPI_CONV, L.conv_w, L.ring, nullptr, nullptr};
+            const GemmEpilogue sig{EPI_SIGMOID, nullptr, nullptr, nullptr, nullptr};
+            const GemmEpilogue gat{EPI_GATE, nullptr, nullptr, L.dt_bias, L.a_log};
+            TRY(lin_group({{&L.qkv, s->xq, s->ds, s->big, conv}, {&L.z, s->xq, s->ds, s->zb, {}},
+                           {&L.beta, s->xq2, s->ds2, s->braw, sig}, {&L.alpha, s->xq2, s->ds2, s->araw, gat}},
+                          rows, stream));
+            const size_t di = Hk * kHd;
+            TRY(gdn_decode(L.state, s->big, s->big + di, OURO_DT_F32, s->big + 2 * di, OURO_DT_F32, s->araw, s->braw,
+                           0.f, 0.f, s->o, rows, Hk, Hv, kHd, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q, c.eps, stream,
+                           s->ch, s->ch));
         } else {
-            TRY(gdn_decode_core(s->big, s->braw, s->araw, L.dt_bias, L.a_log, L.conv_w, L.ring, L.state, s->o, rows,
-                                Hk, Hv, 0u, c.eps, s->ws, stream));
+            TRY(lin_group({{&L.qkv, s->xq, s->ds, s->big}, {&L.z, s->xq, s->ds, s->zb},
+                           {&L.beta, s->xq2, s->ds2, s->braw}, {&L.alpha, s->xq2, s->ds2, s->araw}},
+                          rows, stream));
+            if (prefill) {
+                TRY(prefill_conv_gate(s->big, L.ring, L.conv_w, s->seqid, s->pos, s->braw, s->araw, L.dt_bias, L.a_log,
+                                      s->qb, s->kb, s->vb, s->beta, s->gate, rows, static_cast<int>(s->ch),
+                                      static_cast<int>(s->di), static_cast<int>(Hv), stream));
+                TRY(ring_update(s->big, L.ring, s->cu, N, static_cast<int>(s->ch), stream));
+                TRY(gdn_chunk_prefill(L.state, s->qb, s->kb, s->vb, s->gate, s->beta, s->o, cu_host, N, rows, Hk, Hv,
+                                      kHd, 64, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q, c.eps, s->ws, stream));
+            } else {
+                TRY(gdn_decode_core(s->big, s->braw, s->araw, L.dt_bias, L.a_log, L.conv_w, L.ring, L.state, s->o,
+                                    rows, Hk, Hv, 0u, c.eps, s->ws, stream));
+            }
         }
         // gated RMS norm per head in the V-grouped order, rotated, quantised
         TRY(rq(s, RQ_GNORM, s->o, s->zb, L.ssm_norm, nullptr, rows, s->dv, s->sign_di, stream));

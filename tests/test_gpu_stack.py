@@ -134,7 +134,13 @@ def test_stack_wide_ffn_long_prefill(gpu):
     check(FFN_TALL, prompts, 2, max_seqs=4, max_tokens=900, max_ctx=600)
 
 
-@pytest.mark.parametrize("card,nseq", [(SMALL, 64), (FFN_TALL, 40), (FFN_TALL, 64)])
+# many delta-net heads: the decode step's qkv/z/beta/alpha group (12352
+# rows) runs on the 16x16 MFMA kernel with the conv and gates in its epilogue
+DELTA_WIDE = Card(n_layer=2, n_embd=256, n_ff=256, n_vocab=512, full_attention_interval=2, n_head=2, n_head_kv=1,
+                  n_rot=64, ssm_n_k_heads=16, ssm_n_v_heads=32, eps=1e-6, rope_base=1e7)
+
+
+@pytest.mark.parametrize("card,nseq", [(SMALL, 64), (FFN_TALL, 40), (FFN_TALL, 64), (DELTA_WIDE, 40)])
 def test_stack_many_sequences(gpu, card, nseq):
     # more than 32 sequences: the decode step's int8 activations go out in
     # fragment order over 3 or 4 column tiles (the last one partial for 40);
