@@ -205,7 +205,10 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 constexpr int kVTP = kKT + 4;  // LDS row pitch of V^T (floats)
-constexpr int kAttnLds = (kKT * kQP + kHd * kVTP + kQT * kPP) * 4;
+// P reuses the K tile's space once every wavefront has its scores: 68 KiB,
+// two workgroups per CU
+constexpr int kAttnLds = (kKT * kQP + kHd * kVTP) * 4;
+static_assert(kQT * kPP <= kKT * kQP, "P fits in the K tile");
 
 __device__ __forceinline__ f32x4_t mfma_f32(float a, float b, const f32x4_t &c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -213,14 +216,14 @@ __device__ __forceinline__ f32x4_t mfma_f32(float a, float b, const f32x4_t &c) 
 
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
     extern __shared__ float lds[];
-    float *Ks = lds, *Vt = Ks + kKT * kQP, *Ps = Vt + kHd * kVTP;
+    float *Ks = lds, *Vt = Ks + kKT * kQP;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int s = a.tile_seq[blockIdx.x], p0 = a.tile_p0[blockIdx.x];
     const int h = blockIdx.y;
     const int kvh = h / (a.nh / a.nkv);
     const int t0 = a.cu[s], L = a.cu[s + 1] - t0;
-    float *Pw = Ps + 16 * wave * kPP;  // this wavefront's 16 rows of P
+    float *Pw = Ks + 16 * wave * kPP;  // this wavefront's 16 rows of P (over the K tile)
 
     // Q row 16w + lr, dims 32g .. 32g + 31 as the A operand of k-steps 0..31
     float qa[32];
@@ -290,6 +293,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
                 sc[t] = mfma_f32(qa[4 * i + 3], kv.w, sc[t]);
             }
         }
+        __syncthreads();  // every wavefront's scores are done: P may overwrite the K tile
         float corr[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
