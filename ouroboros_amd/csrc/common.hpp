@@ -127,6 +127,7 @@ struct GemmProblem {
     float *y;
     int32_t *acc;  // optional exact int32 sums
     GemmEpilogue epi;
+    int swiglu;    // rows are interleaved (up, gate) pairs: y[ncols][out_len / 2] = silu(gate) * up
 };
 
 // The epilogue's element-wise step for output (column n, row) of a product

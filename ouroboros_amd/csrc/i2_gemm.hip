@@ -407,6 +407,7 @@ struct SkinnyProblem {
     int32_t *acc;
     int M;
     GemmEpilogue epi;
+    int swiglu;
 };
 struct SkinnyGroup {
     SkinnyProblem p[kSkinnyGroup];
@@ -499,6 +500,17 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
     }
     __syncthreads();
     const float wscale = *a.w_scale;
+    if (pb.swiglu) {  // tile rows 2p, 2p+1 = (up, gate) of output row (rt0 * 16 + 2p) / 2
+        for (int i = tid; i < TR * 8 * WC; i += blockDim.x) {
+            const int nt = i / (TR / 2), rr = 2 * (i % (TR / 2)), row = rt0 * 16 + rr, n = 16 * ct0 + nt;
+            if (n >= a.N || row + 1 >= a.M) continue;
+            const float ds = a.dscale[n];
+            const float up = (static_cast<float>(-(tile[rr * TC + nt] >> 6)) * ds) * wscale;
+            const float gt = (static_cast<float>(-(tile[(rr + 1) * TC + nt] >> 6)) * ds) * wscale;
+            a.y[static_cast<long long>(n) * (a.M / 2) + row / 2] = swiglu_pair(up, gt);
+        }
+        return;
+    }
     for (int i = tid; i < TR * 16 * WC; i += blockDim.x) {
         const int nt = i / TR, rr = i % TR, row = rt0 * 16 + rr, n = 16 * ct0 + nt;
         if (n >= a.N || row >= a.M) continue;
@@ -636,10 +648,12 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
             return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: NULL argument in product %d", i);
         if (reinterpret_cast<uintptr_t>(p.w) % 16 || reinterpret_cast<uintptr_t>(p.xq) % 16)
             return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
-        if (p.epi.op != EPI_NONE && p.acc)
+        if ((p.epi.op != EPI_NONE || p.swiglu) && p.acc)
             return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: an epilogue with int32 output in product %d", i);
+        if (p.swiglu && (p.epi.op != EPI_NONE || p.out_len % 2))
+            return fail(OURO_ERR_SHAPE, "i2 gemm group: SwiGLU pairs need an even row count and no other epilogue");
         g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.dscale, p.y, p.acc,
-                               static_cast<int>(p.out_len), p.epi};
+                               static_cast<int>(p.out_len), p.epi, p.swiglu};
     }
     long long row_tiles = 0;
     for (int i = 0; i < np; ++i) row_tiles += (static_cast<long long>(probs[i].out_len) + 15) / 16;
@@ -648,7 +662,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
         for (int i = 0; i < np; ++i)
             args[i] = GemmArgs{reinterpret_cast<const uint4 *>(probs[i].w), probs[i].w_scale, probs[i].xq,
                                probs[i].dscale, probs[i].y, probs[i].acc, static_cast<int>(probs[i].out_len),
-                               g.K, g.N, g.nkb, 0, x_tiled, 0, probs[i].epi};
+                               g.K, g.N, g.nkb, 0, x_tiled, probs[i].swiglu, probs[i].epi};
         return launch_mfma_group(args, np, stream);
     }
     const int wr = row_tiles >= kSkinnyTallTiles ? 4 : 2;

@@ -97,8 +97,7 @@ struct Lin {
 struct Layer {
     bool delta = false;
     float *attn_norm = nullptr, *post_norm = nullptr;
-    Lin up, gate, down;
-    Lin upgate;  // up and gate rows interleaved, for prefill: its GEMM writes silu(gate) * up
+    Lin upgate, down;  // upgate: the up and gate rows interleaved; its GEMM writes silu(gate) * up
     // delta-net
     Lin qkv, z, beta, alpha, out;
     float *conv_w = nullptr, *dt_bias = nullptr, *a_log = nullptr, *ssm_norm = nullptr;
@@ -121,7 +120,7 @@ struct ouro_stack {
     float *sign_e = nullptr, *sign_ff = nullptr, *sign_di = nullptr, *sign_q = nullptr;
     // activations, rows = max(max_tokens, max_seqs)
     float *x = nullptr, *pre = nullptr, *mix = nullptr;
-    float *big = nullptr, *big2 = nullptr, *zb = nullptr, *braw = nullptr, *araw = nullptr;
+    float *big = nullptr, *zb = nullptr, *braw = nullptr, *araw = nullptr;
     float *o = nullptr, *g = nullptr, *qbuf = nullptr, *gbuf = nullptr, *kbuf = nullptr, *vbuf = nullptr;
     float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *lmx = nullptr, *logits = nullptr;
     int8_t *xq = nullptr, *xq2 = nullptr;  // rotated activations; unrotated h for beta / alpha
@@ -181,7 +180,7 @@ int make_lin(ouro_stack *s, Lin &L, uint32_t tensor, size_t out, size_t in, uint
     return hipDeviceSynchronize() == hipSuccess ? OURO_OK : fail(OURO_ERR_HIP, "stack: weight generation");
 }
 
-// The same codes as make_lin(up) and make_lin(gate), rows interleaved
+// The codes make_lin would give the up and gate tensors, rows interleaved
 // (up row i -> row 2i, gate row i -> row 2i + 1); both have the same scale.
 // The canonical scratch holds up, gate and the interleaved rows (4 out rows).
 int make_lin_pair(ouro_stack *s, Lin &L, uint32_t t_up, uint32_t t_gate, size_t out, size_t in, uint8_t *canon_scratch) {
@@ -236,6 +235,7 @@ struct LinOp {
     const float *ds;
     float *y;
     GemmEpilogue epi;  // few-column launches only
+    int swiglu;        // few-column launches only: interleaved (up, gate) rows -> silu(gate) * up
 };
 int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
     if (!frag_tiles(cols)) {
@@ -244,7 +244,8 @@ int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
     }
     GemmProblem p[4];
     int np = 0;
-    for (const LinOp &o : ops) p[np++] = GemmProblem{o.L->w, o.L->out, o.L->scale, o.xq, o.ds, o.y, nullptr, o.epi};
+    for (const LinOp &o : ops)
+        p[np++] = GemmProblem{o.L->w, o.L->out, o.L->scale, o.xq, o.ds, o.y, nullptr, o.epi, o.swiglu};
     return i2_gemm_skinny_group(p, np, ops.begin()->L->in, cols, 1, stream);
 }
 
@@ -322,14 +323,14 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
     }
     // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = down(silu(gate f) * up f)
     TRY(rq(s, RQ_NORM, s->x, s->mix, L.post_norm, s->pre, rows, s->E, s->sign_e, stream));
-    if (frag_tiles(rows)) {  // few rows (decode): the up and gate products in one launch, SwiGLU in the row kernel
-        TRY(lin_group({{&L.up, s->xq, s->ds, s->big}, {&L.gate, s->xq, s->ds, s->big2}}, rows, stream));
-        TRY(rq(s, RQ_SWIGLU, s->big2, s->big, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
-    } else {  // prefill: the interleaved product writes silu(gate) * up
+    // the interleaved up/gate product writes silu(gate) * up (few rows: the
+    // fragment-ordered launch; more: the row-major one)
+    if (frag_tiles(rows))
+        TRY(lin_group({{&L.upgate, s->xq, s->ds, s->big, {}, 1}}, rows, stream));
+    else
         TRY(i2_gemm_mfma(L.upgate.w, L.upgate.out, L.upgate.in, L.upgate.scale, s->xq, s->ds, rows, s->big, nullptr,
                          stream, 0, 1));
-        TRY(rq(s, RQ_COPY, s->big, nullptr, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
-    }
+    TRY(rq(s, RQ_COPY, s->big, nullptr, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
     TRY(lin(L.down, rows, s->xq, s->ds, s->mix, stream));
     return OURO_OK;
 }
@@ -413,8 +414,6 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         L.delta = (il + 1) % c.full_attention_interval != 0;
         if ((st = make_vec(s, &L.attn_norm, tid_layer(il, T_ATTN_NORM), E, 0.8f, 0.4f)) ||
             (st = make_vec(s, &L.post_norm, tid_layer(il, T_POST_NORM), E, 0.8f, 0.4f)) ||
-            (st = make_lin(s, L.up, tid_layer(il, T_UP), F, E, canon)) ||
-            (st = make_lin(s, L.gate, tid_layer(il, T_GATE), F, E, canon)) ||
             (st = make_lin_pair(s, L.upgate, tid_layer(il, T_UP), tid_layer(il, T_GATE), F, E, canon)) ||
             (st = make_lin(s, L.down, tid_layer(il, T_DOWN), E, F, canon)))
             return done(st);
@@ -457,7 +456,7 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
     // int8 activations of a few-row launch are padded to whole 16-row tiles
     const size_t qrows = std::max(rows, (max_seqs + 15) / 16 * 16);
     if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) || (st = dalloc(s, &s->mix, rows * E)) ||
-        (st = dalloc(s, &s->big, rows * wide)) || (st = dalloc(s, &s->big2, rows * F)) ||
+        (st = dalloc(s, &s->big, rows * wide)) ||
         (st = dalloc(s, &s->zb, rows * s->dv)) || (st = dalloc(s, &s->braw, rows * c.ssm_n_v_heads)) ||
         (st = dalloc(s, &s->araw, rows * c.ssm_n_v_heads)) || (st = dalloc(s, &s->o, rows * s->dv)) ||
         (st = dalloc(s, &s->g, rows * s->dv)) || (st = dalloc(s, &s->qbuf, rows * s->qdim)) ||
