@@ -534,7 +534,10 @@ __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int 
     constexpr int kB = 16;
     const int c = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
     const int ta = static_cast<int>(blockIdx.y) * per, tb = min(ta + per, a.T);
-    if (blockIdx.x == 0 && threadIdx.x < a.Hv) {
+    // the last column of workgroups computes the gates (next to the conv
+    // workgroups rather than in one of them, which made it the longest)
+    if (static_cast<int>(blockIdx.x) == (a.ch + 255) / 256) {
+        if (threadIdx.x >= a.Hv) return;
         const int hv = threadIdx.x;
         const float dtb = a.dt_bias[hv], al = a.a_log[hv];
         for (int t0 = ta; t0 < tb; t0 += kB) {
@@ -554,6 +557,7 @@ __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int 
                 a.gate[ig] = al * (x > 20.0f ? x : logf(1.0f + expf(x)));
             }
         }
+        return;
     }
     if (c >= a.ch || ta >= tb) return;
     const float4 w = *reinterpret_cast<const float4 *>(a.conv_w + 4LL * c);
@@ -789,7 +793,7 @@ int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, 
     // enough that the window is refilled from memory rarely
     const int ranges = static_cast<int>(T < 256 ? T : 256);
     const int per = static_cast<int>((T + ranges - 1) / ranges);
-    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(static_cast<unsigned>(cb), static_cast<unsigned>((T + per - 1) / per)),
+    hipLaunchKernelGGL(prefill_conv_gate_kernel, dim3(static_cast<unsigned>(cb + 1), static_cast<unsigned>((T + per - 1) / per)),
                        dim3(256), 0, as_stream(stream), a, per);
     return check_launch("prefill_conv_gate_kernel");
 }
