@@ -111,7 +111,9 @@ int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *str
 //   EPI_SIGMOID  y <- 1 / (1 + e^-y)  (beta, qwen35.rs:1066-1067)
 //   EPI_GATE     y <- c[row] * softplus(y + b[row])  (qwen35.rs:1068-1070,
 //                1241-1243; b = dt_bias, c = a_log)
-enum { EPI_NONE = 0, EPI_CONV = 1, EPI_SIGMOID = 2, EPI_GATE = 3 };
+//   EPI_RESID    y <- b[n][row] + y  (the residual add after a block's
+//                output projection; b has y's layout and is not y)
+enum { EPI_NONE = 0, EPI_CONV = 1, EPI_SIGMOID = 2, EPI_GATE = 3, EPI_RESID = 4 };
 struct GemmEpilogue {
     int op;
     const float *w;  // EPI_CONV
@@ -149,6 +151,7 @@ __device__ __forceinline__ float gemm_epilogue(const GemmEpilogue &e, float y, l
         const float x = y + e.b[row];
         return e.c[row] * (x > 20.0f ? x : logf(1.0f + expf(x)));
     }
+    if (e.op == EPI_RESID) return e.b[n * rows + row] + y;
     return y;
 }
 int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream);

@@ -343,7 +343,8 @@ void i2_gemm_big_kernel(GemmArgs a) {
     // registers 4q .. 4q+3 of a tile are 4 consecutive rows of one column,
     // contiguous in y: a full quad goes out as one 16-byte store
     const float wscale = *a.w_scale;
-    const bool quad = (a.M % 4) == 0 && !a.acc && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+    const bool quad = (a.M % 4) == 0 && !a.acc && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
+                      (a.epi.op != EPI_RESID || (reinterpret_cast<uintptr_t>(a.epi.b) & 15) == 0);
 #pragma unroll
     for (int c = 0; c < kBigTN; ++c) {
         const int n = n0 + c * 32 + (lane & 31);
@@ -367,10 +368,18 @@ void i2_gemm_big_kernel(GemmArgs a) {
                 }
                 if (quad && row + 3 < a.M) {
                     float4 v;
+                    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (a.epi.op == EPI_RESID) res = *reinterpret_cast<const float4 *>(a.epi.b + o);
                     v.x = (static_cast<float>(-(acc[r][c][4 * q] >> 6)) * ds) * wscale;
                     v.y = (static_cast<float>(-(acc[r][c][4 * q + 1] >> 6)) * ds) * wscale;
                     v.z = (static_cast<float>(-(acc[r][c][4 * q + 2] >> 6)) * ds) * wscale;
                     v.w = (static_cast<float>(-(acc[r][c][4 * q + 3] >> 6)) * ds) * wscale;
+                    if (a.epi.op == EPI_RESID) {
+                        v.x = res.x + v.x;
+                        v.y = res.y + v.y;
+                        v.z = res.z + v.z;
+                        v.w = res.w + v.w;
+                    }
                     *reinterpret_cast<float4 *>(a.y + o) = v;
                     continue;
                 }
@@ -378,7 +387,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     if (row + e >= a.M) break;
                     const int total = -(acc[r][c][4 * q + e] >> 6);
-                    a.y[o + e] = (static_cast<float>(total) * ds) * wscale;
+                    a.y[o + e] = gemm_epilogue(a.epi, (static_cast<float>(total) * ds) * wscale, n, row + e, a.M);
                     if (a.acc) a.acc[o + e] = total;
                 }
             }
@@ -690,7 +699,8 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
 }
 
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu) {
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu,
+                 const GemmEpilogue *epi) {
     int st = check_mfma_shape(out_len, in_len);
     if (st) return st;
     if (!w_mfma || !w_scale || !xq || !dscale || !y || !ncols)
@@ -711,13 +721,16 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     a.nkb = a.K / 256;
     a.x_tiled = x_tiled;
     a.swiglu = swiglu;
+    if (epi) a.epi = *epi;
+    if (epi && (acc || swiglu || (epi->op != EPI_NONE && epi->op != EPI_RESID && ncols > static_cast<size_t>(kSkinnyCols))))
+        return fail(OURO_ERR_INVALID_ARG, "i2 gemm: epilogue not supported with this output");
     if (swiglu && (x_tiled || acc || out_len % 2 || ncols <= static_cast<size_t>(kSkinnyCols)))
         return fail(OURO_ERR_SHAPE, "i2 gemm: the SwiGLU epilogue takes > %d row-major columns, an even row count "
                     "and no int32 output", kSkinnyCols);
     if (x_tiled && ncols > static_cast<size_t>(kSkinnyCols))
         return fail(OURO_ERR_SHAPE, "i2 gemm: fragment-ordered x is for <= %d columns", kSkinnyCols);
     if (ncols <= static_cast<size_t>(kSkinnyCols)) {
-        const GemmProblem one{w_mfma, out_len, w_scale, xq, dscale, y, acc};
+        const GemmProblem one{w_mfma, out_len, w_scale, xq, dscale, y, acc, epi ? *epi : GemmEpilogue{}, 0};
         return i2_gemm_skinny_group(&one, 1, in_len, ncols, x_tiled, stream);
     }
     const int nrt = (a.M + 15) / 16;
@@ -751,7 +764,7 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, cons
                       const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc_or_null,
                       void *stream) {
     OURO_REQUIRE_INIT();
-    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0, 0);
+    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0, 0, nullptr);
 }
 
 }  // extern "C"

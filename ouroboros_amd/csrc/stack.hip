@@ -21,7 +21,8 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
                  void *stream);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0);
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
+                 const GemmEpilogue *epi = nullptr);
 size_t gdn_chunk_ws_bytes(size_t T, size_t N, size_t Hv);
 int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v, const float *gate,
                       const float *beta, float *out, const int32_t *cu_host, size_t N, size_t T, size_t Hk,
@@ -119,10 +120,10 @@ struct ouro_stack {
     Lin lm;
     float *sign_e = nullptr, *sign_ff = nullptr, *sign_di = nullptr, *sign_q = nullptr;
     // activations, rows = max(max_tokens, max_seqs)
-    float *x = nullptr, *pre = nullptr, *mix = nullptr;
+    float *x = nullptr, *pre = nullptr;  // residual stream: x (layer input), pre (after the mixer)
     float *big = nullptr, *zb = nullptr, *braw = nullptr, *araw = nullptr;
     float *o = nullptr, *g = nullptr, *qbuf = nullptr, *gbuf = nullptr, *kbuf = nullptr, *vbuf = nullptr;
-    float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *lmx = nullptr, *logits = nullptr;
+    float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *logits = nullptr;
     int8_t *xq = nullptr, *xq2 = nullptr;  // rotated activations; unrotated h for beta / alpha
     float *ds = nullptr, *ds2 = nullptr;
     uint16_t *qb = nullptr, *kb = nullptr, *vb = nullptr;
@@ -226,6 +227,13 @@ int frag_tiles(size_t rows) { return rows <= kFragRows ? static_cast<int>((rows 
 int lin(const Lin &L, size_t cols, const int8_t *xq, const float *ds, float *y, void *stream) {
     return i2_gemm_mfma(L.w, L.out, L.in, L.scale, xq, ds, cols, y, nullptr, stream, frag_tiles(cols) ? 1 : 0);
 }
+// y = res + L x: a block's output projection with the residual add in the
+// GEMM's epilogue (y and res are different buffers)
+int lin_res(const Lin &L, size_t cols, const int8_t *xq, const float *ds, const float *res, float *y, void *stream) {
+    const GemmEpilogue add{EPI_RESID, nullptr, nullptr, res, nullptr};
+    return i2_gemm_mfma(L.w, L.out, L.in, L.scale, xq, ds, cols, y, nullptr, stream, frag_tiles(cols) ? 1 : 0, 0,
+                        &add);
+}
 
 // Several projections of the same activation rows: one grouped launch for
 // a few rows, else one launch each.
@@ -260,19 +268,17 @@ int rq(ouro_stack *s, int pro, const float *a, const float *b, const float *w, f
 
 
 // Mixer + FFN of one layer over `rows` token rows; x is the layer input (the
-// residual stream), the layer's output is pre + mix.
+// residual stream), and the layer leaves its output (pre + FFN) in x.
 int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *cu_host, size_t N, size_t n_tiles,
               void *stream) {
     Layer &L = s->layers[il];
     const ouro_stack_card &c = s->c;
     const size_t Hk = c.ssm_n_k_heads, Hv = c.ssm_n_v_heads;
-    // h = rmsnorm(x) * attn_norm, where x = pre + mix of the previous layer
-    // (stored), rotated and quantised; delta layers also quantise h itself
-    // for the beta and alpha projections (qwen35.rs:1058-1065)
-    const float *xa = il == 0 ? s->x : s->pre;
-    const float *xb = il == 0 ? nullptr : s->mix;
-    float *xsum = il == 0 ? nullptr : s->x;
-    TRY(rq(s, RQ_NORM, xa, xb, L.attn_norm, xsum, rows, s->E, s->sign_e, stream, L.delta));
+    // h = rmsnorm(x) * attn_norm, where x (the residual stream) = pre + the
+    // previous layer's FFN output, added in its down projection's epilogue;
+    // rotated and quantised; delta layers also quantise h itself for the
+    // beta and alpha projections (qwen35.rs:1058-1065)
+    TRY(rq(s, RQ_NORM, s->x, nullptr, L.attn_norm, nullptr, rows, s->E, s->sign_e, stream, L.delta));
     if (L.delta) {
         if (!prefill && frag_tiles(rows)) {
             // decode: the conv + SiLU (ring shifted in place) and the gates run
@@ -305,7 +311,7 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
         }
         // gated RMS norm per head in the V-grouped order, rotated, quantised
         TRY(rq(s, RQ_GNORM, s->o, s->zb, L.ssm_norm, nullptr, rows, s->dv, s->sign_di, stream));
-        TRY(lin(L.out, rows, s->xq, s->ds, s->mix, stream));
+        TRY(lin_res(L.out, rows, s->xq, s->ds, s->x, s->pre, stream));  // pre = x + mixer
     } else {
         TRY(lin_group({{&L.q, s->xq, s->ds, s->big}, {&L.k, s->xq, s->ds, s->kbuf}, {&L.v, s->xq, s->ds, s->vbuf}},
                       rows, stream));
@@ -319,10 +325,10 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
             TRY(attn_decode(s->qbuf, s->gbuf, L.kc, L.vc, s->pages, s->maxp, s->klen, rows, s->max_len, s->attn_o, c.n_head,
                             c.n_head_kv, s->attn_part, stream));
         TRY(rq(s, RQ_COPY, s->attn_o, nullptr, nullptr, nullptr, rows, s->qdim, s->sign_q, stream));
-        TRY(lin(L.o, rows, s->xq, s->ds, s->mix, stream));
+        TRY(lin_res(L.o, rows, s->xq, s->ds, s->x, s->pre, stream));  // pre = x + mixer
     }
-    // pre = x + mix; f = rmsnorm(pre) * post_norm; mix = down(silu(gate f) * up f)
-    TRY(rq(s, RQ_NORM, s->x, s->mix, L.post_norm, s->pre, rows, s->E, s->sign_e, stream));
+    // f = rmsnorm(pre) * post_norm; x = pre + down(silu(gate f) * up f)
+    TRY(rq(s, RQ_NORM, s->pre, nullptr, L.post_norm, nullptr, rows, s->E, s->sign_e, stream));
     // the interleaved up/gate product writes silu(gate) * up (few rows: the
     // fragment-ordered launch; more: the row-major one)
     if (frag_tiles(rows))
@@ -331,15 +337,14 @@ int run_layer(ouro_stack *s, int il, size_t rows, bool prefill, const int32_t *c
         TRY(i2_gemm_mfma(L.upgate.w, L.upgate.out, L.upgate.in, L.upgate.scale, s->xq, s->ds, rows, s->big, nullptr,
                          stream, 0, 1));
     TRY(rq(s, RQ_COPY, s->big, nullptr, nullptr, nullptr, rows, s->F, s->sign_ff, stream));
-    TRY(lin(L.down, rows, s->xq, s->ds, s->mix, stream));
+    TRY(lin_res(L.down, rows, s->xq, s->ds, s->pre, s->x, stream));  // x = pre + FFN
     return OURO_OK;
 }
 
-// Final norm of the chosen rows of pre + mix, lm_head, greedy token.
+// Final norm of the chosen rows of the residual stream, lm_head, greedy token.
 int head(ouro_stack *s, const int32_t *rows_idx, size_t n, int32_t *next, float *logits_out, void *stream) {
-    TRY(gather_rows(s->pre, rows_idx, s->lp, n, s->E, stream));
-    TRY(gather_rows(s->mix, rows_idx, s->lmx, n, s->E, stream));
-    TRY(rq(s, RQ_NORM, s->lp, s->lmx, s->out_norm, nullptr, n, s->E, s->sign_e, stream));
+    TRY(gather_rows(s->x, rows_idx, s->lp, n, s->E, stream));
+    TRY(rq(s, RQ_NORM, s->lp, nullptr, s->out_norm, nullptr, n, s->E, s->sign_e, stream));
     float *lg = logits_out ? logits_out : s->logits;
     TRY(lin(s->lm, n, s->xq, s->ds, lg, stream));
     return argmax_rows(lg, n, s->V, next, s->arg_keys, stream);
@@ -455,14 +460,14 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
     const size_t tiles = max_tokens / 64 + max_seqs + 1;
     // int8 activations of a few-row launch are padded to whole 16-row tiles
     const size_t qrows = std::max(rows, (max_seqs + 15) / 16 * 16);
-    if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) || (st = dalloc(s, &s->mix, rows * E)) ||
+    if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) ||
         (st = dalloc(s, &s->big, rows * wide)) ||
         (st = dalloc(s, &s->zb, rows * s->dv)) || (st = dalloc(s, &s->braw, rows * c.ssm_n_v_heads)) ||
         (st = dalloc(s, &s->araw, rows * c.ssm_n_v_heads)) || (st = dalloc(s, &s->o, rows * s->dv)) ||
         (st = dalloc(s, &s->g, rows * s->dv)) || (st = dalloc(s, &s->qbuf, rows * s->qdim)) ||
         (st = dalloc(s, &s->gbuf, rows * s->qdim)) || (st = dalloc(s, &s->kbuf, rows * s->kvdim)) ||
         (st = dalloc(s, &s->vbuf, rows * s->kvdim)) || (st = dalloc(s, &s->attn_o, rows * s->qdim)) ||
-        (st = dalloc(s, &s->lp, max_seqs * E)) || (st = dalloc(s, &s->lmx, max_seqs * E)) ||
+        (st = dalloc(s, &s->lp, max_seqs * E)) ||
         (st = dalloc(s, &s->logits, max_seqs * V)) || (st = dalloc(s, &s->xq, qrows * xw)) ||
         (st = dalloc(s, &s->ds, qrows)) || (st = dalloc(s, &s->xq2, qrows * E)) || (st = dalloc(s, &s->ds2, qrows)) ||
         (st = dalloc(s, &s->qb, rows * s->di)) || (st = dalloc(s, &s->kb, rows * s->di)) ||

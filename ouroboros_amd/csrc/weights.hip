@@ -21,7 +21,8 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
                  void *stream);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0);
+                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
+                 const GemmEpilogue *epi = nullptr);
 int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale, void *stream);
 size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
