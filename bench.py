@@ -104,7 +104,7 @@ def time_events(stream, fn, steps: int, warmup: int, min_warm_s: float = 0.15) -
 
 
 def bench_gemv(stream, steps, warmup, orc):
-    from ouroboros_amd import ops
+    from ouroboros_amd import ops, quant
     from ouroboros_amd._lib import call
     from ouroboros_amd.device import DeviceBuffer
 
@@ -113,13 +113,14 @@ def bench_gemv(stream, steps, warmup, orc):
     stride = (tb + 4 + 255) // 256 * 256
     w_all = DeviceBuffer((GEMV_MATS * stride,), np.uint8)
     n_distinct = 4  # distinct contents, copied to GEMV_MATS distinct addresses
-    canons, scales = [], []
+    tensors, scales = [], []
     for m in range(n_distinct):
-        codes = rng.integers(0, 3, size=(GEMV_OUT, GEMV_IN), dtype=np.uint8)
-        canon = (codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
-        canons.append(np.ascontiguousarray(canon))
+        # trits i.i.d. with p = 1/3 each, w_scale ~ U(0.5, 2), as bitnet.cpp I2_S tensors
+        w = rng.integers(-1, 2, size=(GEMV_OUT, GEMV_IN)).astype(np.int8)
         scales.append(np.float32(rng.uniform(0.5, 2.0)))
-    payloads = [ops.i2_payload(c, GEMV_OUT, GEMV_IN, float(s)) for c, s in zip(canons, scales)]
+        tensors.append(quant.i2s_pack(w, scales[-1]))
+    # repacked on the device to the tiled layout, as a resident upload does
+    payloads = [ops.i2s_payload(t, GEMV_OUT, GEMV_IN) for t in tensors]
     for m in range(GEMV_MATS):
         call("ouro_memcpy_dtod", w_all.ptr + m * stride, payloads[m % n_distinct].ptr, tb + 4, None)
     x = rng.standard_normal((GEMV_MATS, GEMV_IN)).astype(np.float32)
@@ -143,8 +144,7 @@ def bench_gemv(stream, steps, warmup, orc):
     if orc is not None:
         xq_h, ds_h = xq.download(), ds.download()
         for m in (0, 5):
-            _, want = orc.gemm_i2(canons[m % n_distinct], GEMV_OUT, GEMV_IN, xq_h[m:m + 1], ds_h[m:m + 1],
-                                  scales[m % n_distinct])
+            _, want = orc.gemm_i2s(tensors[m % n_distinct], GEMV_OUT, GEMV_IN, xq_h[m:m + 1], ds_h[m:m + 1])
             if not np.array_equal(got[m].view(np.uint32), want.view(np.uint32)):
                 raise SystemExit(f"GEMV parity failure on matrix {m}")
 
@@ -268,16 +268,14 @@ def bench_gemm(stream, steps, warmup, orc):
     """Ternary x int8 GEMM (the K-column matmul_q, ops.rs:156-230) on the
     6912x2560 layer: the int8 MFMA GEMM (ouro_gemm_i2_mfma) for 4 .. 2048
     columns, and the multi-column GEMV (ouro_gemm_i2) for few columns."""
-    from ouroboros_amd import ops
+    from ouroboros_amd import ops, quant
     from ouroboros_amd._lib import call
     from ouroboros_amd.device import DeviceBuffer
 
     rng = np.random.default_rng(21)
-    codes = rng.integers(0, 3, size=(GM_OUT, GM_IN), dtype=np.uint8)
-    canon = np.ascontiguousarray(codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
-    w_scale = 1.5
-    p_gemv = ops.i2_payload(canon, GM_OUT, GM_IN, w_scale)
-    p_mfma = ops.i2_mfma_payload(canon, GM_OUT, GM_IN, w_scale)
+    i2s = quant.i2s_pack(rng.integers(-1, 2, size=(GM_OUT, GM_IN)).astype(np.int8), 1.5)
+    p_gemv = ops.i2s_payload(i2s, GM_OUT, GM_IN)
+    p_mfma = ops.i2s_mfma_payload(i2s, GM_OUT, GM_IN)
     tb_g, tb_m = ops.i2_tiled_bytes(GM_OUT, GM_IN), ops.i2_mfma_bytes(GM_OUT, GM_IN)
     nmax = max(GM_COLS)
     x = DeviceBuffer.from_host(rng.standard_normal((nmax, GM_IN)).astype(np.float32))
@@ -322,7 +320,7 @@ def bench_gemm(stream, steps, warmup, orc):
     if orc is not None:
         call("ouro_gemm_i2_mfma", p_mfma.ptr, GM_OUT, GM_IN, p_mfma.ptr + tb_m, xq.ptr, ds.ptr, 64, y.ptr, None, stream)
         got = y.download()[:64 * GM_OUT]
-        _, want = orc.gemm_i2(canon, GM_OUT, GM_IN, xq.download()[:64], ds.download()[:64], w_scale)
+        _, want = orc.gemm_i2s(i2s, GM_OUT, GM_IN, xq.download()[:64], ds.download()[:64])
         if not np.array_equal(got.view(np.uint32), want.reshape(-1).view(np.uint32)):
             raise SystemExit("ternary GEMM parity failure")
     return rows, vendor
@@ -499,14 +497,13 @@ def cpu_baseline(orc, budget_s: float = 12.0) -> dict:
         n += 1
     dt = (time.perf_counter() - t0) / n
     tl1_bytes = payload.nbytes + GEMV_IN * 4 + GEMV_OUT * 4
-    # I2 oracle on the headline format, for reference (scalar C, same threads)
-    codes = rng.integers(0, 3, size=(GEMV_OUT, GEMV_IN), dtype=np.uint8)
-    canon = np.ascontiguousarray(codes[:, 0::4] | (codes[:, 1::4] << 2) | (codes[:, 2::4] << 4) | (codes[:, 3::4] << 6))
+    # bitnet.cpp I2_S / I8_S oracle on the headline format, for reference (scalar C, same threads)
+    i2s = orc.i2s_pack(rng.integers(-1, 2, size=(GEMV_OUT, GEMV_IN)).astype(np.int8), 1.0)
     xq, ds = orc.act_quant_i8(x[None])
     t1 = time.perf_counter()
     m = 0
     while time.perf_counter() - t1 < budget_s / 4 and m < 200:
-        orc.gemm_i2(canon, GEMV_OUT, GEMV_IN, xq, ds, 1.0, nthreads=nt)
+        orc.gemm_i2s(i2s, GEMV_OUT, GEMV_IN, xq, ds, nthreads=nt)
         m += 1
     dt_i2 = (time.perf_counter() - t1) / m
     return {

@@ -7,7 +7,7 @@
  * compute entry points work on DEVICE buffers owned by the caller, are
  * stream-ordered (asynchronous w.r.t. the host) and never allocate device
  * memory, except the documented workspace users (ouro_matvec_q /
- * ouro_matmul_q for the I2 kind), which take memory from a per-device
+ * ouro_matmul_q for the 2-bit kinds), which take memory from a per-device
  * library workspace that is grown on first use and kept until
  * ouro_shutdown().
  *
@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define OURO_ABI_VERSION 1
+#define OURO_ABI_VERSION 2
 
 typedef enum ouro_status {
     OURO_OK = 0,
@@ -54,10 +54,14 @@ enum {
     OURO_KIND_BF16 = 30,
     OURO_KIND_TQ1_0 = 34,  /* 54 B / 256 weights, base-3 (dequant.rs:49-105) */
     OURO_KIND_TL1 = 143,   /* PTQ1_0, 28 B / 128 weights (dequant.rs:124-195) */
-    /* 2-bit ternary codes in the device-tiled layout below, followed by one
-     * little-endian fp32 per-tensor scale (the BitNet convention of a scale
-     * appended at the end of the tensor, dequant.rs:8-11).  No reference
-     * kind: this is the int8-activation x 2-bit format of bitnet.cpp. */
+    /* bitnet.cpp's I2_S tensor (GGML_TYPE_I2_S of microsoft/BitNet's ggml
+     * fork, the reference's bitnet-cpp submodule, .gitmodules): 2-bit codes
+     * in 128-weight blocks, then one fp32 per-tensor scale (layout below).
+     * The reference names it its portable ternary baseline and GPU route
+     * (PLAN.md:465,1277). */
+    OURO_KIND_I2_S = 36,
+    /* This library's resident layout of the same codes: the device-tiled
+     * layout below followed by the fp32 per-tensor scale. */
     OURO_KIND_I2 = 0x4932,
 };
 
@@ -99,14 +103,36 @@ int ouro_event_elapsed_ms(float *ms, void *start, void *stop);
 
 /* ------------------------------------------------------------------ */
 /* Ternary GEMV / GEMM: int8 per-token-absmax activations x 2-bit      */
-/* ternary weights (the I2 format), exact int32 accumulation.          */
+/* ternary weights, exact int32 accumulation (bitnet.cpp's I2_S/I8_S). */
 /* ------------------------------------------------------------------ */
 /*
- * Canonical I2 bytes (host / on disk): row r is in_len/4 bytes; weight k of
- * the row sits in byte k/4 at bits 2*(k%4)..2*(k%4)+1 as code = w + 1,
- * w in {-1, 0, +1}.  Decoding is w = code - 1.
+ * The contract is bitnet.cpp's (microsoft/BitNet, src/ggml-bitnet-mad.cpp;
+ * its pinned commit is not recoverable from the reference checkout, whose
+ * bitnet-cpp submodule is empty, so the rules follow the published source):
  *
- * Device-tiled I2 (what the kernels read; ouro_i2_tile() produces it):
+ * I2_S tensor [out_len][in_len] (quantize_i2_s), n = out_len*in_len: the
+ *   flattened weights in blocks of 128; weight j of block b sits in byte
+ *   32*b + j%32 at bits 6-2*(j/32) .. 7-2*(j/32) as code = w + 1
+ *   (0 = -1, 1 = 0, 2 = +1); one little-endian fp32 scale at byte n/4; the
+ *   tensor is n/4 + 32 bytes (scale, then alignment padding).  With
+ *   in_len % 256 == 0 (required here) row r is bytes r*in_len/4 ..
+ *
+ * Activation quantisation per row of n values (quantize_row_i8_s):
+ *   s = (float)(127 / max(max|x|, 1e-5)) (in double), act_scale = s;
+ *   q = clamp(round(x * s), -128, 127), x * s a float product, round()
+ *   half away from zero.
+ * Output (the I2_S branch of the fork's mul_mat):
+ *   y = ((float)acc / act_scale) * w_scale, acc = sum_k w*q (exact int32),
+ *   the division and the product rounded separately.  bitnet.cpp forms
+ *   acc as sum(code*q) - sum(q) in float, which is the same value while
+ *   both sums stay below 2^24 (in_len <= 66051).
+ *
+ * Canonical I2 bytes (this library's interchange form, e.g. for the
+ * tilers): row r is in_len/4 bytes; weight k of the row sits in byte k/4 at
+ * bits 2*(k%4)..2*(k%4)+1 as code = w + 1.  Decoding is w = code - 1.
+ *
+ * Device-tiled I2 (what the GEMV reads; ouro_i2s_tile() / ouro_i2_tile()
+ * produce it):
  *   G = in_len / 256 four-weight groups per lane per row (in_len % 256 == 0),
  *   R = 8 rows per tile, tiles = ceil(out_len / 8) (rows past out_len hold
  *   code 1, i.e. w = 0, and are never written out).  Tile t starts at byte
@@ -125,13 +151,6 @@ int ouro_event_elapsed_ms(float *ms, void *start, void *stop);
  *   gi = 4d + f (f = 0..3); group gi is row r = gi / G, local group
  *   g = gi % G, i.e. weights k = 4*kg(l, g) + b (b = 0..3), whose codes sit
  *   at bits 8*b + 2*f of the word.
- *
- * Activation quantisation (per row of n values, one row per token):
- *   amax = max|x|; if amax == 0: q = 0, dscale = 0;
- *   else s = 127.0f / amax, q = clamp(rintf(x * s), -127, 127),
- *        dscale = amax / 127.0f.
- * Output: y = ((float)acc * dscale) * w_scale, acc = sum_k w*q (int32), with
- * both products rounded separately (no fused multiply-add).
  */
 
 /* Size in bytes of the device-tiled codes (without the trailing scale). */
@@ -141,27 +160,35 @@ size_t ouro_i2_tiled_bytes(size_t out_len, size_t in_len);
  * tiled codes, making `tiled` a complete OURO_KIND_I2 payload. */
 int ouro_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
                  uint8_t *tiled, const float *w_scale_or_null, void *stream);
-/* Per-row absmax int8 quantisation of rows x n activations (f32 or bf16). */
+/* I2_S tensor (device) -> complete OURO_KIND_I2 payload (tiled codes, then
+ * the tensor's scale).  in_len % 256 == 0, tiled 16-byte aligned with
+ * ouro_i2_tiled_bytes() + 4 bytes.  The device-side repack that the
+ * reference's resident-weight upload does on the host
+ * (ouro-wgpu/src/lib.rs:256-263); no counterpart in bitnet.cpp. */
+int ouro_i2s_tile(const uint8_t *i2s, size_t out_len, size_t in_len,
+                  uint8_t *tiled, void *stream);
+/* quantize_row_i8_s (bitnet.cpp) of rows x n activations (f32 or bf16):
+ * int8 rows xq [rows][n] and act_scale[rows] (s of each row, above). */
 int ouro_act_quant_i8(const void *x, int x_dtype, size_t rows, size_t n,
-                      int8_t *xq, float *dscale, void *stream);
+                      int8_t *xq, float *act_scale, void *stream);
 /* y[c*out_len + r] for ncols activation columns (xq row-major [ncols][in]),
  * column-major output like matmul_q (ops.rs:160-161).  acc_or_null, when
  * given, receives the exact int32 accumulators in the same layout.
  * w_scale is read from the device (4 bytes), e.g. the payload tail.
  * w_tiled and xq need 16-byte alignment. */
 int ouro_gemm_i2(const uint8_t *w_tiled, size_t out_len, size_t in_len,
-                 const float *w_scale, const int8_t *xq, const float *dscale,
+                 const float *w_scale, const int8_t *xq, const float *act_scale,
                  size_t ncols, float *y, int32_t *acc_or_null, void *stream);
 /* Grouped launch over `count` independent (weight, activation, output)
  * triples of one shape, laid out at fixed strides (bytes / elements):
  * matrix m uses w_tiled + m*w_stride, w_scale[m], xq + m*x_stride,
- * dscale[m], y + m*y_stride (w_stride and x_stride multiples of 16, both
+ * act_scale[m], y + m*y_stride (w_stride and x_stride multiples of 16, both
  * bases 16-byte aligned).  One column each.  This is the shape of the
  * projections that share a step but not a matrix (e.g. all layers' weight
  * streams of one decode step handed to the GPU at once). */
 int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride,
                          const float *w_scale, const int8_t *xq,
-                         size_t x_stride, const float *dscale, float *y,
+                         size_t x_stride, const float *act_scale, float *y,
                          size_t y_stride, size_t out_len, size_t in_len,
                          size_t count, void *stream);
 
@@ -186,12 +213,16 @@ size_t ouro_i2_mfma_bytes(size_t out_len, size_t in_len);
  * after the codes. */
 int ouro_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
                       uint8_t *dst, const float *w_scale_or_null, void *stream);
-/* y[c*out_len + r] = (acc * dscale[c]) * w_scale for ncols int8 columns
+/* I2_S tensor (device) -> MFMA-tiled codes followed by the tensor's scale
+ * (dst: ouro_i2_mfma_bytes() + 4 bytes, 16-byte aligned). */
+int ouro_i2s_tile_mfma(const uint8_t *i2s, size_t out_len, size_t in_len,
+                       uint8_t *dst, void *stream);
+/* y[c*out_len + r] = (acc / act_scale[c]) * w_scale for ncols int8 columns
  * (xq row-major [ncols][in_len], 16-byte aligned); acc_or_null receives
  * the exact int32 sums.  Same semantics as ouro_gemm_i2. */
 int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len,
                       const float *w_scale, const int8_t *xq,
-                      const float *dscale, size_t ncols, float *y,
+                      const float *act_scale, size_t ncols, float *y,
                       int32_t *acc_or_null, void *stream);
 
 /* ------------------------------------------------------------------ */
@@ -203,8 +234,11 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len,
  *   OURO_KIND_TL1   - PTQ1_0 groups (fused decode + dot, ops.rs:294-363)
  *   OURO_KIND_TQ1_0 - TQ1_0 blocks (matvec_qblock, ops.rs:101-128)
  *   OURO_KIND_F32 / F16 / BF16 - dense rows (ops.rs:87-98,131-154,600-623)
- *   OURO_KIND_I2    - tiled I2 + scale; x is quantised per call into the
- *                     library workspace (int8 absmax, see above).
+ *   OURO_KIND_I2_S  - a bitnet.cpp I2_S tensor as it is (16-byte aligned,
+ *                     in_len % 256 == 0, in_len <= 32768)
+ *   OURO_KIND_I2    - tiled I2 + scale
+ *   For both ternary 2-bit kinds x is quantised per call (quantize_row_i8_s,
+ *   above) into the library workspace.
  * Floating-point sums are not in the reference's order; results agree to
  * float32 rounding (the reference's own fused-vs-scalar bar is rel 1e-5,
  * ops.rs:800-838). */
@@ -228,13 +262,13 @@ int ouro_matmul_q(const void *payload, int kind, size_t out_len,
  * The fp32 result is bit-identical to the reference: same butterfly stages
  * in the same order (hadamard.rs:15-31), same scale 1/sqrtf(block).
  * x and y may alias.  Either dtype on either side; bf16 output is rounded
- * to nearest-even.  When xq/dscale are non-NULL, each row of the output
+ * to nearest-even.  When xq/act_scale are non-NULL, each row of the output
  * (as stored, i.e. after bf16 rounding) is also int8-absmax-quantised as
  * ouro_act_quant_i8 does (the fused FWHT -> quantisation epilogue);
  * y may then be NULL to skip storing the rotated activations. */
 int ouro_fwht_rows(const void *x, int x_dtype, void *y, int y_dtype,
                    size_t rows, size_t n, size_t block, const float *signs,
-                   unsigned flags, int8_t *xq, float *dscale, void *stream);
+                   unsigned flags, int8_t *xq, float *act_scale, void *stream);
 /* Exact mirrors of hadamard::rotate_fwd / rotate_inv (hadamard.rs:41,57)
  * on one f32 device vector, in place. */
 int ouro_rotate_fwd(float *x, const float *signs, size_t n, size_t block,
@@ -333,8 +367,11 @@ int ouro_gdn_layer_decode(const float *qkv, const float *z, const float *beta_ra
 typedef struct ouro_weight *ouro_weight_t;
 
 /* Upload `bytes` host bytes of a `kind` tensor [out_len][in_len].  For
- * OURO_KIND_I2, `host` holds canonical I2 codes (out_len*in_len/4 bytes)
- * and w_scale is the per-tensor scale; the upload tiles them.  For the
+ * OURO_KIND_I2_S, `host` is a bitnet.cpp I2_S tensor (out_len*in_len/4
+ * code bytes, its fp32 scale, up to 28 padding bytes: 4..32 bytes past the
+ * codes) and w_scale is ignored.  For OURO_KIND_I2, `host` holds canonical
+ * I2 codes (out_len*in_len/4 bytes) and w_scale is the per-tensor scale.
+ * Both are tiled on upload and held as an OURO_KIND_I2 payload.  For the
  * other kinds host holds the reference payload (row_bytes*out_len bytes)
  * and w_scale is ignored.  max_cols sizes the handle's own activation
  * scratch (for matmul up to max_cols columns); an I2 handle with
@@ -344,9 +381,10 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes,
                        size_t out_len, size_t in_len, float w_scale,
                        size_t max_cols, ouro_weight_t *out);
 int ouro_weight_free(ouro_weight_t w);
-/* Device payload of a handle (what ouro_matvec_q takes for its kind); NULL
- * for OURO_KIND_TL1, whose handle holds the payload repacked for the
- * table-lookup GEMV (ouro_weight_matvec/matmul) instead of the raw groups. */
+/* Device payload of a handle (what ouro_matvec_q takes for its kind; I2
+ * and I2_S handles hold an OURO_KIND_I2 payload); NULL for OURO_KIND_TL1,
+ * whose handle holds the payload repacked for the table-lookup GEMV
+ * (ouro_weight_matvec/matmul) instead of the raw groups. */
 const void *ouro_weight_payload(ouro_weight_t w);
 int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y,
                        void *stream);

@@ -15,8 +15,12 @@ Parity status of each function (how it is pinned, tests/test_oracle_*.py):
                                              (hadamard.rs:96-172)
   delta_head_dim ........................... qwen35.rs KATs + float64
                                              brute force
-  I2 pack / act quant / gemm ............... closed forms, brute force,
-                                             invariants (no reference code)
+  I2_S pack / I8_S act quant / gemm ........ bitnet.cpp's published rules
+                                             (third-party, absent from the
+                                             reference checkout): hand KATs of
+                                             bytes, ties, the amax floor and
+                                             the epilogue; brute force;
+                                             invariants
 """
 from __future__ import annotations
 
@@ -31,7 +35,7 @@ HERE = Path(__file__).resolve().parent
 LIB = HERE / "libouro_oracle.so"
 
 L2NORM_QK, SCALE_Q, KHEAD_DIV = 1, 2, 4
-KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2 = 0, 1, 30, 34, 143, 0x4932
+KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2_S, KIND_I2 = 0, 1, 30, 34, 143, 36, 0x4932
 
 _lib: C.CDLL | None = None
 
@@ -68,6 +72,15 @@ def lib() -> C.CDLL:
             "orc_i2_pack": (i32, [vp, sz, sz, vp]),
             "orc_i2_unpack": (None, [vp, sz, sz, vp]),
             "orc_act_quant_i8": (None, [vp, sz, sz, vp, vp]),
+            "orc_i2s_bytes": (sz, [sz, sz]),
+            "orc_quantize_i2_s": (i32, [vp, sz, sz, vp]),
+            "orc_i2s_pack": (i32, [vp, sz, sz, f32, vp]),
+            "orc_i2s_code": (i32, [vp, sz, sz, sz]),
+            "orc_i2s_scale": (f32, [vp, sz, sz]),
+            "orc_quantize_row_i8_s": (None, [vp, sz, vp, vp, vp]),
+            "orc_vec_dot_i2_i8_s": (C.c_int32, [vp, sz, sz, vp]),
+            "orc_gemm_i2s": (None, [vp, sz, sz, vp, vp, sz, vp, vp, i32]),
+            "orc_i2s_to_canonical": (i32, [vp, sz, sz, vp]),
             "orc_i2_tiled_bytes": (sz, [sz, sz]),
             "orc_i2_tile": (sz, [vp, sz, sz, vp]),
             "orc_i2_mfma_bytes": (sz, [sz, sz]),
@@ -217,19 +230,88 @@ def i2_tile_mfma(canonical: np.ndarray, out_len: int, in_len: int) -> np.ndarray
 
 
 def act_quant_i8(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """quantize_row_i8_s per row: (int8 rows, act_scale s = 127 / max(amax, 1e-5))."""
     x = _f32(x)
     if x.ndim == 1:
         x = x[None, :]
     q = np.empty(x.shape, np.int8)
-    ds = np.empty(x.shape[0], np.float32)
-    lib().orc_act_quant_i8(_p(x), x.shape[0], x.shape[1], _p(q), _p(ds))
-    return q, ds
+    s = np.empty(x.shape[0], np.float32)
+    lib().orc_act_quant_i8(_p(x), x.shape[0], x.shape[1], _p(q), _p(s))
+    return q, s
 
 
-def gemm_i2(packed, out_len, in_len, xq, dscale, w_scale, nthreads=0):
+def quantize_row_i8_s(x) -> tuple[np.ndarray, float, int]:
+    x = _f32(x).reshape(-1)
+    q = np.empty(x.size, np.int8)
+    s = np.empty(1, np.float32)
+    t = np.empty(1, np.int32)
+    lib().orc_quantize_row_i8_s(_p(x), x.size, _p(q), _p(s), _p(t))
+    return q, s[0], int(t[0])
+
+
+def i2s_bytes(nrow: int, n_per_row: int) -> int:
+    return int(lib().orc_i2s_bytes(nrow, n_per_row))
+
+
+def quantize_i2_s(src: np.ndarray) -> np.ndarray:
+    """quantize_i2_s of a float [nrow][n_per_row] tensor: n/4 code bytes, the fp32 scale, padding."""
+    s = _f32(src)
+    out = np.empty(i2s_bytes(*s.shape), np.uint8)
+    if lib().orc_quantize_i2_s(_p(s), s.shape[0], s.shape[1], _p(out)):
+        raise ValueError("quantize_i2_s: element count not a multiple of 128")
+    return out
+
+
+def i2s_pack(w: np.ndarray, w_scale: float) -> np.ndarray:
+    """I2_S bytes of ternary w [out][in] with per-tensor scale w_scale (quantize_i2_s of w * w_scale)."""
+    w = np.ascontiguousarray(w, dtype=np.int8)
+    out = np.empty(i2s_bytes(*w.shape), np.uint8)
+    if lib().orc_i2s_pack(_p(w), w.shape[0], w.shape[1], float(w_scale), _p(out)):
+        raise ValueError("i2s_pack: bad weights, scale or shape")
+    return out
+
+
+def i2s_code(i2s, n_per_row: int, r: int, k: int) -> int:
+    p = np.ascontiguousarray(i2s, dtype=np.uint8)
+    return int(lib().orc_i2s_code(_p(p), n_per_row, r, k))
+
+
+def i2s_scale(i2s, nrow: int, n_per_row: int) -> float:
+    p = np.ascontiguousarray(i2s, dtype=np.uint8)
+    return float(lib().orc_i2s_scale(_p(p), nrow, n_per_row))
+
+
+def i2s_to_canonical(i2s, out_len: int, in_len: int) -> np.ndarray:
+    p = np.ascontiguousarray(i2s, dtype=np.uint8)
+    out = np.empty((out_len, in_len // 4), np.uint8)
+    if lib().orc_i2s_to_canonical(_p(p), out_len, in_len, _p(out)):
+        raise ValueError("i2s_to_canonical: bad shape")
+    return out
+
+
+def vec_dot_i2_i8_s(i2s, n_per_row: int, r: int, q) -> int:
+    p = np.ascontiguousarray(i2s, dtype=np.uint8)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    return int(lib().orc_vec_dot_i2_i8_s(_p(p), n_per_row, r, _p(q)))
+
+
+def gemm_i2s(i2s, out_len, in_len, xq, act_scale, nthreads=0):
+    """bitnet.cpp's I2_S mul_mat: returns (acc = sum w*q, y) in column-major [ncols][out_len]."""
+    p = np.ascontiguousarray(i2s, dtype=np.uint8)
+    xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, in_len)
+    s = _f32(act_scale).reshape(-1)
+    nc = xq.shape[0]
+    acc = np.empty(nc * out_len, np.int32)
+    y = np.empty(nc * out_len, np.float32)
+    lib().orc_gemm_i2s(_p(p), out_len, in_len, _p(xq), _p(s), nc, _p(acc), _p(y), nthreads)
+    return acc, y
+
+
+def gemm_i2(packed, out_len, in_len, xq, act_scale, w_scale, nthreads=0):
+    """Canonical codes with bitnet.cpp's epilogue: (acc, y = (acc / s) * w_scale)."""
     p = np.ascontiguousarray(packed, dtype=np.uint8)
     xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, in_len)
-    ds = _f32(dscale).reshape(-1)
+    ds = _f32(act_scale).reshape(-1)
     nc = xq.shape[0]
     acc = np.empty(nc * out_len, np.int32)
     y = np.empty(nc * out_len, np.float32)

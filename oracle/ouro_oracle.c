@@ -218,6 +218,7 @@ size_t orc_row_bytes(int kind, size_t k) /* dequant.rs:350-387 */
     case ORC_KIND_Q5K: return k / 256 * 176;
     case ORC_KIND_Q6K: return k / 256 * 210;
     case ORC_KIND_I2: return k / 4;
+    case ORC_KIND_I2_S: return k / 128 * 32; /* codes; one fp32 scale per tensor */
     default: return 0;
     }
 }
@@ -502,6 +503,16 @@ int orc_matvec_q(const uint8_t *payload, int kind, size_t out_len,
     case ORC_KIND_TQ1_0:
         orc_matvec_tq1(payload, out_len, in_len, x, y, nthreads);
         return 0;
+    case ORC_KIND_I2_S: { /* x quantised by quantize_row_i8_s, then the I2_S mul_mat */
+        if ((out_len * in_len) % 128) return -1;
+        int8_t *q = (int8_t *)malloc(in_len ? in_len : 1);
+        if (!q) return -1;
+        float s;
+        orc_quantize_row_i8_s(x, in_len, q, &s, NULL);
+        orc_gemm_i2s(payload, out_len, in_len, q, &s, 1, NULL, y, nthreads);
+        free(q);
+        return 0;
+    }
     default:
         return -1;
     }
@@ -523,7 +534,7 @@ int orc_matmul_q(const uint8_t *payload, int kind, size_t out_len,
 }
 
 /* ------------------------------------------------------------------------ */
-/* I2: closed-form definition (no reference counterpart).                    */
+/* This library's canonical 2-bit layout (a repack of the I2_S codes).       */
 /* ------------------------------------------------------------------------ */
 
 int orc_i2_pack(const int8_t *w, size_t out_len, size_t in_len, uint8_t *packed)
@@ -618,37 +629,164 @@ size_t orc_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
     return bytes;
 }
 
-void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
-                      float *dscale)
+/* ---- bitnet.cpp I2_S / I8_S (src/ggml-bitnet-mad.cpp) ------------------ */
+
+size_t orc_i2s_bytes(size_t nrow, size_t n_per_row)
 {
-    for (size_t r = 0; r < rows; ++r) {
-        const float *xr = x + r * n;
-        float amax = 0.0f;
-        for (size_t i = 0; i < n; ++i) {
-            float a = fabsf(xr[i]);
-            if (a > amax) amax = a;
+    return nrow * n_per_row / 4 + 32;
+}
+
+int orc_quantize_i2_s(const float *src, size_t nrow, size_t n_per_row,
+                      uint8_t *dst)
+{ /* quantize_i2_s */
+    const size_t n = nrow * n_per_row;
+    if (n % 128) return -1;
+    double max = 0;
+    for (size_t i = 0; i < n; ++i) max = fmax(max, fabs((double)src[i]));
+    const double i2_scale = max;
+    memset(dst, 0, orc_i2s_bytes(nrow, n_per_row));
+    for (size_t i = 0; i < n / 128; ++i)
+        for (size_t j = 0; j < 128; ++j) {
+            const float v = src[i * 128 + j];
+            uint8_t q8;
+            if (fabs((double)v) < 1e-6)
+                q8 = 1;
+            else
+                q8 = (double)v * i2_scale > 0 ? 2 : 0;
+            dst[i * 32 + j % 32] |= (uint8_t)(q8 << (6 - 2 * (j / 32)));
         }
-        if (amax == 0.0f) {
-            memset(q + r * n, 0, n);
-            dscale[r] = 0.0f;
-            continue;
-        }
-        float s = 127.0f / amax;
-        for (size_t i = 0; i < n; ++i) {
-            float t = rintf(xr[i] * s);
-            if (t > 127.0f) t = 127.0f;
-            if (t < -127.0f) t = -127.0f;
-            q[r * n + i] = (int8_t)t;
-        }
-        dscale[r] = amax / 127.0f;
+    const float s = (float)i2_scale;
+    memcpy(dst + n / 4, &s, 4);
+    return 0;
+}
+
+int orc_i2s_pack(const int8_t *w, size_t nrow, size_t n_per_row,
+                 float w_scale, uint8_t *dst)
+{
+    const size_t n = nrow * n_per_row;
+    if (n % 128 || !(w_scale > 0)) return -1;
+    float *src = (float *)malloc(n * sizeof(float));
+    if (!src) return -1;
+    int bad = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (w[i] < -1 || w[i] > 1) bad = 1;
+        src[i] = (float)w[i] * w_scale;
     }
+    int st = bad ? -1 : orc_quantize_i2_s(src, nrow, n_per_row, dst);
+    free(src);
+    return st;
+}
+
+int orc_i2s_code(const uint8_t *i2s, size_t n_per_row, size_t r, size_t k)
+{
+    const size_t e = r * n_per_row + k, i = e / 128, j = e % 128;
+    return (i2s[i * 32 + j % 32] >> (6 - 2 * (j / 32))) & 3;
+}
+
+float orc_i2s_scale(const uint8_t *i2s, size_t nrow, size_t n_per_row)
+{
+    float s;
+    memcpy(&s, i2s + nrow * n_per_row / 4, 4);
+    return s;
+}
+
+void orc_quantize_row_i8_s(const float *x, size_t n, int8_t *q,
+                           float *act_scale, int32_t *act_sum)
+{ /* quantize_row_i8_s */
+    double max = 0.00001;
+    for (size_t i = 0; i < n; ++i) max = fmax(max, fabs((double)x[i]));
+    const float s = (float)(127 / max);
+    int32_t sum = 0;
+    for (size_t i = 0; i < n; ++i) {
+        float t = (float)round((double)(x[i] * s));
+        if (t > 127) t = 127;
+        if (t < -128) t = -128;
+        q[i] = (int8_t)t;
+        sum += q[i];
+    }
+    *act_scale = s;
+    if (act_sum) *act_sum = sum;
+}
+
+void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
+                      float *act_scale)
+{
+    for (size_t r = 0; r < rows; ++r)
+        orc_quantize_row_i8_s(x + r * n, n, q + r * n, act_scale + r, NULL);
+}
+
+int32_t orc_vec_dot_i2_i8_s(const uint8_t *i2s, size_t n_per_row, size_t r,
+                            const int8_t *q)
+{ /* ggml_vec_dot_i2_i8_s: codes (0..2) times int8, summed exactly */
+    int32_t sumi = 0;
+    for (size_t k = 0; k < n_per_row; ++k)
+        sumi += orc_i2s_code(i2s, n_per_row, r, k) * (int32_t)q[k];
+    return sumi;
+}
+
+struct i2s_ctx {
+    const uint8_t *i2s;
+    size_t out_len, in_len, ncols;
+    const int8_t *xq;
+    const float *act_scale;
+    const int32_t *act_sum;
+    float scale;
+    int32_t *acc;
+    float *y;
+};
+
+static void i2s_range(void *p, size_t lo, size_t hi)
+{
+    struct i2s_ctx *c = (struct i2s_ctx *)p;
+    for (size_t r = lo; r < hi; ++r)
+        for (size_t col = 0; col < c->ncols; ++col) {
+            const int32_t sumi = orc_vec_dot_i2_i8_s(c->i2s, c->in_len, r, c->xq + col * c->in_len);
+            float t = (float)sumi;
+            t = t - (float)c->act_sum[col];
+            t = t / c->act_scale[col];
+            t = t * c->scale;
+            c->y[col * c->out_len + r] = t;
+            if (c->acc) c->acc[col * c->out_len + r] = sumi - c->act_sum[col];
+        }
+}
+
+void orc_gemm_i2s(const uint8_t *i2s, size_t out_len, size_t in_len,
+                  const int8_t *xq, const float *act_scale, size_t ncols,
+                  int32_t *acc, float *y, int nthreads)
+{ /* the I2_S branch of the ggml fork's mul_mat: quantized rows times codes */
+    int32_t *sums = (int32_t *)malloc((ncols ? ncols : 1) * sizeof(int32_t));
+    if (!sums) return;
+    for (size_t col = 0; col < ncols; ++col) {
+        int32_t s = 0;
+        for (size_t k = 0; k < in_len; ++k) s += xq[col * in_len + k];
+        sums[col] = s;
+    }
+    struct i2s_ctx c = {i2s, out_len, in_len, ncols, xq, act_scale, sums,
+                        orc_i2s_scale(i2s, out_len, in_len), acc, y};
+    orc_parallel_for(out_len, nthreads, i2s_range, &c);
+    free(sums);
+}
+
+int orc_i2s_to_canonical(const uint8_t *i2s, size_t out_len, size_t in_len,
+                         uint8_t *canonical)
+{
+    if (in_len % 4 || (out_len * in_len) % 128) return -1;
+    const size_t rb = in_len / 4;
+    for (size_t r = 0; r < out_len; ++r)
+        for (size_t b = 0; b < rb; ++b) {
+            uint8_t byte = 0;
+            for (size_t f = 0; f < 4; ++f)
+                byte |= (uint8_t)(orc_i2s_code(i2s, in_len, r, 4 * b + f) << (2 * f));
+            canonical[r * rb + b] = byte;
+        }
+    return 0;
 }
 
 struct i2_ctx {
     const uint8_t *packed;
     size_t out_len, in_len, ncols;
     const int8_t *xq;
-    const float *dscale;
+    const float *act_scale;
     float w_scale;
     int32_t *acc;
     float *y;
@@ -666,17 +804,17 @@ static void i2_range(void *p, size_t lo, size_t hi)
             for (size_t k = 0; k < c->in_len; ++k)
                 a += (((row[k / 4] >> (2 * (k % 4))) & 3) - 1) * (int32_t)x[k];
             if (c->acc) c->acc[col * c->out_len + r] = a;
-            float t = (float)a * c->dscale[col];
+            float t = (float)a / c->act_scale[col];
             c->y[col * c->out_len + r] = t * c->w_scale;
         }
     }
 }
 
 void orc_gemm_i2(const uint8_t *packed, size_t out_len, size_t in_len,
-                 const int8_t *xq, const float *dscale, size_t ncols,
+                 const int8_t *xq, const float *act_scale, size_t ncols,
                  float w_scale, int32_t *acc, float *y, int nthreads)
 {
-    struct i2_ctx c = {packed, out_len, in_len, ncols, xq, dscale, w_scale, acc, y};
+    struct i2_ctx c = {packed, out_len, in_len, ncols, xq, act_scale, w_scale, acc, y};
     orc_parallel_for(out_len, nthreads, i2_range, &c);
 }
 

@@ -7,11 +7,16 @@
  * cpu_baseline leg of bench.py.  The shipped product (libouro_hip.so) never
  * links, loads or calls anything in this directory.
  *
- * Every function cites the reference file:line it follows.  Functions that
- * implement the int8-activation x 2-bit ternary ("I2") format have no
- * counterpart in the reference tree (that format lives only in the absent
- * bitnet-cpp submodule); they implement the closed-form definition written in
- * ouro_hip.h and are pinned by closed forms and brute force in tests/.
+ * Every function cites the reference file:line it follows.  The
+ * int8-activation x 2-bit ternary functions restate a third-party
+ * dependency instead: microsoft/BitNet, the reference's `bitnet-cpp`
+ * submodule (.gitmodules; bitnet-rs/build.rs:10), file
+ * src/ggml-bitnet-mad.cpp (quantize_i2_s, quantize_row_i8_s,
+ * ggml_vec_dot_i2_i8_s) and the I2_S branch of its ggml fork's mul_mat.
+ * The submodule is empty in the reference checkout, so its pinned commit
+ * cannot be recovered; the restatement follows the published source.  The
+ * reference's own plan names this format as its portable ternary baseline
+ * and its GPU route ("I2_S repack", PLAN.md:465,1277).
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; Rust never contracts
  * a*b+c, so neither may the oracle).
@@ -40,7 +45,10 @@ enum {
     ORC_KIND_Q6K = 14,
     ORC_KIND_TQ1_0 = 34,
     ORC_KIND_TL1 = 143,
-    /* not a reference kind: 2-bit ternary codes, per-tensor scale */
+    /* GGML_TYPE_I2_S of BitNet's ggml fork: bitnet.cpp's 2-bit ternary
+     * tensor (codes + one fp32 per-tensor scale) */
+    ORC_KIND_I2_S = 36,
+    /* this build's canonical row-major 2-bit codes (no reference kind) */
     ORC_KIND_I2 = 0x4932,
 };
 
@@ -88,15 +96,64 @@ int orc_matmul_q(const uint8_t *payload, int kind, size_t out_len,
                  size_t in_len, const float *x, size_t k, float *y,
                  int nthreads);
 
-/* ---- I2: int8 per-token absmax activations x 2-bit ternary ------------- */
+/* ---- I2_S / I8_S: int8 per-token absmax activations x 2-bit ternary ----
+ *
+ * bitnet.cpp's format (src/ggml-bitnet-mad.cpp), as restated here:
+ *  I2_S tensor of nrow x n_per_row weights, n = nrow*n_per_row, n % 128 == 0:
+ *    the flattened weights in blocks of 128; weight j of block i sits in
+ *    byte 32*i + j%32 at bits 6 - 2*(j/32) .. 7 - 2*(j/32) as code w + 1
+ *    (0 = -1, 1 = 0, 2 = +1); one fp32 scale at byte n/4; the tensor is
+ *    n/4 + 32 bytes (the scale, then alignment padding).
+ *  quantize_i2_s(src): max = max|src| (double); code = 1 where
+ *    |src| < 1e-6, else 2 where src * max > 0, else 0; scale = max.
+ *  quantize_row_i8_s(x): max = max(1e-5, max|x|) (double);
+ *    s = (float)(127 / max); q = clamp(round((double)(x*s)), -128, 127)
+ *    with round() half away from zero; act_sum = sum of q.
+ *  vec_dot_i2_i8_s: sumi = sum of code * q (integer).
+ *  mul_mat epilogue: y = (((float)sumi - act_sum) / s) * scale.
+ */
+size_t orc_i2s_bytes(size_t nrow, size_t n_per_row);          /* n/4 + 32 */
+/* quantize_i2_s; dst holds orc_i2s_bytes() bytes (padding zeroed).
+ * Returns -1 if n % 128 != 0. */
+int orc_quantize_i2_s(const float *src, size_t nrow, size_t n_per_row,
+                      uint8_t *dst);
+/* Ternary weights w (values in {-1,0,1}) with per-tensor scale: the I2_S
+ * bytes quantize_i2_s makes of w * w_scale (w_scale > 0).  -1 on a bad
+ * weight or n % 128 != 0. */
+int orc_i2s_pack(const int8_t *w, size_t nrow, size_t n_per_row,
+                 float w_scale, uint8_t *dst);
+/* Code of weight (r, k) of an I2_S tensor (0, 1, 2; 3 never produced). */
+int orc_i2s_code(const uint8_t *i2s, size_t n_per_row, size_t r, size_t k);
+float orc_i2s_scale(const uint8_t *i2s, size_t nrow, size_t n_per_row);
+/* quantize_row_i8_s for one row of n floats. */
+void orc_quantize_row_i8_s(const float *x, size_t n, int8_t *q,
+                           float *act_scale, int32_t *act_sum);
+/* Rows of the above: act_scale[r] = s of row r. */
+void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
+                      float *act_scale);
+/* ggml_vec_dot_i2_i8_s on row r: sum of code * q over the row. */
+int32_t orc_vec_dot_i2_i8_s(const uint8_t *i2s, size_t n_per_row, size_t r,
+                            const int8_t *q);
+/* bitnet.cpp's mul_mat over I2_S for ncols activation rows (xq
+ * [ncols][in_len], act_scale [ncols]): y[c*out_len + r] =
+ * (((float)sumi - (float)act_sum[c]) / act_scale[c]) * scale, with
+ * acc[c*out_len + r] = sumi - act_sum[c] (= sum_k w*q) when acc != NULL. */
+void orc_gemm_i2s(const uint8_t *i2s, size_t out_len, size_t in_len,
+                  const int8_t *xq, const float *act_scale, size_t ncols,
+                  int32_t *acc, float *y, int nthreads);
 
-/* Canonical I2 packing: row r is in_len/4 bytes; element k sits in byte k/4
+/* ---- this build's I2 layouts (device repacks of I2_S) -------------------
+ *
+ * Canonical I2 packing: row r is in_len/4 bytes; element k sits in byte k/4
  * at bits 2*(k%4)..2*(k%4)+1 as code = w + 1.  w in {-1,0,1}.
  * Returns -1 if a weight is outside {-1,0,1} or in_len % 4 != 0. */
 int orc_i2_pack(const int8_t *w, size_t out_len, size_t in_len, uint8_t *packed);
 /* Decode: w = code - 1 (code 3, never produced by the packer, decodes to 2). */
 void orc_i2_unpack(const uint8_t *packed, size_t out_len, size_t in_len,
                    int8_t *w);
+/* I2_S codes -> canonical codes (the same code for every weight). */
+int orc_i2s_to_canonical(const uint8_t *i2s, size_t out_len, size_t in_len,
+                         uint8_t *canonical);
 /* Device-tiled I2 layout (ouro_hip.h): G = in_len/256, 8-row tiles,
  * tiles = ceil(out_len/8), lane-local group g of lane l is canonical byte
  * column 64*o + s*l + (g - o) (chunks of 4, 2, 1 groups), a lane's share
@@ -113,15 +170,13 @@ size_t orc_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len,
 size_t orc_i2_mfma_bytes(size_t out_len, size_t in_len);
 size_t orc_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len,
                         uint8_t *dst);
-/* Per-row absmax int8 quantization of `rows` rows of n floats:
- *   amax = max|x|; amax == 0 -> q = 0, dscale = 0;
- *   s = 127.0f / amax; q = clamp(rintf(x*s), -127, 127); dscale = amax/127.0f */
-void orc_act_quant_i8(const float *x, size_t rows, size_t n, int8_t *q,
-                      float *dscale);
-/* y[c*out_len + r] = ((float)acc * dscale[c]) * w_scale,
- * acc = sum_k w[r][k] * xq[c][k] (exact int32).  acc may be NULL. */
+/* The product on canonical codes with bitnet.cpp's epilogue:
+ * y[c*out_len + r] = ((float)acc / act_scale[c]) * w_scale,
+ * acc = sum_k w[r][k] * xq[c][k] (exact int32).  acc may be NULL.  Equal to
+ * orc_gemm_i2s on the same weights while |sumi| and |act_sum| < 2^24 (they
+ * are then exact in float), i.e. for every in_len <= 66051. */
 void orc_gemm_i2(const uint8_t *packed, size_t out_len, size_t in_len,
-                 const int8_t *xq, const float *dscale, size_t ncols,
+                 const int8_t *xq, const float *act_scale, size_t ncols,
                  float w_scale, int32_t *acc, float *y, int nthreads);
 
 /* ---- hadamard.rs ------------------------------------------------------- */

@@ -22,7 +22,7 @@ STATUS_NAMES = {
     7: "OURO_ERR_NOT_INIT",
 }
 
-KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2 = 0, 1, 30, 34, 143, 0x4932
+KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2_S, KIND_I2 = 0, 1, 30, 34, 143, 36, 0x4932
 DT_F32, DT_BF16 = 0, 1
 FWHT_INVERSE = 1
 GDN_L2NORM_QK, GDN_SCALE_Q, GDN_KHEAD_DIV, GDN_V_GROUPED = 1, 2, 4, 8
@@ -76,6 +76,8 @@ SIGNATURES = {
     "ouro_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
     "ouro_i2_tiled_bytes": (sz, [sz, sz]),
     "ouro_i2_tile": (i32, [vp, sz, sz, vp, vp, vp]),
+    "ouro_i2s_tile": (i32, [vp, sz, sz, vp, vp]),
+    "ouro_i2s_tile_mfma": (i32, [vp, sz, sz, vp, vp]),
     "ouro_act_quant_i8": (i32, [vp, i32, sz, sz, vp, vp, vp]),
     "ouro_gemm_i2": (i32, [vp, sz, sz, vp, vp, vp, sz, vp, vp, vp]),
     "ouro_gemv_i2_grouped": (i32, [vp, sz, vp, vp, sz, vp, vp, sz, sz, sz, sz, vp]),

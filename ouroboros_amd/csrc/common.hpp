@@ -57,6 +57,43 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 
+// ---- bitnet.cpp's int8 activation format (I8_S, quantize_row_i8_s in
+// src/ggml-bitnet-mad.cpp) and its I2_S mul_mat epilogue.
+// Scale of a row with largest magnitude amax: s = 127 / max(amax, 1e-5),
+// divided in double and rounded once to float, as the C source does.
+__device__ __forceinline__ float i8s_scale(float amax) {
+    const double m = fmax(1e-5, static_cast<double>(amax));
+    return static_cast<float>(127.0 / m);
+}
+// q = clamp(round(x * s), -128, 127); the product is a float product and
+// round() takes halves away from zero.
+__device__ __forceinline__ int i8s_quant(float x, float s) {
+    float t = roundf(x * s);
+    t = fminf(fmaxf(t, -128.f), 127.f);
+    return static_cast<int>(t);
+}
+// y = (acc / s) * w_scale: the integer sum divided by the activation scale
+// (an IEEE division), then times the per-tensor weight scale.
+__device__ __forceinline__ float i8s_out(int acc, float s, float w_scale) {
+    const float t = static_cast<float>(acc) / s;
+    return t * w_scale;
+}
+
+// Canonical byte (codes of weights 4*kg .. 4*kg+3 at bits 2*i) of row `row`
+// of an I2_S tensor: the flattened weights in 128-blocks, weight j of block
+// b in byte 32*b + j%32 at bits 6 - 2*(j/32) (quantize_i2_s).  The four
+// weights share one block and one bit field, in four consecutive bytes.
+__device__ __forceinline__ uint32_t i2s_canon_byte(const uint8_t *i2s, long long row, int in_len, int kg) {
+    const long long e = row * in_len + 4LL * kg;
+    const int j = static_cast<int>(e & 127);
+    const uint8_t *p = i2s + (e >> 7) * 32 + (j & 31);
+    const int sh = 6 - 2 * (j >> 5);
+    uint32_t byte = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) byte |= ((static_cast<uint32_t>(p[i]) >> sh) & 3u) << (2 * i);
+    return byte;
+}
+
 // Lane exchange across the 64-wide wavefront (ds_bpermute based).
 __device__ __forceinline__ float xor_shfl(float v, int mask) {
     return __shfl_xor(v, mask, 64);
@@ -103,7 +140,7 @@ constexpr int kArgmaxBlocks = 1024;
 int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *stream);
 
 // One ternary x int8 product of a grouped few-column launch (i2_gemm.hip):
-// MFMA-tiled weights w with out_len rows, activations xq/dscale, y[ncols][out_len].
+// MFMA-tiled weights w with out_len rows, activations xq/act_scale, y[ncols][out_len].
 // Optional element-wise epilogue of a product (the delta-net's conv and gates
 // of one decode step, run where the projection outputs are produced):
 //   EPI_CONV     y <- silu(conv4(ring[n][row], y)), ring[n][row] shifted in
@@ -125,7 +162,7 @@ struct GemmProblem {
     size_t out_len;
     const float *w_scale;
     const int8_t *xq;
-    const float *dscale;
+    const float *act_scale;
     float *y;
     int32_t *acc;  // optional exact int32 sums
     GemmEpilogue epi;

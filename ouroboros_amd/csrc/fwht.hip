@@ -8,7 +8,8 @@
 // that differ only in index bits 4p..4p+3.  Every stage is the same set of
 // independent (a+b, a-b) pairs as in the reference, so the fp32 result is
 // bit-identical.  Optional fused epilogue: per-row int8 absmax quantisation
-// of the stored output (the activation quantiser of the ternary GEMV).
+// of the stored output (bitnet.cpp's quantize_row_i8_s, the activation
+// quantiser of the ternary GEMV).
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -94,7 +95,7 @@ struct FwhtArgs {
     void *y;
     const float *signs;
     int8_t *xq;
-    float *dscale;
+    float *act_scale;
     long long rows;
     int n;
     float scale;
@@ -209,25 +210,16 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     int8_t *q = a.xq + row * n;
-    if (amax == 0.f) {
-        for (int c = tid; c < chunks; c += kThreads)
-            *reinterpret_cast<uint4 *>(q + 16 * c) = make_uint4(0, 0, 0, 0);
-        if (tid == 0) a.dscale[row] = 0.f;
-        return;
-    }
-    const float s = 127.0f / amax;
+    const float s = i8s_scale(amax);
     for (int c = tid; c < chunks; c += kThreads) {
         const float *p = lds + 17 * c;
         uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float t = rintf(p[i] * s);
-            t = fminf(fmaxf(t, -127.f), 127.f);
-            w[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xffu) << (8 * (i & 3));
-        }
+        for (int i = 0; i < 16; ++i)
+            w[i >> 2] |= (static_cast<uint32_t>(i8s_quant(p[i], s)) & 0xffu) << (8 * (i & 3));
         *reinterpret_cast<uint4 *>(q + 16 * c) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    if (tid == 0) a.dscale[row] = amax / 127.0f;
+    if (tid == 0) a.act_scale[row] = s;
 }
 
 // ------------------------------------------------------------------------
@@ -267,11 +259,8 @@ __device__ __forceinline__ long long rq_offset(long long row, int c16, int n, in
 __device__ __forceinline__ void quant16_store(const float *p, float s, int8_t *dst) {
     uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float t = rintf(p[i] * s);
-        t = fminf(fmaxf(t, -127.f), 127.f);
-        w[i >> 2] |= (static_cast<uint32_t>(static_cast<int>(t)) & 0xffu) << (8 * (i & 3));
-    }
+    for (int i = 0; i < 16; ++i)
+        w[i >> 2] |= (static_cast<uint32_t>(i8s_quant(p[i], s)) & 0xffu) << (8 * (i & 3));
     *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -403,15 +392,15 @@ __global__ __launch_bounds__(kThreads) void row_rq_kernel(RowRqArgs a) {
     __syncthreads();
     amax = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
     {
-        const float s = amax == 0.f ? 0.f : 127.0f / amax;
+        const float s = i8s_scale(amax);
         for (int c = tid; c < chunks; c += kThreads) quant16_store(lds + 17 * c, s, a.xq + rq_offset(row, c, n, a.tiles));
-        if (tid == 0) a.ds[row] = amax == 0.f ? 0.f : amax / 127.0f;
+        if (tid == 0) a.ds[row] = s;
     }
     if constexpr (Q2) {
         amax2 = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        const float s = amax2 == 0.f ? 0.f : 127.0f / amax2;
+        const float s = i8s_scale(amax2);
         for (int c = tid; c < chunks; c += kThreads) quant16_store(hl + 17 * c, s, a.xq2 + rq_offset(row, c, n, a.tiles));
-        if (tid == 0) a.ds2[row] = amax2 == 0.f ? 0.f : amax2 / 127.0f;
+        if (tid == 0) a.ds2[row] = s;
     }
 }
 
@@ -477,12 +466,12 @@ int launch_io(const FwhtArgs &a, int logb, bool inv, bool quant, bool store, hip
 }  // namespace
 
 int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, size_t n,
-              size_t block, const float *signs, unsigned flags, int8_t *xq, float *dscale,
+              size_t block, const float *signs, unsigned flags, int8_t *xq, float *act_scale,
               void *stream) {
     if (!x) return fail(OURO_ERR_INVALID_ARG, "ouro_fwht_rows: x is NULL");
-    const bool quant = xq || dscale;
-    if (quant && !(xq && dscale))
-        return fail(OURO_ERR_INVALID_ARG, "ouro_fwht_rows: xq and dscale go together");
+    const bool quant = xq || act_scale;
+    if (quant && !(xq && act_scale))
+        return fail(OURO_ERR_INVALID_ARG, "ouro_fwht_rows: xq and act_scale go together");
     if (!y && !quant) return fail(OURO_ERR_INVALID_ARG, "ouro_fwht_rows: nothing to store");
     if (flags & ~OURO_FWHT_INVERSE) return fail(OURO_ERR_INVALID_ARG, "ouro_fwht_rows: bad flags");
     if ((x_dtype != OURO_DT_F32 && x_dtype != OURO_DT_BF16) ||
@@ -503,7 +492,7 @@ int fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, siz
     a.y = y;
     a.signs = signs;
     a.xq = xq;
-    a.dscale = dscale;
+    a.act_scale = act_scale;
     a.rows = static_cast<long long>(rows);
     a.n = static_cast<int>(n);
     int logb = 0;
@@ -563,10 +552,10 @@ using namespace ouro;
 extern "C" {
 
 int ouro_fwht_rows(const void *x, int x_dtype, void *y, int y_dtype, size_t rows, size_t n,
-                   size_t block, const float *signs, unsigned flags, int8_t *xq, float *dscale,
+                   size_t block, const float *signs, unsigned flags, int8_t *xq, float *act_scale,
                    void *stream) {
     OURO_REQUIRE_INIT();
-    return fwht_rows(x, x_dtype, y, y_dtype, rows, n, block, signs, flags, xq, dscale, stream);
+    return fwht_rows(x, x_dtype, y, y_dtype, rows, n, block, signs, flags, xq, act_scale, stream);
 }
 
 int ouro_rotate_fwd(float *x, const float *signs, size_t n, size_t block, void *stream) {

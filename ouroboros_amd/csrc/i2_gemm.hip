@@ -39,9 +39,10 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // HIP's uint4 struct are kept in scratch memory by the compiler.
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-// One thread per 32-bit word of the MFMA layout.
+// One thread per 32-bit word of the MFMA layout.  The source is canonical
+// codes, or (src_i2s) the codes of a bitnet.cpp I2_S tensor.
 __global__ void i2_tile_mfma_kernel(const uint8_t *__restrict__ canon, uint32_t *__restrict__ dst,
-                                    int out_len, int in_len, long long total_words) {
+                                    int out_len, int in_len, long long total_words, int src_i2s) {
     const long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (id >= total_words) return;
     const int nkb = in_len / 256;
@@ -56,13 +57,15 @@ __global__ void i2_tile_mfma_kernel(const uint8_t *__restrict__ canon, uint32_t 
     if (row < out_len) {
         const uint8_t *cr = canon + row * (in_len / 4);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
+            const int kg = (kbase + 4 * j) / 4;  // the four k of field j share a canonical byte
+            const uint32_t byte = src_i2s ? i2s_canon_byte(canon, row, in_len, kg) : cr[kg];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int k = kbase + 4 * j + i;
-                const uint32_t code = (cr[k / 4] >> (2 * (k % 4))) & 3u;
+                const uint32_t code = (byte >> (2 * i)) & 3u;
                 word |= ((1u - code) & 3u) << (8 * i + 2 * j);
             }
+        }
     }
     dst[id] = word;
 }
@@ -73,7 +76,7 @@ struct GemmArgs {
     const uint4 *w;        // MFMA-layout units
     const float *w_scale;  // device scalar
     const int8_t *xq;      // [N][K] int8
-    const float *dscale;   // [N]
+    const float *act_scale;   // [N]
     float *y;              // [N][M]
     int32_t *acc;          // optional, same layout as y
     int M, K, N, nkb, nrb;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
     for (int c = 0; c < WC; ++c) {
         const int n = n0 + 16 * c + (lane & 15);
         if (n >= a.N) continue;
-        const float ds = a.dscale[n];
+        const float ds = a.act_scale[n];
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
@@ -209,8 +212,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
                     if (row + e + 1 >= a.M) break;
-                    const float up = (static_cast<float>(-(acc[r][c][e] >> 6)) * ds) * wscale;
-                    const float gt = (static_cast<float>(-(acc[r][c][e + 1] >> 6)) * ds) * wscale;
+                    const float up = i8s_out(-(acc[r][c][e] >> 6), ds, wscale);
+                    const float gt = i8s_out(-(acc[r][c][e + 1] >> 6), ds, wscale);
                     a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
                 }
                 continue;
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
                 if (row + e >= a.M) break;
                 const int total = -(acc[r][c][e] >> 6);
                 const long long o = static_cast<long long>(n) * a.M + row + e;
-                a.y[o] = gemm_epilogue(a.epi, (static_cast<float>(total) * ds) * wscale, n, row + e, a.M);
+                a.y[o] = gemm_epilogue(a.epi, i8s_out(total, ds, wscale), n, row + e, a.M);
                 if (a.acc) a.acc[o] = total;
             }
         }
@@ -349,7 +352,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
     for (int c = 0; c < kBigTN; ++c) {
         const int n = n0 + c * 32 + (lane & 31);
         if (n >= a.N) continue;
-        const float ds = a.dscale[n];
+        const float ds = a.act_scale[n];
 #pragma unroll
         for (int r = 0; r < kBigTM; ++r)
 #pragma unroll
@@ -360,8 +363,8 @@ void i2_gemm_big_kernel(GemmArgs a) {
 #pragma unroll
                     for (int e = 0; e < 4; e += 2) {
                         if (row + e + 1 >= a.M) break;
-                        const float up = (static_cast<float>(-(acc[r][c][4 * q + e] >> 6)) * ds) * wscale;
-                        const float gt = (static_cast<float>(-(acc[r][c][4 * q + e + 1] >> 6)) * ds) * wscale;
+                        const float up = i8s_out(-(acc[r][c][4 * q + e] >> 6), ds, wscale);
+                        const float gt = i8s_out(-(acc[r][c][4 * q + e + 1] >> 6), ds, wscale);
                         a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
                     }
                     continue;
@@ -370,10 +373,10 @@ void i2_gemm_big_kernel(GemmArgs a) {
                     float4 v;
                     float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (a.epi.op == EPI_RESID) res = *reinterpret_cast<const float4 *>(a.epi.b + o);
-                    v.x = (static_cast<float>(-(acc[r][c][4 * q] >> 6)) * ds) * wscale;
-                    v.y = (static_cast<float>(-(acc[r][c][4 * q + 1] >> 6)) * ds) * wscale;
-                    v.z = (static_cast<float>(-(acc[r][c][4 * q + 2] >> 6)) * ds) * wscale;
-                    v.w = (static_cast<float>(-(acc[r][c][4 * q + 3] >> 6)) * ds) * wscale;
+                    v.x = i8s_out(-(acc[r][c][4 * q] >> 6), ds, wscale);
+                    v.y = i8s_out(-(acc[r][c][4 * q + 1] >> 6), ds, wscale);
+                    v.z = i8s_out(-(acc[r][c][4 * q + 2] >> 6), ds, wscale);
+                    v.w = i8s_out(-(acc[r][c][4 * q + 3] >> 6), ds, wscale);
                     if (a.epi.op == EPI_RESID) {
                         v.x = res.x + v.x;
                         v.y = res.y + v.y;
@@ -387,7 +390,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     if (row + e >= a.M) break;
                     const int total = -(acc[r][c][4 * q + e] >> 6);
-                    a.y[o + e] = gemm_epilogue(a.epi, (static_cast<float>(total) * ds) * wscale, n, row + e, a.M);
+                    a.y[o + e] = gemm_epilogue(a.epi, i8s_out(total, ds, wscale), n, row + e, a.M);
                     if (a.acc) a.acc[o + e] = total;
                 }
             }
@@ -411,7 +414,7 @@ struct SkinnyProblem {
     const uint4 *w;
     const float *w_scale;
     const int8_t *xq;
-    const float *dscale;
+    const float *act_scale;
     float *y;
     int32_t *acc;
     int M;
@@ -438,11 +441,11 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         const uint4 *w;
         const float *w_scale;
         const int8_t *xq;
-        const float *dscale;
+        const float *act_scale;
         float *y;
         int32_t *acc;
         int M, K, N, nkb, x_tiled;
-    } a{pb.w, pb.w_scale, pb.xq, pb.dscale, pb.y, pb.acc, pb.M, g.K, g.N, g.nkb, g.x_tiled};
+    } a{pb.w, pb.w_scale, pb.xq, pb.act_scale, pb.y, pb.acc, pb.M, g.K, g.N, g.nkb, g.x_tiled};
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
     const int ct0 = cg * WC;  // first column tile of this workgroup
     const int rt0 = (bx - g.bstart[pi]) * WR;
@@ -513,9 +516,9 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         for (int i = tid; i < TR * 8 * WC; i += blockDim.x) {
             const int nt = i / (TR / 2), rr = 2 * (i % (TR / 2)), row = rt0 * 16 + rr, n = 16 * ct0 + nt;
             if (n >= a.N || row + 1 >= a.M) continue;
-            const float ds = a.dscale[n];
-            const float up = (static_cast<float>(-(tile[rr * TC + nt] >> 6)) * ds) * wscale;
-            const float gt = (static_cast<float>(-(tile[(rr + 1) * TC + nt] >> 6)) * ds) * wscale;
+            const float ds = a.act_scale[n];
+            const float up = i8s_out(-(tile[rr * TC + nt] >> 6), ds, wscale);
+            const float gt = i8s_out(-(tile[(rr + 1) * TC + nt] >> 6), ds, wscale);
             a.y[static_cast<long long>(n) * (a.M / 2) + row / 2] = swiglu_pair(up, gt);
         }
         return;
@@ -525,7 +528,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         if (n >= a.N || row >= a.M) continue;
         const int total = -(tile[rr * TC + nt] >> 6);
         const long long o = static_cast<long long>(n) * a.M + row;
-        a.y[o] = gemm_epilogue(pb.epi, (static_cast<float>(total) * a.dscale[n]) * wscale, n, row, a.M);
+        a.y[o] = gemm_epilogue(pb.epi, i8s_out(total, a.act_scale[n], wscale), n, row, a.M);
         if (a.acc) a.acc[o] = total;
     }
 }
@@ -618,7 +621,7 @@ size_t i2_mfma_bytes(size_t out_len, size_t in_len) {
 }
 
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst,
-                 const float *w_scale, void *stream) {
+                 const float *w_scale, void *stream, int src_i2s) {
     int st = check_mfma_shape(out_len, in_len);
     if (st) return st;
     if (!canonical || !dst) return fail(OURO_ERR_INVALID_ARG, "ouro_i2_tile_mfma: NULL argument");
@@ -627,7 +630,7 @@ int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_
     const long long words = static_cast<long long>(bytes / 4);
     hipLaunchKernelGGL(i2_tile_mfma_kernel, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0,
                        as_stream(stream), canonical, reinterpret_cast<uint32_t *>(dst), static_cast<int>(out_len),
-                       static_cast<int>(in_len), words);
+                       static_cast<int>(in_len), words, src_i2s);
     st = check_launch("i2_tile_mfma_kernel");
     if (st || !w_scale) return st;
     hipLaunchKernelGGL(copy_scale_mfma_kernel, dim3(1), dim3(1), 0, as_stream(stream), w_scale,
@@ -653,7 +656,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
         const GemmProblem &p = probs[i];
         int st = check_mfma_shape(p.out_len, in_len);
         if (st) return st;
-        if (!p.w || !p.w_scale || !p.xq || !p.dscale || !p.y)
+        if (!p.w || !p.w_scale || !p.xq || !p.act_scale || !p.y)
             return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: NULL argument in product %d", i);
         if (reinterpret_cast<uintptr_t>(p.w) % 16 || reinterpret_cast<uintptr_t>(p.xq) % 16)
             return fail(OURO_ERR_ALIGN, "ouro_gemm_i2_mfma: weights and xq need 16-byte alignment");
@@ -661,7 +664,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
             return fail(OURO_ERR_INVALID_ARG, "i2 gemm group: an epilogue with int32 output in product %d", i);
         if (p.swiglu && (p.epi.op != EPI_NONE || p.out_len % 2))
             return fail(OURO_ERR_SHAPE, "i2 gemm group: SwiGLU pairs need an even row count and no other epilogue");
-        g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.dscale, p.y, p.acc,
+        g.p[i] = SkinnyProblem{reinterpret_cast<const uint4 *>(p.w), p.w_scale, p.xq, p.act_scale, p.y, p.acc,
                                static_cast<int>(p.out_len), p.epi, p.swiglu};
     }
     long long row_tiles = 0;
@@ -670,7 +673,7 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
         GemmArgs args[kMfmaGroup];
         for (int i = 0; i < np; ++i)
             args[i] = GemmArgs{reinterpret_cast<const uint4 *>(probs[i].w), probs[i].w_scale, probs[i].xq,
-                               probs[i].dscale, probs[i].y, probs[i].acc, static_cast<int>(probs[i].out_len),
+                               probs[i].act_scale, probs[i].y, probs[i].acc, static_cast<int>(probs[i].out_len),
                                g.K, g.N, g.nkb, 0, x_tiled, probs[i].swiglu, probs[i].epi};
         return launch_mfma_group(args, np, stream);
     }
@@ -699,11 +702,11 @@ int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t
 }
 
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu,
+                 const float *act_scale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu,
                  const GemmEpilogue *epi) {
     int st = check_mfma_shape(out_len, in_len);
     if (st) return st;
-    if (!w_mfma || !w_scale || !xq || !dscale || !y || !ncols)
+    if (!w_mfma || !w_scale || !xq || !act_scale || !y || !ncols)
         return fail(OURO_ERR_INVALID_ARG, "ouro_gemm_i2_mfma: NULL argument or ncols == 0");
     if (ncols > (1u << 24)) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: ncols %zu too large", ncols);
     if (reinterpret_cast<uintptr_t>(w_mfma) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
@@ -712,7 +715,7 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     a.w = reinterpret_cast<const uint4 *>(w_mfma);
     a.w_scale = w_scale;
     a.xq = xq;
-    a.dscale = dscale;
+    a.act_scale = act_scale;
     a.y = y;
     a.acc = acc;
     a.M = static_cast<int>(out_len);
@@ -730,7 +733,7 @@ int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const flo
     if (x_tiled && ncols > static_cast<size_t>(kSkinnyCols))
         return fail(OURO_ERR_SHAPE, "i2 gemm: fragment-ordered x is for <= %d columns", kSkinnyCols);
     if (ncols <= static_cast<size_t>(kSkinnyCols)) {
-        const GemmProblem one{w_mfma, out_len, w_scale, xq, dscale, y, acc, epi ? *epi : GemmEpilogue{}, 0};
+        const GemmProblem one{w_mfma, out_len, w_scale, xq, act_scale, y, acc, epi ? *epi : GemmEpilogue{}, 0};
         return i2_gemm_skinny_group(&one, 1, in_len, ncols, x_tiled, stream);
     }
     const int nrt = (a.M + 15) / 16;
@@ -757,14 +760,21 @@ size_t ouro_i2_mfma_bytes(size_t out_len, size_t in_len) { return ouro::i2_mfma_
 int ouro_i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst,
                       const float *w_scale_or_null, void *stream) {
     OURO_REQUIRE_INIT();
-    return ouro::i2_tile_mfma(canonical, out_len, in_len, dst, w_scale_or_null, stream);
+    return ouro::i2_tile_mfma(canonical, out_len, in_len, dst, w_scale_or_null, stream, 0);
+}
+
+int ouro_i2s_tile_mfma(const uint8_t *i2s, size_t out_len, size_t in_len, uint8_t *dst, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (!i2s) return ouro::fail(OURO_ERR_INVALID_ARG, "ouro_i2s_tile_mfma: NULL argument");
+    return ouro::i2_tile_mfma(i2s, out_len, in_len, dst, reinterpret_cast<const float *>(i2s + out_len * in_len / 4),
+                              stream, 1);
 }
 
 int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale,
-                      const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc_or_null,
+                      const int8_t *xq, const float *act_scale, size_t ncols, float *y, int32_t *acc_or_null,
                       void *stream) {
     OURO_REQUIRE_INIT();
-    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream, 0, 0, nullptr);
+    return ouro::i2_gemm_mfma(w_mfma, out_len, in_len, w_scale, xq, act_scale, ncols, y, acc_or_null, stream, 0, 0, nullptr);
 }
 
 }  // extern "C"

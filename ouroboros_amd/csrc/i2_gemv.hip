@@ -7,8 +7,10 @@
 // its activation slice in registers for all rows it visits, and 2-bit codes
 // are expanded to int8 in registers and consumed by v_dot4_i32_i8.
 //
-// Integer accumulation is exact in any order; the fp32 epilogue is two
-// separately rounded products, so results are bit-identical to the oracle.
+// Activations are bitnet.cpp's I8_S rows (quantize_row_i8_s) and the
+// epilogue is its I2_S mul_mat one, y = (acc / s) * w_scale.  Integer
+// accumulation is exact in any order and the epilogue is two separately
+// rounded operations, so results are bit-identical to the oracle.
 #include "common.hpp"
 
 #include <type_traits>
@@ -47,9 +49,10 @@ __host__ __device__ constexpr int kgroup(int G, int l, int g) {
 
 // ------------------------------------------------------------ tiling --
 
-// One thread per 32-bit word of the tiled layout.
+// One thread per 32-bit word of the tiled layout.  The source is canonical
+// codes, or (src_i2s) the codes of a bitnet.cpp I2_S tensor.
 __global__ void i2_tile_kernel(const uint8_t *__restrict__ canon, uint32_t *__restrict__ tiled,
-                               int out_len, int G, long long total_words) {
+                               int out_len, int G, long long total_words, int src_i2s) {
     long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (id >= total_words) return;
     constexpr int R = kTileRows;
@@ -67,7 +70,9 @@ __global__ void i2_tile_kernel(const uint8_t *__restrict__ canon, uint32_t *__re
         const int r = gi / G, g = gi % G;
         const long long row = t * R + r;
         uint32_t byte = 0x55;  // padding rows: code 1 (w = 0) everywhere
-        if (row < out_len) byte = canon[row * row_bytes + kgroup(G, lane, g)];
+        if (row < out_len)
+            byte = src_i2s ? i2s_canon_byte(canon, row, 256 * G, kgroup(G, lane, g))
+                           : canon[row * row_bytes + kgroup(G, lane, g)];
 #pragma unroll
         for (int b = 0; b < 4; ++b) word |= ((byte >> (2 * b)) & 3u) << (8 * b + 2 * f);
     }
@@ -98,11 +103,12 @@ __device__ __forceinline__ float block_max_256(float v, float *red) {
     return m;
 }
 
-// One 256-thread block per row.
+// One 256-thread block per row: quantize_row_i8_s (bitnet.cpp), s = 127 /
+// max(max|x|, 1e-5), q = clamp(round(x * s), -128, 127).
 template <typename T>
 __global__ __launch_bounds__(256) void act_quant_kernel(const T *__restrict__ x, long long n,
                                                         int8_t *__restrict__ xq,
-                                                        float *__restrict__ dscale) {
+                                                        float *__restrict__ act_scale) {
     __shared__ float red[4];
     const long long row = blockIdx.x;
     const T *xr = x + row * n;
@@ -110,18 +116,10 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const T *__restrict__ x,
     for (long long i = threadIdx.x; i < n; i += blockDim.x) amax = fmaxf(amax, fabsf(load_act(xr, i)));
     amax = block_max_256(amax, red);
     int8_t *qr = xq + row * n;
-    if (amax == 0.f) {
-        for (long long i = threadIdx.x; i < n; i += blockDim.x) qr[i] = 0;
-        if (threadIdx.x == 0) dscale[row] = 0.f;
-        return;
-    }
-    const float s = 127.0f / amax;
-    for (long long i = threadIdx.x; i < n; i += blockDim.x) {
-        float t = rintf(load_act(xr, i) * s);
-        t = fminf(fmaxf(t, -127.f), 127.f);
-        qr[i] = static_cast<int8_t>(t);
-    }
-    if (threadIdx.x == 0) dscale[row] = amax / 127.0f;
+    const float s = i8s_scale(amax);
+    for (long long i = threadIdx.x; i < n; i += blockDim.x)
+        qr[i] = static_cast<int8_t>(i8s_quant(load_act(xr, i), s));
+    if (threadIdx.x == 0) act_scale[row] = s;
 }
 
 // ------------------------------------------------------------- GEMV --
@@ -132,7 +130,7 @@ struct GemvArgs {
     const float *w_scale;   // per matrix, stride 1
     const int8_t *xq;       // [ncols][in_len] of matrix 0
     long long x_stride;     // elements between matrices
-    const float *dscale;    // [ncols] of matrix 0, per matrix stride ncols
+    const float *act_scale;    // [ncols] of matrix 0, per matrix stride ncols
     float *y;               // [ncols][out_len] of matrix 0
     long long y_stride;     // elements between matrices
     int32_t *acc;           // optional, same layout as y (matrix 0 only)
@@ -241,7 +239,7 @@ __global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
 
     const uint8_t *w = a.w + mat * a.w_stride;
     const int8_t *xq = a.xq + mat * a.x_stride;
-    const float *dscale = a.dscale + static_cast<long long>(mat) * a.ncols;
+    const float *act_scale = a.act_scale + static_cast<long long>(mat) * a.ncols;
     float *y = a.y + mat * a.y_stride;
     const float wscale = a.w_scale[mat];
 
@@ -340,7 +338,7 @@ __global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
             const int row = tile * R + lane / span;
             if (lane % span == span - 1 && row < a.out_len && c0 + c < a.ncols) {
                 const long long o = static_cast<long long>(c0 + c) * a.out_len + row;
-                const float v = (static_cast<float>(total) * dscale[c0 + c]) * wscale;
+                const float v = i8s_out(total, act_scale[c0 + c], wscale);
                 y[o] = v;
                 if (a.acc) a.acc[o] = total;
             }
@@ -397,6 +395,98 @@ GemvPick pick_gemv(int G, int ncols, long long total_tiles) {
     }
 }
 
+// ------------------------------------------------------- raw I2_S GEMV --
+//
+// y = W x straight from a bitnet.cpp I2_S tensor (ouro_matvec_q with
+// OURO_KIND_I2_S).  Row r is in_len/4 bytes at r*in_len/4 (in_len % 256 == 0,
+// so no 128-block straddles two rows), i.e. in_len/64 chunks of 16 bytes;
+// chunk c is half h = c%2 of block c/2, and field f (bits 6-2f) of its word
+// w (bytes 4w..4w+3) holds the codes of weights
+// k = 128*(c/2) + 32*f + 16*h + 4*w + i (byte i of the word), so every
+// field of a word meets four consecutive activations.  Lane l owns chunks
+// c = l + 64*s (s < NS) of every row: its activations (one 16-byte load per
+// field and chunk) stay in registers while the wavefront reads its 8 rows,
+// each row one contiguous in_len/4-byte span.  Lanes past the last chunk read a
+// clamped chunk against zero activations.
+struct I2sArgs {
+    const uint8_t *w;
+    const float *w_scale;
+    const int8_t *xq;        // [ncols][in_len]
+    const float *act_scale;  // [ncols]
+    float *y;                // [ncols][out_len]
+    int32_t *acc;            // optional, same layout as y
+    int out_len, in_len;
+};
+
+constexpr int kI2sWaves = 4;
+
+template <int NS>
+__global__ __launch_bounds__(kWave *kI2sWaves) void i2s_gemv_kernel(I2sArgs a) {
+    constexpr int R = kTileRows;  // rows per wavefront, reduced as in the tiled GEMV
+    const int lane = threadIdx.x % kWave;
+    const int row0 = (blockIdx.x * kI2sWaves + static_cast<int>(threadIdx.x / kWave)) * R;
+    if (row0 >= a.out_len) return;  // whole wavefront leaves together
+    const int col = blockIdx.y;
+    const int chunks = a.in_len / 64;
+    const int8_t *xr = a.xq + static_cast<long long>(col) * a.in_len;
+    u32x4 xv[NS][4];
+    int sx = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int c = lane + 64 * s;
+        const int cc = c < chunks ? c : chunks - 1;
+        const int k0 = 128 * (cc >> 1) + 16 * (cc & 1);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(xr + k0 + 32 * f);
+            xv[s][f] = c < chunks ? v : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                sx = __builtin_amdgcn_sdot4(static_cast<int>(xv[s][f][q]), 0x01010101, sx, false);
+        }
+    }
+    const long long rb = a.in_len / 4;
+    int s1[R], s4[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        s1[r] = -sx;  // codes are w + 1
+        s4[r] = 0;
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int c = lane + 64 * s;
+        const int cc = c < chunks ? c : chunks - 1;
+        u32x4 wv[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int row = row0 + r < a.out_len ? row0 + r : a.out_len - 1;
+            wv[r] = *reinterpret_cast<const u32x4 *>(a.w + row * rb + 16 * cc);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t word = wv[r][q], hi = word >> 4;
+                // fields 0 and 2 masked at scale 4, fields 1 and 3 at scale 1
+                s4[r] = __builtin_amdgcn_sdot4(static_cast<int>(hi & 0x0c0c0c0cu), static_cast<int>(xv[s][0][q]), s4[r], false);
+                s1[r] = __builtin_amdgcn_sdot4(static_cast<int>(hi & 0x03030303u), static_cast<int>(xv[s][1][q]), s1[r], false);
+                s4[r] = __builtin_amdgcn_sdot4(static_cast<int>(word & 0x0c0c0c0cu), static_cast<int>(xv[s][2][q]), s4[r], false);
+                s1[r] = __builtin_amdgcn_sdot4(static_cast<int>(word & 0x03030303u), static_cast<int>(xv[s][3][q]), s1[r], false);
+            }
+    }
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = s1[r] + (s4[r] >> 2);  // s4 is a multiple of 4
+    const int total = row_totals<R>(acc, lane);
+    constexpr int span = kWave / R;
+    const int row = row0 + lane / span;
+    if (lane % span == span - 1 && row < a.out_len) {
+        const long long o = static_cast<long long>(col) * a.out_len + row;
+        a.y[o] = i8s_out(total, a.act_scale[col], *a.w_scale);
+        if (a.acc) a.acc[o] = total;
+    }
+}
+
 int launch_gemv(const GemvArgs &base, int count, void *stream) {
     const int G = base.in_len / 256;
     const int tiles = base.tiles;
@@ -422,11 +512,11 @@ int check_i2_shape(size_t out_len, size_t in_len) {
 
 // Internal entry shared with the matvec_q surface and resident weights.
 int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *w_scale,
-            const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc,
+            const int8_t *xq, const float *act_scale, size_t ncols, float *y, int32_t *acc,
             void *stream) {
     int st = check_i2_shape(out_len, in_len);
     if (st) return st;
-    if (!w_tiled || !w_scale || !xq || !dscale || !y || !ncols)
+    if (!w_tiled || !w_scale || !xq || !act_scale || !y || !ncols)
         return fail(OURO_ERR_INVALID_ARG, "ouro_gemm_i2: NULL argument or ncols == 0");
     if (reinterpret_cast<uintptr_t>(w_tiled) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
         return fail(OURO_ERR_ALIGN, "ouro_gemm_i2: weights and xq need 16-byte alignment");
@@ -437,7 +527,7 @@ int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *
     a.w_scale = w_scale;
     a.xq = xq;
     a.x_stride = 0;
-    a.dscale = dscale;
+    a.act_scale = act_scale;
     a.y = y;
     a.y_stride = 0;
     a.acc = acc;
@@ -448,18 +538,18 @@ int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *
     return launch_gemv(a, 1, stream);
 }
 
-int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale,
+int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *act_scale,
               void *stream) {
-    if (!x || !xq || !dscale) return fail(OURO_ERR_INVALID_ARG, "ouro_act_quant_i8: NULL argument");
+    if (!x || !xq || !act_scale) return fail(OURO_ERR_INVALID_ARG, "ouro_act_quant_i8: NULL argument");
     if (!rows || !n) return fail(OURO_ERR_SHAPE, "ouro_act_quant_i8: empty shape");
     if (rows > 0x7fffffff) return fail(OURO_ERR_SHAPE, "ouro_act_quant_i8: too many rows");
     dim3 grid(static_cast<unsigned>(rows)), block(256);
     if (x_dtype == OURO_DT_F32)
         hipLaunchKernelGGL(act_quant_kernel<float>, grid, block, 0, as_stream(stream),
-                           static_cast<const float *>(x), static_cast<long long>(n), xq, dscale);
+                           static_cast<const float *>(x), static_cast<long long>(n), xq, act_scale);
     else if (x_dtype == OURO_DT_BF16)
         hipLaunchKernelGGL(act_quant_kernel<uint16_t>, grid, block, 0, as_stream(stream),
-                           static_cast<const uint16_t *>(x), static_cast<long long>(n), xq, dscale);
+                           static_cast<const uint16_t *>(x), static_cast<long long>(n), xq, act_scale);
     else
         return fail(OURO_ERR_INVALID_ARG, "ouro_act_quant_i8: bad dtype %d", x_dtype);
     return check_launch("act_quant_kernel");
@@ -472,8 +562,9 @@ size_t i2_tiled_bytes(size_t out_len, size_t in_len) {
     return tiles * R * (in_len / 4);
 }
 
+// Tiles canonical codes (src_i2s = 0) or the codes of an I2_S tensor.
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
-            const float *w_scale, void *stream) {
+            const float *w_scale, void *stream, int src_i2s) {
     int st = check_i2_shape(out_len, in_len);
     if (st) return st;
     if (!canonical || !tiled) return fail(OURO_ERR_INVALID_ARG, "ouro_i2_tile: NULL argument");
@@ -483,7 +574,7 @@ int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *ti
     const long long words = static_cast<long long>(bytes / 4);
     const unsigned blocks = static_cast<unsigned>((words + 255) / 256);
     hipLaunchKernelGGL(i2_tile_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), canonical,
-                       reinterpret_cast<uint32_t *>(tiled), static_cast<int>(out_len), G, words);
+                       reinterpret_cast<uint32_t *>(tiled), static_cast<int>(out_len), G, words, src_i2s);
     st = check_launch("i2_tile_kernel");
     if (st) return st;
     if (w_scale) {
@@ -492,6 +583,38 @@ int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *ti
         st = check_launch("copy_scale_kernel");
     }
     return st;
+}
+
+// y = W x on a raw I2_S tensor (codes, then the fp32 scale at byte
+// out_len*in_len/4) for ncols int8 rows xq with their act_scale.
+int i2s_gemm(const uint8_t *i2s, size_t out_len, size_t in_len, const int8_t *xq, const float *act_scale,
+             size_t ncols, float *y, int32_t *acc, void *stream) {
+    int st = check_i2_shape(out_len, in_len);
+    if (st) return st;
+    if (!i2s || !xq || !act_scale || !y || !ncols)
+        return fail(OURO_ERR_INVALID_ARG, "i2_s gemv: NULL argument or ncols == 0");
+    if (reinterpret_cast<uintptr_t>(i2s) % 16 || reinterpret_cast<uintptr_t>(xq) % 16)
+        return fail(OURO_ERR_ALIGN, "i2_s gemv: payload and xq need 16-byte alignment");
+    if (ncols > 65535) return fail(OURO_ERR_SHAPE, "i2_s gemv: more than 65535 columns");
+    const int ns = static_cast<int>((in_len / 64 + 63) / 64);
+    I2sArgs a{i2s, reinterpret_cast<const float *>(i2s + out_len * in_len / 4), xq, act_scale, y, acc,
+              static_cast<int>(out_len), static_cast<int>(in_len)};
+    void (*fn)(I2sArgs) = nullptr;
+    switch (ns) {
+    case 1: fn = i2s_gemv_kernel<1>; break;
+    case 2: fn = i2s_gemv_kernel<2>; break;
+    case 3: fn = i2s_gemv_kernel<3>; break;
+    case 4: fn = i2s_gemv_kernel<4>; break;
+    case 5: fn = i2s_gemv_kernel<5>; break;
+    case 6: fn = i2s_gemv_kernel<6>; break;
+    case 7: fn = i2s_gemv_kernel<7>; break;
+    case 8: fn = i2s_gemv_kernel<8>; break;
+    default: return fail(OURO_ERR_SHAPE, "i2_s gemv: in_len %zu > 32768", in_len);
+    }
+    const size_t rows_per_block = static_cast<size_t>(kTileRows) * kI2sWaves;
+    dim3 grid(static_cast<unsigned>((out_len + rows_per_block - 1) / rows_per_block), static_cast<unsigned>(ncols));
+    hipLaunchKernelGGL(fn, grid, dim3(kWave * kI2sWaves), 0, as_stream(stream), a);
+    return check_launch("i2s_gemv_kernel");
 }
 
 }  // namespace ouro
@@ -505,30 +628,36 @@ size_t ouro_i2_tiled_bytes(size_t out_len, size_t in_len) { return i2_tiled_byte
 int ouro_i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
                  const float *w_scale_or_null, void *stream) {
     OURO_REQUIRE_INIT();
-    return i2_tile(canonical, out_len, in_len, tiled, w_scale_or_null, stream);
+    return i2_tile(canonical, out_len, in_len, tiled, w_scale_or_null, stream, 0);
+}
+
+int ouro_i2s_tile(const uint8_t *i2s, size_t out_len, size_t in_len, uint8_t *tiled, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (!i2s) return fail(OURO_ERR_INVALID_ARG, "ouro_i2s_tile: NULL argument");
+    return i2_tile(i2s, out_len, in_len, tiled, reinterpret_cast<const float *>(i2s + out_len * in_len / 4), stream, 1);
 }
 
 int ouro_act_quant_i8(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq,
-                      float *dscale, void *stream) {
+                      float *act_scale, void *stream) {
     OURO_REQUIRE_INIT();
-    return act_quant(x, x_dtype, rows, n, xq, dscale, stream);
+    return act_quant(x, x_dtype, rows, n, xq, act_scale, stream);
 }
 
 int ouro_gemm_i2(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *w_scale,
-                 const int8_t *xq, const float *dscale, size_t ncols, float *y,
+                 const int8_t *xq, const float *act_scale, size_t ncols, float *y,
                  int32_t *acc_or_null, void *stream) {
     OURO_REQUIRE_INIT();
-    return i2_gemm(w_tiled, out_len, in_len, w_scale, xq, dscale, ncols, y, acc_or_null, stream);
+    return i2_gemm(w_tiled, out_len, in_len, w_scale, xq, act_scale, ncols, y, acc_or_null, stream);
 }
 
 int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride, const float *w_scale,
-                         const int8_t *xq, size_t x_stride, const float *dscale, float *y,
+                         const int8_t *xq, size_t x_stride, const float *act_scale, float *y,
                          size_t y_stride, size_t out_len, size_t in_len, size_t count,
                          void *stream) {
     OURO_REQUIRE_INIT();
     int st = check_i2_shape(out_len, in_len);
     if (st) return st;
-    if (!w_tiled || !w_scale || !xq || !dscale || !y || !count)
+    if (!w_tiled || !w_scale || !xq || !act_scale || !y || !count)
         return fail(OURO_ERR_INVALID_ARG, "ouro_gemv_i2_grouped: NULL argument or count == 0");
     if (count > 65535) return fail(OURO_ERR_SHAPE, "ouro_gemv_i2_grouped: count > 65535");
     if (w_stride < i2_tiled_bytes(out_len, in_len) || w_stride % 16 || x_stride < in_len ||
@@ -543,7 +672,7 @@ int ouro_gemv_i2_grouped(const uint8_t *w_tiled, size_t w_stride, const float *w
     a.w_scale = w_scale;
     a.xq = xq;
     a.x_stride = static_cast<long long>(x_stride);
-    a.dscale = dscale;
+    a.act_scale = act_scale;
     a.y = y;
     a.y_stride = static_cast<long long>(y_stride);
     a.acc = nullptr;

@@ -13,11 +13,13 @@
 namespace ouro {
 
 int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *w_scale,
-            const int8_t *xq, const float *dscale, size_t ncols, float *y, int32_t *acc,
+            const int8_t *xq, const float *act_scale, size_t ncols, float *y, int32_t *acc,
             void *stream);
-int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale,
+int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *act_scale,
               void *stream);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
+int i2s_gemm(const uint8_t *i2s, size_t out_len, size_t in_len, const int8_t *xq, const float *act_scale,
+             size_t ncols, float *y, int32_t *acc, void *stream);
 
 namespace {
 
@@ -218,7 +220,7 @@ int launch_mv(int kind, const MvArgs &a, hipStream_t s) {
 // (ops.rs:296), TQ1_0 rows whole 256-blocks (QuantKind::row_bytes,
 // dequant.rs:376-387).
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *dscale_scratch, void *stream) {
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream) {
     if (!payload || !x || !y) return fail(OURO_ERR_INVALID_ARG, "matvec_q: NULL argument");
     if (!out_len || !in_len || !k) return fail(OURO_ERR_SHAPE, "matvec_q: empty shape");
     if (out_len > 0x7fffffffULL || in_len > 0x7fffffffULL || k > 0x7fffffffULL)
@@ -237,11 +239,12 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     case OURO_KIND_BF16:
         if (reinterpret_cast<uintptr_t>(payload) % 2) return fail(OURO_ERR_ALIGN, "matvec_q F16: payload alignment");
         break;
-    case OURO_KIND_I2: {
+    case OURO_KIND_I2:
+    case OURO_KIND_I2_S: {
         const size_t tb = i2_tiled_bytes(out_len, in_len);
         if (!tb) return fail(OURO_ERR_SHAPE, "matvec_q I2: in_len %zu not a multiple of 256", in_len);
         int8_t *xq = xq_scratch;
-        float *ds = dscale_scratch;
+        float *ds = act_scale_scratch;
         if (!xq) {
             const size_t xb = (k * in_len + 255) & ~size_t(255);
             uint8_t *ws = static_cast<uint8_t *>(workspace(xb + k * sizeof(float), stream));
@@ -252,6 +255,7 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
         int st = act_quant(x, OURO_DT_F32, k, in_len, xq, ds, stream);
         if (st) return st;
         const uint8_t *w = static_cast<const uint8_t *>(payload);
+        if (kind == OURO_KIND_I2_S) return i2s_gemm(w, out_len, in_len, xq, ds, k, y, nullptr, stream);
         return i2_gemm(w, out_len, in_len, reinterpret_cast<const float *>(w + tb), xq, ds, k, y,
                        nullptr, stream);
     }

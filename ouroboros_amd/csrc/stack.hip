@@ -19,9 +19,9 @@ namespace ouro {
 // hot-path kernels
 size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
-                 void *stream);
+                 void *stream, int src_i2s);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
+                 const float *act_scale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
                  const GemmEpilogue *epi = nullptr);
 size_t gdn_chunk_ws_bytes(size_t T, size_t N, size_t Hv);
 int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v, const float *gate,
@@ -175,7 +175,7 @@ int make_lin(ouro_stack *s, Lin &L, uint32_t tensor, size_t out, size_t in, uint
     if (st) return st;
     L.scale = reinterpret_cast<float *>(L.w + tb);
     if ((st = gen_codes(s->seed, tensor, out, in, canon_scratch, nullptr))) return st;
-    if ((st = i2_tile_mfma(canon_scratch, out, in, L.w, nullptr, nullptr))) return st;
+    if ((st = i2_tile_mfma(canon_scratch, out, in, L.w, nullptr, nullptr, 0))) return st;
     const float sc = static_cast<float>(1.0 / std::sqrt(static_cast<double>(in) * 2.0 / 3.0));
     if (hipMemcpy(L.scale, &sc, 4, hipMemcpyHostToDevice) != hipSuccess) return fail(OURO_ERR_HIP, "stack: scale copy");
     return hipDeviceSynchronize() == hipSuccess ? OURO_OK : fail(OURO_ERR_HIP, "stack: weight generation");
@@ -197,7 +197,7 @@ int make_lin_pair(ouro_stack *s, Lin &L, uint32_t t_up, uint32_t t_gate, size_t 
     if (hipMemcpy2D(pair, 2 * rb, up, rb, rb, out, hipMemcpyDeviceToDevice) != hipSuccess ||
         hipMemcpy2D(pair + rb, 2 * rb, gate, rb, rb, out, hipMemcpyDeviceToDevice) != hipSuccess)
         return fail(OURO_ERR_HIP, "stack: interleaving up and gate");
-    if ((st = i2_tile_mfma(pair, 2 * out, in, L.w, nullptr, nullptr))) return st;
+    if ((st = i2_tile_mfma(pair, 2 * out, in, L.w, nullptr, nullptr, 0))) return st;
     const float sc = static_cast<float>(1.0 / std::sqrt(static_cast<double>(in) * 2.0 / 3.0));
     if (hipMemcpy(L.scale, &sc, 4, hipMemcpyHostToDevice) != hipSuccess) return fail(OURO_ERR_HIP, "stack: scale copy");
     return hipDeviceSynchronize() == hipSuccess ? OURO_OK : fail(OURO_ERR_HIP, "stack: weight generation");

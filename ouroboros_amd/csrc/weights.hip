@@ -9,21 +9,22 @@
 // nothing.
 #include "common.hpp"
 
+#include <cstring>
 #include <new>
 
 namespace ouro {
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *dscale_scratch, void *stream);
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream);
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
-            const float *w_scale, void *stream);
+            const float *w_scale, void *stream, int src_i2s);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
 size_t i2_mfma_bytes(size_t out_len, size_t in_len);
 int i2_tile_mfma(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *dst, const float *w_scale,
-                 void *stream);
+                 void *stream, int src_i2s);
 int i2_gemm_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len, const float *w_scale, const int8_t *xq,
-                 const float *dscale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
+                 const float *act_scale, size_t ncols, float *y, int32_t *acc, void *stream, int x_tiled, int swiglu = 0,
                  const GemmEpilogue *epi = nullptr);
-int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *dscale, void *stream);
+int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, float *act_scale, void *stream);
 size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream);
@@ -38,7 +39,7 @@ struct ouro_weight {
     void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
     void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes
     int8_t *xq = nullptr;     // I2: activation scratch
-    float *dscale = nullptr;
+    float *act_scale = nullptr;
     float *partial = nullptr; // TL1: per-group-block partial sums
     void *aux = nullptr;      // one allocation: y scratch [out_len] f32, then the argmax key slots
     float *y = nullptr;
@@ -60,10 +61,15 @@ size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:
     case OURO_KIND_BF16: return k * 2;
     case OURO_KIND_TL1: return k / 128 * 28;
     case OURO_KIND_TQ1_0: return k / 256 * 54;
-    case OURO_KIND_I2: return k / 4;
+    case OURO_KIND_I2:
+    case OURO_KIND_I2_S: return k / 4;
     default: return 0;
     }
 }
+
+// Bytes of a bitnet.cpp I2_S tensor: the codes, the fp32 scale, and up to
+// 28 bytes of alignment padding (quantize_i2_s writes n/4 + 32).
+bool i2s_size_ok(size_t bytes, size_t codes) { return bytes >= codes + 4 && bytes <= codes + 32; }
 
 void release(ouro_weight *w) {
     if (!w) return;
@@ -86,15 +92,19 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
     *out = nullptr;
     const size_t rb = ref_row_bytes(kind, in_len);
     if (!rb) return fail(OURO_ERR_KIND, "ouro_weight_upload: kind %d / in_len %zu unsupported", kind, in_len);
-    if (!out_len || bytes != rb * out_len)
-        return fail(OURO_ERR_SHAPE, "ouro_weight_upload: %zu bytes, expected %zu", bytes, rb * out_len);
+    if (!out_len || (kind == OURO_KIND_I2_S ? !i2s_size_ok(bytes, rb * out_len) : bytes != rb * out_len))
+        return fail(OURO_ERR_SHAPE, "ouro_weight_upload: %zu bytes, expected %zu%s", bytes, rb * out_len,
+                    kind == OURO_KIND_I2_S ? " + 4..32 (scale and padding)" : "");
     ouro_weight *w = new (std::nothrow) ouro_weight;
     if (!w) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_upload: out of host memory");
     w->kind = kind;
     w->out_len = out_len;
     w->in_len = in_len;
     w->max_cols = max_cols ? max_cols : 1;
-    if (kind == OURO_KIND_I2) {
+    if (kind == OURO_KIND_I2 || kind == OURO_KIND_I2_S) {
+        // both are held as the tiled I2 payload (and the MFMA layout)
+        const int src_i2s = kind == OURO_KIND_I2_S;
+        w->kind = OURO_KIND_I2;
         const size_t tb = i2_tiled_bytes(out_len, in_len);
         if (!tb) {
             release(w);
@@ -107,17 +117,20 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
         }
         int st = OURO_OK;
+        // I2_S carries its own scale right after the codes (quantize_i2_s)
+        float scale = w_scale;
+        if (src_i2s) memcpy(&scale, static_cast<const uint8_t *>(host) + rb * out_len, 4);
         if (hipMemcpy(canon, host, bytes, hipMemcpyHostToDevice) != hipSuccess ||
-            hipMemcpy(static_cast<uint8_t *>(w->payload) + tb, &w_scale, 4, hipMemcpyHostToDevice) != hipSuccess)
+            hipMemcpy(static_cast<uint8_t *>(w->payload) + tb, &scale, 4, hipMemcpyHostToDevice) != hipSuccess)
             st = fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         if (!st) st = i2_tile(static_cast<const uint8_t *>(canon), out_len, in_len,
-                              static_cast<uint8_t *>(w->payload), nullptr, nullptr);
+                              static_cast<uint8_t *>(w->payload), nullptr, nullptr, src_i2s);
         if (!st && w->max_cols >= kMfmaCols) {  // second layout for many-column matmuls
             if (hipMalloc(&w->mfma, i2_mfma_bytes(out_len, in_len)) != hipSuccess)
                 st = fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
             else
                 st = i2_tile_mfma(static_cast<const uint8_t *>(canon), out_len, in_len,
-                                  static_cast<uint8_t *>(w->mfma), nullptr, nullptr);
+                                  static_cast<uint8_t *>(w->mfma), nullptr, nullptr, src_i2s);
         }
         if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
         (void)hipFree(canon);
@@ -132,7 +145,7 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             return fail(OURO_ERR_HIP, "ouro_weight_upload: scratch allocation failed");
         }
         w->xq = static_cast<int8_t *>(scratch);
-        w->dscale = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + xb);
+        w->act_scale = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + xb);
     } else if (kind == OURO_KIND_TL1) {
         // repack for the lookup kernel; the raw payload lives only during the upload
         void *raw = nullptr;
@@ -204,14 +217,14 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         return OURO_OK;
     }
     if (w->kind == OURO_KIND_I2 && w->mfma && k >= kMfmaCols) {
-        int st = act_quant(x, OURO_DT_F32, k, w->in_len, w->xq, w->dscale, stream);
+        int st = act_quant(x, OURO_DT_F32, k, w->in_len, w->xq, w->act_scale, stream);
         if (st) return st;
         const float *w_scale =
             reinterpret_cast<const float *>(static_cast<const uint8_t *>(w->payload) + i2_tiled_bytes(w->out_len, w->in_len));
-        return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->dscale,
+        return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->act_scale,
                             k, y, nullptr, stream, 0);
     }
-    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->dscale, stream);
+    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->act_scale, stream);
 }
 
 int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t *idx, void *stream) {

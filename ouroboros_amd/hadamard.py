@@ -39,11 +39,11 @@ def rotate_inv(x, signs, block_size: int, stream=None) -> None:
 
 def fwht_rows(x: DeviceBuffer, y: DeviceBuffer | None, rows: int, n: int, block: int,
               signs: DeviceBuffer | None = None, inverse: bool = False,
-              xq: DeviceBuffer | None = None, dscale: DeviceBuffer | None = None,
+              xq: DeviceBuffer | None = None, act_scale: DeviceBuffer | None = None,
               stream=None) -> None:
     """Rotate `rows` rows of n (dtype from the buffers: float32 or bf16 as uint16)."""
     dt = lambda b: _lib.DT_BF16 if b.dtype == np.uint16 else _lib.DT_F32
     call("ouro_fwht_rows", x.ptr, dt(x), y.ptr if y is not None else None,
          dt(y) if y is not None else _lib.DT_F32, rows, n, block,
          signs.ptr if signs is not None else None, _lib.FWHT_INVERSE if inverse else 0,
-         xq.ptr if xq is not None else None, dscale.ptr if dscale is not None else None, stream)
+         xq.ptr if xq is not None else None, act_scale.ptr if act_scale is not None else None, stream)

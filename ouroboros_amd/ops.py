@@ -57,6 +57,28 @@ def i2_payload(canonical: np.ndarray | DeviceBuffer, out_len: int, in_len: int, 
     return out
 
 
+def i2s_payload(i2s: np.ndarray | DeviceBuffer, out_len: int, in_len: int, stream=None) -> DeviceBuffer:
+    """Device OURO_KIND_I2 payload (tiled codes + the tensor's scale) from a bitnet.cpp I2_S tensor."""
+    ib, _ = _dev(i2s, np.uint8)
+    tb = i2_tiled_bytes(out_len, in_len)
+    if tb == 0:
+        raise ValueError(f"I2_S repack needs in_len % 256 == 0 (got {in_len})")
+    out = DeviceBuffer((tb + 16,), np.uint8)
+    call("ouro_i2s_tile", ib.ptr, out_len, in_len, out.ptr, stream)
+    return out
+
+
+def i2s_mfma_payload(i2s: np.ndarray | DeviceBuffer, out_len: int, in_len: int, stream=None) -> DeviceBuffer:
+    """Device MFMA-tiled codes + the tensor's scale from a bitnet.cpp I2_S tensor."""
+    ib, _ = _dev(i2s, np.uint8)
+    tb = i2_mfma_bytes(out_len, in_len)
+    if tb == 0:
+        raise ValueError(f"I2_S repack needs in_len % 256 == 0 (got {in_len})")
+    out = DeviceBuffer((tb + 16,), np.uint8)
+    call("ouro_i2s_tile_mfma", ib.ptr, out_len, in_len, out.ptr, stream)
+    return out
+
+
 def i2_mfma_bytes(out_len: int, in_len: int) -> int:
     return int(_lib.lib().ouro_i2_mfma_bytes(out_len, in_len))
 
@@ -75,26 +97,27 @@ def i2_mfma_payload(canonical: np.ndarray | DeviceBuffer, out_len: int, in_len: 
 
 
 def gemm_i2_mfma(w_payload: DeviceBuffer, out_len: int, in_len: int, xq: DeviceBuffer,
-                 dscale: DeviceBuffer, ncols: int, y: DeviceBuffer, acc: DeviceBuffer | None = None,
+                 act_scale: DeviceBuffer, ncols: int, y: DeviceBuffer, acc: DeviceBuffer | None = None,
                  stream=None) -> None:
     """MFMA-tiled I2 x int8 columns -> fp32 (and optionally the exact int32 sums)."""
     tb = i2_mfma_bytes(out_len, in_len)
-    call("ouro_gemm_i2_mfma", w_payload.ptr, out_len, in_len, w_payload.ptr + tb, xq.ptr, dscale.ptr,
+    call("ouro_gemm_i2_mfma", w_payload.ptr, out_len, in_len, w_payload.ptr + tb, xq.ptr, act_scale.ptr,
          ncols, y.ptr, acc.ptr if acc is not None else None, stream)
 
 
-def act_quant_i8(x: DeviceBuffer, rows: int, n: int, xq: DeviceBuffer, dscale: DeviceBuffer,
+def act_quant_i8(x: DeviceBuffer, rows: int, n: int, xq: DeviceBuffer, act_scale: DeviceBuffer,
                  stream=None) -> None:
+    """quantize_row_i8_s (bitnet.cpp) per row: int8 rows and act_scale = 127 / max(amax, 1e-5)."""
     dt = _lib.DT_BF16 if x.dtype == np.uint16 else _lib.DT_F32
-    call("ouro_act_quant_i8", x.ptr, dt, rows, n, xq.ptr, dscale.ptr, stream)
+    call("ouro_act_quant_i8", x.ptr, dt, rows, n, xq.ptr, act_scale.ptr, stream)
 
 
 def gemm_i2(w_payload: DeviceBuffer, out_len: int, in_len: int, xq: DeviceBuffer,
-            dscale: DeviceBuffer, ncols: int, y: DeviceBuffer, acc: DeviceBuffer | None = None,
+            act_scale: DeviceBuffer, ncols: int, y: DeviceBuffer, acc: DeviceBuffer | None = None,
             stream=None) -> None:
     """Tiled-I2 x int8 columns -> fp32 (and optionally the exact int32 sums)."""
     tb = i2_tiled_bytes(out_len, in_len)
-    call("ouro_gemm_i2", w_payload.ptr, out_len, in_len, w_payload.ptr + tb, xq.ptr, dscale.ptr,
+    call("ouro_gemm_i2", w_payload.ptr, out_len, in_len, w_payload.ptr + tb, xq.ptr, act_scale.ptr,
          ncols, y.ptr, acc.ptr if acc is not None else None, stream)
 
 

@@ -1,8 +1,10 @@
-"""Quant kinds and the canonical I2 packing (host side, no GPU needed).
+"""Quant kinds and the 2-bit ternary packings (host side, no GPU needed).
 
 ``QuantKind`` mirrors the reference enum (cluster/src/infer/dequant.rs:315-388)
-with the same ggml dtype ids; ``I2`` is the int8-activation x 2-bit ternary
-format of this library (no reference counterpart).
+with the same ggml dtype ids.  ``I2_S`` is bitnet.cpp's 2-bit ternary tensor
+(GGML_TYPE_I2_S of microsoft/BitNet's ggml fork, the reference's bitnet-cpp
+submodule); ``I2`` is this library's resident (device-tiled) layout of the
+same codes.
 """
 from __future__ import annotations
 
@@ -19,6 +21,7 @@ class QuantKind(enum.IntEnum):
     BF16 = _lib.KIND_BF16
     TQ1_0 = _lib.KIND_TQ1_0
     TL1 = _lib.KIND_TL1
+    I2_S = _lib.KIND_I2_S
     I2 = _lib.KIND_I2
 
     @classmethod
@@ -31,10 +34,12 @@ class QuantKind(enum.IntEnum):
         return None if k is cls.I2 else k
 
     def block_bytes(self) -> int:  # dequant.rs:351-363
-        return {self.F32: 4, self.F16: 2, self.BF16: 2, self.TQ1_0: 54, self.TL1: 28, self.I2: 1}[self]
+        return {self.F32: 4, self.F16: 2, self.BF16: 2, self.TQ1_0: 54, self.TL1: 28, self.I2_S: 32,
+                self.I2: 1}[self]
 
     def block_elems(self) -> int:  # dequant.rs:366-373
-        return {self.F32: 1, self.F16: 1, self.BF16: 1, self.TQ1_0: 256, self.TL1: 128, self.I2: 4}[self]
+        return {self.F32: 1, self.F16: 1, self.BF16: 1, self.TQ1_0: 256, self.TL1: 128, self.I2_S: 128,
+                self.I2: 4}[self]
 
     def row_bytes(self, k: int) -> int:  # dequant.rs:376-387
         return k // self.block_elems() * self.block_bytes()
@@ -59,6 +64,41 @@ def i2_unpack(packed: np.ndarray, in_len: int) -> np.ndarray:
     p = np.asarray(packed, dtype=np.uint8).reshape(-1, in_len // 4)
     codes = np.stack([(p >> (2 * f)) & 3 for f in range(4)], axis=-1).reshape(p.shape[0], in_len)
     return codes.astype(np.int8) - 1
+
+
+def i2s_pack(w: np.ndarray, w_scale: float) -> np.ndarray:
+    """bitnet.cpp I2_S bytes of ternary w[out][in] with per-tensor scale w_scale > 0.
+
+    These are the bytes quantize_i2_s makes of w * w_scale: the flattened
+    weights go in blocks of 128; weight j of block b sits in byte
+    32*b + j%32 at bits 6 - 2*(j/32) as code w+1; the fp32 scale
+    max|w * w_scale| (w_scale, or 0 for an all-zero w) follows the n/4 code
+    bytes, then 28 zero bytes (quantize_i2_s writes n/4 + 32 bytes).
+    """
+    w = np.asarray(w)
+    if w.ndim != 2 or w.size % 128:
+        raise ValueError("i2s_pack: need a 2-D matrix with a multiple of 128 elements")
+    if w.size and (w.min() < -1 or w.max() > 1):
+        raise ValueError("i2s_pack: weights must be in {-1, 0, +1}")
+    if not w_scale > 0:
+        raise ValueError("i2s_pack: w_scale must be positive")
+    codes = (w.astype(np.int16) + 1).astype(np.uint8).reshape(-1, 4, 32)  # [block][j/32][j%32]
+    packed = (codes[:, 0] << 6) | (codes[:, 1] << 4) | (codes[:, 2] << 2) | codes[:, 3]
+    out = np.zeros(w.size // 4 + 32, np.uint8)
+    out[: w.size // 4] = packed.reshape(-1)
+    scale = np.float32(w_scale) if w.any() else np.float32(0.0)
+    out[w.size // 4: w.size // 4 + 4] = np.array([scale], np.float32).view(np.uint8)
+    return out
+
+
+def i2s_unpack(buf: np.ndarray, out_len: int, in_len: int) -> tuple[np.ndarray, float]:
+    """Inverse of :func:`i2s_pack`: (w[out][in] with code 3 as +2, the fp32 scale)."""
+    b = np.asarray(buf, dtype=np.uint8)
+    n = out_len * in_len
+    p = b[: n // 4].reshape(-1, 32)
+    codes = np.stack([(p >> (6 - 2 * f)) & 3 for f in range(4)], axis=1)  # [block][j/32][j%32]
+    scale = float(b[n // 4: n // 4 + 4].view(np.float32)[0])
+    return codes.reshape(out_len, in_len).astype(np.int8) - 1, scale
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:

@@ -39,16 +39,19 @@ def main():
              y_scalar=orc.matvec_tl1(payload, out_len, in_len, x, simd=0),
              y_sse=orc.matvec_tl1(payload, out_len, in_len, x, simd=1))
 
-    # 2. I2 GEMM: 3 columns of a 40x512 ternary matrix.
+    # 2. Ternary GEMM in bitnet.cpp's I2_S / I8_S format: 3 columns of a
+    #    40x512 ternary matrix (w_scale 1.5), the int8 rows, the exact sums,
+    #    the outputs and this library's tiled repack of the codes.
     rng = np.random.default_rng(20261201)
     w = rng.integers(-1, 2, size=(40, 512)).astype(np.int8)
     xa = rng.standard_normal((3, 512)).astype(np.float32)
     xa[1, 7] = 40.0  # an outlier row
-    canon = orc.i2_pack(w)
-    xq, ds = orc.act_quant_i8(xa)
-    acc, y = orc.gemm_i2(canon, 40, 512, xq, ds, 1.5)
-    np.savez(HERE / "i2_gemm_40x512x3.npz", canonical=canon, x=xa, w_scale=np.float32(1.5), xq=xq, dscale=ds,
-             acc=acc, y=y, tiled=orc.i2_tile(canon, 40, 512))
+    xa[2, :] = xa[2, :] * 1e-6  # a row below the 1e-5 amax floor
+    i2s = orc.quantize_i2_s((w * np.float32(1.5)).astype(np.float32))
+    xq, s = orc.act_quant_i8(xa)
+    acc, y = orc.gemm_i2s(i2s, 40, 512, xq, s)
+    np.savez(HERE / "i2s_gemm_40x512x3.npz", i2s=i2s, x=xa, xq=xq, act_scale=s, acc=acc, y=y,
+             tiled=orc.i2_tile(orc.i2s_to_canonical(i2s, 40, 512), 40, 512))
 
     # 3. Hadamard: the reference vectors (hadamard.rs:96-126) and a 2x4096 bf16 case.
     n = 16

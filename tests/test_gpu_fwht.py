@@ -87,7 +87,7 @@ def test_fused_quant_equals_separate(gpu, orc, ydt):
     y = DeviceBuffer((rows, n), ydt)
     xq = DeviceBuffer((rows, n), np.int8)
     ds = DeviceBuffer((rows,), np.float32)
-    hadamard.fwht_rows(xd, y, rows, n, 4096, xq=xq, dscale=ds)
+    hadamard.fwht_rows(xd, y, rows, n, 4096, xq=xq, act_scale=ds)
     stored = y.download()
     as_f32 = quant.bf16_bits_to_f32(stored) if ydt == np.uint16 else stored
     want_q, want_ds = orc.act_quant_i8(as_f32)

@@ -1,5 +1,5 @@
 """The HIP path against the committed golden fixtures: bit-exact where the
-path is exact (I2, FWHT), within the stated tolerances elsewhere."""
+path is exact (I2_S / I8_S, FWHT), within the stated tolerances elsewhere."""
 from pathlib import Path
 
 import numpy as np
@@ -19,20 +19,24 @@ def test_tl1_golden(gpu):
     assert (np.abs(y - f["y_scalar"]) / np.maximum(np.abs(f["y_scalar"]), 1e-9) < 1e-5).all()
 
 
-def test_i2_golden(gpu):
-    f = np.load(G / "i2_gemm_40x512x3.npz")
-    p = ops.i2_payload(f["canonical"], 40, 512, float(f["w_scale"]))
+def test_i2s_golden(gpu):
+    f = np.load(G / "i2s_gemm_40x512x3.npz")
+    p = ops.i2s_payload(f["i2s"], 40, 512)
     assert np.array_equal(p.download()[: f["tiled"].size], f["tiled"])
     xd = DeviceBuffer.from_host(f["x"])
     xq = DeviceBuffer((3, 512), np.int8)
-    ds = DeviceBuffer((3,), np.float32)
-    ops.act_quant_i8(xd, 3, 512, xq, ds)
+    s = DeviceBuffer((3,), np.float32)
+    ops.act_quant_i8(xd, 3, 512, xq, s)
     y = DeviceBuffer((3 * 40,), np.float32)
     acc = DeviceBuffer((3 * 40,), np.int32)
-    ops.gemm_i2(p, 40, 512, xq, ds, 3, y, acc)
+    ops.gemm_i2(p, 40, 512, xq, s, 3, y, acc)
     assert np.array_equal(xq.download(), f["xq"])
+    assert np.array_equal(s.download().view(np.uint32), f["act_scale"].view(np.uint32))
     assert np.array_equal(acc.download(), f["acc"])
     assert np.array_equal(y.download().view(np.uint32), f["y"].view(np.uint32))
+    # the raw I2_S tensor through matmul_q gives the same bits
+    y2 = ops.matmul_q(f["i2s"], QuantKind.I2_S, 40, 512, f["x"], 3)
+    assert np.array_equal(y2.view(np.uint32), f["y"].view(np.uint32))
 
 
 def test_hadamard_golden(gpu):

@@ -14,13 +14,13 @@ def test_tl1(orc):
     assert np.array_equal(orc.matvec_tl1(f["payload"], n, k, f["x"], simd=1), f["y_sse"])
 
 
-def test_i2(orc):
-    f = np.load(G / "i2_gemm_40x512x3.npz")
-    xq, ds = orc.act_quant_i8(f["x"])
-    assert np.array_equal(xq, f["xq"]) and np.array_equal(ds, f["dscale"])
-    acc, y = orc.gemm_i2(f["canonical"], 40, 512, xq, ds, float(f["w_scale"]))
+def test_i2s(orc):
+    f = np.load(G / "i2s_gemm_40x512x3.npz")
+    xq, s = orc.act_quant_i8(f["x"])
+    assert np.array_equal(xq, f["xq"]) and np.array_equal(s, f["act_scale"])
+    acc, y = orc.gemm_i2s(f["i2s"], 40, 512, xq, s)
     assert np.array_equal(acc, f["acc"]) and np.array_equal(y, f["y"])
-    assert np.array_equal(orc.i2_tile(f["canonical"], 40, 512), f["tiled"])
+    assert np.array_equal(orc.i2_tile(orc.i2s_to_canonical(f["i2s"], 40, 512), 40, 512), f["tiled"])
 
 
 def test_hadamard(orc):
