@@ -249,6 +249,18 @@ int ouro_matvec_q(const void *payload, int kind, size_t out_len,
 int ouro_matmul_q(const void *payload, int kind, size_t out_len,
                   size_t in_len, const float *x, size_t k, float *y,
                   void *stream);
+/* ouro_matvec_q that allocates nothing, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  No counterpart in the reference.  For the 2-bit
+ * kinds (OURO_KIND_I2_S, OURO_KIND_I2) x is quantised into a static
+ * per-device scratch array of 32 KiB + 256 B that each device holds until
+ * the process ends, so in_len <= 32768 (OURO_ERR_SHAPE beyond); the other
+ * kinds use no scratch and behave exactly as ouro_matvec_q.  Results equal
+ * ouro_matvec_q's bit for bit.  All calls on one device share the scratch:
+ * calls that overlap on one device (e.g. on two streams) race. */
+int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len,
+                          size_t in_len, const float *x, float *y,
+                          void *stream);
 
 /* ------------------------------------------------------------------ */
 /* Walsh-Hadamard rotation                                              */

@@ -85,6 +85,7 @@ SIGNATURES = {
     "ouro_i2_tile_mfma": (i32, [vp, sz, sz, vp, vp, vp]),
     "ouro_gemm_i2_mfma": (i32, [vp, sz, sz, vp, vp, vp, sz, vp, vp, vp]),
     "ouro_matvec_q": (i32, [vp, i32, sz, sz, vp, vp, vp]),
+    "ouro_matvec_q_noalloc": (i32, [vp, i32, sz, sz, vp, vp, vp]),
     "ouro_matmul_q": (i32, [vp, i32, sz, sz, vp, sz, vp, vp]),
     "ouro_fwht_rows": (i32, [vp, i32, vp, i32, sz, sz, sz, vp, u32, vp, vp, vp]),
     "ouro_rotate_fwd": (i32, [vp, vp, sz, sz, vp]),

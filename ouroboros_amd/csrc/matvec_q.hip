@@ -10,6 +10,8 @@
 // payload bytes.  matmul_q decodes each byte once for up to 8 columns.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace ouro {
 
 int i2_gemm(const uint8_t *w_tiled, size_t out_len, size_t in_len, const float *w_scale,
@@ -267,11 +269,63 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     return launch_mv(kind, a, as_stream(stream));
 }
 
+// ---- the allocation-free variant of matvec_q ----
+//
+// Callers that cannot allocate (code under HIP graph capture, tight serving
+// loops) get ouro_matvec_q_noalloc: its 2-bit kinds quantise x into this
+// file-scope device array instead of the library workspace.  Each device
+// holds its own copy until the process ends; its address on a device comes
+// from hipGetSymbolAddress (the array's name is not a device address in
+// host code).  All calls on one device share it, so calls that overlap on
+// one device race.  Nothing in it needs to start at zero: each call writes
+// the in_len int8 values and the scale before the product reads them.
+constexpr size_t kNoAllocMaxIn = 32768;                 // the raw I2_S kernel's limit
+constexpr size_t kNoAllocScratch = kNoAllocMaxIn + 256;  // int8 row, then act_scale
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratch];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up once per device).
+int scratch_ptr(void **out) {
+    const int dev = current_device();
+    if (dev < 0 || dev >= kMaxDevices) return fail(OURO_ERR_NO_DEVICE, "matvec_q_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(OURO_ERR_HIP, "matvec_q_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return OURO_OK;
+}
+}  // namespace
+
 }  // namespace ouro
 
 using namespace ouro;
 
 extern "C" {
+
+int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
+                          float *y, void *stream) {
+    OURO_REQUIRE_INIT();
+    if (kind != OURO_KIND_I2 && kind != OURO_KIND_I2_S)  // no scratch: the plain entry allocates nothing
+        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream);
+    if (in_len > kNoAllocMaxIn)
+        return fail(OURO_ERR_SHAPE, "ouro_matvec_q_noalloc: in_len %zu exceeds the %zu-element static scratch",
+                    in_len, kNoAllocMaxIn);
+    void *p = nullptr;
+    const int st = scratch_ptr(&p);
+    if (st) return st;
+    int8_t *xq = static_cast<int8_t *>(p);
+    float *s = reinterpret_cast<float *>(static_cast<uint8_t *>(p) + kNoAllocMaxIn);
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, xq, s, stream);
+}
 
 int ouro_matvec_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                   float *y, void *stream) {
