@@ -49,9 +49,12 @@ GDN_BYTES = (2 * GDN_B * GDN_HV * GDN_D * GDN_D * 4 + 2 * GDN_B * GDN_HK * GDN_D
 # FWHT 512 x 4096 bf16 in and out.
 FW_ROWS, FW_N, FW_BUFS = 512, 4096, 32
 FW_BYTES = 2 * FW_ROWS * FW_N * 2
+# fused int8 epilogue: bf16 in, int8 rows and one fp32 scale per row out
+FW_Q_BYTES = FW_ROWS * FW_N * 2 + FW_ROWS * FW_N + FW_ROWS * 4
 # Chunked prefill: 4 sequences x 4096 tokens, chunk 64, same heads.
 PF_SEQ, PF_LEN, PF_C = 4, 4096, 64
 PF_T = PF_SEQ * PF_LEN
+PF_CPU_LEN = 512  # tokens per sequence of the CPU baseline's sample
 # Each contraction counted once per (chunk, v-head): K K^T, Q K^T (64x64x128),
 # K S0, Q S0 (64x128x128), T R, Pt U (64x64x128), K^T U (128x64x128).
 PF_FLOP_CHUNK_HEAD = 2 * (64 * 64 * 128 * 4 + 64 * 128 * 128 * 2 + 128 * 64 * 128)
@@ -70,11 +73,58 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_threads() -> int:
+BOX_CPU_SHARE = 16  # host threads one GPU's job may keep busy on the GPU hosts
+
+
+def available_parallelism() -> tuple[int, dict]:
+    """Rust's std::thread::available_parallelism, the reference's default
+    thread count (mt_threads, ops.rs:62-73): the CPUs this process may run on
+    (its affinity mask), bounded by a cgroup v2 CPU quota when one is set."""
+    info = {"nproc": os.cpu_count() or 1}
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    info["affinity_cpus"] = n
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            q = max(1, -(-int(quota) // int(period)))
+            info["cgroup_quota_cpus"] = q
+            n = min(n, q)
+    except (OSError, ValueError):
+        pass
+    return n, info
+
+
+def cpu_threads() -> tuple[int, dict]:
+    """OURO_N_THREADS, else available_parallelism (ops.rs:62-73), at most the
+    GPU host's per-job CPU share (recorded when it applies)."""
+    n, info = available_parallelism()
     env = os.environ.get("OURO_N_THREADS")
     if env and env.isdigit() and int(env) > 0:
-        return int(env)
-    return min(os.cpu_count() or 1, 16)
+        info["source"] = "OURO_N_THREADS"
+        return int(env), info
+    info["source"] = "available_parallelism"
+    if n > BOX_CPU_SHARE:
+        info["capped_from"] = n
+        info["cap_reason"] = f"{BOX_CPU_SHARE} threads: the CPU share of one GPU's job on the GPU host"
+        n = BOX_CPU_SHARE
+    return n, info
+
+
+def cpu_median(fn, warmup: int = 3, min_runs: int = 10, budget_s: float = 4.0, max_runs: int = 200):
+    """Median wall time of fn() over >= min_runs runs after `warmup` untimed ones
+    (more runs while the budget lasts); returns (seconds, runs)."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
 
 
 def time_events(stream, fn, steps: int, warmup: int, min_warm_s: float = 0.15) -> float:
@@ -353,7 +403,21 @@ def bench_fwht(stream, steps, warmup):
              None, None, stream)
 
     ms_all = time_events(stream, whole, max(2, steps // 4), 2)
-    return ms, ms_all
+
+    # the fused epilogue: each rotated row (as bf16) quantised to int8 for the
+    # ternary product that follows (quantize_row_i8_s), with and without
+    # storing the bf16 rows
+    xq = DeviceBuffer((FW_BUFS, per), np.int8)
+    sc = DeviceBuffer((FW_BUFS, FW_ROWS), np.float32)
+
+    def fused(i, store):
+        b = i % FW_BUFS
+        call("ouro_fwht_rows", src.ptr + 2 * b * per, DT_BF16, dst.ptr + 2 * b * per if store else None, DT_BF16,
+             FW_ROWS, FW_N, FW_N, None, 0, xq.ptr + b * per, sc.ptr + 4 * b * FW_ROWS, stream)
+
+    ms_q = time_events(stream, lambda i: fused(i, False), max(steps, 2 * FW_BUFS), warmup)
+    ms_qs = time_events(stream, lambda i: fused(i, True), max(steps, 2 * FW_BUFS), warmup)
+    return ms, ms_all, ms_q, ms_qs
 
 
 def bench_prefill(stream, steps, warmup):
@@ -455,9 +519,35 @@ def bench_stack(stream, steps, warmup):
             p, d_ = run()
             pf.append(p)
             dec.append(d_)
-        return float(np.mean(pf)), float(np.mean(dec)), st.device_bytes, T, card, lens
+        check = stack_check(st, toks, cu, card.n_vocab, stream)
+        return float(np.mean(pf)), float(np.mean(dec)), st.device_bytes, T, card, lens, check
     finally:
         st.free()
+
+
+def stack_check(st, toks, cu, V, stream) -> dict:
+    """Untimed sanity check of the benchmark's own workload: one more prefill
+    and decode steps with the logits kept; every logit finite and every greedy
+    token the first index of its row's largest logit (finite_argmax,
+    infer/mod.rs:70-83)."""
+    from ouroboros_amd.device import DeviceBuffer, synchronize
+
+    N = len(cu) - 1
+    lg = DeviceBuffer((N * V,), np.float32)
+    a, b = DeviceBuffer((N,), np.int32), DeviceBuffer((N,), np.int32)
+    res = {"finite": True, "tokens_are_argmax": True}
+    st.prefill(toks, cu, a, lg, stream)
+    for step in range(3):
+        if step:
+            st.decode(b, a, lg, stream)  # the previous step's tokens in b
+        synchronize(stream)
+        logits, tok = lg.download().reshape(N, V), a.download()
+        res["finite"] &= bool(np.isfinite(logits).all())
+        res["tokens_are_argmax"] &= bool(np.array_equal(tok, logits.argmax(axis=1)))
+        a, b = b, a
+    if not (res["finite"] and res["tokens_are_argmax"]):
+        raise SystemExit(f"hybrid stack check failed: {res}")
+    return res
 
 
 COPY_BYTES = 512 << 20
@@ -478,10 +568,11 @@ def bench_copy(stream, steps):
     return time_events(stream, step, max(3, steps // 5), 2)
 
 
-def cpu_baseline(orc, budget_s: float = 12.0) -> dict:
+def cpu_baseline(orc) -> dict:
     """The reference's own CPU GEMV (matvec_tl1, SSE4.1 order, row-split
-    threads) on the same 6912x2560 shape in its PTQ1_0 format."""
-    nt = cpu_threads()
+    threads, ops.rs:294-321) on the same 6912x2560 shape in its PTQ1_0 form,
+    and the bitnet.cpp I2_S / I8_S oracle on the headline format itself."""
+    nt, info = cpu_threads()
     rng = np.random.default_rng(5)
     rb = GEMV_IN // 128 * 28
     payload = rng.integers(0, 256, GEMV_OUT * rb, dtype=np.uint8)
@@ -489,32 +580,27 @@ def cpu_baseline(orc, budget_s: float = 12.0) -> dict:
     d = rng.uniform(0.01, 0.1, g.shape[0]).astype(np.float16).view(np.uint16)
     g[:, 26], g[:, 27] = d & 0xFF, d >> 8
     x = rng.standard_normal(GEMV_IN).astype(np.float32)
-    orc.matvec_tl1(payload, GEMV_OUT, GEMV_IN, x, simd=1, nthreads=nt)  # warm
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < budget_s and n < 2000:
-        orc.matvec_tl1(payload, GEMV_OUT, GEMV_IN, x, simd=1, nthreads=nt)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
+    dt, n = cpu_median(lambda: orc.matvec_tl1(payload, GEMV_OUT, GEMV_IN, x, simd=1, nthreads=nt))
     tl1_bytes = payload.nbytes + GEMV_IN * 4 + GEMV_OUT * 4
-    # bitnet.cpp I2_S / I8_S oracle on the headline format, for reference (scalar C, same threads)
     i2s = orc.i2s_pack(rng.integers(-1, 2, size=(GEMV_OUT, GEMV_IN)).astype(np.int8), 1.0)
-    xq, ds = orc.act_quant_i8(x[None])
-    t1 = time.perf_counter()
-    m = 0
-    while time.perf_counter() - t1 < budget_s / 4 and m < 200:
-        orc.gemm_i2s(i2s, GEMV_OUT, GEMV_IN, xq, ds, nthreads=nt)
-        m += 1
-    dt_i2 = (time.perf_counter() - t1) / m
+
+    def i2s_call():
+        xq, s = orc.act_quant_i8(x[None])
+        orc.gemm_i2s(i2s, GEMV_OUT, GEMV_IN, xq, s, nthreads=nt)
+
+    dt_i2, m = cpu_median(i2s_call, min_runs=10, budget_s=2.0)
     return {
         "value": round(tl1_bytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": nt,
         "kind": "port",
-        "sample": (f"{n} calls of the oracle's matvec_tl1 (SSE4.1 order, {nt} row-split threads) on one "
-                   f"6912x2560 PTQ1_0 matrix ({tl1_bytes} B per call), {dt * 1e3:.2f} ms/call; the int8 x 2-bit "
-                   f"oracle (scalar C) ran {GEMV_BYTES / dt_i2 / 1e9:.3f} GB/s ({dt_i2 * 1e3:.2f} ms/call, {m} calls)"),
-        "cpu": _cpu_model(),
+        "sample": (f"median of {n} calls (after 3 warm-ups) of the oracle's matvec_tl1 (SSE4.1 lane order, {nt} "
+                   f"row-split threads) on one 6912x2560 PTQ1_0 matrix ({tl1_bytes} B per call): "
+                   f"{dt * 1e3:.3f} ms/call.  The bitnet.cpp I2_S/I8_S oracle (scalar C, quantisation included) on "
+                   f"the headline format: {GEMV_BYTES / dt_i2 / 1e9:.3f} GB/s ({dt_i2 * 1e3:.2f} ms/call, median of "
+                   f"{m})"),
+        "i2s_oracle_GBs": round(GEMV_BYTES / dt_i2 / 1e9, 3),
+        "cpu": _cpu_model(), "threads": info,
     }
 
 
@@ -528,8 +614,10 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def gdn_cpu_baseline(orc, budget_s: float = 6.0) -> dict:
-    nt = cpu_threads()
+def gdn_cpu_baseline(orc) -> dict:
+    """delta_head_dim (qwen35.rs:27-57) per (sequence, head), threaded over
+    the 32 x 32 heads, on the decode workload."""
+    nt, info = cpu_threads()
     rng = np.random.default_rng(3)
     B, Hk, Hv, d = GDN_B, GDN_HK, GDN_HV, GDN_D
     state = (0.02 * rng.standard_normal((B, Hv, d * d))).astype(np.float32)
@@ -538,14 +626,68 @@ def gdn_cpu_baseline(orc, budget_s: float = 6.0) -> dict:
     v = rng.standard_normal((B, Hv, d)).astype(np.float32)
     gate = -np.log1p(np.exp(rng.standard_normal((B, Hv)))).astype(np.float32)
     beta = (1 / (1 + np.exp(-rng.standard_normal((B, Hv))))).astype(np.float32)
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < budget_s and n < 500:
-        orc.gdn_decode(state, q, k, v, gate, beta, B, Hk, Hv, d, orc.L2NORM_QK | orc.SCALE_Q, 1e-6, nt)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
+    dt, n = cpu_median(lambda: orc.gdn_decode(state, q, k, v, gate, beta, B, Hk, Hv, d,
+                                              orc.L2NORM_QK | orc.SCALE_Q, 1e-6, nt), budget_s=3.0)
     return {"value": round(B / dt, 1), "unit": "tokens/s", "cores": nt, "kind": "port",
-            "sample": f"{n} decode steps of the oracle's delta_head_dim loop over 32x32 heads, {dt * 1e3:.2f} ms/step"}
+            "sample": f"median of {n} decode steps (after 3 warm-ups) of the oracle's delta_head_dim loop over "
+                      f"32x32 heads, {nt} threads: {dt * 1e3:.3f} ms/step",
+            "cpu": _cpu_model(), "threads": info}
+
+
+def fwht_cpu_baseline(orc) -> dict:
+    """rotate_fwd (hadamard.rs:41-53) on each of the 512 rows of 4096 (f32,
+    as the reference computes), rows over threads; GB/s counts the GPU row's
+    bf16 bytes."""
+    from ouroboros_amd import quant
+
+    nt, info = cpu_threads()
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((FW_ROWS, FW_N)).astype(np.float32)
+    x[rng.random(x.shape) < 0.01] *= 50.0
+    base = quant.bf16_bits_to_f32(quant.f32_to_bf16_bits(x))
+    work = base.copy()
+
+    def call():
+        work[:] = base
+        orc.rotate_rows(work, None, FW_N, nthreads=nt)
+
+    dt, n = cpu_median(call, budget_s=2.0)
+    return {"value": round(FW_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+            "sample": f"median of {n} calls (after 3 warm-ups) of the oracle's rotate_fwd over 512 rows of 4096 "
+                      f"(f32, {nt} threads over rows, the copy-in of the input included): {dt * 1e3:.3f} ms/call",
+            "cpu": _cpu_model(), "threads": info}
+
+
+def prefill_cpu_baseline(orc) -> dict:
+    """The reference's prefill: each of the 4 sequences token by token through
+    delta_head_dim (shell/src/bonsai.rs:48-52 driving qwen35.rs:27-57),
+    (sequence, head) pairs over threads, on the 4 x 4096-token workload."""
+    nt, info = cpu_threads()
+    rng = np.random.default_rng(11)
+    # a bounded sample: the first 512 tokens of each of the 4 sequences (the
+    # loop costs the same per token at any length, and the 128 (sequence,
+    # head) pairs keep every thread busy)
+    L = PF_CPU_LEN
+    T, Hk, Hv, d = PF_SEQ * L, GDN_HK, GDN_HV, GDN_D
+    q = rng.standard_normal((T, Hk, d)).astype(np.float32)
+    k = rng.standard_normal((T, Hk, d)).astype(np.float32)
+    v = rng.standard_normal((T, Hv, d)).astype(np.float32)
+    gate = -np.log1p(np.exp(rng.standard_normal((T, Hv)))).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((T, Hv))))).astype(np.float32)
+    state0 = (0.02 * rng.standard_normal((PF_SEQ, Hv, d * d))).astype(np.float32)
+    cu = np.arange(PF_SEQ + 1, dtype=np.int32) * L
+    st = state0.copy()
+
+    def call():
+        st[:] = state0
+        orc.gdn_prefill_varlen(st, q, k, v, gate, beta, cu, Hk, Hv, d, orc.L2NORM_QK | orc.SCALE_Q, 1e-6, nt)
+
+    dt, n = cpu_median(call, budget_s=0.0)
+    return {"value": round(T / dt, 1), "unit": "tokens/s", "cores": nt, "kind": "port",
+            "sample": f"median of {n} runs (after 3 warm-ups) of the oracle's token-loop prefill of 4 x {L} tokens "
+                      f"(the first {L} of each 4096-token sequence; f32, {nt} threads over the 128 (sequence, head) "
+                      f"pairs): {dt * 1e3:.1f} ms/run",
+            "cpu": _cpu_model(), "threads": info}
 
 
 def load_traffic() -> dict:
@@ -704,7 +846,7 @@ def main() -> int:
             "vendor_int8_gemm_8bit_weights_us": round(vendor * 1e3, 2) if vendor else None,
         }
     if "fwht" in res:
-        ms, ms_all = res["fwht"]
+        ms, ms_all, ms_q, ms_qs = res["fwht"]
         gbs = FW_BYTES / (ms * 1e-3) / 1e9
         gbs_all = FW_BYTES * FW_BUFS / (ms_all * 1e-3) / 1e9
         sec["fwht"] = {
@@ -714,6 +856,15 @@ def main() -> int:
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "fwht_row_kernel", FW_ROWS * 256)},
             "streaming_16384_rows_GBs": round(gbs_all, 1),
             "bytes_per_call": FW_BYTES,
+            "fused_int8_epilogue": {
+                "config": "the same rotation with each bf16 row quantised to int8 (quantize_row_i8_s) in the "
+                          "kernel's epilogue; bf16 rows not stored / stored",
+                "bytes_per_call": FW_Q_BYTES, "ms_per_call": round(ms_q, 4),
+                "GBs": round(FW_Q_BYTES / (ms_q * 1e-3) / 1e9, 1),
+                "frac": round(FW_Q_BYTES / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "with_bf16_store_bytes": FW_Q_BYTES + FW_BYTES // 2, "with_bf16_store_ms": round(ms_qs, 4),
+                "with_bf16_store_GBs": round((FW_Q_BYTES + FW_BYTES // 2) / (ms_qs * 1e-3) / 1e9, 1),
+            },
         }
     if "copy" in res:
         ms = res["copy"]
@@ -735,7 +886,7 @@ def main() -> int:
             "frac_of_min_roofline": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
         }
     if "stack" in res:
-        pf_ms, dec_ms, dev_bytes, T, card, lens = res["stack"]
+        pf_ms, dec_ms, dev_bytes, T, card, lens, check = res["stack"]
         alg = stack_algorithmic(card, lens)
         step_ms = dec_ms / ST_STEPS
         dec_gbs = alg["decode_step_bytes"] / (step_ms * 1e-3) / 1e9
@@ -754,13 +905,18 @@ def main() -> int:
                                 "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
             "prefill_ternary_TOPs": round(pf_tops, 1),
             "algorithmic": alg, "device_bytes": int(dev_bytes),
+            "output_check": check,
         }
     if orc is not None:
-        log("CPU baseline")
+        log("CPU baselines")
         if "gemv" in res:
             out["cpu_baseline"] = cpu_baseline(orc)
         if "gdn" in res:
             sec.setdefault("gdn_decode", {})["cpu_baseline"] = gdn_cpu_baseline(orc)
+        if "fwht" in res:
+            sec.setdefault("fwht", {})["cpu_baseline"] = fwht_cpu_baseline(orc)
+        if "prefill" in res:
+            sec.setdefault("gdn_prefill", {})["cpu_baseline"] = prefill_cpu_baseline(orc)
     out["secondary"] = sec
     print(json.dumps(out), flush=True)
     return 0

@@ -299,7 +299,9 @@ int ouro_rotate_inv(float *x, const float *signs, size_t n, size_t block,
 
 /* delta_head_dim (qwen35.rs:27-57) for one head, in place on the device:
  * decay = exp(gate); sk = decay * S^T k; dv = beta (v - sk);
- * S = decay S + k dv^T; out = S^T q.  sdim == 128; q is pre-scaled. */
+ * S = decay S + k dv^T; out = S^T q.  Like the reference's runtime-dim
+ * variant any sdim works, here 1..256 (128 runs the tuned decode kernel);
+ * q is pre-scaled. */
 int ouro_delta_head_dim(float *state, size_t sdim, const float *q,
                         const float *k, const float *v, float gate,
                         float beta, float *out, void *stream);
@@ -311,7 +313,9 @@ int ouro_delta_head_dim(float *state, size_t sdim, const float *q,
  *   gate   : [B][Hv] f32 log-decay (decay = exp(gate)); beta: [B][Hv] f32
  *   state  : [B][Hv][d][d] f32, element (i,j) of a head at i + j*d; updated
  *   out    : [B][Hv][d] f32
- * d == 128, Hv % Hk == 0.  eps is the l2_norm epsilon (outside the sqrt). */
+ * d in 1..256 (d == 128, the qwen35 family's d_state, runs the tuned
+ * kernel; OURO_GDN_SCALE_Q scales q by 1/sqrt(d)), Hv % Hk == 0.  eps is the
+ * l2_norm epsilon (outside the sqrt). */
 int ouro_gdn_decode(float *state, const void *q, const void *k, int qk_dtype,
                     const void *v, int v_dtype, const float *gate,
                     const float *beta, float *out, size_t B, size_t Hk,

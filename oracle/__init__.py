@@ -102,6 +102,7 @@ def lib() -> C.CDLL:
             "orc_gdn_layer_decode": (None, [vp] * 11 + [sz, sz, sz, sz, u32, f32, i32]),
             "orc_finite_argmax": (sz, [vp, sz]),
             "orc_gdn_prefill_tokens": (None, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
+            "orc_gdn_prefill_varlen": (None, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, u32, f32, i32]),
             "orc_mt_threads": (i32, []),
         }
         for name, (res, args) in sig.items():
@@ -402,6 +403,18 @@ def gdn_prefill_tokens(state, q, k, v, gate, beta, T, Hk, Hv, d, flags, eps, nth
     q, k, v, gate, beta = _f32(q), _f32(k), _f32(v), _f32(gate), _f32(beta)
     out = np.empty((T, Hv, d), np.float32)
     lib().orc_gdn_prefill_tokens(_p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(out), T, Hk,
+                                 Hv, d, flags, eps, nthreads)
+    return out
+
+
+def gdn_prefill_varlen(state, q, k, v, gate, beta, cu_seqlens, Hk, Hv, d, flags, eps, nthreads=0):
+    """Token-loop prefill of N packed sequences (state [N][Hv][d*d], updated in place)."""
+    assert state.dtype == np.float32 and state.flags.c_contiguous
+    q, k, v, gate, beta = _f32(q), _f32(k), _f32(v), _f32(gate), _f32(beta)
+    cu = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+    T, N = int(cu[-1]), len(cu) - 1
+    out = np.empty((T, Hv, d), np.float32)
+    lib().orc_gdn_prefill_varlen(_p(state), _p(q), _p(k), _p(v), _p(gate), _p(beta), _p(out), _p(cu), N, Hk,
                                  Hv, d, flags, eps, nthreads)
     return out
 

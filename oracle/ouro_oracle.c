@@ -1049,6 +1049,39 @@ void orc_gdn_prefill_tokens(float *state, const float *q, const float *k,
     orc_parallel_for(Hv, nthreads, gdn_prefill_range, &c);
 }
 
+struct gdn_varlen_ctx {
+    struct gdn_ctx base;
+    const int32_t *cu;
+};
+
+static void gdn_varlen_range(void *p, size_t lo, size_t hi)
+{
+    struct gdn_varlen_ctx *c = (struct gdn_varlen_ctx *)p;
+    const size_t d = c->base.d, Hv = c->base.Hv, Hk = c->base.Hk;
+    for (size_t sh = lo; sh < hi; ++sh) {
+        const size_t s = sh / Hv, h = sh % Hv;
+        const size_t kh = gdn_khead(h, Hk, Hv, c->base.flags);
+        for (size_t t = (size_t)c->cu[s]; t < (size_t)c->cu[s + 1]; ++t) {
+            const size_t th = t * Hv + h;
+            gdn_one_head(c->base.state + sh * d * d, c->base.q + (t * Hk + kh) * d,
+                         c->base.k + (t * Hk + kh) * d, c->base.v + th * d, c->base.gate[th],
+                         c->base.beta[th], c->base.out + th * d, d, c->base.flags, c->base.eps);
+        }
+    }
+}
+
+void orc_gdn_prefill_varlen(float *state, const float *q, const float *k,
+                            const float *v, const float *gate,
+                            const float *beta, float *out,
+                            const int32_t *cu_seqlens, size_t N, size_t Hk,
+                            size_t Hv, size_t d, unsigned flags, float eps,
+                            int nthreads)
+{ /* the reference prefill (shell/src/bonsai.rs:48-52): each sequence token by
+     token through the recurrence, (sequence, v-head) pairs over threads */
+    struct gdn_varlen_ctx c = {{state, q, k, v, gate, beta, out, 1, Hk, Hv, d, 0, flags, eps}, cu_seqlens};
+    orc_parallel_for(N * Hv, nthreads, gdn_varlen_range, &c);
+}
+
 /* ---- run_delta's layer block (qwen35.rs:1066-1140) ---------------------- */
 
 struct layer_ctx {

@@ -227,6 +227,14 @@ void orc_gdn_prefill_tokens(float *state, const float *q, const float *k,
                             const float *beta, float *out, size_t T,
                             size_t Hk, size_t Hv, size_t d, unsigned flags,
                             float eps, int nthreads);
+/* N sequences packed varlen (cu_seqlens[0..N], state [N][Hv][d*d]), each
+ * token by token as orc_gdn_prefill_tokens, threads over (sequence, head). */
+void orc_gdn_prefill_varlen(float *state, const float *q, const float *k,
+                            const float *v, const float *gate,
+                            const float *beta, float *out,
+                            const int32_t *cu_seqlens, size_t N, size_t Hk,
+                            size_t Hv, size_t d, unsigned flags, float eps,
+                            int nthreads);
 
 #define ORC_GDN_V_GROUPED   8u  /* gated output in V-grouped order (qwen35.rs:1122-1138) */
 

@@ -68,14 +68,15 @@ class Lin:
         self.scale = np.float32(1.0 / np.sqrt(inp * 2.0 / 3.0))
 
     def __call__(self, xq, ds):
-        return orc.gemm_i2(self.canon, self.out, self.inp, xq, ds, self.scale)[1]
+        # small products run on the calling thread (thread start-up would dominate)
+        nt = 1 if self.out * self.inp < (1 << 22) else 0
+        return orc.gemm_i2(self.canon, self.out, self.inp, xq, ds, self.scale, nthreads=nt)[1]
 
 
 def rmsnorm(x, w, eps):
     x = np.asarray(x, np.float32)
-    ms = np.float32(0.0)
-    for v in x:  # sequential f32 sum, as ops.rs:14
-        ms = np.float32(ms + v * v)
+    # sequential f32 sum, as ops.rs:14 (np.add.accumulate adds in order, in float32)
+    ms = np.add.accumulate((x * x).astype(np.float32), dtype=np.float32)[-1]
     ms = np.float32(ms / np.float32(x.size))
     inv = np.float32(1.0) / np.float32(np.sqrt(np.float32(ms + np.float32(eps))))
     return (x * inv * w).astype(np.float32)
@@ -87,15 +88,15 @@ def silu(x):
 
 
 def rope_partial_neox(v, t, rot, base):
-    v = v.copy()
+    v = np.array(v, np.float32, copy=True)
     half = rot // 2
-    for i in range(half):
-        theta = np.float32(1.0) / np.float32(np.power(np.float32(base), np.float32(2 * i) / np.float32(rot)))
-        ang = np.float32(np.float32(t) * theta)
-        c, s = np.float32(np.cos(ang)), np.float32(np.sin(ang))
-        a, b = v[i], v[i + half]
-        v[i] = a * c - b * s
-        v[i + half] = b * c + a * s
+    i = np.arange(half, dtype=np.float32)
+    theta = (np.float32(1.0) / np.power(np.float32(base), (np.float32(2) * i) / np.float32(rot))).astype(np.float32)
+    ang = (np.float32(t) * theta).astype(np.float32)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    a, b = v[:half].copy(), v[half:rot].copy()
+    v[:half] = a * c - b * s
+    v[half:rot] = b * c + a * s
     return v
 
 

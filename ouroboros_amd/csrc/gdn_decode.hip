@@ -158,13 +158,96 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     if ((lane & (kSpan - 1)) == 0) a.out[static_cast<long long>(bh) * kD + myj] = oj;
 }
 
+// Any other head dimension d <= 256 (delta_head_dim is the runtime-dim
+// variant, qwen35.rs:26-27): one 256-thread workgroup per (sequence, head),
+// each wavefront walking columns w, w + 4, ..; lane l holds rows
+// i = l + 64m (m < M = ceil(d / 64)) of a column, so every column access is
+// coalesced, and S^T k and S'^T q are wavefront reductions.
+constexpr int kAnyWaves = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
+    return v;
+}
+
+template <typename TQK, typename TV, int M>
+__global__ __launch_bounds__(64 * kAnyWaves) void gdn_decode_any_kernel(DecodeArgs a, int d) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int bh = blockIdx.x;
+    const int b = bh / a.Hv, h = bh % a.Hv;
+    const int kh = (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
+    const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * d;
+    float k[M], q[M];
+    float kk = 0.f, qq = 0.f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int i = lane + 64 * m;
+        k[m] = i < d ? ld1(static_cast<const TQK *>(a.k) + qk_off + i) : 0.f;
+        q[m] = i < d ? ld1(static_cast<const TQK *>(a.q) + qk_off + i) : 0.f;
+        kk += k[m] * k[m];
+        qq += q[m] * q[m];
+    }
+    if (a.flags & OURO_GDN_L2NORM_QK) {  // l2_norm: 1 / (sqrt(sum) + eps)
+        const float ik = 1.0f / (sqrtf(wave_sum(kk)) + a.eps);
+        const float iq = 1.0f / (sqrtf(wave_sum(qq)) + a.eps);
+#pragma unroll
+        for (int m = 0; m < M; ++m) k[m] = k[m] * ik, q[m] = q[m] * iq;
+    }
+    if (a.flags & OURO_GDN_SCALE_Q) {
+        const float sc = 1.0f / sqrtf(static_cast<float>(d));
+#pragma unroll
+        for (int m = 0; m < M; ++m) q[m] = q[m] * sc;
+    }
+    const float gate = a.gate ? a.gate[bh] : a.gate_s;
+    const float beta = a.beta ? a.beta[bh] : a.beta_s;
+    const float decay = expf(gate);
+    float *S = a.state + static_cast<long long>(bh) * d * d;
+    const TV *v = static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * d;
+    for (int j = wave; j < d; j += kAnyWaves) {
+        float s[M];
+        float part = 0.f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int i = lane + 64 * m;
+            s[m] = i < d ? S[static_cast<long long>(j) * d + i] : 0.f;
+            part += s[m] * k[m];
+        }
+        const float sk = wave_sum(part) * decay;
+        const float dv = beta * (ld1(v + j) - sk);
+        float o = 0.f;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int i = lane + 64 * m;
+            const float t = s[m] * decay + k[m] * dv;
+            if (i < d) S[static_cast<long long>(j) * d + i] = t;
+            o += t * q[m];
+        }
+        o = wave_sum(o);
+        if (lane == 0) a.out[static_cast<long long>(bh) * d + j] = o;
+    }
+}
+
+template <typename TQK, typename TV>
+int launch_any(const DecodeArgs &a, int d, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(a.B * a.Hv)), block(64 * kAnyWaves);
+    switch ((d + 63) / 64) {
+    case 1: hipLaunchKernelGGL((gdn_decode_any_kernel<TQK, TV, 1>), grid, block, 0, s, a, d); break;
+    case 2: hipLaunchKernelGGL((gdn_decode_any_kernel<TQK, TV, 2>), grid, block, 0, s, a, d); break;
+    case 3: hipLaunchKernelGGL((gdn_decode_any_kernel<TQK, TV, 3>), grid, block, 0, s, a, d); break;
+    default: hipLaunchKernelGGL((gdn_decode_any_kernel<TQK, TV, 4>), grid, block, 0, s, a, d); break;
+    }
+    return check_launch("gdn_decode_any_kernel");
+}
+
 // Measured on B=32, Hv=32 with 8 rotating 64 MiB state sets: 4 columns per
 // wavefront in 8-wavefront blocks streams the state at ~91% of the in-place
 // read-modify-write rate of a plain copy-style kernel on the same bytes.
 constexpr int kCPW = 4, kWPB = 8;
 
 template <typename TQK, typename TV>
-int launch(const DecodeArgs &a, hipStream_t s) {
+int launch(const DecodeArgs &a, int d, hipStream_t s) {
+    if (d != kD) return launch_any<TQK, TV>(a, d, s);
     dim3 grid(static_cast<unsigned>(a.B * a.Hv), kD / (kCPW * kWPB));
     hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV, kCPW, kWPB>), grid, dim3(64 * kWPB), 0, s, a);
     return check_launch("gdn_decode_kernel");
@@ -177,13 +260,16 @@ int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const v
                size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream,
                size_t qk_bs, size_t v_bs) {
     if (!state || !q || !k || !v || !out) return fail(OURO_ERR_INVALID_ARG, "gdn decode: NULL argument");
-    if (d != static_cast<size_t>(kD)) return fail(OURO_ERR_SHAPE, "gdn decode: d = %zu, only 128 is supported", d);
+    if (!d || d > 256) return fail(OURO_ERR_SHAPE, "gdn decode: d = %zu, supported 1..256", d);
     if (!B || !Hk || !Hv || Hv % Hk) return fail(OURO_ERR_SHAPE, "gdn decode: bad heads B=%zu Hk=%zu Hv=%zu", B, Hk, Hv);
     if (B * Hv > 0x7fffffffULL) return fail(OURO_ERR_SHAPE, "gdn decode: too many heads");
     if (flags & ~(OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | OURO_GDN_KHEAD_DIV))
         return fail(OURO_ERR_INVALID_ARG, "gdn decode: bad flags 0x%x", flags);
-    if (reinterpret_cast<uintptr_t>(state) % 16) return fail(OURO_ERR_ALIGN, "gdn decode: state needs 16-byte alignment");
-    const size_t qa = qk_dtype == OURO_DT_F32 ? 16 : 8;
+    // d = 128 reads q, k and the state in 16-byte pieces; other d element-wise
+    const bool wide = d == static_cast<size_t>(kD);
+    if (reinterpret_cast<uintptr_t>(state) % (wide ? 16 : 4))
+        return fail(OURO_ERR_ALIGN, "gdn decode: state needs %d-byte alignment", wide ? 16 : 4);
+    const size_t qa = wide ? (qk_dtype == OURO_DT_F32 ? 16 : 8) : (qk_dtype == OURO_DT_F32 ? 4 : 2);
     if (reinterpret_cast<uintptr_t>(q) % qa || reinterpret_cast<uintptr_t>(k) % qa)
         return fail(OURO_ERR_ALIGN, "gdn decode: q/k need %zu-byte alignment", qa);
     if ((qk_bs * (qk_dtype == OURO_DT_F32 ? 4 : 2)) % qa)
@@ -209,10 +295,11 @@ int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const v
     const bool qf = qk_dtype == OURO_DT_F32, vf = v_dtype == OURO_DT_F32;
     if ((qk_dtype != OURO_DT_F32 && qk_dtype != OURO_DT_BF16) || (v_dtype != OURO_DT_F32 && v_dtype != OURO_DT_BF16))
         return fail(OURO_ERR_INVALID_ARG, "gdn decode: bad dtype");
-    if (qf && vf) return launch<float, float>(a, s);
-    if (qf) return launch<float, uint16_t>(a, s);
-    if (vf) return launch<uint16_t, float>(a, s);
-    return launch<uint16_t, uint16_t>(a, s);
+    const int dd = static_cast<int>(d);
+    if (qf && vf) return launch<float, float>(a, dd, s);
+    if (qf) return launch<float, uint16_t>(a, dd, s);
+    if (vf) return launch<uint16_t, float>(a, dd, s);
+    return launch<uint16_t, uint16_t>(a, dd, s);
 }
 
 }  // namespace ouro

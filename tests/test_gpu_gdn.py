@@ -93,11 +93,42 @@ def test_delta_head_dim_kats_on_gpu(gpu):
     assert np.abs(out - np.float32(0.1 * S) * expect).max() < 1e-4
 
 
+@pytest.mark.parametrize("sdim", [1, 16, 64, 100, 192, 256])
+def test_delta_head_dim_runtime_sdim(gpu, orc, sdim):
+    # delta_head_dim is the reference's runtime-dim variant (qwen35.rs:26-27)
+    rng = np.random.default_rng(sdim)
+    state = (0.1 * rng.standard_normal(sdim * sdim)).astype(np.float32)
+    q, k, v = (rng.standard_normal(sdim).astype(np.float32) for _ in range(3))
+    step = qwen35.DeltaStep(gate=-0.3, beta=0.7)
+    ref, want = state.copy(), np.zeros(sdim, np.float32)
+    orc.delta_head_dim(ref, sdim, q, k, v, step.gate, step.beta, want)
+    got = np.zeros(sdim, np.float32)
+    qwen35.delta_head_dim(state, sdim, q, k, v, step, got)
+    assert rel_err(got, want)[0] < TOL and rel_err(state, ref)[0] < TOL
+
+
+@pytest.mark.parametrize("d,dt", [(64, "bf16"), (96, "f32"), (256, "bf16")])
+def test_decode_other_head_dims(gpu, orc, d, dt):
+    rng = np.random.default_rng(d)
+    B, Hk, Hv, flags = 3, 2, 4, GDN_L2NORM_QK | GDN_SCALE_Q
+    state, q, k, v, gate, beta = config3_inputs(rng, B, Hk, Hv, d)
+    if dt == "f32":
+        q, k, v = (quant.bf16_bits_to_f32(a) for a in (q, k, v))
+    ref = state.copy()
+    f32 = lambda a: quant.bf16_bits_to_f32(a) if a.dtype == np.uint16 else a  # noqa: E731
+    want = orc.gdn_decode(ref, f32(q), f32(k), f32(v), gate, beta, B, Hk, Hv, d, flags, 1e-6)
+    sd = DeviceBuffer.from_host(state)
+    out = DeviceBuffer((B, Hv, d), np.float32)
+    qwen35.gdn_decode(sd, *(DeviceBuffer.from_host(a) for a in (q, k, v, gate, beta)), out, B, Hk, Hv, d,
+                      flags=flags, eps=1e-6)
+    assert rel_err(out.download(), want)[0] < TOL and rel_err(sd.download(), ref)[0] < TOL
+
+
 def test_bad_shapes_rejected(gpu):
     from ouroboros_amd._lib import OuroError
 
-    st = DeviceBuffer((64 * 64,), np.float32)
-    v = DeviceBuffer((64,), np.float32)
+    st = DeviceBuffer((257 * 257,), np.float32)
+    v = DeviceBuffer((257,), np.float32)
     with pytest.raises(OuroError) as e:
-        qwen35.delta_head_dim(st, 64, v, v, v, qwen35.DeltaStep(0.0, 1.0), v)
+        qwen35.delta_head_dim(st, 257, v, v, v, qwen35.DeltaStep(0.0, 1.0), v)
     assert e.value.code == 2

@@ -152,6 +152,33 @@ def test_stack_many_sequences(gpu, card, nseq):
     check(card, prompts, 2, max_seqs=64, max_tokens=256, max_ctx=16)
 
 
+# two layers (one delta-net, one attention) keep the oracle quick for many sequences
+MANY = Card(n_layer=2, n_embd=256, n_ff=512, n_vocab=512, full_attention_interval=2, n_head=2, n_head_kv=1,
+            n_rot=64, ssm_n_k_heads=1, ssm_n_v_heads=2, eps=1e-6, rope_base=1e7)
+
+
+def test_stack_more_than_64_sequences(gpu):
+    # 72 sequences: decode steps take the path for more than 64 sequences
+    # (conv and gates in their own kernel, one launch per product, row-major
+    # activations), and the 66 prompts of exactly 64 tokens all enter a new
+    # KV page on the first decode step, more assignments than one batch (64)
+    from oracle.stack_oracle import StackOracle
+
+    rng = np.random.default_rng(12)
+    lens = [64] * 66 + [1, 2, 3, 5, 9, 17]
+    prompts = [list(rng.integers(0, MANY.n_vocab, n)) for n in lens]
+    steps = 2
+    l16, t16 = StackOracle(MANY, seed=7, bf16_prefill=True).run(prompts, steps)
+    got, gtok = gpu_run(MANY, prompts, t16[:-1], max_seqs=72, max_tokens=sum(lens), max_ctx=64 + steps + 1)
+    e16 = [rel(g, w) for g, w in zip(got, l16)]
+    print("72 sequences vs bf16-prefill oracle", e16)
+    assert max(e16) < TOL_BF16, e16
+    for g, w, lg in zip(gtok, t16, l16):
+        top2 = np.sort(lg, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2 * TOL_BF16 * np.abs(lg).max(axis=1)
+        assert np.array_equal(np.asarray(g)[clear], np.asarray(w)[clear])
+
+
 def test_stack_rejects_bad_calls(gpu):
     st = Stack(SMALL, 7, max_seqs=2, max_tokens=10, max_ctx=8)
     try:

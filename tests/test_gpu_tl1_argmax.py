@@ -96,3 +96,30 @@ def test_matvec_argmax_tl1_handle(gpu, orc):
         assert idx == best or abs(float(want[idx]) - float(want[best])) <= 1e-5 * abs(float(want[best])), call
         assert h.matvec_argmax(x) == idx  # without a caller y
     h.free()
+
+
+def test_lm_head_full_size(gpu, orc):
+    # The reference's lm_head shape, 248320 x 5120 TL1 (docs/BONSAI_PTQ1.md:30;
+    # the head of Qwen35Stage::sample, qwen35.rs:746-757): the resident
+    # table-lookup GEMV with the fused finite_argmax, and the raw-payload
+    # matvec_q, against the oracle's matvec_tl1 and finite_argmax.
+    rng = np.random.default_rng(248320)
+    out_len, in_len = 248320, 5120
+    p = tl1_payload(rng, out_len, in_len)
+    h = ops.Weight(QuantKind.TL1, p, out_len, in_len)
+    try:
+        for call in range(2):
+            x = rng.standard_normal(in_len).astype(np.float32)
+            want = orc.matvec_tl1(p, out_len, in_len, x)
+            y = DeviceBuffer((out_len,), np.float32)
+            idx = h.matvec_argmax(x, y)
+            yv = y.download()
+            ok = close(yv, want, 1e-5)
+            assert ok.all(), (call, int((~ok).sum()))
+            assert idx == orc.finite_argmax(yv)
+            best = orc.finite_argmax(want)
+            assert idx == best or abs(float(want[idx]) - float(want[best])) <= 1e-5 * abs(float(want[best])), call
+        raw = ops.matvec_q(p, QuantKind.TL1, out_len, in_len, x)
+        assert close(raw, want, 1e-5).all()
+    finally:
+        h.free()
