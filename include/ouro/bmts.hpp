@@ -107,7 +107,10 @@ private:
                 case 'f': c = '\f'; break;
                 case 'u': {
                     if (i_ + 4 > s_.size()) bail("BMTS tensor table: bad \\u escape");
-                    const unsigned v = static_cast<unsigned>(std::stoul(s_.substr(i_, 4), nullptr, 16));
+                    const std::string hex = s_.substr(i_, 4);
+                    if (hex.find_first_not_of("0123456789abcdefABCDEF") != std::string::npos)
+                        bail("BMTS tensor table: bad \\u escape");
+                    const unsigned v = static_cast<unsigned>(std::stoul(hex, nullptr, 16));
                     i_ += 4;
                     if (v > 0x7f) bail("BMTS tensor table: non-ASCII \\u escape");
                     c = static_cast<char>(v);
@@ -129,7 +132,11 @@ private:
         if (b == i_) bail("BMTS tensor table: expected a number");
         const std::string t = s_.substr(b, i_ - b);
         if (t.find_first_of("-.eE") != std::string::npos) bail("BMTS tensor table: '" + t + "' is not a u64");
-        return std::stoull(t);
+        try {
+            return std::stoull(t);
+        } catch (const std::exception &) {  // out of range, or a lone sign
+            bail("BMTS tensor table: '" + t + "' is not a u64");
+        }
     }
     Tensor object() {
         Tensor t;
@@ -247,8 +254,10 @@ public:
     // A span of a tensor, refused past the declared length (bmts.rs:286-308).
     std::pair<const uint8_t *, size_t> read_span(const std::string &name, uint64_t offset, uint64_t length) const {
         const Tensor &t = tensor(name);
-        if (offset + length > t.length || offset + length < offset)
+        if (offset > t.length || length > t.length - offset)
             bail("span exceeds tensor " + name + " of " + std::to_string(t.length) + " bytes");
+        if (t.offset > UINT64_MAX - offset)
+            bail("tensor " + name + " range exceeds file of " + std::to_string(size_) + " bytes");
         return range(name, t.offset + offset, length);
     }
 
@@ -295,10 +304,12 @@ private:
         data_start_ = kHeaderLen + meta_len;
     }
     std::pair<const uint8_t *, size_t> range(const std::string &name, uint64_t offset, uint64_t length) const {
-        const uint64_t start = data_start_ + offset;
-        if (start + length > size_ || start + length < start)
+        // offset and length are checked against the data region before any
+        // addition, so a table entry near 2^64 cannot wrap into the header
+        const uint64_t data_len = size_ - data_start_;
+        if (offset > data_len || length > data_len - offset)
             bail("tensor " + name + " range exceeds file of " + std::to_string(size_) + " bytes");
-        return {map_ + start, static_cast<size_t>(length)};
+        return {map_ + data_start_ + offset, static_cast<size_t>(length)};
     }
 
     std::string path_;

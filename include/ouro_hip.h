@@ -12,6 +12,14 @@
  * ouro_shutdown().
  *
  * Conventions
+ *  - Library scratch is per device, not per stream: ouro_finite_argmax, the
+ *    library workspace (ouro_matvec_q / ouro_matmul_q on the 2-bit kinds,
+ *    ouro_gdn_chunk_prefill and ouro_gdn_layer_decode with a NULL
+ *    workspace), the static scratch of ouro_matvec_q_noalloc and each
+ *    weight handle's own scratch are each shared by every call that uses
+ *    them on that device.  Such calls must be ordered: issue them on one
+ *    stream (or synchronise between streams); overlapping calls race.
+ *    Entry points given caller buffers share nothing.
  *  - Return value: OURO_OK (0) or an ouro_status code.  The failing call's
  *    message is kept in a thread-local buffer, read with ouro_last_error().
  *    No entry point aborts the process (the reference's assert!/bail! paths,
@@ -414,8 +422,8 @@ int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y,
                               int32_t *idx, void *stream);
 /* finite_argmax (infer/mod.rs:70-83) of n device floats: the first index of
  * the largest non-NaN value (-0 and +0 compare equal), 0 if every value is
- * NaN; *idx is a device int32.  Uses 8 KiB of per-device scratch allocated
- * on the first call. */
+ * NaN; *idx is a device int32.  Uses 8 KiB of per-device scratch that
+ * ouro_init allocates; the call allocates nothing. */
 int ouro_finite_argmax(const float *y, size_t n, int32_t *idx, void *stream);
 
 #ifdef __cplusplus

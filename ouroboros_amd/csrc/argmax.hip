@@ -34,9 +34,6 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const unsigned long 
     if (threadIdx.x == 0) *idx = argmax_index(k);
 }
 
-namespace {
-}  // namespace
-
 // scratch: kArgmaxBlocks 64-bit keys of device memory (no initial value).
 int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream) {
     if (!y || !scratch || !idx) return fail(OURO_ERR_INVALID_ARG, "argmax: NULL argument");
@@ -56,32 +53,40 @@ int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *str
     return check_launch("argmax_final_kernel");
 }
 
-}  // namespace ouro
-
-using namespace ouro;
-
 namespace {
 std::mutex g_am_mu;
 void *g_am_scratch[64] = {};  // per device ordinal: kArgmaxBlocks keys
 }  // namespace
 
+// Called by ouro_init with the device current: the argmax scratch is
+// allocated there, once per device, so ouro_finite_argmax allocates nothing.
+int argmax_scratch_init(int dev) {
+    if (dev < 0 || dev >= 64) return fail(OURO_ERR_NO_DEVICE, "argmax: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_am_mu);
+    if (!g_am_scratch[dev]) {
+        void *p = nullptr;
+        if (hipMalloc(&p, kArgmaxBlocks * 8) != hipSuccess)
+            return fail(OURO_ERR_HIP, "argmax: scratch allocation failed");
+        g_am_scratch[dev] = p;
+    }
+    return OURO_OK;
+}
+
+}  // namespace ouro
+
+using namespace ouro;
+
 extern "C" {
 
 int ouro_finite_argmax(const float *y, size_t n, int32_t *idx, void *stream) {
     OURO_REQUIRE_INIT();
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(OURO_ERR_HIP, "argmax: no device");
-    void *scratch;
+    const int dev = current_device();
+    void *scratch = nullptr;
     {
         std::lock_guard<std::mutex> lock(g_am_mu);
-        if (!g_am_scratch[dev]) {
-            void *p = nullptr;
-            if (hipMalloc(&p, kArgmaxBlocks * 8) != hipSuccess)
-                return fail(OURO_ERR_HIP, "argmax: scratch allocation failed");
-            g_am_scratch[dev] = p;
-        }
-        scratch = g_am_scratch[dev];
+        if (dev >= 0 && dev < 64) scratch = g_am_scratch[dev];
     }
+    if (!scratch) return fail(OURO_ERR_NOT_INIT, "ouro_finite_argmax: ouro_init() did not set up device %d", dev);
     return argmax_f32(y, n, scratch, idx, stream);
 }
 

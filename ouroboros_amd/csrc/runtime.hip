@@ -9,6 +9,8 @@
 
 namespace ouro {
 
+int argmax_scratch_init(int dev);
+
 namespace {
 thread_local char g_err[512] = "";
 int g_device = -1;
@@ -115,6 +117,8 @@ int ouro_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(OURO_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
+    const int st = argmax_scratch_init(device);
+    if (st) return st;
     g_device = device;
     return OURO_OK;
 }

@@ -112,6 +112,33 @@ static void test_bmts_malformed() {
     write_raw(path, header(1, 1, static_cast<uint32_t>(meta.size())) + meta + std::string(8, '\0'));
     bmts::Shard s(path);
     EXPECT(throws([&] { s.tensor_bytes("a"); }));
+    // an offset near 2^64 must not wrap back into the header or the table
+    const std::string wrap =
+        "[{\"name\":\"w\",\"shape\":[4],\"dtype\":0,\"offset\":18446744073709551595,\"length\":16}]";
+    const std::string wpath = g_dir + "/wrapped.bmts";
+    write_raw(wpath, header(1, 1, static_cast<uint32_t>(wrap.size())) + wrap + std::string(16, '\0'));
+    bmts::Shard sw(wpath);
+    EXPECT(throws([&] { sw.tensor_bytes("w"); }));
+    EXPECT(throws([&] { sw.read_span("w", 0, 16); }));
+    // spans near 2^64 inside a valid tensor are refused too
+    const std::string okp = g_dir + "/ok.bmts";
+    write_raw(okp, header(1, 1, static_cast<uint32_t>(meta.size())) + meta + std::string(16, '\0'));
+    bmts::Shard so(okp);
+    EXPECT(throws([&] { so.read_span("a", 18446744073709551615ull, 2); }));
+    EXPECT(throws([&] { so.read_span("a", 8, 18446744073709551615ull); }));
+    // a number past 2^64 - 1 is a parse error of the table (ouro::Error), not std::out_of_range
+    const std::string big =
+        "[{\"name\":\"b\",\"shape\":[4],\"dtype\":0,\"offset\":99999999999999999999999,\"length\":16}]";
+    const std::string bpath = g_dir + "/bignum.bmts";
+    write_raw(bpath, header(1, 1, static_cast<uint32_t>(big.size())) + big);
+    bool parse_error = false;
+    try {
+        bmts::Shard sb(bpath);
+    } catch (const ouro::Error &) {
+        parse_error = true;
+    } catch (const std::exception &) {
+    }
+    EXPECT(parse_error);
 }
 
 static void test_had_runtime_offsets() {  // qwen35.rs:603-613

@@ -120,9 +120,12 @@ def test_full_card_against_oracle(gpu):
         errs.append(l2(one[0][i][f["single_idx"][i]], f["single_bf16"][i]))
     floor = float(max(f["noise_single_l2"].max(), f["noise_3tok_l2"].max()))
     print(f"relative L2 against the bf16-prefill oracle: {np.round(errs, 4).tolist()}; noise floor {floor:.4f}")
+    assert floor < BAR_L2  # the committed fixture still carries the floor the bar is set from
     assert max(errs) < BAR_L2, errs
 
 
-# set from the fixture's noise floor (see the module docstring)
-BAR_L2 = 0.25
-BAR_CORR = 0.97
+# From the fixture's noise floor: the oracle against itself with the epsilon
+# moved by 1e-7 differs by 0.13-0.18 relative L2 (noise_single_l2,
+# noise_3tok_l2); unrelated logits differ by ~1.4 with correlation ~0.
+BAR_L2 = 0.3
+BAR_CORR = 0.95
