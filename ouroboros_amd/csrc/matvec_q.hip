@@ -22,6 +22,13 @@ int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, flo
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
 int i2s_gemm(const uint8_t *i2s, size_t out_len, size_t in_len, const int8_t *xq, const float *act_scale,
              size_t ncols, float *y, int32_t *acc, void *stream);
+size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
+int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream, int raw);
+
+// TL1 matvecs with at least this many rows run the table-lookup kernel on
+// the raw payload (its table build only pays over many rows).
+constexpr size_t kTl1LutRows = 2048;
 
 namespace {
 
@@ -221,8 +228,10 @@ int launch_mv(int kind, const MvArgs &a, hipStream_t s) {
 // Shape rules of the reference decoders: TL1 rows are whole 128-groups
 // (ops.rs:296), TQ1_0 rows whole 256-blocks (QuantKind::row_bytes,
 // dequant.rs:376-387).
+// use_workspace = false keeps every path off the library workspace (the
+// 2-bit kinds then need xq_scratch / act_scale_scratch).
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream) {
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace) {
     if (!payload || !x || !y) return fail(OURO_ERR_INVALID_ARG, "matvec_q: NULL argument");
     if (!out_len || !in_len || !k) return fail(OURO_ERR_SHAPE, "matvec_q: empty shape");
     if (out_len > 0x7fffffffULL || in_len > 0x7fffffffULL || k > 0x7fffffffULL)
@@ -230,6 +239,15 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     switch (kind) {
     case OURO_KIND_TL1:
         if (in_len % 128) return fail(OURO_ERR_SHAPE, "matvec_q TL1: in_len %zu not a multiple of 128", in_len);
+        // one column of a large matrix: the lookup kernel straight on the
+        // reference bytes (per-block partial sums in the library workspace);
+        // allocation-free calls keep the direct kernel
+        if (k == 1 && out_len >= kTl1LutRows && use_workspace &&
+            reinterpret_cast<uintptr_t>(payload) % 4 == 0 && in_len <= 65536) {
+            float *partial = static_cast<float *>(workspace(tl1_lut_partial_floats(out_len, in_len) * 4, stream));
+            if (!partial) return OURO_ERR_HIP;
+            return tl1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream, 1);
+        }
         break;
     case OURO_KIND_TQ1_0:
         if (in_len % 256) return fail(OURO_ERR_SHAPE, "matvec_q TQ1_0: in_len %zu not a multiple of 256", in_len);
@@ -248,6 +266,7 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
         int8_t *xq = xq_scratch;
         float *ds = act_scale_scratch;
         if (!xq) {
+            if (!use_workspace) return fail(OURO_ERR_INVALID_ARG, "matvec_q: no activation scratch");
             const size_t xb = (k * in_len + 255) & ~size_t(255);
             uint8_t *ws = static_cast<uint8_t *>(workspace(xb + k * sizeof(float), stream));
             if (!ws) return OURO_ERR_HIP;
@@ -314,8 +333,8 @@ extern "C" {
 int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                           float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    if (kind != OURO_KIND_I2 && kind != OURO_KIND_I2_S)  // no scratch: the plain entry allocates nothing
-        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream);
+    if (kind != OURO_KIND_I2 && kind != OURO_KIND_I2_S)  // no scratch, and no workspace (TL1: the direct kernel)
+        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, false);
     if (in_len > kNoAllocMaxIn)
         return fail(OURO_ERR_SHAPE, "ouro_matvec_q_noalloc: in_len %zu exceeds the %zu-element static scratch",
                     in_len, kNoAllocMaxIn);
@@ -324,19 +343,19 @@ int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len, size_t 
     if (st) return st;
     int8_t *xq = static_cast<int8_t *>(p);
     float *s = reinterpret_cast<float *>(static_cast<uint8_t *>(p) + kNoAllocMaxIn);
-    return matmul_q(payload, kind, out_len, in_len, x, 1, y, xq, s, stream);
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, xq, s, stream, false);
 }
 
 int ouro_matvec_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                   float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream);
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, true);
 }
 
 int ouro_matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                   size_t k, float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    return matmul_q(payload, kind, out_len, in_len, x, k, y, nullptr, nullptr, stream);
+    return matmul_q(payload, kind, out_len, in_len, x, k, y, nullptr, nullptr, stream, true);
 }
 
 }  // extern "C"

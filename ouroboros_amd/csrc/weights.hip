@@ -14,7 +14,7 @@
 
 namespace ouro {
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream);
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace);
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
             const float *w_scale, void *stream, int src_i2s);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
@@ -29,7 +29,7 @@ size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream);
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
-                   void *amax_scratch, int32_t *idx, void *stream);
+                   void *amax_scratch, int32_t *idx, void *stream, int raw);
 int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream);
 }  // namespace ouro
 
@@ -211,7 +211,7 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
     if (w->kind == OURO_KIND_TL1) {  // one lookup pass per column, y column-major as matmul_q
         for (size_t c = 0; c < k; ++c) {
             const int st = tl1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,
-                                          w->partial, nullptr, nullptr, stream);
+                                          w->partial, nullptr, nullptr, stream, 0);
             if (st) return st;
         }
         return OURO_OK;
@@ -224,7 +224,7 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->act_scale,
                             k, y, nullptr, stream, 0);
     }
-    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->act_scale, stream);
+    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->act_scale, stream, false);
 }
 
 int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t *idx, void *stream) {
@@ -232,7 +232,7 @@ int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t
     if (!w || !x || !idx) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matvec_argmax: NULL argument");
     float *yy = y ? y : w->y;
     if (w->kind == OURO_KIND_TL1)  // the argmax rides on the partial-sum kernel
-        return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream);
+        return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream, 0);
     const int st = ouro_weight_matmul(w, x, 1, yy, stream);
     if (st) return st;
     return argmax_f32(yy, w->out_len, w->amax, idx, stream);

@@ -57,6 +57,31 @@ def test_tl1_matvec(gpu, orc, out_len, in_len):
     assert close(got, want, 1e-5).all()
 
 
+# Raw payloads of >= 2048 rows run the table-lookup kernel on the reference
+# bytes: row pitches of 4k groups (16-byte loads staged through LDS), 4k+2
+# groups (8-byte loads) and odd counts (4-byte), partial last group blocks,
+# partial 64-row tiles, and payloads 4 or 8 bytes past an aligned address.
+@pytest.mark.parametrize("out_len,in_len,offset", [(2048, 512, 0), (4111, 2560, 0), (4099, 6912, 0),
+                                                   (3001, 384, 0), (2500, 640, 0), (2113, 1024, 4),
+                                                   (2048, 5120, 8)])
+def test_tl1_matvec_raw_lookup(gpu, orc, out_len, in_len, offset):
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(out_len + in_len + offset)
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(in_len).astype(np.float32)
+    want = orc.matvec_tl1(p, out_len, in_len, x)
+    buf = DeviceBuffer((p.size + 16,), np.uint8)
+    from ouroboros_amd._lib import call
+    call("ouro_memcpy_htod", buf.ptr + offset, p.ctypes.data, p.size)
+    xd, y = DeviceBuffer.from_host(x), DeviceBuffer((out_len,), np.float32)
+    call("ouro_matvec_q", buf.ptr + offset, int(QuantKind.TL1), out_len, in_len, xd.ptr, y.ptr, None)
+    assert close(y.download(), want, 1e-5).all()
+    # the allocation-free entry takes the direct kernel; same tolerance
+    call("ouro_matvec_q_noalloc", buf.ptr + offset, int(QuantKind.TL1), out_len, in_len, xd.ptr, y.ptr, None)
+    assert close(y.download(), want, 1e-5).all()
+
+
 @pytest.mark.parametrize("k", [1, 3, 4, 8, 11])
 def test_tl1_matmul_column_major(gpu, orc, k):
     rng = np.random.default_rng(k)
