@@ -605,13 +605,19 @@ def cpu_baseline(orc) -> dict:
 
 
 def _cpu_model() -> str:
+    """/proc/cpuinfo's model name with family / model / stepping, which still
+    identify the part where a virtualised host shortens the name."""
+    f = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first logical CPU's block
+            k, _, v = line.partition(":")
+            f[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    ids = ", ".join(f"{k} {f[k]}" for k in ("cpu family", "model", "stepping") if k in f)
+    return f"{f.get('model name', 'unknown')} ({ids})" if ids else f.get("model name", "unknown")
 
 
 def gdn_cpu_baseline(orc) -> dict:

@@ -18,7 +18,9 @@
 // Every contraction runs on v_mfma_f32_16x16x32_bf16 with fp32 accumulate.
 // Raw bf16 q, k, v are exact MFMA operands; fp32 operands (S, T, R, U, Pt)
 // are split as hi + lo bf16 and multiplied in two or three passes, so the
-// products carry ~16 mantissa bits.  T is solved in fp32 on the VALU.
+// products carry ~16 mantissa bits.  T = (I + A)^-1 is inverted in fp32:
+// the four 16x16 diagonal blocks by substitution on the VALU, the six blocks
+// below them on v_mfma_f32_16x16x4f32.
 //
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
 // and computes what does not depend on the state: row norms, g, T and Pt,

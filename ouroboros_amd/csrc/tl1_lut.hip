@@ -36,8 +36,24 @@ __device__ __forceinline__ int tl1_trit(uint32_t v, uint32_t pow3) {
     return static_cast<int>((q * 3u) >> 8) - 1;
 }
 
+// Table slot of byte value v: v ^ (v >> 6), a bijection on 0..255.  A table
+// row is 256 floats, so values that agree in their low six bits share an
+// LDS bank; payloads whose rows are correlated (the lm_head probe payload of
+// ops.rs:694-717 has bytes (i ^ i >> 13) * 0x9E, even and equal mod 32 down
+// a column) put most lanes of a lookup on a few banks.  Folding the top two
+// bits into the bottom two spreads such values over four banks; on random
+// bytes it changes nothing.
+__device__ __forceinline__ uint32_t tl1_slot(uint32_t v) { return v ^ (v >> 6); }
+// The same on the bytes of a word that carry trits (mask 0x03 per trit byte;
+// the group's f16 scale bytes keep their value).
+__device__ __forceinline__ uint32_t tl1_slot4(uint32_t w, uint32_t mask) { return w ^ ((w >> 6) & mask); }
+// Trit-byte mask of word i of a row's 28-byte group (word 6 holds trit
+// bytes 24, 25 and the scale bytes 26, 27).
+__host__ __device__ constexpr uint32_t tl1_word_mask(int i) { return i % 7 == 6 ? 0x00000303u : 0x03030303u; }
+
 // Raw row-major payload [rows][groups][28] -> [block][tile][chunk][lane] x 16 B,
-// zero-padded (a padded group has d = 0).  One thread per (row, block, 16 B chunk).
+// trit bytes replaced by their table slots, zero-padded (a padded group has
+// d = 0).  One thread per (row, block, 16 B chunk).
 __global__ void tl1_repack_kernel(const uint8_t *raw, uint4 *dst, int out_len, int groups, int nb, int ntiles) {
     const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
     const long long total = static_cast<long long>(nb) * ntiles * 64 * kChunks;
@@ -54,7 +70,8 @@ __global__ void tl1_repack_kernel(const uint8_t *raw, uint4 *dst, int out_len, i
             const int off = c * 16 + k;          // byte within the block's 112
             const int g = b * kGB + off / 28;   // group
             if (g < groups) {
-                const uint32_t v = raw[row * rb + static_cast<long long>(g) * 28 + off % 28];
+                uint32_t v = raw[row * rb + static_cast<long long>(g) * 28 + off % 28];
+                if (off % 28 < 26) v = tl1_slot(v);  // trit bytes; 26, 27 are the scale
                 w[k / 4] |= v << (8 * (k % 4));
             }
         }
@@ -62,11 +79,7 @@ __global__ void tl1_repack_kernel(const uint8_t *raw, uint4 *dst, int out_len, i
     dst[i] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// One group block per blockIdx.y; waves walk row tiles.  RAW = 0 reads the
-// repacked layout; RAW = 16, 8 or 4 reads the reference's row-major payload
-// itself (matvec_q on device bytes), the 112 bytes of a lane's row block as
-// RAW-byte loads (the widest the row pitch groups * 28 keeps aligned).
-template <int RAW>
+// One group block per blockIdx.y; waves walk row tiles of the repacked layout.
 __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const float *x, float *partial,
                                                            int out_len, int groups, int ntiles) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -88,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const
 #pragma unroll
             for (int n = 0; n < 5; ++n, p3 *= 3) tr[n] = static_cast<float>(tl1_trit(static_cast<uint32_t>(v), p3));
             const float *xg = xs + g * 128;
-            float *Tg = T + g * 26 * 256 + v;
+            float *Tg = T + g * 26 * 256 + tl1_slot(static_cast<uint32_t>(v));
 #pragma unroll
             for (int bb = 0; bb < 26; ++bb) {
                 const int base = bb < 16 ? bb : bb < 24 ? 80 + (bb - 16) : 120 + (bb - 24);
@@ -111,38 +124,9 @@ __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const
     // while it looks up the current one
     uint4 nx[kAhead][kChunks];
     auto load_tile = [&](uint4 (&dst)[kChunks], int tile) {
-        if constexpr (RAW == 0) {
-            const uint4 *src = wb + static_cast<long long>(tile) * kChunks * 64 + lane;
+        const uint4 *src = wb + static_cast<long long>(tile) * kChunks * 64 + lane;
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) dst[c] = src[c * 64];
-        } else {
-            // row-major: this lane's row, bytes b*112 .. b*112 + 28*gcnt - 1
-            // (rows past the end read the last row and are never stored)
-            const int row = min(tile * 64 + lane, out_len - 1);
-            const uint8_t *src = reinterpret_cast<const uint8_t *>(w) + static_cast<long long>(row) * groups * 28 +
-                                 static_cast<long long>(b) * kGB * 28;
-            uint32_t u[kChunks * 4];
-            constexpr int kW = RAW / 4;  // words per load
-#pragma unroll
-            for (int i = 0; i < kChunks * 4; i += kW) {
-                if (i * 4 < gcnt * 28) {
-                    if constexpr (kW == 4) {
-                        const uint4 t = *reinterpret_cast<const uint4 *>(src + 4 * i);
-                        u[i] = t.x, u[i + 1] = t.y, u[i + 2] = t.z, u[i + 3] = t.w;
-                    } else if constexpr (kW == 2) {
-                        const uint2 t = *reinterpret_cast<const uint2 *>(src + 4 * i);
-                        u[i] = t.x, u[i + 1] = t.y;
-                    } else {
-                        u[i] = *reinterpret_cast<const uint32_t *>(src + 4 * i);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < kW; ++j) u[i + j] = 0u;
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < kChunks; ++c) dst[c] = make_uint4(u[4 * c], u[4 * c + 1], u[4 * c + 2], u[4 * c + 3]);
-        }
+        for (int c = 0; c < kChunks; ++c) dst[c] = src[c * 64];
     };
 #pragma unroll
     for (int a = 0; a < kAhead; ++a)
@@ -182,104 +166,118 @@ __global__ __launch_bounds__(kThreads) void tl1_lut_kernel(const uint4 *w, const
     }
 }
 
-// The same lookups on the reference's row-major payload when a row's group
-// blocks are 16-byte aligned (groups % 4 == 0): each wave stages a tile of
-// 64 rows x 112 bytes through its own LDS region so the loads stay
-// coalesced -- load k of the tile has lane 7j + c read 16-byte chunk c of
-// row 9k + j (63 lanes, nine 112-byte row segments per instruction), which
-// lands at byte 16 * (63k + lane) of the staging; then lane r reads row r's
-// 112 bytes back (both access patterns are bank-conflict free) and looks
-// them up exactly as above.  The next tile's loads are in flight during the
-// lookups.  Eight waves: the table and 8 x 7 KiB of staging fill the 160 KiB
-// of LDS, so x is read from global memory (L1/L2 broadcasts) in the build.
-// (Measured alternatives, on 248320x5120: one row per lane read straight
-// from global memory, 113 us; 16 waves staging 32-row tiles with a row's
-// groups split over lanes l and l ^ 32, 144 us; this one 100 us; the
-// repacked layout of a resident weight, 61 us.)
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-constexpr int kRawThreads = 512;
-constexpr int kRawStage = 64 * kGB * 28;                              // bytes per wave
-constexpr int RAW_LDS = kTable * 4 + (kRawThreads / 64) * kRawStage;  // 163840
+// The same lookups on the reference's row-major payload (matvec_q on device
+// bytes, 4-byte aligned).  Lane 4j + g of a wave owns group g of the block
+// for row 16k + j of a 64-row tile: it reads the group's 28 bytes as one
+// 16-byte and one 12-byte load (dword-aligned; the 16 rows of a load are
+// 16 contiguous 112-byte segments), looks up its 26 trit bytes, scales by
+// the group's own f16 d, and the four lanes of a row add their products
+// with two DPP quad swaps.  No byte leaves the lane that loaded it, so the
+// weights need no LDS staging and every lookup instruction has 64 live
+// lanes.  Each group's table starts 16 banks after the previous one, so the
+// four groups of a lookup spread over the banks.  The next tile's loads are
+// in flight during the lookups.
+// A block's 112-byte segments share 128-byte lines with the neighbouring
+// blocks' segments, so the workgroups of all blocks of one set of tiles are
+// placed on one XCD (workgroup i runs on XCD i mod 8) and read those lines
+// through one L2: reading the 248320x5120 payload in this pattern alone
+// takes 45 us that way and 76 us with the blocks spread over XCDs.
+// (Measured alternatives, on 248320x5120: one row per lane, its 112 bytes
+// read straight from global memory, 113 us; whole rows staged through LDS
+// per wave, 92-96 us; this kernel with the blocks on different XCDs, 92 us;
+// the repacked layout of a resident weight, 55-62 us.)
+typedef unsigned v4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef unsigned v3a __attribute__((ext_vector_type(3), aligned(4)));
+constexpr int kRawThreads = 1024;
+constexpr int kGStride = 26 * 256 + 16;  // floats per group table
+constexpr int RAW_LDS = kGB * kGStride * 4;
+constexpr int kXcds = 8;  // MI355X: workgroup i of a launch runs on XCD i mod 8
 
-// Orders a wave's LDS accesses across lanes: LDS executes one wave's
-// instructions in issue order, so only the compiler must not move them
-// across this point (a memory fence here would also wait for the global
-// loads of the next tile that are meant to stay in flight).
-__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); }
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 
+// 1D grid of kXcds * per_xcd * nb workgroups: workgroup i is block
+// (i / kXcds) % nb of tile set (i % kXcds) * per_xcd + i / (kXcds * nb).
 __global__ __launch_bounds__(kRawThreads) void tl1_lut_raw_kernel(const uint8_t *w, const float *x, float *partial,
-                                                                  int out_len, int groups, int ntiles) {
+                                                                  int out_len, int groups, int ntiles, int nb,
+                                                                  int per_xcd) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    float *T = lds;  // [g][b][256]
     const int tid = threadIdx.x;
-    const int b = blockIdx.y;  // groups % 4 == 0: every block has kGB groups
-    uint8_t *stage = reinterpret_cast<uint8_t *>(lds + kTable) + (tid >> 6) * kRawStage;
-    for (int p = tid; p < kGB * 256; p += kRawThreads) {  // (group, byte value) pairs
-        const int v = p & 255, g = p >> 8;
-        float tr[5];
-        uint32_t p3 = 1;
+    const int slot = blockIdx.x / kXcds;
+    const int b = slot % nb;
+    const int set = (blockIdx.x % kXcds) * per_xcd + slot / nb;
+    const int gcnt = min(kGB, groups - b * kGB);
+    static_assert(kRawThreads == kGB * 256, "one thread per (group, byte value)");
+    {
+        const int v = tid & 255, g = tid >> 8;
+        if (g < gcnt) {
+            float tr[5];
+            uint32_t p3 = 1;
 #pragma unroll
-        for (int n = 0; n < 5; ++n, p3 *= 3) tr[n] = static_cast<float>(tl1_trit(static_cast<uint32_t>(v), p3));
-        const float *xg = x + (b * kGB + g) * 128;
-        float *Tg = T + g * 26 * 256 + v;
+            for (int n = 0; n < 5; ++n, p3 *= 3) tr[n] = static_cast<float>(tl1_trit(static_cast<uint32_t>(v), p3));
+            const float *xg = x + (b * kGB + g) * 128;
+            float *Tg = lds + g * kGStride + tl1_slot(static_cast<uint32_t>(v));
 #pragma unroll
-        for (int bb = 0; bb < 26; ++bb) {
-            const int base = bb < 16 ? bb : bb < 24 ? 80 + (bb - 16) : 120 + (bb - 24);
-            const int stride = bb < 16 ? 16 : bb < 24 ? 8 : 2;
-            float s = 0.f;
+            for (int bb = 0; bb < 26; ++bb) {
+                const int base = bb < 16 ? bb : bb < 24 ? 80 + (bb - 16) : 120 + (bb - 24);
+                const int stride = bb < 16 ? 16 : bb < 24 ? 8 : 2;
+                float s = 0.f;
 #pragma unroll
-            for (int n = 0; n < (bb < 24 ? 5 : 4); ++n) s += tr[n] * xg[base + n * stride];
-            Tg[bb * 256] = s;
+                for (int n = 0; n < (bb < 24 ? 5 : 4); ++n) s += tr[n] * xg[base + n * stride];
+                Tg[bb * 256] = s;
+            }
         }
     }
     __syncthreads();
 
     const int lane = tid & 63;
-    const int j = lane / 7, cc = lane - 7 * j;  // loading: row 9k + j of the tile, 16-byte chunk cc
-    const int wglobal = blockIdx.x * (kRawThreads / 64) + (tid >> 6);
-    const int wstride = gridDim.x * (kRawThreads / 64);
+    const int j = lane >> 2, g = lane & 3;
+    const bool live = g < gcnt;  // lanes past a short last block load group 0 and add nothing
+    const int wglobal = set * (kRawThreads / 64) + (tid >> 6);
+    const int wstride = kXcds * per_xcd * (kRawThreads / 64);
     const long long rowb = static_cast<long long>(groups) * 28;
-    const uint8_t *wb = w + static_cast<long long>(b) * kGB * 28 + 16 * cc;
+    const uint8_t *wb = w + static_cast<long long>(b * kGB + (live ? g : 0)) * 28;
+    const float *Tg = lds + g * kGStride;
     float *pb = partial + static_cast<long long>(b) * out_len;
-    v4u ld[8];  // native vectors: an array of uint4 structs would live in scratch memory
+    v4a ld4[4];
+    v3a ld3[4];
     auto load_tile = [&](int tile) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int row = min(tile * 64 + 9 * k + j, out_len - 1);  // rows past the end: never stored
-            ld[k] = *reinterpret_cast<const v4u *>(wb + row * rowb);
+        for (int k = 0; k < 4; ++k) {
+            const int row = min(tile * 64 + 16 * k + j, out_len - 1);  // rows past the end: never stored
+            const uint8_t *p = wb + row * rowb;
+            ld4[k] = *reinterpret_cast<const v4a *>(p);
+            ld3[k] = *reinterpret_cast<const v3a *>(p + 16);
         }
     };
     if (wglobal < ntiles) load_tile(wglobal);
     for (int tile = wglobal; tile < ntiles; tile += wstride) {  // wave-uniform
+        uint32_t u[4][7];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (lane < 63 && 9 * k + j < 64) *reinterpret_cast<v4u *>(stage + 16 * (63 * k + lane)) = ld[k];
-        wave_sync();
-        if (tile + wstride < ntiles) load_tile(tile + wstride);
-        uint32_t u[kChunks * 4];
-#pragma unroll
-        for (int q = 0; q < kChunks; ++q) {
-            const v4u t = *reinterpret_cast<const v4u *>(stage + 112 * lane + 16 * q);
-            u[4 * q] = t[0], u[4 * q + 1] = t[1], u[4 * q + 2] = t[2], u[4 * q + 3] = t[3];
+        for (int k = 0; k < 4; ++k) {
+            u[k][0] = ld4[k][0], u[k][1] = ld4[k][1], u[k][2] = ld4[k][2], u[k][3] = ld4[k][3];
+            u[k][4] = ld3[k][0], u[k][5] = ld3[k][1], u[k][6] = ld3[k][2];
         }
-        wave_sync();  // the staging is free for the next tile
-        float acc = 0.f;
+        if (tile + wstride < ntiles) load_tile(tile + wstride);
 #pragma unroll
-        for (int g = 0; g < kGB; ++g) {
-            const float *Tg = T + g * 26 * 256;
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int i = 0; i < 7; ++i) u[k][i] = tl1_slot4(u[k][i], tl1_word_mask(i));
             float gs = 0.f;
 #pragma unroll
             for (int bb = 0; bb < 26; ++bb) {
-                const int by = g * 28 + bb;
-                const uint32_t v = (u[by >> 2] >> (8 * (by & 3))) & 0xffu;
+                const uint32_t v = (u[k][bb >> 2] >> (8 * (bb & 3))) & 0xffu;
                 gs += Tg[bb * 256 + v];
             }
-            const uint32_t dw = u[(g * 28 + 24) >> 2] >> 16;  // bytes 26, 27 of the group
-            const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dw)));
-            acc += d * gs;
+            const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u[k][6] >> 16)));
+            float part = live ? d * gs : 0.f;
+            part += quad_perm<0xB1>(part);  // lanes [1,0,3,2] of each quad
+            part += quad_perm<0x4E>(part);  // lanes [2,3,0,1]
+            const int row = tile * 64 + 16 * k + j;
+            if (g == 0 && row < out_len) pb[row] = part;
         }
-        const int row = tile * 64 + lane;
-        if (row < out_len) pb[row] = acc;
     }
 }
 
@@ -322,45 +320,10 @@ int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, voi
     return check_launch("tl1_repack_kernel");
 }
 
-// raw: 0 for the repacked layout, else the payload is the reference's
-// row-major bytes (4-byte aligned).
-int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
-                   void *amax_scratch, int32_t *idx, void *stream, int raw) {
-    const int groups = static_cast<int>(in_len / 128), nb = (groups + kGB - 1) / kGB;
-    // the widest load the row pitch (groups * 28 bytes) and the base keep aligned
-    const uintptr_t base = reinterpret_cast<uintptr_t>(packed);
-    const int width = !raw ? 0 : (groups % 4 == 0 && base % 16 == 0) ? 16 : (groups % 2 == 0 && base % 8 == 0) ? 8 : 4;
-    void (*kern)(const uint4 *, const float *, float *, int, int, int) =
-        width == 0 ? tl1_lut_kernel<0> : width == 8 ? tl1_lut_kernel<8> : tl1_lut_kernel<4>;
-    const bool staged = width == 16;  // coalesced loads through LDS staging
-    static bool attr[4] = {false, false, false, false};
-    const int ai = width == 0 ? 0 : width == 16 ? 1 : width == 8 ? 2 : 3;
-    const int lds_bytes = staged ? RAW_LDS : LUT_LDS;
-    if (!attr[ai]) {
-        const void *f = staged ? reinterpret_cast<const void *>(tl1_lut_raw_kernel) : reinterpret_cast<const void *>(kern);
-        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess)
-            return fail(OURO_ERR_HIP, "tl1 lut: %d B of LDS refused", lds_bytes);
-        attr[ai] = true;
-    }
-    const int ntiles = static_cast<int>((out_len + 63) / 64);
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    // at most one workgroup per CU in all (LDS holds one): a grid larger than
-    // the CU count would run a second round on a few CUs
-    const int wpb = (staged ? kRawThreads : kThreads) / 64;
-    int gx = cus / nb;
-    gx = std::max(1, std::min(gx, (ntiles + wpb - 1) / wpb));
+// y = the sum of the nb block partials; with idx, also its finite_argmax.
+static int tl1_sum(const float *partial, float *y, size_t out_len, int nb, void *amax_scratch, int32_t *idx,
+                   void *stream) {
     hipStream_t s = as_stream(stream);
-    if (staged)
-        hipLaunchKernelGGL(tl1_lut_raw_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(nb)),
-                           dim3(kRawThreads), RAW_LDS, s, static_cast<const uint8_t *>(packed), x, partial,
-                           static_cast<int>(out_len), groups, ntiles);
-    else
-        hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(nb)), dim3(kThreads), LUT_LDS,
-                           s, static_cast<const uint4 *>(packed), x, partial, static_cast<int>(out_len), groups,
-                           ntiles);
-    int st = check_launch("tl1_lut_kernel");
-    if (st) return st;
     if (!idx) {
         hipLaunchKernelGGL(tl1_sum_kernel<false>, dim3(static_cast<unsigned>((out_len + 255) / 256)), dim3(256), 0, s,
                            partial, y, static_cast<int>(out_len), nb, nullptr);
@@ -370,9 +333,49 @@ int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const floa
     const int blocks = static_cast<int>(std::min<size_t>((out_len + 255) / 256, kArgmaxBlocks));
     hipLaunchKernelGGL(tl1_sum_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, partial, y,
                        static_cast<int>(out_len), nb, keys);
-    st = check_launch("tl1_sum_kernel");
+    const int st = check_launch("tl1_sum_kernel");
     if (st) return st;
     return argmax_final(keys, blocks, idx, stream);
+}
+
+// raw: 0 for the repacked layout, else the payload is the reference's
+// row-major bytes (4-byte aligned).
+int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream, int raw) {
+    const int groups = static_cast<int>(in_len / 128), nb = (groups + kGB - 1) / kGB;
+    static bool attr[2] = {false, false};
+    const int lds_bytes = raw ? RAW_LDS : LUT_LDS;
+    if (!attr[raw ? 1 : 0]) {
+        const void *f = raw ? reinterpret_cast<const void *>(tl1_lut_raw_kernel)
+                            : reinterpret_cast<const void *>(tl1_lut_kernel);
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess)
+            return fail(OURO_ERR_HIP, "tl1 lut: %d B of LDS refused", lds_bytes);
+        attr[raw ? 1 : 0] = true;
+    }
+    const int ntiles = static_cast<int>((out_len + 63) / 64);
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    // at most one workgroup per CU in all (LDS holds one): a grid larger than
+    // the CU count would run a second round on a few CUs
+    hipStream_t s = as_stream(stream);
+    if (raw) {
+        const int per_xcd = std::max(1, std::min(cus / kXcds / nb, (ntiles + 16 * kXcds - 1) / (16 * kXcds)));
+        hipLaunchKernelGGL(tl1_lut_raw_kernel, dim3(static_cast<unsigned>(kXcds * per_xcd * nb)), dim3(kRawThreads),
+                           RAW_LDS, s, static_cast<const uint8_t *>(packed), x, partial, static_cast<int>(out_len),
+                           groups, ntiles, nb, per_xcd);
+        const int st = check_launch("tl1_lut_raw_kernel");
+        if (st) return st;
+        return tl1_sum(partial, y, out_len, nb, amax_scratch, idx, stream);
+    }
+    const int wpb = kThreads / 64;
+    int gx = cus / nb;
+    gx = std::max(1, std::min(gx, (ntiles + wpb - 1) / wpb));
+        hipLaunchKernelGGL(tl1_lut_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(nb)), dim3(kThreads),
+                           LUT_LDS, s, static_cast<const uint4 *>(packed), x, partial, static_cast<int>(out_len),
+                           groups, ntiles);
+    const int st = check_launch("tl1_lut_kernel");
+    if (st) return st;
+    return tl1_sum(partial, y, out_len, nb, amax_scratch, idx, stream);
 }
 
 }  // namespace ouro

@@ -30,7 +30,7 @@ def config3_inputs(rng, B=32, Hk=16, Hv=32, d=S):
 
 
 @pytest.mark.parametrize("flags", [GDN_L2NORM_QK | GDN_SCALE_Q, GDN_L2NORM_QK | GDN_SCALE_Q | GDN_KHEAD_DIV])
-def test_config3_decode_steps(gpu, orc, flags):
+def test_config3_decode_steps(gpu, orc, margin, flags):
     rng = np.random.default_rng(0)
     B, Hk, Hv, d, eps = 32, 16, 32, S, 1e-6
     state, q, k, v, gate, beta = config3_inputs(rng, B, Hk, Hv, d)
@@ -45,13 +45,13 @@ def test_config3_decode_steps(gpu, orc, flags):
         qwen35.gdn_decode(sd, DeviceBuffer.from_host(q), DeviceBuffer.from_host(k), DeviceBuffer.from_host(v),
                           DeviceBuffer.from_host(gate), DeviceBuffer.from_host(beta), out, B, Hk, Hv, d,
                           flags=flags, eps=eps)
-        eo = rel_err(out.download(), want)
-        es = rel_err(sd.download(), ref_state)
+        eo = margin(f"out step {step}", out.download(), want, TOL)
+        es = margin(f"state step {step}", sd.download(), ref_state, TOL)
         assert eo[0] < TOL and eo[1] < TOL, (step, eo)
         assert es[0] < TOL and es[1] < TOL, (step, es)
 
 
-def test_f32_inputs_unnormalised(gpu, orc):
+def test_f32_inputs_unnormalised(gpu, orc, margin):
     rng = np.random.default_rng(1)
     B, Hk, Hv, d = 2, 2, 4, S
     state = rng.standard_normal((B, Hv, d * d)).astype(np.float32)
@@ -65,8 +65,8 @@ def test_f32_inputs_unnormalised(gpu, orc):
     sd = DeviceBuffer.from_host(state)
     out = DeviceBuffer((B, Hv, d), np.float32)
     qwen35.gdn_decode(sd, *(DeviceBuffer.from_host(a) for a in (q, k, v, gate, beta)), out, B, Hk, Hv, d, flags=0)
-    assert rel_err(out.download(), want)[0] < TOL
-    assert rel_err(sd.download(), ref)[0] < TOL
+    assert margin("out", out.download(), want, TOL)[0] < TOL
+    assert margin("state", sd.download(), ref, TOL)[0] < TOL
 
 
 def test_delta_head_dim_kats_on_gpu(gpu):
@@ -94,7 +94,7 @@ def test_delta_head_dim_kats_on_gpu(gpu):
 
 
 @pytest.mark.parametrize("sdim", [1, 16, 64, 100, 192, 256])
-def test_delta_head_dim_runtime_sdim(gpu, orc, sdim):
+def test_delta_head_dim_runtime_sdim(gpu, orc, margin, sdim):
     # delta_head_dim is the reference's runtime-dim variant (qwen35.rs:26-27)
     rng = np.random.default_rng(sdim)
     state = (0.1 * rng.standard_normal(sdim * sdim)).astype(np.float32)
@@ -104,11 +104,11 @@ def test_delta_head_dim_runtime_sdim(gpu, orc, sdim):
     orc.delta_head_dim(ref, sdim, q, k, v, step.gate, step.beta, want)
     got = np.zeros(sdim, np.float32)
     qwen35.delta_head_dim(state, sdim, q, k, v, step, got)
-    assert rel_err(got, want)[0] < TOL and rel_err(state, ref)[0] < TOL
+    assert margin("out", got, want, TOL)[0] < TOL and margin("state", state, ref, TOL)[0] < TOL
 
 
 @pytest.mark.parametrize("d,dt", [(64, "bf16"), (96, "f32"), (256, "bf16")])
-def test_decode_other_head_dims(gpu, orc, d, dt):
+def test_decode_other_head_dims(gpu, orc, margin, d, dt):
     rng = np.random.default_rng(d)
     B, Hk, Hv, flags = 3, 2, 4, GDN_L2NORM_QK | GDN_SCALE_Q
     state, q, k, v, gate, beta = config3_inputs(rng, B, Hk, Hv, d)
@@ -121,7 +121,7 @@ def test_decode_other_head_dims(gpu, orc, d, dt):
     out = DeviceBuffer((B, Hv, d), np.float32)
     qwen35.gdn_decode(sd, *(DeviceBuffer.from_host(a) for a in (q, k, v, gate, beta)), out, B, Hk, Hv, d,
                       flags=flags, eps=1e-6)
-    assert rel_err(out.download(), want)[0] < TOL and rel_err(sd.download(), ref)[0] < TOL
+    assert margin("out", out.download(), want, TOL)[0] < TOL and margin("state", sd.download(), ref, TOL)[0] < TOL
 
 
 def test_bad_shapes_rejected(gpu):

@@ -25,7 +25,7 @@ def inputs(rng, B, Hk, Hv):
                 norm_w=f(D), conv=f(B, ch, 3), state=(0.02 * f(B, Hv, D * D)).astype(np.float32))
 
 
-def run(orc, B, Hk, Hv, flags, steps=1, seed=0, workspace=False):
+def run(orc, B, Hk, Hv, flags, steps=1, seed=0, workspace=False, margin=None):
     rng = np.random.default_rng(seed)
     x = inputs(rng, B, Hk, Hv)
     conv_ref, st_ref = x["conv"].copy(), x["state"].copy()
@@ -39,23 +39,27 @@ def run(orc, B, Hk, Hv, flags, steps=1, seed=0, workspace=False):
         qwen35.gdn_layer_decode(*(DeviceBuffer.from_host(x[n]) for n in NAMES), dconv, dst, out, B, Hk, Hv,
                                 flags=flags, eps=1e-6, workspace=ws)
         got = out.download()
+        if margin:
+            margin(f"out step {s}", got, want, TOL)
         assert rel(got, want) < TOL, (s, rel(got, want))
     assert np.array_equal(dconv.download(), conv_ref)  # the ring update is a pure shift
+    if margin:
+        margin("state", dst.download(), st_ref, TOL)
     assert rel(dst.download(), st_ref) < TOL
 
 
 @pytest.mark.parametrize("flags", [0, GDN_KHEAD_DIV, GDN_V_GROUPED, GDN_KHEAD_DIV | GDN_V_GROUPED])
-def test_layer_block_matches_oracle(gpu, orc, flags):
-    run(orc, 3, 2, 4, flags, seed=flags)
+def test_layer_block_matches_oracle(gpu, orc, margin, flags):
+    run(orc, 3, 2, 4, flags, seed=flags, margin=margin)
 
 
 def test_layer_block_three_steps_carry_conv_and_state(gpu, orc):
     run(orc, 2, 2, 6, GDN_V_GROUPED, steps=3, seed=11, workspace=True)
 
 
-def test_layer_block_config3_shape(gpu, orc):
+def test_layer_block_config3_shape(gpu, orc, margin):
     # B=32 sequences, Hk=16, Hv=32, d=128 (the decode workload's shape)
-    run(orc, 32, 16, 32, GDN_V_GROUPED, seed=12)
+    run(orc, 32, 16, 32, GDN_V_GROUPED, seed=12, margin=margin)
 
 
 def test_layer_block_rejects_bad_flags(gpu):
