@@ -23,13 +23,14 @@
 // below them on v_mfma_f32_16x16x4f32.
 //
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
-// and computes what does not depend on the state: row norms, g, T and Pt,
-// written to a workspace record.  gdn_chunk_scan_kernel then walks the chunks
-// of a sequence in order.  Output column j of the recurrence only touches
-// state column j, so 16-column stripes of the state are independent chains:
-// a "chain" wave keeps one stripe in registers and runs K S0 -> R -> U ->
-// S update, while a paired "output" wave forms O for the same stripe; two
-// barriers per chunk.
+// and computes what does not depend on the state: row norms, g, T and the
+// per-row coefficients, written to a workspace record.  gdn_chunk_scan_kernel
+// then walks the chunks of a sequence in order.  Output column j of the
+// recurrence only touches state column j, so 16-column stripes of the state
+// are independent chains: a "chain" wave keeps one stripe in registers and
+// runs K S0 -> R -> U -> S update, while a paired "output" wave forms Pt
+// from the chunk's K and Q rows and O for the same stripe; two barriers per
+// chunk.
 #include "common.hpp"
 
 namespace ouro {
@@ -45,43 +46,45 @@ constexpr int kMaxSeq = 256;      // sequences per launch (offsets by value)
 constexpr int KP = kD + 8;        // bf16 row pitch of K, Q (272 B)
 constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free 8-byte reads)
 
-// Workspace record of one (chunk, v-head), 256-byte aligned, everything the
-// scan reads in the lane order of its MFMA operands:
+// Workspace record of one (chunk, v-head), 256-byte aligned:
 //   T as A operands [slot][hi, lo][64 lanes] x 16 B                  12 KiB
-//   Pt as A operands [slot][hi, lo][64 lanes] x 16 B                 12 KiB
 //   vectors [64] fp32: beta, rk = beta e^g nk, w = nk e^(g_C - g),
-//   so = e^g nq, g                                                 1280 B
+//   so = e^g nq, g, nk, nq, rho = e^(g - g_16floor(r/16)) nq and
+//   cb_b = e^(g_16b - g) nk for rows < 16b (b = 1..3)               2816 B
 // T slots are (s-tile a, t-slab q) = (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
-// (T is lower triangular: slab q is zero for a < 2q); Pt slots are
-// (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
+// (T is lower triangular: slab q is zero for a < 2q); the scan's Pt slots
+// are (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
 constexpr int REC_T = 0;
-constexpr int REC_P = 12 * 64 * 16;
-constexpr int REC_V = REC_P + 12 * 64 * 16;
-enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_G = 256, kVec = 320 };
-constexpr size_t kRec = 26112;
+constexpr int REC_V = 12 * 64 * 16;
+enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_G = 256, V_NK = 320, V_NQ = 384, V_RHO = 448, V_CB = 512,
+       kVec = 704 };
+constexpr size_t kRec = 15104;
 static_assert(REC_V + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
 
-// Scan kernel LDS byte offsets.  K and the T operands are read in the first
-// half of a chunk only and refilled in the second; the Pt operands (of the
-// chunk before, read in the first half) likewise; K^T, Q and the vectors are
-// double-buffered; X passes S0 and U (hi/lo operand registers) from each
+// Scan kernel LDS byte offsets: K, Q, V, K^T, the vectors and the T
+// operands of chunk c are staged in the second half of chunk c - 1 and read
+// in the first half of chunk c (K^T in the second: it is double-buffered);
+// the Pt operands are formed from K and Q in the first half of chunk c and
+// read in its second half; X passes so (Q S0) and U (first half) from each
 // chain wave to its output wave.
-constexpr int S_K = 0;                          // K [64][KP]
-constexpr int S_Q = S_K + kC * KP * 2;          // Q [2][64][KP]
-constexpr int S_KT = S_Q + 2 * kC * KP * 2;     // K^T [2][128][KTP]
-constexpr int S_VEC = S_KT + 2 * kD * KTP * 2;  // vectors [2][kVec]
-constexpr int S_T = S_VEC + 2 * kVec * 4;       // T operands [12][64] x 16 B
-constexpr int S_P = S_T + 12 * 64 * 16;         // Pt operands [12][64] x 16 B
-constexpr int S_X = S_P + 12 * 64 * 16;         // [4 waves][S0 hi/lo 8 KiB, U hi/lo 4 KiB]
-constexpr int X_WAVE = 12288;
+constexpr int VP = kDVB + 8;                // bf16 row pitch of the V tile (144 B)
+constexpr int S_K = 0;                      // K [64][KP]
+constexpr int S_Q = S_K + kC * KP * 2;      // Q [64][KP]
+constexpr int S_KT = S_Q + kC * KP * 2;     // K^T [2][128][KTP]
+constexpr int S_V = S_KT + 2 * kD * KTP * 2;  // V [64][VP]: the workgroup's 64 columns
+constexpr int S_VEC = S_V + kC * VP * 2;    // vectors [kVec]
+constexpr int S_T = S_VEC + kVec * 4;       // T operands [12][64] x 16 B
+constexpr int S_P = S_T + 12 * 64 * 16;     // Pt operands [12][64] x 16 B
+constexpr int S_X = S_P + 12 * 64 * 16;     // [4 waves][(so Q S0)^T 4 KiB, U hi/lo 4 KiB]
+constexpr int X_WAVE = 8192;
 constexpr int SCAN_LDS = S_X + 4 * X_WAVE;
-static_assert(SCAN_LDS <= 160 * 1024, "LDS budget of a gfx950 workgroup");
+static_assert(SCAN_LDS <= 160 * 1024 && S_V % 16 == 0 && S_VEC % 16 == 0 && S_T % 16 == 0, "scan LDS layout");
 
 // Prep kernel: one wave per (chunk, v-head), four per workgroup; each wave
-// has A (then T) [64][AP] fp32 and eight vectors [64] in LDS.
+// has A (then T) [64][AP] fp32 and four vectors [64] in LDS.
 constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int AP = kC + 4;                         // fp32 row pitch of A / T
-constexpr int PW_BYTES = kC * AP * 4 + 8 * kC * 4; // per-wave LDS
+constexpr int PW_BYTES = kC * AP * 4 + 4 * kC * 4; // per-wave LDS
 constexpr int PREP_LDS = kPrepWaves * PW_BYTES;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -179,12 +182,11 @@ __host__ __device__ constexpr int pslot(int bb, int q) { return bb < 2 ? bb : 2 
 __host__ __device__ constexpr int tslot(int aa, int q) { return q == 0 ? aa : 2 + aa; }
 
 // ---------------------------------------------------------------------------
-// Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K and Q
-// stay in registers in MFMA operand layout (lane r + 16 g holds
-// X[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so K K^T and
-// K Q^T need no LDS.  Pt is scaled, split and written in the operand order
-// of the scan's output lanes; A^T goes to the wave's LDS and T = (I + A)^-1
-// is solved with one column of T per lane.
+// Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K stays
+// in registers in MFMA operand layout (lane r + 16 g holds
+// K[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so K K^T needs
+// no LDS; Q rows are read for their norms only.  A^T goes to the wave's LDS
+// and T = (I + A)^-1 is solved in 16 x 16 blocks.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -197,8 +199,6 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     float *nq = nk + kC;
     float *gv = nq + kC;
     float *bv = gv + kC;
-    float *rho = bv + kC;   // e^(g - g_16floor(r/16)) nq
-    float *cb = rho + kC;   // [3][64]: e^(g_16b - g) nk for rows < 16b, b = 1..3
 
     // items of one chunk in k-head order, so that the v-heads reading the
     // same K and Q rows sit in the same workgroup
@@ -261,60 +261,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         rv[V_W + lane] = kn * __expf(gC - g);
         rv[V_SO + lane] = eg * qn;
         rv[V_G + lane] = g;
-        rho[lane] = __expf(g - gv[lane & ~15]) * qn;
+        rv[V_NK + lane] = kn;
+        rv[V_NQ + lane] = qn;
+        // Pt's decay e^(g_r - g_s) as e^(g_r - g_16b) e^(g_16b - g_s) off the
+        // diagonal tiles (both factors <= 1)
+        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]) * qn;
 #pragma unroll
-        for (int bb = 1; bb < 4; ++bb) cb[64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
-    }
-    __builtin_amdgcn_wave_barrier();
-
-    // Pt: P^T = K Q^T tiles (s-tile aa <= r-tile bb) at pt[bb (bb + 1) / 2 + aa]
-    {
-        f32x4 pt[10];
-#pragma unroll
-        for (int i = 0; i < 10; ++i) pt[i] = f32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-                for (int aa = 0; aa <= bb; ++aa)
-                    pt[bb * (bb + 1) / 2 + aa] = mfma(__builtin_bit_cast(bf16x8, kr[aa][kk]),
-                                                      __builtin_bit_cast(bf16x8, qr[bb][kk]), pt[bb * (bb + 1) / 2 + aa]);
-        uint4 *rp = reinterpret_cast<uint4 *>(rec + REC_P);
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-            const int r = 16 * bb + lr;  // this lane's r in the P^T tiles
-            const float rr = rho[r], gr = gv[r], nqr = nq[r];
-            f32x4 ps[4];
-#pragma unroll
-            for (int aa = 0; aa < 4; ++aa) {
-                if (aa > bb) {
-                    ps[aa] = f32x4{0, 0, 0, 0};
-                    continue;
-                }
-                ps[aa] = pt[bb * (bb + 1) / 2 + aa];
-                if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
-                    const f32x4 c4 = ld4(cb + 64 * (bb - 1) + 16 * aa + 4 * lg);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) ps[aa][e] *= rr * c4[e];
-                } else {  // diagonal tile: s <= r only
-                    const f32x4 gs = ld4(gv + 16 * aa + 4 * lg), ks = ld4(nk + 16 * aa + 4 * lg);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int sr = 16 * aa + 4 * lg + e;
-                        const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
-                        ps[aa][e] = sr <= r ? ev * nqr * ks[e] * ps[aa][e] : 0.f;
-                    }
-                }
-            }
-#pragma unroll
-            for (int q = 0; q <= bb / 2; ++q) {
-                bf16x8 ph, pl;
-                split8(ps[2 * q], ps[2 * q + 1], ph, pl);
-                rp[(2 * pslot(bb, q)) * 64 + lane] = __builtin_bit_cast(uint4, ph);
-                rp[(2 * pslot(bb, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, pl);
-            }
-        }
+        for (int bb = 1; bb < 4; ++bb) rv[V_CB + 64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
     }
 
     // A[r][c] = beta_r exp(g_r - g_c) nk_r nk_c (K K^T)[r][c], c < r, stored
@@ -432,23 +385,25 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
 // ---------------------------------------------------------------------------
 // Scan: one 512-thread workgroup per (sequence, v-head, 64 state columns).
 // Chain wave w (0..3) owns state columns jb + 16w .. +15, all 128 rows, in
-// registers and runs the recurrence for them: K S0, R, U = T R, and
-// S = b_C S0 + K^T U~, every contraction an MFMA whose operands are its own
-// accumulators or chunk rows in LDS.  Output wave 4 + w takes S0 and U from
-// chain wave w through LDS and computes O = so (Q S0) + Pt U with Pt from
-// the record, one chunk behind the chain.  The output waves load the next
-// chunk's K, Q and vectors in the first half and stage them into LDS at the
-// start of the second; the chain waves load their T operands and V values
-// for the next chunk in the second half.
+// registers and runs the recurrence for them: K S0 and (beside it, on the
+// same B operands) Q S0, R, U = T R, and S = b_C S0 + K^T U~, every
+// contraction an MFMA whose operands are its own accumulators or chunk rows
+// in LDS.  Output wave 4 + w finishes O of the same chunk for the same
+// stripe: in the first half it forms its share of the Pt operands from the
+// K and Q rows in LDS; in the second half it takes so (Q S0) and U
+// from chain wave w (through LDS), adds Pt U, stores O and stages the next
+// chunk's K, K^T, Q, V, vectors and T operands, whose loads it issued at the
+// start of the chunk.  O is formed transposed (O^T = S0^T Q^T + U^T Pt^T,
+// the same operands with A and B swapped), so a lane holds four adjacent
+// columns of a row and stores them as one 16-byte write.
 // ---------------------------------------------------------------------------
 
-// Output-wave prefetch of the next chunk: K rows (as pairs, for the K^T
-// store), Q, the vectors and the T operands.  Output thread to, item it (0, 1):
+// Output-wave loads of the next chunk.  Output thread to, item it (0, 1):
 // id = to + 256 it covers K rows 2p, 2p+1 (p = id % 32) and bf16 columns
-// 8c .. 8c+7 (c = id / 32).
+// 8c .. 8c+7 (c = id / 32); V item i is row id / 8, columns 8 (id % 8) ..
+// of the workgroup's 64.
 struct NextRegs {
-    uint4 k[2][2], q[4], vec, t[3];
-    uint4 p0, p1, p2;  // this thread's share of the Pt operands of the current chunk
+    uint4 k[2][2], q[4], vec, t[3], v[2];
 };
 
 // base + a 32-bit byte offset (lets the loads use a uniform base address)
@@ -458,18 +413,19 @@ __device__ __forceinline__ const T &at(const void *base, unsigned byte_off) {
 }
 
 // Rows at or past n load row n - 1 (always valid, n >= 1) and are zeroed
-// when staged into LDS (or used), so the loads carry no branches and nothing
-// waits for them before the stage.
+// when staged into LDS, so the loads carry no branches and nothing waits
+// for them before the stage.
 __device__ __forceinline__ uint4 zero_if(bool z, uint4 v) {
     return z ? make_uint4(0, 0, 0, 0) : v;
 }
 
-__device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int to, int t0, int n, int kh,
-                                          const unsigned char *rec) {
+__device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int to, int t0, int n, int kh, int h,
+                                          int jb, const unsigned char *rec) {
     // uniform chunk bases, 32-bit lane offsets
     const uint16_t *kb = a.k + (static_cast<long long>(t0) * a.Hk + kh) * kD;
     const uint16_t *qb = a.q + (static_cast<long long>(t0) * a.Hk + kh) * kD;
-    const unsigned ks = static_cast<unsigned>(a.Hk) * kD;
+    const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jb;
+    const unsigned ks = static_cast<unsigned>(a.Hk) * kD, vs = static_cast<unsigned>(a.Hv) * kD;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = to + 256 * it;
@@ -479,6 +435,8 @@ __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int t
             const unsigned row = static_cast<unsigned>(min(2 * p + w, n - 1));
             r.k[it][w] = at<uint4>(kb, 2u * (row * ks + 8u * c));
         }
+        const unsigned vrow = static_cast<unsigned>(min(id >> 3, n - 1));
+        r.v[it] = at<uint4>(vb, 2u * (vrow * vs + 8u * (id & 7)));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -491,12 +449,13 @@ __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int t
     for (int i = 0; i < 3; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec + REC_T)[to + 256 * i];
 }
 
-// Stage the next chunk: K and the T operands (read in the first half of a
-// chunk) and K^T, Q, vectors into buffer `buf`.
+// Stage the next chunk's K, K^T (into buffer buf), Q, V, vectors and T
+// operands.
 __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds, int buf, int to, int n) {
     uint16_t *K = reinterpret_cast<uint16_t *>(lds + S_K);
     uint32_t *KT = reinterpret_cast<uint32_t *>(lds + S_KT + buf * kD * KTP * 2);
-    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q + buf * kC * KP * 2);
+    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q);
+    uint16_t *V = reinterpret_cast<uint16_t *>(lds + S_V);
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = to + 256 * it;
@@ -512,92 +471,55 @@ __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds
             KT[((8 * c + 2 * e) * KTP + 2 * p) >> 1] = (x0[e] & 0xffffu) | (x1[e] << 16);
             KT[((8 * c + 2 * e + 1) * KTP + 2 * p) >> 1] = (x0[e] >> 16) | (x1[e] & 0xffff0000u);
         }
+        *reinterpret_cast<uint4 *>(V + (id >> 3) * VP + 8 * (id & 7)) = zero_if((id >> 3) >= n, r.v[it]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int idx = to + 256 * i;
         *reinterpret_cast<uint4 *>(Q + (idx >> 4) * KP + 8 * (idx & 15)) = zero_if((idx >> 4) >= n, r.q[i]);
     }
-    if (to < kVec / 4) reinterpret_cast<uint4 *>(lds + S_VEC + buf * kVec * 4)[to] = r.vec;
+    if (to < kVec / 4) reinterpret_cast<uint4 *>(lds + S_VEC)[to] = r.vec;
 #pragma unroll
     for (int i = 0; i < 3; ++i) reinterpret_cast<uint4 *>(lds + S_T)[to + 256 * i] = r.t[i];
 }
 
-// V of a chain wave's stripe in D layout: v[4a + e] = V[16a + 4g + e][jw + r]
-// (row clamped to n - 1; zeroed when used).
-__device__ __forceinline__ void load_v(const ChunkArgs &a, uint16_t (&v)[16], int t0, int n, int h, int jw, int lr,
-                                       int lg) {
-    const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
-    const unsigned vs = static_cast<unsigned>(a.Hv) * kD;
+// Pt slot (r-tile bb, s-slab q) of the chunk in LDS: the P^T tiles
+// (s-tile aa = 2q, 2q + 1) = K Q^T scaled by e^(g_r - g_s) nq_r nk_s for
+// s <= r, as hi/lo A operands of Pt U (lane r + 16 g: row 16 bb + r).
+__device__ __forceinline__ void pt_slot(unsigned char *lds, int bb, int q, int lane, int lr, int lg) {
+    const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
+    const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q);
+    const float *cv = reinterpret_cast<const float *>(lds + S_VEC);
+    const int r = 16 * bb + lr;
+    const float rr = cv[V_RHO + r], gr = cv[V_G + r], nqr = cv[V_NQ + r];
+    f32x4 ps[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const unsigned row = static_cast<unsigned>(min(16 * (i >> 2) + 4 * lg + (i & 3), n - 1));
-        v[i] = at<uint16_t>(vb, 2u * (row * vs + static_cast<unsigned>(lr)));
-    }
-}
-
-// O = so (Q S0) + Pt U for one output stripe of the chunk at t0 (n rows),
-// with Q and the vectors in buffer buf and Pt in the Pt slot.
-__device__ __forceinline__ void out_chunk(const ChunkArgs &a, const unsigned char *lds, int buf, const bf16x8 (&sh)[4],
-                                          const bf16x8 (&sl)[4], const bf16x8 (&uh)[2], const bf16x8 (&ul)[2],
-                                          int t0, int n, int h, int jw, int lane, int lr, int lg) {
-    const uint4 *P = reinterpret_cast<const uint4 *>(lds + S_P);  // [slot][lane]
-    const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q + buf * kC * KP * 2);
-    const float *cv = reinterpret_cast<const float *>(lds + S_VEC + buf * kVec * 4);
-    f32x4 o[4];
+    for (int t = 0; t < 2; ++t) {
+        const int aa = 2 * q + t;
+        ps[t] = f32x4{0, 0, 0, 0};
+        if (aa > bb) continue;
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb) o[bb] = f32x4{0, 0, 0, 0};
+        for (int kk = 0; kk < 4; ++kk)
+            ps[t] = mfma(ld_perm(K + (16 * aa + lr) * KP, 32 * kk, lg), ld_perm(Q + r * KP, 32 * kk, lg), ps[t]);
+        if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
+            const f32x4 c4 = ld4(cv + V_CB + 64 * (bb - 1) + 16 * aa + 4 * lg);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        bf16x8 qa[4];
+            for (int e = 0; e < 4; ++e) ps[t][e] *= rr * c4[e];
+        } else {  // diagonal tile: s <= r only
+            const f32x4 gs = ld4(cv + V_G + 16 * aa + 4 * lg), kn = ld4(cv + V_NK + 16 * aa + 4 * lg);
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) qa[bb] = ld_perm(Q + (16 * bb + lr) * KP, 32 * q, lg);
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sh[q], o[bb]);
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) o[bb] = mfma(qa[bb], sl[q], o[bb]);
-    }
-#pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-        const f32x4 so = ld4(cv + V_SO + 16 * bb + 4 * lg);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[bb][e] *= so[e];
-    }
-    // Pt U over s-slab q for r-tiles bb with q <= bb / 2
-#pragma unroll
-    for (int pass = 0; pass < 3; ++pass) {
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-#pragma unroll
-            for (int q = 0; q <= bb / 2; ++q) {
-                const bf16x8 ph = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q)) * 64 + lane]);
-                const bf16x8 pl = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q) + 1) * 64 + lane]);
-                if (pass == 0) o[bb] = mfma(ph, uh[q], o[bb]);
-                if (pass == 1) o[bb] = mfma(ph, ul[q], o[bb]);
-                if (pass == 2) o[bb] = mfma(pl, uh[q], o[bb]);
+            for (int e = 0; e < 4; ++e) {
+                const int sr = 16 * aa + 4 * lg + e;
+                const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
+                ps[t][e] = sr <= r ? ev * nqr * kn[e] * ps[t][e] : 0.f;
             }
         }
     }
-    float *ob = a.out + (static_cast<long long>(t0) * a.Hv + h) * kD + jw;
-    const unsigned os = static_cast<unsigned>(a.Hv) * kD;
-    if (n == kC) {
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
-                    4u * (static_cast<unsigned>(16 * bb + 4 * lg + e) * os + static_cast<unsigned>(lr))) = o[bb][e];
-    } else {
-#pragma unroll
-        for (int bb = 0; bb < 4; ++bb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = 16 * bb + 4 * lg + e;
-                if (row < n)
-                    *reinterpret_cast<float *>(reinterpret_cast<char *>(ob) +
-                        4u * (static_cast<unsigned>(row) * os + static_cast<unsigned>(lr))) = o[bb][e];
-            }
-    }
+    bf16x8 ph, pl;
+    split8(ps[0], ps[1], ph, pl);
+    uint4 *P = reinterpret_cast<uint4 *>(lds + S_P);
+    P[(2 * pslot(bb, q)) * 64 + lane] = __builtin_bit_cast(uint4, ph);
+    P[(2 * pslot(bb, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, pl);
 }
 
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs a) {
@@ -625,53 +547,40 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
     }
     const int seq = grp / a.Hk, kh = grp % a.Hk;
     const int h = vhead(a, kh, mem >> 1);
-    const int jw = (mem & 1) * kDVB + 16 * (wave & 3);  // first state column of this stripe
+    const int jb = (mem & 1) * kDVB;    // first state column of the workgroup
+    const int jw = jb + 16 * (wave & 3);  // first state column of this stripe
     const int t_begin = a.cu[seq], t_end = a.cu[seq + 1];
     if (t_end <= t_begin) return;  // empty sequence: state unchanged (uniform per block)
     const int nchunks = (t_end - t_begin + kC - 1) / kC;
     auto record = [&](int c) { return a.ws + (static_cast<size_t>(a.coff[seq] + c) * a.Hv + h) * kRec; };
-    uint4 *X = reinterpret_cast<uint4 *>(lds + S_X + (wave & 3) * X_WAVE);  // [slot][lane]
+    uint4 *X = reinterpret_cast<uint4 *>(lds + S_X + (wave & 3) * X_WAVE);  // [slot][lane]: O^T 0..3, U 4..7
+    const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
+    const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q);
+    const float *cv = reinterpret_cast<const float *>(lds + S_VEC);
 
-    // Both roles run the same number of barriers (two per chunk and one
-    // after the loop); their registers are disjoint because each role has
-    // its own loop.
+    // Both roles run the same barriers: two per chunk.
     if (chain) {
         // state tile t holds S[16t + 4g + e][jw + r]
         float *S = a.state + (static_cast<long long>(seq) * a.Hv + h) * kD * kD + static_cast<long long>(jw + lr) * kD;
         f32x4 st[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) st[t] = ld4(S + 16 * t + 4 * lg);
-        bf16x8 sh[4], sl[4];  // S0 of the next chunk as hi/lo B operands, slab q = tiles 2q, 2q+1
+        bf16x8 sh[4], sl[4];  // S0 of the chunk as hi/lo B operands, slab q = tiles 2q, 2q+1
 #pragma unroll
         for (int q = 0; q < 4; ++q) split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
-        uint16_t vn[16];
-        load_v(a, vn, t_begin, min(kC, t_end - t_begin), h, jw, lr, lg);
+        const uint16_t *Vl = reinterpret_cast<const uint16_t *>(lds + S_V) + 16 * (wave & 3) + lr;
+        const uint4 *Tl = reinterpret_cast<const uint4 *>(lds + S_T);  // [slot][lane]
 
         for (int c = 0; c < nchunks; ++c) {
-            const int t0 = t_begin + c * kC;
-            const int n = min(kC, t_end - t0);
-            const int b = c & 1;
+            const int n = min(kC, t_end - t_begin - c * kC);
             const bool more = c + 1 < nchunks;
-            const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
-            const uint16_t *KT = reinterpret_cast<const uint16_t *>(lds + S_KT + b * kD * KTP * 2);
-            const float *cv = reinterpret_cast<const float *>(lds + S_VEC + b * kVec * 4);
-            __syncthreads();  // chunk c is in K, the T slot and buffer b; X is free
+            __syncthreads();  // chunk c staged (K, Q, V, vectors, T); X is free
 
-            // ---- first half: S0 -> X, KS, R, U -> X, U~ ---------------------
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                X[(2 * q) * 64 + lane] = __builtin_bit_cast(uint4, sh[q]);
-                X[(2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, sl[q]);
-            }
-            uint16_t vcur[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) vcur[i] = (16 * (i >> 2) + 4 * lg + (i & 3)) < n ? vn[i] : 0;
-            const uint4 *Tl = reinterpret_cast<const uint4 *>(lds + S_T);  // [slot][lane]
+            // ---- first half: KS and (Q S0)^T, R, U -> X, U~ -----------------
             const float bC = __expf(cv[V_G + n - 1]);
-
-            f32x4 ks[4], rr[4];
+            f32x4 ks[4], rr[4], ot[4];
 #pragma unroll
-            for (int aa = 0; aa < 4; ++aa) ks[aa] = f32x4{0, 0, 0, 0};
+            for (int aa = 0; aa < 4; ++aa) ks[aa] = ot[aa] = f32x4{0, 0, 0, 0};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 bf16x8 ka[4];
@@ -681,13 +590,27 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                 for (int aa = 0; aa < 4; ++aa) ks[aa] = mfma(ka[aa], sh[q], ks[aa]);
 #pragma unroll
                 for (int aa = 0; aa < 4; ++aa) ks[aa] = mfma(ka[aa], sl[q], ks[aa]);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) ka[bb] = ld_perm(Q + (16 * bb + lr) * KP, 32 * q, lg);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sh[q], ka[bb], ot[bb]);
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sl[q], ka[bb], ot[bb]);
+            }
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {  // ot[bb][e] = (Q S0)[16 bb + r][jw + 4 g + e], scaled by so of row 16 bb + r
+                const float so = cv[V_SO + 16 * bb + lr];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ot[bb][e] *= so;
+                X[bb * 64 + lane] = __builtin_bit_cast(uint4, ot[bb]);
             }
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) {
                 const f32x4 b4 = ld4(cv + V_BETA + 16 * aa + 4 * lg);
                 const f32x4 r4 = ld4(cv + V_RK + 16 * aa + 4 * lg);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) rr[aa][e] = b4[e] * bf(vcur[4 * aa + e]) - r4[e] * ks[aa][e];
+                for (int e = 0; e < 4; ++e)  // V rows past n are zero in LDS
+                    rr[aa][e] = b4[e] * bf(Vl[(16 * aa + 4 * lg + e) * VP]) - r4[e] * ks[aa][e];
             }
             bf16x8 rh[2], rl[2];
             split8(rr[0], rr[1], rh[0], rl[0]);
@@ -712,8 +635,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
             for (int q = 0; q < 2; ++q) {
                 bf16x8 uh, ul;
                 split8(u[2 * q], u[2 * q + 1], uh, ul);
-                X[512 + (2 * q) * 64 + lane] = __builtin_bit_cast(uint4, uh);
-                X[512 + (2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, ul);
+                X[256 + (2 * q) * 64 + lane] = __builtin_bit_cast(uint4, uh);
+                X[256 + (2 * q + 1) * 64 + lane] = __builtin_bit_cast(uint4, ul);
                 f32x4 w0 = u[2 * q], w1 = u[2 * q + 1];
                 const f32x4 c0 = ld4(cv + V_W + 32 * q + 4 * lg), c1 = ld4(cv + V_W + 32 * q + 16 + 4 * lg);
 #pragma unroll
@@ -724,10 +647,10 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                 split8(w0, w1, wh[q], wl[q]);
             }
 
-            __syncthreads();  // X holds S0 and U of chunk c; K and T may be refilled
+            __syncthreads();  // X holds (Q S0)^T and U of chunk c; K, Q, V, T may be refilled
 
-            // ---- second half: next chunk's V, S = b_C S0 + K^T U~ -----------
-            if (more) load_v(a, vn, t0 + kC, min(kC, t_end - t0 - kC), h, jw, lr, lg);
+            // ---- second half: S = b_C S0 + K^T U~ ----------------------------
+            const uint16_t *KT = reinterpret_cast<const uint16_t *>(lds + S_KT + (c & 1) * kD * KTP * 2);
 #pragma unroll
             for (int t = 0; t < 8; ++t) st[t] = st[t] * bC;
 #pragma unroll
@@ -747,59 +670,78 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
         }
 #pragma unroll
         for (int t = 0; t < 8; ++t) *reinterpret_cast<f32x4 *>(S + 16 * t + 4 * lg) = st[t];
-        __syncthreads();  // pairs with the output waves' last barrier
     } else {
-        // Output waves trail the chain by one chunk: O of chunk c - 1 is
-        // formed in the first half of chunk c, beside the chain's K S0 -> U.
+        const int ow = wave - 4;
         NextRegs nx;
         {
             const int n0 = min(kC, t_end - t_begin);
-            load_next(a, nx, tr, t_begin, n0, kh, record(0));
+            load_next(a, nx, tr, t_begin, n0, kh, h, jb, record(0));
             store_next(nx, lds, 0, tr, n0);
         }
-        bf16x8 sh[4], sl[4], uh[2], ul[2];  // S0 and U of the chunk before, from X
+        float *ob = a.out + static_cast<long long>(h) * kD + jw + 4 * lg;
+        const long long os = static_cast<long long>(a.Hv) * kD;
 
         for (int c = 0; c < nchunks; ++c) {
             const int t0 = t_begin + c * kC;
-            const int b = c & 1;
+            const int n = min(kC, t_end - t0);
             const bool more = c + 1 < nchunks;
             const int n1 = more ? min(kC, t_end - t0 - kC) : 0;
-            __syncthreads();  // chunk c is in buffer b; Pt of chunk c - 1 in the Pt slot
+            __syncthreads();  // chunk c staged
 
-            // ---- first half: loads (chunk c + 1, Pt of c), O of chunk c - 1 --
+            // ---- first half: next loads, Pt -----------------------------------
+            if (more) load_next(a, nx, tr, t0 + kC, n1, kh, h, jb, record(c + 1));
+            // this wave's Pt slots (two off-diagonal tiles and a diagonal one,
+            // or one of each; the diagonal tiles carry the exponentials):
+            // (3,0), (0,0) | (2,0), (2,1) | (1,0) | (3,1)
+            if (ow == 0) {
+                pt_slot(lds, 3, 0, lane, lr, lg);
+                pt_slot(lds, 0, 0, lane, lr, lg);
+            }
+            if (ow == 1) {
+                pt_slot(lds, 2, 0, lane, lr, lg);
+                pt_slot(lds, 2, 1, lane, lr, lg);
+            }
+            if (ow == 2) pt_slot(lds, 1, 0, lane, lr, lg);
+            if (ow == 3) pt_slot(lds, 3, 1, lane, lr, lg);
+
+            __syncthreads();  // X holds (Q S0)^T and U of chunk c; the Pt operands are complete
+
+            // ---- second half: O^T = (so Q S0)^T + U^T Pt^T, store O, stage chunk c + 1
             {
-                const uint4 *rp = reinterpret_cast<const uint4 *>(record(c) + REC_P) + tr;
-                nx.p0 = rp[0];
-                nx.p1 = rp[256];
-                nx.p2 = rp[512];
-            }
-            if (more) load_next(a, nx, tr, t0 + kC, n1, kh, record(c + 1));
-            if (c > 0) out_chunk(a, lds, b ^ 1, sh, sl, uh, ul, t0 - kC, kC, h, jw, lane, lr, lg);
-
-            __syncthreads();  // X holds S0 and U of chunk c; K, T and Pt are free
-
-            // ---- second half: stage chunk c + 1 and Pt of c, take S0, U of c -
-            if (more) store_next(nx, lds, b ^ 1, tr, n1);
-            {
-                uint4 *sp = reinterpret_cast<uint4 *>(lds + S_P) + tr;
-                sp[0] = nx.p0;
-                sp[256] = nx.p1;
-                sp[512] = nx.p2;
-            }
+                const uint4 *P = reinterpret_cast<const uint4 *>(lds + S_P);  // [slot][lane]
+                f32x4 ot[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                sh[q] = __builtin_bit_cast(bf16x8, X[(2 * q) * 64 + lane]);
-                sl[q] = __builtin_bit_cast(bf16x8, X[(2 * q + 1) * 64 + lane]);
-            }
+                for (int bb = 0; bb < 4; ++bb) ot[bb] = __builtin_bit_cast(f32x4, X[bb * 64 + lane]);
+                bf16x8 uh[2], ul[2];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                uh[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q) * 64 + lane]);
-                ul[q] = __builtin_bit_cast(bf16x8, X[512 + (2 * q + 1) * 64 + lane]);
+                for (int q = 0; q < 2; ++q) {
+                    uh[q] = __builtin_bit_cast(bf16x8, X[256 + (2 * q) * 64 + lane]);
+                    ul[q] = __builtin_bit_cast(bf16x8, X[256 + (2 * q + 1) * 64 + lane]);
+                }
+#pragma unroll
+                for (int pass = 0; pass < 3; ++pass) {
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb) {
+#pragma unroll
+                        for (int q = 0; q <= bb / 2; ++q) {
+                            const bf16x8 ph = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q)) * 64 + lane]);
+                            const bf16x8 pl = __builtin_bit_cast(bf16x8, P[(2 * pslot(bb, q) + 1) * 64 + lane]);
+                            if (pass == 0) ot[bb] = mfma(uh[q], ph, ot[bb]);
+                            if (pass == 1) ot[bb] = mfma(ul[q], ph, ot[bb]);
+                            if (pass == 2) ot[bb] = mfma(uh[q], pl, ot[bb]);
+                        }
+                    }
+                }
+                // ot[bb][e] = O[16 bb + r][jw + 4 g + e]
+                float *obc = ob + static_cast<long long>(t0) * os;
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) {
+                    const int row = 16 * bb + lr;
+                    if (row < n) *reinterpret_cast<f32x4 *>(obc + row * os) = ot[bb];
+                }
             }
+            if (more) store_next(nx, lds, (c + 1) & 1, tr, n1);
         }
-        __syncthreads();  // Pt of the last chunk is staged (its buffers are not overwritten)
-        const int tl = t_begin + (nchunks - 1) * kC;
-        out_chunk(a, lds, (nchunks - 1) & 1, sh, sl, uh, ul, tl, t_end - tl, h, jw, lane, lr, lg);
     }
 }
 
