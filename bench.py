@@ -290,11 +290,12 @@ def tl1_lmhead_payload():
 def bench_tl1(stream, steps, warmup):
     """TL1 (PTQ1_0) matvec at the reference's lm_head probe shape 248320x5120:
     a resident weight handle (repacked on upload for the table-lookup GEMV),
-    the same with the fused finite_argmax (greedy sample), and the raw-payload
-    ouro_matvec_q path."""
+    the same with the fused finite_argmax (greedy sample), the raw-payload
+    ouro_matvec_q path, and ouro_matvec_q on a raw TQ1_0 payload of the same
+    shape."""
     import ctypes as C
 
-    from ouroboros_amd._lib import KIND_TL1, call
+    from ouroboros_amd._lib import KIND_TL1, KIND_TQ1_0, call
     from ouroboros_amd.device import DeviceBuffer
 
     payload, x = tl1_lmhead_payload()
@@ -310,8 +311,17 @@ def bench_tl1(stream, steps, warmup):
     call("ouro_weight_free", h.value)
     w = DeviceBuffer.from_host(payload)
     ms_raw = time_events(stream, lambda _i: call("ouro_matvec_q", w.ptr, KIND_TL1, TL1_OUT, TL1_IN, xd.ptr, y.ptr,
-                                                 stream), 3, 1)
-    return ms, ms_am, ms_raw
+                                                 stream), n, 2)
+    del w
+    # the same shape as a raw TQ1_0 payload (random bytes, d = 1.0)
+    rng = np.random.default_rng(17)
+    tq = rng.integers(0, 256, TL1_OUT * (TL1_IN // 256) * 54, dtype=np.uint8)
+    g = tq.reshape(-1, 54)
+    g[:, 52], g[:, 53] = 0x00, 0x3C
+    wq = DeviceBuffer.from_host(tq)
+    ms_tq1 = time_events(stream, lambda _i: call("ouro_matvec_q", wq.ptr, KIND_TQ1_0, TL1_OUT, TL1_IN, xd.ptr, y.ptr,
+                                                 stream), n, 2)
+    return ms, ms_am, ms_raw, ms_tq1, tq.nbytes
 
 
 def bench_gemm(stream, steps, warmup, orc):
@@ -825,7 +835,7 @@ def main() -> int:
             "bytes_per_step": LY_BYTES,
         }
     if "tl1" in res:
-        ms, ms_am, ms_raw = res["tl1"]
+        ms, ms_am, ms_raw, ms_tq1, tq1_bytes = res["tl1"]
         gbs = TL1_BYTES / (ms * 1e-3) / 1e9
         sec["tl1_matvec_lmhead"] = {
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4),
@@ -837,6 +847,9 @@ def main() -> int:
             "greedy_sample_ms": round(ms_am, 4),
             "greedy_sample_tokens_per_s": round(1e3 / ms_am, 1),
             "raw_payload_matvec_q_ms": round(ms_raw, 4),
+            "raw_payload_matvec_q_GBs": round(TL1_BYTES / (ms_raw * 1e-3) / 1e9, 1),
+            "raw_tq1_0_matvec_q_ms": round(ms_tq1, 4),
+            "raw_tq1_0_matvec_q_GBs": round((tq1_bytes + 4 * (TL1_IN + TL1_OUT)) / (ms_tq1 * 1e-3) / 1e9, 1),
         }
     if "gemm" in res:
         rows, vendor = res["gemm"]

@@ -25,10 +25,16 @@ int i2s_gemm(const uint8_t *i2s, size_t out_len, size_t in_len, const int8_t *xq
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw);
+size_t tq1_lut_partial_floats(size_t out_len, size_t in_len);
+bool tq1_lut_fits(const void *payload, size_t in_len);
+int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream);
 
-// TL1 matvecs with at least this many rows run the table-lookup kernel on
-// the raw payload (its table build only pays over many rows).
-constexpr size_t kTl1LutRows = 2048;
+// TL1 and TQ1_0 matvecs with at least this many rows run the table-lookup
+// kernels on the raw payload: the table build and the partial-sum launch
+// cost ~14 us, which the direct kernels undercut below ~8192 rows (measured
+// at in_len 2560 and 5120).
+constexpr size_t kLutRows = 8192;
 
 namespace {
 
@@ -242,7 +248,7 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
         // one column of a large matrix: the lookup kernel straight on the
         // reference bytes (per-block partial sums in the library workspace);
         // allocation-free calls keep the direct kernel
-        if (k == 1 && out_len >= kTl1LutRows && use_workspace &&
+        if (k == 1 && out_len >= kLutRows && use_workspace &&
             reinterpret_cast<uintptr_t>(payload) % 4 == 0 && in_len <= 65536) {
             float *partial = static_cast<float *>(workspace(tl1_lut_partial_floats(out_len, in_len) * 4, stream));
             if (!partial) return OURO_ERR_HIP;
@@ -251,6 +257,12 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
         break;
     case OURO_KIND_TQ1_0:
         if (in_len % 256) return fail(OURO_ERR_SHAPE, "matvec_q TQ1_0: in_len %zu not a multiple of 256", in_len);
+        // one column of a large matrix: the lookup kernel on the reference bytes
+        if (k == 1 && out_len >= kLutRows && use_workspace && tq1_lut_fits(payload, in_len)) {
+            float *partial = static_cast<float *>(workspace(tq1_lut_partial_floats(out_len, in_len) * 4, stream));
+            if (!partial) return OURO_ERR_HIP;
+            return tq1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream);
+        }
         break;
     case OURO_KIND_F32:
         if (reinterpret_cast<uintptr_t>(payload) % 4) return fail(OURO_ERR_ALIGN, "matvec_q F32: payload alignment");

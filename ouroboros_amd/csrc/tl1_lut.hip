@@ -320,6 +320,111 @@ int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, voi
     return check_launch("tl1_repack_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// TQ1_0 (dequant.rs:49-105, ggml's block_tq1_0) by the same table lookups,
+// on the raw row-major payload (matvec_q on device bytes).  A 256-element
+// block is 54 bytes: qs[0..32] hold elements m + 32n, qs[32..48] elements
+// 160 + m + 16n (n = 0..4), qh[0..4] elements 240 + m + 4n (n = 0..3), then
+// the f16 d; a byte's digits decode as TL1's.  A workgroup takes a pair of
+// blocks (two tables of 52 positions x 256 values, 104 KiB; the second
+// starts 16 banks after the first).  Lane 2j + g owns block g of the pair for
+// row 32k + j of a 64-row tile: it reads the block as 14 dwords (an odd
+// block starts 2 bytes past a dword, so it reads from 2 bytes earlier and
+// realigns with one funnel shift per word), looks up its 52 trit bytes,
+// scales by its own d, and the pair of lanes adds with one DPP swap.  Needs
+// an even block count per row (so every pair is whole and every row starts
+// on a dword) and a 4-byte-aligned payload.  Workgroups of one tile set sit
+// on one XCD, as for TL1.
+constexpr int kTqPos = 52;
+constexpr int kTqGStride = kTqPos * 256 + 16;  // floats per block table
+constexpr int TQ_LDS = 2 * kTqGStride * 4;
+typedef unsigned v2a __attribute__((ext_vector_type(2), aligned(4)));
+
+__global__ __launch_bounds__(kRawThreads) void tq1_lut_raw_kernel(const uint8_t *w, const float *x, float *partial,
+                                                                  int out_len, int blocks, int ntiles, int npairs,
+                                                                  int per_xcd) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int tid = threadIdx.x;
+    const int slot = blockIdx.x / kXcds;
+    const int pr = slot % npairs;  // block pair
+    const int set = (blockIdx.x % kXcds) * per_xcd + slot / npairs;
+    static_assert(kRawThreads == 4 * 256, "one thread per (block, byte value, half of the positions)");
+    {
+        const int v = tid & 255, g = (tid >> 8) & 1, half = tid >> 9;  // g and half are wave-uniform
+        float tr[5];
+        uint32_t p3 = 1;
+#pragma unroll
+        for (int n = 0; n < 5; ++n, p3 *= 3) tr[n] = static_cast<float>(tl1_trit(static_cast<uint32_t>(v), p3));
+        const float *xg = x + (2 * pr + g) * 256;
+        float *Tg = lds + g * kTqGStride + tl1_slot(static_cast<uint32_t>(v));
+#pragma unroll
+        for (int bb = 0; bb < kTqPos; ++bb) {
+            if ((bb >= kTqPos / 2) != (half == 1)) continue;
+            const int base = bb < 32 ? bb : bb < 48 ? 160 + (bb - 32) : 240 + (bb - 48);
+            const int stride = bb < 32 ? 32 : bb < 48 ? 16 : 4;
+            float s = 0.f;
+#pragma unroll
+            for (int n = 0; n < (bb < 48 ? 5 : 4); ++n) s += tr[n] * xg[base + n * stride];
+            Tg[bb * 256] = s;
+        }
+    }
+    __syncthreads();
+
+    const int lane = tid & 63;
+    const int j = lane >> 1, g = lane & 1;
+    const int wglobal = set * (kRawThreads / 64) + (tid >> 6);
+    const int wstride = kXcds * per_xcd * (kRawThreads / 64);
+    const long long rowb = static_cast<long long>(blocks) * 54;
+    const uint8_t *wb = w + static_cast<long long>(2 * pr + g) * 54 - 2 * g;  // dword-aligned
+    const float *Tg = lds + g * kTqGStride;
+    float *pb = partial + static_cast<long long>(pr) * out_len;
+    v4a l0[2], l1[2], l2[2];
+    v2a l3[2];
+    auto load_tile = [&](int tile) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int row = min(tile * 64 + 32 * k + j, out_len - 1);  // rows past the end: never stored
+            const uint8_t *p = wb + row * rowb;
+            l0[k] = *reinterpret_cast<const v4a *>(p);
+            l1[k] = *reinterpret_cast<const v4a *>(p + 16);
+            l2[k] = *reinterpret_cast<const v4a *>(p + 32);
+            l3[k] = *reinterpret_cast<const v2a *>(p + 48);
+        }
+    };
+    if (wglobal < ntiles) load_tile(wglobal);
+    for (int tile = wglobal; tile < ntiles; tile += wstride) {  // wave-uniform
+        uint32_t wd[2][14];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wd[k][i] = l0[k][i], wd[k][4 + i] = l1[k][i], wd[k][8 + i] = l2[k][i];
+            wd[k][12] = l3[k][0], wd[k][13] = l3[k][1];
+        }
+        if (tile + wstride < ntiles) load_tile(tile + wstride);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            uint32_t u[13];
+#pragma unroll
+            for (int i = 0; i < 13; ++i) {
+                const uint32_t t = g ? __builtin_amdgcn_alignbit(wd[k][i + 1], wd[k][i], 16) : wd[k][i];
+                u[i] = tl1_slot4(t, 0x03030303u);
+            }
+            const uint32_t dbits = g ? (wd[k][13] >> 16) : (wd[k][13] & 0xffffu);
+            float gs = 0.f;
+#pragma unroll
+            for (int bb = 0; bb < kTqPos; ++bb) {
+                const uint32_t v = (u[bb >> 2] >> (8 * (bb & 3))) & 0xffu;
+                gs += Tg[bb * 256 + v];
+            }
+            const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(dbits)));
+            float part = d * gs;
+            part += quad_perm<0xB1>(part);  // lanes [1,0,3,2]: the other block of the pair
+            const int row = tile * 64 + 32 * k + j;
+            if (g == 0 && row < out_len) pb[row] = part;
+        }
+    }
+}
+
 // y = the sum of the nb block partials; with idx, also its finite_argmax.
 static int tl1_sum(const float *partial, float *y, size_t out_len, int nb, void *amax_scratch, int32_t *idx,
                    void *stream) {
@@ -376,6 +481,35 @@ int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const floa
     const int st = check_launch("tl1_lut_kernel");
     if (st) return st;
     return tl1_sum(partial, y, out_len, nb, amax_scratch, idx, stream);
+}
+
+size_t tq1_lut_partial_floats(size_t out_len, size_t in_len) { return (in_len / 512) * out_len; }
+
+// The lookup path takes TQ1_0 rows of an even block count on a 4-byte-aligned payload.
+bool tq1_lut_fits(const void *payload, size_t in_len) {
+    return in_len % 512 == 0 && in_len <= 65536 && reinterpret_cast<uintptr_t>(payload) % 4 == 0;
+}
+
+int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream) {
+    const int blocks = static_cast<int>(in_len / 256), npairs = blocks / 2;
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(tq1_lut_raw_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, TQ_LDS) != hipSuccess)
+            return fail(OURO_ERR_HIP, "tq1 lut: %d B of LDS refused", TQ_LDS);
+        attr = true;
+    }
+    const int ntiles = static_cast<int>((out_len + 63) / 64);
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int per_xcd = std::max(1, std::min(cus / kXcds / npairs, (ntiles + 16 * kXcds - 1) / (16 * kXcds)));
+    hipLaunchKernelGGL(tq1_lut_raw_kernel, dim3(static_cast<unsigned>(kXcds * per_xcd * npairs)), dim3(kRawThreads),
+                       TQ_LDS, as_stream(stream), static_cast<const uint8_t *>(payload), x, partial,
+                       static_cast<int>(out_len), blocks, ntiles, npairs, per_xcd);
+    const int st = check_launch("tq1_lut_raw_kernel");
+    if (st) return st;
+    return tl1_sum(partial, y, out_len, npairs, amax_scratch, idx, stream);
 }
 
 }  // namespace ouro

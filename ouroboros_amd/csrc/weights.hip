@@ -28,6 +28,10 @@ int act_quant(const void *x, int x_dtype, size_t rows, size_t n, int8_t *xq, flo
 size_t tl1_lut_bytes(size_t out_len, size_t in_len);
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_repack(const uint8_t *raw, size_t out_len, size_t in_len, void *dst, void *stream);
+size_t tq1_lut_partial_floats(size_t out_len, size_t in_len);
+bool tq1_lut_fits(const void *payload, size_t in_len);
+int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
+                   void *amax_scratch, int32_t *idx, void *stream);
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw);
 int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream);
@@ -40,7 +44,7 @@ struct ouro_weight {
     void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes
     int8_t *xq = nullptr;     // I2: activation scratch
     float *act_scale = nullptr;
-    float *partial = nullptr; // TL1: per-group-block partial sums
+    float *partial = nullptr; // TL1, large TQ1_0: per-block partial sums of the lookup kernels
     void *aux = nullptr;      // one allocation: y scratch [out_len] f32, then the argmax key slots
     float *y = nullptr;
     void *amax = nullptr;
@@ -53,6 +57,8 @@ namespace {
 // Columns from which an I2 matmul runs on the int8 MFMA GEMM instead of the
 // multi-column GEMV (measured crossover on the 6912x2560 layer).
 constexpr size_t kMfmaCols = 8;
+// Rows from which a TQ1_0 handle runs the table-lookup kernel (as matvec_q).
+constexpr size_t kTq1LutRows = 8192;
 
 size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:376-387)
     switch (kind) {
@@ -176,6 +182,13 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             release(w);
             return fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         }
+        // a large TQ1_0 matrix runs the lookup kernel: its block partials live with the handle
+        if (kind == OURO_KIND_TQ1_0 && out_len >= kTq1LutRows && tq1_lut_fits(w->payload, in_len) &&
+            hipMalloc(reinterpret_cast<void **>(&w->partial), tq1_lut_partial_floats(out_len, in_len) * sizeof(float)) !=
+                hipSuccess) {
+            release(w);
+            return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+        }
     }
     // y scratch (for argmax without a caller y) and the argmax key slots
     const size_t yb = (out_len * sizeof(float) + 255) & ~size_t(255);
@@ -216,6 +229,14 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         }
         return OURO_OK;
     }
+    if (w->kind == OURO_KIND_TQ1_0 && w->partial) {  // one lookup pass per column
+        for (size_t c = 0; c < k; ++c) {
+            const int st = tq1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,
+                                          w->partial, nullptr, nullptr, stream);
+            if (st) return st;
+        }
+        return OURO_OK;
+    }
     if (w->kind == OURO_KIND_I2 && w->mfma && k >= kMfmaCols) {
         int st = act_quant(x, OURO_DT_F32, k, w->in_len, w->xq, w->act_scale, stream);
         if (st) return st;
@@ -233,6 +254,8 @@ int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t
     float *yy = y ? y : w->y;
     if (w->kind == OURO_KIND_TL1)  // the argmax rides on the partial-sum kernel
         return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream, 0);
+    if (w->kind == OURO_KIND_TQ1_0 && w->partial)
+        return tq1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream);
     const int st = ouro_weight_matmul(w, x, 1, yy, stream);
     if (st) return st;
     return argmax_f32(yy, w->out_len, w->amax, idx, stream);

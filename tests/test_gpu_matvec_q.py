@@ -57,13 +57,13 @@ def test_tl1_matvec(gpu, orc, out_len, in_len):
     assert close(got, want, 1e-5).all()
 
 
-# Raw payloads of >= 2048 rows run the table-lookup kernel on the reference
-# bytes: row pitches of 4k groups (16-byte loads staged through LDS), 4k+2
-# groups (8-byte loads) and odd counts (4-byte), partial last group blocks,
-# partial 64-row tiles, and payloads 4 or 8 bytes past an aligned address.
-@pytest.mark.parametrize("out_len,in_len,offset", [(2048, 512, 0), (4111, 2560, 0), (4099, 6912, 0),
-                                                   (3001, 384, 0), (2500, 640, 0), (2113, 1024, 4),
-                                                   (2048, 5120, 8)])
+# Raw payloads of >= 8192 rows run the table-lookup kernel on the reference
+# bytes (a lane per (row, group)): row pitches of 4k, 4k+2 and odd group
+# counts, partial last group blocks, partial 64-row tiles, and payloads 4 or
+# 8 bytes past an aligned address.
+@pytest.mark.parametrize("out_len,in_len,offset", [(8192, 512, 0), (8209, 2560, 0), (8195, 6912, 0),
+                                                   (8250, 384, 0), (8500, 640, 0), (8257, 1024, 4),
+                                                   (8192, 5120, 8)])
 def test_tl1_matvec_raw_lookup(gpu, orc, out_len, in_len, offset):
     from ouroboros_amd.device import DeviceBuffer
 
@@ -80,6 +80,45 @@ def test_tl1_matvec_raw_lookup(gpu, orc, out_len, in_len, offset):
     # the allocation-free entry takes the direct kernel; same tolerance
     call("ouro_matvec_q_noalloc", buf.ptr + offset, int(QuantKind.TL1), out_len, in_len, xd.ptr, y.ptr, None)
     assert close(y.download(), want, 1e-5).all()
+
+
+# TQ1_0 payloads of >= 8192 rows with an even block count per row on a
+# 4-byte-aligned address run the table-lookup kernel (a lane per (row,
+# block), odd blocks realigned by 2 bytes); odd block counts, a payload 2
+# bytes past a dword and the allocation-free entry take the direct kernel.
+@pytest.mark.parametrize("out_len,in_len,offset", [(8192, 512, 0), (8209, 5120, 0), (8257, 2560, 4),
+                                                   (9001, 1024, 8), (8500, 768, 0), (8193, 1024, 2)])
+def test_tq1_matvec_raw_lookup(gpu, orc, out_len, in_len, offset):
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(out_len + in_len + offset)
+    p = tq1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(in_len).astype(np.float32)
+    want = orc.matvec_q(p, orc.KIND_TQ1_0, out_len, in_len, x)
+    buf = DeviceBuffer((p.size + 16,), np.uint8)
+    call("ouro_memcpy_htod", buf.ptr + offset, p.ctypes.data, p.size)
+    xd, y = DeviceBuffer.from_host(x), DeviceBuffer((out_len,), np.float32)
+    for entry in ("ouro_matvec_q", "ouro_matvec_q_noalloc"):
+        call(entry, buf.ptr + offset, int(QuantKind.TQ1_0), out_len, in_len, xd.ptr, y.ptr, None)
+        assert close(y.download(), want, 1e-5).all(), entry
+
+
+def test_tq1_handle_lookup_and_argmax(gpu, orc):
+    # a resident TQ1_0 weight of >= 8192 rows: matvec, 3 columns and the greedy sample
+    rng = np.random.default_rng(77)
+    out_len, in_len = 9000, 2048
+    p = tq1_payload(rng, out_len, in_len)
+    h = ops.Weight(QuantKind.TQ1_0, p, out_len, in_len)
+    x = rng.standard_normal(3 * in_len).astype(np.float32)
+    want = np.concatenate([orc.matvec_q(p, orc.KIND_TQ1_0, out_len, in_len, x[c * in_len:(c + 1) * in_len])
+                           for c in range(3)])
+    assert close(h.matvec(x[:in_len]), want[:out_len], 1e-5).all()
+    assert close(h.matmul(x, 3), want, 1e-5).all()
+    idx = h.matvec_argmax(x[:in_len])
+    best = orc.finite_argmax(want[:out_len])
+    assert idx == best or abs(float(want[idx]) - float(want[best])) <= 1e-5 * abs(float(want[best]))
+    h.free()
 
 
 @pytest.mark.parametrize("k", [1, 3, 4, 8, 11])
