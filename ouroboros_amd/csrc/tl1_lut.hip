@@ -248,6 +248,8 @@ __global__ __launch_bounds__(kRawThreads) void tl1_lut_raw_kernel(const uint8_t 
         for (int k = 0; k < 4; ++k) {
             const int row = min(tile * 64 + 16 * k + j, out_len - 1);  // rows past the end: never stored
             const uint8_t *p = wb + row * rowb;
+            // ordinary loads: the lines this block shares with its neighbours
+            // must stay in L2 for them (non-temporal loads: 65 -> 117 us)
             ld4[k] = *reinterpret_cast<const v4a *>(p);
             ld3[k] = *reinterpret_cast<const v3a *>(p + 16);
         }
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(kRawThreads) void tq1_lut_raw_kernel(const uint8_t 
         for (int k = 0; k < 2; ++k) {
             const int row = min(tile * 64 + 32 * k + j, out_len - 1);  // rows past the end: never stored
             const uint8_t *p = wb + row * rowb;
-            l0[k] = *reinterpret_cast<const v4a *>(p);
+            l0[k] = *reinterpret_cast<const v4a *>(p);  // ordinary loads, as for TL1
             l1[k] = *reinterpret_cast<const v4a *>(p + 16);
             l2[k] = *reinterpret_cast<const v4a *>(p + 32);
             l3[k] = *reinterpret_cast<const v2a *>(p + 48);
