@@ -17,6 +17,7 @@
 
 namespace ouro {
 namespace {
+typedef float nt4 __attribute__((ext_vector_type(4)));  // 16-byte vector for non-temporal loads
 
 constexpr int kHd = 128;  // attention head dim and delta-net d handled here
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -410,8 +411,9 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     for (int it = 0; it < (wkeys > 0 ? kWK / 4 : 0); ++it) {
         const int jj = 4 * it + g4;
         const float *kp = a.kc + ((wrow + min(jj, max(wkeys - 1, 0))) * a.nkv + kvh) * kHd + 8 * gl;
-        const float4 k0 = *reinterpret_cast<const float4 *>(kp);
-        const float4 k1 = *reinterpret_cast<const float4 *>(kp + 4);
+        // the KV cache is read once per step: non-temporal loads
+        const float4 k0 = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp)));
+        const float4 k1 = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp + 4)));
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float d = q[g][0].x * k0.x + q[g][0].y * k0.y + q[g][0].z * k0.z + q[g][0].w * k0.w +
@@ -453,7 +455,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
 #pragma unroll 8
     for (int j0 = 2 * wave; j0 < n; j0 += 8) {
         const int j = min(j0 + h, n - 1);  // clamped; its weight is zeroed
-        const float4 v = *reinterpret_cast<const float4 *>(vp + (prow[j / kPage] + j % kPage) * vstride);
+        const float4 v = __builtin_bit_cast(
+            float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(vp + (prow[j / kPage] + j % kPage) * vstride)));
         const bool live = j0 + h < n;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
