@@ -829,7 +829,7 @@ def main() -> int:
         sec["gdn_layer_block"] = {
             "value": round(GDN_B / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 4),
             "config": "run_delta's block between the projections: gates, conv+SiLU, normed recurrence, gated RMS "
-                      "norm, V-grouped; B=32, Hk=16, Hv=32, d=128, f32, 8 rotating state sets (3 launches)",
+                      "norm, V-grouped; B=32, Hk=16, Hv=32, d=128, f32, 8 rotating state sets (2 launches)",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
             "bytes_per_step": LY_BYTES,

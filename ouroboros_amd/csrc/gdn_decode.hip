@@ -31,7 +31,27 @@ struct DecodeArgs {
     int B, Hk, Hv;
     unsigned flags;
     float eps;
+    // conv mode (the layer block, run_delta qwen35.rs:1066-1112): q, k, v are
+    // conv_step + SiLU of the qkv projection over the conv ring (only read
+    // here; the gated-norm kernel shifts it afterwards), and gate and beta
+    // come from the raw projections
+    const float *qkv, *ring, *conv_w, *beta_raw, *alpha_raw, *dt_bias, *a_log;
+    int ch;
 };
+
+// conv_step (qwen35.rs:64-70) of one channel, then SiLU (ops.rs:34-36), in
+// the reference's operation order.
+__device__ __forceinline__ float conv_silu(const float4 &w, float r0, float r1, float r2, float x) {
+#pragma clang fp contract(off)
+    const float y = w.x * r0 + w.y * r1 + w.z * r2 + w.w * x;
+    return y / (1.0f + expf(-y));
+}
+
+__device__ __forceinline__ float conv1(const DecodeArgs &a, int b, int c) {
+    const long long base = static_cast<long long>(b) * a.ch + c;
+    const float *r = a.ring + base * 3;
+    return conv_silu(reinterpret_cast<const float4 *>(a.conv_w)[c], r[0], r[1], r[2], a.qkv[base]);
+}
 
 template <typename T>
 __device__ __forceinline__ float4 ld4(const T *p);
@@ -80,10 +100,12 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// CPW state columns per wavefront, WPB wavefronts per block.
-template <typename TQK, typename TV, int CPW, int WPB>
+// CPW state columns per wavefront, WPB wavefronts per block; CONV: the
+// layer block's inputs (DecodeArgs).
+template <typename TQK, typename TV, int CPW, int WPB, bool CONV>
 __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     static_assert(CPW == 4, "two column pairs per wavefront: one per 16-lane row of each half");
+    static_assert(!CONV || 64 * WPB >= 2 * kD + CPW * WPB, "one thread per conv channel");
     constexpr int kPairs = CPW / 2;
     constexpr int kSpan = 32 / kPairs;  // lanes of a half that end up holding one pair
     const int lane = threadIdx.x & 63;
@@ -105,11 +127,34 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
         s[p] = make_float4(t[0], t[1], t[2], t[3]);
     }
 
-    const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * kD + i0;
-    float4 k = ld4(static_cast<const TQK *>(a.k) + qk_off);
-    float4 q = ld4(static_cast<const TQK *>(a.q) + qk_off);
-    const float gate = a.gate ? a.gate[bh] : a.gate_s;
-    const float beta = a.beta ? a.beta[bh] : a.beta_s;
+    float4 k, q;
+    float gate, beta;
+    // conv mode: the workgroup's threads compute q and k of its k-head and v
+    // of its columns once, into LDS (channels: q at kh d, k at (Hk + kh) d,
+    // v at (2 Hk + h) d)
+    __shared__ float cv[CONV ? 2 * kD + CPW * WPB : 1];
+    if constexpr (CONV) {
+        const int t = threadIdx.x;
+        if (t < 2 * kD)
+            cv[t] = conv1(a, b, ((t >> 7) * a.Hk + kh) * kD + (t & (kD - 1)));
+        else if (t < 2 * kD + CPW * WPB)
+            cv[t] = conv1(a, b, (2 * a.Hk + h) * kD + blockIdx.y * (CPW * WPB) + t - 2 * kD);
+        __syncthreads();
+        q = *reinterpret_cast<const float4 *>(cv + i0);
+        k = *reinterpret_cast<const float4 *>(cv + kD + i0);
+        {
+#pragma clang fp contract(off)
+            beta = 1.0f / (1.0f + expf(-a.beta_raw[bh]));  // qwen35.rs:1066-1070, 1241-1243
+            const float x = a.alpha_raw[bh] + a.dt_bias[h];
+            gate = a.a_log[h] * (x > 20.0f ? x : logf(1.0f + expf(x)));
+        }
+    } else {
+        const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * kD + i0;
+        k = ld4(static_cast<const TQK *>(a.k) + qk_off);
+        q = ld4(static_cast<const TQK *>(a.q) + qk_off);
+        gate = a.gate ? a.gate[bh] : a.gate_s;
+        beta = a.beta ? a.beta[bh] : a.beta_s;
+    }
     if (a.flags & OURO_GDN_L2NORM_QK) {  // l2_norm: 1 / (sqrt(sum) + eps)
         const float ik = 1.0f / (sqrtf(sum_half(dot4(k, k))) + a.eps);
         const float iq = 1.0f / (sqrtf(sum_half(dot4(q, q))) + a.eps);
@@ -131,7 +176,8 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     // This lane now holds column pair (lane & 31) / kSpan of its half.
     const int myp = (lane & 31) / kSpan;
     const int myj = col0 + 2 * myp + half;
-    const float vj = ld1(static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD + myj);
+    const float vj = CONV ? cv[2 * kD + myj - blockIdx.y * (CPW * WPB)]
+                          : ld1(static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD + myj);
     const float dj = beta * (vj - skj);
     // dv of pair p in half hh sits in every lane of row 2*hh + p (named
     // scalars: an array indexed by the half would be placed in memory).
@@ -249,11 +295,39 @@ template <typename TQK, typename TV>
 int launch(const DecodeArgs &a, int d, hipStream_t s) {
     if (d != kD) return launch_any<TQK, TV>(a, d, s);
     dim3 grid(static_cast<unsigned>(a.B * a.Hv), kD / (kCPW * kWPB));
-    hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV, kCPW, kWPB>), grid, dim3(64 * kWPB), 0, s, a);
+    hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV, kCPW, kWPB, false>), grid, dim3(64 * kWPB), 0, s, a);
     return check_launch("gdn_decode_kernel");
 }
 
 }  // namespace
+
+// The layer block's recurrence with its conv + SiLU and gates computed in
+// the decode kernel (d = 128, f32; shapes and alignment checked by the
+// caller: qkv, ring, conv_w 16-byte aligned, channels a multiple of 4).
+int gdn_decode_conv(float *state, const float *qkv, const float *ring, const float *conv_w, const float *beta_raw,
+                    const float *alpha_raw, const float *dt_bias, const float *a_log, float *out, size_t B, size_t Hk,
+                    size_t Hv, unsigned flags, float eps, void *stream) {
+    DecodeArgs a{};
+    a.state = state;
+    a.out = out;
+    a.B = static_cast<int>(B);
+    a.Hk = static_cast<int>(Hk);
+    a.Hv = static_cast<int>(Hv);
+    a.flags = flags;
+    a.eps = eps;
+    a.qkv = qkv;
+    a.ring = ring;
+    a.conv_w = conv_w;
+    a.beta_raw = beta_raw;
+    a.alpha_raw = alpha_raw;
+    a.dt_bias = dt_bias;
+    a.a_log = a_log;
+    a.ch = static_cast<int>((2 * Hk + Hv) * kD);
+    dim3 grid(static_cast<unsigned>(B * Hv), kD / (kCPW * kWPB));
+    hipLaunchKernelGGL((gdn_decode_kernel<float, float, kCPW, kWPB, true>), grid, dim3(64 * kWPB), 0, as_stream(stream),
+                       a);
+    return check_launch("gdn_decode_kernel");
+}
 
 int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,
                const float *gate, const float *beta, float gate_s, float beta_s, float *out,

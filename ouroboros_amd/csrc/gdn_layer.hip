@@ -8,12 +8,14 @@
 //   the recurrence (delta_head_dim), giving o
 //   gated = gated_norm_rms(o, norm_w, z) per head, optionally permuted to
 //   the V-grouped head order.
-// Here that is three launches on the caller's stream with no host round
-// trip: gdn_conv_gate_kernel (elementwise, writes conv_out, beta, gate into
-// the workspace), the decode kernel reading q, k, v in place from conv_out
-// (sequence stride = channels), and gdn_gated_norm_kernel.  The state
-// update dominates the bytes (2 x 64 KiB per head); the other two kernels
-// move about B * (channels * 28 + Hv * d * 16) bytes.
+// Here that is two launches on the caller's stream with no host round
+// trip: the decode kernel computing each head's q, k, v (conv + SiLU over
+// the ring, which it only reads) and its gates from the raw projections,
+// then gdn_gated_norm_kernel, which also shifts the ring (every wavefront
+// the channels of its v-head, and those of its k-head when it is the first
+// v-head reading it).  The state update dominates the bytes (2 x 64 KiB per
+// head).  gdn_decode_core (the hybrid stack's path for more than 64
+// sequences) keeps the separate conv/gate kernel.
 #include "common.hpp"
 
 namespace ouro {
@@ -22,6 +24,9 @@ int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const v
                const float *gate, const float *beta, float gate_s, float beta_s, float *out,
                size_t B, size_t Hk, size_t Hv, size_t d, unsigned flags, float eps, void *stream,
                size_t qk_bs, size_t v_bs);
+int gdn_decode_conv(float *state, const float *qkv, const float *ring, const float *conv_w, const float *beta_raw,
+                    const float *alpha_raw, const float *dt_bias, const float *a_log, float *out, size_t B, size_t Hk,
+                    size_t Hv, unsigned flags, float eps, void *stream);
 
 namespace {
 
@@ -55,12 +60,27 @@ __global__ __launch_bounds__(256) void gdn_conv_gate_kernel(const float *qkv, fl
     }
 }
 
+// The conv ring shift of conv_step (qwen35.rs:64-70) for channel c of
+// sequence b: the window moves by one and the new input enters last.
+__device__ __forceinline__ void ring_shift(float *ring, const float *qkv, long long b, int ch, int c) {
+    const long long i = b * ch + c;
+    float *r = ring + i * 3;
+    const float r1 = r[1], r2 = r[2];
+    r[0] = r1;
+    r[1] = r2;
+    r[2] = qkv[i];
+}
+
 // gated_norm_rms (qwen35.rs:82-92) per (sequence, v-head), one wavefront
 // each, written at the head's V-grouped position when asked
-// (qwen35.rs:1122-1138: v-head r*Hk + k goes to k*(Hv/Hk) + r).
+// (qwen35.rs:1122-1138: v-head r*Hk + k goes to k*(Hv/Hk) + r).  RING: the
+// wavefront also shifts the conv ring of its v-head's channels and, when
+// it is the first v-head reading its k-head, of that k-head's q and k
+// channels (the decode kernel before it read the ring unchanged).
+template <bool RING>
 __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const float *o, const float *z, const float *norm_w,
                                                              float *out, int B, int Hk, int Hv, unsigned flags,
-                                                             float eps) {
+                                                             float eps, const float *qkv, float *ring) {
 #pragma clang fp contract(off)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long long bh = static_cast<long long>(blockIdx.x) * 4 + wave;
@@ -78,6 +98,17 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(const float *o, con
     const int dst = (flags & OURO_GDN_V_GROUPED) ? (h % Hk) * (Hv / Hk) + h / Hk : h;
     *reinterpret_cast<float2 *>(out + (b * Hv + dst) * kD + 2 * lane) =
         make_float2(x.x * inv * w.x * g0, x.y * inv * w.y * g1);
+    if constexpr (RING) {
+        const int ch = (2 * Hk + Hv) * kD, g = Hv / Hk;
+        ring_shift(ring, qkv, b, ch, (2 * Hk + h) * kD + lane);
+        ring_shift(ring, qkv, b, ch, (2 * Hk + h) * kD + 64 + lane);
+        const bool div = (flags & OURO_GDN_KHEAD_DIV) != 0;
+        if (div ? h % g == 0 : h < Hk) {
+            const int kh = div ? h / g : h;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) ring_shift(ring, qkv, b, ch, ((c >> 1) * Hk + kh) * kD + 64 * (c & 1) + lane);
+        }
+    }
 }
 
 constexpr size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
@@ -90,9 +121,9 @@ int gdn_gated_norm(const float *o, const float *z, const float *norm_w, float *o
                    size_t Hv, unsigned flags, float eps, void *stream) {
     const long long items = static_cast<long long>(rows * Hv);
     if (!items) return OURO_OK;
-    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
+    hipLaunchKernelGGL(gdn_gated_norm_kernel<false>, dim3(static_cast<unsigned>((items + 3) / 4)), dim3(256), 0,
                        as_stream(stream), o, z, norm_w, out, static_cast<int>(rows), static_cast<int>(Hk),
-                       static_cast<int>(Hv), flags, eps);
+                       static_cast<int>(Hv), flags, eps, nullptr, nullptr);
     return check_launch("gdn_gated_norm_kernel");
 }
 
@@ -137,21 +168,23 @@ int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, co
         return fail(OURO_ERR_INVALID_ARG, "gdn layer: bad flags 0x%x", flags);
     const size_t ch = 2 * Hk * kD + Hv * kD;
     if (B * ch > 0x7fffffffULL) return fail(OURO_ERR_SHAPE, "gdn layer: too many channels");
-    if ((reinterpret_cast<uintptr_t>(conv_w) | reinterpret_cast<uintptr_t>(workspace)) % 16 ||
+    if ((reinterpret_cast<uintptr_t>(conv_w) | reinterpret_cast<uintptr_t>(workspace) |
+         reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(conv) | reinterpret_cast<uintptr_t>(state)) % 16 ||
         (reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(out)) % 8)
-        return fail(OURO_ERR_ALIGN, "gdn layer: conv_w and workspace need 16-byte, z, norm_w, out 8-byte alignment");
+        return fail(OURO_ERR_ALIGN,
+                    "gdn layer: qkv, conv ring, state, conv_w and workspace need 16-byte, z, norm_w, out 8-byte alignment");
     unsigned char *ws = static_cast<unsigned char *>(workspace);
     if (!ws) {
         ws = static_cast<unsigned char *>(ouro::workspace(gdn_layer_ws_bytes(B, Hk, Hv), stream));
         if (!ws) return OURO_ERR_HIP;
     }
     float *o = reinterpret_cast<float *>(ws + align256(B * ch * 4) + 2 * align256(B * Hv * 4));
-    int st = gdn_decode_core(qkv, beta_raw, alpha_raw, dt_bias, a_log, conv_w, conv, state, o, B, Hk, Hv, flags, eps,
-                             ws, stream);
+    int st = gdn_decode_conv(state, qkv, conv, conv_w, beta_raw, alpha_raw, dt_bias, a_log, o, B, Hk, Hv,
+                             OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | (flags & OURO_GDN_KHEAD_DIV), eps, stream);
     if (st) return st;
-    hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3(static_cast<unsigned>((B * Hv + 3) / 4)), dim3(256), 0,
+    hipLaunchKernelGGL(gdn_gated_norm_kernel<true>, dim3(static_cast<unsigned>((B * Hv + 3) / 4)), dim3(256), 0,
                        as_stream(stream), o, z, norm_w, out, static_cast<int>(B), static_cast<int>(Hk),
-                       static_cast<int>(Hv), flags, eps);
+                       static_cast<int>(Hv), flags, eps, qkv, conv);
     return check_launch("gdn_gated_norm_kernel");
 }
 
