@@ -191,6 +191,34 @@ __device__ __forceinline__ float gemm_epilogue(const GemmEpilogue &e, float y, l
     if (e.op == EPI_RESID) return e.b[n * rows + row] + y;
     return y;
 }
+// gemm_epilogue on rows row .. row+3 of column n (row and rows multiples of
+// 4; y, ring, w and b 16-byte aligned), the operands moved as 16-byte
+// pieces; the same arithmetic per element.  Row i's ring is floats 3i .. 3i+2
+// of the three pieces.
+__device__ __forceinline__ float4 gemm_epilogue4(const GemmEpilogue &e, float4 y, long long n, int row, int rows) {
+#pragma clang fp contract(off)
+    if (e.op == EPI_CONV) {
+        float4 *r = reinterpret_cast<float4 *>(e.ring + (n * rows + row) * 3);
+        const float4 R0 = r[0], R1 = r[1], R2 = r[2];
+        const float4 *wp = reinterpret_cast<const float4 *>(e.w + 4LL * row);
+        const float4 w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3];
+        const float c0 = w0.x * R0.x + w0.y * R0.y + w0.z * R0.z + w0.w * y.x;
+        const float c1 = w1.x * R0.w + w1.y * R1.x + w1.z * R1.y + w1.w * y.y;
+        const float c2 = w2.x * R1.z + w2.y * R1.w + w2.z * R2.x + w2.w * y.z;
+        const float c3 = w3.x * R2.y + w3.y * R2.z + w3.z * R2.w + w3.w * y.w;
+        r[0] = make_float4(R0.y, R0.z, y.x, R1.x);
+        r[1] = make_float4(R1.y, y.y, R1.w, R2.x);
+        r[2] = make_float4(y.z, R2.z, R2.w, y.w);
+        return make_float4(c0 / (1.0f + expf(-c0)), c1 / (1.0f + expf(-c1)), c2 / (1.0f + expf(-c2)),
+                           c3 / (1.0f + expf(-c3)));
+    }
+    if (e.op == EPI_RESID) {
+        const float4 b = *reinterpret_cast<const float4 *>(e.b + n * rows + row);
+        return make_float4(b.x + y.x, b.y + y.y, b.z + y.z, b.w + y.w);
+    }
+    return make_float4(gemm_epilogue(e, y.x, n, row, rows), gemm_epilogue(e, y.y, n, row + 1, rows),
+                       gemm_epilogue(e, y.z, n, row + 2, rows), gemm_epilogue(e, y.w, n, row + 3, rows));
+}
 int i2_gemm_skinny_group(const GemmProblem *probs, int np, size_t in_len, size_t ncols, int x_tiled, void *stream);
 
 // KV-cache pages handed out by the host for one decode step of the hybrid

@@ -108,11 +108,17 @@ struct MfmaGroup {
 // fragment order, whose 1 KiB pieces (k block, step, column tile) are the
 // MFMA B operands lane by lane; they are copied to LDS as they are and read
 // back at lane * 16.  A launch may hold several products (MfmaGroup).
-template <int WR, int WC, bool XT>
-__global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGroup grp) {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2][WC * 16 * kXPitch];
+// KS > 1: KS groups of 4 wavefronts split the k blocks (each group its own
+// LDS buffers), so the latency chain is nkb / KS blocks long; the groups'
+// int32 tiles are added in LDS at the end (exact) and group 0 stores.
+template <int WR, int WC, bool XT, int KS>
+__global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(MfmaGroup grp) {
+    __shared__ __attribute__((aligned(16))) uint8_t xs[KS][2][WC * 16 * kXPitch];
     static_assert(WC * 4 * 1024 <= WC * 16 * kXPitch, "fragment-ordered tile fits the LDS buffer");
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert((KS - 1) * kGemmWaves * WR * WC * 4 * kWave * 4 <= KS * 2 * WC * 16 * kXPitch,
+                  "the k groups' partial tiles fit the LDS buffers");
+    const int tid0 = threadIdx.x, lane = tid0 & 63, kg = tid0 / (kWave * kGemmWaves);
+    const int tid = tid0 % (kWave * kGemmWaves), wave = tid >> 6;  // within the k group
     int pi = 0;
     while (pi + 1 < grp.np && static_cast<int>(blockIdx.x) >= grp.bstart[pi + 1]) ++pi;
     const GemmArgs &a = grp.p[pi];
@@ -145,7 +151,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kGemmWaves * i;
             const int off = XT ? 16 * c : (c / 16) * kXPitch + 16 * (c % 16);
-            *reinterpret_cast<v4u *>(&xs[buf][off]) = xr[i];
+            *reinterpret_cast<v4u *>(&xs[kg][buf][off]) = xr[i];
         }
     };
     v4u wr[WR];
@@ -163,20 +169,27 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
 #pragma unroll
         for (int c = 0; c < WC; ++c) acc[r][c] = v4i{0, 0, 0, 0};
 
-    load_x(0);
-    load_w(0);
+    // k blocks kb0 .. kb1-1 of this group; every group runs `per` steps (the
+    // same barriers), a group past its range loads a valid block and skips
+    // the products
+    const int per = (a.nkb + KS - 1) / KS;
+    const int kb0 = min(kg * per, a.nkb), kb1 = min(kb0 + per, a.nkb);
+    const auto kbc = [&](int it) { return min(kb0 + it, a.nkb - 1); };
+    load_x(kbc(0));
+    load_w(kbc(0));
     store_x(0);
     __syncthreads();
-    for (int kb = 0; kb < a.nkb; ++kb) {
+    for (int it = 0; it < per; ++it) {
         v4u wc[WR];
 #pragma unroll
         for (int r = 0; r < WR; ++r) wc[r] = wr[r];
-        const bool more = kb + 1 < a.nkb;
+        const bool more = it + 1 < per;
         if (more) {
-            load_x(kb + 1);
-            load_w(kb + 1);
+            load_x(kbc(it + 1));
+            load_w(kbc(it + 1));
         }
-        const uint8_t *xb = XT ? xs[kb & 1] + 16 * lane : xs[kb & 1] + (lane & 15) * kXPitch + 16 * (lane >> 4);
+        const uint8_t *xb = XT ? xs[kg][it & 1] + 16 * lane : xs[kg][it & 1] + (lane & 15) * kXPitch + 16 * (lane >> 4);
+        if (kb0 + it < kb1) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             v4i A[WR];
@@ -194,12 +207,44 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
                     acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B, acc[r][c], 0, 0, 0);
             }
         }
-        if (more) store_x((kb + 1) & 1);
+        }
+        if (more) store_x((it + 1) & 1);
         __syncthreads();
     }
+    if constexpr (KS > 1) {  // every LDS read of the loop is behind its last barrier
+        int *red = reinterpret_cast<int *>(&xs[0][0][0]);
+        constexpr int kAcc = WR * WC * 4;
+        if (kg > 0) {
+#pragma unroll
+            for (int r = 0; r < WR; ++r)
+#pragma unroll
+                for (int c = 0; c < WC; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        red[(((kg - 1) * kGemmWaves + wave) * kAcc + (r * WC + c) * 4 + e) * kWave + lane] = acc[r][c][e];
+        }
+        __syncthreads();
+        if (kg > 0) return;  // no barrier follows
+#pragma unroll
+        for (int g = 1; g < KS; ++g)
+#pragma unroll
+            for (int r = 0; r < WR; ++r)
+#pragma unroll
+                for (int c = 0; c < WC; ++c)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[r][c][e] += red[(((g - 1) * kGemmWaves + wave) * kAcc + (r * WC + c) * 4 + e) * kWave + lane];
+    }
 
-    // D lane l: rows 4*(l/16) + e of the row tile, column l % 16.
+    // D lane l: rows 4*(l/16) + e of the row tile, column l % 16.  With the
+    // row count a multiple of 4 and 16-byte aligned outputs and operands, a
+    // lane's four rows are stored (and the epilogue's operands moved) as one
+    // 16-byte piece.
     const float wscale = *a.w_scale;
+    const bool vec = (a.M & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(a.y) | reinterpret_cast<uintptr_t>(a.acc) |
+                       reinterpret_cast<uintptr_t>(a.epi.b) | reinterpret_cast<uintptr_t>(a.epi.ring) |
+                       reinterpret_cast<uintptr_t>(a.epi.w)) & 15) == 0;
 #pragma unroll
     for (int c = 0; c < WC; ++c) {
         const int n = n0 + 16 * c + (lane & 15);
@@ -208,6 +253,22 @@ __global__ __launch_bounds__(kWave *kGemmWaves) void i2_gemm_mfma_kernel(MfmaGro
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
+            if (vec && row + 3 < a.M) {
+                int t[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) t[e] = -(acc[r][c][e] >> 6);
+                const float4 v = make_float4(i8s_out(t[0], ds, wscale), i8s_out(t[1], ds, wscale),
+                                             i8s_out(t[2], ds, wscale), i8s_out(t[3], ds, wscale));
+                if (a.swiglu) {  // outputs row/2 and row/2 + 1: an 8-byte piece
+                    *reinterpret_cast<float2 *>(a.y + static_cast<long long>(n) * (a.M / 2) + row / 2) =
+                        make_float2(swiglu_pair(v.x, v.y), swiglu_pair(v.z, v.w));
+                    continue;
+                }
+                const long long o = static_cast<long long>(n) * a.M + row;
+                *reinterpret_cast<float4 *>(a.y + o) = gemm_epilogue4(a.epi, v, n, row, a.M);
+                if (a.acc) *reinterpret_cast<int4 *>(a.acc + o) = make_int4(t[0], t[1], t[2], t[3]);
+                continue;
+            }
             if (a.swiglu) {  // rows row .. row+3 = (up, gate) of outputs row/2, row/2 + 1
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
@@ -538,7 +599,7 @@ using SkinnyFn = void (*)(SkinnyGroup);
 
 struct GemmPick {
     GemmFn fn;
-    int wr, wc;
+    int wr, wc, ks;
 };
 
 // Row tiles per wavefront WR and column tiles per block WC, from sweeps on
@@ -546,16 +607,22 @@ struct GemmPick {
 // largest wavefront tile (2x4: 32 rows x 64 columns, 8 MFMAs per pair of
 // fragment loads) while it still gives >= 1024 workgroups, then 2x2 while
 // >= 512, else 1x1 (16x16 per wavefront, the most workgroups, which is what
-// few columns need).  nrt = row tiles of all products of the launch.
+// few columns need).  Few-column launches of 17 .. 64 columns (the decode
+// step's tall projections) take 1x2 with the k blocks split over two groups
+// of four wavefronts: half the activation traffic of 1x1 and half its chain
+// (12352x2560 and 13824x2560 at 64 columns, weights streamed from HBM:
+// 10.4 -> 9.1 and 9.7 -> 8.7 us).  nrt = row tiles of all products of the
+// launch.
 template <bool XT>
 GemmPick pick_gemm_xt(long long nrt, int N) {
     const auto blocks = [&](int wr, int wc) {
         const long long nrb = (nrt + kGemmWaves * wr - 1) / (kGemmWaves * wr);
         return nrb * ((N + 16 * wc - 1) / (16 * wc));
     };
-    if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4, XT>, 2, 4};
-    if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2, XT>, 2, 2};
-    return {i2_gemm_mfma_kernel<1, 1, XT>, 1, 1};
+    if (blocks(2, 4) >= 1024) return {i2_gemm_mfma_kernel<2, 4, XT, 1>, 2, 4, 1};
+    if (blocks(2, 2) >= 512) return {i2_gemm_mfma_kernel<2, 2, XT, 1>, 2, 2, 1};
+    if (N > 16 && N <= kSkinnyCols) return {i2_gemm_mfma_kernel<1, 2, XT, 2>, 1, 2, 2};
+    return {i2_gemm_mfma_kernel<1, 1, XT, 1>, 1, 1, 1};
 }
 
 // One launch of the 16x16 kernel over np products (shared k, column count
@@ -577,7 +644,7 @@ int launch_mfma_group(const GemmArgs *args, int np, void *stream) {
         if (grid > 0x7fffffffLL) return fail(OURO_ERR_SHAPE, "ouro_gemm_i2_mfma: grid too large");
     }
     g.bstart[np] = static_cast<int>(grid);
-    hipLaunchKernelGGL(p.fn, dim3(static_cast<unsigned>(grid)), dim3(kWave * kGemmWaves), 0, as_stream(stream), g);
+    hipLaunchKernelGGL(p.fn, dim3(static_cast<unsigned>(grid)), dim3(kWave * kGemmWaves * p.ks), 0, as_stream(stream), g);
     return check_launch("i2_gemm_mfma_kernel");
 }
 
