@@ -273,7 +273,15 @@ __global__ __launch_bounds__(kThreads) void row_rq_kernel(RowRqArgs a) {
     float *hl = lds + 17 * chunks + 16;  // Q2: the unrotated row, same padded layout
     const float *ar = a.a + row * n;
     float inv = 0.f;
+    // RQ_NORM with one chunk per thread: the norm weights and signs of the
+    // thread's chunk are loaded with the row, not after the sum of squares
+    const bool pre = PRO == RQ_NORM && chunks <= kThreads;
+    float wpre[16], spre[16];
     if constexpr (PRO == RQ_NORM) {
+        if (pre && tid < chunks) {
+            ld16(a.w + 16 * tid, wpre);
+            if (a.signs) ld16(a.signs + 16 * tid, spre);
+        }
         const float *br = a.b ? a.b + row * n : nullptr;
         float ss = 0.f;
         for (int c = tid; c < chunks; c += kThreads) {
@@ -306,7 +314,12 @@ __global__ __launch_bounds__(kThreads) void row_rq_kernel(RowRqArgs a) {
         if constexpr (PRO == RQ_NORM) {
             const float *p = lds + 17 * c;
             float wv[16];
-            ld16(a.w + 16 * c, wv);
+            if (pre) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) wv[i] = wpre[i];
+            } else {
+                ld16(a.w + 16 * c, wv);
+            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = p[i] * inv * wv[i];
             if constexpr (Q2) {
@@ -349,7 +362,12 @@ __global__ __launch_bounds__(kThreads) void row_rq_kernel(RowRqArgs a) {
         }
         if (a.signs) {
             float sg[16];
-            ld16(a.signs + 16 * dc, sg);
+            if (pre) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sg[i] = spre[i];
+            } else {
+                ld16(a.signs + 16 * dc, sg);
+            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = v[i] * sg[i];
         }
