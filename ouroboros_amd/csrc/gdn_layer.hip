@@ -127,10 +127,13 @@ int gdn_gated_norm(const float *o, const float *z, const float *norm_w, float *o
     return check_launch("gdn_gated_norm_kernel");
 }
 
+// gdn_decode_core's workspace: conv_out, beta, gate, then o.
 size_t gdn_layer_ws_bytes(size_t B, size_t Hk, size_t Hv) {
     const size_t ch = 2 * Hk * kD + Hv * kD;
     return align256(B * ch * 4) + 2 * align256(B * Hv * 4) + align256(B * Hv * kD * 4);
 }
+// ouro_gdn_layer_decode's workspace: the recurrence output o[B][Hv][d].
+static size_t layer_o_bytes(size_t B, size_t Hv) { return align256(B * Hv * kD * 4); }
 
 // run_delta's block up to the recurrence output: gates, conv + SiLU (ring
 // updated), normed recurrence into o[B][Hv][d] (no gated norm).  The
@@ -175,10 +178,10 @@ int gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, co
                     "gdn layer: qkv, conv ring, state, conv_w and workspace need 16-byte, z, norm_w, out 8-byte alignment");
     unsigned char *ws = static_cast<unsigned char *>(workspace);
     if (!ws) {
-        ws = static_cast<unsigned char *>(ouro::workspace(gdn_layer_ws_bytes(B, Hk, Hv), stream));
+        ws = static_cast<unsigned char *>(ouro::workspace(layer_o_bytes(B, Hv), stream));
         if (!ws) return OURO_ERR_HIP;
     }
-    float *o = reinterpret_cast<float *>(ws + align256(B * ch * 4) + 2 * align256(B * Hv * 4));
+    float *o = reinterpret_cast<float *>(ws);
     int st = gdn_decode_conv(state, qkv, conv, conv_w, beta_raw, alpha_raw, dt_bias, a_log, o, B, Hk, Hv,
                              OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q | (flags & OURO_GDN_KHEAD_DIV), eps, stream);
     if (st) return st;
@@ -196,7 +199,7 @@ extern "C" {
 
 size_t ouro_gdn_layer_workspace_bytes(size_t B, size_t Hk, size_t Hv, size_t d) {
     if (d != static_cast<size_t>(kD) || !Hk) return 0;
-    return gdn_layer_ws_bytes(B, Hk, Hv);
+    return layer_o_bytes(B, Hv);
 }
 
 int ouro_gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,

@@ -88,6 +88,7 @@ def test_layer_workspace_bytes():
 
     a = lambda n: (n + 255) // 256 * 256  # noqa: E731
     B, Hk, Hv, d = 32, 16, 32, 128
-    ch = 2 * Hk * d + Hv * d
-    assert qwen35.layer_workspace_bytes(B, Hk, Hv) == a(B * ch * 4) + 2 * a(B * Hv * 4) + a(B * Hv * d * 4)
+    # the recurrence output o[B][Hv][d] between the two launches
+    assert qwen35.layer_workspace_bytes(B, Hk, Hv) == a(B * Hv * d * 4)
+    assert qwen35.layer_workspace_bytes(3, 2, 6) == a(3 * 6 * d * 4)
     assert qwen35.layer_workspace_bytes(B, Hk, Hv, d=64) == 0
