@@ -371,10 +371,10 @@ int ouro_gdn_chunk_prefill(float *state, const void *q, const void *k,
  * [B][Hv*d], beta_raw/alpha_raw [B][Hv], dt_bias/a_log [Hv], conv_w
  * [ch][4], norm_w [d], conv_state [B][ch][3] (oldest first) and state
  * [B][Hv][d][d] updated in place, out [B][Hv*d].  d == 128; flags:
- * OURO_GDN_KHEAD_DIV, OURO_GDN_V_GROUPED.  `workspace` holds the
- * recurrence output o [B][Hv][d] between the two launches:
- * ouro_gdn_layer_workspace_bytes(B, Hk, Hv, d) bytes, 16-byte aligned, or
- * NULL for the library workspace. */
+ * OURO_GDN_KHEAD_DIV, OURO_GDN_V_GROUPED.  One launch that needs no
+ * scratch: `workspace` is ignored (pass NULL) and
+ * ouro_gdn_layer_workspace_bytes returns 0; both stay for callers written
+ * against a workspace-taking form. */
 size_t ouro_gdn_layer_workspace_bytes(size_t B, size_t Hk, size_t Hv, size_t d);
 int ouro_gdn_layer_decode(const float *qkv, const float *z, const float *beta_raw,
                           const float *alpha_raw, const float *dt_bias,

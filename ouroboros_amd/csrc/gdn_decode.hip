@@ -31,12 +31,6 @@ struct DecodeArgs {
     int B, Hk, Hv;
     unsigned flags;
     float eps;
-    // conv mode (the layer block, run_delta qwen35.rs:1066-1112): q, k, v are
-    // conv_step + SiLU of the qkv projection over the conv ring (only read
-    // here; the gated-norm kernel shifts it afterwards), and gate and beta
-    // come from the raw projections
-    const float *qkv, *ring, *conv_w, *beta_raw, *alpha_raw, *dt_bias, *a_log;
-    int ch;
 };
 
 // conv_step (qwen35.rs:64-70) of one channel, then SiLU (ops.rs:34-36), in
@@ -47,11 +41,6 @@ __device__ __forceinline__ float conv_silu(const float4 &w, float r0, float r1, 
     return y / (1.0f + expf(-y));
 }
 
-__device__ __forceinline__ float conv1(const DecodeArgs &a, int b, int c) {
-    const long long base = static_cast<long long>(b) * a.ch + c;
-    const float *r = a.ring + base * 3;
-    return conv_silu(reinterpret_cast<const float4 *>(a.conv_w)[c], r[0], r[1], r[2], a.qkv[base]);
-}
 
 template <typename T>
 __device__ __forceinline__ float4 ld4(const T *p);
@@ -100,73 +89,29 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b) {
     return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// CPW state columns per wavefront, WPB wavefronts per block; CONV: the
-// layer block's inputs (DecodeArgs).
-template <typename TQK, typename TV, int CPW, int WPB, bool CONV>
-__global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
-    static_assert(CPW == 4, "two column pairs per wavefront: one per 16-lane row of each half");
-    static_assert(!CONV || 64 * WPB >= 2 * kD + CPW * WPB, "one thread per conv channel");
-    constexpr int kPairs = CPW / 2;
-    constexpr int kSpan = 32 / kPairs;  // lanes of a half that end up holding one pair
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int half = lane >> 5;
-    const int i0 = 4 * (lane & 31);
-    const int bh = blockIdx.x;  // b * Hv + h
-    const int b = bh / a.Hv, h = bh % a.Hv;
-    const int kh = (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
-    const int col0 = (blockIdx.y * WPB + wave) * CPW;
+// One wavefront's update of state columns col0 .. col0+3 of a head (S):
+// lanes 0-31 hold rows i0 .. i0+3 of columns col0 + 2p, lanes 32-63 of
+// col0 + 2p + 1 (p = 0, 1), loaded by the caller into s.  k and q are
+// normalised; vcol(j) is v of column j.  Writes the columns back and
+// returns o of column myj (set here) in every lane of its 8-lane group.
+constexpr int kCPW = 4;   // state columns per wavefront
+constexpr int kPairs = kCPW / 2;
+constexpr int kSpan = 32 / kPairs;  // lanes of a half that end up holding one pair
 
-    float *S = a.state + static_cast<long long>(bh) * kD * kD;
-    // State columns first: they are the bytes that matter.
-    float4 s[kPairs];
+__device__ __forceinline__ void load_cols(const float *S, int col0, int lane, float4 (&s)[kPairs]) {
+    const int half = lane >> 5, i0 = 4 * (lane & 31);
 #pragma unroll
     for (int p = 0; p < kPairs; ++p) {
         const f32x4 t = __builtin_nontemporal_load(
             reinterpret_cast<const f32x4 *>(S + (col0 + 2 * p + half) * kD + i0));
         s[p] = make_float4(t[0], t[1], t[2], t[3]);
     }
+}
 
-    float4 k, q;
-    float gate, beta;
-    // conv mode: the workgroup's threads compute q and k of its k-head and v
-    // of its columns once, into LDS (channels: q at kh d, k at (Hk + kh) d,
-    // v at (2 Hk + h) d)
-    __shared__ float cv[CONV ? 2 * kD + CPW * WPB : 1];
-    if constexpr (CONV) {
-        const int t = threadIdx.x;
-        if (t < 2 * kD)
-            cv[t] = conv1(a, b, ((t >> 7) * a.Hk + kh) * kD + (t & (kD - 1)));
-        else if (t < 2 * kD + CPW * WPB)
-            cv[t] = conv1(a, b, (2 * a.Hk + h) * kD + blockIdx.y * (CPW * WPB) + t - 2 * kD);
-        __syncthreads();
-        q = *reinterpret_cast<const float4 *>(cv + i0);
-        k = *reinterpret_cast<const float4 *>(cv + kD + i0);
-        {
-#pragma clang fp contract(off)
-            beta = 1.0f / (1.0f + expf(-a.beta_raw[bh]));  // qwen35.rs:1066-1070, 1241-1243
-            const float x = a.alpha_raw[bh] + a.dt_bias[h];
-            gate = a.a_log[h] * (x > 20.0f ? x : logf(1.0f + expf(x)));
-        }
-    } else {
-        const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * kD + i0;
-        k = ld4(static_cast<const TQK *>(a.k) + qk_off);
-        q = ld4(static_cast<const TQK *>(a.q) + qk_off);
-        gate = a.gate ? a.gate[bh] : a.gate_s;
-        beta = a.beta ? a.beta[bh] : a.beta_s;
-    }
-    if (a.flags & OURO_GDN_L2NORM_QK) {  // l2_norm: 1 / (sqrt(sum) + eps)
-        const float ik = 1.0f / (sqrtf(sum_half(dot4(k, k))) + a.eps);
-        const float iq = 1.0f / (sqrtf(sum_half(dot4(q, q))) + a.eps);
-        k = make_float4(k.x * ik, k.y * ik, k.z * ik, k.w * ik);
-        q = make_float4(q.x * iq, q.y * iq, q.z * iq, q.w * iq);
-    }
-    if (a.flags & OURO_GDN_SCALE_Q) {
-        const float sc = 1.0f / sqrtf(static_cast<float>(kD));
-        q = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
-    }
-    const float decay = expf(gate);
-
+template <typename VF>
+__device__ __forceinline__ float update_cols(float *S, int col0, int lane, const float4 (&s)[kPairs], const float4 &k,
+                                             const float4 &q, float decay, float beta, VF vcol, int &myj) {
+    const int half = lane >> 5, i0 = 4 * (lane & 31);
     // sk for the column pairs: over each 32-lane half, row r of the half
     // (16 lanes) ends up holding pair r.
     float part[kPairs];
@@ -175,9 +120,8 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
     const float skj = sum_row16(sum_rows_pair(part[0], part[1])) * decay;
     // This lane now holds column pair (lane & 31) / kSpan of its half.
     const int myp = (lane & 31) / kSpan;
-    const int myj = col0 + 2 * myp + half;
-    const float vj = CONV ? cv[2 * kD + myj - blockIdx.y * (CPW * WPB)]
-                          : ld1(static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD + myj);
+    myj = col0 + 2 * myp + half;
+    const float vj = vcol(myj);
     const float dj = beta * (vj - skj);
     // dv of pair p in half hh sits in every lane of row 2*hh + p (named
     // scalars: an array indexed by the half would be placed in memory).
@@ -200,7 +144,50 @@ __global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
         __builtin_nontemporal_store(tv, reinterpret_cast<f32x4 *>(S + (col0 + 2 * p + half) * kD + i0));
         o[p] = dot4(t, q);
     }
-    const float oj = sum_row16(sum_rows_pair(o[0], o[1]));
+    return sum_row16(sum_rows_pair(o[0], o[1]));
+}
+
+// l2_norm of k and q (1 / (sqrt(sum) + eps)) and the 1/sqrt(d) scale of q,
+// per the flags, over the 32 lanes of each half (rows i0 .. i0+3 per lane).
+__device__ __forceinline__ void norm_qk(float4 &k, float4 &q, unsigned flags, float eps) {
+    if (flags & OURO_GDN_L2NORM_QK) {
+        const float ik = 1.0f / (sqrtf(sum_half(dot4(k, k))) + eps);
+        const float iq = 1.0f / (sqrtf(sum_half(dot4(q, q))) + eps);
+        k = make_float4(k.x * ik, k.y * ik, k.z * ik, k.w * ik);
+        q = make_float4(q.x * iq, q.y * iq, q.z * iq, q.w * iq);
+    }
+    if (flags & OURO_GDN_SCALE_Q) {
+        const float sc = 1.0f / sqrtf(static_cast<float>(kD));
+        q = make_float4(q.x * sc, q.y * sc, q.z * sc, q.w * sc);
+    }
+}
+
+// kCPW state columns per wavefront, WPB wavefronts per block.
+template <typename TQK, typename TV, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gdn_decode_kernel(DecodeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int i0 = 4 * (lane & 31);
+    const int bh = blockIdx.x;  // b * Hv + h
+    const int b = bh / a.Hv, h = bh % a.Hv;
+    const int kh = (a.flags & OURO_GDN_KHEAD_DIV) ? h / (a.Hv / a.Hk) : h % a.Hk;
+    const int col0 = (blockIdx.y * WPB + wave) * kCPW;
+
+    float *S = a.state + static_cast<long long>(bh) * kD * kD;
+    // State columns first: they are the bytes that matter.
+    float4 s[kPairs];
+    load_cols(S, col0, lane, s);
+
+    const long long qk_off = b * a.qk_bs + static_cast<long long>(kh) * kD + i0;
+    float4 k = ld4(static_cast<const TQK *>(a.k) + qk_off);
+    float4 q = ld4(static_cast<const TQK *>(a.q) + qk_off);
+    const float gate = a.gate ? a.gate[bh] : a.gate_s;
+    const float beta = a.beta ? a.beta[bh] : a.beta_s;
+    norm_qk(k, q, a.flags, a.eps);
+    const float decay = expf(gate);
+    const TV *v = static_cast<const TV *>(a.v) + b * a.v_bs + static_cast<long long>(h) * kD;
+    int myj;
+    const float oj = update_cols(S, col0, lane, s, k, q, decay, beta, [&](int j) { return ld1(v + j); }, myj);
     if ((lane & (kSpan - 1)) == 0) a.out[static_cast<long long>(bh) * kD + myj] = oj;
 }
 
@@ -289,44 +276,133 @@ int launch_any(const DecodeArgs &a, int d, hipStream_t s) {
 // Measured on B=32, Hv=32 with 8 rotating 64 MiB state sets: 4 columns per
 // wavefront in 8-wavefront blocks streams the state at ~91% of the in-place
 // read-modify-write rate of a plain copy-style kernel on the same bytes.
-constexpr int kCPW = 4, kWPB = 8;
+constexpr int kWPB = 8;
 
 template <typename TQK, typename TV>
 int launch(const DecodeArgs &a, int d, hipStream_t s) {
     if (d != kD) return launch_any<TQK, TV>(a, d, s);
     dim3 grid(static_cast<unsigned>(a.B * a.Hv), kD / (kCPW * kWPB));
-    hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV, kCPW, kWPB, false>), grid, dim3(64 * kWPB), 0, s, a);
+    hipLaunchKernelGGL((gdn_decode_kernel<TQK, TV, kWPB>), grid, dim3(64 * kWPB), 0, s, a);
     return check_launch("gdn_decode_kernel");
+}
+
+// ---- the whole delta-net layer block between the projections -------------
+// run_delta (qwen35.rs:1048-1151) for one decode token per sequence, in one
+// launch: one workgroup per (sequence b, k-head kh) with the g = Hv / Hk
+// v-heads that read it, so every conv channel it reads belongs to it alone.
+//   1. conv_step + SiLU (qwen35.rs:64-70, 1080-1088) of the k-head's q and k
+//      channels and of each v-head's v channels from the ring (read only),
+//      and beta, decay per v-head (qwen35.rs:1066-1070, 1241-1243), in LDS;
+//   2. the normed recurrence of every v-head (update_cols, as the decode
+//      kernel), outputs o in LDS;
+//   3. gated_norm_rms per v-head (qwen35.rs:82-92) written at its V-grouped
+//      position when asked (qwen35.rs:1122-1138);
+//   4. the ring shift of every channel read in 1.
+struct LayerArgs {
+    const float *qkv, *z, *beta_raw, *alpha_raw, *dt_bias, *a_log, *conv_w, *norm_w;
+    float *ring, *state, *out;
+    int Hk, Hv, ch;
+    unsigned flags;  // OURO_GDN_KHEAD_DIV, OURO_GDN_V_GROUPED
+    float eps;
+};
+constexpr int kLayerWaves = 16;
+
+// The conv channel of item t of the workgroup's (2 + g) * d: q, k, then v
+// of each v-head.
+__device__ __forceinline__ int layer_channel(const LayerArgs &a, int kh, int g, int t) {
+    const int blk = t / kD, i = t % kD;
+    if (blk == 0) return kh * kD + i;
+    if (blk == 1) return (a.Hk + kh) * kD + i;
+    const int j = blk - 2;
+    const int h = (a.flags & OURO_GDN_KHEAD_DIV) ? kh * g + j : kh + a.Hk * j;
+    return (2 * a.Hk + h) * kD + i;
+}
+
+__global__ __launch_bounds__(64 * kLayerWaves) void gdn_layer_kernel(LayerArgs a) {
+    extern __shared__ float lsm[];  // q[d] k[d] v[g][d] o[g][d] beta[g] decay[g]
+    const int g = a.Hv / a.Hk;
+    const int b = blockIdx.x / a.Hk, kh = blockIdx.x % a.Hk;
+    const bool div = (a.flags & OURO_GDN_KHEAD_DIV) != 0;
+    float *os = lsm + (2 + g) * kD, *bs = os + g * kD, *ds = bs + g;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int nthr = 64 * kLayerWaves;
+    const long long row = static_cast<long long>(b) * a.ch;
+
+    for (int t = tid; t < (2 + g) * kD; t += nthr) {
+        const long long c = row + layer_channel(a, kh, g, t);
+        const float *r = a.ring + c * 3;
+        lsm[t] = conv_silu(reinterpret_cast<const float4 *>(a.conv_w)[c - row], r[0], r[1], r[2], a.qkv[c]);
+    }
+    if (tid < g) {
+#pragma clang fp contract(off)
+        const int h = div ? kh * g + tid : kh + a.Hk * tid;
+        const long long bh = static_cast<long long>(b) * a.Hv + h;
+        bs[tid] = 1.0f / (1.0f + expf(-a.beta_raw[bh]));
+        const float x = a.alpha_raw[bh] + a.dt_bias[h];
+        ds[tid] = expf(a.a_log[h] * (x > 20.0f ? x : logf(1.0f + expf(x))));
+    }
+    __syncthreads();
+
+    const int i0 = 4 * (lane & 31);
+    float4 q = *reinterpret_cast<const float4 *>(lsm + i0);
+    float4 k = *reinterpret_cast<const float4 *>(lsm + kD + i0);
+    norm_qk(k, q, OURO_GDN_L2NORM_QK | OURO_GDN_SCALE_Q, a.eps);
+    for (int gi = wave; gi < g * (kD / kCPW); gi += kLayerWaves) {  // column groups of the g heads
+        const int j = gi / (kD / kCPW), col0 = gi % (kD / kCPW) * kCPW;
+        const int h = div ? kh * g + j : kh + a.Hk * j;
+        float *S = a.state + (static_cast<long long>(b) * a.Hv + h) * kD * kD;
+        float4 s[kPairs];
+        load_cols(S, col0, lane, s);
+        const float *vs = lsm + (2 + j) * kD;
+        int myj;
+        const float oj = update_cols(S, col0, lane, s, k, q, ds[j], bs[j], [&](int c) { return vs[c]; }, myj);
+        if ((lane & (kSpan - 1)) == 0) os[j * kD + myj] = oj;
+    }
+    __syncthreads();
+
+    for (int j = wave; j < g; j += kLayerWaves) {
+#pragma clang fp contract(off)
+        const int h = div ? kh * g + j : kh + a.Hk * j;
+        const long long bh = static_cast<long long>(b) * a.Hv + h;
+        const float2 x = *reinterpret_cast<const float2 *>(os + j * kD + 2 * lane);
+        float ss = x.x * x.x + x.y * x.y;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(kD) + a.eps);
+        const float2 zz = *reinterpret_cast<const float2 *>(a.z + bh * kD + 2 * lane);
+        const float2 w = *reinterpret_cast<const float2 *>(a.norm_w + 2 * lane);
+        const float g0 = zz.x / (1.0f + expf(-zz.x)), g1 = zz.y / (1.0f + expf(-zz.y));
+        const int dst = (a.flags & OURO_GDN_V_GROUPED) ? (h % a.Hk) * g + h / a.Hk : h;
+        *reinterpret_cast<float2 *>(a.out + (static_cast<long long>(b) * a.Hv + dst) * kD + 2 * lane) =
+            make_float2(x.x * inv * w.x * g0, x.y * inv * w.y * g1);
+    }
+    for (int t = tid; t < (2 + g) * kD; t += nthr) {  // the window moves by one, the new input enters last
+        const long long c = row + layer_channel(a, kh, g, t);
+        float *r = a.ring + c * 3;
+        const float r1 = r[1], r2 = r[2];
+        r[0] = r1;
+        r[1] = r2;
+        r[2] = a.qkv[c];
+    }
 }
 
 }  // namespace
 
-// The layer block's recurrence with its conv + SiLU and gates computed in
-// the decode kernel (d = 128, f32; shapes and alignment checked by the
-// caller: qkv, ring, conv_w 16-byte aligned, channels a multiple of 4).
-int gdn_decode_conv(float *state, const float *qkv, const float *ring, const float *conv_w, const float *beta_raw,
-                    const float *alpha_raw, const float *dt_bias, const float *a_log, float *out, size_t B, size_t Hk,
-                    size_t Hv, unsigned flags, float eps, void *stream) {
-    DecodeArgs a{};
-    a.state = state;
-    a.out = out;
-    a.B = static_cast<int>(B);
-    a.Hk = static_cast<int>(Hk);
-    a.Hv = static_cast<int>(Hv);
-    a.flags = flags;
-    a.eps = eps;
-    a.qkv = qkv;
-    a.ring = ring;
-    a.conv_w = conv_w;
-    a.beta_raw = beta_raw;
-    a.alpha_raw = alpha_raw;
-    a.dt_bias = dt_bias;
-    a.a_log = a_log;
-    a.ch = static_cast<int>((2 * Hk + Hv) * kD);
-    dim3 grid(static_cast<unsigned>(B * Hv), kD / (kCPW * kWPB));
-    hipLaunchKernelGGL((gdn_decode_kernel<float, float, kCPW, kWPB, true>), grid, dim3(64 * kWPB), 0, as_stream(stream),
-                       a);
-    return check_launch("gdn_decode_kernel");
+size_t gdn_layer_lds_bytes(size_t Hk, size_t Hv) { return ((2 + 2 * (Hv / Hk)) * kD + 2 * (Hv / Hk)) * 4; }
+
+// The layer block in one launch (d = 128, f32; shapes and alignment checked
+// by the caller).
+int gdn_layer_fused(const float *qkv, const float *z, const float *beta_raw, const float *alpha_raw,
+                    const float *dt_bias, const float *a_log, const float *conv_w, const float *norm_w, float *ring,
+                    float *state, float *out, size_t B, size_t Hk, size_t Hv, unsigned flags, float eps,
+                    void *stream) {
+    const LayerArgs a{qkv, z, beta_raw, alpha_raw, dt_bias, a_log, conv_w, norm_w, ring, state, out,
+                      static_cast<int>(Hk), static_cast<int>(Hv), static_cast<int>((2 * Hk + Hv) * kD), flags, eps};
+    const size_t lds = gdn_layer_lds_bytes(Hk, Hv);
+    if (lds > 64 * 1024) return fail(OURO_ERR_SHAPE, "gdn layer: %zu v-heads per k-head is too many", Hv / Hk);
+    hipLaunchKernelGGL(gdn_layer_kernel, dim3(static_cast<unsigned>(B * Hk)), dim3(64 * kLayerWaves),
+                       static_cast<unsigned>(lds), as_stream(stream), a);
+    return check_launch("gdn_layer_kernel");
 }
 
 int gdn_decode(float *state, const void *q, const void *k, int qk_dtype, const void *v, int v_dtype,

@@ -89,7 +89,7 @@ def chunk_workspace_bytes(T: int, N: int, Hv: int, d: int = S, chunk: int = 64) 
 
 
 def layer_workspace_bytes(B: int, Hk: int, Hv: int, d: int = S) -> int:
-    """Bytes of the scratch gdn_layer_decode uses (0 = unsupported shape)."""
+    """Bytes of scratch gdn_layer_decode uses: 0 (one launch, no scratch)."""
     return int(_lib.lib().ouro_gdn_layer_workspace_bytes(B, Hk, Hv, d))
 
 

@@ -30,7 +30,8 @@ def run(orc, B, Hk, Hv, flags, steps=1, seed=0, workspace=False, margin=None):
     x = inputs(rng, B, Hk, Hv)
     conv_ref, st_ref = x["conv"].copy(), x["state"].copy()
     dconv, dst = DeviceBuffer.from_host(x["conv"]), DeviceBuffer.from_host(x["state"])
-    ws = DeviceBuffer((qwen35.layer_workspace_bytes(B, Hk, Hv),), np.uint8) if workspace else None
+    # a caller workspace is accepted and ignored (the block needs none)
+    ws = DeviceBuffer((256,), np.uint8) if workspace else None
     for s in range(steps):
         if s:  # fresh token inputs for the next step, same weights
             x["qkv"], x["z"] = inputs(rng, B, Hk, Hv)["qkv"], inputs(rng, B, Hk, Hv)["z"]
