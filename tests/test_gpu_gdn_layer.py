@@ -58,6 +58,15 @@ def test_layer_block_three_steps_carry_conv_and_state(gpu, orc):
     run(orc, 2, 2, 6, GDN_V_GROUPED, steps=3, seed=11, workspace=True)
 
 
+@pytest.mark.parametrize("B,Hk,Hv,flags", [(5, 3, 3, 0), (4, 2, 8, GDN_KHEAD_DIV | GDN_V_GROUPED),
+                                           (3, 1, 8, GDN_V_GROUPED), (2, 2, 32, GDN_KHEAD_DIV)])
+def test_layer_block_heads_per_khead(gpu, orc, B, Hk, Hv, flags):
+    # one workgroup per (sequence, k-head) walks the g = Hv / Hk v-heads:
+    # g = 1, 4, 8 and 16 (more column groups than wavefronts), two steps so
+    # the ring shift of every channel is checked too
+    run(orc, B, Hk, Hv, flags, steps=2, seed=B * 100 + Hv)
+
+
 def test_layer_block_config3_shape(gpu, orc, margin):
     # B=32 sequences, Hk=16, Hv=32, d=128 (the decode workload's shape)
     run(orc, 32, 16, 32, GDN_V_GROUPED, seed=12, margin=margin)
