@@ -86,6 +86,7 @@ constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int AP = kC + 4;                         // fp32 row pitch of A / T
 constexpr int PW_BYTES = kC * AP * 4 + 4 * kC * 4; // per-wave LDS
 constexpr int PREP_LDS = kPrepWaves * PW_BYTES;
+constexpr int kPrepGrid = 512;  // prep workgroups per launch: two per CU
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -206,48 +207,74 @@ __host__ __device__ constexpr int tslot(int aa, int q) { return q == 0 ? aa : 2 
 // no LDS; Q rows are read for their norms only.  A^T goes to the wave's LDS
 // and T = (I + A)^-1 is solved in 16 x 16 blocks.
 // ---------------------------------------------------------------------------
+// Where item `item` (a (chunk, v-head) pair) lies: items of one chunk in
+// k-head order, so that the v-heads reading the same K and Q rows are
+// neighbours.
+struct PrepItem {
+    int cg, h, t0, n, kh;
+};
+__device__ __forceinline__ PrepItem prep_item(const ChunkArgs &a, int item) {
+    PrepItem p;
+    p.cg = item / a.Hv;
+    p.h = vhead(a, (item % a.Hv) / (a.Hv / a.Hk), (item % a.Hv) % (a.Hv / a.Hk));
+    int lo = 0, hi = a.nseq;  // sequence of chunk cg: coff[lo] <= cg < coff[lo + 1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (a.coff[mid] <= p.cg) lo = mid; else hi = mid;
+    }
+    p.t0 = a.cu[lo] + (p.cg - a.coff[lo]) * kC;
+    p.n = min(kC, a.cu[lo + 1] - p.t0);
+    p.kh = khead(a, p.h);
+    return p;
+}
+
+// K and Q rows 16aa + lr, columns 32kk + 8lg .. +7 of an item (rows past n
+// load row n - 1 and are zeroed when used).
+__device__ __forceinline__ void prep_load(const ChunkArgs &a, const PrepItem &p, int lr, int lg, uint4 (&kr)[4][4],
+                                          uint4 (&qr)[4][4]) {
+#pragma unroll
+    for (int aa = 0; aa < 4; ++aa) {
+        const int row = min(16 * aa + lr, p.n - 1);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const long long off = (static_cast<long long>(p.t0 + row) * a.Hk + p.kh) * kD + 32 * kk + 8 * lg;
+            kr[aa][kk] = *reinterpret_cast<const uint4 *>(a.k + off);
+            qr[aa][kk] = *reinterpret_cast<const uint4 *>(a.q + off);
+        }
+    }
+}
+
+// Each wave walks items wave, wave + waves, ...; the next item's K and Q
+// rows are loaded (into the same registers, which K K^T has finished with)
+// while the current one's T is solved and written.
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int item = blockIdx.x * kPrepWaves + wave;
+    const int stride = static_cast<int>(gridDim.x) * kPrepWaves;
+    int item = blockIdx.x * kPrepWaves + wave;
     if (item >= items) return;  // whole wave
     float *Al = reinterpret_cast<float *>(lds + wave * PW_BYTES);
     float *nk = Al + kC * AP;
     float *nq = nk + kC;
     float *gv = nq + kC;
     float *bv = gv + kC;
-
-    // items of one chunk in k-head order, so that the v-heads reading the
-    // same K and Q rows sit in the same workgroup
-    const int cg = item / a.Hv;
-    const int h = vhead(a, (item % a.Hv) / (a.Hv / a.Hk), (item % a.Hv) % (a.Hv / a.Hk));
-    int lo = 0, hi = a.nseq;  // sequence of chunk cg: coff[lo] <= cg < coff[lo + 1]
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (a.coff[mid] <= cg) lo = mid; else hi = mid;
-    }
-    const int seq = lo;
-    const int t0 = a.cu[seq] + (cg - a.coff[seq]) * kC;
-    const int n = min(kC, a.cu[seq + 1] - t0);
-    const int kh = khead(a, h);
     const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
     const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
-    unsigned char *rec = a.ws + (static_cast<size_t>(cg) * a.Hv + h) * kRec;
 
-    // K and Q rows 16aa + lr, columns 32kk + 8lg .. +7 (zero past n)
+    PrepItem cur = prep_item(a, item);
     uint4 kr[4][4], qr[4][4];
+    prep_load(a, cur, lr, lg, kr, qr);
+    for (;;) {
+    const int next = item + stride;
+    const int cg = cur.cg, h = cur.h, t0 = cur.t0, n = cur.n;
+    unsigned char *rec = a.ws + (static_cast<size_t>(cg) * a.Hv + h) * kRec;
 #pragma unroll
     for (int aa = 0; aa < 4; ++aa) {
         const int row = 16 * aa + lr;
+        if (row >= n) {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            kr[aa][kk] = qr[aa][kk] = make_uint4(0, 0, 0, 0);
-            if (row < n) {
-                const long long off = (static_cast<long long>(t0 + row) * a.Hk + kh) * kD + 32 * kk + 8 * lg;
-                kr[aa][kk] = *reinterpret_cast<const uint4 *>(a.k + off);
-                qr[aa][kk] = *reinterpret_cast<const uint4 *>(a.q + off);
-            }
+            for (int kk = 0; kk < 4; ++kk) kr[aa][kk] = qr[aa][kk] = make_uint4(0, 0, 0, 0);
         }
         float sk = sumsq32(kr[aa]), sq = sumsq32(qr[aa]);
         sk += __shfl_xor(sk, 16, 64);
@@ -314,6 +341,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         }
     }
     __builtin_amdgcn_wave_barrier();
+    // K and Q are consumed: the next item's rows load during the solve
+    PrepItem nxt{};
+    if (next < items) {
+        nxt = prep_item(a, next);
+        prep_load(a, nxt, lr, lg, kr, qr);
+    }
 
     // T = (I + A)^-1 in 16 x 16 blocks.  A sits transposed in the blocks on
     // and above the diagonal of Al (block (j, i) holds A_ij^T, i >= j); T
@@ -397,6 +430,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
                 rt[(2 * tslot(aa, q)) * 64 + lane] = __builtin_bit_cast(uint4, th);
                 rt[(2 * tslot(aa, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, tl);
             }
+    }
+    if (next >= items) break;
+    item = next;
+    cur = nxt;
+    __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -841,8 +879,11 @@ int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v,
         const int chunks = a.coff[ns];
         if (chunks == 0) continue;
         const int items = chunks * static_cast<int>(Hv);
-        hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(static_cast<unsigned>((items + kPrepWaves - 1) / kPrepWaves)),
-                           dim3(kPrepThreads), PREP_LDS, as_stream(stream), a, items);
+        // resident workgroups only (two per CU by their LDS); each wave
+        // walks items with a stride of the whole grid
+        const int wgs = std::min((items + kPrepWaves - 1) / kPrepWaves, kPrepGrid);
+        hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kPrepThreads), PREP_LDS,
+                           as_stream(stream), a, items);
         int st = check_launch("gdn_chunk_prep_kernel");
         if (st) return st;
         hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(static_cast<unsigned>(ns * Hv * 2)), dim3(kScanThreads),
