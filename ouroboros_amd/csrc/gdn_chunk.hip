@@ -23,14 +23,15 @@
 // below them on v_mfma_f32_16x16x4f32.
 //
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
-// and computes what does not depend on the state: row norms, g, T and the
-// per-row coefficients, written to a workspace record.  gdn_chunk_scan_kernel
-// then walks the chunks of a sequence in order.  Output column j of the
-// recurrence only touches state column j, so 16-column stripes of the state
-// are independent chains: a "chain" wave keeps one stripe in registers and
-// runs K S0 -> R -> U -> S update, while a paired "output" wave forms Pt
-// from the chunk's K and Q rows and O for the same stripe; two barriers per
-// chunk.
+// and computes what does not depend on the state: k-row norms, g, T and the
+// per-row coefficients, written to a workspace record (it does not read Q).
+// gdn_chunk_scan_kernel then walks the chunks of a sequence in order.
+// Output column j of the recurrence only touches state column j, so
+// 16-column stripes of the state are independent chains: a "chain" wave
+// keeps one stripe in registers and runs K S0 -> R -> U -> S update (and
+// forms the q-row norms of one row tile from the Q operands it reads),
+// while a paired "output" wave forms Pt from the chunk's K and Q rows and O
+// for the same stripe; two barriers per chunk.
 #include "common.hpp"
 
 namespace ouro {
@@ -49,16 +50,18 @@ constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free
 // Workspace record of one (chunk, v-head), 256-byte aligned:
 //   T as A operands [slot][hi, lo][64 lanes] x 16 B                  12 KiB
 //   vectors [64] fp32: beta, rk = beta e^g nk, w = nk e^(g_C - g),
-//   so = e^g nq, g, nk, nq, rho = e^(g - g_16floor(r/16)) nq and
-//   cb_b = e^(g_16b - g) nk for rows < 16b (b = 1..3)               2816 B
+//   eg = e^g, g, nk, rho = e^(g - g_16floor(r/16)) and
+//   cb_b = e^(g_16b - g) nk for rows < 16b (b = 1..3)               2560 B
+// (the q-row norms nq are formed by the scan from the Q rows it stages and
+// applied to the output rows last: O = nq (e^g Q S0 + Pt U) with nq taken
+// out of Pt)
 // T slots are (s-tile a, t-slab q) = (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
 // (T is lower triangular: slab q is zero for a < 2q); the scan's Pt slots
 // are (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
 constexpr int REC_T = 0;
 constexpr int REC_V = 12 * 64 * 16;
-enum { V_BETA = 0, V_RK = 64, V_W = 128, V_SO = 192, V_G = 256, V_NK = 320, V_NQ = 384, V_RHO = 448, V_CB = 512,
-       kVec = 704 };
-constexpr size_t kRec = 15104;
+enum { V_BETA = 0, V_RK = 64, V_W = 128, V_EG = 192, V_G = 256, V_NK = 320, V_RHO = 384, V_CB = 448, kVec = 640 };
+constexpr size_t kRec = 14848;
 static_assert(REC_V + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
 
 // Scan kernel LDS byte offsets: K, Q, V, K^T, the vectors and the T
@@ -77,14 +80,15 @@ constexpr int S_T = S_VEC + kVec * 4;       // T operands [12][64] x 16 B
 constexpr int S_P = S_T + 12 * 64 * 16;     // Pt operands [12][64] x 16 B
 constexpr int S_X = S_P + 12 * 64 * 16;     // [4 waves][(so Q S0)^T 4 KiB, U hi/lo 4 KiB]
 constexpr int X_WAVE = 8192;
-constexpr int SCAN_LDS = S_X + 4 * X_WAVE;
+constexpr int S_NQ = S_X + 4 * X_WAVE;      // nq [64] of the chunk (chain wave w: rows 16w.., read by the output waves)
+constexpr int SCAN_LDS = S_NQ + kC * 4;
 static_assert(SCAN_LDS <= 160 * 1024 && S_V % 16 == 0 && S_VEC % 16 == 0 && S_T % 16 == 0, "scan LDS layout");
 
 // Prep kernel: one wave per (chunk, v-head), four per workgroup; each wave
-// has A (then T) [64][AP] fp32 and four vectors [64] in LDS.
+// has A (then T) [64][AP] fp32 and three vectors [64] in LDS.
 constexpr int kPrepWaves = kPrepThreads / 64;
 constexpr int AP = kC + 4;                         // fp32 row pitch of A / T
-constexpr int PW_BYTES = kC * AP * 4 + 4 * kC * 4; // per-wave LDS
+constexpr int PW_BYTES = kC * AP * 4 + 3 * kC * 4; // per-wave LDS
 constexpr int PREP_LDS = kPrepWaves * PW_BYTES;
 constexpr int kPrepGrid = 512;  // prep workgroups per launch: two per CU
 
@@ -204,7 +208,7 @@ __host__ __device__ constexpr int tslot(int aa, int q) { return q == 0 ? aa : 2 
 // Prep: one wave per (chunk, v-head) item, no workgroup barriers.  K stays
 // in registers in MFMA operand layout (lane r + 16 g holds
 // K[16a + r][32kk + 8g .. +7] for row tile a and k-step kk), so K K^T needs
-// no LDS; Q rows are read for their norms only.  A^T goes to the wave's LDS
+// no LDS; Q is not read (the scan forms the q-row norms).  A^T goes to the wave's LDS
 // and T = (I + A)^-1 is solved in 16 x 16 blocks.
 // ---------------------------------------------------------------------------
 // Where item `item` (a (chunk, v-head) pair) lies: items of one chunk in
@@ -228,10 +232,9 @@ __device__ __forceinline__ PrepItem prep_item(const ChunkArgs &a, int item) {
     return p;
 }
 
-// K and Q rows 16aa + lr, columns 32kk + 8lg .. +7 of an item (rows past n
-// load row n - 1 and are zeroed when used).
-__device__ __forceinline__ void prep_load(const ChunkArgs &a, const PrepItem &p, int lr, int lg, uint4 (&kr)[4][4],
-                                          uint4 (&qr)[4][4]) {
+// K rows 16aa + lr, columns 32kk + 8lg .. +7 of an item (rows past n load
+// row n - 1 and are zeroed when used).
+__device__ __forceinline__ void prep_load(const ChunkArgs &a, const PrepItem &p, int lr, int lg, uint4 (&kr)[4][4]) {
 #pragma unroll
     for (int aa = 0; aa < 4; ++aa) {
         const int row = min(16 * aa + lr, p.n - 1);
@@ -239,14 +242,13 @@ __device__ __forceinline__ void prep_load(const ChunkArgs &a, const PrepItem &p,
         for (int kk = 0; kk < 4; ++kk) {
             const long long off = (static_cast<long long>(p.t0 + row) * a.Hk + p.kh) * kD + 32 * kk + 8 * lg;
             kr[aa][kk] = *reinterpret_cast<const uint4 *>(a.k + off);
-            qr[aa][kk] = *reinterpret_cast<const uint4 *>(a.q + off);
         }
     }
 }
 
-// Each wave walks items wave, wave + waves, ...; the next item's K and Q
-// rows are loaded (into the same registers, which K K^T has finished with)
-// while the current one's T is solved and written.
+// Each wave walks items wave, wave + waves, ...; the next item's K rows are
+// loaded (into the same registers, which K K^T has finished with) while the
+// current one's T is solved and written.
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -256,15 +258,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     if (item >= items) return;  // whole wave
     float *Al = reinterpret_cast<float *>(lds + wave * PW_BYTES);
     float *nk = Al + kC * AP;
-    float *nq = nk + kC;
-    float *gv = nq + kC;
+    float *gv = nk + kC;
     float *bv = gv + kC;
     const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
-    const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
 
     PrepItem cur = prep_item(a, item);
-    uint4 kr[4][4], qr[4][4];
-    prep_load(a, cur, lr, lg, kr, qr);
+    uint4 kr[4][4];
+    prep_load(a, cur, lr, lg, kr);
     for (;;) {
     const int next = item + stride;
     const int cg = cur.cg, h = cur.h, t0 = cur.t0, n = cur.n;
@@ -274,17 +274,12 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         const int row = 16 * aa + lr;
         if (row >= n) {
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) kr[aa][kk] = qr[aa][kk] = make_uint4(0, 0, 0, 0);
+            for (int kk = 0; kk < 4; ++kk) kr[aa][kk] = make_uint4(0, 0, 0, 0);
         }
-        float sk = sumsq32(kr[aa]), sq = sumsq32(qr[aa]);
+        float sk = sumsq32(kr[aa]);
         sk += __shfl_xor(sk, 16, 64);
         sk += __shfl_xor(sk, 32, 64);
-        sq += __shfl_xor(sq, 16, 64);
-        sq += __shfl_xor(sq, 32, 64);
-        if (lg == 0) {
-            nk[row] = row < n ? (l2 ? 1.0f / (sqrtf(sk) + a.eps) : 1.0f) : 0.f;
-            nq[row] = row < n ? (l2 ? 1.0f / (sqrtf(sq) + a.eps) : 1.0f) * qscale : 0.f;
-        }
+        if (lg == 0) nk[row] = row < n ? (l2 ? 1.0f / (sqrtf(sk) + a.eps) : 1.0f) : 0.f;
     }
     {  // inclusive scan of the log-decays, one token per lane
         float g = lane < n ? a.gate[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
@@ -297,20 +292,19 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
     }
     __builtin_amdgcn_wave_barrier();
-    {  // per-row coefficients, row = lane (zero past n: nk = nq = beta = 0)
+    {  // per-row coefficients, row = lane (zero past n: nk = beta = 0)
         float *rv = reinterpret_cast<float *>(rec + REC_V);
-        const float g = gv[lane], b = bv[lane], kn = nk[lane], qn = nq[lane];
+        const float g = gv[lane], b = bv[lane], kn = nk[lane];
         const float gC = gv[n - 1], eg = __expf(g);
         rv[V_BETA + lane] = b;
         rv[V_RK + lane] = b * eg * kn;
         rv[V_W + lane] = kn * __expf(gC - g);
-        rv[V_SO + lane] = eg * qn;
+        rv[V_EG + lane] = eg;
         rv[V_G + lane] = g;
         rv[V_NK + lane] = kn;
-        rv[V_NQ + lane] = qn;
         // Pt's decay e^(g_r - g_s) as e^(g_r - g_16b) e^(g_16b - g_s) off the
         // diagonal tiles (both factors <= 1)
-        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]) * qn;
+        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]);
 #pragma unroll
         for (int bb = 1; bb < 4; ++bb) rv[V_CB + 64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
     }
@@ -341,11 +335,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         }
     }
     __builtin_amdgcn_wave_barrier();
-    // K and Q are consumed: the next item's rows load during the solve
+    // K is consumed: the next item's rows load during the solve
     PrepItem nxt{};
     if (next < items) {
         nxt = prep_item(a, next);
-        prep_load(a, nxt, lr, lg, kr, qr);
+        prep_load(a, nxt, lr, lg, kr);
     }
 
     // T = (I + A)^-1 in 16 x 16 blocks.  A sits transposed in the blocks on
@@ -540,14 +534,15 @@ __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds
 }
 
 // Pt slot (r-tile bb, s-slab q) of the chunk in LDS: the P^T tiles
-// (s-tile aa = 2q, 2q + 1) = K Q^T scaled by e^(g_r - g_s) nq_r nk_s for
-// s <= r, as hi/lo A operands of Pt U (lane r + 16 g: row 16 bb + r).
+// (s-tile aa = 2q, 2q + 1) = K Q^T scaled by e^(g_r - g_s) nk_s for s <= r
+// (nq_r is applied to the output rows), as hi/lo A operands of Pt U (lane
+// r + 16 g: row 16 bb + r).
 __device__ __forceinline__ void pt_slot(unsigned char *lds, int bb, int q, int lane, int lr, int lg) {
     const uint16_t *K = reinterpret_cast<const uint16_t *>(lds + S_K);
     const uint16_t *Q = reinterpret_cast<const uint16_t *>(lds + S_Q);
     const float *cv = reinterpret_cast<const float *>(lds + S_VEC);
     const int r = 16 * bb + lr;
-    const float rr = cv[V_RHO + r], gr = cv[V_G + r], nqr = cv[V_NQ + r];
+    const float rr = cv[V_RHO + r], gr = cv[V_G + r];
     f32x4 ps[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -557,7 +552,7 @@ __device__ __forceinline__ void pt_slot(unsigned char *lds, int bb, int q, int l
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
             ps[t] = mfma(ld_op(K + (16 * aa + lr) * KP, 32 * kk, lg), ld_op(Q + r * KP, 32 * kk, lg), ps[t]);
-        if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) nq_r * e^(g_16b - g_s) nk_s
+        if (aa < bb) {  // s < 16 bb <= r: e^(g_r - g_16b) * e^(g_16b - g_s) nk_s
             const f32x4 c4 = ld4(cv + V_CB + 64 * (bb - 1) + 16 * aa + 4 * lg);
 #pragma unroll
             for (int e = 0; e < 4; ++e) ps[t][e] *= rr * c4[e];
@@ -567,7 +562,7 @@ __device__ __forceinline__ void pt_slot(unsigned char *lds, int bb, int q, int l
             for (int e = 0; e < 4; ++e) {
                 const int sr = 16 * aa + 4 * lg + e;
                 const float ev = __expf(sr <= r ? gr - gs[e] : 0.f);
-                ps[t][e] = sr <= r ? ev * nqr * kn[e] * ps[t][e] : 0.f;
+                ps[t][e] = sr <= r ? ev * kn[e] * ps[t][e] : 0.f;
             }
         }
     }
@@ -635,6 +630,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
             // ---- first half: KS and (Q S0)^T, R, U -> X, U~ -----------------
             const float bC = __expf(cv[V_G + n - 1]);
             f32x4 ks[4], rr[4], ot[4];
+            float qss = 0.f;  // sum of squares of the lane's Q values of row 16 wave + r
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) ks[aa] = ot[aa] = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -649,16 +645,38 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ka[bb] = ld_op(Q + (16 * bb + lr) * KP, 32 * q, lg);
 #pragma unroll
+                for (int bb = 0; bb < 4; ++bb) {
+                    if (bb != wave) continue;  // chain wave w forms the norms of row tile w
+                    const uint4 w = __builtin_bit_cast(uint4, ka[bb]);
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = __uint_as_float(ws[e] << 16), x1 = __uint_as_float(ws[e] & 0xffff0000u);
+                        qss += x0 * x0 + x1 * x1;
+                    }
+                }
+#pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sh[q], ka[bb], ot[bb]);
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sl[q], ka[bb], ot[bb]);
             }
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {  // ot[bb][e] = (Q S0)[16 bb + r][jw + 4 g + e], scaled by so of row 16 bb + r
-                const float so = cv[V_SO + 16 * bb + lr];
+            for (int bb = 0; bb < 4; ++bb) {  // ot[bb][e] = (Q S0)[16 bb + r][jw + 4 g + e], scaled by e^g of row 16 bb + r
+                const float eg = cv[V_EG + 16 * bb + lr];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) ot[bb][e] *= so;
+                for (int e = 0; e < 4; ++e) ot[bb][e] *= eg;
                 X[bb * 64 + lane] = __builtin_bit_cast(uint4, ot[bb]);
+            }
+            {  // nq of row 16 wave + r: l2_norm and the 1/sqrt(d) scale (qwen35.rs:73-79, 1103-1107)
+                const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
+                const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
+                float sq = qss;
+                sq += __shfl_xor(sq, 16, 64);
+                sq += __shfl_xor(sq, 32, 64);
+                const int row = 16 * wave + lr;
+                if (lg == 0)
+                    reinterpret_cast<float *>(lds + S_NQ)[row] =
+                        row < n ? (l2 ? 1.0f / (sqrtf(sq) + a.eps) : 1.0f) * qscale : 0.f;
             }
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) {
@@ -788,11 +806,15 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                         }
                     }
                 }
-                // ot[bb][e] = O[16 bb + r][jw + 4 g + e]
+                // ot[bb][e] = O[16 bb + r][jw + 4 g + e] / nq_r
                 float *obc = ob + static_cast<long long>(t0) * os;
+                const float *nqs = reinterpret_cast<const float *>(lds + S_NQ);
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) {
                     const int row = 16 * bb + lr;
+                    const float nq = nqs[row];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ot[bb][e] *= nq;
                     if (row < n) *reinterpret_cast<f32x4 *>(obc + row * os) = ot[bb];
                 }
             }
