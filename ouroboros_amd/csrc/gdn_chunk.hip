@@ -630,7 +630,6 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
             // ---- first half: KS and (Q S0)^T, R, U -> X, U~ -----------------
             const float bC = __expf(cv[V_G + n - 1]);
             f32x4 ks[4], rr[4], ot[4];
-            float qss = 0.f;  // sum of squares of the lane's Q values of row 16 wave + r
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) ks[aa] = ot[aa] = f32x4{0, 0, 0, 0};
 #pragma unroll
@@ -645,17 +644,6 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ka[bb] = ld_op(Q + (16 * bb + lr) * KP, 32 * q, lg);
 #pragma unroll
-                for (int bb = 0; bb < 4; ++bb) {
-                    if (bb != wave) continue;  // chain wave w forms the norms of row tile w
-                    const uint4 w = __builtin_bit_cast(uint4, ka[bb]);
-                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float x0 = __uint_as_float(ws[e] << 16), x1 = __uint_as_float(ws[e] & 0xffff0000u);
-                        qss += x0 * x0 + x1 * x1;
-                    }
-                }
-#pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sh[q], ka[bb], ot[bb]);
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) ot[bb] = mfma(sl[q], ka[bb], ot[bb]);
@@ -666,17 +654,6 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
 #pragma unroll
                 for (int e = 0; e < 4; ++e) ot[bb][e] *= eg;
                 X[bb * 64 + lane] = __builtin_bit_cast(uint4, ot[bb]);
-            }
-            {  // nq of row 16 wave + r: l2_norm and the 1/sqrt(d) scale (qwen35.rs:73-79, 1103-1107)
-                const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
-                const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
-                float sq = qss;
-                sq += __shfl_xor(sq, 16, 64);
-                sq += __shfl_xor(sq, 32, 64);
-                const int row = 16 * wave + lr;
-                if (lg == 0)
-                    reinterpret_cast<float *>(lds + S_NQ)[row] =
-                        row < n ? (l2 ? 1.0f / (sqrtf(sq) + a.eps) : 1.0f) * qscale : 0.f;
             }
 #pragma unroll
             for (int aa = 0; aa < 4; ++aa) {
@@ -719,6 +696,29 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                     w1[e] *= c1[e];
                 }
                 split8(w0, w1, wh[q], wl[q]);
+            }
+            {  // nq of row 16 wave + r: l2_norm and the 1/sqrt(d) scale (qwen35.rs:73-79, 1103-1107),
+               // from the row's Q operands read once more (after the chain's products, where the
+               // chain waits for the output waves anyway)
+                const bool l2 = (a.flags & OURO_GDN_L2NORM_QK) != 0;
+                const float qscale = (a.flags & OURO_GDN_SCALE_Q) ? 1.0f / sqrtf(static_cast<float>(kD)) : 1.0f;
+                float sq = 0.f;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint4 w = __builtin_bit_cast(uint4, ld_op(Q + (16 * wave + lr) * KP, 32 * kk, lg));
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = __uint_as_float(ws[e] << 16), x1 = __uint_as_float(ws[e] & 0xffff0000u);
+                        sq += x0 * x0 + x1 * x1;
+                    }
+                }
+                sq += __shfl_xor(sq, 16, 64);
+                sq += __shfl_xor(sq, 32, 64);
+                const int row = 16 * wave + lr;
+                if (lg == 0)
+                    reinterpret_cast<float *>(lds + S_NQ)[row] =
+                        row < n ? (l2 ? 1.0f / (sqrtf(sq) + a.eps) : 1.0f) * qscale : 0.f;
             }
 
             __syncthreads();  // X holds (Q S0)^T and U of chunk c; K, Q, V, T may be refilled
