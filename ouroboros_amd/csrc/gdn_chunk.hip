@@ -438,22 +438,31 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
 // registers and runs the recurrence for them: K S0 and (beside it, on the
 // same B operands) Q S0, R, U = T R, and S = b_C S0 + K^T U~, every
 // contraction an MFMA whose operands are its own accumulators or chunk rows
-// in LDS.  Output wave 4 + w finishes O of the same chunk for the same
-// stripe: in the first half it forms its share of the Pt operands from the
-// K and Q rows in LDS; in the second half it takes so (Q S0) and U
-// from chain wave w (through LDS), adds Pt U, stores O and stages the next
-// chunk's K, K^T, Q, V, vectors and T operands, whose loads it issued at the
-// start of the chunk.  O is formed transposed (O^T = S0^T Q^T + U^T Pt^T,
+// in LDS; after the state update it stages the next chunk's K and K^T,
+// whose loads it issued at the start of the chunk.  Output wave 4 + w
+// finishes O of the same chunk for the same stripe: in the first half it
+// forms its share of the Pt operands from the K and Q rows in LDS; in the
+// second half it takes so (Q S0) and U from chain wave w (through LDS),
+// adds Pt U, stores O and stages the next chunk's Q, V, vectors and T
+// operands (loads also issued at the start of the chunk).  Staging K and
+// K^T on the chain waves, whose second half is the shorter one, took a
+// 4 x 4096-token call from 0.299 to 0.291 ms; Q as well was slower
+// (0.350 ms).  O is formed transposed (O^T = S0^T Q^T + U^T Pt^T,
 // the same operands with A and B swapped), so a lane holds four adjacent
 // columns of a row and stores them as one 16-byte write.
 // ---------------------------------------------------------------------------
 
-// Output-wave loads of the next chunk.  Output thread to, item it (0, 1):
-// id = to + 256 it covers K rows 2p, 2p+1 (p = id % 32) and bf16 columns
-// 8c .. 8c+7 (c = id / 32); V item i is row id / 8, columns 8 (id % 8) ..
-// of the workgroup's 64.
+// Loads of the next chunk.  The chain waves stage K and K^T (their second
+// half is short), the output waves Q, V, the vectors and the T operands.
+// Thread to (0..255 within its role), item it (0, 1): id = to + 256 it
+// covers K rows 2p, 2p+1 (p = id % 32) and bf16 columns 8c .. 8c+7
+// (c = id / 32); V item i is row id / 8, columns 8 (id % 8) .. of the
+// workgroup's 64.
 struct NextRegs {
-    uint4 k[2][2], q[4], vec, t[3], v[2];
+    uint4 q[4], vec, t[3], v[2];
+};
+struct NextK {
+    uint4 k[2][2];
 };
 
 // base + a 32-bit byte offset (lets the loads use a uniform base address)
@@ -472,19 +481,12 @@ __device__ __forceinline__ uint4 zero_if(bool z, uint4 v) {
 __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int to, int t0, int n, int kh, int h,
                                           int jb, const unsigned char *rec) {
     // uniform chunk bases, 32-bit lane offsets
-    const uint16_t *kb = a.k + (static_cast<long long>(t0) * a.Hk + kh) * kD;
     const uint16_t *qb = a.q + (static_cast<long long>(t0) * a.Hk + kh) * kD;
     const uint16_t *vb = a.v + (static_cast<long long>(t0) * a.Hv + h) * kD + jb;
     const unsigned ks = static_cast<unsigned>(a.Hk) * kD, vs = static_cast<unsigned>(a.Hv) * kD;
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = to + 256 * it;
-        const int p = id & 31, c = id >> 5;
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const unsigned row = static_cast<unsigned>(min(2 * p + w, n - 1));
-            r.k[it][w] = at<uint4>(kb, 2u * (row * ks + 8u * c));
-        }
         const unsigned vrow = static_cast<unsigned>(min(id >> 3, n - 1));
         r.v[it] = at<uint4>(vb, 2u * (vrow * vs + 8u * (id & 7)));
     }
@@ -499,13 +501,28 @@ __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int t
     for (int i = 0; i < 3; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec + REC_T)[to + 256 * i];
 }
 
-// Stage the next chunk's K, K^T (into buffer buf), Q, V, vectors and T
-// operands.
-__device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds, int buf, int to, int n) {
+// The next chunk's K rows (chain waves).
+__device__ __forceinline__ void load_next_k(const ChunkArgs &a, NextK &r, int to, int t0, int n, int kh) {
+    const uint16_t *kb = a.k + (static_cast<long long>(t0) * a.Hk + kh) * kD;
+    const unsigned ks = static_cast<unsigned>(a.Hk) * kD;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int id = to + 256 * it;
+        const int p = id & 31, c = id >> 5;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const unsigned row = static_cast<unsigned>(min(2 * p + w, n - 1));
+            r.k[it][w] = at<uint4>(kb, 2u * (row * ks + 8u * c));
+        }
+    }
+}
+
+// Stage the next chunk's K and K^T (into buffer buf); nothing reads K in
+// a chunk's second half, and K^T buffer buf is the one the current chunk
+// does not use.
+__device__ __forceinline__ void store_next_k(const NextK &r, unsigned char *lds, int buf, int to, int n) {
     uint16_t *K = reinterpret_cast<uint16_t *>(lds + S_K);
     uint32_t *KT = reinterpret_cast<uint32_t *>(lds + S_KT + buf * kD * KTP * 2);
-    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q);
-    uint16_t *V = reinterpret_cast<uint16_t *>(lds + S_V);
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int id = to + 256 * it;
@@ -521,6 +538,16 @@ __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds
             KT[((8 * c + 2 * e) * KTP + 2 * p) >> 1] = (x0[e] & 0xffffu) | (x1[e] << 16);
             KT[((8 * c + 2 * e + 1) * KTP + 2 * p) >> 1] = (x0[e] >> 16) | (x1[e] & 0xffff0000u);
         }
+    }
+}
+
+// Stage the next chunk's Q, V, vectors and T operands (output waves).
+__device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds, int to, int n) {
+    uint16_t *Q = reinterpret_cast<uint16_t *>(lds + S_Q);
+    uint16_t *V = reinterpret_cast<uint16_t *>(lds + S_V);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int id = to + 256 * it;
         *reinterpret_cast<uint4 *>(V + (id >> 3) * VP + 8 * (id & 7)) = zero_if((id >> 3) >= n, r.v[it]);
     }
 #pragma unroll
@@ -621,11 +648,19 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
         for (int q = 0; q < 4; ++q) split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
         const uint16_t *Vl = reinterpret_cast<const uint16_t *>(lds + S_V) + 16 * (wave & 3) + lr;
         const uint4 *Tl = reinterpret_cast<const uint4 *>(lds + S_T);  // [slot][lane]
+        NextK nk;
+        {
+            const int n0 = min(kC, t_end - t_begin);
+            load_next_k(a, nk, tr, t_begin, n0, kh);
+            store_next_k(nk, lds, 0, tr, n0);
+        }
 
         for (int c = 0; c < nchunks; ++c) {
             const int n = min(kC, t_end - t_begin - c * kC);
             const bool more = c + 1 < nchunks;
+            const int n1 = more ? min(kC, t_end - t_begin - (c + 1) * kC) : 0;
             __syncthreads();  // chunk c staged (K, Q, V, vectors, T); X is free
+            if (more) load_next_k(a, nk, tr, t_begin + (c + 1) * kC, n1, kh);
 
             // ---- first half: KS and (Q S0)^T, R, U -> X, U~ -----------------
             const float bC = __expf(cv[V_G + n - 1]);
@@ -738,6 +773,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                 for (int t = 0; t < 8; ++t) st[t] = mfma(kt[t], wl[q], st[t]);
             }
             if (more) {
+                store_next_k(nk, lds, (c + 1) & 1, tr, n1);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) split8(st[2 * q], st[2 * q + 1], sh[q], sl[q]);
             }
@@ -750,7 +786,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
         {
             const int n0 = min(kC, t_end - t_begin);
             load_next(a, nx, tr, t_begin, n0, kh, h, jb, record(0));
-            store_next(nx, lds, 0, tr, n0);
+            store_next(nx, lds, tr, n0);
         }
         float *ob = a.out + static_cast<long long>(h) * kD + jw + 4 * lg;
         const long long os = static_cast<long long>(a.Hv) * kD;
@@ -818,7 +854,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
                     if (row < n) *reinterpret_cast<f32x4 *>(obc + row * os) = ot[bb];
                 }
             }
-            if (more) store_next(nx, lds, (c + 1) & 1, tr, n1);
+            if (more) store_next(nx, lds, tr, n1);
         }
     }
 }
