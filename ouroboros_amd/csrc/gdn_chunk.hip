@@ -47,22 +47,36 @@ constexpr int kMaxSeq = 256;      // sequences per launch (offsets by value)
 constexpr int KP = kD + 8;        // bf16 row pitch of K, Q (272 B)
 constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free 8-byte reads)
 
-// Workspace record of one (chunk, v-head), 256-byte aligned:
-//   T as A operands [slot][hi, lo][64 lanes] x 16 B                  12 KiB
-//   vectors [64] fp32: beta, rk = beta e^g nk, w = nk e^(g_C - g),
-//   eg = e^g, g, nk, rho = e^(g - g_16floor(r/16)) and
-//   cb_b = e^(g_16b - g) nk for rows < 16b (b = 1..3)               2560 B
-// (the q-row norms nq are formed by the scan from the Q rows it stages and
-// applied to the output rows last: O = nq (e^g Q S0 + Pt U) with nq taken
-// out of Pt)
 // T slots are (s-tile a, t-slab q) = (0,0) (1,0) (2,0) (3,0) (2,1) (3,1)
 // (T is lower triangular: slab q is zero for a < 2q); the scan's Pt slots
-// are (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).
+// are (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).  A slot
+// is an A operand: lane r + 16 g holds T[16a + r][32q + 4g .. +3] ++
+// T[16a + r][32q + 16 + 4g .. +3], as hi and lo bf16.  In slots (0,0) and
+// (2,1) the second half lies in a block above the diagonal and is zero.
+//
+// Workspace record of one (chunk, v-head), 256-byte aligned, 11,008 B:
+//   the full T slots (1,0) (2,0) (3,0) (3,1) as [slot][hi, lo][64 lanes]
+//   x 16 B, then the half slots (0,0) (2,1) as [slot][64 lanes] x 16 B
+//   holding the non-zero halves (hi.xy, lo.xy)                      10 KiB
+//   beta, g (inclusive cumsum of the log-decays), nk [64] fp32        768 B
+// The scan forms the other per-row coefficients from these while it
+// stages them (LDS vectors below), and the q-row norms nq from the Q rows
+// it stages; nq is applied to the output rows last: O = nq (e^g Q S0 +
+// Pt U) with nq taken out of Pt.
 constexpr int REC_T = 0;
-constexpr int REC_V = 12 * 64 * 16;
+constexpr int REC_HALF = 8 * 64 * 16;  // the half slots
+constexpr int REC_V = 10 * 64 * 16;
+enum { R_BETA = 0, R_G = 64, R_NK = 128, kRecVec = 192 };
+constexpr size_t kRec = 11008;
+static_assert(REC_V + kRecVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
+// T slot of full record slot j and of half record slot k.
+__host__ __device__ constexpr int full_tslot(int j) { return j < 3 ? j + 1 : 5; }
+__host__ __device__ constexpr int half_tslot(int k) { return k == 0 ? 0 : 4; }
+
+// The scan's LDS vectors [64] fp32 of a chunk: beta, rk = beta e^g nk,
+// w = nk e^(g_C - g), eg = e^g, g, nk, rho = e^(g - g_16floor(r/16)) and
+// cb_b = e^(g_16b - g) nk for rows < 16b (b = 1..3).
 enum { V_BETA = 0, V_RK = 64, V_W = 128, V_EG = 192, V_G = 256, V_NK = 320, V_RHO = 384, V_CB = 448, kVec = 640 };
-constexpr size_t kRec = 14848;
-static_assert(REC_V + kVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
 
 // Scan kernel LDS byte offsets: K, Q, V, K^T, the vectors and the T
 // operands of chunk c are staged in the second half of chunk c - 1 and read
@@ -292,21 +306,11 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         bv[lane] = lane < n ? a.beta[static_cast<long long>(t0 + lane) * a.Hv + h] : 0.f;
     }
     __builtin_amdgcn_wave_barrier();
-    {  // per-row coefficients, row = lane (zero past n: nk = beta = 0)
+    {  // per-row beta, g, nk, row = lane (zero past n: nk = beta = 0; g stays at g_{n-1})
         float *rv = reinterpret_cast<float *>(rec + REC_V);
-        const float g = gv[lane], b = bv[lane], kn = nk[lane];
-        const float gC = gv[n - 1], eg = __expf(g);
-        rv[V_BETA + lane] = b;
-        rv[V_RK + lane] = b * eg * kn;
-        rv[V_W + lane] = kn * __expf(gC - g);
-        rv[V_EG + lane] = eg;
-        rv[V_G + lane] = g;
-        rv[V_NK + lane] = kn;
-        // Pt's decay e^(g_r - g_s) as e^(g_r - g_16b) e^(g_16b - g_s) off the
-        // diagonal tiles (both factors <= 1)
-        rv[V_RHO + lane] = __expf(g - gv[lane & ~15]);
-#pragma unroll
-        for (int bb = 1; bb < 4; ++bb) rv[V_CB + 64 * (bb - 1) + lane] = lane < 16 * bb ? __expf(gv[16 * bb] - g) * kn : 0.f;
+        rv[R_BETA + lane] = bv[lane];
+        rv[R_G + lane] = gv[lane];
+        rv[R_NK + lane] = nk[lane];
     }
 
     // A[r][c] = beta_r exp(g_r - g_c) nk_r nk_c (K K^T)[r][c], c < r, stored
@@ -368,10 +372,13 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
         for (int s2 = 0; s2 < 16; ++s2) Al[(16 * lg + s2) * AP + 16 * lg + lr] = t[s2];
         __builtin_amdgcn_wave_barrier();
     }
-    // T_ij = -T_ii (sum over k = j .. i-1 of A_ik T_kj) on fp32 MFMA: the sum
-    // goes through block (i, j), which the second product then overwrites
-    // (D lane l, register e: row 4 (l / 16) + e, column l % 16)
-    auto offdiag = [&](int i, int j) {
+    // T_ij = -T_ii (sum over k = j .. i-1 of A_ik T_kj) on fp32 MFMA, level
+    // by level (i - j = 1, 2, 3; the blocks of a level are independent, so
+    // their products interleave and a level ends with one barrier).  The sum
+    // Y in D layout (lane l, register e: row 4 (l / 16) + e, column l % 16)
+    // is the B operand of the second product as it stands, with the k index
+    // of step e taken as 4 (l / 16) + e.
+    auto offdiag_y = [&](int i, int j) {
         f32x4 y = {0.f, 0.f, 0.f, 0.f};
         for (int k = j; k < i; ++k)
 #pragma unroll
@@ -380,38 +387,40 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
                 y = __builtin_amdgcn_mfma_f32_16x16x4f32(Al[kk * AP + 16 * i + lr], Al[kk * AP + 16 * j + lr], y, 0, 0,
                                                          0);
             }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) Al[(16 * i + 4 * lg + e) * AP + 16 * j + lr] = y[e];
-        __builtin_amdgcn_wave_barrier();
+        return y;
+    };
+    auto offdiag_x = [&](int i, const f32x4 &y) {  // T_ii Y
         f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            const int kk = 4 * s4 + lg;  // T_ii[lr][kk] Y[kk][lr]
-            x = __builtin_amdgcn_mfma_f32_16x16x4f32(Al[(16 * i + lr) * AP + 16 * i + kk],
-                                                     Al[(16 * i + kk) * AP + 16 * j + lr], x, 0, 0, 0);
-        }
-        __builtin_amdgcn_wave_barrier();
+        for (int e = 0; e < 4; ++e)
+            x = __builtin_amdgcn_mfma_f32_16x16x4f32(Al[(16 * i + lr) * AP + 16 * i + 4 * lg + e], y[e], x, 0, 0, 0);
+        return x;
+    };
+    auto put = [&](int i, int j, const f32x4 &x) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) Al[(16 * i + 4 * lg + e) * AP + 16 * j + lr] = -x[e];
-        __builtin_amdgcn_wave_barrier();
     };
-    offdiag(1, 0);
-    offdiag(2, 1);
-    offdiag(3, 2);
-    offdiag(2, 0);
-    offdiag(3, 1);
-    offdiag(3, 0);
-    // the T operands below also read blocks (0, 1) and (2, 3) above the
-    // diagonal (A_10^T and A_32^T until now): T is zero there
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        Al[(4 * lg + e) * AP + 16 + lr] = 0.f;
-        Al[(32 + 4 * lg + e) * AP + 48 + lr] = 0.f;
+    {
+        const f32x4 y10 = offdiag_y(1, 0), y21 = offdiag_y(2, 1), y32 = offdiag_y(3, 2);
+        const f32x4 x10 = offdiag_x(1, y10), x21 = offdiag_x(2, y21), x32 = offdiag_x(3, y32);
+        put(1, 0, x10);
+        put(2, 1, x21);
+        put(3, 2, x32);
+        __builtin_amdgcn_wave_barrier();
     }
+    {
+        const f32x4 y20 = offdiag_y(2, 0), y31 = offdiag_y(3, 1);
+        const f32x4 x20 = offdiag_x(2, y20), x31 = offdiag_x(3, y31);
+        put(2, 0, x20);
+        put(3, 1, x31);
+        __builtin_amdgcn_wave_barrier();
+    }
+    put(3, 0, offdiag_x(3, offdiag_y(3, 0)));
     __builtin_amdgcn_wave_barrier();
 
     // T operands: slot (aa, q) of lane (lr, lg) is T[16aa + lr][32q + 4lg .. +3]
-    // ++ T[16aa + lr][32q + 16 + 4lg .. +3], split hi/lo
+    // ++ T[16aa + lr][32q + 16 + 4lg .. +3], split hi/lo; slots (0,0) and
+    // (2,1) (aa = 2q) keep only their first half
     {
         uint4 *rt = reinterpret_cast<uint4 *>(rec + REC_T);
 #pragma unroll
@@ -419,10 +428,16 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
 #pragma unroll
             for (int aa = 2 * q; aa < 4; ++aa) {
                 const float *row = Al + (16 * aa + lr) * AP + 32 * q + 4 * lg;
-                bf16x8 th, tl;
-                split8(ld4(row), ld4(row + 16), th, tl);
-                rt[(2 * tslot(aa, q)) * 64 + lane] = __builtin_bit_cast(uint4, th);
-                rt[(2 * tslot(aa, q) + 1) * 64 + lane] = __builtin_bit_cast(uint4, tl);
+                bf16x8 th, tl;  // the second half of slots (0,0), (2,1) lies above the diagonal: zero
+                split8(ld4(row), aa == 2 * q ? f32x4{0.f, 0.f, 0.f, 0.f} : ld4(row + 16), th, tl);
+                const uint4 h = __builtin_bit_cast(uint4, th), l = __builtin_bit_cast(uint4, tl);
+                if (aa == 2 * q) {
+                    rt[REC_HALF / 16 + q * 64 + lane] = make_uint4(h.x, h.y, l.x, l.y);
+                } else {
+                    const int j = q == 0 ? aa - 1 : 3;
+                    rt[(2 * j) * 64 + lane] = h;
+                    rt[(2 * j + 1) * 64 + lane] = l;
+                }
             }
     }
     if (next >= items) break;
@@ -459,7 +474,8 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
 // (c = id / 32); V item i is row id / 8, columns 8 (id % 8) .. of the
 // workgroup's 64.
 struct NextRegs {
-    uint4 q[4], vec, t[3], v[2];
+    uint4 q[4], t[3], v[2];
+    float vec[8];  // threads 0..63: row's beta, g, nk; g_{n-1}, g_16floor(r/16), g_16, g_32, g_48
 };
 struct NextK {
     uint4 k[2][2];
@@ -496,9 +512,21 @@ __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int t
         const unsigned row = static_cast<unsigned>(min(idx >> 4, n - 1));
         r.q[i] = at<uint4>(qb, 2u * (row * ks + 8u * (idx & 15)));
     }
-    r.vec = reinterpret_cast<const uint4 *>(rec + REC_V)[min(to, kVec / 4 - 1)];
+    {
+        const float *rv = reinterpret_cast<const float *>(rec + REC_V);
+        const int row = to & 63;
+        r.vec[0] = rv[R_BETA + row];
+        r.vec[1] = rv[R_G + row];
+        r.vec[2] = rv[R_NK + row];
+        r.vec[3] = rv[R_G + n - 1];
+        r.vec[4] = rv[R_G + (row & ~15)];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) r.t[i] = reinterpret_cast<const uint4 *>(rec + REC_T)[to + 256 * i];
+        for (int bb = 1; bb < 4; ++bb) r.vec[4 + bb] = rv[R_G + 16 * bb];
+    }
+    const uint4 *rt = reinterpret_cast<const uint4 *>(rec + REC_T);
+    r.t[0] = rt[to];
+    r.t[1] = rt[to + 256];
+    r.t[2] = rt[min(to + 512, 10 * 64 - 1)];  // half slots: threads 0..127
 }
 
 // The next chunk's K rows (chain waves).
@@ -555,9 +583,41 @@ __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds
         const int idx = to + 256 * i;
         st_op(Q + (idx >> 4) * KP, idx & 15, zero_if((idx >> 4) >= n, r.q[i]));
     }
-    if (to < kVec / 4) reinterpret_cast<uint4 *>(lds + S_VEC)[to] = r.vec;
+    {  // the coefficients of row to % 64, split over the four waves (wave-uniform branches)
+        float *cv = reinterpret_cast<float *>(lds + S_VEC);
+        const int row = to & 63, part = to >> 6;
+        const float b = r.vec[0], g = r.vec[1], kn = r.vec[2];
+        if (part == 0) {
+            const float eg = __expf(g);
+            cv[V_BETA + row] = b;
+            cv[V_RK + row] = b * eg * kn;
+            cv[V_EG + row] = eg;
+            cv[V_G + row] = g;
+        } else if (part == 1) {
+            cv[V_W + row] = kn * __expf(r.vec[3] - g);
+            cv[V_NK + row] = kn;
+        } else if (part == 2) {
+            // Pt's decay e^(g_r - g_s) as e^(g_r - g_16b) e^(g_16b - g_s) off the
+            // diagonal tiles (both factors <= 1)
+            cv[V_RHO + row] = __expf(g - r.vec[4]);
+            cv[V_CB + row] = row < 16 ? __expf(r.vec[5] - g) * kn : 0.f;
+        } else {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) reinterpret_cast<uint4 *>(lds + S_T)[to + 256 * i] = r.t[i];
+            for (int bb = 2; bb < 4; ++bb)
+                cv[V_CB + 64 * (bb - 1) + row] = row < 16 * bb ? __expf(r.vec[4 + bb] - g) * kn : 0.f;
+        }
+    }
+    uint4 *T = reinterpret_cast<uint4 *>(lds + S_T);  // [slot][hi, lo][lane]
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // full record slots: unit u = (2j + hl) * 64 + lane
+        const int u = to + 256 * i;
+        T[(2 * full_tslot(u >> 7) + ((u >> 6) & 1)) * 64 + (u & 63)] = r.t[i];
+    }
+    if (to < 128) {  // half record slots: the zero halves are written here
+        const int ts = half_tslot(to >> 6), ln = to & 63;
+        T[(2 * ts) * 64 + ln] = make_uint4(r.t[2].x, r.t[2].y, 0u, 0u);
+        T[(2 * ts + 1) * 64 + ln] = make_uint4(r.t[2].z, r.t[2].w, 0u, 0u);
+    }
 }
 
 // Pt slot (r-tile bb, s-slab q) of the chunk in LDS: the P^T tiles
