@@ -427,7 +427,15 @@ def bench_fwht(stream, steps, warmup):
 
     ms_q = time_events(stream, lambda i: fused(i, False), max(steps, 2 * FW_BUFS), warmup)
     ms_qs = time_events(stream, lambda i: fused(i, True), max(steps, 2 * FW_BUFS), warmup)
-    return ms, ms_all, ms_q, ms_qs
+
+    # the floor of a call this size: a device-to-device copy of the same
+    # 4 MiB of rows (8 MiB moved) over the same rotating buffers
+    def copy(i):
+        b = i % FW_BUFS
+        call("ouro_memcpy_dtod", dst.ptr + 2 * b * per, src.ptr + 2 * b * per, 2 * per, stream)
+
+    ms_cp = time_events(stream, copy, max(steps, 2 * FW_BUFS), warmup)
+    return ms, ms_all, ms_q, ms_qs, ms_cp
 
 
 def bench_prefill(stream, steps, warmup):
@@ -865,7 +873,7 @@ def main() -> int:
             "vendor_int8_gemm_8bit_weights_us": round(vendor * 1e3, 2) if vendor else None,
         }
     if "fwht" in res:
-        ms, ms_all, ms_q, ms_qs = res["fwht"]
+        ms, ms_all, ms_q, ms_qs, ms_cp = res["fwht"]
         gbs = FW_BYTES / (ms * 1e-3) / 1e9
         gbs_all = FW_BYTES * FW_BUFS / (ms_all * 1e-3) / 1e9
         sec["fwht"] = {
@@ -875,6 +883,11 @@ def main() -> int:
                          "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "fwht_row_kernel", FW_ROWS * 256)},
             "streaming_16384_rows_GBs": round(gbs_all, 1),
             "bytes_per_call": FW_BYTES,
+            "same_size_copy": {"config": "hipMemcpyAsync device-to-device of the call's 4 MiB of bf16 rows "
+                                         "(8 MiB moved), same 32 rotating buffers: the floor of a call this size",
+                               "ms_per_call": round(ms_cp, 4),
+                               "GBs": round(FW_BYTES / (ms_cp * 1e-3) / 1e9, 1),
+                               "frac": round(FW_BYTES / (ms_cp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "fused_int8_epilogue": {
                 "config": "the same rotation with each bf16 row quantised to int8 (quantize_row_i8_s) in the "
                           "kernel's epilogue; bf16 rows not stored / stored",
