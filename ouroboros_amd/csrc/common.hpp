@@ -78,6 +78,39 @@ __device__ __forceinline__ float i8s_out(int acc, float s, float w_scale) {
     const float t = static_cast<float>(acc) / s;
     return t * w_scale;
 }
+// The same value from a per-row reciprocal: for s >= 2^-76, inv = RN(1 / s)
+// (one IEEE division per activation row); q = RN(acc inv) is within an ulp
+// of acc / s, the residual r = acc - q s is exact in one fma, and
+// RN(q + r inv) is the correctly rounded quotient (Markstein's theorem,
+// which holds without overflow or underflow: |acc| < 2^24 keeps
+// |q| < 2^100, and s <= 127 / 1e-5 keeps it normal).  Three instructions
+// instead of the ~10 of a correctly rounded division.  A smaller scale
+// (amax past ~1e24) is taken as s 2^64 and the quotient scaled back by 2^64,
+// exact since scaling by a power of two commutes with rounding and
+// overflows to inf exactly where the quotient does; s = 0 (amax = inf)
+// gives acc * (1 / 0), which is acc / 0 (+-inf, or NaN for 0).
+// tests/cpp/i8s_quotient_check.c compares this with the division on the host
+// for every integer |acc| <= 2^20 against a spread of scales.
+struct I8sInv {
+    float s, inv, post;
+    bool zero;
+};
+__device__ __forceinline__ I8sInv i8s_inv(float s) {
+    I8sInv r;
+    const bool small = s < 0x1p-76f;
+    r.s = small ? s * 0x1p64f : s;
+    r.inv = 1.0f / r.s;
+    r.post = small ? 0x1p64f : 1.0f;
+    r.zero = s == 0.0f;
+    return r;
+}
+__device__ __forceinline__ float i8s_out_inv(int acc, const I8sInv &d, float w_scale) {
+    const float a = static_cast<float>(acc);
+    const float q = a * d.inv;
+    const float r = __builtin_fmaf(-q, d.s, a);
+    const float t = d.zero ? q : __builtin_fmaf(r, d.inv, q) * d.post;
+    return t * w_scale;
+}
 
 // Canonical byte (codes of weights 4*kg .. 4*kg+3 at bits 2*i) of row `row`
 // of an I2_S tensor: the flattened weights in 128-blocks, weight j of block

@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
     for (int c = 0; c < WC; ++c) {
         const int n = n0 + 16 * c + (lane & 15);
         if (n >= a.N) continue;
-        const float ds = a.act_scale[n];
+        const I8sInv ds = i8s_inv(a.act_scale[n]);  // (acc / s) without a division per output
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
@@ -257,8 +257,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
                 int t[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) t[e] = -(acc[r][c][e] >> 6);
-                const float4 v = make_float4(i8s_out(t[0], ds, wscale), i8s_out(t[1], ds, wscale),
-                                             i8s_out(t[2], ds, wscale), i8s_out(t[3], ds, wscale));
+                const float4 v = make_float4(i8s_out_inv(t[0], ds, wscale), i8s_out_inv(t[1], ds, wscale),
+                                             i8s_out_inv(t[2], ds, wscale), i8s_out_inv(t[3], ds, wscale));
                 if (a.swiglu) {  // outputs row/2 and row/2 + 1: an 8-byte piece
                     *reinterpret_cast<float2 *>(a.y + static_cast<long long>(n) * (a.M / 2) + row / 2) =
                         make_float2(swiglu_pair(v.x, v.y), swiglu_pair(v.z, v.w));
@@ -273,8 +273,8 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
 #pragma unroll
                 for (int e = 0; e < 4; e += 2) {
                     if (row + e + 1 >= a.M) break;
-                    const float up = i8s_out(-(acc[r][c][e] >> 6), ds, wscale);
-                    const float gt = i8s_out(-(acc[r][c][e + 1] >> 6), ds, wscale);
+                    const float up = i8s_out_inv(-(acc[r][c][e] >> 6), ds, wscale);
+                    const float gt = i8s_out_inv(-(acc[r][c][e + 1] >> 6), ds, wscale);
                     a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
                 }
                 continue;
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
                 if (row + e >= a.M) break;
                 const int total = -(acc[r][c][e] >> 6);
                 const long long o = static_cast<long long>(n) * a.M + row + e;
-                a.y[o] = gemm_epilogue(a.epi, i8s_out(total, ds, wscale), n, row + e, a.M);
+                a.y[o] = gemm_epilogue(a.epi, i8s_out_inv(total, ds, wscale), n, row + e, a.M);
                 if (a.acc) a.acc[o] = total;
             }
         }
@@ -308,9 +308,15 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
 // 8 (e / 4) + 4 (l / 32) + e % 4.
 //
 // The activation tile of a 256-deep k block (32 KiB) is double-buffered in
-// LDS; activations and weights are prefetched a k block ahead in registers
-// (indices clamped, not guarded, so the loads are unconditional and the
-// waits count them exactly).  Workgroups are handed out XCD by XCD
+// LDS and filled a k block ahead by direct global-to-LDS loads
+// (global_load_lds_dwordx4: lane i of a wavefront's load lands at the
+// wavefront's LDS base + 16 i, from an address the lane chooses), so the
+// tile takes no registers and no LDS write instructions; column n's 256
+// bytes are one LDS row, its 16-byte chunk u at slot u ^ (n % 16), so the
+// B-fragment reads (32 columns, one chunk) hit distinct banks.  The
+// weights are prefetched a k block ahead in registers.  Indices are
+// clamped, not guarded, so the loads are unconditional and the waits count
+// them exactly.  Workgroups are handed out XCD by XCD
 // (blockIdx % 8 is the XCD): each XCD takes a contiguous run of tiles, row
 // blocks fastest, so the 128 activation columns a run shares stay in that
 // XCD's L2.
@@ -319,9 +325,12 @@ constexpr int kBigTM = 2, kBigTN = 4;  // 32 x 32 MFMA tiles per wavefront
 constexpr int kBigCols = kBigTN * 32;  // columns per workgroup (rows: 4 kBigTM 32)
 constexpr int kBigMinBlocks = 192;  // fewer tiles than this: the 16x16 kernel (faster there)
 
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
 __global__ __launch_bounds__(kWave *kGemmWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void i2_gemm_big_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t xs[2][kBigCols * kXPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t xs[2][kBigCols * 256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nblk = static_cast<int>(gridDim.x), xcd = static_cast<int>(blockIdx.x) % 8;
     const int q8 = nblk / 8, r8 = nblk % 8;
@@ -333,20 +342,20 @@ void i2_gemm_big_kernel(GemmArgs a) {
     const int half = (lane & 31) >> 4, g = lane >> 5;
 
     constexpr int XV = kBigCols * 16 / (kWave * kGemmWaves);  // 16-byte pieces per thread per k block
-    v4u xr[XV], wr[kBigTM][2];
-    auto load_x = [&](int kb) {
+    v4u wr[kBigTM][2];
+    // load i of wavefront `wave` fills LDS bytes 1024 (XV wave + i) .. +1023 of
+    // buffer buf: slot 16 lane of that KiB is column n = 4 (XV wave + i) +
+    // lane / 16, chunk (lane % 16) ^ (n % 16)
+    auto load_x = [&](int kb, int buf) {
 #pragma unroll
         for (int i = 0; i < XV; ++i) {
-            const int c = tid + kWave * kGemmWaves * i;
-            const int n = min(n0 + c / 16, a.N - 1);  // clamped: columns past N are never stored
-            xr[i] = *reinterpret_cast<const v4u *>(a.xq + static_cast<long long>(n) * a.K + 256 * kb + 16 * (c % 16));
-        }
-    };
-    auto store_x = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int c = tid + kWave * kGemmWaves * i;
-            *reinterpret_cast<v4u *>(&xs[buf][(c / 16) * kXPitch + 16 * (c % 16)]) = xr[i];
+            const int piece = XV * wave + i;
+            const int nl = 4 * piece + (lane >> 4);
+            const int u = (lane & 15) ^ (nl & 15);
+            const int n = min(n0 + nl, a.N - 1);  // clamped: columns past N are never stored
+            __builtin_amdgcn_global_load_lds(
+                (global_void *)(a.xq + static_cast<long long>(n) * a.K + 256 * kb + 16 * u),
+                (lds_void *)(&xs[buf][1024 * piece]), 16, 0, 0);
         }
     };
     auto load_w = [&](int kb) {
@@ -368,20 +377,21 @@ void i2_gemm_big_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[r][c][e] = 0;
 
-    load_x(0);
+    load_x(0, 0);
     load_w(0);
-    store_x(0);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wavefront's LDS fills have landed
     __syncthreads();
+    const int ncol = lane & 31;  // the B fragment's column within its 32-column tile (same low bits for every tile)
     for (int kb = 0; kb < a.nkb; ++kb) {
         v4u wc[kBigTM][2];
 #pragma unroll
         for (int r = 0; r < kBigTM; ++r) wc[r][0] = wr[r][0], wc[r][1] = wr[r][1];
         const bool more = kb + 1 < a.nkb;
-        if (more) {
-            load_x(kb + 1);
+        if (more) {  // the other buffer: its last reads were before the previous barrier
+            load_x(kb + 1, (kb + 1) & 1);
             load_w(kb + 1);
         }
-        const uint8_t *xb = xs[kb & 1] + (lane & 31) * kXPitch + 16 * g;
+        const uint8_t *xb = xs[kb & 1] + ncol * 256;
 #pragma unroll
         for (int sp = 0; sp < 8; ++sp) {
             const int s = sp / 2, p = sp % 2;  // MFMA step (s, p): k = 64 s + 32 p + 16 g
@@ -392,15 +402,16 @@ void i2_gemm_big_kernel(GemmArgs a) {
                 A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
                            static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
             }
+            const int slot = 16 * ((2 * sp + g) ^ (ncol & 15));  // chunk 2 sp + g of column 32 c + ncol
 #pragma unroll
             for (int c = 0; c < kBigTN; ++c) {
-                const v4i B = *reinterpret_cast<const v4i *>(xb + c * 32 * kXPitch + 32 * sp);
+                const v4i B = *reinterpret_cast<const v4i *>(xb + c * 32 * 256 + slot);
 #pragma unroll
                 for (int r = 0; r < kBigTM; ++r)
                     acc[r][c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[r], B, acc[r][c], 0, 0, 0);
             }
         }
-        if (more) store_x((kb + 1) & 1);
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): the next block's LDS fills (and weights) have landed
         __syncthreads();
     }
 
@@ -413,7 +424,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
     for (int c = 0; c < kBigTN; ++c) {
         const int n = n0 + c * 32 + (lane & 31);
         if (n >= a.N) continue;
-        const float ds = a.act_scale[n];
+        const I8sInv ds = i8s_inv(a.act_scale[n]);  // (acc / s) without a division per output
 #pragma unroll
         for (int r = 0; r < kBigTM; ++r)
 #pragma unroll
@@ -424,8 +435,8 @@ void i2_gemm_big_kernel(GemmArgs a) {
 #pragma unroll
                     for (int e = 0; e < 4; e += 2) {
                         if (row + e + 1 >= a.M) break;
-                        const float up = i8s_out(-(acc[r][c][4 * q + e] >> 6), ds, wscale);
-                        const float gt = i8s_out(-(acc[r][c][4 * q + e + 1] >> 6), ds, wscale);
+                        const float up = i8s_out_inv(-(acc[r][c][4 * q + e] >> 6), ds, wscale);
+                        const float gt = i8s_out_inv(-(acc[r][c][4 * q + e + 1] >> 6), ds, wscale);
                         a.y[static_cast<long long>(n) * (a.M / 2) + (row + e) / 2] = swiglu_pair(up, gt);
                     }
                     continue;
@@ -434,10 +445,10 @@ void i2_gemm_big_kernel(GemmArgs a) {
                     float4 v;
                     float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
                     if (a.epi.op == EPI_RESID) res = *reinterpret_cast<const float4 *>(a.epi.b + o);
-                    v.x = i8s_out(-(acc[r][c][4 * q] >> 6), ds, wscale);
-                    v.y = i8s_out(-(acc[r][c][4 * q + 1] >> 6), ds, wscale);
-                    v.z = i8s_out(-(acc[r][c][4 * q + 2] >> 6), ds, wscale);
-                    v.w = i8s_out(-(acc[r][c][4 * q + 3] >> 6), ds, wscale);
+                    v.x = i8s_out_inv(-(acc[r][c][4 * q] >> 6), ds, wscale);
+                    v.y = i8s_out_inv(-(acc[r][c][4 * q + 1] >> 6), ds, wscale);
+                    v.z = i8s_out_inv(-(acc[r][c][4 * q + 2] >> 6), ds, wscale);
+                    v.w = i8s_out_inv(-(acc[r][c][4 * q + 3] >> 6), ds, wscale);
                     if (a.epi.op == EPI_RESID) {
                         v.x = res.x + v.x;
                         v.y = res.y + v.y;
@@ -451,7 +462,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     if (row + e >= a.M) break;
                     const int total = -(acc[r][c][4 * q + e] >> 6);
-                    a.y[o + e] = gemm_epilogue(a.epi, i8s_out(total, ds, wscale), n, row + e, a.M);
+                    a.y[o + e] = gemm_epilogue(a.epi, i8s_out_inv(total, ds, wscale), n, row + e, a.M);
                     if (a.acc) a.acc[o + e] = total;
                 }
             }
