@@ -65,13 +65,17 @@ def run(prompts, feeds, seed=1234):
         st.free()
 
 
+# 40 sequences: the decode step's tall products (the qkv/z/beta/alpha group,
+# up/gate) run on the k-split 16x16 MFMA kernel over fragment-ordered int8
+# activations (3 column tiles, the last one partial), a sequence decoded
+# alone on the one-tile kernel
 @pytest.fixture(scope="module")
 def batch():
     rng = np.random.default_rng(11)
-    lens = rng.integers(16, 2049, 16)
+    lens = rng.integers(16, 2049, 40)
     lens[3], lens[9] = 2048, 16
     prompts = [rng.integers(0, V, int(n)).astype(np.int32) for n in lens]
-    feeds = [rng.integers(0, V, 16) for _ in range(2)]
+    feeds = [rng.integers(0, V, 40) for _ in range(2)]
     logits, toks = run(prompts, feeds)
     return prompts, feeds, logits, toks
 
