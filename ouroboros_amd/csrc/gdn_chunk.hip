@@ -23,15 +23,16 @@
 // below them on v_mfma_f32_16x16x4f32.
 //
 // Two kernels.  gdn_chunk_prep_kernel runs every (chunk, v-head) in parallel
-// and computes what does not depend on the state: k-row norms, g, T and the
-// per-row coefficients, written to a workspace record (it does not read Q).
+// and computes what does not depend on the state: k-row norms, g, beta and
+// T, written to a workspace record (it does not read Q).
 // gdn_chunk_scan_kernel then walks the chunks of a sequence in order.
 // Output column j of the recurrence only touches state column j, so
 // 16-column stripes of the state are independent chains: a "chain" wave
 // keeps one stripe in registers and runs K S0 -> R -> U -> S update (and
 // forms the q-row norms of one row tile from the Q operands it reads),
 // while a paired "output" wave forms Pt from the chunk's K and Q rows and O
-// for the same stripe; two barriers per chunk.
+// for the same stripe and, with the record's beta, g and k-norms, the other
+// per-row coefficients of the next chunk; two barriers per chunk.
 #include "common.hpp"
 
 namespace ouro {
