@@ -52,27 +52,39 @@ constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free
 // (T is lower triangular: slab q is zero for a < 2q); the scan's Pt slots
 // are (r-tile b, s-slab q) = (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).  A slot
 // is an A operand: lane r + 16 g holds T[16a + r][32q + 4g .. +3] ++
-// T[16a + r][32q + 16 + 4g .. +3], as hi and lo bf16.  In slots (0,0) and
-// (2,1) the second half lies in a block above the diagonal and is zero.
+// T[16a + r][32q + 16 + 4g .. +3], as hi and lo bf16: its first half is
+// 16x16 block (a, 2q) of T, its second half block (a, 2q + 1).  In slots
+// (0,0) and (2,1) the second half lies above the diagonal and is zero; in
+// a diagonal block (i, i) lane r + 16 g is zero when 4 g > r, so 40 of its
+// 64 lanes carry values.
 //
-// Workspace record of one (chunk, v-head), 256-byte aligned, 11,008 B:
-//   the full T slots (1,0) (2,0) (3,0) (3,1) as [slot][hi, lo][64 lanes]
-//   x 16 B, then the half slots (0,0) (2,1) as [slot][64 lanes] x 16 B
-//   holding the non-zero halves (hi.xy, lo.xy)                      10 KiB
-//   beta, g (inclusive cumsum of the log-decays), nk [64] fp32        768 B
+// Workspace record of one (chunk, v-head), 256-byte aligned, 9,472 B, in
+// 16-byte units:
+//   0 .. 255    the dense slots (2,0) (3,0) as [slot][hi, lo][64 lanes]
+//   256 .. 383  the dense blocks (1,0) (3,2), [block][64 lanes] holding
+//               (hi.xy, lo.xy) of the lane's four values
+//   384 .. 543  the diagonal blocks (0,0) (1,1) (2,2) (3,3), [block][40]
+//               in the same form, lane r + 16 g (4 g <= r) at diag_unit
+//   8,704 B:    beta, g (inclusive cumsum of the log-decays), nk [64] fp32
 // The scan forms the other per-row coefficients from these while it
 // stages them (LDS vectors below), and the q-row norms nq from the Q rows
 // it stages; nq is applied to the output rows last: O = nq (e^g Q S0 +
-// Pt U) with nq taken out of Pt.
+// Pt U) with nq taken out of Pt.  (All ten blocks stored whole took
+// 11,008 B per record; per 4 x 4096-token call the record is written once
+// and read once, 2 x 8,192 records.)
 constexpr int REC_T = 0;
-constexpr int REC_HALF = 8 * 64 * 16;  // the half slots
-constexpr int REC_V = 10 * 64 * 16;
+constexpr int RU_HALF = 256;  // first unit of the dense blocks (1,0) (3,2)
+constexpr int RU_DIAG = 384;  // first unit of the diagonal blocks
+constexpr int kRecUnits = RU_DIAG + 4 * 40;
+constexpr int REC_V = kRecUnits * 16;
 enum { R_BETA = 0, R_G = 64, R_NK = 128, kRecVec = 192 };
-constexpr size_t kRec = 11008;
+constexpr size_t kRec = 9472;
 static_assert(REC_V + kRecVec * 4 <= static_cast<int>(kRec) && kRec % 256 == 0, "record size");
-// T slot of full record slot j and of half record slot k.
-__host__ __device__ constexpr int full_tslot(int j) { return j < 3 ? j + 1 : 5; }
-__host__ __device__ constexpr int half_tslot(int k) { return k == 0 ? 0 : 4; }
+// Unit of lane r + 16 g (4 g <= r) of diagonal block i: lanes in g-major
+// order, g = 0 holding 16 rows, g = 1 12, g = 2 8, g = 3 4.
+__host__ __device__ constexpr int diag_unit(int i, int r, int g) { return RU_DIAG + 40 * i + r + 2 * g * (7 - g); }
+// T slot holding diagonal block i (its first half for even i, second for odd).
+__host__ __device__ constexpr int diag_tslot(int i) { return i < 2 ? i : i + 2; }
 
 // The scan's LDS vectors [64] fp32 of a chunk: beta, rk = beta e^g nk,
 // w = nk e^(g_C - g), eg = e^g, g, nk, rho = e^(g - g_16floor(r/16)) and
@@ -263,13 +275,20 @@ __device__ __forceinline__ void prep_load(const ChunkArgs &a, const PrepItem &p,
 
 // Each wave walks items wave, wave + waves, ...; the next item's K rows are
 // loaded (into the same registers, which K K^T has finished with) while the
-// current one's T is solved and written.
+// current one's T is solved and written.  With the grid a multiple of 8,
+// workgroups are numbered XCD by XCD (workgroup b runs on XCD b % 8), so
+// the v-heads of a chunk, whose beta and gate reads share 128-byte lines
+// (one line per token), are served by one L2 (per 4 x 4096-token call the
+// prep read 101 MB for its 71 MB of K, beta and gate with the heads of a
+// chunk spread over all eight).
 __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs a, int items) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const int stride = static_cast<int>(gridDim.x) * kPrepWaves;
-    int item = blockIdx.x * kPrepWaves + wave;
+    const int grid = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+    const int wg = grid % 8 == 0 ? (b % 8) * (grid / 8) + b / 8 : b;
+    const int stride = grid * kPrepWaves;
+    int item = wg * kPrepWaves + wave;
     if (item >= items) return;  // whole wave
     float *Al = reinterpret_cast<float *>(lds + wave * PW_BYTES);
     float *nk = Al + kC * AP;
@@ -419,27 +438,37 @@ __global__ __launch_bounds__(kPrepThreads) void gdn_chunk_prep_kernel(ChunkArgs 
     put(3, 0, offdiag_x(3, offdiag_y(3, 0)));
     __builtin_amdgcn_wave_barrier();
 
-    // T operands: slot (aa, q) of lane (lr, lg) is T[16aa + lr][32q + 4lg .. +3]
-    // ++ T[16aa + lr][32q + 16 + 4lg .. +3], split hi/lo; slots (0,0) and
-    // (2,1) (aa = 2q) keep only their first half
+    // T operands, split hi/lo: lane (lr, lg) of block (i, j) holds
+    // T[16i + lr][16j + 4lg .. +3]
     {
         uint4 *rt = reinterpret_cast<uint4 *>(rec + REC_T);
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int aa = 2; aa < 4; ++aa) {  // dense slots (2,0), (3,0)
+            const float *row = Al + (16 * aa + lr) * AP + 4 * lg;
+            bf16x8 th, tl;
+            split8(ld4(row), ld4(row + 16), th, tl);
+            rt[(2 * (aa - 2)) * 64 + lane] = __builtin_bit_cast(uint4, th);
+            rt[(2 * (aa - 2) + 1) * 64 + lane] = __builtin_bit_cast(uint4, tl);
+        }
 #pragma unroll
-            for (int aa = 2 * q; aa < 4; ++aa) {
-                const float *row = Al + (16 * aa + lr) * AP + 32 * q + 4 * lg;
-                bf16x8 th, tl;  // the second half of slots (0,0), (2,1) lies above the diagonal: zero
-                split8(ld4(row), aa == 2 * q ? f32x4{0.f, 0.f, 0.f, 0.f} : ld4(row + 16), th, tl);
+        for (int k = 0; k < 2; ++k) {  // dense blocks (1,0), (3,2)
+            const float *row = Al + (16 * (2 * k + 1) + lr) * AP + 32 * k + 4 * lg;
+            bf16x8 th, tl;
+            split8(ld4(row), z4, th, tl);
+            const uint4 h = __builtin_bit_cast(uint4, th), l = __builtin_bit_cast(uint4, tl);
+            rt[RU_HALF + 64 * k + lane] = make_uint4(h.x, h.y, l.x, l.y);
+        }
+        if (4 * lg <= lr) {  // the diagonal blocks' non-zero lanes
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float *row = Al + (16 * i + lr) * AP + 16 * i + 4 * lg;
+                bf16x8 th, tl;
+                split8(ld4(row), z4, th, tl);
                 const uint4 h = __builtin_bit_cast(uint4, th), l = __builtin_bit_cast(uint4, tl);
-                if (aa == 2 * q) {
-                    rt[REC_HALF / 16 + q * 64 + lane] = make_uint4(h.x, h.y, l.x, l.y);
-                } else {
-                    const int j = q == 0 ? aa - 1 : 3;
-                    rt[(2 * j) * 64 + lane] = h;
-                    rt[(2 * j + 1) * 64 + lane] = l;
-                }
+                rt[diag_unit(i, lr, lg)] = make_uint4(h.x, h.y, l.x, l.y);
             }
+        }
     }
     if (next >= items) break;
     item = next;
@@ -527,7 +556,7 @@ __device__ __forceinline__ void load_next(const ChunkArgs &a, NextRegs &r, int t
     const uint4 *rt = reinterpret_cast<const uint4 *>(rec + REC_T);
     r.t[0] = rt[to];
     r.t[1] = rt[to + 256];
-    r.t[2] = rt[min(to + 512, 10 * 64 - 1)];  // half slots: threads 0..127
+    r.t[2] = rt[min(to + 512, kRecUnits - 1)];  // threads 0..31
 }
 
 // The next chunk's K rows (chain waves).
@@ -608,16 +637,48 @@ __device__ __forceinline__ void store_next(const NextRegs &r, unsigned char *lds
                 cv[V_CB + 64 * (bb - 1) + row] = row < 16 * bb ? __expf(r.vec[4 + bb] - g) * kn : 0.f;
         }
     }
-    uint4 *T = reinterpret_cast<uint4 *>(lds + S_T);  // [slot][hi, lo][lane]
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {  // full record slots: unit u = (2j + hl) * 64 + lane
-        const int u = to + 256 * i;
-        T[(2 * full_tslot(u >> 7) + ((u >> 6) & 1)) * 64 + (u & 63)] = r.t[i];
+    // T operands [slot][hi, lo][lane] x 16 B; the positions that are always
+    // zero were cleared by zero_t and are not written here
+    uint4 *T = reinterpret_cast<uint4 *>(lds + S_T);
+    uint2 *T2 = reinterpret_cast<uint2 *>(lds + S_T);  // the same in 8-byte halves
+    // units 0..255: dense slots 2, 3
+    T[(2 * (2 + (to >> 7)) + ((to >> 6) & 1)) * 64 + (to & 63)] = r.t[0];
+    // one unit (hi.xy, lo.xy) into half hf of lane ln of slot ts
+    const auto put_half = [&](const uint4 &v, int ts, int hf, int ln) {
+        T2[((2 * ts) * 64 + ln) * 2 + hf] = make_uint2(v.x, v.y);
+        T2[((2 * ts + 1) * 64 + ln) * 2 + hf] = make_uint2(v.z, v.w);
+    };
+    // the unit of diagonal-block index d (0 .. 159): block d / 40, lane in g-major order
+    const auto put_diag = [&](const uint4 &v, int d) {
+        const int i = d / 40, x = d % 40;
+        const int g = x < 16 ? 0 : x < 28 ? 1 : x < 36 ? 2 : 3;
+        put_half(v, diag_tslot(i), i & 1, x - 2 * g * (7 - g) + 16 * g);
+    };
+    if (to < 128) {  // units 256..383: blocks (1,0), (3,2), first half of slots 1, 5
+        put_half(r.t[1], to < 64 ? 1 : 5, 0, to & 63);
+    } else {         // units 384..511
+        put_diag(r.t[1], to - 128);
     }
-    if (to < 128) {  // half record slots: the zero halves are written here
-        const int ts = half_tslot(to >> 6), ln = to & 63;
-        T[(2 * ts) * 64 + ln] = make_uint4(r.t[2].x, r.t[2].y, 0u, 0u);
-        T[(2 * ts + 1) * 64 + ln] = make_uint4(r.t[2].z, r.t[2].w, 0u, 0u);
+    if (to < 32) put_diag(r.t[2], to + 128);  // units 512..543
+}
+
+// The T operand positions no record unit covers, cleared once before the
+// first chunk is staged (store_next never writes them): the second halves
+// of slots 0 and 4 (blocks above the diagonal) and, in each diagonal
+// block, the lanes r + 16 g with 4 g > r.
+__device__ __forceinline__ void zero_t(unsigned char *lds, int to) {
+    uint2 *T2 = reinterpret_cast<uint2 *>(lds + S_T);
+    const int i = to >> 6, ln = to & 63, r = ln & 15, g = ln >> 4;
+    const uint2 z = make_uint2(0u, 0u);
+    if (4 * g > r) {
+        const int ts = diag_tslot(i), hf = i & 1;
+        T2[((2 * ts) * 64 + ln) * 2 + hf] = z;
+        T2[((2 * ts + 1) * 64 + ln) * 2 + hf] = z;
+    }
+    if (i < 2) {
+        const int ts = i == 0 ? 0 : 4;
+        T2[((2 * ts) * 64 + ln) * 2 + 1] = z;
+        T2[((2 * ts + 1) * 64 + ln) * 2 + 1] = z;
     }
 }
 
@@ -847,6 +908,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(ChunkArgs 
         {
             const int n0 = min(kC, t_end - t_begin);
             load_next(a, nx, tr, t_begin, n0, kh, h, jb, record(0));
+            zero_t(lds, tr);
             store_next(nx, lds, tr, n0);
         }
         float *ob = a.out + static_cast<long long>(h) * kD + jw + 4 * lg;
@@ -1000,7 +1062,8 @@ int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v,
         const int items = chunks * static_cast<int>(Hv);
         // resident workgroups only (two per CU by their LDS); each wave
         // walks items with a stride of the whole grid
-        const int wgs = std::min((items + kPrepWaves - 1) / kPrepWaves, kPrepGrid);
+        int wgs = std::min((items + kPrepWaves - 1) / kPrepWaves, kPrepGrid);
+        if (wgs > 8) wgs -= wgs % 8;  // XCD-ordered numbering (waves stride over the rest)
         hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(static_cast<unsigned>(wgs)), dim3(kPrepThreads), PREP_LDS,
                            as_stream(stream), a, items);
         int st = check_launch("gdn_chunk_prep_kernel");

@@ -69,7 +69,7 @@ def test_i2_tiled_bytes_matches_oracle(orc):
 def test_chunk_workspace_bytes():
     from ouroboros_amd import qwen35
 
-    rec = 11008  # T operands 10 KiB (two slots stored by their non-zero half) + beta, g, nk [64] fp32
+    rec = 9472  # T operands 8.5 KiB (six dense blocks, four diagonal blocks by their 40 non-zero lanes) + beta, g, nk [64] fp32
     assert qwen35.chunk_workspace_bytes(16384, 4, 32) == (256 + 4 + 1) * 32 * rec
     assert qwen35.chunk_workspace_bytes(100, 1000, 2) == (1 + 256 + 1) * 2 * rec
     assert qwen35.chunk_workspace_bytes(64, 1, 4, d=64) == 0
