@@ -69,9 +69,10 @@ constexpr int KTP = kC + 4;       // bf16 row pitch of K^T (136 B; conflict-free
 // The scan forms the other per-row coefficients from these while it
 // stages them (LDS vectors below), and the q-row norms nq from the Q rows
 // it stages; nq is applied to the output rows last: O = nq (e^g Q S0 +
-// Pt U) with nq taken out of Pt.  (All ten blocks stored whole took
-// 11,008 B per record; per 4 x 4096-token call the record is written once
-// and read once, 2 x 8,192 records.)
+// Pt U) with nq taken out of Pt.  Each record is written once by the prep
+// and read once by the scan, so its size is HBM traffic twice over: with
+// all ten blocks stored whole (11,008 B) a 4 x 4096-token call (8,192
+// records) moved 25 MB more.
 constexpr int REC_T = 0;
 constexpr int RU_HALF = 256;  // first unit of the dense blocks (1,0) (3,2)
 constexpr int RU_DIAG = 384;  // first unit of the diagonal blocks
