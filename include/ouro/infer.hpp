@@ -71,7 +71,10 @@ private:
 namespace infer {
 
 // QuantKind (dequant.rs:315-348), ggml dtype ids; I2 is this library's.
-enum class QuantKind : int { F32 = 0, F16 = 1, Bf16 = 30, Tq1_0 = 34, Tl1 = 143, I2 = OURO_KIND_I2 };
+enum class QuantKind : int {
+    F32 = 0, F16 = 1, Bf16 = 30, Q8_0 = 8, Q3K = 11, Q4K = 12, Q5K = 13, Q6K = 14, Tq1_0 = 34, Tl1 = 143,
+    I2 = OURO_KIND_I2
+};
 
 namespace ops {
 
@@ -193,7 +196,8 @@ public:
         for (const bmts::Tensor &t : shard.tensors()) {
             const int d = static_cast<int>(t.dtype);
             if (d != OURO_KIND_F32 && d != OURO_KIND_F16 && d != OURO_KIND_BF16 && d != OURO_KIND_TQ1_0 &&
-                d != OURO_KIND_TL1)
+                d != OURO_KIND_TL1 && d != OURO_KIND_Q8_0 && d != OURO_KIND_Q3K && d != OURO_KIND_Q4K &&
+                d != OURO_KIND_Q5K && d != OURO_KIND_Q6K)
                 throw Error(OURO_ERR_KIND, "unsupported dtype " + std::to_string(t.dtype) + " on " + t.name);
             size_t out_len = 0, in_len = 0;
             shard.weight_shape(t.name, &out_len, &in_len);

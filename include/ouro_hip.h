@@ -60,6 +60,11 @@ enum {
     OURO_KIND_F32 = 0,
     OURO_KIND_F16 = 1,
     OURO_KIND_BF16 = 30,
+    OURO_KIND_Q8_0 = 8,    /* 34 B / 32: d f16, qs int8[32] (dequant.rs:225-231) */
+    OURO_KIND_Q3K = 11,    /* 110 B / 256: hmask, qs, scales[12], d (dequant.rs:398-451) */
+    OURO_KIND_Q4K = 12,    /* 144 B / 256: d, dmin, scales[12], qs (dequant.rs:257-282) */
+    OURO_KIND_Q5K = 13,    /* 176 B / 256: d, dmin, scales[12], qh, qs (dequant.rs:454-481) */
+    OURO_KIND_Q6K = 14,    /* 210 B / 256: ql, qh, scales int8[16], d (dequant.rs:484-510) */
     OURO_KIND_TQ1_0 = 34,  /* 54 B / 256 weights, base-3 (dequant.rs:49-105) */
     OURO_KIND_TL1 = 143,   /* PTQ1_0, 28 B / 128 weights (dequant.rs:124-195) */
     /* bitnet.cpp's I2_S tensor (GGML_TYPE_I2_S of microsoft/BitNet's ggml
@@ -241,6 +246,11 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len,
  * device payload of `kind`:
  *   OURO_KIND_TL1   - PTQ1_0 groups (fused decode + dot, ops.rs:294-363)
  *   OURO_KIND_TQ1_0 - TQ1_0 blocks (matvec_qblock, ops.rs:101-128)
+ *   OURO_KIND_Q8_0, OURO_KIND_Q3K, OURO_KIND_Q4K, OURO_KIND_Q5K,
+ *   OURO_KIND_Q6K   - ggml blocks as they are, any byte alignment
+ *                     (matvec_qblock, ops.rs:101-128; in_len a multiple of
+ *                     the block's 32 / 256 elements, x 4-byte aligned);
+ *                     decode and dot fused in one pass, no scratch
  *   OURO_KIND_F32 / F16 / BF16 - dense rows (ops.rs:87-98,131-154,600-623)
  *   OURO_KIND_I2_S  - a bitnet.cpp I2_S tensor as it is (16-byte aligned,
  *                     in_len % 256 == 0, in_len <= 32768)

@@ -36,6 +36,7 @@ LIB = HERE / "libouro_oracle.so"
 
 L2NORM_QK, SCALE_Q, KHEAD_DIV = 1, 2, 4
 KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2_S, KIND_I2 = 0, 1, 30, 34, 143, 36, 0x4932
+KIND_Q8_0, KIND_Q3K, KIND_Q4K, KIND_Q5K, KIND_Q6K = 8, 11, 12, 13, 14
 
 _lib: C.CDLL | None = None
 
@@ -60,6 +61,13 @@ def lib() -> C.CDLL:
             "orc_dequant_tl1_row": (None, [vp, sz, sz, vp]),
             "orc_tq1_block": (None, [vp, vp]),
             "orc_dequant_tq1_row": (None, [vp, sz, sz, vp]),
+            "orc_q8_block": (None, [vp, vp]),
+            "orc_q4k_block": (None, [vp, vp]),
+            "orc_q3k_block": (None, [vp, vp]),
+            "orc_q5k_block": (None, [vp, vp]),
+            "orc_q6k_block": (None, [vp, vp]),
+            "orc_dequant_qblock_row": (i32, [i32, vp, sz, sz, vp]),
+            "orc_matvec_qblock": (i32, [vp, i32, sz, sz, vp, vp, i32]),
             "orc_row_bytes": (sz, [i32, sz]),
             "orc_kind_supported": (i32, [u32]),
             "orc_dot": (f32, [vp, vp, sz]),
@@ -154,6 +162,35 @@ def dequant_tq1_row(payload: np.ndarray, row: int, in_len: int) -> np.ndarray:
     p = np.ascontiguousarray(payload, dtype=np.uint8)
     out = np.empty(in_len, np.float32)
     lib().orc_dequant_tq1_row(_p(p), row, in_len // 256 * 54, _p(out))
+    return out
+
+
+# Block bytes / elements of the block-quantised kinds (QuantKind::block_bytes,
+# block_elems, dequant.rs:350-372), keyed by ggml dtype id.
+QBLOCK = {34: (54, 256), 8: (34, 32), 11: (110, 256), 12: (144, 256), 13: (176, 256), 14: (210, 256)}
+_QBLOCK_FN = {8: "orc_q8_block", 11: "orc_q3k_block", 12: "orc_q4k_block", 13: "orc_q5k_block",
+              14: "orc_q6k_block", 34: "orc_tq1_block"}
+
+
+def qblock(kind: int, blk: np.ndarray) -> np.ndarray:
+    """Decode one block of a block-quantised kind (q8_block, q4k_block, ...)."""
+    bb, be = QBLOCK[kind]
+    b = np.ascontiguousarray(blk, dtype=np.uint8)
+    assert b.size == bb
+    out = np.empty(be, np.float32)
+    getattr(lib(), _QBLOCK_FN[kind])(_p(b), _p(out))
+    return out
+
+
+def dequant_qblock(kind: int, payload: np.ndarray) -> np.ndarray:
+    """A whole payload of blocks, decoded (dequant_q8_0, dequant_q4_k, ...)."""
+    bb, be = QBLOCK[kind]
+    p = np.ascontiguousarray(payload, dtype=np.uint8).reshape(-1)
+    assert p.size % bb == 0
+    nb = p.size // bb
+    out = np.empty(nb * be, np.float32)
+    if nb:
+        lib().orc_dequant_qblock_row(kind, _p(p), 0, p.size, _p(out))
     return out
 
 

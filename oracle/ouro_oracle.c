@@ -204,6 +204,168 @@ void orc_dequant_tq1_row(const uint8_t *payload, size_t row, size_t row_bytes,
         orc_tq1_block(payload + start + b * 54, out + b * 256);
 }
 
+/* ---- the K-quant and Q8_0 blocks (dequant.rs:218-310, 390-560) ---------- */
+
+static float f16_at(const uint8_t *b) { return orc_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))); }
+
+void orc_q8_block(const uint8_t *bytes, float *out) /* dequant.rs:225-231 */
+{
+    float d = f16_at(bytes);
+    for (int j = 0; j < 32; ++j) out[j] = (float)(int8_t)bytes[2 + j] * d;
+}
+
+/* scale_min_k4 (dequant.rs:245-254) */
+static void scale_min_k4(int j, const uint8_t *sc, uint8_t *d, uint8_t *m)
+{
+    if (j < 4) {
+        *d = sc[j] & 63;
+        *m = sc[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4));
+        *m = (uint8_t)((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4));
+    }
+}
+
+void orc_q4k_block(const uint8_t *bytes, float *out) /* dequant.rs:257-282 */
+{
+    float d = f16_at(bytes), min = f16_at(bytes + 2);
+    const uint8_t *scales = bytes + 4, *q = bytes + 16;
+    int is = 0, o = 0;
+    for (int blk = 0; blk < 4; ++blk) {
+        uint8_t s1, m1, s2, m2;
+        scale_min_k4(is, scales, &s1, &m1);
+        scale_min_k4(is + 1, scales, &s2, &m2);
+        float d1 = d * (float)s1, d2 = d * (float)s2;
+        float mm1 = min * (float)m1, mm2 = min * (float)m2;
+        for (int l = 0; l < 32; ++l) out[o + l] = d1 * (float)(q[l] & 0xF) - mm1;
+        for (int l = 0; l < 32; ++l) out[o + 32 + l] = d2 * (float)(q[l] >> 4) - mm2;
+        o += 64;
+        q += 32;
+        is += 2;
+    }
+}
+
+void orc_q3k_block(const uint8_t *bytes, float *out) /* dequant.rs:398-451 */
+{
+    const uint8_t *hm = bytes, *q = bytes + 32, *sc = bytes + 96;
+    float d_all = f16_at(bytes + 108);
+    uint32_t aux[4];
+    for (int i = 0; i < 3; ++i)
+        aux[i] = (uint32_t)sc[4 * i] | ((uint32_t)sc[4 * i + 1] << 8) |
+                 ((uint32_t)sc[4 * i + 2] << 16) | ((uint32_t)sc[4 * i + 3] << 24);
+    const uint32_t K1 = 0x03030303u, K2 = 0x0f0f0f0fu, tmp = aux[2];
+    uint32_t na[4];
+    na[0] = (aux[0] & K2) | ((tmp & K1) << 4);
+    na[1] = (aux[1] & K2) | (((tmp >> 2) & K1) << 4);
+    na[2] = ((aux[0] >> 4) & K2) | (((tmp >> 4) & K1) << 4);
+    na[3] = ((aux[1] >> 4) & K2) | (((tmp >> 6) & K1) << 4);
+    int8_t scales[16];
+    for (int i = 0; i < 16; ++i) scales[i] = (int8_t)(uint8_t)(na[i / 4] >> (8 * (i % 4)));
+    int o = 0, is = 0;
+    uint8_t m = 1;
+    for (int n = 0; n < 2; ++n) {
+        int shift = 0;
+        for (int j = 0; j < 4; ++j) {
+            float dl = d_all * ((float)scales[is] - 32.0f);
+            ++is;
+            for (int l = 0; l < 16; ++l) {
+                int8_t bit = (hm[l] & m) ? 0 : 4;
+                int8_t qi = (int8_t)((q[l] >> shift) & 3);
+                out[o + l] = dl * (float)(int8_t)(qi - bit);
+            }
+            float dl2 = d_all * ((float)scales[is] - 32.0f);
+            ++is;
+            for (int l = 0; l < 16; ++l) {
+                int8_t bit = (hm[l + 16] & m) ? 0 : 4;
+                int8_t qi = (int8_t)((q[l + 16] >> shift) & 3);
+                out[o + 16 + l] = dl2 * (float)(int8_t)(qi - bit);
+            }
+            o += 32;
+            shift += 2;
+            m = (uint8_t)(m << 1);
+        }
+        q += 32;
+    }
+}
+
+void orc_q5k_block(const uint8_t *bytes, float *out) /* dequant.rs:454-481 */
+{
+    float d = f16_at(bytes), min = f16_at(bytes + 2);
+    const uint8_t *sc = bytes + 4, *qh = bytes + 16, *ql = bytes + 48;
+    int o = 0, is = 0;
+    uint8_t u1 = 1, u2 = 2;
+    for (int j = 0; j < 4; ++j) {
+        uint8_t s1, m1, s2, m2;
+        scale_min_k4(is, sc, &s1, &m1);
+        scale_min_k4(is + 1, sc, &s2, &m2);
+        float d1 = d * (float)s1, m1f = min * (float)m1;
+        float d2 = d * (float)s2, m2f = min * (float)m2;
+        for (int l = 0; l < 32; ++l)
+            out[o + l] = d1 * ((float)(ql[l] & 0xF) + ((qh[l] & u1) ? 16.0f : 0.0f)) - m1f;
+        for (int l = 0; l < 32; ++l)
+            out[o + 32 + l] = d2 * ((float)(ql[l] >> 4) + ((qh[l] & u2) ? 16.0f : 0.0f)) - m2f;
+        o += 64;
+        ql += 32;
+        is += 2;
+        u1 = (uint8_t)(u1 << 2);
+        u2 = (uint8_t)(u2 << 2);
+    }
+}
+
+void orc_q6k_block(const uint8_t *bytes, float *out) /* dequant.rs:484-510 */
+{
+    const uint8_t *ql = bytes, *qh = bytes + 128;
+    const int8_t *sc = (const int8_t *)(bytes + 192);
+    float d = f16_at(bytes + 208);
+    int o = 0, qlo = 0, qho = 0, sco = 0;
+    for (int n = 0; n < 2; ++n) {
+        for (int l = 0; l < 32; ++l) {
+            int is = l / 16;
+            int h = qh[qho + l];
+            int8_t q1 = (int8_t)((int8_t)((ql[qlo + l] & 0xF) | (((h >> 0) & 3) << 4)) - 32);
+            int8_t q2 = (int8_t)((int8_t)((ql[qlo + l + 32] & 0xF) | (((h >> 2) & 3) << 4)) - 32);
+            int8_t q3 = (int8_t)((int8_t)((ql[qlo + l] >> 4) | (((h >> 4) & 3) << 4)) - 32);
+            int8_t q4 = (int8_t)((int8_t)((ql[qlo + l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32);
+            out[o + l] = d * (float)sc[sco + is] * (float)q1;
+            out[o + l + 32] = d * (float)sc[sco + is + 2] * (float)q2;
+            out[o + l + 64] = d * (float)sc[sco + is + 4] * (float)q3;
+            out[o + l + 96] = d * (float)sc[sco + is + 6] * (float)q4;
+        }
+        o += 128;
+        qlo += 64;
+        qho += 32;
+        sco += 8;
+    }
+}
+
+/* Bytes and elements of one block of a block-quantised kind (QuantKind::
+ * block_bytes / block_elems, dequant.rs:350-372); 0 for other kinds. */
+static int qblock_geometry(int kind, size_t *bb, size_t *be, void (**fn)(const uint8_t *, float *))
+{
+    switch (kind) {
+    case ORC_KIND_TQ1_0: *bb = 54; *be = 256; *fn = orc_tq1_block; return 1;
+    case ORC_KIND_Q8_0: *bb = 34; *be = 32; *fn = orc_q8_block; return 1;
+    case ORC_KIND_Q3K: *bb = 110; *be = 256; *fn = orc_q3k_block; return 1;
+    case ORC_KIND_Q4K: *bb = 144; *be = 256; *fn = orc_q4k_block; return 1;
+    case ORC_KIND_Q5K: *bb = 176; *be = 256; *fn = orc_q5k_block; return 1;
+    case ORC_KIND_Q6K: *bb = 210; *be = 256; *fn = orc_q6k_block; return 1;
+    default: return 0;
+    }
+}
+
+/* dequant_{q8,q3k,q4k,q5k,q6k}_row (dequant.rs:285-310, 532-560): the
+ * row's whole blocks, row_bytes / block_bytes of them.  -1 for a kind that
+ * is not block-quantised. */
+int orc_dequant_qblock_row(int kind, const uint8_t *payload, size_t row, size_t row_bytes, float *out)
+{
+    size_t bb, be;
+    void (*fn)(const uint8_t *, float *);
+    if (!qblock_geometry(kind, &bb, &be, &fn)) return -1;
+    size_t start = row * row_bytes, blocks = row_bytes / bb;
+    for (size_t b = 0; b < blocks; ++b) fn(payload + start + b * bb, out + b * be);
+    return 0;
+}
+
 size_t orc_row_bytes(int kind, size_t k) /* dequant.rs:350-387 */
 {
     switch (kind) {
@@ -441,29 +603,42 @@ void orc_matmul_tl1(const uint8_t *payload, size_t out_len, size_t in_len,
     orc_parallel_for(out_len, nthreads, tl1_mm_range, &c);
 }
 
-struct tq1_ctx {
+struct qblock_ctx {
     const uint8_t *payload;
+    int kind;
     size_t in_len, rb;
     const float *x;
     float *y;
 };
 
-static void tq1_range(void *p, size_t lo, size_t hi)
+/* matvec_qblock's worker (ops.rs:104-124): a zeroed row of in_len floats per
+ * worker, the row's blocks decoded into it, then dot with x. */
+static void qblock_range(void *p, size_t lo, size_t hi)
 {
-    struct tq1_ctx *c = (struct tq1_ctx *)p;
-    float *row = (float *)malloc(sizeof(float) * c->in_len);
+    struct qblock_ctx *c = (struct qblock_ctx *)p;
+    float *row = (float *)calloc(c->in_len ? c->in_len : 1, sizeof(float));
     for (size_t r = lo; r < hi; ++r) {
-        orc_dequant_tq1_row(c->payload, r, c->rb, row);
+        orc_dequant_qblock_row(c->kind, c->payload, r, c->rb, row);
         c->y[r] = orc_dot(row, c->x, c->in_len);
     }
     free(row);
 }
 
+int orc_matvec_qblock(const uint8_t *payload, int kind, size_t out_len, size_t in_len,
+                      const float *x, float *y, int nthreads)
+{ /* ops.rs:101-128 */
+    size_t bb, be;
+    void (*fn)(const uint8_t *, float *);
+    if (!qblock_geometry(kind, &bb, &be, &fn)) return -1;
+    struct qblock_ctx c = {payload, kind, in_len, orc_row_bytes(kind, in_len), x, y};
+    orc_parallel_for(out_len, nthreads, qblock_range, &c);
+    return 0;
+}
+
 void orc_matvec_tq1(const uint8_t *payload, size_t out_len, size_t in_len,
                     const float *x, float *y, int nthreads)
 { /* ops.rs:101-128 */
-    struct tq1_ctx c = {payload, in_len, orc_row_bytes(ORC_KIND_TQ1_0, in_len), x, y};
-    orc_parallel_for(out_len, nthreads, tq1_range, &c);
+    orc_matvec_qblock(payload, ORC_KIND_TQ1_0, out_len, in_len, x, y, nthreads);
 }
 
 void orc_matvec_dense(const uint8_t *payload, int kind, size_t out_len,
@@ -501,8 +676,12 @@ int orc_matvec_q(const uint8_t *payload, int kind, size_t out_len,
         orc_matvec_tl1(payload, out_len, in_len, x, y, 1, nthreads);
         return 0;
     case ORC_KIND_TQ1_0:
-        orc_matvec_tq1(payload, out_len, in_len, x, y, nthreads);
-        return 0;
+    case ORC_KIND_Q8_0:
+    case ORC_KIND_Q3K:
+    case ORC_KIND_Q4K:
+    case ORC_KIND_Q5K:
+    case ORC_KIND_Q6K:
+        return orc_matvec_qblock(payload, kind, out_len, in_len, x, y, nthreads);
     case ORC_KIND_I2_S: { /* x quantised by quantize_row_i8_s, then the I2_S mul_mat */
         if ((out_len * in_len) % 128) return -1;
         int8_t *q = (int8_t *)malloc(in_len ? in_len : 1);

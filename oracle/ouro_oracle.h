@@ -61,6 +61,22 @@ void orc_dequant_tl1_row(const uint8_t *payload, size_t row, size_t row_elems,
 void orc_tq1_block(const uint8_t *b54, float *out256); /* dequant.rs:50-80 */
 void orc_dequant_tq1_row(const uint8_t *payload, size_t row, size_t row_bytes,
                          float *out);                  /* dequant.rs:96-105 */
+/* The Q8_0 and K-quant blocks (ggml's layouts, as dequant.rs decodes them):
+ *   Q8_0 34 B / 32: d f16, qs int8[32]                    (dequant.rs:225-231)
+ *   Q4_K 144 B / 256: d, dmin f16, scales[12], qs[128]     (dequant.rs:257-282)
+ *   Q3_K 110 B / 256: hmask[32], qs[64], scales[12], d     (dequant.rs:398-451)
+ *   Q5_K 176 B / 256: d, dmin, scales[12], qh[32], qs[128] (dequant.rs:454-481)
+ *   Q6_K 210 B / 256: ql[128], qh[64], scales int8[16], d  (dequant.rs:484-510) */
+void orc_q8_block(const uint8_t *b34, float *out32);
+void orc_q4k_block(const uint8_t *b144, float *out256);
+void orc_q3k_block(const uint8_t *b110, float *out256);
+void orc_q5k_block(const uint8_t *b176, float *out256);
+void orc_q6k_block(const uint8_t *b210, float *out256);
+/* dequant_{tq1,q8,q3k,q4k,q5k,q6k}_row (dequant.rs:96-105,285-310,532-560):
+ * the whole blocks of row `row` (row_bytes / block bytes of them) into out.
+ * -1 for a kind that is not block-quantised. */
+int orc_dequant_qblock_row(int kind, const uint8_t *payload, size_t row,
+                           size_t row_bytes, float *out);
 /* QuantKind::row_bytes (dequant.rs:376-387); 0 for an unknown kind. */
 size_t orc_row_bytes(int kind, size_t k);
 /* QuantKind::from_dtype (dequant.rs:334-348): 1 if supported, else 0. */
@@ -81,6 +97,11 @@ void orc_matvec_tl1(const uint8_t *payload, size_t out_len, size_t in_len,
  * tl1_rows_avx2_k (ops.rs:381-473). */
 void orc_matmul_tl1(const uint8_t *payload, size_t out_len, size_t in_len,
                     const float *x, size_t k, float *y, int simd, int nthreads);
+/* matvec_qblock (ops.rs:101-128) for TQ1_0, Q8_0, Q3_K..Q6_K: each row
+ * decoded into a zeroed row of in_len floats, then dot with x.  -1 for
+ * another kind. */
+int orc_matvec_qblock(const uint8_t *payload, int kind, size_t out_len,
+                      size_t in_len, const float *x, float *y, int nthreads);
 /* matvec_qblock for TQ1_0 (ops.rs:101-128): dequant row, then dot. */
 void orc_matvec_tq1(const uint8_t *payload, size_t out_len, size_t in_len,
                     const float *x, float *y, int nthreads);

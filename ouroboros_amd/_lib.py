@@ -23,6 +23,7 @@ STATUS_NAMES = {
 }
 
 KIND_F32, KIND_F16, KIND_BF16, KIND_TQ1_0, KIND_TL1, KIND_I2_S, KIND_I2 = 0, 1, 30, 34, 143, 36, 0x4932
+KIND_Q8_0, KIND_Q3K, KIND_Q4K, KIND_Q5K, KIND_Q6K = 8, 11, 12, 13, 14
 DT_F32, DT_BF16 = 0, 1
 FWHT_INVERSE = 1
 GDN_L2NORM_QK, GDN_SCALE_Q, GDN_KHEAD_DIV, GDN_V_GROUPED = 1, 2, 4, 8

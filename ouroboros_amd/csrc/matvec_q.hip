@@ -25,6 +25,9 @@ int i2s_gemm(const uint8_t *i2s, size_t out_len, size_t in_len, const int8_t *xq
 size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw);
+bool is_kquant(int kind);
+int kq_matmul(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k, float *y,
+              void *stream);
 size_t tq1_lut_partial_floats(size_t out_len, size_t in_len);
 bool tq1_lut_fits(const void *payload, size_t in_len);
 int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
@@ -242,6 +245,7 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     if (!out_len || !in_len || !k) return fail(OURO_ERR_SHAPE, "matvec_q: empty shape");
     if (out_len > 0x7fffffffULL || in_len > 0x7fffffffULL || k > 0x7fffffffULL)
         return fail(OURO_ERR_SHAPE, "matvec_q: shape too large");
+    if (is_kquant(kind)) return kq_matmul(payload, kind, out_len, in_len, x, k, y, stream);
     switch (kind) {
     case OURO_KIND_TL1:
         if (in_len % 128) return fail(OURO_ERR_SHAPE, "matvec_q TL1: in_len %zu not a multiple of 128", in_len);

@@ -67,6 +67,11 @@ size_t ref_row_bytes(int kind, size_t k) {  // QuantKind::row_bytes (dequant.rs:
     case OURO_KIND_BF16: return k * 2;
     case OURO_KIND_TL1: return k / 128 * 28;
     case OURO_KIND_TQ1_0: return k / 256 * 54;
+    case OURO_KIND_Q8_0: return k / 32 * 34;
+    case OURO_KIND_Q3K: return k / 256 * 110;
+    case OURO_KIND_Q4K: return k / 256 * 144;
+    case OURO_KIND_Q5K: return k / 256 * 176;
+    case OURO_KIND_Q6K: return k / 256 * 210;
     case OURO_KIND_I2:
     case OURO_KIND_I2_S: return k / 4;
     default: return 0;

@@ -19,6 +19,11 @@ class QuantKind(enum.IntEnum):
     F32 = _lib.KIND_F32
     F16 = _lib.KIND_F16
     BF16 = _lib.KIND_BF16
+    Q8_0 = _lib.KIND_Q8_0
+    Q3K = _lib.KIND_Q3K
+    Q4K = _lib.KIND_Q4K
+    Q5K = _lib.KIND_Q5K
+    Q6K = _lib.KIND_Q6K
     TQ1_0 = _lib.KIND_TQ1_0
     TL1 = _lib.KIND_TL1
     I2_S = _lib.KIND_I2_S
@@ -26,20 +31,22 @@ class QuantKind(enum.IntEnum):
 
     @classmethod
     def from_dtype(cls, dtype_id: int) -> "QuantKind | None":
-        """QuantKind::from_dtype (dequant.rs:334-348) for the kinds on this path."""
+        """QuantKind::from_dtype (dequant.rs:334-348): the reference's set of
+        ggml dtype ids; None for any other id, I2_S's 36 included (bitnet.cpp
+        tensors are uploaded by kind, not from a shard's dtype)."""
         try:
             k = cls(dtype_id)
         except ValueError:
             return None
-        return None if k is cls.I2 else k
+        return None if k in (cls.I2, cls.I2_S) else k
 
     def block_bytes(self) -> int:  # dequant.rs:351-363
         return {self.F32: 4, self.F16: 2, self.BF16: 2, self.TQ1_0: 54, self.TL1: 28, self.I2_S: 32,
-                self.I2: 1}[self]
+                self.I2: 1, self.Q8_0: 34, self.Q3K: 110, self.Q4K: 144, self.Q5K: 176, self.Q6K: 210}[self]
 
     def block_elems(self) -> int:  # dequant.rs:366-373
         return {self.F32: 1, self.F16: 1, self.BF16: 1, self.TQ1_0: 256, self.TL1: 128, self.I2_S: 128,
-                self.I2: 4}[self]
+                self.I2: 4, self.Q8_0: 32, self.Q3K: 256, self.Q4K: 256, self.Q5K: 256, self.Q6K: 256}[self]
 
     def row_bytes(self, k: int) -> int:  # dequant.rs:376-387
         return k // self.block_elems() * self.block_bytes()

@@ -177,7 +177,7 @@ def test_kind_errors(gpu):
     from ouroboros_amd._lib import OuroError
 
     with pytest.raises(OuroError) as e:
-        ops.matvec_q(np.zeros(64, np.uint8), 12, 1, 256, np.zeros(256, np.float32))  # Q4_K not on GPU
+        ops.matvec_q(np.zeros(64, np.uint8), 10, 1, 256, np.zeros(256, np.float32))  # Q2_K: not a reference kind
     assert e.value.code == 4
     with pytest.raises(OuroError) as e:
         ops.matvec_q(np.zeros(64, np.uint8), QuantKind.TL1, 1, 100, np.zeros(100, np.float32))

@@ -73,7 +73,10 @@ def test_weight_shape_follows_stage_from_shard(tmp_path):  # mod.rs:114-123
                BmtsTensor("blk.3.attn_norm.weight", [2560], 0, 0, 0),
                BmtsTensor("output.weight", [5120, 248320], 34, 0, 0),
                BmtsTensor("blk.12.bad", [2, 2, 2], 0, 0, 0),
-               BmtsTensor("blk.12.q4k", [256, 1], 12, 0, 0)]
+               BmtsTensor("blk.12.q4k", [256, 1], 12, 0, 0),
+               BmtsTensor("blk.12.q6k", [512, 3], 14, 0, 0),
+               BmtsTensor("blk.12.i2s", [256, 4], 36, 0, 0),
+               BmtsTensor("blk.12.q2k", [256, 4], 10, 0, 0)]
     write_shard(str(p), 2, tensors, b"")
     with BmtsShard(str(p)) as shard:
         assert shard.weight_shape("blk.3.ffn_up.weight") == (QuantKind.TL1, 6912, 2560)
@@ -81,8 +84,13 @@ def test_weight_shape_follows_stage_from_shard(tmp_path):  # mod.rs:114-123
         assert shard.weight_shape("output.weight") == (QuantKind.TQ1_0, 248320, 5120)
         with pytest.raises(ShardError):
             shard.weight_shape("blk.12.bad")  # rank 3
-        with pytest.raises(ShardError):
-            shard.weight_shape("blk.12.q4k")  # a kind this path does not decode
+        # the K-quant ids of QuantKind::from_dtype (dequant.rs:334-348)
+        assert shard.weight_shape("blk.12.q4k") == (QuantKind.Q4K, 1, 256)
+        assert shard.weight_shape("blk.12.q6k") == (QuantKind.Q6K, 3, 512)
+        # from_dtype's None: I2_S (36) and Q2_K (10) are not in the reference's set
+        for name in ("blk.12.i2s", "blk.12.q2k"):
+            with pytest.raises(ShardError):
+                shard.weight_shape(name)
         assert shard.layers() == [3, 12]
 
 
