@@ -54,7 +54,6 @@ FW_Q_BYTES = FW_ROWS * FW_N * 2 + FW_ROWS * FW_N + FW_ROWS * 4
 # Chunked prefill: 4 sequences x 4096 tokens, chunk 64, same heads.
 PF_SEQ, PF_LEN, PF_C = 4, 4096, 64
 PF_T = PF_SEQ * PF_LEN
-PF_CPU_LEN = 512  # tokens per sequence of the CPU baseline's sample
 # Each contraction counted once per (chunk, v-head): K K^T, Q K^T (64x64x128),
 # K S0, Q S0 (64x128x128), T R, Pt U (64x64x128), K^T U (128x64x128).
 PF_FLOP_CHUNK_HEAD = 2 * (64 * 64 * 128 * 4 + 64 * 128 * 128 * 2 + 128 * 64 * 128)
@@ -322,6 +321,45 @@ def bench_tl1(stream, steps, warmup):
     ms_tq1 = time_events(stream, lambda _i: call("ouro_matvec_q", wq.ptr, KIND_TQ1_0, TL1_OUT, TL1_IN, xd.ptr, y.ptr,
                                                  stream), n, 2)
     return ms, ms_am, ms_raw, ms_tq1, tq.nbytes
+
+
+# The block-quantised kinds of matvec_q (Q8_0, Q3_K..Q6_K) on the lm_head
+# probe shape and on the 6912x2560 layer (64 rotating copies, ~0.7-1.2 GB).
+KQ_KINDS = (("Q8_0", 8, 34, 32), ("Q3_K", 11, 110, 256), ("Q4_K", 12, 144, 256), ("Q5_K", 13, 176, 256),
+            ("Q6_K", 14, 210, 256))
+
+
+def bench_kquant(stream, steps, warmup):
+    """ouro_matvec_q on raw ggml blocks (matvec_qblock, ops.rs:101-128):
+    random code bytes with f16 scales in a model's range, fp32 x and y."""
+    from ouroboros_amd._lib import call
+    from ouroboros_amd.device import DeviceBuffer
+
+    rng = np.random.default_rng(23)
+    rows = []
+    for name, kind, bb, be in KQ_KINDS:
+        for out_len, in_len, copies in ((TL1_OUT, TL1_IN, 1), (GEMV_OUT, GEMV_IN, 64)):
+            wb = out_len * (in_len // be) * bb
+            p = rng.integers(0, 256, wb, dtype=np.uint8)
+            blk = p.reshape(-1, bb)
+            for o in ({8: [0], 11: [108], 12: [0, 2], 13: [0, 2], 14: [208]}[kind]):
+                d = rng.uniform(0.002, 0.02, blk.shape[0]).astype(np.float16).view(np.uint16)
+                blk[:, o], blk[:, o + 1] = d & 0xFF, d >> 8
+            w = DeviceBuffer((wb * copies,), np.uint8)
+            for c in range(copies):  # the same bytes in each copy; each launch reads a different one
+                call("ouro_memcpy_htod", w.ptr + c * wb, p.ctypes.data, wb)
+            del p, blk
+            xd = DeviceBuffer.from_host(rng.standard_normal(in_len).astype(np.float32))
+            y = DeviceBuffer((out_len,), np.float32)
+            n = max(3, steps // 5) if copies == 1 else steps
+            ms = time_events(stream, lambda i: call("ouro_matvec_q", w.ptr + (i % copies) * wb, kind, out_len,
+                                                    in_len, xd.ptr, y.ptr, stream), n, 2)
+            alg = wb + 4 * (in_len + out_len)
+            gbs = alg / (ms * 1e-3) / 1e9
+            rows.append({"kind": name, "out_len": out_len, "in_len": in_len, "us_per_call": round(ms * 1e3, 2),
+                         "bytes_per_call": alg, "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del w
+    return rows
 
 
 def bench_gemm(stream, steps, warmup, orc):
@@ -688,10 +726,8 @@ def prefill_cpu_baseline(orc) -> dict:
     (sequence, head) pairs over threads, on the 4 x 4096-token workload."""
     nt, info = cpu_threads()
     rng = np.random.default_rng(11)
-    # a bounded sample: the first 512 tokens of each of the 4 sequences (the
-    # loop costs the same per token at any length, and the 128 (sequence,
-    # head) pairs keep every thread busy)
-    L = PF_CPU_LEN
+    # the whole workload: 4 sequences of 4096 tokens (~0.6 s a run on 16 threads)
+    L = PF_LEN
     T, Hk, Hv, d = PF_SEQ * L, GDN_HK, GDN_HV, GDN_D
     q = rng.standard_normal((T, Hk, d)).astype(np.float32)
     k = rng.standard_normal((T, Hk, d)).astype(np.float32)
@@ -706,11 +742,11 @@ def prefill_cpu_baseline(orc) -> dict:
         st[:] = state0
         orc.gdn_prefill_varlen(st, q, k, v, gate, beta, cu, Hk, Hv, d, orc.L2NORM_QK | orc.SCALE_Q, 1e-6, nt)
 
-    dt, n = cpu_median(call, budget_s=0.0)
+    dt, n = cpu_median(call, warmup=1, min_runs=5, budget_s=0.0)
     return {"value": round(T / dt, 1), "unit": "tokens/s", "cores": nt, "kind": "port",
-            "sample": f"median of {n} runs (after 3 warm-ups) of the oracle's token-loop prefill of 4 x {L} tokens "
-                      f"(the first {L} of each 4096-token sequence; f32, {nt} threads over the 128 (sequence, head) "
-                      f"pairs): {dt * 1e3:.1f} ms/run",
+            "sample": f"median of {n} runs (after 1 warm-up) of the oracle's token-loop prefill of the whole "
+                      f"workload, 4 x {L} tokens (f32, {nt} threads over the 128 (sequence, head) pairs): "
+                      f"{dt * 1e3:.1f} ms/run",
             "cpu": _cpu_model(), "threads": info}
 
 
@@ -723,6 +759,11 @@ def load_traffic() -> dict:
         return json.loads(f.read_text()).get("kernels", {})
     except (OSError, ValueError):
         return {}
+
+
+TRAFFIC_SOURCE = ("profiles/pmc_traffic.json: HBM bytes per dispatch from two rocprofv3 --pmc runs of bench.py "
+                  "(FETCH_SIZE, then WRITE_SIZE), each scaled by what the counter reads for the 512 MiB device "
+                  "copy of the same run; measured in that profiling run, not in this one")
 
 
 def traffic_of(traffic: dict, prefix: str, grid: int | None = None):
@@ -750,7 +791,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-stack", action="store_true",
                     help="skip the hybrid-stack leg (profiling runs of the kernel legs)")
-    ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "fwht", "prefill", "copy", "stack"],
+    ap.add_argument("--only", choices=["gemv", "gemm", "gdn", "layer", "tl1", "kquant", "fwht", "prefill", "copy",
+                                       "stack"],
                     default=None,
                     help="run one workload (for profiling)")
     args = ap.parse_args()
@@ -780,6 +822,9 @@ def main() -> int:
     if args.only in (None, "tl1"):
         log("TL1 matvec 248320x5120 (lm_head probe)")
         res["tl1"] = bench_tl1(stream, args.steps, args.warmup)
+    if args.only in (None, "kquant"):
+        log("matvec_q on Q8_0 / Q3_K..Q6_K blocks, 248320x5120 and 6912x2560")
+        res["kquant"] = bench_kquant(stream, args.steps, args.warmup)
     if args.only in (None, "gemm"):
         log("ternary GEMM 6912x2560, 4..2048 columns")
         res["gemm"] = bench_gemm(stream, args.steps, args.warmup, orc)
@@ -798,7 +843,8 @@ def main() -> int:
 
     traffic = load_traffic()
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic",
+           "traffic_source": TRAFFIC_SOURCE}
     sec = {}
     if "gemv" in res:
         ms, ms_single, ms_small = res["gemv"]
@@ -859,6 +905,17 @@ def main() -> int:
             "raw_tq1_0_matvec_q_ms": round(ms_tq1, 4),
             "raw_tq1_0_matvec_q_GBs": round((tq1_bytes + 4 * (TL1_IN + TL1_OUT)) / (ms_tq1 * 1e-3) / 1e9, 1),
         }
+    if "kquant" in res:
+        rows = res["kquant"]
+        big = [r for r in rows if r["out_len"] == TL1_OUT]
+        sec["kquant_matvec"] = {
+            "value": round(min(r["GBs"] for r in big), 1), "unit": "GB/s",
+            "config": "ouro_matvec_q on raw ggml Q8_0 / Q3_K / Q4_K / Q5_K / Q6_K blocks (matvec_qblock, "
+                      "ops.rs:101-128), fp32 x and y; value = the slowest kind at 248320x5120",
+            "roofline": {"bound": "hbm", "achieved": round(min(r["GBs"] for r in big), 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(min(r["frac"] for r in big), 4)},
+            "by_kind": rows,
+        }
     if "gemm" in res:
         rows, vendor = res["gemm"]
         main = next(r for r in rows if r["cols"] == GM_COLS_MAIN)
@@ -912,10 +969,13 @@ def main() -> int:
         sec["gdn_prefill"] = {
             "value": round(PF_T / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_call": round(ms, 4),
             "config": "4 seqs x 4096 tokens packed varlen, chunk 64, Hk=16, Hv=32, d=128, bf16 q/k/v, fp32 state/out",
-            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_sum(traffic, ["gdn_chunk_prep_kernel", "gdn_chunk_scan_kernel"])},
+            # the binding roof: at 154 flop/B (below the bf16 ridge of 312) HBM bounds the call
+            "roofline": {"bound": "hbm" if t_mem >= t_mfma else "mfma", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
+                         "traffic": traffic_sum(traffic, ["gdn_chunk_prep_kernel", "gdn_chunk_scan_kernel"])},
+            "mfma_roofline": {"achieved": round(tf, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
             "algorithmic_gflop": round(PF_FLOPS / 1e9, 2), "bytes": PF_BYTES, "hbm_GBs": round(gbs, 1),
-            "frac_of_min_roofline": round(max(t_mem, t_mfma) / (ms * 1e-3), 4),
         }
     if "stack" in res:
         pf_ms, dec_ms, dev_bytes, T, card, lens, check = res["stack"]

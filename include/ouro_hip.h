@@ -6,19 +6,27 @@
  * reference function it replaces (file:line in the reference tree).  All
  * compute entry points work on DEVICE buffers owned by the caller, are
  * stream-ordered (asynchronous w.r.t. the host) and never allocate device
- * memory, except the documented workspace users (ouro_matvec_q /
- * ouro_matmul_q for the 2-bit kinds), which take memory from a per-device
- * library workspace that is grown on first use and kept until
- * ouro_shutdown().
+ * memory, except the documented workspace users, which take memory from a
+ * library workspace kept per (device, stream), grown on first use (after a
+ * synchronise of that stream) and kept until ouro_stream_destroy() of the
+ * stream or ouro_shutdown():
+ *   - ouro_matvec_q / ouro_matmul_q on the 2-bit kinds (the int8
+ *     activations of x);
+ *   - ouro_matvec_q on a raw TL1 or TQ1_0 payload of 8192 rows or more
+ *     (k == 1): the lookup kernels' per-block partial sums;
+ *   - ouro_gdn_chunk_prefill with a NULL workspace.
+ * A weight handle (ouro_weight_upload) or ouro_matvec_q_noalloc avoids them.
  *
  * Conventions
- *  - Library scratch is per device, not per stream: ouro_finite_argmax, the
- *    library workspace (ouro_matvec_q / ouro_matmul_q on the 2-bit kinds,
- *    ouro_gdn_chunk_prefill and ouro_gdn_layer_decode with a NULL
- *    workspace), the static scratch of ouro_matvec_q_noalloc and each
- *    weight handle's own scratch are each shared by every call that uses
- *    them on that device.  Such calls must be ordered: issue them on one
- *    stream (or synchronise between streams); overlapping calls race.
+ *  - Scratch is per stream: the library workspace, the ouro_finite_argmax
+ *    key slots (the null stream's made by ouro_init, another stream's on its
+ *    first call) and each weight handle's scratch (the null stream's made at
+ *    upload, another stream's on the handle's first call there) are kept
+ *    per (device, stream), so calls on different streams never share any;
+ *    calls on one stream are ordered by it.  The first call on a new stream
+ *    allocates that stream's share (hipMalloc) and is not capturable.  The
+ *    one exception is the static array of ouro_matvec_q_noalloc: one per
+ *    device, shared by every stream (overlapping calls race).
  *    Entry points given caller buffers share nothing.
  *  - Return value: OURO_OK (0) or an ouro_status code.  The failing call's
  *    message is kept in a thread-local buffer, read with ouro_last_error().
@@ -256,7 +264,10 @@ int ouro_gemm_i2_mfma(const uint8_t *w_mfma, size_t out_len, size_t in_len,
  *                     in_len % 256 == 0, in_len <= 32768)
  *   OURO_KIND_I2    - tiled I2 + scale
  *   For both ternary 2-bit kinds x is quantised per call (quantize_row_i8_s,
- *   above) into the library workspace.
+ *   above) into the library workspace.  TL1 and TQ1_0 payloads of 8192 rows
+ *   or more run the table-lookup kernels, whose per-block partial sums also
+ *   live in the library workspace (per stream; ouro_matvec_q_noalloc or a
+ *   weight handle keeps these calls allocation-free).
  * Floating-point sums are not in the reference's order; results agree to
  * float32 rounding (the reference's own fused-vs-scalar bar is rel 1e-5,
  * ops.rs:800-838). */

@@ -53,22 +53,13 @@ int argmax_final(const unsigned long long *keys, int nk, int32_t *idx, void *str
     return check_launch("argmax_final_kernel");
 }
 
-namespace {
-std::mutex g_am_mu;
-void *g_am_scratch[64] = {};  // per device ordinal: kArgmaxBlocks keys
-}  // namespace
 
-// Called by ouro_init with the device current: the argmax scratch is
-// allocated there, once per device, so ouro_finite_argmax allocates nothing.
-int argmax_scratch_init(int dev) {
-    if (dev < 0 || dev >= 64) return fail(OURO_ERR_NO_DEVICE, "argmax: device %d out of range", dev);
-    std::lock_guard<std::mutex> lock(g_am_mu);
-    if (!g_am_scratch[dev]) {
-        void *p = nullptr;
-        if (hipMalloc(&p, kArgmaxBlocks * 8) != hipSuccess)
-            return fail(OURO_ERR_HIP, "argmax: scratch allocation failed");
-        g_am_scratch[dev] = p;
-    }
+// Called by ouro_init with the device current: the null stream's key slots
+// are allocated there, so ouro_finite_argmax on the null stream allocates
+// nothing; any other stream gets its own slots on its first call.
+int argmax_scratch_init(int) {
+    if (!stream_scratch(SCRATCH_ARGMAX, kArgmaxBlocks * 8, nullptr, kArgmaxBlocks * 8))
+        return fail(OURO_ERR_HIP, "argmax: scratch allocation failed");
     return OURO_OK;
 }
 
@@ -80,13 +71,8 @@ extern "C" {
 
 int ouro_finite_argmax(const float *y, size_t n, int32_t *idx, void *stream) {
     OURO_REQUIRE_INIT();
-    const int dev = current_device();
-    void *scratch = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_am_mu);
-        if (dev >= 0 && dev < 64) scratch = g_am_scratch[dev];
-    }
-    if (!scratch) return fail(OURO_ERR_NOT_INIT, "ouro_finite_argmax: ouro_init() did not set up device %d", dev);
+    void *scratch = stream_scratch(SCRATCH_ARGMAX, kArgmaxBlocks * 8, stream, kArgmaxBlocks * 8);
+    if (!scratch) return OURO_ERR_HIP;
     return argmax_f32(y, n, scratch, idx, stream);
 }
 

@@ -39,8 +39,13 @@ int current_device();
 // Checks the launch that was just enqueued.
 int check_launch(const char *what);
 
-// Per-device workspace owned by the library (grown on demand, freed by
-// ouro_shutdown).  Returns nullptr and sets the error on failure.
+// Library scratch per (device, stream, purpose): grown on demand (after a
+// synchronise of that stream), freed by ouro_stream_destroy of the stream or
+// ouro_shutdown.  Calls on different streams never share a block.  Returns
+// nullptr and sets the error on failure.
+enum { SCRATCH_WORKSPACE = 0, SCRATCH_ARGMAX = 1 };
+void *stream_scratch(int kind, size_t bytes, void *stream, size_t min_bytes);
+// The workspace of matvec_q / matmul_q and the chunked prefill (at least 1 MiB).
 void *workspace(size_t bytes, void *stream);
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
@@ -262,6 +267,7 @@ struct PageAssign {
     int slot[kMaxPageAssign];
     int page[kMaxPageAssign];
 };
+static_assert(sizeof(PageAssign) == 516, "PageAssign: kernel argument layout");
 
 // finite_argmax keys (infer/mod.rs:70-83): the value's bits in an
 // order-preserving form (-0 taken as +0, as `>` does) in the high word, the

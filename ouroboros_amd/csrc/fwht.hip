@@ -100,6 +100,9 @@ struct FwhtArgs {
     int n;
     float scale;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (56 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(FwhtArgs) == 56, "FwhtArgs: kernel argument layout");
 
 // Pass P (P >= 1) of a block of 2^LOGB: stages 2^(4P) .. over the <= 16
 // elements of one set, which differ only in index bits 4P .. 4P+NB-1.  The
@@ -249,6 +252,9 @@ struct RowRqArgs {
     unsigned flags;
     float eps, scale;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (104 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(RowRqArgs) == 104, "RowRqArgs: kernel argument layout");
 
 __device__ __forceinline__ long long rq_offset(long long row, int c16, int n, int tiles) {
     if (!tiles) return row * n + 16LL * c16;

@@ -35,6 +35,8 @@
 // per-row coefficients of the next chunk; two barriers per chunk.
 #include "common.hpp"
 
+#include <atomic>
+
 namespace ouro {
 namespace {
 
@@ -137,6 +139,9 @@ struct ChunkArgs {
     int cu[kMaxSeq + 1];    // token offsets of the sequences
     int coff[kMaxSeq + 1];  // chunk offsets (cumulative chunk counts)
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (2144 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(ChunkArgs) == 2144, "ChunkArgs: kernel argument layout");
 
 __device__ __forceinline__ f32x4 mfma(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -1028,12 +1033,14 @@ int gdn_chunk_prefill(float *state, const void *q, const void *k, const void *v,
         ws = static_cast<unsigned char *>(ouro::workspace(gdn_chunk_ws_bytes(T, N, Hv), stream));
         if (!ws) return OURO_ERR_HIP;
     }
-    static bool attr_set = false;
-    if (!attr_set) {
+    // LDS opt-in once per process (an idempotent call; threads that race
+    // here both make it)
+    static std::atomic<bool> attr_set{false};
+    if (!attr_set.load(std::memory_order_acquire)) {
         int st = set_lds(reinterpret_cast<const void *>(gdn_chunk_scan_kernel), SCAN_LDS);
         if (!st) st = set_lds(reinterpret_cast<const void *>(gdn_chunk_prep_kernel), PREP_LDS);
         if (st) return st;
-        attr_set = true;
+        attr_set.store(true, std::memory_order_release);
     }
     ChunkArgs a{};
     a.q = static_cast<const uint16_t *>(q);

@@ -32,6 +32,9 @@ struct DecodeArgs {
     unsigned flags;
     float eps;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (104 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(DecodeArgs) == 104, "DecodeArgs: kernel argument layout");
 
 // conv_step (qwen35.rs:64-70) of one channel, then SiLU (ops.rs:34-36), in
 // the reference's operation order.
@@ -305,6 +308,9 @@ struct LayerArgs {
     unsigned flags;  // OURO_GDN_KHEAD_DIV, OURO_GDN_V_GROUPED
     float eps;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (112 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(LayerArgs) == 112, "LayerArgs: kernel argument layout");
 constexpr int kLayerWaves = 16;
 
 // The conv channel of item t of the workgroup's (2 + g) * d: q, k, then v

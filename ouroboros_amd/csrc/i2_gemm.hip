@@ -21,6 +21,8 @@
 // -64 * sum(w*x), and acc = -(D >> 6) exactly.
 #include "common.hpp"
 
+#include <cstddef>
+
 #pragma clang fp contract(off)
 
 namespace ouro {
@@ -84,6 +86,9 @@ struct GemmArgs {
     int swiglu;            // rows are (up, gate) pairs: y[N][M/2] = silu(gate) * up (no acc)
     GemmEpilogue epi;      // element-wise step on every stored output (not with acc or swiglu)
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (120 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(GemmArgs) == 120, "GemmArgs: kernel argument layout");
 
 // The SwiGLU of an interleaved (up, gate) row pair, in the row kernel's
 // arithmetic (silu(gate) * up, run_ffn qwen35.rs:802).
@@ -98,6 +103,9 @@ struct MfmaGroup {
     int bstart[kMfmaGroup + 1];
     int np;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (504 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(MfmaGroup) == 504, "MfmaGroup: kernel argument layout");
 
 // Block: 4 wavefronts stacked along rows; wavefront w owns row tiles
 // (4*rb + w)*WR .. +WR-1 and the block's WC column tiles of 16 columns.
@@ -493,6 +501,9 @@ struct SkinnyProblem {
     GemmEpilogue epi;
     int swiglu;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (104 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(SkinnyProblem) == 104, "SkinnyProblem: kernel argument layout");
 struct SkinnyGroup {
     SkinnyProblem p[kSkinnyGroup];
     int bstart[kSkinnyGroup + 1];
@@ -500,6 +511,11 @@ struct SkinnyGroup {
     int tiles;  // column tiles of the whole launch, ceil(N / 16)
     int ncg;    // column groups of WC tiles; workgroup x = row block * ncg + column group
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (464 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(SkinnyGroup) == 464, "SkinnyGroup: kernel argument layout");
+static_assert(offsetof(SkinnyGroup, bstart) == 416 && offsetof(SkinnyGroup, np) == 436 &&
+                  offsetof(SkinnyGroup, ncg) == 460, "SkinnyGroup: kernel argument layout");
 
 template <int WC, int WR>
 __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(SkinnyGroup g) {

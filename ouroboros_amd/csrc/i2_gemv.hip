@@ -136,6 +136,9 @@ struct GemvArgs {
     int32_t *acc;           // optional, same layout as y (matrix 0 only)
     int out_len, in_len, ncols, tiles;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (88 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(GemvArgs) == 88, "GemvArgs: kernel argument layout");
 
 // Row totals of a tile: each lane holds R partial sums (one per row of the
 // tile); row r's total is the sum over the span = 64 / R lanes of group r.
@@ -419,6 +422,9 @@ struct I2sArgs {
     int32_t *acc;            // optional, same layout as y
     int out_len, in_len;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (56 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(I2sArgs) == 56, "I2sArgs: kernel argument layout");
 
 constexpr int kI2sWaves = 4;
 

@@ -18,9 +18,10 @@
 // values and their run sums stay in registers while the workgroup walks row
 // tiles, so x is read once per workgroup.  A workgroup is `slots` side-by-side
 // copies of one row's task set (slots * tasks_per_row threads, rounded up to a
-// whole wavefront), each copy walking R consecutive rows per tile with all R
-// rows' loads issued before any is used; the per-thread sums of a tile meet
-// in LDS and one wavefront per output row adds them.  Blocks of Q8_0, Q3_K
+// whole wavefront, at most 256 unless one row needs more), each copy walking
+// R consecutive rows per tile; the next tile's loads are issued before the
+// current tile is summed; the per-thread sums of a tile meet in LDS and one
+// wavefront per output row adds them.  Blocks of Q8_0, Q3_K
 // and Q6_K (34, 110, 210 bytes) are only 2-byte aligned: their 16-byte pieces
 // are read as the aligned dwords that cover them and shifted into place with
 // v_alignbyte.  Scale bytes are read as bytes.
@@ -128,16 +129,17 @@ template <> struct Fmt<OURO_KIND_Q8_0> {
 };
 
 // Q4_K / Q5_K scales (scale_min_k4, dequant.rs:245-254) of sub-block k from
-// the 12 scale bytes held in words h1 (bytes 0..3), h2 (4..7), h3 (8..11).
+// the 12 scale bytes held in words h1 (bytes 0..3), h2 (4..7), h3 (8..11):
+// for k < 4 the low six bits of byte k (scale) and k + 4 (min); for k >= 4
+// the low / high nibble of byte k + 4 below the top two bits of byte k - 4 /
+// k.  Branch-free (k differs between the lanes of a wavefront): v_bfe with
+// width 0 yields 0.
 __device__ __forceinline__ void scale_min_k4(int k, uint32_t h1, uint32_t h2, uint32_t h3, uint32_t &s, uint32_t &m) {
-    if (k < 4) {
-        s = bfe(h1, 8 * k, 6);
-        m = bfe(h2, 8 * k, 6);
-    } else {
-        const int o = 8 * (k - 4);
-        s = bfe(h3, o, 4) | (bfe(h1, o + 6, 2) << 4);
-        m = bfe(h3, o + 4, 4) | (bfe(h2, o + 6, 2) << 4);
-    }
+    const bool hi = k >= 4;
+    const uint32_t o = 8 * (k & 3);
+    const uint32_t wa = hi ? 4 : 6, wb = hi ? 2 : 0;
+    s = bfe(hi ? h3 : h1, o, wa) | (bfe(h1, o + 6, wb) << 4);
+    m = bfe(hi ? h3 : h2, o + (hi ? 4 : 0), wa) | (bfe(h2, o + 6, wb) << 4);
 }
 
 // Q4_K (dequant.rs:257-282): d, dmin f16, scales[12], qs[128].  Task u:
@@ -278,6 +280,9 @@ struct KqArgs {
     int slots;  // row task sets side by side in a workgroup
     int tiles;  // ceil(out_len / (slots * R))
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (56 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(KqArgs) == 56, "KqArgs: kernel argument layout");
 
 template <int KIND>
 __device__ __forceinline__ void load_x(const float *xc, int blk, int u, float (&xa)[16], float (&xb)[16], float &XA,
@@ -298,43 +303,74 @@ __device__ __forceinline__ void load_x(const float *xc, int blk, int u, float (&
     }
 }
 
+// The per-thread sums of one tile (R rows of each slot) into LDS, then one
+// wavefront per output row adds its task set's sums.
+template <int R>
+__device__ __forceinline__ void tile_reduce(const KqArgs &a, float *red, const float (&v)[R], int tile, int col) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    const int rows_per_tile = a.slots * R;
+    const int wave = t >> 6, lane = t & 63, nwaves = nt >> 6;
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[r * nt + t] = v[r];
+    __syncthreads();
+    for (int o = wave; o < rows_per_tile; o += nwaves) {
+        const int s = o / R, r = o - s * R;
+        const float *src = red + r * nt + s * a.tpr;
+        float acc = 0.f;
+        for (int i = lane; i < a.tpr; i += 64) acc += src[i];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc += xor_shfl(acc, off);
+        const int row = tile * rows_per_tile + o;
+        if (lane == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+    }
+    __syncthreads();
+}
+
+// One workgroup walks tiles blockIdx.x, + gridDim.x, ...; the loads of the
+// next tile are issued before the current one is summed (two register sets).
+// Lanes past the last slot (padding to a whole wavefront) run a clamped copy
+// of a real task whose sums are never read, so no load sits behind a branch.
 template <int KIND, int R, bool AL16, int MAXT>
 __global__ __launch_bounds__(MAXT) void kq_gemv_kernel(KqArgs a) {
     using F = Fmt<KIND>;
     extern __shared__ float red[];  // [R][blockDim.x]
-    const int t = threadIdx.x, nt = blockDim.x;
-    const int slot = t / a.tpr, task = t - slot * a.tpr;
-    const bool active = slot < a.slots;
+    const int t = threadIdx.x;
+    const int slot = min(t / a.tpr, a.slots - 1);
+    const int task = min(t - slot * a.tpr, a.tpr - 1);
     const int blk = task / F::TPB, u = task % F::TPB;
     const int col = blockIdx.y;
-    float xa[16], xb[16], XA = 0.f, XB = 0.f;
-    if (active) load_x<KIND>(a.x + static_cast<long long>(col) * a.in_len, blk, u, xa, xb, XA, XB);
+    float xa[16], xb[16], XA, XB;
+    load_x<KIND>(a.x + static_cast<long long>(col) * a.in_len, blk, u, xa, xb, XA, XB);
     const int rows_per_tile = a.slots * R;
-    const int wave = t >> 6, lane = t & 63, nwaves = nt >> 6;
-    for (int tile = blockIdx.x; tile < a.tiles; tile += gridDim.x) {
-        if (active) {
-            const int row0 = tile * rows_per_tile + slot * R;
-            typename F::Raw raw[R];
+    const uint8_t *wb = a.w + static_cast<long long>(blk) * F::BB;
+    auto issue = [&](typename F::Raw(&raw)[R], int tile) {
+        const int row0 = min(tile, a.tiles - 1) * rows_per_tile + slot * R;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = min(row0 + r, a.out_len - 1);  // clamped rows are computed and dropped
-                raw[r] = F::template load<AL16>(a.w + row * a.row_bytes + static_cast<long long>(blk) * F::BB, u);
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r) red[r * nt + t] = F::dot(raw[r], u, xa, xb, XA, XB);
+        for (int r = 0; r < R; ++r) {
+            const int row = min(row0 + r, a.out_len - 1);  // clamped rows are computed and dropped
+            raw[r] = F::template load<AL16>(wb + row * a.row_bytes, u);
         }
-        __syncthreads();
-        for (int o = wave; o < rows_per_tile; o += nwaves) {
-            const int s = o / R, r = o - s * R;
-            const float *src = red + r * nt + s * a.tpr;
-            float v = 0.f;
-            for (int i = lane; i < a.tpr; i += 64) v += src[i];
+    };
+    auto sum = [&](const typename F::Raw(&raw)[R], int tile) {
+        float v[R];
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
-            const int row = tile * rows_per_tile + o;
-            if (lane == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = v;
-        }
-        __syncthreads();
+        for (int r = 0; r < R; ++r) v[r] = F::dot(raw[r], u, xa, xb, XA, XB);
+        tile_reduce<R>(a, red, v, tile, col);
+    };
+    typename F::Raw ra[R], rb[R];
+    const int g = gridDim.x;
+    int tile = blockIdx.x;
+    if (tile >= a.tiles) return;
+    issue(ra, tile);
+    for (;;) {
+        issue(rb, tile + g);
+        sum(ra, tile);
+        tile += g;
+        if (tile >= a.tiles) break;
+        issue(ra, tile + g);
+        sum(rb, tile);
+        tile += g;
+        if (tile >= a.tiles) break;
     }
 }
 
@@ -362,9 +398,11 @@ __global__ __launch_bounds__(256) void kq_row_kernel(KqArgs a) {
     if (lane == 0) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
 }
 
-// Rows per slot per tile: all of them in flight at once, so the kinds with
-// bigger per-task loads take fewer.
-template <int KIND> constexpr int kRows = (KIND == OURO_KIND_Q8_0 || KIND == OURO_KIND_Q4K) ? 8 : 4;
+// Rows per slot per tile (two tiles' loads in flight): measured best on
+// 248320x5120 and 6912x2560, with workgroups of at most 256 threads (larger
+// ones, 320-512 threads, were 10-40 % slower at the same rows per tile).
+template <int KIND> constexpr int kRows = KIND == OURO_KIND_Q3K ? 1 : (KIND == OURO_KIND_Q5K || KIND == OURO_KIND_Q6K) ? 2 : 4;
+constexpr int kSlotCap = 256;
 
 int cu_count() {
     static std::once_flag once;
@@ -387,16 +425,17 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         hipLaunchKernelGGL(kq_row_kernel<KIND>, grid, dim3(256), 0, s, a);
         return check_launch("kq_row_kernel");
     }
-    // slots: the most rows side by side with the fewest idle lanes, at most
-    // 512 threads (1024 when one row needs more)
-    const int cap = a.tpr > 512 ? kMaxThreads : 512;
+    // slots: up to 256 threads, the most rows side by side with the fewest
+    // idle lanes; a longer row is one task set of up to 1024 threads
     int best = 1;
-    double best_util = 0.0;
-    for (int sl = 1; sl * a.tpr <= cap; ++sl) {
-        const int nt = (sl * a.tpr + 63) / 64 * 64;
-        if (nt > cap) break;
-        const double util = static_cast<double>(sl * a.tpr) / nt;
-        if (util > best_util + 1e-9) best_util = util, best = sl;
+    if (a.tpr <= kSlotCap) {
+        double best_util = 0.0;
+        for (int sl = 1; sl * a.tpr <= kSlotCap; ++sl) {
+            const int nt = (sl * a.tpr + 63) / 64 * 64;
+            if (nt > kSlotCap) break;
+            const double util = static_cast<double>(sl * a.tpr) / nt;
+            if (util > best_util + 1e-9) best_util = util, best = sl;
+        }
     }
     a.slots = best;
     const int nt = (best * a.tpr + 63) / 64 * 64;
@@ -411,7 +450,7 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         else hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, false, MAXT>), grid, dim3(nt), lds, ss, a);
     };
     if (nt <= 512) go(std::integral_constant<int, kRows<KIND>>{}, std::integral_constant<int, 512>{});
-    else go(std::integral_constant<int, 2>{}, std::integral_constant<int, kMaxThreads>{});
+    else go(std::integral_constant<int, 1>{}, std::integral_constant<int, kMaxThreads>{});
     return check_launch("kq_gemv_kernel");
 }
 

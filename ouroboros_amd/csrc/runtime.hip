@@ -15,11 +15,16 @@ namespace {
 thread_local char g_err[512] = "";
 int g_device = -1;
 std::mutex g_ws_mu;
-struct Workspace {
-    void *ptr = nullptr;
-    size_t bytes = 0;
+// Library scratch blocks, one per (device, stream, purpose): calls issued on
+// different streams never share one.
+struct Scratch {
+    int dev;
+    void *stream;
+    int kind;
+    void *ptr;
+    size_t bytes;
 };
-std::vector<Workspace> g_ws;  // indexed by device ordinal
+std::vector<Scratch> g_scratch;
 }  // namespace
 
 int fail(int code, const char *fmt, ...) {
@@ -41,35 +46,52 @@ int check_launch(const char *what) {
     return OURO_OK;
 }
 
-void *workspace(size_t bytes, void *stream) {
+void *stream_scratch(int kind, size_t bytes, void *stream, size_t min_bytes) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
-    int dev = g_device;
+    const int dev = g_device;
     if (dev < 0) {
         fail(OURO_ERR_NOT_INIT, "ouro_init() not called");
         return nullptr;
     }
-    if (static_cast<size_t>(dev) >= g_ws.size()) g_ws.resize(dev + 1);
-    Workspace &w = g_ws[dev];
-    if (w.bytes >= bytes) return w.ptr;
-    // Growing: work already queued may still read the old block.
-    if (w.ptr) {
-        if (hipStreamSynchronize(as_stream(stream)) != hipSuccess ||
-            hipDeviceSynchronize() != hipSuccess) {
-            fail(OURO_ERR_HIP, "workspace: synchronize before growth failed");
+    Scratch *w = nullptr;
+    for (Scratch &e : g_scratch)
+        if (e.dev == dev && e.stream == stream && e.kind == kind) w = &e;
+    if (w && w->bytes >= bytes) return w->ptr;
+    if (w) {  // growing: work already queued on this stream may still read the old block
+        if (hipStreamSynchronize(as_stream(stream)) != hipSuccess) {
+            fail(OURO_ERR_HIP, "scratch: synchronize before growth failed");
             return nullptr;
         }
-        (void)hipFree(w.ptr);
-        w.ptr = nullptr;
-        w.bytes = 0;
+        (void)hipFree(w->ptr);
+        w->ptr = nullptr;
+        w->bytes = 0;
+    } else {
+        g_scratch.push_back(Scratch{dev, stream, kind, nullptr, 0});
+        w = &g_scratch.back();
     }
-    size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (hipMalloc(&w.ptr, want) != hipSuccess) {
-        w.ptr = nullptr;
-        fail(OURO_ERR_HIP, "workspace: hipMalloc(%zu) failed", want);
+    const size_t want = bytes < min_bytes ? min_bytes : bytes;
+    if (hipMalloc(&w->ptr, want) != hipSuccess) {
+        w->ptr = nullptr;
+        fail(OURO_ERR_HIP, "scratch: hipMalloc(%zu) failed", want);
         return nullptr;
     }
-    w.bytes = want;
-    return w.ptr;
+    w->bytes = want;
+    return w->ptr;
+}
+
+void *workspace(size_t bytes, void *stream) { return stream_scratch(SCRATCH_WORKSPACE, bytes, stream, 1u << 20); }
+
+// Frees the scratch blocks of one stream (after its work has finished).
+void release_stream_scratch(void *stream) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (size_t i = 0; i < g_scratch.size();) {
+        if (g_scratch[i].stream == stream && g_scratch[i].dev == g_device) {
+            (void)hipFree(g_scratch[i].ptr);
+            g_scratch.erase(g_scratch.begin() + static_cast<long>(i));
+        } else {
+            ++i;
+        }
+    }
 }
 
 }  // namespace ouro
@@ -117,21 +139,24 @@ int ouro_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(OURO_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950",
                     device, prop.gcnArchName);
-    const int st = argmax_scratch_init(device);
-    if (st) return st;
+    const int prev = g_device;
     g_device = device;
+    const int st = argmax_scratch_init(device);
+    if (st) {
+        g_device = prev;
+        return st;
+    }
     return OURO_OK;
 }
 
 int ouro_shutdown(void) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
-    for (size_t d = 0; d < g_ws.size(); ++d) {
-        if (!g_ws[d].ptr) continue;
-        (void)hipSetDevice(static_cast<int>(d));
+    for (Scratch &e : g_scratch) {
+        (void)hipSetDevice(e.dev);
         (void)hipDeviceSynchronize();
-        (void)hipFree(g_ws[d].ptr);
-        g_ws[d] = Workspace{};
+        (void)hipFree(e.ptr);
     }
+    g_scratch.clear();
     if (g_device >= 0) (void)hipSetDevice(g_device);
     return OURO_OK;
 }
@@ -201,7 +226,11 @@ int ouro_stream_create(void **stream) {
 
 int ouro_stream_destroy(void *stream) {
     OURO_REQUIRE_INIT();
-    if (stream) OURO_HIP_TRY(hipStreamDestroy(as_stream(stream)));
+    if (stream) {
+        OURO_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+        release_stream_scratch(stream);
+        OURO_HIP_TRY(hipStreamDestroy(as_stream(stream)));
+    }
     return OURO_OK;
 }
 

@@ -125,6 +125,7 @@ struct ouro_stack {
     float *o = nullptr, *g = nullptr, *qbuf = nullptr, *gbuf = nullptr, *kbuf = nullptr, *vbuf = nullptr;
     float *attn_o = nullptr, *attn_part = nullptr, *lp = nullptr, *logits = nullptr;
     int8_t *xq = nullptr, *xq2 = nullptr;  // rotated activations; unrotated h for beta / alpha
+    size_t qrows = 0;                       // rows of xq / xq2 / ds / ds2
     float *ds = nullptr, *ds2 = nullptr;
     uint16_t *qb = nullptr, *kb = nullptr, *vb = nullptr;
     float *beta = nullptr, *gate = nullptr;
@@ -261,6 +262,10 @@ int lin_group(std::initializer_list<LinOp> ops, size_t cols, void *stream) {
 int rq(ouro_stack *s, int pro, const float *a, const float *b, const float *w, float *sum_out, size_t rows, size_t n,
        const float *signs, void *stream, bool also_plain = false) {
     const ouro_stack_card &c = s->c;
+    const size_t laid = frag_tiles(rows) ? static_cast<size_t>(frag_tiles(rows)) * 16 : rows;
+    if (laid > s->qrows)
+        return fail(OURO_ERR_SHAPE, "ouro_stack: %zu activation rows (%zu laid out) exceed the %zu allocated", rows,
+                    laid, s->qrows);
     return row_rotate_quant(pro, a, b, w, sum_out, rows, n, rot_block(n), signs, s->xq, s->ds,
                             also_plain ? s->xq2 : nullptr, also_plain ? s->ds2 : nullptr, frag_tiles(rows),
                             c.ssm_n_k_heads, c.ssm_n_v_heads, OURO_GDN_V_GROUPED, c.eps, stream);
@@ -458,8 +463,12 @@ int ouro_stack_create(const ouro_stack_card *card, uint32_t seed, size_t max_seq
         return done(st);
     const size_t xw = std::max({E, F, s->dv, s->qdim});
     const size_t tiles = max_tokens / 64 + max_seqs + 1;
-    // int8 activations of a few-row launch are padded to whole 16-row tiles
-    const size_t qrows = std::max(rows, (max_seqs + 15) / 16 * 16);
+    // int8 activations of a few-row launch (any launch of <= 64 rows: decode
+    // steps, and prefills of <= 64 tokens) are laid out in whole 16-row
+    // tiles, whose chunks interleave every row across the padded layout, so
+    // the buffers hold round_up(rows, 16) rows
+    const size_t qrows = (rows + 15) / 16 * 16;
+    s->qrows = qrows;
     if ((st = dalloc(s, &s->x, rows * E)) || (st = dalloc(s, &s->pre, rows * E)) ||
         (st = dalloc(s, &s->big, rows * wide)) ||
         (st = dalloc(s, &s->zb, rows * s->dv)) || (st = dalloc(s, &s->braw, rows * c.ssm_n_v_heads)) ||

@@ -13,6 +13,8 @@
 // rope_partial_neox (qwen35.rs:96-106).
 #include "common.hpp"
 
+#include <atomic>
+
 #pragma clang fp contract(off)
 
 namespace ouro {
@@ -107,6 +109,9 @@ struct AttnPrepArgs {
     int T, nh, nkv, n_rot, maxp;
     float rope_base, eps;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (128 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(AttnPrepArgs) == 128, "AttnPrepArgs: kernel argument layout");
 
 // One wavefront per (token, head of q or k); lane l holds dims 2l, 2l+1.
 __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
@@ -179,6 +184,9 @@ struct AttnArgs {
     int nh, nkv, maxp;
     float scale;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (96 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(AttnArgs) == 96, "AttnArgs: kernel argument layout");
 
 // Causal attention over a packed varlen batch on fp32 MFMA
 // (v_mfma_f32_16x16x4f32: fp32 products and sums, the reference's f32
@@ -521,6 +529,9 @@ struct ConvArgs {
     float *beta, *gate;        // [T][Hv]
     int T, ch, di, Hv;
 };
+// passed by value to a kernel: the host and device passes must lay it out
+// alike (128 bytes in the code object's kernel-argument metadata)
+static_assert(sizeof(ConvArgs) == 128, "ConvArgs: kernel argument layout");
 
 __device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x); }
 
@@ -734,12 +745,13 @@ int attn_prefill(const float *q, const float *gate, const float *kc, const float
                  const int32_t *cu, const int32_t *tile_seq, const int32_t *tile_p0, size_t n_tiles, float *out,
                  int nh, int nkv, void *stream) {
     if (!n_tiles) return OURO_OK;
-    static bool lds_set = false;  // one opt-in per process for > 64 KiB of dynamic LDS
-    if (!lds_set) {
+    // one opt-in per process for > 64 KiB of dynamic LDS (idempotent)
+    static std::atomic<bool> lds_set{false};
+    if (!lds_set.load(std::memory_order_acquire)) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kAttnLds);
         if (e != hipSuccess) return fail(OURO_ERR_HIP, "attn_prefill: LDS opt-in: %s", hipGetErrorString(e));
-        lds_set = true;
+        lds_set.store(true, std::memory_order_release);
     }
     AttnArgs a{q, gate, kc, vc, pages, cu, nullptr, tile_seq, tile_p0, out, nh, nkv, maxp,
                1.0f / sqrtf(static_cast<float>(kHd))};

@@ -20,6 +20,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace ouro {
 namespace {
@@ -450,14 +451,15 @@ static int tl1_sum(const float *partial, float *y, size_t out_len, int nb, void 
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw) {
     const int groups = static_cast<int>(in_len / 128), nb = (groups + kGB - 1) / kGB;
-    static bool attr[2] = {false, false};
+    // LDS opt-in once per process and kernel (idempotent)
+    static std::atomic<bool> attr[2] = {{false}, {false}};
     const int lds_bytes = raw ? RAW_LDS : LUT_LDS;
-    if (!attr[raw ? 1 : 0]) {
+    if (!attr[raw ? 1 : 0].load(std::memory_order_acquire)) {
         const void *f = raw ? reinterpret_cast<const void *>(tl1_lut_raw_kernel)
                             : reinterpret_cast<const void *>(tl1_lut_kernel);
         if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes) != hipSuccess)
             return fail(OURO_ERR_HIP, "tl1 lut: %d B of LDS refused", lds_bytes);
-        attr[raw ? 1 : 0] = true;
+        attr[raw ? 1 : 0].store(true, std::memory_order_release);
     }
     const int ntiles = static_cast<int>((out_len + 63) / 64);
     int dev = 0, cus = 256;
@@ -495,12 +497,12 @@ bool tq1_lut_fits(const void *payload, size_t in_len) {
 int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream) {
     const int blocks = static_cast<int>(in_len / 256), npairs = blocks / 2;
-    static bool attr = false;
-    if (!attr) {
+    static std::atomic<bool> attr{false};  // LDS opt-in once per process (idempotent)
+    if (!attr.load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(tq1_lut_raw_kernel),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, TQ_LDS) != hipSuccess)
             return fail(OURO_ERR_HIP, "tq1 lut: %d B of LDS refused", TQ_LDS);
-        attr = true;
+        attr.store(true, std::memory_order_release);
     }
     const int ntiles = static_cast<int>((out_len + 63) / 64);
     int dev = 0, cus = 256;

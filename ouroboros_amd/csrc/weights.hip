@@ -3,14 +3,18 @@
 // once (and repacked on upload, as upload_q6k repacks 210 -> 212 B blocks),
 // then applied by handle.  I2 codes are tiled for the int8 GEMV (and, for
 // handles that expect many columns, also for the int8 MFMA GEMM); TL1
-// payloads are repacked for the table-lookup GEMV.  Every handle owns the scratch its
-// calls need (activation quantisation for up to max_cols columns, TL1
-// partial sums, a logits vector and the argmax key), so its calls allocate
-// nothing.
+// payloads are repacked for the table-lookup GEMV.  Every handle owns the
+// scratch its calls need (activation quantisation for up to max_cols columns,
+// TL1 / TQ1_0 partial sums, a logits vector and the argmax keys), one set per
+// stream it is used on: the null stream's set is made at upload, another
+// stream's on the handle's first call on that stream; after that the calls
+// allocate nothing, and calls on different streams share nothing.
 #include "common.hpp"
 
 #include <cstring>
+#include <mutex>
 #include <new>
+#include <deque>
 
 namespace ouro {
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
@@ -37,17 +41,27 @@ int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const floa
 int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream);
 }  // namespace ouro
 
+// The per-stream scratch of a handle: one allocation holding the I2
+// activation codes and scales, the lookup kernels' partial sums, a y vector
+// and the argmax key slots (each part only where the handle's kind uses it).
+struct WeightScratch {
+    void *stream = nullptr;
+    void *block = nullptr;
+    int8_t *xq = nullptr;
+    float *act_scale = nullptr;
+    float *partial = nullptr;
+    float *y = nullptr;
+    void *amax = nullptr;
+};
+
 struct ouro_weight {
     int kind = 0;
     size_t out_len = 0, in_len = 0, max_cols = 0;
     void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
     void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes
-    int8_t *xq = nullptr;     // I2: activation scratch
-    float *act_scale = nullptr;
-    float *partial = nullptr; // TL1, large TQ1_0: per-block partial sums of the lookup kernels
-    void *aux = nullptr;      // one allocation: y scratch [out_len] f32, then the argmax key slots
-    float *y = nullptr;
-    void *amax = nullptr;
+    size_t partial_floats = 0;  // TL1, large TQ1_0: per-block partial sums of the lookup kernels
+    std::mutex mu;
+    std::deque<WeightScratch> scratch;  // stable addresses as sets are added
 };
 
 using namespace ouro;
@@ -86,10 +100,38 @@ void release(ouro_weight *w) {
     if (!w) return;
     if (w->payload) (void)hipFree(w->payload);
     if (w->mfma) (void)hipFree(w->mfma);
-    if (w->xq) (void)hipFree(w->xq);
-    if (w->partial) (void)hipFree(w->partial);
-    if (w->aux) (void)hipFree(w->aux);
+    for (WeightScratch &sc : w->scratch) (void)hipFree(sc.block);
     delete w;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+// The handle's scratch set for `stream`, made on its first use there.
+WeightScratch *scratch_for(ouro_weight *w, void *stream) {
+    std::lock_guard<std::mutex> lock(w->mu);
+    for (WeightScratch &sc : w->scratch)
+        if (sc.stream == stream) return &sc;
+    const bool i2 = w->kind == OURO_KIND_I2;
+    const size_t xb = i2 ? align256(w->max_cols * w->in_len) : 0;
+    const size_t sb = i2 ? align256(w->max_cols * sizeof(float)) : 0;
+    const size_t pb = align256(w->partial_floats * sizeof(float));
+    const size_t yb = align256(w->out_len * sizeof(float));
+    WeightScratch sc;
+    sc.stream = stream;
+    if (hipMalloc(&sc.block, xb + sb + pb + yb + kArgmaxBlocks * 8) != hipSuccess) {
+        fail(OURO_ERR_HIP, "weight handle: scratch allocation failed");
+        return nullptr;
+    }
+    uint8_t *p = static_cast<uint8_t *>(sc.block);
+    if (i2) {
+        sc.xq = reinterpret_cast<int8_t *>(p);
+        sc.act_scale = reinterpret_cast<float *>(p + xb);
+    }
+    if (w->partial_floats) sc.partial = reinterpret_cast<float *>(p + xb + sb);
+    sc.y = reinterpret_cast<float *>(p + xb + sb + pb);
+    sc.amax = p + xb + sb + pb + yb;
+    w->scratch.push_back(sc);
+    return &w->scratch.back();
 }
 
 }  // namespace
@@ -149,20 +191,11 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             release(w);
             return st;
         }
-        const size_t xb = (w->max_cols * in_len + 255) & ~size_t(255);
-        void *scratch = nullptr;
-        if (hipMalloc(&scratch, xb + w->max_cols * sizeof(float)) != hipSuccess) {
-            release(w);
-            return fail(OURO_ERR_HIP, "ouro_weight_upload: scratch allocation failed");
-        }
-        w->xq = static_cast<int8_t *>(scratch);
-        w->act_scale = reinterpret_cast<float *>(static_cast<uint8_t *>(scratch) + xb);
     } else if (kind == OURO_KIND_TL1) {
         // repack for the lookup kernel; the raw payload lives only during the upload
         void *raw = nullptr;
-        const size_t pf = tl1_lut_partial_floats(out_len, in_len);
+        w->partial_floats = tl1_lut_partial_floats(out_len, in_len);
         if (hipMalloc(&w->payload, tl1_lut_bytes(out_len, in_len)) != hipSuccess ||
-            hipMalloc(reinterpret_cast<void **>(&w->partial), pf * sizeof(float)) != hipSuccess ||
             hipMalloc(&raw, bytes) != hipSuccess) {
             if (raw) (void)hipFree(raw);
             release(w);
@@ -188,21 +221,14 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
             return fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         }
         // a large TQ1_0 matrix runs the lookup kernel: its block partials live with the handle
-        if (kind == OURO_KIND_TQ1_0 && out_len >= kTq1LutRows && tq1_lut_fits(w->payload, in_len) &&
-            hipMalloc(reinterpret_cast<void **>(&w->partial), tq1_lut_partial_floats(out_len, in_len) * sizeof(float)) !=
-                hipSuccess) {
-            release(w);
-            return fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
-        }
+        if (kind == OURO_KIND_TQ1_0 && out_len >= kTq1LutRows && tq1_lut_fits(w->payload, in_len))
+            w->partial_floats = tq1_lut_partial_floats(out_len, in_len);
     }
-    // y scratch (for argmax without a caller y) and the argmax key slots
-    const size_t yb = (out_len * sizeof(float) + 255) & ~size_t(255);
-    if (hipMalloc(&w->aux, yb + kArgmaxBlocks * 8) != hipSuccess) {
+    // the null stream's scratch set
+    if (!scratch_for(w, nullptr)) {
         release(w);
-        return fail(OURO_ERR_HIP, "ouro_weight_upload: scratch allocation failed");
+        return OURO_ERR_HIP;
     }
-    w->y = static_cast<float *>(w->aux);
-    w->amax = static_cast<uint8_t *>(w->aux) + yb;
     *out = w;
     return OURO_OK;
 }
@@ -226,44 +252,48 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
     if (!x || !y || !k) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matmul: NULL argument or k = 0");
     if (w->kind == OURO_KIND_I2 && k > w->max_cols)
         return fail(OURO_ERR_SHAPE, "ouro_weight_matmul: k %zu > max_cols %zu of the handle", k, w->max_cols);
+    WeightScratch *sc = scratch_for(w, stream);
+    if (!sc) return OURO_ERR_HIP;
     if (w->kind == OURO_KIND_TL1) {  // one lookup pass per column, y column-major as matmul_q
         for (size_t c = 0; c < k; ++c) {
             const int st = tl1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,
-                                          w->partial, nullptr, nullptr, stream, 0);
+                                          sc->partial, nullptr, nullptr, stream, 0);
             if (st) return st;
         }
         return OURO_OK;
     }
-    if (w->kind == OURO_KIND_TQ1_0 && w->partial) {  // one lookup pass per column
+    if (w->kind == OURO_KIND_TQ1_0 && sc->partial) {  // one lookup pass per column
         for (size_t c = 0; c < k; ++c) {
             const int st = tq1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,
-                                          w->partial, nullptr, nullptr, stream);
+                                          sc->partial, nullptr, nullptr, stream);
             if (st) return st;
         }
         return OURO_OK;
     }
     if (w->kind == OURO_KIND_I2 && w->mfma && k >= kMfmaCols) {
-        int st = act_quant(x, OURO_DT_F32, k, w->in_len, w->xq, w->act_scale, stream);
+        int st = act_quant(x, OURO_DT_F32, k, w->in_len, sc->xq, sc->act_scale, stream);
         if (st) return st;
         const float *w_scale =
             reinterpret_cast<const float *>(static_cast<const uint8_t *>(w->payload) + i2_tiled_bytes(w->out_len, w->in_len));
-        return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, w->xq, w->act_scale,
-                            k, y, nullptr, stream, 0);
+        return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, sc->xq,
+                            sc->act_scale, k, y, nullptr, stream, 0);
     }
-    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, w->xq, w->act_scale, stream, false);
+    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, sc->xq, sc->act_scale, stream, false);
 }
 
 int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t *idx, void *stream) {
     OURO_REQUIRE_INIT();
     if (!w || !x || !idx) return fail(OURO_ERR_INVALID_ARG, "ouro_weight_matvec_argmax: NULL argument");
-    float *yy = y ? y : w->y;
+    WeightScratch *sc = scratch_for(w, stream);
+    if (!sc) return OURO_ERR_HIP;
+    float *yy = y ? y : sc->y;
     if (w->kind == OURO_KIND_TL1)  // the argmax rides on the partial-sum kernel
-        return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream, 0);
-    if (w->kind == OURO_KIND_TQ1_0 && w->partial)
-        return tq1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, w->partial, w->amax, idx, stream);
+        return tl1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, sc->partial, sc->amax, idx, stream, 0);
+    if (w->kind == OURO_KIND_TQ1_0 && sc->partial)
+        return tq1_lut_matvec(w->payload, w->out_len, w->in_len, x, yy, sc->partial, sc->amax, idx, stream);
     const int st = ouro_weight_matmul(w, x, 1, yy, stream);
     if (st) return st;
-    return argmax_f32(yy, w->out_len, w->amax, idx, stream);
+    return argmax_f32(yy, w->out_len, sc->amax, idx, stream);
 }
 
 int ouro_weight_matvec(ouro_weight_t w, const float *x, float *y, void *stream) {

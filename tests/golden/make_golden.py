@@ -41,7 +41,10 @@ def main():
 
     # 2. Ternary GEMM in bitnet.cpp's I2_S / I8_S format: 3 columns of a
     #    40x512 ternary matrix (w_scale 1.5), the int8 rows, the exact sums,
-    #    the outputs and this library's tiled repack of the codes.
+    #    the outputs and this library's tiled repack of the codes.  These
+    #    outputs come from the oracle's transcription of the published
+    #    bitnet.cpp source, not from bitnet.cpp (its submodule is empty in
+    #    the reference): a regression fixture, not a reference vector.
     rng = np.random.default_rng(20261201)
     w = rng.integers(-1, 2, size=(40, 512)).astype(np.int8)
     xa = rng.standard_normal((3, 512)).astype(np.float32)

@@ -1,8 +1,13 @@
 """bitnet.cpp's int8-activation x 2-bit ternary contract on the GPU: I2_S
-tensors (raw, and repacked on upload) with I8_S activations, bit-exact
-against the oracle's restatement of src/ggml-bitnet-mad.cpp (quantisation,
-int32 sums and the fp32 epilogue), at the 6912x2560 / 2560x6912 layer shapes
-and at every raw-kernel shape class."""
+tensors (raw, and repacked on upload) with I8_S activations, bit-exact vs
+the oracle (quantisation, int32 sums and the fp32 epilogue), at the
+6912x2560 / 2560x6912 layer shapes and at every raw-kernel shape class.
+
+The oracle's I2_S / I8_S functions are this repository's transcription of
+the published bitnet.cpp source (src/ggml-bitnet-mad.cpp); the reference's
+bitnet-cpp submodule is empty, so no output of bitnet.cpp itself (and no
+reference fixture) backs them.  Their rules are pinned by hand-made vectors
+in tests/test_oracle_i2.py, not by bitnet.cpp runs."""
 import numpy as np
 import pytest
 

@@ -2,7 +2,12 @@
 I8_S activation rules (microsoft/BitNet, src/ggml-bitnet-mad.cpp, the
 reference's absent bitnet-cpp submodule), pinned by hand-computed bytes and
 values, by int64 brute force and by invariants; and this library's canonical
-and tiled repacks of the same codes, pinned by round trips."""
+and tiled repacks of the same codes, pinned by round trips.
+
+These rules are this repository's transcription of the published bitnet.cpp
+source: with the submodule empty there is no bitnet.cpp output or reference
+fixture to compare with, so "bit-exact" elsewhere means bit-exact vs this
+oracle."""
 import numpy as np
 import pytest
 
