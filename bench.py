@@ -320,7 +320,27 @@ def bench_tl1(stream, steps, warmup):
     wq = DeviceBuffer.from_host(tq)
     ms_tq1 = time_events(stream, lambda _i: call("ouro_matvec_q", wq.ptr, KIND_TQ1_0, TL1_OUT, TL1_IN, xd.ptr, y.ptr,
                                                  stream), n, 2)
-    return ms, ms_am, ms_raw, ms_tq1, tq.nbytes
+    del wq
+    # K columns from one pass over a resident weight (matmul_tl1, ops.rs:156-286): K = 1 is the lookup
+    # matvec, K >= 2 the int8 MFMA pass; the lm_head probe payload and a random 6912x2560 layer
+    rng = np.random.default_rng(19)
+    small = rng.integers(0, 256, GEMV_OUT * (GEMV_IN // 128) * 28, dtype=np.uint8)
+    gs = small.reshape(-1, 28)
+    gs[:, 26], gs[:, 27] = 0x00, 0x2C  # d = 1/16
+    kcols = []
+    for name, pl, out_len, in_len in (("248320x5120 (lm_head probe)", payload, TL1_OUT, TL1_IN),
+                                      ("6912x2560", small, GEMV_OUT, GEMV_IN)):
+        hk = C.c_void_p()
+        call("ouro_weight_upload", KIND_TL1, pl.ctypes.data, pl.nbytes, out_len, in_len, 1.0, 8, C.byref(hk))
+        xk = DeviceBuffer.from_host(rng.standard_normal(8 * in_len).astype(np.float32))
+        yk = DeviceBuffer((8 * out_len,), np.float32)
+        nk = max(3, steps // 5) if out_len == TL1_OUT else steps
+        for k in (1, 4, 8):
+            t = time_events(stream, lambda _i: call("ouro_weight_matmul", hk.value, xk.ptr, k, yk.ptr, stream), nk, 2)
+            kcols.append({"shape": name, "k": k, "us_per_call": round(t * 1e3, 2),
+                          "weight_stream_GBs": round(out_len * (in_len // 128) * 28 / (t * 1e-3) / 1e9, 1)})
+        call("ouro_weight_free", hk.value)
+    return ms, ms_am, ms_raw, ms_tq1, tq.nbytes, kcols
 
 
 # The block-quantised kinds of matvec_q (Q8_0, Q3_K..Q6_K) on the lm_head
@@ -889,7 +909,7 @@ def main() -> int:
             "bytes_per_step": LY_BYTES,
         }
     if "tl1" in res:
-        ms, ms_am, ms_raw, ms_tq1, tq1_bytes = res["tl1"]
+        ms, ms_am, ms_raw, ms_tq1, tq1_bytes, kcols = res["tl1"]
         gbs = TL1_BYTES / (ms * 1e-3) / 1e9
         sec["tl1_matvec_lmhead"] = {
             "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4),
@@ -904,6 +924,14 @@ def main() -> int:
             "raw_payload_matvec_q_GBs": round(TL1_BYTES / (ms_raw * 1e-3) / 1e9, 1),
             "raw_tq1_0_matvec_q_ms": round(ms_tq1, 4),
             "raw_tq1_0_matvec_q_GBs": round((tq1_bytes + 4 * (TL1_IN + TL1_OUT)) / (ms_tq1 * 1e-3) / 1e9, 1),
+            "k_columns": {
+                "config": "ouro_weight_matmul of a resident TL1 handle (max_cols 8) for K columns: K = 1 the "
+                          "table-lookup matvec, K >= 2 one int8 MFMA pass over the trits for all K",
+                "by_k": kcols,
+                "k8_over_k1": {r0["shape"]: round(r8["us_per_call"] / r0["us_per_call"], 2)
+                               for r0 in kcols if r0["k"] == 1 for r8 in kcols
+                               if r8["k"] == 8 and r8["shape"] == r0["shape"]},
+            },
         }
     if "kquant" in res:
         rows = res["kquant"]

@@ -39,6 +39,12 @@ int tq1_lut_matvec(const void *payload, size_t out_len, size_t in_len, const flo
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw);
 int argmax_f32(const float *y, size_t n, void *scratch, int32_t *idx, void *stream);
+size_t tl1_mfma_code_bytes(size_t M, size_t K);
+size_t tl1_mfma_scale_bytes(size_t M, size_t K);
+size_t tl1_xprep_bytes(size_t K, size_t ncols);
+int tl1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream);
+int tl1_mfma_matmul(const uint8_t *codes, const uint16_t *scales, size_t M, size_t K, const float *x, size_t ncols,
+                    float *y, void *scratch, void *stream);
 }  // namespace ouro
 
 // The per-stream scratch of a handle: one allocation holding the I2
@@ -52,13 +58,15 @@ struct WeightScratch {
     float *partial = nullptr;
     float *y = nullptr;
     void *amax = nullptr;
+    void *xprep = nullptr;  // TL1 with the MFMA layout: x digit planes of up to 16 columns
 };
 
 struct ouro_weight {
     int kind = 0;
     size_t out_len = 0, in_len = 0, max_cols = 0;
     void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
-    void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes
+    void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes;
+                              // TL1 with max_cols >= 2: the trits in that layout, then the group scales
     size_t partial_floats = 0;  // TL1, large TQ1_0: per-block partial sums of the lookup kernels
     std::mutex mu;
     std::deque<WeightScratch> scratch;  // stable addresses as sets are added
@@ -116,9 +124,10 @@ WeightScratch *scratch_for(ouro_weight *w, void *stream) {
     const size_t sb = i2 ? align256(w->max_cols * sizeof(float)) : 0;
     const size_t pb = align256(w->partial_floats * sizeof(float));
     const size_t yb = align256(w->out_len * sizeof(float));
+    const size_t mb = (w->kind == OURO_KIND_TL1 && w->mfma) ? align256(tl1_xprep_bytes(w->in_len, 16)) : 0;
     WeightScratch sc;
     sc.stream = stream;
-    if (hipMalloc(&sc.block, xb + sb + pb + yb + kArgmaxBlocks * 8) != hipSuccess) {
+    if (hipMalloc(&sc.block, xb + sb + pb + yb + mb + kArgmaxBlocks * 8) != hipSuccess) {
         fail(OURO_ERR_HIP, "weight handle: scratch allocation failed");
         return nullptr;
     }
@@ -129,7 +138,8 @@ WeightScratch *scratch_for(ouro_weight *w, void *stream) {
     }
     if (w->partial_floats) sc.partial = reinterpret_cast<float *>(p + xb + sb);
     sc.y = reinterpret_cast<float *>(p + xb + sb + pb);
-    sc.amax = p + xb + sb + pb + yb;
+    if (mb) sc.xprep = p + xb + sb + pb + yb;
+    sc.amax = p + xb + sb + pb + yb + mb;
     w->scratch.push_back(sc);
     return &w->scratch.back();
 }
@@ -205,6 +215,14 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
         if (hipMemcpy(raw, host, bytes, hipMemcpyHostToDevice) != hipSuccess)
             st = fail(OURO_ERR_HIP, "ouro_weight_upload: copy failed");
         if (!st) st = tl1_repack(static_cast<const uint8_t *>(raw), out_len, in_len, w->payload, nullptr);
+        if (!st && w->max_cols >= 2) {  // matmuls of several columns: the trits on int8 MFMA
+            const size_t cb = tl1_mfma_code_bytes(out_len, in_len);
+            if (hipMalloc(&w->mfma, cb + tl1_mfma_scale_bytes(out_len, in_len)) != hipSuccess)
+                st = fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+            else
+                st = tl1_tile_mfma(static_cast<const uint8_t *>(raw), out_len, in_len, static_cast<uint8_t *>(w->mfma),
+                                   reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(w->mfma) + cb), nullptr);
+        }
         if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
         (void)hipFree(raw);
         if (st) {
@@ -254,6 +272,12 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         return fail(OURO_ERR_SHAPE, "ouro_weight_matmul: k %zu > max_cols %zu of the handle", k, w->max_cols);
     WeightScratch *sc = scratch_for(w, stream);
     if (!sc) return OURO_ERR_HIP;
+    if (w->kind == OURO_KIND_TL1 && w->mfma && k >= 2) {  // one pass over the trits for all k columns
+        const size_t cb = tl1_mfma_code_bytes(w->out_len, w->in_len);
+        return tl1_mfma_matmul(static_cast<const uint8_t *>(w->mfma),
+                               reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(w->mfma) + cb),
+                               w->out_len, w->in_len, x, k, y, sc->xprep, stream);
+    }
     if (w->kind == OURO_KIND_TL1) {  // one lookup pass per column, y column-major as matmul_q
         for (size_t c = 0; c < k; ++c) {
             const int st = tl1_lut_matvec(w->payload, w->out_len, w->in_len, x + c * w->in_len, y + c * w->out_len,

@@ -38,7 +38,7 @@ def test_config2_bf16_bit_exact(gpu, orc):
 @pytest.mark.parametrize("n,block", [(16, 16), (32, 16), (64, 64), (128, 64), (192, 64), (256, 2),
                                      (512, 8), (1024, 1024), (5120, 1024), (6144, 1024),
                                      (17408, 1024), (2048, 2048), (8192, 8192), (2560, 512),
-                                     (6912, 256), (4096, 32)])
+                                     (6912, 256), (4096, 32), (4096, 4096), (8192, 4096), (12288, 4096)])
 @pytest.mark.parametrize("inverse", [False, True])
 def test_f32_bit_exact_with_signs(gpu, orc, n, block, inverse):
     rng = np.random.default_rng(n + block)

@@ -58,7 +58,8 @@ def test_tl1_handle_matmul_columns(gpu, orc):
     x = rng.standard_normal(k * in_len).astype(np.float32)
     h = ops.Weight(QuantKind.TL1, p, out_len, in_len)
     want = orc.matmul_tl1(p, out_len, in_len, x, k)  # column-major y[c*out + r]
-    assert close(h.matmul(x, k), want, 1e-5).all()
+    # several columns run the MFMA pass (rel 1e-3, the reference's K-column bar, ops.rs:720-750)
+    assert close(h.matmul(x, k), want, 1e-3).all()
     h.free()
 
 

@@ -1,0 +1,91 @@
+"""K-column TL1 (PTQ1_0) matmul of a resident weight in one pass over its
+trits (matmul_tl1, ops.rs:156-286): trits on int8 MFMA, x as exact int8
+digit planes per group, the f16 group scales applied per group.  Checked
+against the oracle's matmul_tl1 at the reference's K-column bar, rel 1e-3
+(ops.rs:720-750), on the reference's own K-column inputs, on the ternary
+layer and lm_head shapes, on rows of 128 (not 256) elements and on more
+columns than one launch takes (16)."""
+import numpy as np
+import pytest
+
+from ouroboros_amd import ops
+from ouroboros_amd.quant import QuantKind
+
+pytestmark = pytest.mark.gpu
+
+
+def tl1_payload(rng, out_len, in_len):
+    p = rng.integers(0, 256, out_len * (in_len // 128) * 28, dtype=np.uint8)
+    g = p.reshape(-1, 28)
+    d = rng.uniform(0.01, 0.1, g.shape[0]).astype(np.float16).view(np.uint16)
+    g[:, 26], g[:, 27] = d & 0xFF, d >> 8
+    return p
+
+
+def close(got, want, rtol):
+    scale = np.abs(want).max()
+    return np.abs(got - want) <= rtol * np.maximum(np.abs(want), 1e-2 * scale) + 1e-6 * scale
+
+
+def test_reference_k_columns_inputs(gpu, orc):
+    """ops.rs:720-750: 97 x 384, K = 4, bytes i * (0x9B ^ (i >> 5)), d bytes
+    0x10 0x38, x[i] = ((i % 11) - 5) / 4; each column against matvec_tl1 at
+    |got - want| <= 1e-3 max(|want|, 1)."""
+    out_len, in_len, k = 97, 384, 4
+    i = np.arange(out_len * in_len // 128 * 28, dtype=np.uint64)
+    p = ((i * (0x9B ^ (i >> 5))) & 0xFF).astype(np.uint8)
+    g = p.reshape(-1, 28)
+    g[:, 26], g[:, 27] = 0x10, 0x38
+    x = (((np.arange(k * in_len) % 11) - 5.0) * 0.25).astype(np.float32)
+    h = ops.Weight(QuantKind.TL1, p, out_len, in_len, max_cols=k)
+    got = h.matmul(x, k)
+    for c in range(k):
+        want = orc.matvec_tl1(p, out_len, in_len, x[c * in_len:(c + 1) * in_len])
+        assert (np.abs(got[c * out_len:(c + 1) * out_len] - want) <= 1e-3 * np.maximum(np.abs(want), 1.0)).all()
+    h.free()
+
+
+@pytest.mark.parametrize("out_len,in_len,k", [(6912, 2560, 2), (6912, 2560, 4), (6912, 2560, 8), (2560, 6912, 8),
+                                              (97, 384, 3), (97, 384, 6), (37, 128, 5), (300, 1024, 11),
+                                              (300, 1024, 16), (300, 1024, 17), (129, 640, 33)])
+def test_tl1_handle_matmul_mfma(gpu, orc, margin, out_len, in_len, k):
+    rng = np.random.default_rng(out_len + in_len + k)
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    x[3] = 40.0  # an outlier in a group of column 0
+    h = ops.Weight(QuantKind.TL1, p, out_len, in_len, max_cols=k)
+    want = orc.matmul_tl1(p, out_len, in_len, x, k)
+    got = h.matmul(x, k)
+    margin(f"TL1 {out_len}x{in_len} k={k}", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+    # the first column through the table-lookup matvec of the same handle
+    y0 = h.matvec(x[:in_len])
+    assert close(y0, want[:out_len], 1e-5).all()
+    h.free()
+
+
+def test_tl1_handle_matmul_lm_head(gpu, orc, margin):
+    """The reference's lm_head probe shape, 248320 x 5120, at 8 columns."""
+    out_len, in_len, k = 248320, 5120, 8
+    rng = np.random.default_rng(9)
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    h = ops.Weight(QuantKind.TL1, p, out_len, in_len, max_cols=k)
+    got = h.matmul(x, k)
+    h.free()
+    want = orc.matmul_tl1(p, out_len, in_len, x, k)
+    margin("TL1 248320x5120 k=8", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+
+
+def test_tl1_handle_single_column_layout_keeps_lookups(gpu, orc):
+    """A handle for one column holds no MFMA layout; its matmuls are one
+    lookup pass per column (rel 1e-5 per column)."""
+    rng = np.random.default_rng(4)
+    out_len, in_len, k = 300, 1024, 3
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    h = ops.Weight(QuantKind.TL1, p, out_len, in_len, max_cols=1)
+    want = orc.matmul_tl1(p, out_len, in_len, x, k)
+    assert close(h.matmul(x, k), want, 1e-5).all()
+    h.free()
