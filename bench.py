@@ -340,6 +340,15 @@ def bench_tl1(stream, steps, warmup):
             kcols.append({"shape": name, "k": k, "us_per_call": round(t * 1e3, 2),
                           "weight_stream_GBs": round(out_len * (in_len // 128) * 28 / (t * 1e-3) / 1e9, 1)})
         call("ouro_weight_free", hk.value)
+    # the same on the raw payload through ouro_matmul_q (K = 1: the raw lookup matvec)
+    w = DeviceBuffer.from_host(payload)
+    xk = DeviceBuffer.from_host(rng.standard_normal(8 * TL1_IN).astype(np.float32))
+    yk = DeviceBuffer((8 * TL1_OUT,), np.float32)
+    for k in (1, 4, 8):
+        t = time_events(stream, lambda _i: call("ouro_matmul_q", w.ptr, KIND_TL1, TL1_OUT, TL1_IN, xk.ptr, k, yk.ptr,
+                                                stream), max(3, steps // 5), 2)
+        kcols.append({"shape": "248320x5120 raw payload (ouro_matmul_q)", "k": k, "us_per_call": round(t * 1e3, 2),
+                      "weight_stream_GBs": round(payload.nbytes / (t * 1e-3) / 1e9, 1)})
     return ms, ms_am, ms_raw, ms_tq1, tq.nbytes, kcols
 
 

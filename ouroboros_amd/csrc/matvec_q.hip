@@ -7,7 +7,9 @@
 // task, and multiplied straight into fp32 accumulators: trits never touch
 // memory (ops.rs:288-293).  One wavefront per output row; a task is one
 // payload byte with its 4 or 5 trits, so consecutive lanes read consecutive
-// payload bytes.  matmul_q decodes each byte once for up to 8 columns.
+// payload bytes.  matmul_q decodes each byte once for up to 8 columns; a
+// 4-byte-aligned TL1 payload of several columns goes to the int8 MFMA pass of
+// tl1_mfma.hip instead (one pass over the payload for all columns).
 #include "common.hpp"
 
 #include <mutex>
@@ -26,6 +28,9 @@ size_t tl1_lut_partial_floats(size_t out_len, size_t in_len);
 int tl1_lut_matvec(const void *packed, size_t out_len, size_t in_len, const float *x, float *y, float *partial,
                    void *amax_scratch, int32_t *idx, void *stream, int raw);
 bool is_kquant(int kind);
+size_t tl1_xprep_bytes(size_t K, size_t ncols);
+int tl1_mfma_matmul_raw(const uint8_t *raw, size_t M, size_t K, const float *x, size_t ncols, float *y, void *scratch,
+                        void *stream);
 int kq_matmul(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k, float *y,
               void *stream);
 size_t tq1_lut_partial_floats(size_t out_len, size_t in_len);
@@ -257,6 +262,14 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
             float *partial = static_cast<float *>(workspace(tl1_lut_partial_floats(out_len, in_len) * 4, stream));
             if (!partial) return OURO_ERR_HIP;
             return tl1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream, 1);
+        }
+        // several columns: one pass over the payload for all of them (int8 MFMA
+        // on the decoded digits, x as exact digit planes in the workspace)
+        if (k >= 2 && use_workspace && reinterpret_cast<uintptr_t>(payload) % 4 == 0 &&
+            reinterpret_cast<uintptr_t>(x) % 4 == 0) {
+            void *ws = workspace(tl1_xprep_bytes(in_len, k), stream);
+            if (!ws) return OURO_ERR_HIP;
+            return tl1_mfma_matmul_raw(static_cast<const uint8_t *>(payload), out_len, in_len, x, k, y, ws, stream);
         }
         break;
     case OURO_KIND_TQ1_0:

@@ -100,14 +100,16 @@ struct XprepArgs {
     const float *x;  // [ncols][K]
     int8_t *xb;      // B fragments: [nkb][4 steps][tiles][64 lanes][16 bytes]
     float *wt;       // [G][16 tiles] plane weights
+    int32_t *sx;     // [G][16 tiles] sums of each B column's digits over the group
     int K, G, tiles, ncols;
 };
-static_assert(sizeof(XprepArgs) == 40, "XprepArgs: kernel argument layout");
+static_assert(sizeof(XprepArgs) == 48, "XprepArgs: kernel argument layout");
 
 // One workgroup of 128 threads per (group g, virtual column c); columns past
 // ncols (up to the last tile's end) and k past K write zero digits.
 __global__ __launch_bounds__(128) void tl1_xprep_kernel(XprepArgs a) {
     __shared__ float red[2];
+    __shared__ int dsum[2][kPlanes];
     const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
     const int k = g * 128 + t;
     const float x = (c < a.ncols && k < a.K) ? a.x[static_cast<long long>(c) * a.K + k] : 0.f;
@@ -128,23 +130,57 @@ __global__ __launch_bounds__(128) void tl1_xprep_kernel(XprepArgs a) {
     const int kb = k >> 8, s = (k & 255) >> 6, quarter = (k & 63) >> 4, byte = k & 15;
 #pragma unroll
     for (int p = 0; p < kPlanes; ++p) {
+        int v = dig[p];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
+        if ((t & 63) == 0) dsum[t >> 6][p] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) {
         const int j = kPlanes * c + p;
         if (j >= 16 * a.tiles) continue;
         const int ct = j >> 4, lane = (j & 15) + 16 * quarter;
         a.xb[((static_cast<long long>(kb) * 4 + s) * a.tiles + ct) * 1024 + lane * 16 + byte] = static_cast<int8_t>(dig[p]);
-        if (t == 0) a.wt[static_cast<long long>(g) * 16 * a.tiles + j] = (c < a.ncols) ? -ldexpf(1.0f, E - 28 + 8 * (2 - p)) : 0.f;
+        if (t == 0) {
+            a.wt[static_cast<long long>(g) * 16 * a.tiles + j] = (c < a.ncols) ? -ldexpf(1.0f, E - 28 + 8 * (2 - p)) : 0.f;
+            a.sx[static_cast<long long>(g) * 16 * a.tiles + j] = dsum[0][p] + dsum[1][p];
+        }
     }
 }
 
 struct Tl1MmArgs {
-    const v4u *w;        // unit layout [nrt][nkb][64] x 16 B
-    const uint16_t *d;   // [M][G] f16
+    const v4u *w;        // unit layout [nrt][nkb][64] x 16 B (RAW: unused)
+    const uint16_t *d;   // [M][G] f16 (RAW: unused)
+    const uint8_t *raw;  // RAW: the reference's row-major groups of 28 bytes
     const int8_t *xb;    // B fragments
     const float *wt;     // [G][16 tiles]
+    const int32_t *sx;   // [G][16 tiles] digit sums (RAW)
     float *y;            // [ncols][M]
-    int M, nkb, G, tiles, ncols, nrb;
+    int M, nkb, G, tiles, ncols, nrb, graw;  // graw: groups of a raw row (K / 128)
 };
-static_assert(sizeof(Tl1MmArgs) == 64, "Tl1MmArgs: kernel argument layout");
+static_assert(sizeof(Tl1MmArgs) == 88, "Tl1MmArgs: kernel argument layout");
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned v4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef unsigned v3a __attribute__((ext_vector_type(3), aligned(4)));
+
+// Base-3 digits (0..2) of the four bytes of S, byte b taking digit n_b
+// (dequant.rs:134-138: ((v * 3^n mod 256) * 3) >> 8), with the multipliers
+// packed per 16-bit half: me = 3^n0 | 3^n2 << 16 for bytes 0 and 2, mo the
+// same for bytes 1 and 3.  One byte per 16-bit lane keeps every product
+// within 16 bits.
+__device__ __forceinline__ uint32_t digits4(uint32_t S, uint32_t me, uint32_t mo) {
+    const u16x2 e = __builtin_bit_cast(u16x2, S & 0x00ff00ffu);
+    const u16x2 o = __builtin_bit_cast(u16x2, (S >> 8) & 0x00ff00ffu);
+    const u16x2 k3 = {3, 3};
+    const u16x2 ff = {0xff, 0xff};
+    const u16x2 qe = ((e * __builtin_bit_cast(u16x2, me)) & ff) * k3;
+    const u16x2 qo = ((o * __builtin_bit_cast(u16x2, mo)) & ff) * k3;
+    const uint32_t de = __builtin_bit_cast(uint32_t, static_cast<u16x2>(qe >> 8));
+    const uint32_t dd = __builtin_bit_cast(uint32_t, static_cast<u16x2>(qo >> 8));
+    return de | (dd << 8);
+}
 
 // Workgroup: 4 wavefronts along the rows, wavefront w owns row tiles
 // (4 rb + w) WR .. +WR-1 and all WC column tiles.  Per 256-deep k block the
@@ -152,7 +188,17 @@ static_assert(sizeof(Tl1MmArgs) == 64, "Tl1MmArgs: kernel argument layout");
 // prefetched a block ahead in registers) and each wavefront loads its WR
 // weight units and their scales a block ahead.  Indices are clamped, so
 // every load is unconditional.
-template <int WR, int WC>
+//
+// RAW: the weights are the reference's row-major payload.  Lane l loads the
+// 28 bytes of group g of row 16 rt + l%16 (one 16- and one 12-byte load) and
+// makes its A fragment of each step from them: the base-3 digit (0..2) of
+// every element, elements 16 (l/16) .. +15 of the step's half group in the
+// payload's order (qs bytes 0..15 carry elements 16 n + m, bytes 16..23
+// elements 80 + 8 n + m, bytes 24, 25 elements 120 + 2 n + h).  The MFMA
+// then sums digit * x_p; the trit sum is that minus the group's digit sum of
+// the B column (exact integers), and the group scale d comes from bytes 26,
+// 27, moved to the lanes of the D rows by a lane shuffle.
+template <int WR, int WC, bool RAW>
 __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     constexpr int kPiece = 1024;
     __shared__ __attribute__((aligned(16))) int8_t xs[2][4 * WC * kPiece];
@@ -160,13 +206,33 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rt0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * WR;
     const int nrt = (a.M + 15) / 16;
+    const int q = lane >> 4;
+
+    // RAW: per-lane digit multipliers of the odd steps' four A dwords (the
+    // even steps take digit q of qs bytes 0..15: 3^q in both halves)
+    uint32_t m_even = 0, me1[4] = {0, 0, 0, 0}, mo1[4] = {0, 0, 0, 0};
+    if constexpr (RAW) {
+        const uint32_t p3q = q == 0 ? 1u : q == 1 ? 3u : q == 2 ? 9u : 27u;
+        m_even = p3q | (p3q << 16);
+        const uint32_t lo = q == 0 ? 81u : q == 1 ? 1u : q == 2 ? 9u : 81u;   // dwords 0, 1
+        const uint32_t hi = q == 0 ? 81u : q == 1 ? 3u : q == 2 ? 27u : 0u;   // dwords 2, 3 (q = 3: below)
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            const uint32_t m = dw < 2 ? lo : hi;
+            me1[dw] = mo1[dw] = m | (m << 16);
+        }
+        if (q == 3) {  // bytes (24, 25, 24, 25): digits (0, 0, 1, 1), then (2, 2, 3, 3)
+            me1[2] = mo1[2] = 1u | (3u << 16);
+            me1[3] = mo1[3] = 9u | (27u << 16);
+        }
+    }
 
     v4u xr[WC];
     auto load_x = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) {
             const int c = tid + kWave * kWaves * i;  // chunk c: piece c / 64 (step-major), lane c % 64
-            const int q = c / 64, s = q / WC, ct = q % WC;
+            const int pq = c / 64, s = pq / WC, ct = pq % WC;
             xr[i] = *reinterpret_cast<const v4u *>(a.xb + ((static_cast<long long>(kb) * 4 + s) * a.tiles + ct) * kPiece +
                                                    (c % 64) * 16);
         }
@@ -175,17 +241,33 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) *reinterpret_cast<v4u *>(&xs[buf][16 * (tid + kWave * kWaves * i)]) = xr[i];
     };
+    // unit layout: the lane's word of each step and the f16 scales of its 4 D
+    // rows for the block's two groups; RAW: the 7 dwords of its row's groups
     v4u wr[WR];
-    uint32_t dr[WR][4];  // f16 scales of the lane's 4 rows, groups 2 kb (low half) and 2 kb + 1 (high half)
+    uint32_t dr[WR][4];
+    uint32_t rr[WR][2][7];
     auto load_w = [&](int kb) {
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int rt = min(rt0 + r, nrt - 1);
-            wr[r] = a.w[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane];
+            if constexpr (RAW) {
+                const long long row = min(rt * 16 + (lane & 15), a.M - 1);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = min(rt * 16 + 4 * (lane >> 4) + e, a.M - 1);
-                dr[r][e] = *reinterpret_cast<const uint32_t *>(a.d + static_cast<long long>(row) * a.G + 2 * kb);
+                for (int h = 0; h < 2; ++h) {
+                    const int g = min(2 * kb + h, a.graw - 1);  // the padding group loads a real one, d = 0 below
+                    const uint8_t *p = a.raw + row * (static_cast<long long>(a.graw) * 28) + static_cast<long long>(g) * 28;
+                    const v4a u4 = *reinterpret_cast<const v4a *>(p);
+                    const v3a u3 = *reinterpret_cast<const v3a *>(p + 16);
+                    rr[r][h][0] = u4.x, rr[r][h][1] = u4.y, rr[r][h][2] = u4.z, rr[r][h][3] = u4.w;
+                    rr[r][h][4] = u3.x, rr[r][h][5] = u3.y, rr[r][h][6] = u3.z;
+                }
+            } else {
+                wr[r] = a.w[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = min(rt * 16 + 4 * (lane >> 4) + e, a.M - 1);
+                    dr[r][e] = *reinterpret_cast<const uint32_t *>(a.d + static_cast<long long>(row) * a.G + 2 * kb);
+                }
             }
         }
     };
@@ -205,11 +287,19 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     for (int kb = 0; kb < a.nkb; ++kb) {
         v4u wc[WR];
         uint32_t dc[WR][4];
+        uint32_t rc[WR][2][7];
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
-            wc[r] = wr[r];
+            if constexpr (RAW) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dc[r][e] = dr[r][e];
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 7; ++i) rc[r][h][i] = rr[r][h][i];
+            } else {
+                wc[r] = wr[r];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dc[r][e] = dr[r][e];
+            }
         }
         const bool more = kb + 1 < a.nkb;
         if (more) {
@@ -231,9 +321,27 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
                 v4i A[WR];
 #pragma unroll
                 for (int r = 0; r < WR; ++r) {
-                    const uint32_t wd = s == 0 ? wc[r][0] : s == 1 ? wc[r][1] : s == 2 ? wc[r][2] : wc[r][3];
-                    A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
-                               static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+                    if constexpr (RAW) {
+                        const uint32_t *w7 = rc[r][half];
+                        uint32_t d4[4];
+                        if (s2 == 0) {
+#pragma unroll
+                            for (int dw = 0; dw < 4; ++dw) d4[dw] = digits4(w7[dw], m_even, m_even);
+                        } else {
+                            const uint32_t qh = (w7[6] & 0xffffu) * 0x00010001u;  // bytes 24, 25, 24, 25
+                            const uint32_t src[4] = {q == 0 ? w7[0] : w7[4], q == 0 ? w7[1] : w7[5],
+                                                     q == 0 ? w7[2] : q == 3 ? qh : w7[4],
+                                                     q == 0 ? w7[3] : q == 3 ? qh : w7[5]};
+#pragma unroll
+                            for (int dw = 0; dw < 4; ++dw) d4[dw] = digits4(src[dw], me1[dw], mo1[dw]);
+                        }
+                        A[r] = v4i{static_cast<int>(d4[0]), static_cast<int>(d4[1]), static_cast<int>(d4[2]),
+                                   static_cast<int>(d4[3])};
+                    } else {
+                        const uint32_t wd = s == 0 ? wc[r][0] : s == 1 ? wc[r][1] : s == 2 ? wc[r][2] : wc[r][3];
+                        A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
+                                   static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+                    }
                 }
 #pragma unroll
                 for (int c = 0; c < WC; ++c) {
@@ -243,18 +351,33 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
                         acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B, acc[r][c], 0, 0, 0);
                 }
             }
-            // the group's term: d(row) * w(g, column) * acc
+            // the group's term: d(row) * w(g, column) * trit sum
 #pragma unroll
-            for (int c = 0; c < WC; ++c) {
-                const float wv = a.wt[static_cast<long long>(g) * 16 * a.tiles + 16 * c + (lane & 15)];
+            for (int r = 0; r < WR; ++r) {
+                float dv[4];
+                if constexpr (RAW) {
+                    // d of the lane's A row, then of its 4 D rows (lane 4 (l/16) + e holds row 4 (l/16) + e)
+                    const float own = 2 * kb + half < a.graw
+                        ? static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(rc[r][half][6] >> 16)))
+                        : 0.f;
 #pragma unroll
-                for (int r = 0; r < WR; ++r)
+                    for (int e = 0; e < 4; ++e) dv[e] = __shfl(own, 4 * (lane >> 4) + e, 64);
+                } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint16_t db = static_cast<uint16_t>(half ? dc[r][e] >> 16 : dc[r][e] & 0xffffu);
-                        const float dv = static_cast<float>(__builtin_bit_cast(_Float16, db));
-                        yacc[r][c][e] = __builtin_fmaf(static_cast<float>(acc[r][c][e]), dv * wv, yacc[r][c][e]);
+                        dv[e] = static_cast<float>(__builtin_bit_cast(_Float16, db));
                     }
+                }
+#pragma unroll
+                for (int c = 0; c < WC; ++c) {
+                    const long long wi = static_cast<long long>(g) * 16 * a.tiles + 16 * c + (lane & 15);
+                    const float wv = RAW ? -64.f * a.wt[wi] : a.wt[wi];
+                    const int corr = RAW ? a.sx[wi] : 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        yacc[r][c][e] = __builtin_fmaf(static_cast<float>(acc[r][c][e] - corr), dv[e] * wv, yacc[r][c][e]);
+                }
             }
         }
         if (more) store_x((kb + 1) & 1);
@@ -273,10 +396,10 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         for (int idx = lane; idx < 16 * a.ncols; idx += kWave) {
-            const int rr = idx & 15, col = idx >> 4;
-            const float v = comb[wave][rr][kPlanes * col] + comb[wave][rr][kPlanes * col + 1] +
-                            comb[wave][rr][kPlanes * col + 2];
-            const int row = rt * 16 + rr;
+            const int rr2 = idx & 15, col = idx >> 4;
+            const float v = comb[wave][rr2][kPlanes * col] + comb[wave][rr2][kPlanes * col + 1] +
+                            comb[wave][rr2][kPlanes * col + 2];
+            const int row = rt * 16 + rr2;
             if (rt < nrt && row < a.M) a.y[static_cast<long long>(col) * a.M + row] = v;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -297,7 +420,7 @@ size_t tl1_xprep_bytes(size_t K, size_t ncols) {
     const size_t nc = std::min(ncols, static_cast<size_t>(kTl1MmCols));
     const size_t tiles = (kPlanes * nc + 15) / 16;
     const size_t nkb = (K + 255) / 256;
-    return nkb * 4 * tiles * 1024 + nkb * 2 * 16 * tiles * sizeof(float);
+    return nkb * 4 * tiles * 1024 + nkb * 2 * 16 * tiles * (sizeof(float) + sizeof(int32_t));
 }
 
 // Raw TL1 payload (device, row-major groups) -> unit layout + scales.
@@ -317,15 +440,16 @@ int tl1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16
     return check_launch("tl1_scales_kernel");
 }
 
-// y[c][M] = W x_c for ncols columns of x [ncols][K], W in the unit layout.
-// scratch: tl1_xprep_bytes(K, ncols) bytes, 16-byte aligned.
-int tl1_mfma_matmul(const uint8_t *codes, const uint16_t *scales, size_t M, size_t K, const float *x, size_t ncols,
-                    float *y, void *scratch, void *stream) {
-    if (!codes || !scales || !x || !y || !scratch) return fail(OURO_ERR_INVALID_ARG, "tl1 matmul: NULL argument");
+namespace {
+// y[c][M] = W x_c for ncols columns of x [ncols][K]; W in the unit layout
+// (codes, scales) or, raw != nullptr, the reference's payload.
+int tl1_mfma_run(const uint8_t *codes, const uint16_t *scales, const uint8_t *raw, size_t M, size_t K, const float *x,
+                 size_t ncols, float *y, void *scratch, void *stream) {
+    if ((!raw && (!codes || !scales)) || !x || !y || !scratch) return fail(OURO_ERR_INVALID_ARG, "tl1 matmul: NULL argument");
     if (!M || !K || K % 128 || !ncols || M > 0x7fffffffULL || K > 0x7fffffffULL)
         return fail(OURO_ERR_SHAPE, "tl1 matmul: bad shape");
     if ((reinterpret_cast<uintptr_t>(codes) | reinterpret_cast<uintptr_t>(scratch)) % 16 ||
-        reinterpret_cast<uintptr_t>(scales) % 4)
+        (reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(raw)) % 4)
         return fail(OURO_ERR_ALIGN, "tl1 matmul: alignment");
     const hipStream_t s = as_stream(stream);
     const int nkb = static_cast<int>((K + 255) / 256);
@@ -334,23 +458,45 @@ int tl1_mfma_matmul(const uint8_t *codes, const uint16_t *scales, size_t M, size
         const int tiles = (kPlanes * nc + 15) / 16;
         int8_t *xb = static_cast<int8_t *>(scratch);
         float *wt = reinterpret_cast<float *>(xb + static_cast<size_t>(nkb) * 4 * tiles * 1024);
-        XprepArgs xa{x + c0 * K, xb, wt, static_cast<int>(K), 2 * nkb, tiles, nc};
+        int32_t *sx = reinterpret_cast<int32_t *>(wt + static_cast<size_t>(nkb) * 2 * 16 * tiles);
+        XprepArgs xa{x + c0 * K, xb, wt, sx, static_cast<int>(K), 2 * nkb, tiles, nc};
         const int vcols = (16 * tiles + kPlanes - 1) / kPlanes;  // virtual columns cover every B column
         hipLaunchKernelGGL(tl1_xprep_kernel, dim3(2 * nkb, vcols), dim3(128), 0, s, xa);
         int st = check_launch("tl1_xprep_kernel");
         if (st) return st;
-        Tl1MmArgs a{reinterpret_cast<const v4u *>(codes), scales, xb, wt, y + c0 * M, static_cast<int>(M), nkb,
-                    2 * nkb, tiles, nc, 0};
+        Tl1MmArgs a{reinterpret_cast<const v4u *>(codes), scales, raw, xb, wt, sx, y + c0 * M, static_cast<int>(M), nkb,
+                    2 * nkb, tiles, nc, 0, static_cast<int>(K / 128)};
         const int nrt = static_cast<int>((M + 15) / 16);
         constexpr int WR = 2;
         a.nrb = (nrt + kWaves * WR - 1) / (kWaves * WR);
-        if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 1>), dim3(a.nrb), dim3(kWave * kWaves), 0, s, a);
-        else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 2>), dim3(a.nrb), dim3(kWave * kWaves), 0, s, a);
-        else hipLaunchKernelGGL((tl1_mfma_kernel<WR, 3>), dim3(a.nrb), dim3(kWave * kWaves), 0, s, a);
+        const dim3 grid(a.nrb), block(kWave * kWaves);
+        if (raw) {
+            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 1, true>), grid, block, 0, s, a);
+            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 2, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((tl1_mfma_kernel<WR, 3, true>), grid, block, 0, s, a);
+        } else {
+            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 1, false>), grid, block, 0, s, a);
+            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 2, false>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((tl1_mfma_kernel<WR, 3, false>), grid, block, 0, s, a);
+        }
         st = check_launch("tl1_mfma_kernel");
         if (st) return st;
     }
     return OURO_OK;
+}
+}  // namespace
+
+// W in the unit layout (a resident handle).  scratch: tl1_xprep_bytes(K,
+// ncols) bytes, 16-byte aligned.
+int tl1_mfma_matmul(const uint8_t *codes, const uint16_t *scales, size_t M, size_t K, const float *x, size_t ncols,
+                    float *y, void *scratch, void *stream) {
+    return tl1_mfma_run(codes, scales, nullptr, M, K, x, ncols, y, scratch, stream);
+}
+
+// W the reference's row-major payload on the device (4-byte aligned).
+int tl1_mfma_matmul_raw(const uint8_t *raw, size_t M, size_t K, const float *x, size_t ncols, float *y, void *scratch,
+                        void *stream) {
+    return tl1_mfma_run(nullptr, nullptr, raw, M, K, x, ncols, y, scratch, stream);
 }
 
 }  // namespace ouro

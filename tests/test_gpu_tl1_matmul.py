@@ -78,6 +78,31 @@ def test_tl1_handle_matmul_lm_head(gpu, orc, margin):
     assert close(got, want, 1e-3).all()
 
 
+@pytest.mark.parametrize("out_len,in_len,k", [(6912, 2560, 8), (97, 384, 4), (37, 128, 3), (300, 1024, 17)])
+def test_tl1_raw_matmul_q_mfma(gpu, orc, margin, out_len, in_len, k):
+    """ouro_matmul_q on a raw device payload: the digits decoded in registers
+    for the int8 MFMA pass (rows of one group, 128-element rows past a
+    256-deep block, more than one launch's 16 columns)."""
+    rng = np.random.default_rng(out_len * 7 + k)
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    want = orc.matmul_tl1(p, out_len, in_len, x, k)
+    got = ops.matmul_q(p, QuantKind.TL1, out_len, in_len, x, k)
+    margin(f"raw TL1 {out_len}x{in_len} k={k}", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+
+
+def test_tl1_raw_matmul_q_lm_head(gpu, orc, margin):
+    out_len, in_len, k = 248320, 5120, 8
+    rng = np.random.default_rng(10)
+    p = tl1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    got = ops.matmul_q(p, QuantKind.TL1, out_len, in_len, x, k)
+    want = orc.matmul_tl1(p, out_len, in_len, x, k)
+    margin("raw TL1 248320x5120 k=8", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+
+
 def test_tl1_handle_single_column_layout_keeps_lookups(gpu, orc):
     """A handle for one column holds no MFMA layout; its matmuls are one
     lookup pass per column (rel 1e-5 per column)."""
