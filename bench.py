@@ -925,7 +925,7 @@ def main() -> int:
             "config": "TL1 (PTQ1_0) 248320x5120 resident weight (table-lookup GEMV), fp32 x and y, the reference's "
                       "lm_head probe payload (ops.rs:694-717; its CPU figure is 1.75 GB/s on an i7-3770)",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "tl1_lut_kernel")},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of(traffic, "tl1_lut_kernel", 256000)},
             "bytes_per_call": TL1_BYTES,
             "greedy_sample_ms": round(ms_am, 4),
             "greedy_sample_tokens_per_s": round(1e3 / ms_am, 1),
@@ -945,12 +945,16 @@ def main() -> int:
     if "kquant" in res:
         rows = res["kquant"]
         big = [r for r in rows if r["out_len"] == TL1_OUT]
+        kind_id = {name: kind for name, kind, _bb, _be in KQ_KINDS}
+        for r in big:  # the lm_head launch of each kind's GEMV (one grid for every kind)
+            r["traffic"] = traffic_of(traffic, f"kq_gemv_kernel<{kind_id[r['kind']]},", 491520)
+        slow = min(big, key=lambda r: r["GBs"])
         sec["kquant_matvec"] = {
-            "value": round(min(r["GBs"] for r in big), 1), "unit": "GB/s",
+            "value": slow["GBs"], "unit": "GB/s",
             "config": "ouro_matvec_q on raw ggml Q8_0 / Q3_K / Q4_K / Q5_K / Q6_K blocks (matvec_qblock, "
                       "ops.rs:101-128), fp32 x and y; value = the slowest kind at 248320x5120",
-            "roofline": {"bound": "hbm", "achieved": round(min(r["GBs"] for r in big), 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(min(r["frac"] for r in big), 4)},
+            "roofline": {"bound": "hbm", "achieved": slow["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": slow["frac"], "traffic": slow["traffic"]},
             "by_kind": rows,
         }
     if "gemm" in res:
