@@ -280,13 +280,19 @@ int ouro_matmul_q(const void *payload, int kind, size_t out_len,
                   void *stream);
 /* ouro_matvec_q that allocates nothing, for callers that cannot call
  * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
- * that forbid allocation).  No counterpart in the reference.  For the 2-bit
- * kinds (OURO_KIND_I2_S, OURO_KIND_I2) x is quantised into a static
- * per-device scratch array of 32 KiB + 256 B that each device holds until
- * the process ends, so in_len <= 32768 (OURO_ERR_SHAPE beyond); the other
- * kinds use no scratch and behave exactly as ouro_matvec_q.  Results equal
- * ouro_matvec_q's bit for bit.  All calls on one device share the scratch:
- * calls that overlap on one device (e.g. on two streams) race. */
+ * that forbid allocation).  No counterpart in the reference.  It uses a
+ * static per-device scratch array of 16 MiB that each device holds until
+ * the process ends.  For the 2-bit kinds (OURO_KIND_I2_S, OURO_KIND_I2) x
+ * is quantised into its first 32 KiB + 256 B, so in_len <= 32768
+ * (OURO_ERR_SHAPE beyond).  TL1 and TQ1_0 payloads of 8192 rows or more
+ * keep the table-lookup kernels' per-block partial sums there when they fit
+ * (TL1: ceil(in_len/512) * out_len floats, TQ1_0: in_len/512 * out_len,
+ * at most 16 MiB: the 248320x5120 lm_head takes 9.9 MB); larger ones run
+ * the direct decode kernel, which needs no scratch (slower; within rel
+ * 1e-5 of ouro_matvec_q).  The other kinds use no scratch.  Wherever the
+ * same kernels run, results equal ouro_matvec_q's bit for bit.  All calls on
+ * one device share the scratch: calls that overlap on one device (e.g. on
+ * two streams) race. */
 int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len,
                           size_t in_len, const float *x, float *y,
                           void *stream);

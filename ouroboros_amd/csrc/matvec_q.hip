@@ -243,9 +243,23 @@ int launch_mv(int kind, const MvArgs &a, hipStream_t s) {
 // (ops.rs:296), TQ1_0 rows whole 256-blocks (QuantKind::row_bytes,
 // dequant.rs:376-387).
 // use_workspace = false keeps every path off the library workspace (the
-// 2-bit kinds then need xq_scratch / act_scale_scratch).
+// 2-bit kinds then need xq_scratch / act_scale_scratch; a TL1 or TQ1_0
+// lookup GEMV runs only if lut_partial holds its partial sums, else the
+// direct kernel does).
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace) {
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace,
+             float *lut_partial, size_t lut_partial_bytes) {
+    // partial sums of a lookup GEMV: the library workspace, or the caller's
+    // buffer if it is large enough (nullptr: run the direct kernel)
+    auto partials = [&](size_t floats, bool &failed) -> float * {
+        failed = false;
+        if (use_workspace) {
+            float *p = static_cast<float *>(workspace(floats * 4, stream));
+            failed = !p;
+            return p;
+        }
+        return lut_partial && floats * 4 <= lut_partial_bytes ? lut_partial : nullptr;
+    };
     if (!payload || !x || !y) return fail(OURO_ERR_INVALID_ARG, "matvec_q: NULL argument");
     if (!out_len || !in_len || !k) return fail(OURO_ERR_SHAPE, "matvec_q: empty shape");
     if (out_len > 0x7fffffffULL || in_len > 0x7fffffffULL || k > 0x7fffffffULL)
@@ -255,13 +269,13 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     case OURO_KIND_TL1:
         if (in_len % 128) return fail(OURO_ERR_SHAPE, "matvec_q TL1: in_len %zu not a multiple of 128", in_len);
         // one column of a large matrix: the lookup kernel straight on the
-        // reference bytes (per-block partial sums in the library workspace);
-        // allocation-free calls keep the direct kernel
-        if (k == 1 && out_len >= kLutRows && use_workspace &&
-            reinterpret_cast<uintptr_t>(payload) % 4 == 0 && in_len <= 65536) {
-            float *partial = static_cast<float *>(workspace(tl1_lut_partial_floats(out_len, in_len) * 4, stream));
-            if (!partial) return OURO_ERR_HIP;
-            return tl1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream, 1);
+        // reference bytes (per-block partial sums in the library workspace or
+        // the caller's buffer)
+        if (k == 1 && out_len >= kLutRows && reinterpret_cast<uintptr_t>(payload) % 4 == 0 && in_len <= 65536) {
+            bool failed = false;
+            float *partial = partials(tl1_lut_partial_floats(out_len, in_len), failed);
+            if (failed) return OURO_ERR_HIP;
+            if (partial) return tl1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream, 1);
         }
         // several columns: one pass over the payload for all of them (int8 MFMA
         // on the decoded digits, x as exact digit planes in the workspace)
@@ -275,10 +289,11 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
     case OURO_KIND_TQ1_0:
         if (in_len % 256) return fail(OURO_ERR_SHAPE, "matvec_q TQ1_0: in_len %zu not a multiple of 256", in_len);
         // one column of a large matrix: the lookup kernel on the reference bytes
-        if (k == 1 && out_len >= kLutRows && use_workspace && tq1_lut_fits(payload, in_len)) {
-            float *partial = static_cast<float *>(workspace(tq1_lut_partial_floats(out_len, in_len) * 4, stream));
-            if (!partial) return OURO_ERR_HIP;
-            return tq1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream);
+        if (k == 1 && out_len >= kLutRows && tq1_lut_fits(payload, in_len)) {
+            bool failed = false;
+            float *partial = partials(tq1_lut_partial_floats(out_len, in_len), failed);
+            if (failed) return OURO_ERR_HIP;
+            if (partial) return tq1_lut_matvec(payload, out_len, in_len, x, y, partial, nullptr, nullptr, stream);
         }
         break;
     case OURO_KIND_F32:
@@ -321,14 +336,18 @@ int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const
 //
 // Callers that cannot allocate (code under HIP graph capture, tight serving
 // loops) get ouro_matvec_q_noalloc: its 2-bit kinds quantise x into this
-// file-scope device array instead of the library workspace.  Each device
-// holds its own copy until the process ends; its address on a device comes
-// from hipGetSymbolAddress (the array's name is not a device address in
-// host code).  All calls on one device share it, so calls that overlap on
-// one device race.  Nothing in it needs to start at zero: each call writes
-// the in_len int8 values and the scale before the product reads them.
-constexpr size_t kNoAllocMaxIn = 32768;                 // the raw I2_S kernel's limit
-constexpr size_t kNoAllocScratch = kNoAllocMaxIn + 256;  // int8 row, then act_scale
+// file-scope device array, and its TL1 / TQ1_0 lookup GEMVs keep their
+// per-block partial sums there, instead of the library workspace.  Each
+// device holds its own copy until the process ends; its address on a device
+// comes from hipGetSymbolAddress (the array's name is not a device address
+// in host code).  All calls on one device share it, so calls that overlap
+// on one device race.  Nothing in it needs to start at zero: each call
+// writes the in_len int8 values and the scale, or every partial sum, before
+// the next kernel reads them.
+constexpr size_t kNoAllocMaxIn = 32768;          // the raw I2_S kernel's limit
+constexpr size_t kNoAllocLut = size_t(16) << 20;  // lookup partial sums (the 248320x5120 lm_head needs 9.9 MB)
+constexpr size_t kNoAllocScratch = kNoAllocLut;  // 2-bit kinds: int8 row at 0, act_scale at kNoAllocMaxIn
+static_assert(kNoAllocMaxIn + 256 <= kNoAllocScratch, "noalloc scratch layout");
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratch];
 
 namespace {
@@ -362,8 +381,18 @@ extern "C" {
 int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                           float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    if (kind != OURO_KIND_I2 && kind != OURO_KIND_I2_S)  // no scratch, and no workspace (TL1: the direct kernel)
-        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, false);
+    if (kind == OURO_KIND_TL1 || kind == OURO_KIND_TQ1_0) {
+        // the lookup GEMV's partial sums in the static array when they fit;
+        // larger shapes (and fewer than 8192 rows) run the direct kernel,
+        // which needs no scratch
+        void *p = nullptr;
+        const int st = scratch_ptr(&p);
+        if (st) return st;
+        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, false,
+                        static_cast<float *>(p), kNoAllocLut);
+    }
+    if (kind != OURO_KIND_I2 && kind != OURO_KIND_I2_S)  // no scratch, and no workspace
+        return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, false, nullptr, 0);
     if (in_len > kNoAllocMaxIn)
         return fail(OURO_ERR_SHAPE, "ouro_matvec_q_noalloc: in_len %zu exceeds the %zu-element static scratch",
                     in_len, kNoAllocMaxIn);
@@ -372,19 +401,19 @@ int ouro_matvec_q_noalloc(const void *payload, int kind, size_t out_len, size_t 
     if (st) return st;
     int8_t *xq = static_cast<int8_t *>(p);
     float *s = reinterpret_cast<float *>(static_cast<uint8_t *>(p) + kNoAllocMaxIn);
-    return matmul_q(payload, kind, out_len, in_len, x, 1, y, xq, s, stream, false);
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, xq, s, stream, false, nullptr, 0);
 }
 
 int ouro_matvec_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                   float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, true);
+    return matmul_q(payload, kind, out_len, in_len, x, 1, y, nullptr, nullptr, stream, true, nullptr, 0);
 }
 
 int ouro_matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x,
                   size_t k, float *y, void *stream) {
     OURO_REQUIRE_INIT();
-    return matmul_q(payload, kind, out_len, in_len, x, k, y, nullptr, nullptr, stream, true);
+    return matmul_q(payload, kind, out_len, in_len, x, k, y, nullptr, nullptr, stream, true, nullptr, 0);
 }
 
 }  // extern "C"

@@ -18,7 +18,8 @@
 
 namespace ouro {
 int matmul_q(const void *payload, int kind, size_t out_len, size_t in_len, const float *x, size_t k,
-             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace);
+             float *y, int8_t *xq_scratch, float *act_scale_scratch, void *stream, bool use_workspace,
+             float *lut_partial, size_t lut_partial_bytes);
 int i2_tile(const uint8_t *canonical, size_t out_len, size_t in_len, uint8_t *tiled,
             const float *w_scale, void *stream, int src_i2s);
 size_t i2_tiled_bytes(size_t out_len, size_t in_len);
@@ -302,7 +303,8 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         return i2_gemm_mfma(static_cast<const uint8_t *>(w->mfma), w->out_len, w->in_len, w_scale, sc->xq,
                             sc->act_scale, k, y, nullptr, stream, 0);
     }
-    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, sc->xq, sc->act_scale, stream, false);
+    return matmul_q(w->payload, w->kind, w->out_len, w->in_len, x, k, y, sc->xq, sc->act_scale, stream, false,
+                    nullptr, 0);
 }
 
 int ouro_weight_matvec_argmax(ouro_weight_t w, const float *x, float *y, int32_t *idx, void *stream) {
