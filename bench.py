@@ -340,6 +340,18 @@ def bench_tl1(stream, steps, warmup):
             kcols.append({"shape": name, "k": k, "us_per_call": round(t * 1e3, 2),
                           "weight_stream_GBs": round(out_len * (in_len // 128) * 28 / (t * 1e-3) / 1e9, 1)})
         call("ouro_weight_free", hk.value)
+    # a resident TQ1_0 handle of the lm_head shape (random bytes, d = 1): K = 1 the lookup matvec, K >= 2
+    # the same int8 MFMA pass on its trits
+    hk = C.c_void_p()
+    call("ouro_weight_upload", KIND_TQ1_0, tq.ctypes.data, tq.nbytes, TL1_OUT, TL1_IN, 1.0, 8, C.byref(hk))
+    xk = DeviceBuffer.from_host(rng.standard_normal(8 * TL1_IN).astype(np.float32))
+    yk = DeviceBuffer((8 * TL1_OUT,), np.float32)
+    for k in (1, 4, 8):
+        t = time_events(stream, lambda _i: call("ouro_weight_matmul", hk.value, xk.ptr, k, yk.ptr, stream),
+                        max(3, steps // 5), 2)
+        kcols.append({"shape": "248320x5120 TQ1_0 handle", "k": k, "us_per_call": round(t * 1e3, 2),
+                      "weight_stream_GBs": round(tq.nbytes / (t * 1e-3) / 1e9, 1)})
+    call("ouro_weight_free", hk.value)
     # the same on the raw payload through ouro_matmul_q (K = 1: the raw lookup matvec)
     w = DeviceBuffer.from_host(payload)
     xk = DeviceBuffer.from_host(rng.standard_normal(8 * TL1_IN).astype(np.float32))

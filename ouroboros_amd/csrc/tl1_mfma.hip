@@ -52,8 +52,24 @@ __device__ __forceinline__ int tl1_trit_at(const uint8_t *grp, int e) {
     return static_cast<int>((q * 3u) >> 8) - 1;
 }
 
+__device__ __forceinline__ int tq1_trit_at(const uint8_t *blk, int e) {
+    // element e of a 54-byte TQ1_0 block (dequant.rs:50-80): qs bytes 0..31
+    // carry elements 32 n + m, bytes 32..47 elements 160 + 16 n + m, qh
+    // bytes 48..51 elements 240 + 4 n + m, n the base-3 digit
+    int byte, n;
+    if (e < 160) byte = e & 31, n = e >> 5;
+    else if (e < 240) byte = 32 + ((e - 160) & 15), n = (e - 160) >> 4;
+    else byte = 48 + ((e - 240) & 3), n = (e - 240) >> 2;
+    uint32_t p3 = 1;
+    for (int i = 0; i < n; ++i) p3 *= 3;
+    const uint32_t q = (static_cast<uint32_t>(blk[byte]) * p3) & 0xffu;
+    return static_cast<int>((q * 3u) >> 8) - 1;
+}
+
 // One thread per 32-bit word of the unit layout (rows past M and k past K
-// hold zero trits).
+// hold zero trits).  TQ: the source is TQ1_0 (54-byte blocks of 256), else
+// TL1 (28-byte groups of 128).
+template <bool TQ>
 __global__ void tl1_tile_mfma_kernel(const uint8_t *__restrict__ raw, uint32_t *__restrict__ dst, int M, int K,
                                      int nkb, long long total_words) {
     const long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -65,7 +81,7 @@ __global__ void tl1_tile_mfma_kernel(const uint8_t *__restrict__ raw, uint32_t *
     const int kb = static_cast<int>(unit % nkb);
     const long long row = rt * 16 + (l % 16);
     const int kbase = 256 * kb + 64 * s + 16 * (l / 16);
-    const long long rowb = static_cast<long long>(K / 128) * 28;
+    const long long rowb = TQ ? static_cast<long long>(K / 256) * 54 : static_cast<long long>(K / 128) * 28;
     uint32_t word = 0;
     if (row < M) {
 #pragma unroll
@@ -74,7 +90,8 @@ __global__ void tl1_tile_mfma_kernel(const uint8_t *__restrict__ raw, uint32_t *
             for (int i = 0; i < 4; ++i) {
                 const int k = kbase + 4 * j + i;
                 if (k < K) {
-                    const int t = tl1_trit_at(raw + row * rowb + static_cast<long long>(k / 128) * 28, k % 128);
+                    const int t = TQ ? tq1_trit_at(raw + row * rowb + static_cast<long long>(k / 256) * 54, k % 256)
+                                     : tl1_trit_at(raw + row * rowb + static_cast<long long>(k / 128) * 28, k % 128);
                     word |= (static_cast<uint32_t>(-t) & 3u) << (8 * i + 2 * j);
                 }
             }
@@ -82,7 +99,9 @@ __global__ void tl1_tile_mfma_kernel(const uint8_t *__restrict__ raw, uint32_t *
     dst[id] = word;
 }
 
-// d of every (row, group) as f16 bits; groups past K / 128 are 0.
+// d of every (row, group of 128) as f16 bits; groups past K / 128 are 0.
+// TQ: both 128-groups of a TQ1_0 block take the block's d (bytes 52, 53).
+template <bool TQ>
 __global__ void tl1_scales_kernel(const uint8_t *__restrict__ raw, uint16_t *__restrict__ d, int M, int K, int G) {
     const long long id = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (id >= static_cast<long long>(M) * G) return;
@@ -90,8 +109,9 @@ __global__ void tl1_scales_kernel(const uint8_t *__restrict__ raw, uint16_t *__r
     const int g = static_cast<int>(id % G);
     uint16_t v = 0;
     if (g < K / 128) {
-        const uint8_t *p = raw + row * (static_cast<long long>(K / 128) * 28) + static_cast<long long>(g) * 28;
-        v = static_cast<uint16_t>(p[26] | (p[27] << 8));
+        const uint8_t *p = TQ ? raw + row * (static_cast<long long>(K / 256) * 54) + static_cast<long long>(g / 2) * 54 + 52
+                              : raw + row * (static_cast<long long>(K / 128) * 28) + static_cast<long long>(g) * 28 + 26;
+        v = static_cast<uint16_t>(p[0] | (p[1] << 8));
     }
     d[id] = v;
 }
@@ -423,21 +443,34 @@ size_t tl1_xprep_bytes(size_t K, size_t ncols) {
     return nkb * 4 * tiles * 1024 + nkb * 2 * 16 * tiles * (sizeof(float) + sizeof(int32_t));
 }
 
-// Raw TL1 payload (device, row-major groups) -> unit layout + scales.
-int tl1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream) {
-    if (!raw || !codes || !scales || !M || !K || K % 128 || M > 0x7fffffffULL || K > 0x7fffffffULL)
-        return fail(OURO_ERR_SHAPE, "tl1 mfma tiling: bad shape %zu x %zu", M, K);
+namespace {
+template <bool TQ>
+int tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream) {
+    if (!raw || !codes || !scales || !M || !K || K % (TQ ? 256 : 128) || M > 0x7fffffffULL || K > 0x7fffffffULL)
+        return fail(OURO_ERR_SHAPE, "%s mfma tiling: bad shape %zu x %zu", TQ ? "tq1_0" : "tl1", M, K);
     const int nkb = static_cast<int>((K + 255) / 256), G = 2 * nkb;
     const long long words = static_cast<long long>(tl1_mfma_code_bytes(M, K) / 4);
     const hipStream_t s = as_stream(stream);
-    hipLaunchKernelGGL(tl1_tile_mfma_kernel, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, s, raw,
-                       reinterpret_cast<uint32_t *>(codes), static_cast<int>(M), static_cast<int>(K), nkb, words);
+    hipLaunchKernelGGL(tl1_tile_mfma_kernel<TQ>, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, s,
+                       raw, reinterpret_cast<uint32_t *>(codes), static_cast<int>(M), static_cast<int>(K), nkb, words);
     int st = check_launch("tl1_tile_mfma_kernel");
     if (st) return st;
     const long long n = static_cast<long long>(M) * G;
-    hipLaunchKernelGGL(tl1_scales_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, raw, scales,
-                       static_cast<int>(M), static_cast<int>(K), G);
+    hipLaunchKernelGGL(tl1_scales_kernel<TQ>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, raw,
+                       scales, static_cast<int>(M), static_cast<int>(K), G);
     return check_launch("tl1_scales_kernel");
+}
+}  // namespace
+
+// Raw TL1 payload (device, row-major groups) -> unit layout + scales.
+int tl1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream) {
+    return tile_mfma<false>(raw, M, K, codes, scales, stream);
+}
+
+// Raw TQ1_0 payload (device, row-major 54-byte blocks) -> the same unit
+// layout + scales (each block's d for both of its 128-groups).
+int tq1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream) {
+    return tile_mfma<true>(raw, M, K, codes, scales, stream);
 }
 
 namespace {

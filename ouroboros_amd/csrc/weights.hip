@@ -44,6 +44,7 @@ size_t tl1_mfma_code_bytes(size_t M, size_t K);
 size_t tl1_mfma_scale_bytes(size_t M, size_t K);
 size_t tl1_xprep_bytes(size_t K, size_t ncols);
 int tl1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream);
+int tq1_tile_mfma(const uint8_t *raw, size_t M, size_t K, uint8_t *codes, uint16_t *scales, void *stream);
 int tl1_mfma_matmul(const uint8_t *codes, const uint16_t *scales, size_t M, size_t K, const float *x, size_t ncols,
                     float *y, void *scratch, void *stream);
 }  // namespace ouro
@@ -67,7 +68,8 @@ struct ouro_weight {
     size_t out_len = 0, in_len = 0, max_cols = 0;
     void *payload = nullptr;  // device layout of the kind (TL1: the lookup layout)
     void *mfma = nullptr;     // I2 with max_cols >= kMfmaCols: the MFMA layout of the codes;
-                              // TL1 with max_cols >= 2: the trits in that layout, then the group scales
+                              // TL1 / TQ1_0 with max_cols >= 2: the trits in that layout, then the
+                              // scales of every 128-group
     size_t partial_floats = 0;  // TL1, large TQ1_0: per-block partial sums of the lookup kernels
     std::mutex mu;
     std::deque<WeightScratch> scratch;  // stable addresses as sets are added
@@ -125,7 +127,8 @@ WeightScratch *scratch_for(ouro_weight *w, void *stream) {
     const size_t sb = i2 ? align256(w->max_cols * sizeof(float)) : 0;
     const size_t pb = align256(w->partial_floats * sizeof(float));
     const size_t yb = align256(w->out_len * sizeof(float));
-    const size_t mb = (w->kind == OURO_KIND_TL1 && w->mfma) ? align256(tl1_xprep_bytes(w->in_len, 16)) : 0;
+    const size_t mb = ((w->kind == OURO_KIND_TL1 || w->kind == OURO_KIND_TQ1_0) && w->mfma)
+                          ? align256(tl1_xprep_bytes(w->in_len, 16)) : 0;
     WeightScratch sc;
     sc.stream = stream;
     if (hipMalloc(&sc.block, xb + sb + pb + yb + mb + kArgmaxBlocks * 8) != hipSuccess) {
@@ -156,6 +159,11 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
     *out = nullptr;
     const size_t rb = ref_row_bytes(kind, in_len);
     if (!rb) return fail(OURO_ERR_KIND, "ouro_weight_upload: kind %d / in_len %zu unsupported", kind, in_len);
+    const size_t be = kind == OURO_KIND_TL1 ? 128 : kind == OURO_KIND_Q8_0 ? 32
+                      : (kind == OURO_KIND_TQ1_0 || kind == OURO_KIND_Q3K || kind == OURO_KIND_Q4K ||
+                         kind == OURO_KIND_Q5K || kind == OURO_KIND_Q6K) ? 256 : 1;
+    if (in_len % be)  // rows of whole blocks (QuantKind::row_bytes, dequant.rs:376-387)
+        return fail(OURO_ERR_SHAPE, "ouro_weight_upload: in_len %zu not a multiple of the %zu-element block", in_len, be);
     if (!out_len || (kind == OURO_KIND_I2_S ? !i2s_size_ok(bytes, rb * out_len) : bytes != rb * out_len))
         return fail(OURO_ERR_SHAPE, "ouro_weight_upload: %zu bytes, expected %zu%s", bytes, rb * out_len,
                     kind == OURO_KIND_I2_S ? " + 4..32 (scale and padding)" : "");
@@ -242,6 +250,21 @@ int ouro_weight_upload(int kind, const void *host, size_t bytes, size_t out_len,
         // a large TQ1_0 matrix runs the lookup kernel: its block partials live with the handle
         if (kind == OURO_KIND_TQ1_0 && out_len >= kTq1LutRows && tq1_lut_fits(w->payload, in_len))
             w->partial_floats = tq1_lut_partial_floats(out_len, in_len);
+        if (kind == OURO_KIND_TQ1_0 && w->max_cols >= 2) {  // matmuls of several columns: the trits on int8 MFMA
+            const size_t cb = tl1_mfma_code_bytes(out_len, in_len);
+            int st = OURO_OK;
+            if (hipMalloc(&w->mfma, cb + tl1_mfma_scale_bytes(out_len, in_len)) != hipSuccess)
+                st = fail(OURO_ERR_HIP, "ouro_weight_upload: device allocation failed");
+            else
+                st = tq1_tile_mfma(static_cast<const uint8_t *>(w->payload), out_len, in_len,
+                                   static_cast<uint8_t *>(w->mfma),
+                                   reinterpret_cast<uint16_t *>(static_cast<uint8_t *>(w->mfma) + cb), nullptr);
+            if (!st && hipDeviceSynchronize() != hipSuccess) st = fail(OURO_ERR_HIP, "ouro_weight_upload: sync failed");
+            if (st) {
+                release(w);
+                return st;
+            }
+        }
     }
     // the null stream's scratch set
     if (!scratch_for(w, nullptr)) {
@@ -273,7 +296,8 @@ int ouro_weight_matmul(ouro_weight_t w, const float *x, size_t k, float *y, void
         return fail(OURO_ERR_SHAPE, "ouro_weight_matmul: k %zu > max_cols %zu of the handle", k, w->max_cols);
     WeightScratch *sc = scratch_for(w, stream);
     if (!sc) return OURO_ERR_HIP;
-    if (w->kind == OURO_KIND_TL1 && w->mfma && k >= 2) {  // one pass over the trits for all k columns
+    if ((w->kind == OURO_KIND_TL1 || w->kind == OURO_KIND_TQ1_0) && w->mfma && k >= 2) {
+        // one pass over the trits for all k columns
         const size_t cb = tl1_mfma_code_bytes(w->out_len, w->in_len);
         return tl1_mfma_matmul(static_cast<const uint8_t *>(w->mfma),
                                reinterpret_cast<const uint16_t *>(static_cast<const uint8_t *>(w->mfma) + cb),

@@ -114,7 +114,8 @@ def test_tq1_handle_lookup_and_argmax(gpu, orc):
     want = np.concatenate([orc.matvec_q(p, orc.KIND_TQ1_0, out_len, in_len, x[c * in_len:(c + 1) * in_len])
                            for c in range(3)])
     assert close(h.matvec(x[:in_len]), want[:out_len], 1e-5).all()
-    assert close(h.matmul(x, 3), want, 1e-5).all()
+    # 3 columns: one int8 MFMA pass (the handle holds max_cols = 8), the K-column bar (ops.rs:720-750)
+    assert close(h.matmul(x, 3), want, 1e-3).all()
     idx = h.matvec_argmax(x[:in_len])
     best = orc.finite_argmax(want[:out_len])
     assert idx == best or abs(float(want[idx]) - float(want[best])) <= 1e-5 * abs(float(want[best]))

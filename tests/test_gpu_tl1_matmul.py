@@ -4,7 +4,9 @@ digit planes per group, the f16 group scales applied per group.  Checked
 against the oracle's matmul_tl1 at the reference's K-column bar, rel 1e-3
 (ops.rs:720-750), on the reference's own K-column inputs, on the ternary
 layer and lm_head shapes, on rows of 128 (not 256) elements and on more
-columns than one launch takes (16)."""
+columns than one launch takes (16).  TQ1_0 handles take the same pass (their
+trits tiled from the 54-byte blocks, each block's d for both 128-groups),
+checked against the oracle's matmul_q (ops.rs:219-230)."""
 import numpy as np
 import pytest
 
@@ -114,3 +116,48 @@ def test_tl1_handle_single_column_layout_keeps_lookups(gpu, orc):
     want = orc.matmul_tl1(p, out_len, in_len, x, k)
     assert close(h.matmul(x, k), want, 1e-5).all()
     h.free()
+
+
+def tq1_payload(rng, out_len, in_len):
+    p = rng.integers(0, 256, out_len * (in_len // 256) * 54, dtype=np.uint8)
+    g = p.reshape(-1, 54)
+    d = rng.uniform(0.01, 0.1, g.shape[0]).astype(np.float16).view(np.uint16)
+    g[:, 52], g[:, 53] = d & 0xFF, d >> 8
+    return p
+
+
+@pytest.mark.parametrize("out_len,in_len,k", [(6912, 2560, 2), (6912, 2560, 8), (2560, 6912, 4), (37, 256, 5),
+                                              (300, 1024, 17), (129, 768, 33), (9000, 2048, 3)])
+def test_tq1_handle_matmul_mfma(gpu, orc, margin, out_len, in_len, k):
+    rng = np.random.default_rng(out_len * 3 + in_len + k)
+    p = tq1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    x[5] = -30.0  # an outlier in a group of column 0
+    h = ops.Weight(QuantKind.TQ1_0, p, out_len, in_len, max_cols=k)
+    want = orc.matmul_q(p, orc.KIND_TQ1_0, out_len, in_len, x, k)
+    got = h.matmul(x, k)
+    margin(f"TQ1_0 {out_len}x{in_len} k={k}", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+    assert close(h.matvec(x[:in_len]), want[:out_len], 1e-5).all()  # the matvec keeps its own kernels
+    h.free()
+
+
+def test_tq1_handle_matmul_lm_head(gpu, orc, margin):
+    out_len, in_len, k = 248320, 5120, 8
+    rng = np.random.default_rng(12)
+    p = tq1_payload(rng, out_len, in_len)
+    x = rng.standard_normal(k * in_len).astype(np.float32)
+    h = ops.Weight(QuantKind.TQ1_0, p, out_len, in_len, max_cols=k)
+    got = h.matmul(x, k)
+    h.free()
+    want = orc.matmul_q(p, orc.KIND_TQ1_0, out_len, in_len, x, k)
+    margin("TQ1_0 248320x5120 k=8", got, want, 1e-3)
+    assert close(got, want, 1e-3).all()
+
+
+def test_upload_rejects_partial_blocks(gpu):
+    from ouroboros_amd._lib import OuroError
+    for kind, in_len, nb in ((QuantKind.TQ1_0, 384, 54), (QuantKind.TL1, 192, 28), (QuantKind.Q4K, 384, 144)):
+        with pytest.raises(OuroError) as e:
+            ops.Weight(kind, np.zeros(4 * nb, np.uint8), 4, in_len, max_cols=4)
+        assert e.value.code == 2
