@@ -8,11 +8,20 @@
 // one 16-byte piece of the block (plus, for Q3_K, Q5_K and Q6_K, a 16-byte
 // piece of high bits) and whose x values are two runs of 16: elements
 // A + i and A + G + i, i < 16.  A 256-element block has 8 tasks, a Q8_0 block
-// one.  Per task the codes are summed against x as integers-in-float
-// (S = sum q x, an fma chain) and scaled once per run: the contribution is
-// cA S_A - mA X_A + cB S_B - mB X_B with X the run's sum of x (the min, or the
-// code offset -32 / -4 of Q6_K / Q3_K, taken out of the sum).  That keeps the
-// per-element work at a mask, a byte-to-float conversion and an fma.
+// one.  Per task the codes are summed against x (S = sum q x) and scaled once
+// per run: the contribution is cA S_A - mA X_A + cB S_B - mB X_B with X the
+// run's sum of x (the min, or the code offset -32 / -4 of Q6_K / Q3_K, taken
+// out of the sum).
+//
+// Integer sums.  Each run of x is held as exact fixed point: with E the binary
+// exponent of the run's largest |x| (|x| < 2^E), x_int = rint(x 2^(22-E)) =
+// 65536 p0 + 256 p1 + p2 in balanced int8 digits (elements below 2^(E-23) of
+// the run's largest lose their low bits).  The codes, unpacked to one byte
+// each, are dotted with the three digit planes by v_dot4_i32_i8 (4 products
+// a lane operation, exact int32 sums), and S = 2^(E-22) (65536 S0 + 256 S1 +
+// S2) in float.  x is converted once per thread (it stays in registers for
+// the whole launch), so the per-element work is a share of a mask and three
+// quarter-width dot steps.
 //
 // Mapping.  A thread owns one task position of a row (k-stationary): its 32 x
 // values and their run sums stay in registers while the workgroup walks row
@@ -43,11 +52,14 @@ constexpr int kMaxThreads = 1024;
 // 16 bytes at any address: the 4-byte-aligned dwords that cover them, shifted
 // into place.  Every dword read holds at least one of the 16 bytes, so the
 // read stays inside the pages the bytes are on.
+// Ordinary loads: the lines a block shares with its neighbours, and the
+// dword a piece shares with the next piece, are read again from L2.
 __device__ __forceinline__ u32x4 load16_any(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const u32x4 lo = *reinterpret_cast<const u32x4_a4 *>(a & ~uintptr_t(3));
-    const uint32_t e = *reinterpret_cast<const uint32_t *>((a + 15) & ~uintptr_t(3));
-    const uint32_t s = static_cast<uint32_t>(a & 3);
+    // pointer arithmetic (not integer masks) keeps the global address space
+    const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint8_t *base = p - s;
+    const u32x4 lo = *reinterpret_cast<const u32x4_a4 *>(base);
+    const uint32_t e = *reinterpret_cast<const uint32_t *>(base + ((s + 15) & ~3u));
     u32x4 r;
     r.x = __builtin_amdgcn_alignbyte(lo.y, lo.x, s);
     r.y = __builtin_amdgcn_alignbyte(lo.z, lo.y, s);
@@ -62,6 +74,30 @@ __device__ __forceinline__ u32x4 load16(const uint8_t *p) {
     else return load16_any(p);
 }
 
+// The same at a known phase s = (bp + off) & 3: when every row is a whole
+// number of dwords, a lane's phase is the same on every row, so it is worked
+// out once and each load costs one address add per row.
+__device__ __forceinline__ u32x4 load16_at(const uint8_t *bp, int off, uint32_t s) {
+    const uint8_t *base = bp + (off - static_cast<int>(s));
+    const u32x4 lo = *reinterpret_cast<const u32x4_a4 *>(base);
+    const uint32_t e = *reinterpret_cast<const uint32_t *>(base + ((s + 15) & ~3u));
+    u32x4 r;
+    r.x = __builtin_amdgcn_alignbyte(lo.y, lo.x, s);
+    r.y = __builtin_amdgcn_alignbyte(lo.z, lo.y, s);
+    r.z = __builtin_amdgcn_alignbyte(lo.w, lo.z, s);
+    r.w = __builtin_amdgcn_alignbyte(e, lo.w, s);
+    return r;
+}
+
+// Piece j of a block, at offset off: aligned (AL16), at the lane's fixed
+// phase sh[j] (PH), or at any address.
+template <bool AL16, bool PH>
+__device__ __forceinline__ u32x4 piece(const uint8_t *bp, int off, const uint32_t *sh, int j) {
+    if constexpr (AL16) return *reinterpret_cast<const u32x4 *>(bp + off);
+    else if constexpr (PH) return load16_at(bp, off, sh[j]);
+    else return load16_any(bp + off);
+}
+
 __device__ __forceinline__ float f16f(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
@@ -70,35 +106,56 @@ __device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
     return __builtin_amdgcn_ubfe(v, off, w);
 }
 
-// Byte b of a 16-byte piece as a float (unsigned).
-__device__ __forceinline__ float ub(uint32_t w, int b) { return static_cast<float>((w >> (8 * b)) & 0xffu); }
+// A run of 16 x values: its digit planes (byte i of dword d = element
+// 4 d + i), the scale 2^(E-22) and the float sum of the run.
+struct XRun {
+    u32x4 p0, p1, p2;
+    float s, X;
+};
 
-// sum over the 16 bytes of v (each an unsigned code) times x[0..15]
-__device__ __forceinline__ float dot16u(const u32x4 &v, const float (&x)[16]) {
-    float s = 0.f;
+__device__ __forceinline__ void make_run(const float *p, XRun &r) {
+    float v[16];
+    float m = 0.f;
+    r.X = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const uint32_t w = v[d];
+    for (int i = 0; i < 16; ++i) v[i] = p[i];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) s = __builtin_fmaf(ub(w, b), x[4 * d + b], s);
+    for (int i = 0; i < 16; ++i) r.X += v[i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    int E = 0;
+    (void)frexpf(m, &E);  // m = f 2^E, f in [0.5, 1): |x| < 2^E (E = 0 for m = 0)
+    // a non-finite x makes the run's sum NaN
+    r.s = __builtin_isfinite(m) ? ldexpf(1.0f, E - 22) : __builtin_nanf("");
+    uint32_t w0[4] = {0, 0, 0, 0}, w1[4] = {0, 0, 0, 0}, w2[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int xi = __builtin_isfinite(m) ? static_cast<int>(rintf(ldexpf(v[i], 22 - E))) : 0;
+        const int p2 = ((xi + 128) & 255) - 128;
+        const int r1 = (xi - p2) >> 8;  // exact: xi - p2 is a multiple of 256
+        const int p1 = ((r1 + 128) & 255) - 128;
+        const int p0 = (r1 - p1) >> 8;
+        w0[i >> 2] |= static_cast<uint32_t>(p0 & 255) << (8 * (i & 3));
+        w1[i >> 2] |= static_cast<uint32_t>(p1 & 255) << (8 * (i & 3));
+        w2[i >> 2] |= static_cast<uint32_t>(p2 & 255) << (8 * (i & 3));
     }
-    return s;
+    r.p0 = u32x4{w0[0], w0[1], w0[2], w0[3]};
+    r.p1 = u32x4{w1[0], w1[1], w1[2], w1[3]};
+    r.p2 = u32x4{w2[0], w2[1], w2[2], w2[3]};
 }
 
-// the same with signed bytes (Q8_0); the builtin returns the sign-extended
-// field as an unsigned int, so it is read back as int32 before conversion
-__device__ __forceinline__ float dot16s(const u32x4 &v, const float (&x)[16]) {
-    float s = 0.f;
+// sum over the 16 int8 codes of c (byte i of dword d = element 4 d + i)
+// times the run's x, from exact int32 sums per digit plane
+__device__ __forceinline__ float idot(const u32x4 &c, const XRun &x) {
+    int a = 0, b = 0, e = 0;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        const uint32_t w = v[d];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int32_t q = static_cast<int32_t>(__builtin_amdgcn_sbfe(w, 8 * b, 8));
-            s = __builtin_fmaf(static_cast<float>(q), x[4 * d + b], s);
-        }
+        a = __builtin_amdgcn_sdot4(static_cast<int>(c[d]), static_cast<int>(x.p0[d]), a, false);
+        b = __builtin_amdgcn_sdot4(static_cast<int>(c[d]), static_cast<int>(x.p1[d]), b, false);
+        e = __builtin_amdgcn_sdot4(static_cast<int>(c[d]), static_cast<int>(x.p2[d]), e, false);
     }
-    return s;
+    return x.s * __builtin_fmaf(static_cast<float>(a), 65536.f,
+                                __builtin_fmaf(static_cast<float>(b), 256.f, static_cast<float>(e)));
 }
 
 __device__ __forceinline__ u32x4 vmap(const u32x4 &a, uint32_t mask, uint32_t sh) {
@@ -111,20 +168,21 @@ template <int KIND> struct Fmt;
 
 // Q8_0 (dequant.rs:225-231): d f16, then 32 int8 codes; one task per block.
 template <> struct Fmt<OURO_KIND_Q8_0> {
-    static constexpr int BB = 34, EPB = 32, TPB = 1, G = 16;
+    static constexpr int BB = 34, EPB = 32, TPB = 1, G = 16, NP = 2;
     __device__ static int A(int) { return 0; }
+    __device__ static int poff(int, int j) { return 2 + 16 * j; }
     struct Raw { u32x4 a, b; uint32_t d0, d1; };
-    template <bool AL16> __device__ static Raw load(const uint8_t *bp, int) {
+    template <bool AL16, bool PH> __device__ static Raw load(const uint8_t *bp, int, const uint32_t *sh) {
         Raw r;
-        r.a = load16_any(bp + 2);
-        r.b = load16_any(bp + 18);
+        r.a = piece<false, PH>(bp, 2, sh, 0);
+        r.b = piece<false, PH>(bp, 18, sh, 1);
         r.d0 = bp[0];
         r.d1 = bp[1];
         return r;
     }
-    __device__ static float dot(const Raw &r, int, const float (&xa)[16], const float (&xb)[16], float, float) {
+    __device__ static float dot(const Raw &r, int, const XRun &xa, const XRun &xb) {
         const float d = f16f(r.d0 | (r.d1 << 8));
-        return d * (dot16s(r.a, xa) + dot16s(r.b, xb));
+        return d * (idot(r.a, xa) + idot(r.b, xb));
     }
 };
 
@@ -147,36 +205,39 @@ __device__ __forceinline__ void scale_min_k4(int k, uint32_t h1, uint32_t h2, ui
 // 64j + 16h + i (low nibble, sub-block 2j) and 64j + 32 + 16h + i (high
 // nibble, sub-block 2j + 1).
 template <> struct Fmt<OURO_KIND_Q4K> {
-    static constexpr int BB = 144, EPB = 256, TPB = 8, G = 32;
+    static constexpr int BB = 144, EPB = 256, TPB = 8, G = 32, NP = 2;
     __device__ static int A(int u) { return 64 * (u >> 1) + 16 * (u & 1); }
+    __device__ static int poff(int u, int j) { return j ? 16 + 16 * u : 0; }
     struct Raw { u32x4 h, q; };
-    template <bool AL16> __device__ static Raw load(const uint8_t *bp, int u) {
-        return Raw{load16<AL16>(bp), load16<AL16>(bp + 16 + 16 * u)};
+    template <bool AL16, bool PH> __device__ static Raw load(const uint8_t *bp, int u, const uint32_t *sh) {
+        return Raw{piece<AL16, PH>(bp, 0, sh, 0), piece<AL16, PH>(bp, 16 + 16 * u, sh, 1)};
     }
-    __device__ static float dot(const Raw &r, int u, const float (&xa)[16], const float (&xb)[16], float XA, float XB) {
+    __device__ static float dot(const Raw &r, int u, const XRun &xa, const XRun &xb) {
 #pragma clang fp contract(off)
         const int j = u >> 1;
         uint32_t s1, m1, s2, m2;
         scale_min_k4(2 * j, r.h.y, r.h.z, r.h.w, s1, m1);
         scale_min_k4(2 * j + 1, r.h.y, r.h.z, r.h.w, s2, m2);
         const float d = f16f(r.h.x & 0xffffu), dmin = f16f(r.h.x >> 16);
-        const float SA = dot16u(vmap(r.q, 0x0f0f0f0fu, 0), xa);
-        const float SB = dot16u(vmap(r.q, 0x0f0f0f0fu, 4), xb);
-        return (d * static_cast<float>(s1)) * SA - (dmin * static_cast<float>(m1)) * XA +
-               ((d * static_cast<float>(s2)) * SB - (dmin * static_cast<float>(m2)) * XB);
+        const float SA = idot(vmap(r.q, 0x0f0f0f0fu, 0), xa);
+        const float SB = idot(vmap(r.q, 0x0f0f0f0fu, 4), xb);
+        return (d * static_cast<float>(s1)) * SA - (dmin * static_cast<float>(m1)) * xa.X +
+               ((d * static_cast<float>(s2)) * SB - (dmin * static_cast<float>(m2)) * xb.X);
     }
 };
 
 // Q5_K (dequant.rs:454-481): d, dmin, scales[12], qh[32], qs[128].  As Q4_K,
 // with bit 2j (low nibble) / 2j + 1 (high nibble) of qh[16h + i] adding 16.
 template <> struct Fmt<OURO_KIND_Q5K> {
-    static constexpr int BB = 176, EPB = 256, TPB = 8, G = 32;
+    static constexpr int BB = 176, EPB = 256, TPB = 8, G = 32, NP = 3;
     __device__ static int A(int u) { return 64 * (u >> 1) + 16 * (u & 1); }
+    __device__ static int poff(int u, int j) { return j == 0 ? 0 : j == 1 ? 16 + 16 * (u & 1) : 48 + 16 * u; }
     struct Raw { u32x4 h, qh, q; };
-    template <bool AL16> __device__ static Raw load(const uint8_t *bp, int u) {
-        return Raw{load16<AL16>(bp), load16<AL16>(bp + 16 + 16 * (u & 1)), load16<AL16>(bp + 48 + 16 * u)};
+    template <bool AL16, bool PH> __device__ static Raw load(const uint8_t *bp, int u, const uint32_t *sh) {
+        return Raw{piece<AL16, PH>(bp, 0, sh, 0), piece<AL16, PH>(bp, 16 + 16 * (u & 1), sh, 1),
+                   piece<AL16, PH>(bp, 48 + 16 * u, sh, 2)};
     }
-    __device__ static float dot(const Raw &r, int u, const float (&xa)[16], const float (&xb)[16], float XA, float XB) {
+    __device__ static float dot(const Raw &r, int u, const XRun &xa, const XRun &xb) {
 #pragma clang fp contract(off)
         const int j = u >> 1;
         uint32_t s1, m1, s2, m2;
@@ -185,10 +246,10 @@ template <> struct Fmt<OURO_KIND_Q5K> {
         const float d = f16f(r.h.x & 0xffffu), dmin = f16f(r.h.x >> 16);
         const u32x4 lo = vmap(r.q, 0x0f0f0f0fu, 0) | (vmap(r.qh, 0x01010101u, 2 * j) << 4);
         const u32x4 hi = vmap(r.q, 0x0f0f0f0fu, 4) | (vmap(r.qh, 0x01010101u, 2 * j + 1) << 4);
-        const float SA = dot16u(lo, xa);
-        const float SB = dot16u(hi, xb);
-        return (d * static_cast<float>(s1)) * SA - (dmin * static_cast<float>(m1)) * XA +
-               ((d * static_cast<float>(s2)) * SB - (dmin * static_cast<float>(m2)) * XB);
+        const float SA = idot(lo, xa);
+        const float SB = idot(hi, xb);
+        return (d * static_cast<float>(s1)) * SA - (dmin * static_cast<float>(m1)) * xa.X +
+               ((d * static_cast<float>(s2)) * SB - (dmin * static_cast<float>(m2)) * xb.X);
     }
 };
 
@@ -198,14 +259,18 @@ template <> struct Fmt<OURO_KIND_Q5K> {
 // element 128n + 32s + l0 + i (scale 8n + l0/16 + 2s) and that + 64 (scale + 4),
 // code - 32.
 template <> struct Fmt<OURO_KIND_Q6K> {
-    static constexpr int BB = 210, EPB = 256, TPB = 8, G = 64;
+    static constexpr int BB = 210, EPB = 256, TPB = 8, G = 64, NP = 2;
     __device__ static int A(int u) { return 128 * (u >> 2) + 32 * (u & 1) + 16 * ((u >> 1) & 1); }
+    __device__ static int poff(int u, int j) {
+        const int n = u >> 2, s = u & 1, l0 = 16 * ((u >> 1) & 1);
+        return j ? 128 + 32 * n + l0 : 64 * n + 32 * s + l0;
+    }
     struct Raw { u32x4 ql, qh; uint32_t sa, sb, d0, d1; };
-    template <bool AL16> __device__ static Raw load(const uint8_t *bp, int u) {
+    template <bool AL16, bool PH> __device__ static Raw load(const uint8_t *bp, int u, const uint32_t *sh) {
         const int n = u >> 2, s = u & 1, l0 = 16 * ((u >> 1) & 1);
         Raw r;
-        r.ql = load16_any(bp + 64 * n + 32 * s + l0);
-        r.qh = load16_any(bp + 128 + 32 * n + l0);
+        r.ql = piece<false, PH>(bp, 64 * n + 32 * s + l0, sh, 0);
+        r.qh = piece<false, PH>(bp, 128 + 32 * n + l0, sh, 1);
         const uint8_t *sc = bp + 192 + 8 * n + (l0 >> 4) + 2 * s;
         r.sa = sc[0];
         r.sb = sc[4];
@@ -213,14 +278,14 @@ template <> struct Fmt<OURO_KIND_Q6K> {
         r.d1 = bp[209];
         return r;
     }
-    __device__ static float dot(const Raw &r, int u, const float (&xa)[16], const float (&xb)[16], float XA, float XB) {
+    __device__ static float dot(const Raw &r, int u, const XRun &xa, const XRun &xb) {
 #pragma clang fp contract(off)
         const int s = u & 1;
         const float d = f16f(r.d0 | (r.d1 << 8));
         const u32x4 lo = vmap(r.ql, 0x0f0f0f0fu, 0) | (vmap(r.qh, 0x03030303u, 2 * s) << 4);
         const u32x4 hi = vmap(r.ql, 0x0f0f0f0fu, 4) | (vmap(r.qh, 0x03030303u, 4 + 2 * s) << 4);
-        const float SA = dot16u(lo, xa) - 32.f * XA;
-        const float SB = dot16u(hi, xb) - 32.f * XB;
+        const float SA = idot(lo, xa) - 32.f * xa.X;
+        const float SB = idot(hi, xb) - 32.f * xb.X;
         const float ca = d * static_cast<float>(static_cast<int8_t>(r.sa));
         const float cb = d * static_cast<float>(static_cast<int8_t>(r.sb));
         return ca * SA + cb * SB;
@@ -234,15 +299,19 @@ template <> struct Fmt<OURO_KIND_Q6K> {
 // low four bits nibble k / 8 of scale byte k % 8, its high two bits field
 // k / 4 of byte 8 + k % 4), value d (scale - 32) code.
 template <> struct Fmt<OURO_KIND_Q3K> {
-    static constexpr int BB = 110, EPB = 256, TPB = 8, G = 32;
+    static constexpr int BB = 110, EPB = 256, TPB = 8, G = 32, NP = 2;
     __device__ static int A(int u) { return 128 * (u >> 2) + 64 * (u & 1) + 16 * ((u >> 1) & 1); }
+    __device__ static int poff(int u, int j) {
+        const int n = u >> 2, l0 = 16 * ((u >> 1) & 1);
+        return j ? l0 : 32 + 32 * n + l0;
+    }
     struct Raw { u32x4 q, hm; uint32_t la, ha, lb, hb, d0, d1; };
-    template <bool AL16> __device__ static Raw load(const uint8_t *bp, int u) {
+    template <bool AL16, bool PH> __device__ static Raw load(const uint8_t *bp, int u, const uint32_t *sh) {
         const int n = u >> 2, t = u & 1, l0 = 16 * ((u >> 1) & 1);
         const int ka = 8 * n + 4 * t + (l0 >> 4), kb = ka + 2;
         Raw r;
-        r.q = load16_any(bp + 32 + 32 * n + l0);
-        r.hm = load16_any(bp + l0);
+        r.q = piece<false, PH>(bp, 32 + 32 * n + l0, sh, 0);
+        r.hm = piece<false, PH>(bp, l0, sh, 1);
         const uint8_t *sc = bp + 96;
         r.la = sc[ka & 7];
         r.ha = sc[8 + (ka & 3)];
@@ -252,7 +321,7 @@ template <> struct Fmt<OURO_KIND_Q3K> {
         r.d1 = bp[109];
         return r;
     }
-    __device__ static float dot(const Raw &r, int u, const float (&xa)[16], const float (&xb)[16], float XA, float XB) {
+    __device__ static float dot(const Raw &r, int u, const XRun &xa, const XRun &xb) {
 #pragma clang fp contract(off)
         const int n = u >> 2, t = u & 1, l0 = 16 * ((u >> 1) & 1);
         const int ka = 8 * n + 4 * t + (l0 >> 4), kb = ka + 2;
@@ -262,8 +331,8 @@ template <> struct Fmt<OURO_KIND_Q3K> {
         const uint32_t sb = bfe(r.lb, 4 * (kb >> 3), 4) | (bfe(r.hb, 2 * (kb >> 2), 2) << 4);
         const u32x4 ca = vmap(r.q, 0x03030303u, 2 * j0) | (vmap(r.hm, 0x01010101u, 4 * n + j0) << 2);
         const u32x4 cb = vmap(r.q, 0x03030303u, 2 * j0 + 2) | (vmap(r.hm, 0x01010101u, 4 * n + j0 + 1) << 2);
-        const float SA = dot16u(ca, xa) - 4.f * XA;
-        const float SB = dot16u(cb, xb) - 4.f * XB;
+        const float SA = idot(ca, xa) - 4.f * xa.X;
+        const float SB = idot(cb, xb) - 4.f * xb.X;
         const float fa = d * (static_cast<float>(sa) - 32.f);
         const float fb = d * (static_cast<float>(sb) - 32.f);
         return fa * SA + fb * SB;
@@ -285,91 +354,201 @@ struct KqArgs {
 static_assert(sizeof(KqArgs) == 56, "KqArgs: kernel argument layout");
 
 template <int KIND>
-__device__ __forceinline__ void load_x(const float *xc, int blk, int u, float (&xa)[16], float (&xb)[16], float &XA,
-                                       float &XB) {
+__device__ __forceinline__ void load_x(const float *xc, int blk, int u, XRun &xa, XRun &xb) {
     using F = Fmt<KIND>;
     const float *p = xc + static_cast<long long>(blk) * F::EPB + F::A(u);
-    XA = 0.f;
-    XB = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        xa[i] = p[i];
-        xb[i] = p[F::G + i];
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        XA += xa[i];
-        XB += xb[i];
-    }
+    make_run(p, xa);
+    make_run(p + F::G, xb);
 }
 
-// The per-thread sums of one tile (R rows of each slot) into LDS, then one
-// wavefront per output row adds its task set's sums.
+// Row sums meet in LDS and are added and stored once per batch of tiles, so
+// no global store sits between a tile's loads and the next tile's: a store
+// in the loop makes the compiler wait for every load in flight (the vector
+// memory counter covers loads and stores in issue order) before it reuses the
+// store's registers.
+//
+// Several task sets per workgroup (slots > 1): each thread's sum of each row
+// of a batch of up to kBatch tiles, red[(b R + r) nt + t]; one wavefront per
+// row adds a row's task sums.
+constexpr int kBatch = 4;
+// One task set per workgroup (slots == 1): each wavefront adds its lanes'
+// sums in registers and keeps one value per row, red[(b R + r) nwaves +
+// wave], for a batch of up to kBatch1 tiles.
+constexpr int kBatch1 = 64;
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt and lgkmcnt left at their
+// maxima) at the end of a flush: its stores are then known complete on the
+// way back to the loop head, so the compiler need not drain the next tile's
+// loads there before reusing the stores' registers.
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 template <int R>
-__device__ __forceinline__ void tile_reduce(const KqArgs &a, float *red, const float (&v)[R], int tile, int col) {
+__device__ __forceinline__ void stash(float *red, const float (&v)[R], int b) {
+    const int t = threadIdx.x, nt = blockDim.x;
+#pragma unroll
+    for (int r = 0; r < R; ++r) red[(b * R + r) * nt + t] = v[r];
+}
+
+// Rows of the nb tiles tile0, tile0 + g, ... of a batch.
+template <int R>
+__device__ __forceinline__ void flush(const KqArgs &a, const float *red, int nb, int tile0, int g, int col) {
     const int t = threadIdx.x, nt = blockDim.x;
     const int rows_per_tile = a.slots * R;
     const int wave = t >> 6, lane = t & 63, nwaves = nt >> 6;
-#pragma unroll
-    for (int r = 0; r < R; ++r) red[r * nt + t] = v[r];
     __syncthreads();
-    for (int o = wave; o < rows_per_tile; o += nwaves) {
-        const int s = o / R, r = o - s * R;
-        const float *src = red + r * nt + s * a.tpr;
+    for (int o = wave; o < nb * rows_per_tile; o += nwaves) {
+        const int b = o / rows_per_tile, ob = o - b * rows_per_tile;
+        const int s = ob / R, r = ob - s * R;
+        const float *src = red + (b * R + r) * nt + s * a.tpr;
         float acc = 0.f;
         for (int i = lane; i < a.tpr; i += 64) acc += src[i];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) acc += xor_shfl(acc, off);
-        const int row = tile * rows_per_tile + o;
+        const int row = (tile0 + b * g) * rows_per_tile + ob;
         if (lane == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
     }
     __syncthreads();
+    vm_drain();
+}
+
+__device__ __forceinline__ float fbits(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ unsigned ubits(float f) { return __builtin_bit_cast(unsigned, f); }
+// x of the lane the DPP control selects (0 where it selects none)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return fbits(static_cast<unsigned>(__builtin_amdgcn_update_dpp(0, static_cast<int>(ubits(x)), CTRL, 0xf, 0xf, false)));
+}
+
+// Row totals of R per-lane values over the 64 lanes without LDS: offsets 32
+// and 16 by v_permlane32_swap / v_permlane16_swap (halving the value count
+// while R allows), then a DPP shift-right scan inside 16-lane rows.  Lane L
+// with L % (64 / R) == 64 / R - 1 returns the total of row L / (64 / R).
+template <int R>
+__device__ __forceinline__ float row_totals_f(float (&v)[R]) {
+    static_assert(R == 1 || R == 2 || R == 4, "R is 1, 2 or 4");
+    constexpr int span = 64 / R;
+    if constexpr (R > 1) {
+#pragma unroll
+        for (int i = 0; i < R / 2; ++i) {
+            const auto q = __builtin_amdgcn_permlane32_swap(ubits(v[i]), ubits(v[i + R / 2]), false, false);
+            v[i] = fbits(q[0]) + fbits(q[1]);
+        }
+    } else {
+        const auto q = __builtin_amdgcn_permlane32_swap(ubits(v[0]), ubits(v[0]), false, false);
+        v[0] = fbits(q[0]) + fbits(q[1]);
+    }
+    if constexpr (R > 2) {
+        const auto q = __builtin_amdgcn_permlane16_swap(ubits(v[0]), ubits(v[1]), false, false);
+        v[0] = fbits(q[0]) + fbits(q[1]);
+    } else {
+        const auto q = __builtin_amdgcn_permlane16_swap(ubits(v[0]), ubits(v[0]), false, false);
+        v[0] = fbits(q[0]) + fbits(q[1]);
+    }
+    constexpr int tail = span < 16 ? span : 16;
+    if constexpr (tail > 1) v[0] += dpp_f<0x111>(v[0]);  // row_shr:1
+    if constexpr (tail > 2) v[0] += dpp_f<0x112>(v[0]);
+    if constexpr (tail > 4) v[0] += dpp_f<0x114>(v[0]);
+    if constexpr (tail > 8) v[0] += dpp_f<0x118>(v[0]);
+    return v[0];
+}
+
+// slots == 1: the wavefront's totals of tile b's R rows into LDS (lanes past
+// the task set add 0).
+template <int R>
+__device__ __forceinline__ void stash1(float *red, float (&v)[R], int b, bool live) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nwaves = blockDim.x >> 6;
+    if (!live) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = 0.f;
+    }
+    const float s = row_totals_f<R>(v);
+    constexpr int span = 64 / R;
+    if (lane % span == span - 1) red[(b * R + lane / span) * nwaves + wave] = s;
+}
+
+template <int R>
+__device__ __forceinline__ void flush1(const KqArgs &a, const float *red, int nb, int tile0, int g, int col) {
+    const int t = threadIdx.x, nwaves = blockDim.x >> 6;
+    __syncthreads();
+    for (int o = t; o < nb * R; o += blockDim.x) {
+        const int b = o / R, r = o - b * R;
+        float acc = 0.f;
+        for (int w = 0; w < nwaves; ++w) acc += red[(b * R + r) * nwaves + w];
+        const int row = (tile0 + b * g) * R + r;
+        if (row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+    }
+    __syncthreads();
+    vm_drain();
 }
 
 // One workgroup walks tiles blockIdx.x, + gridDim.x, ...; the loads of the
 // next tile are issued before the current one is summed (two register sets).
 // Lanes past the last slot (padding to a whole wavefront) run a clamped copy
 // of a real task whose sums are never read, so no load sits behind a branch.
-template <int KIND, int R, bool AL16, int MAXT>
+template <int KIND, int R, bool AL16, bool PH, int MAXT>
 __global__ __launch_bounds__(MAXT) void kq_gemv_kernel(KqArgs a) {
     using F = Fmt<KIND>;
-    extern __shared__ float red[];  // [R][blockDim.x]
+    extern __shared__ float red[];  // slots == 1: [kBatch1][R][wavefronts], else [kBatch][R][blockDim.x]
     const int t = threadIdx.x;
     const int slot = min(t / a.tpr, a.slots - 1);
     const int task = min(t - slot * a.tpr, a.tpr - 1);
     const int blk = task / F::TPB, u = task % F::TPB;
     const int col = blockIdx.y;
-    float xa[16], xb[16], XA, XB;
-    load_x<KIND>(a.x + static_cast<long long>(col) * a.in_len, blk, u, xa, xb, XA, XB);
+    XRun xa, xb;
+    load_x<KIND>(a.x + static_cast<long long>(col) * a.in_len, blk, u, xa, xb);
     const int rows_per_tile = a.slots * R;
     const uint8_t *wb = a.w + static_cast<long long>(blk) * F::BB;
+    // a row is under 4 GiB (the host checks), so its offset is one 32 x 32 -> 64-bit multiply-add
+    const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
+    // PH: rows are whole dwords, so each piece's byte phase is the same on every row
+    uint32_t sh[F::NP];
+#pragma unroll
+    for (int j = 0; j < F::NP; ++j) sh[j] = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(wb + F::poff(u, j)) & 3);
     auto issue = [&](typename F::Raw(&raw)[R], int tile) {
         const int row0 = min(tile, a.tiles - 1) * rows_per_tile + slot * R;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int row = min(row0 + r, a.out_len - 1);  // clamped rows are computed and dropped
-            raw[r] = F::template load<AL16>(wb + row * a.row_bytes, u);
+            const uint32_t row = static_cast<uint32_t>(min(row0 + r, a.out_len - 1));  // clamped rows are dropped
+            raw[r] = F::template load<AL16, PH>(wb + static_cast<uint64_t>(row) * rb32, u, sh);
         }
     };
-    auto sum = [&](const typename F::Raw(&raw)[R], int tile) {
-        float v[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) v[r] = F::dot(raw[r], u, xa, xb, XA, XB);
-        tile_reduce<R>(a, red, v, tile, col);
-    };
-    typename F::Raw ra[R], rb[R];
     const int g = gridDim.x;
     int tile = blockIdx.x;
     if (tile >= a.tiles) return;
+    int tile0 = tile, nb = 0;  // the batch's first tile and its tiles so far
+    // sum one tile into the batch; a full batch, or the last tile, is added up
+    const bool one = a.slots == 1;          // uniform
+    const bool live = t < a.tpr * a.slots;  // not a padding lane
+    const int batch = one ? kBatch1 : kBatch;
+    auto sum = [&](const typename F::Raw(&raw)[R]) {
+        float v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = F::dot(raw[r], u, xa, xb);
+        if (one) stash1<R>(red, v, nb, live);
+        else stash<R>(red, v, nb);
+        ++nb;
+        tile += g;
+        if (nb == batch || tile >= a.tiles) {  // uniform over the workgroup
+            if (one) flush1<R>(a, red, nb, tile0, g, col);
+            else flush<R>(a, red, nb, tile0, g, col);
+            nb = 0;
+            tile0 = tile;
+        }
+    };
+    // The scheduling barriers keep each tile's loads ahead of the previous
+    // tile's arithmetic: without them the compiler starts the sum first, and
+    // then waits for every load in flight before issuing the next tile's.
+    typename F::Raw ra[R], rb[R];
     issue(ra, tile);
+    vm_drain();  // the loop head is then reached with only the loop's own loads in flight
     for (;;) {
         issue(rb, tile + g);
-        sum(ra, tile);
-        tile += g;
+        __builtin_amdgcn_sched_barrier(0);
+        sum(ra);
         if (tile >= a.tiles) break;
         issue(ra, tile + g);
-        sum(rb, tile);
-        tile += g;
+        __builtin_amdgcn_sched_barrier(0);
+        sum(rb);
         if (tile >= a.tiles) break;
     }
 }
@@ -387,21 +566,22 @@ __global__ __launch_bounds__(256) void kq_row_kernel(KqArgs a) {
     float acc = 0.f;
     for (int task = lane; task < a.tpr; task += 64) {
         const int blk = task / F::TPB, u = task % F::TPB;
-        float xa[16], xb[16], XA, XB;
-        load_x<KIND>(xc, blk, u, xa, xb, XA, XB);
+        XRun xa, xb;
+        load_x<KIND>(xc, blk, u, xa, xb);
+        const uint32_t none[F::NP] = {};
         const typename F::Raw raw =
-            F::template load<false>(a.w + row * a.row_bytes + static_cast<long long>(blk) * F::BB, u);
-        acc += F::dot(raw, u, xa, xb, XA, XB);
+            F::template load<false, false>(a.w + row * a.row_bytes + static_cast<long long>(blk) * F::BB, u, none);
+        acc += F::dot(raw, u, xa, xb);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc += xor_shfl(acc, off);
     if (lane == 0) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
 }
 
-// Rows per slot per tile (two tiles' loads in flight): measured best on
-// 248320x5120 and 6912x2560, with workgroups of at most 256 threads (larger
-// ones, 320-512 threads, were 10-40 % slower at the same rows per tile).
-template <int KIND> constexpr int kRows = KIND == OURO_KIND_Q3K ? 1 : (KIND == OURO_KIND_Q5K || KIND == OURO_KIND_Q6K) ? 2 : 4;
+// Rows per slot per tile (two tiles' loads in flight): measured best over
+// 248320x5120 and 6912x2560 (R = 1, 2, 4), with workgroups of at most 256
+// threads (384- and 512-thread caps were 10-60 % slower).
+template <int KIND> constexpr int kRows = KIND == OURO_KIND_Q4K ? 4 : 2;
 constexpr int kSlotCap = 256;
 
 int cu_count() {
@@ -416,38 +596,52 @@ int cu_count() {
     return n;
 }
 
+// Launch shape for rows of tpr tasks: slots side by side in a workgroup of
+// nt threads (up to 256 threads, the most rows side by side with the fewest
+// idle lanes; a longer row is one task set of up to 1024 threads).  tpr past
+// 1024: the row kernel (slots = 0).
+struct KqPlan {
+    int slots, nt;
+};
+
+KqPlan kq_plan(int tpr) {
+    if (tpr > kMaxThreads) return KqPlan{0, 0};
+    int best = 1;
+    if (tpr <= kSlotCap) {
+        double best_util = 0.0;
+        for (int sl = 1; sl * tpr <= kSlotCap; ++sl) {
+            const int nt = (sl * tpr + 63) / 64 * 64;
+            if (nt > kSlotCap) break;
+            const double util = static_cast<double>(sl * tpr) / nt;
+            if (util > best_util + 1e-9) best_util = util, best = sl;
+        }
+    }
+    return KqPlan{best, (best * tpr + 63) / 64 * 64};
+}
+
 template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
+    const bool ph = a.row_bytes % 4 == 0;
     using F = Fmt<KIND>;
     a.tpr = a.in_len / F::EPB * F::TPB;
-    if (a.tpr > kMaxThreads) {
+    const KqPlan pl = kq_plan(a.tpr);
+    if (!pl.slots) {
         dim3 grid((a.out_len + 3) / 4, k);
         hipLaunchKernelGGL(kq_row_kernel<KIND>, grid, dim3(256), 0, s, a);
         return check_launch("kq_row_kernel");
     }
-    // slots: up to 256 threads, the most rows side by side with the fewest
-    // idle lanes; a longer row is one task set of up to 1024 threads
-    int best = 1;
-    if (a.tpr <= kSlotCap) {
-        double best_util = 0.0;
-        for (int sl = 1; sl * a.tpr <= kSlotCap; ++sl) {
-            const int nt = (sl * a.tpr + 63) / 64 * 64;
-            if (nt > kSlotCap) break;
-            const double util = static_cast<double>(sl * a.tpr) / nt;
-            if (util > best_util + 1e-9) best_util = util, best = sl;
-        }
-    }
-    a.slots = best;
-    const int nt = (best * a.tpr + 63) / 64 * 64;
-    const hipStream_t ss = s;
+    a.slots = pl.slots;
+    const int nt = pl.nt;
     auto go = [&](auto rows_c, auto maxt_c) {
         constexpr int R = decltype(rows_c)::value, MAXT = decltype(maxt_c)::value;
-        a.tiles = (a.out_len + best * R - 1) / (best * R);
+        a.tiles = (a.out_len + a.slots * R - 1) / (a.slots * R);
         const int grid_x = std::min(a.tiles, cu_count() * std::max(1, 2048 / nt));
-        const size_t lds = static_cast<size_t>(R) * nt * sizeof(float);
+        const size_t lds = (a.slots == 1 ? static_cast<size_t>(kBatch1) * R * (nt / 64)
+                                         : static_cast<size_t>(kBatch) * R * nt) * sizeof(float);
         dim3 grid(grid_x, k);
-        if (al16) hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, true, MAXT>), grid, dim3(nt), lds, ss, a);
-        else hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, false, MAXT>), grid, dim3(nt), lds, ss, a);
+        if (al16) hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, true, false, MAXT>), grid, dim3(nt), lds, s, a);
+        else if (ph) hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, false, true, MAXT>), grid, dim3(nt), lds, s, a);
+        else hipLaunchKernelGGL((kq_gemv_kernel<KIND, R, false, false, MAXT>), grid, dim3(nt), lds, s, a);
     };
     if (nt <= 512) go(std::integral_constant<int, kRows<KIND>>{}, std::integral_constant<int, 512>{});
     else go(std::integral_constant<int, 1>{}, std::integral_constant<int, kMaxThreads>{});
@@ -483,6 +677,7 @@ int kq_matmul(const void *payload, int kind, size_t out_len, size_t in_len, cons
     a.x = x;
     a.y = y;
     a.row_bytes = static_cast<long long>(in_len / epb * bb);
+    if (a.row_bytes >= (1LL << 32)) return fail(OURO_ERR_SHAPE, "matvec_q kind %d: in_len %zu too large", kind, in_len);
     a.out_len = static_cast<int>(out_len);
     a.in_len = static_cast<int>(in_len);
     // the 144- and 176-byte blocks keep 16-byte alignment when the payload has it
