@@ -415,19 +415,31 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     static_assert(kPage % kWK == 0, "a wavefront's keys lie in one page");
     const int wkeys = min(kWK, n - wave * kWK);  // keys of this wave (<= 0: none)
     const long long wrow = wkeys > 0 ? prow[wave * kWK / kPage] + wave * kWK % kPage : 0;
-#pragma unroll 8
-    for (int it = 0; it < (wkeys > 0 ? kWK / 4 : 0); ++it) {
-        const int jj = 4 * it + g4;
-        const float *kp = a.kc + ((wrow + min(jj, max(wkeys - 1, 0))) * a.nkv + kvh) * kHd + 8 * gl;
-        // the KV cache is read once per step: non-temporal loads
-        const float4 k0 = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp)));
-        const float4 k1 = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp + 4)));
+    // kB key rows' loads are issued together before their dot products: the
+    // conditional score store splits an iteration into several basic blocks,
+    // so the compiler would not hoist the next key's loads across it
+    constexpr int kB = 8;
+    static_assert((kWK / 4) % kB == 0, "whole load batches");
+    for (int it0 = 0; it0 < (wkeys > 0 ? kWK / 4 : 0); it0 += kB) {
+        float4 k0[kB], k1[kB];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float d = q[g][0].x * k0.x + q[g][0].y * k0.y + q[g][0].z * k0.z + q[g][0].w * k0.w +
-                      q[g][1].x * k1.x + q[g][1].y * k1.y + q[g][1].z * k1.z + q[g][1].w * k1.w;
-            d = row16_sum(d);
-            if (gl == 0 && jj < wkeys) sc[g][wave * kWK + jj] = d * a.scale;
+        for (int i = 0; i < kB; ++i) {
+            const int jj = 4 * (it0 + i) + g4;
+            const float *kp = a.kc + ((wrow + min(jj, max(wkeys - 1, 0))) * a.nkv + kvh) * kHd + 8 * gl;
+            // the KV cache is read once per step: non-temporal loads
+            k0[i] = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp)));
+            k1[i] = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(kp + 4)));
+        }
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+            const int jj = 4 * (it0 + i) + g4;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float d = q[g][0].x * k0[i].x + q[g][0].y * k0[i].y + q[g][0].z * k0[i].z + q[g][0].w * k0[i].w +
+                          q[g][1].x * k1[i].x + q[g][1].y * k1[i].y + q[g][1].z * k1[i].z + q[g][1].w * k1[i].w;
+                d = row16_sum(d);
+                if (gl == 0 && jj < wkeys) sc[g][wave * kWK + jj] = d * a.scale;
+            }
         }
     }
     __syncthreads();
