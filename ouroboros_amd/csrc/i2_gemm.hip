@@ -171,6 +171,12 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
         }
     };
 
+    // every column's activation scale, for the epilogue, ahead of the k loop:
+    // its stores would keep the compiler from moving a later load above them
+    float as[WC];
+#pragma unroll
+    for (int c = 0; c < WC; ++c) as[c] = a.act_scale[min(n0 + 16 * c + (lane & 15), a.N - 1)];
+
     v4i acc[WR][WC];
 #pragma unroll
     for (int r = 0; r < WR; ++r)
@@ -257,7 +263,7 @@ __global__ __launch_bounds__(kWave *kGemmWaves *KS) void i2_gemm_mfma_kernel(Mfm
     for (int c = 0; c < WC; ++c) {
         const int n = n0 + 16 * c + (lane & 15);
         if (n >= a.N) continue;
-        const I8sInv ds = i8s_inv(a.act_scale[n]);  // (acc / s) without a division per output
+        const I8sInv ds = i8s_inv(as[c]);  // (acc / s) without a division per output
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int row = (rt0 + r) * 16 + 4 * (lane >> 4);
@@ -385,6 +391,11 @@ void i2_gemm_big_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[r][c][e] = 0;
 
+    // every column's activation scale, for the epilogue, ahead of the k loop:
+    // its stores would keep the compiler from moving a later load above them
+    float as[kBigTN];
+#pragma unroll
+    for (int c = 0; c < kBigTN; ++c) as[c] = a.act_scale[min(n0 + c * 32 + (lane & 31), a.N - 1)];
     load_x(0, 0);
     load_w(0);
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): this wavefront's LDS fills have landed
@@ -432,7 +443,7 @@ void i2_gemm_big_kernel(GemmArgs a) {
     for (int c = 0; c < kBigTN; ++c) {
         const int n = n0 + c * 32 + (lane & 31);
         if (n >= a.N) continue;
-        const I8sInv ds = i8s_inv(a.act_scale[n]);  // (acc / s) without a division per output
+        const I8sInv ds = i8s_inv(as[c]);  // (acc / s) without a division per output
 #pragma unroll
         for (int r = 0; r < kBigTM; ++r)
 #pragma unroll
@@ -521,6 +532,7 @@ template <int WC, int WR>
 __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel(SkinnyGroup g) {
     constexpr int TR = 16 * WR, TC = 16 * WC + 1;
     __shared__ int tile[TR * TC];
+    __shared__ float sas[16 * WC];  // the columns' activation scales, read before the k loop
     // Workgroups numbered XCD by XCD (workgroup i runs on XCD i % 8), so the
     // ncg column groups of a row block, which read the same weight units,
     // are served by one L2: numbered round-robin, each group's XCD fetched
@@ -547,6 +559,8 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
     const int rt0 = (bx - g.bstart[pi]) * WR;
     const int nrt = (a.M + 15) / 16;
     for (int i = tid; i < TR * TC; i += blockDim.x) tile[i] = 0;
+    // (the epilogue's loads would otherwise wait behind its own stores)
+    if (tid < 16 * WC) sas[tid] = a.act_scale[min(16 * ct0 + tid, a.N - 1)];
     v4i acc[WR][WC];
 #pragma unroll
     for (int r = 0; r < WR; ++r)
@@ -612,7 +626,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         for (int i = tid; i < TR * 8 * WC; i += blockDim.x) {
             const int nt = i / (TR / 2), rr = 2 * (i % (TR / 2)), row = rt0 * 16 + rr, n = 16 * ct0 + nt;
             if (n >= a.N || row + 1 >= a.M) continue;
-            const float ds = a.act_scale[n];
+            const float ds = sas[nt];
             const float up = i8s_out(-(tile[rr * TC + nt] >> 6), ds, wscale);
             const float gt = i8s_out(-(tile[(rr + 1) * TC + nt] >> 6), ds, wscale);
             a.y[static_cast<long long>(n) * (a.M / 2) + row / 2] = swiglu_pair(up, gt);
@@ -624,7 +638,7 @@ __global__ __launch_bounds__(kWave *skinny_waves(WC)) void i2_gemm_skinny_kernel
         if (n >= a.N || row >= a.M) continue;
         const int total = -(tile[rr * TC + nt] >> 6);
         const long long o = static_cast<long long>(n) * a.M + row;
-        a.y[o] = gemm_epilogue(pb.epi, i8s_out(total, a.act_scale[n], wscale), n, row, a.M);
+        a.y[o] = gemm_epilogue(pb.epi, i8s_out(total, sas[nt], wscale), n, row, a.M);
         if (a.acc) a.acc[o] = total;
     }
 }
