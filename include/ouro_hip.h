@@ -14,6 +14,8 @@
  *     activations of x);
  *   - ouro_matvec_q on a raw TL1 or TQ1_0 payload of 8192 rows or more
  *     (k == 1): the lookup kernels' per-block partial sums;
+ *   - ouro_matmul_q on a raw TL1 payload for k >= 2 columns: x as int8
+ *     digit planes for the MFMA pass;
  *   - ouro_gdn_chunk_prefill with a NULL workspace.
  * A weight handle (ouro_weight_upload) or ouro_matvec_q_noalloc avoids them.
  *
@@ -425,10 +427,17 @@ typedef struct ouro_weight *ouro_weight_t;
  * I2 codes (out_len*in_len/4 bytes) and w_scale is the per-tensor scale.
  * Both are tiled on upload and held as an OURO_KIND_I2 payload.  For the
  * other kinds host holds the reference payload (row_bytes*out_len bytes)
- * and w_scale is ignored.  max_cols sizes the handle's own activation
- * scratch (for matmul up to max_cols columns); an I2 handle with
+ * and w_scale is ignored.  In_len must be a whole number of the kind's
+ * blocks (OURO_ERR_SHAPE otherwise).  max_cols sizes the handle's own
+ * activation scratch (for matmul up to max_cols columns); an I2 handle with
  * max_cols >= 8 also keeps the codes in the MFMA layout, and its matmuls
- * of 8 or more columns run on the int8 MFMA GEMM (same results). */
+ * of 8 or more columns run on the int8 MFMA GEMM (same results).  A TL1 or
+ * TQ1_0 handle with max_cols >= 2 also keeps its trits in that layout with
+ * the f16 scale of every 128-group (0.266 bytes per weight, built on the
+ * device at upload): its matmuls of 2 or more columns are one int8 MFMA
+ * pass for all of them (matmul_tl1's K-column amortisation, ops.rs:156-286;
+ * within the reference's K-column bar, rel 1e-3), its matvec stays on the
+ * table lookups. */
 int ouro_weight_upload(int kind, const void *host, size_t bytes,
                        size_t out_len, size_t in_len, float w_scale,
                        size_t max_cols, ouro_weight_t *out);
