@@ -140,6 +140,50 @@ __device__ __forceinline__ void wht_pass(float *lds, int n, int tid) {
     }
 }
 
+// The last pass of a plain rotation (no quantisation) straight to the
+// output: the same stages as wht_pass<LOGB, P>, then each value scaled (and,
+// inverse, signed) exactly as the epilogue does and stored at its element
+// index.  For a fixed j the lanes of a wavefront hold consecutive elements,
+// so every store instruction is contiguous; this saves the epilogue's LDS
+// round trip and its barrier.
+template <typename TO, bool INV, int LOGB, int P>
+__device__ __forceinline__ void wht_pass_store(const float *lds, int n, int tid, const FwhtArgs &a, long long row) {
+    constexpr int LO = 4 * P;
+    constexpr int NB = (LOGB - LO) < 4 ? (LOGB - LO) : 4;
+    constexpr int SPAN = 1 << NB;
+    constexpr int STRIDE = (1 << LO) + (1 << (LO - 4));
+    TO *y = static_cast<TO *>(a.y) + row * n;
+    const int sets = n >> NB;
+    for (int s = tid; s < sets; s += kThreads) {
+        const int low = s & ((1 << LO) - 1);
+        const int high = s >> LO;
+        const int base = (high << (LO + NB)) + low;
+        const float *p = lds + pad_idx(base);
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) v[j] = p[j * STRIDE];
+#pragma unroll
+        for (int st_ = 0; st_ < NB; ++st_) {
+            const int h = 1 << st_;
+#pragma unroll
+            for (int j = 0; j < SPAN; ++j) {
+                if ((j & h) == 0) {
+                    const float u = v[j], w = v[j + h];
+                    v[j] = u + w;
+                    v[j + h] = u - w;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < SPAN; ++j) {
+            const int e = base + (j << LO);
+            const float t = (INV && a.signs) ? v[j] * (a.signs[e] * a.scale) : v[j] * a.scale;
+            if constexpr (sizeof(TO) == 2) y[e] = f32_to_bf16_bits(t);
+            else y[e] = t;
+        }
+    }
+}
+
 template <typename TI, typename TO, bool INV, bool QUANT, bool STORE, int LOGB>
 __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
     extern __shared__ float lds[];
@@ -166,18 +210,36 @@ __global__ __launch_bounds__(kThreads) void fwht_row_kernel(FwhtArgs a) {
         for (int i = 0; i < 16; ++i) p[i] = v[i];
     }
 
-    // Passes 1..3: stages 16, 32, ... in the reference's order, 4 per pass.
+    // Passes 1..3: stages 16, 32, ... in the reference's order, 4 per pass;
+    // a plain rotation stores its last pass straight to the output.
+    constexpr int kLast = (LOGB - 1) / 4;  // index of the last pass
+    constexpr bool kDirect = !QUANT && STORE && LOGB > 4;
     if constexpr (LOGB > 4) {
         __syncthreads();
-        wht_pass<LOGB, 1>(lds, n, tid);
+        if constexpr (kDirect && kLast == 1) {
+            wht_pass_store<TO, INV, LOGB, 1>(lds, n, tid, a, row);
+            return;
+        } else {
+            wht_pass<LOGB, 1>(lds, n, tid);
+        }
     }
     if constexpr (LOGB > 8) {
         __syncthreads();
-        wht_pass<LOGB, 2>(lds, n, tid);
+        if constexpr (kDirect && kLast == 2) {
+            wht_pass_store<TO, INV, LOGB, 2>(lds, n, tid, a, row);
+            return;
+        } else {
+            wht_pass<LOGB, 2>(lds, n, tid);
+        }
     }
     if constexpr (LOGB > 12) {
         __syncthreads();
-        wht_pass<LOGB, 3>(lds, n, tid);
+        if constexpr (kDirect && kLast == 3) {
+            wht_pass_store<TO, INV, LOGB, 3>(lds, n, tid, a, row);
+            return;
+        } else {
+            wht_pass<LOGB, 3>(lds, n, tid);
+        }
     }
     __syncthreads();
 
