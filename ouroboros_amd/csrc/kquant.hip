@@ -485,8 +485,15 @@ __device__ __forceinline__ void flush1(const KqArgs &a, const float *red, int nb
 // next tile are issued before the current one is summed (two register sets).
 // Lanes past the last slot (padding to a whole wavefront) run a clamped copy
 // of a real task whose sums are never read, so no load sits behind a branch.
+// Wavefronts per SIMD the register allocation is held to: Q3_K fits 4
+// (136 -> 128 VGPRs, no spill); the other kinds are left as the compiler
+// allocates them (4 waves already; Q8_0 held to 5 ran 10 % slower, the
+// others spill when pressed).
+template <int KIND> constexpr int kWavesPerSimd = KIND == OURO_KIND_Q3K ? 4 : 1;
+
 template <int KIND, int R, bool AL16, bool PH, int MAXT>
-__global__ __launch_bounds__(MAXT) void kq_gemv_kernel(KqArgs a) {
+__global__ __launch_bounds__(MAXT) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd<KIND>)))
+void kq_gemv_kernel(KqArgs a) {
     using F = Fmt<KIND>;
     extern __shared__ float red[];  // slots == 1: [kBatch1][R][wavefronts], else [kBatch][R][blockDim.x]
     const int t = threadIdx.x;
