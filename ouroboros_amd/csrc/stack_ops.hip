@@ -168,10 +168,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
 
 // ---------------------------------------------------- attention (prefill) --
 
-constexpr int kQT = 64;        // query rows per tile
-constexpr int kKT = 64;        // keys per tile
-constexpr int kQP = kHd + 4;   // LDS row pitch (floats) of Q, K, V tiles
-constexpr int kPP = kKT + 4;   // LDS row pitch of P
+constexpr int kQT = 64;  // query rows per tile
+constexpr int kKT = 64;  // keys per tile (one KV page)
 
 struct AttnArgs {
     const float *q, *gate;    // [T][nh][hd]
@@ -188,23 +186,6 @@ struct AttnArgs {
 // alike (96 bytes in the code object's kernel-argument metadata)
 static_assert(sizeof(AttnArgs) == 96, "AttnArgs: kernel argument layout");
 
-// Causal attention over a packed varlen batch on fp32 MFMA
-// (v_mfma_f32_16x16x4f32: fp32 products and sums, the reference's f32
-// arithmetic up to summation order).  One workgroup per (query tile of 64
-// tokens of one sequence, q head); wavefront w owns query rows 16w..16w+15
-// and keeps their Q in registers as A operands.  Per key tile of 64 (one KV
-// page): S = Q K^T as 4 MFMA tiles of 16 keys (k = 128 dims, the dims of
-// k-step s and lane group g being 32g + s), online softmax per row with DPP
-// row reductions, P to the wavefront's LDS rows, then O += P V as 8 MFMA
-// tiles of 16 dims (k = 64 keys, key 16g + s at step s) with V staged
-// transposed.  The sigmoid output gate is applied at the end.
-__device__ __forceinline__ float row16_max(float v) {
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
-    return v;
-}
 __device__ __forceinline__ float row16_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
@@ -213,159 +194,241 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
-constexpr int kVTP = kKT + 4;  // LDS row pitch of V^T (floats)
-// P reuses the K tile's space once every wavefront has its scores: 68 KiB,
-// two workgroups per CU
-constexpr int kAttnLds = (kKT * kQP + kHd * kVTP) * 4;
-static_assert(kQT * kPP <= kKT * kQP, "P fits in the K tile");
+// Causal attention over a packed varlen batch on bf16 MFMA with every fp32
+// operand split as x = hi + lo (hi = bf16(x), lo = bf16(x - hi)) and each
+// product taken as hi*hi + hi*lo + lo*hi (v_mfma_f32_16x16x32_bf16, fp32
+// sums): products to about 2^-16 of their size, well inside the 1e-3
+// relative bar on the attention output, at about five times the fp32 MFMA
+// rate.  One workgroup per (query tile of 64 tokens of one sequence, q
+// head); wavefront w owns query rows 16w..16w+15 as the 16 columns of its
+// products, with their Q (hi, lo) in registers as B operands.  Per key tile
+// of 64 (one KV page), staged in LDS as split operand fragments:
+// S^T = K Q^T (4 tiles of 16 keys, k = 128 dims), the online softmax per
+// query (a lane holds one query: in-lane maxima and sums, then the three
+// other lanes of that query), then O^T += V^T P^T with P^T taken straight
+// from the score registers as the B operand (keys 32q + 4g + 0..3 and
+// 32q + 16 + 4g + 0..3 of lane group g, the order the V^T fragments are
+// staged in), so P never goes through LDS.  The sigmoid output gate is
+// applied at the end, and a lane stores four consecutive dims of its query.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ f32x4_t mfma_f32(float a, float b, const f32x4_t &c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4_t mfma_bf16(const bf16x8_t &a, const bf16x8_t &b, const f32x4_t &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// (a, b) = hi + lo as bf16 pairs (round to nearest even; x - hi is exact)
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    hi = h;
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+                                          f32x2_t{a - __uint_as_float(h << 16), b - __uint_as_float(h & 0xffff0000u)},
+                                          bf16x2_t));
+}
+// eight values (x0[0..3], x1[0..3]) as hi and lo operands
+__device__ __forceinline__ void split_op(const f32x4_t &x0, const f32x4_t &x1, bf16x8_t &hi, bf16x8_t &lo) {
+    uint4 h, l;
+    split_pair(x0[0], x0[1], h.x, l.x);
+    split_pair(x0[2], x0[3], h.y, l.y);
+    split_pair(x1[0], x1[1], h.z, l.z);
+    split_pair(x1[2], x1[3], h.w, l.w);
+    hi = __builtin_bit_cast(bf16x8_t, h);
+    lo = __builtin_bit_cast(bf16x8_t, l);
 }
 
+// LDS operand fragments: a block is one 16 x 32 bf16 operand (64 lanes x
+// 16 B), lane r + 16 g at 272 g + 16 r, so a wavefront's 16-byte operand
+// read is 16 contiguous lanes per group (conflict-free) and the 16 B of
+// padding per group spread the staging writes over the banks.
+constexpr int kFragGrp = 272;
+constexpr int kFragBlk = 4 * kFragGrp;
+__device__ __forceinline__ int frag_off(int blk, int lane) { return blk * kFragBlk + (lane >> 4) * kFragGrp + (lane & 15) * 16; }
+// K tile: block (4 t + j) * 2 + hl holds keys 16 t + r, dims 32 j + 8 g + 0..7
+// at lane r + 16 g (hl: 0 hi, 1 lo).  V^T tile: block kVtBlk + (2 t + q) * 2 +
+// hl holds dims 16 t + r over keys 32 q + 4 g + 0..3 and 32 q + 16 + 4 g + 0..3.
+constexpr int kVtBlk = 32;
+constexpr int kAttnLds = 64 * kFragBlk;  // 68 KiB: two workgroups per CU
+
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs a) {
-    extern __shared__ float lds[];
-    float *Ks = lds, *Vt = Ks + kKT * kQP;
+    extern __shared__ __attribute__((aligned(16))) unsigned char alds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int s = a.tile_seq[blockIdx.x], p0 = a.tile_p0[blockIdx.x];
     const int h = blockIdx.y;
     const int kvh = h / (a.nh / a.nkv);
     const int t0 = a.cu[s], L = a.cu[s + 1] - t0;
-    float *Pw = Ks + 16 * wave * kPP;  // this wavefront's 16 rows of P (over the K tile)
+    const int qp = p0 + 16 * wave + lr;  // this lane's query position
 
-    // Q row 16w + lr, dims 32g .. 32g + 31 as the A operand of k-steps 0..31
-    float qa[32];
+    // Q row qp, dims 32 j + 8 g .. +7: the B operand of k-step j
+    bf16x8_t qh[4], ql[4];
     {
-        const int qp = min(p0 + 16 * wave + lr, L - 1);  // rows past the end: any valid row, never stored
-        const float *qr = a.q + ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + 32 * lg;
+        const float *qr = a.q + ((static_cast<long long>(t0) + min(qp, L - 1)) * a.nh + h) * kHd + 8 * lg;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 v = *reinterpret_cast<const float4 *>(qr + 4 * i);
-            qa[4 * i] = v.x, qa[4 * i + 1] = v.y, qa[4 * i + 2] = v.z, qa[4 * i + 3] = v.w;
-        }
+        for (int j = 0; j < 4; ++j)  // rows past the end: any valid row, never stored
+            split_op(*reinterpret_cast<const f32x4_t *>(qr + 32 * j), *reinterpret_cast<const f32x4_t *>(qr + 32 * j + 4),
+                     qh[j], ql[j]);
     }
-    f32x4_t o[8];
+    f32x4_t o[8];  // o[t][e] = O[qp][16 t + 4 g + e] (unnormalised)
 #pragma unroll
     for (int t = 0; t < 8; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        m[e] = -INFINITY;
-        l[e] = 0.f;
-    }
-    const int last = min(p0 + kQT, L) - 1;  // last query position in the tile
-    // K and V of the next key tile are loaded into registers while the
-    // current one is used (a key tile is one KV page; rows past L read the
-    // page's unused rows and are zeroed)
-    constexpr int kPer = kKT * (kHd / 4) / 256;  // float4 of K (and of V) per thread
-    float4 kpre[kPer], vpre[kPer];
+    float m = -INFINITY, l = 0.f;
+    const float sl2 = a.scale * 1.4426950408889634f;  // scale * log2(e)
+    const int last = min(p0 + kQT, L) - 1;  // last query position of the tile
+    // Staging units u = tid + 256 i: keys 2 p, 2 p + 1 (p = u / 32), dims
+    // 4 c .. 4 c + 3 (c = u % 32); the next tile's K and V are loaded into
+    // registers while the current one is used (rows past L read the page's
+    // unused rows and are zeroed)
+    f32x4_t kpre[4][2], vpre[4][2];
     auto load_kv = [&](int k0) {
         const long long row0 = kv_row(a.pages, a.maxp, s, k0);
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int i = tid + 256 * j, r = i / (kHd / 4), c4 = i % (kHd / 4);
-            const long long off = ((row0 + r) * a.nkv + kvh) * kHd + 4 * c4;
-            kpre[j] = *reinterpret_cast<const float4 *>(a.kc + off);
-            vpre[j] = *reinterpret_cast<const float4 *>(a.vc + off);
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + 256 * i, pr = u >> 5, c4 = u & 31;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const long long off = ((row0 + 2 * pr + w) * a.nkv + kvh) * kHd + 4 * c4;
+                kpre[i][w] = *reinterpret_cast<const f32x4_t *>(a.kc + off);
+                vpre[i][w] = *reinterpret_cast<const f32x4_t *>(a.vc + off);
+            }
         }
     };
     load_kv(0);
     for (int k0 = 0; k0 <= last; k0 += kKT) {
-        __syncthreads();  // the previous tile's K and V are consumed
+        __syncthreads();  // the previous tile's fragments are consumed
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const int i = tid + 256 * j, r = i / (kHd / 4), c4 = i % (kHd / 4);
-            const bool live = k0 + r < L;
-            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 kv = live ? kpre[j] : z, vv = live ? vpre[j] : z;
-            *reinterpret_cast<float4 *>(Ks + r * kQP + 4 * c4) = kv;
-            Vt[(4 * c4) * kVTP + r] = vv.x;
-            Vt[(4 * c4 + 1) * kVTP + r] = vv.y;
-            Vt[(4 * c4 + 2) * kVTP + r] = vv.z;
-            Vt[(4 * c4 + 3) * kVTP + r] = vv.w;
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + 256 * i, pr = u >> 5, c4 = u & 31;
+            const f32x4_t z = {0.f, 0.f, 0.f, 0.f};
+            f32x4_t kv[2], vv[2];
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const bool live = k0 + 2 * pr + w < L;
+                kv[w] = live ? kpre[i][w] : z;
+                vv[w] = live ? vpre[i][w] : z;
+            }
+            // K: key kk = 2 pr + w, dims 4 c4 .. +3 -> 8 bytes of lane r + 16 g of block (4 t + j) * 2 + hl
+            const int j = c4 >> 3, g = (c4 >> 1) & 3, half = c4 & 1;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int kk = 2 * pr + w, t = kk >> 4, r = kk & 15;
+                uint2 hi, lo;
+                split_pair(kv[w][0], kv[w][1], hi.x, lo.x);
+                split_pair(kv[w][2], kv[w][3], hi.y, lo.y);
+                const int blk = (4 * t + j) * 2;
+                *reinterpret_cast<uint2 *>(alds + frag_off(blk, r + 16 * g) + 8 * half) = hi;
+                *reinterpret_cast<uint2 *>(alds + frag_off(blk + 1, r + 16 * g) + 8 * half) = lo;
+            }
+            // V^T: dim d = 4 c4 + e, keys kk, kk + 1 (kk = 2 pr even) -> one bf16 pair at
+            // position (kk & 3) + 4 ((kk & 31) >> 4) of lane (d & 15) + 16 ((kk & 15) >> 2)
+            const int kk = 2 * pr, q = kk >> 5, pos = (kk & 3) + 4 * ((kk & 31) >> 4), gv = (kk & 15) >> 2;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int d = 4 * c4 + e, t = d >> 4;
+                uint32_t hi, lo;
+                split_pair(vv[0][e], vv[1][e], hi, lo);
+                const int blk = kVtBlk + (2 * t + q) * 2;
+                *reinterpret_cast<uint32_t *>(alds + frag_off(blk, (d & 15) + 16 * gv) + 2 * pos) = hi;
+                *reinterpret_cast<uint32_t *>(alds + frag_off(blk + 1, (d & 15) + 16 * gv) + 2 * pos) = lo;
+            }
         }
         __syncthreads();
         if (k0 + kKT <= last) load_kv(k0 + kKT);
-        // S: tile t holds S[16w + 4g + e][k0 + 16t + lr]
+        // S^T: sc[t][e] = S[qp][k0 + 16 t + 4 g + e]
         f32x4_t sc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            const float *kr = Ks + (16 * t + lr) * kQP + 32 * lg;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 kv = *reinterpret_cast<const float4 *>(kr + 4 * i);
-                sc[t] = mfma_f32(qa[4 * i], kv.x, sc[t]);
-                sc[t] = mfma_f32(qa[4 * i + 1], kv.y, sc[t]);
-                sc[t] = mfma_f32(qa[4 * i + 2], kv.z, sc[t]);
-                sc[t] = mfma_f32(qa[4 * i + 3], kv.w, sc[t]);
+            for (int j = 0; j < 4; ++j) {
+                const int blk = (4 * t + j) * 2;
+                const bf16x8_t kh = *reinterpret_cast<const bf16x8_t *>(alds + frag_off(blk, lane));
+                const bf16x8_t kl = *reinterpret_cast<const bf16x8_t *>(alds + frag_off(blk + 1, lane));
+                sc[t] = mfma_bf16(kh, qh[j], sc[t]);
+                sc[t] = mfma_bf16(kh, ql[j], sc[t]);
+                sc[t] = mfma_bf16(kl, qh[j], sc[t]);
             }
         }
-        __syncthreads();  // every wavefront's scores are done: P may overwrite the K tile
-        float corr[4];
+        // online softmax of query qp (its keys are spread over lanes lr + 16 g),
+        // in base 2: scores scaled by scale * log2(e), p = 2^(s - m)
+        float mx = -INFINITY;
+        if (k0 + kKT - 1 <= p0 + 16 * wave && k0 + kKT <= L) {  // every key visible to every row of the wave
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int qp = p0 + 16 * wave + 4 * lg + e;
-            float mx = -INFINITY;
+            for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int kp = k0 + 16 * t + lr;
-                sc[t][e] = (kp <= qp && kp < L) ? sc[t][e] * a.scale : -INFINITY;
-                mx = fmaxf(mx, sc[t][e]);
-            }
-            mx = row16_max(mx);
-            const float mn = fmaxf(m[e], mx);
-            // rows with no visible key yet keep m = -inf; use 0 to avoid inf - inf
-            const float mref = mn == -INFINITY ? 0.f : mn;
-            corr[e] = expf(m[e] - mref);
-            float ps = 0.f;
+                for (int e = 0; e < 4; ++e) {
+                    sc[t][e] *= sl2;
+                    mx = fmaxf(mx, sc[t][e]);
+                }
+        } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const float pv = expf(sc[t][e] - mref);
-                Pw[(4 * lg + e) * kPP + 16 * t + lr] = pv;
-                ps += pv;
-            }
-            l[e] = l[e] * corr[e] + row16_sum(ps);
-            m[e] = mn;
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int kp = k0 + 16 * t + 4 * lg + e;
+                    sc[t][e] = (kp <= qp && kp < L) ? sc[t][e] * sl2 : -INFINITY;
+                    mx = fmaxf(mx, sc[t][e]);
+                }
         }
+        {
+            const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(x32[0]), __uint_as_float(x32[1]));
+            const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(x16[0]), __uint_as_float(x16[1]));
+        }
+        const float mn = fmaxf(m, mx);
+        // a query with no visible key yet keeps m = -inf; use 0 to avoid inf - inf
+        const float mref = mn == -INFINITY ? 0.f : mn;
+        const float corr = __builtin_amdgcn_exp2f(m - mref);
+        float ps = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sc[t][e] = __builtin_amdgcn_exp2f(sc[t][e] - mref);
+                ps += sc[t][e];
+            }
+        {
+            const auto x32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+            ps = __uint_as_float(x32[0]) + __uint_as_float(x32[1]);
+            const auto x16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+            ps = __uint_as_float(x16[0]) + __uint_as_float(x16[1]);
+        }
+        l = l * corr + ps;
+        m = mn;
+        if (!__all(corr == 1.0f)) {  // the running maxima moved
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[t][e] *= corr;
+        }
+        // P^T as B operands: slab q = score tiles 2 q, 2 q + 1
+        bf16x8_t ph[2], pl[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) split_op(sc[2 * q], sc[2 * q + 1], ph[q], pl[q]);
+        // O^T += V^T P^T
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[t][e] *= corr[e];
-        __builtin_amdgcn_wave_barrier();  // P rows written by this wavefront only
-        // O += P V: A = P[16w + lr][16g + s], B = V[16g + s][16t + lr]
-        float pa[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = *reinterpret_cast<const float4 *>(Pw + lr * kPP + 16 * lg + 4 * i);
-            pa[4 * i] = v.x, pa[4 * i + 1] = v.y, pa[4 * i + 2] = v.z, pa[4 * i + 3] = v.w;
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float *vr = Vt + (16 * t + lr) * kVTP + 16 * lg;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 vv = *reinterpret_cast<const float4 *>(vr + 4 * i);
-                o[t] = mfma_f32(pa[4 * i], vv.x, o[t]);
-                o[t] = mfma_f32(pa[4 * i + 1], vv.y, o[t]);
-                o[t] = mfma_f32(pa[4 * i + 2], vv.z, o[t]);
-                o[t] = mfma_f32(pa[4 * i + 3], vv.w, o[t]);
+            for (int q = 0; q < 2; ++q) {
+                const int blk = kVtBlk + (2 * t + q) * 2;
+                const bf16x8_t vh = *reinterpret_cast<const bf16x8_t *>(alds + frag_off(blk, lane));
+                const bf16x8_t vl = *reinterpret_cast<const bf16x8_t *>(alds + frag_off(blk + 1, lane));
+                o[t] = mfma_bf16(vh, ph[q], o[t]);
+                o[t] = mfma_bf16(vh, pl[q], o[t]);
+                o[t] = mfma_bf16(vl, ph[q], o[t]);
             }
-        }
-        __builtin_amdgcn_wave_barrier();  // P reads done before the next tile's writes
     }
-    // o / l, times sigmoid(gate) (qwen35.rs:1208-1210); lane holds rows 4g + e, dims 16t + lr
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int qp = p0 + 16 * wave + 4 * lg + e;
-        if (qp >= L) continue;
-        const long long base = ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + lr;
-        const float il = 1.0f / l[e];
+    // o / l, times sigmoid(gate) (qwen35.rs:1208-1210): dims 16 t + 4 g .. +3 of query qp
+    if (qp < L) {
+        const long long base = ((static_cast<long long>(t0) + qp) * a.nh + h) * kHd + 4 * lg;
+        const float il = 1.0f / l;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const float g = a.gate[base + 16 * t];
-            a.out[base + 16 * t] = (o[t][e] * il) * (1.0f / (1.0f + expf(-g)));
+            const f32x4_t g = *reinterpret_cast<const f32x4_t *>(a.gate + base + 16 * t);
+            f32x4_t r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = (o[t][e] * il) * (1.0f / (1.0f + expf(-g[e])));
+            *reinterpret_cast<f32x4_t *>(a.out + base + 16 * t) = r;
         }
     }
 }
