@@ -450,7 +450,7 @@ constexpr int kDecKeys = 256;
 constexpr int kPartStride = kHd + 4;  // floats per (b, head, split) record: o[128], m, l
 
 template <int G>
-__global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, float *part, int nsplit) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G <= 4 ? 5 : 1))) void attn_decode_split_kernel(AttnArgs a, float *part, int nsplit) {
     __shared__ float sc[G][kDecKeys];
     __shared__ float red[4][G][kHd];
     __shared__ float ml[G][2];
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(AttnArgs a, floa
     // kB key rows' loads are issued together before their dot products: the
     // conditional score store splits an iteration into several basic blocks,
     // so the compiler would not hoist the next key's loads across it
-    constexpr int kB = 8;
+    constexpr int kB = 4;
     static_assert((kWK / 4) % kB == 0, "whole load batches");
     for (int it0 = 0; it0 < (wkeys > 0 ? kWK / 4 : 0); it0 += kB) {
         float4 k0[kB], k1[kB];
