@@ -613,19 +613,24 @@ __device__ __forceinline__ uint16_t to_bf16(float x) { return f32_to_bf16_bits(x
 // conv_step + SiLU per (token, channel) with the causal window inside the
 // token's sequence (inputs before the sequence come from its ring), then
 // beta and gate per (token, v-head) (qwen35.rs:1066-1088).
-// Grid: x = channel blocks of 256, y = contiguous token ranges.  A thread
-// walks its channel along its range with the last three inputs in registers
-// (each input read once), taking them from the sequence's ring at a
-// sequence start.  The gates of token t are written by channel block 0.
+// Grid: x = blocks of 1024 channels (a thread takes 4 adjacent channels:
+// 16-byte loads, 8-byte bf16 stores), y = contiguous token ranges.  A
+// thread walks its channels along its range with the last three inputs in
+// registers (each input read once), taking them from the sequence's ring
+// at a sequence start.  The gates of token t are written by the last column
+// of workgroups.
+__device__ __forceinline__ float silu_f(float y) { return y / (1.0f + expf(-y)); }
+
 __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int per) {
-    // tokens go in batches of kB: a batch's loads are issued together (the
-    // token loop is otherwise one dependent HBM round trip per token)
+    // tokens go in batches of kB: a batch's loads (inputs and positions) are
+    // issued together (the token loop is otherwise one dependent HBM round
+    // trip per token)
     constexpr int kB = 16;
-    const int c = static_cast<int>(blockIdx.x) * 256 + threadIdx.x;
     const int ta = static_cast<int>(blockIdx.y) * per, tb = min(ta + per, a.T);
+    const int nc4 = a.ch / 4;  // channel quads (the host checks ch % 4 == 0)
     // the last column of workgroups computes the gates (next to the conv
     // workgroups rather than in one of them, which made it the longest)
-    if (static_cast<int>(blockIdx.x) == (a.ch + 255) / 256) {
+    if (static_cast<int>(blockIdx.x) == (nc4 + 255) / 256) {
         if (threadIdx.x >= a.Hv) return;
         const int hv = threadIdx.x;
         const float dtb = a.dt_bias[hv], al = a.a_log[hv];
@@ -648,44 +653,69 @@ __global__ __launch_bounds__(256) void prefill_conv_gate_kernel(ConvArgs a, int 
         }
         return;
     }
-    if (c >= a.ch || ta >= tb) return;
-    const float4 w = *reinterpret_cast<const float4 *>(a.conv_w + 4LL * c);
+    const int c4 = static_cast<int>(blockIdx.x) * 256 + static_cast<int>(threadIdx.x);
+    if (c4 >= nc4 || ta >= tb) return;
+    const int c = 4 * c4;
+    f32x4_t w[4];  // conv weights of channels c .. c + 3
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = *reinterpret_cast<const f32x4_t *>(a.conv_w + 4LL * (c + e));
     const int di = a.di, dv = a.ch - 2 * a.di;
+    // the quad lies in one of q, k, v (di % 4 == 0): its output row and column
+    uint16_t *dst;
+    int dstride, dc;
+    if (c < di) dst = a.qb, dstride = di, dc = c;
+    else if (c < 2 * di) dst = a.kb, dstride = di, dc = c - di;
+    else dst = a.vb, dstride = dv, dc = c - 2 * di;
     // window x[t-3], x[t-2], x[t-1] for the range's first token
-    float x0, x1, x2;
+    f32x4_t x0, x1, x2;
+    auto ring_window = [&](int t) {
+        const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;  // [channel][3]
+        const f32x4_t r0 = *reinterpret_cast<const f32x4_t *>(r), r1 = *reinterpret_cast<const f32x4_t *>(r + 4),
+                      r2 = *reinterpret_cast<const f32x4_t *>(r + 8);  // 12 floats, channel-major
+        const float rr[12] = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3], r2[0], r2[1], r2[2], r2[3]};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x0[e] = rr[3 * e], x1[e] = rr[3 * e + 1], x2[e] = rr[3 * e + 2];
+    };
     {
+        // x[ta-3] = ring[p] (p < 3), x[ta-2] = ring[1 + p] (p < 2), x[ta-1] = ring[2] (p < 1)
         const int p = a.pos[ta];
-        const float *r = a.ring + (static_cast<long long>(a.seq[ta]) * a.ch + c) * 3;
-        x0 = p >= 3 ? a.qkv[(static_cast<long long>(ta) - 3) * a.ch + c] : r[p];
-        x1 = p >= 2 ? a.qkv[(static_cast<long long>(ta) - 2) * a.ch + c] : r[1 + p];
-        x2 = p >= 1 ? a.qkv[(static_cast<long long>(ta) - 1) * a.ch + c] : r[2];
+        ring_window(ta);  // x0, x1, x2 = ring[0], ring[1], ring[2]
+        const f32x4_t r1 = x1, r2 = x2;
+        if (p == 1) x0 = r1, x1 = r2;
+        if (p == 2) x0 = r2;
+        const float *q = a.qkv + static_cast<long long>(ta) * a.ch + c;
+        if (p >= 3) x0 = *reinterpret_cast<const f32x4_t *>(q - 3LL * a.ch);
+        if (p >= 2) x1 = *reinterpret_cast<const f32x4_t *>(q - 2LL * a.ch);
+        if (p >= 1) x2 = *reinterpret_cast<const f32x4_t *>(q - a.ch);
     }
     for (int t0 = ta; t0 < tb; t0 += kB) {
-        float xb[kB];
+        f32x4_t xb[kB];
+        int pb[kB];
 #pragma unroll
-        for (int u = 0; u < kB; ++u) xb[u] = a.qkv[static_cast<long long>(min(t0 + u, tb - 1)) * a.ch + c];
+        for (int u = 0; u < kB; ++u) {
+            const int t = min(t0 + u, tb - 1);
+            xb[u] = *reinterpret_cast<const f32x4_t *>(a.qkv + static_cast<long long>(t) * a.ch + c);
+            pb[u] = a.pos[t];
+        }
 #pragma unroll
         for (int u = 0; u < kB; ++u) {
             const int t = t0 + u;
-            if (t >= tb) break;
-            if (t > ta && a.pos[t] == 0) {  // a sequence starts: its ring is the window
-                const float *r = a.ring + (static_cast<long long>(a.seq[t]) * a.ch + c) * 3;
-                x0 = r[0];
-                x1 = r[1];
-                x2 = r[2];
+            if (t < tb) {
+                if (t > ta && pb[u] == 0) ring_window(t);  // a sequence starts: its ring is the window
+                const f32x4_t x = xb[u];
+                uint32_t o[2];
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const float y0 = w[e][0] * x0[e] + w[e][1] * x1[e] + w[e][2] * x2[e] + w[e][3] * x[e];
+                    const float y1 = w[e + 1][0] * x0[e + 1] + w[e + 1][1] * x1[e + 1] + w[e + 1][2] * x2[e + 1] +
+                                     w[e + 1][3] * x[e + 1];
+                    o[e / 2] = static_cast<uint32_t>(to_bf16(silu_f(y0))) | (static_cast<uint32_t>(to_bf16(silu_f(y1))) << 16);
+                }
+                x0 = x1;
+                x1 = x2;
+                x2 = x;
+                *reinterpret_cast<uint2 *>(dst + static_cast<long long>(t) * dstride + dc) = make_uint2(o[0], o[1]);
             }
-            const float x = xb[u];
-            const float y = w.x * x0 + w.y * x1 + w.z * x2 + w.w * x;
-            x0 = x1;
-            x1 = x2;
-            x2 = x;
-            const uint16_t sy = to_bf16(y / (1.0f + expf(-y)));
-            if (c < di)
-                a.qb[static_cast<long long>(t) * di + c] = sy;
-            else if (c < 2 * di)
-                a.kb[static_cast<long long>(t) * di + c - di] = sy;
-            else
-                a.vb[static_cast<long long>(t) * dv + c - 2 * di] = sy;
         }
     }
 }
@@ -878,7 +908,8 @@ int prefill_conv_gate(const float *qkv, const float *ring, const float *conv_w, 
                static_cast<int>(T), ch, di, Hv};
     if (!T) return OURO_OK;
     if (Hv > 256) return fail(OURO_ERR_SHAPE, "prefill_conv_gate: %d v-heads (<= 256)", Hv);
-    const int cb = (ch + 255) / 256;
+    if (ch % 4 || di % 4) return fail(OURO_ERR_SHAPE, "prefill_conv_gate: %d channels, %d per q/k (multiples of 4)", ch, di);
+    const int cb = (ch / 4 + 255) / 256;
     // token ranges: enough workgroups to fill the chip, each range long
     // enough that the window is refilled from memory rarely
     const int ranges = static_cast<int>(T < 256 ? T : 256);
