@@ -113,56 +113,71 @@ struct AttnPrepArgs {
 // alike (128 bytes in the code object's kernel-argument metadata)
 static_assert(sizeof(AttnPrepArgs) == 128, "AttnPrepArgs: kernel argument layout");
 
-// One wavefront per (token, head of q or k); lane l holds dims 2l, 2l+1.
+// Workgroup (token, y) of gridDim.y per token; wavefront w takes heads
+// 4 y + w, then every 4 gridDim.y-th (q heads, then k heads); lane l holds
+// dims 2l, 2l+1.  The rope's angles depend on the position and the dim
+// only, so each wavefront computes its lanes' cos / sin once and uses them
+// for all its heads (a long prefill: one workgroup per token; a decode
+// step: one head per wavefront, for parallelism).
 __global__ __launch_bounds__(256) void attn_prep_kernel(AttnPrepArgs a) {
-    const int lane = threadIdx.x & 63;
-    const long long item = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = static_cast<int>(blockIdx.x);
+    if (t >= a.T) return;  // whole workgroup
     const int heads = a.nh + a.nkv;
-    if (item >= static_cast<long long>(a.T) * heads) return;  // whole wavefront
-    const int t = static_cast<int>(item / heads), hh = static_cast<int>(item % heads);
-    const bool isq = hh < a.nh;
-    const int h = isq ? hh : hh - a.nh;
-    const float *src = isq ? a.qfull + (static_cast<long long>(t) * a.nh + h) * (2 * kHd)
-                           : a.k + (static_cast<long long>(t) * a.nkv + h) * kHd;
-    float2 x = *reinterpret_cast<const float2 *>(src + 2 * lane);
-    // rmsnorm_head (qwen35.rs:1246-1248)
-    float ss = x.x * x.x + x.y * x.y;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + a.eps);
-    const float2 g = *reinterpret_cast<const float2 *>((isq ? a.qn : a.kn) + 2 * lane);
-    x.x = x.x * inv * g.x;
-    x.y = x.y * inv * g.y;
     // rope_partial_neox on the first n_rot dims: pair (i, i + n_rot/2)
     const int half = a.n_rot / 2;
     const int p = a.pos[t];
     const int partner = lane < half / 2 ? lane + half / 2 : lane - half / 2;
-    const float px = __shfl(x.x, partner, 64), py = __shfl(x.y, partner, 64);
-    if (2 * lane < a.n_rot) {
-        float r[2] = {x.x, x.y};
-        const float pr[2] = {px, py};
+    const bool rot = 2 * lane < a.n_rot;
+    float cs[2] = {1.f, 1.f}, sn[2] = {0.f, 0.f};
+    if (rot) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int d = 2 * lane + e;
             const int i = d < half ? d : d - half;
             const float theta = 1.0f / powf(a.rope_base, static_cast<float>(2 * i) / static_cast<float>(a.n_rot));
             const float ang = static_cast<float>(p) * theta;
-            const float c = cosf(ang), s = sinf(ang);
-            r[e] = d < half ? r[e] * c - pr[e] * s : r[e] * c + pr[e] * s;
+            cs[e] = cosf(ang);
+            sn[e] = sinf(ang);
         }
-        x.x = r[0];
-        x.y = r[1];
     }
-    if (isq) {
-        const long long o = (static_cast<long long>(t) * a.nh + h) * kHd + 2 * lane;
-        *reinterpret_cast<float2 *>(a.q_out + o) = x;
-        *reinterpret_cast<float2 *>(a.gate_out + o) = *reinterpret_cast<const float2 *>(src + kHd + 2 * lane);
-    } else {
-        const long long row = kv_row(a.pages, a.maxp, a.seq[t], p);
-        const long long o = (row * a.nkv + h) * kHd + 2 * lane;
-        *reinterpret_cast<float2 *>(a.kc + o) = x;
-        *reinterpret_cast<float2 *>(a.vc + o) =
-            *reinterpret_cast<const float2 *>(a.v + (static_cast<long long>(t) * a.nkv + h) * kHd + 2 * lane);
+    const long long krow = kv_row(a.pages, a.maxp, a.seq[t], p);  // the token's cache row
+    for (int hh = 4 * static_cast<int>(blockIdx.y) + wave; hh < heads; hh += 4 * static_cast<int>(gridDim.y)) {
+        const bool isq = hh < a.nh;
+        const int h = isq ? hh : hh - a.nh;
+        const float *src = isq ? a.qfull + (static_cast<long long>(t) * a.nh + h) * (2 * kHd)
+                               : a.k + (static_cast<long long>(t) * a.nkv + h) * kHd;
+        float2 x = *reinterpret_cast<const float2 *>(src + 2 * lane);
+        // rmsnorm_head (qwen35.rs:1246-1248)
+        float ss = x.x * x.x + x.y * x.y;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += xor_shfl(ss, off);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(kHd) + a.eps);
+        const float2 g = *reinterpret_cast<const float2 *>((isq ? a.qn : a.kn) + 2 * lane);
+        x.x = x.x * inv * g.x;
+        x.y = x.y * inv * g.y;
+        const float px = __shfl(x.x, partner, 64), py = __shfl(x.y, partner, 64);
+        if (rot) {
+            float r[2] = {x.x, x.y};
+            const float pr[2] = {px, py};
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int d = 2 * lane + e;
+                r[e] = d < half ? r[e] * cs[e] - pr[e] * sn[e] : r[e] * cs[e] + pr[e] * sn[e];
+            }
+            x.x = r[0];
+            x.y = r[1];
+        }
+        if (isq) {
+            const long long o = (static_cast<long long>(t) * a.nh + h) * kHd + 2 * lane;
+            *reinterpret_cast<float2 *>(a.q_out + o) = x;
+            *reinterpret_cast<float2 *>(a.gate_out + o) = *reinterpret_cast<const float2 *>(src + kHd + 2 * lane);
+        } else {
+            const long long o = (krow * a.nkv + h) * kHd + 2 * lane;
+            *reinterpret_cast<float2 *>(a.kc + o) = x;
+            *reinterpret_cast<float2 *>(a.vc + o) =
+                *reinterpret_cast<const float2 *>(a.v + (static_cast<long long>(t) * a.nkv + h) * kHd + 2 * lane);
+        }
     }
 }
 
@@ -839,10 +854,11 @@ int attn_prep(const float *qfull, const float *k, const float *v, const float *q
               float *kc, float *vc, size_t T, int nh, int nkv, int n_rot, float rope_base, float eps,
               void *stream) {
     if (n_rot < 0 || n_rot > kHd || n_rot % 4) return fail(OURO_ERR_SHAPE, "attn_prep: n_rot %d", n_rot);
+    if (!T) return OURO_OK;
     AttnPrepArgs a{qfull, k, v, qn, kn, pos, seq, pages, q_out, gate_out, kc, vc,
                    static_cast<int>(T), nh, nkv, n_rot, maxp, rope_base, eps};
-    const long long items = static_cast<long long>(T) * (nh + nkv);
-    hipLaunchKernelGGL(attn_prep_kernel, dim3(blocks_for(items, 4)), dim3(256), 0, as_stream(stream), a);
+    const unsigned gy = T >= 4096 ? 1u : static_cast<unsigned>((nh + nkv + 3) / 4);
+    hipLaunchKernelGGL(attn_prep_kernel, dim3(static_cast<unsigned>(T), gy), dim3(256), 0, as_stream(stream), a);
     return check_launch("attn_prep_kernel");
 }
 
