@@ -162,6 +162,16 @@ __device__ __forceinline__ u32x4 vmap(const u32x4 &a, uint32_t mask, uint32_t sh
     return u32x4{(a.x >> sh) & mask, (a.y >> sh) & mask, (a.z >> sh) & mask, (a.w >> sh) & mask};
 }
 
+// (c & cm) | (rotr(h, r) & hm) per dword: a code field merged with high bits
+// rotated into place (one v_alignbit, an and and an and-or a dword; the
+// rotation wraps only bits that hm drops)
+__device__ __forceinline__ u32x4 merge_hi(const u32x4 &c, uint32_t cm, const u32x4 &h, uint32_t r, uint32_t hm) {
+    const auto one = [&](uint32_t cv, uint32_t hv) {
+        return (cv & cm) | (__builtin_amdgcn_alignbit(hv, hv, r & 31) & hm);
+    };
+    return u32x4{one(c.x, h.x), one(c.y, h.y), one(c.z, h.z), one(c.w, h.w)};
+}
+
 // ---- per kind: block geometry, a task's x runs, its raw loads, its sum ----
 
 template <int KIND> struct Fmt;
@@ -244,8 +254,9 @@ template <> struct Fmt<OURO_KIND_Q5K> {
         scale_min_k4(2 * j, r.h.y, r.h.z, r.h.w, s1, m1);
         scale_min_k4(2 * j + 1, r.h.y, r.h.z, r.h.w, s2, m2);
         const float d = f16f(r.h.x & 0xffffu), dmin = f16f(r.h.x >> 16);
-        const u32x4 lo = vmap(r.q, 0x0f0f0f0fu, 0) | (vmap(r.qh, 0x01010101u, 2 * j) << 4);
-        const u32x4 hi = vmap(r.q, 0x0f0f0f0fu, 4) | (vmap(r.qh, 0x01010101u, 2 * j + 1) << 4);
+        // bit 2j / 2j + 1 of qh to bit 4 of each byte
+        const u32x4 lo = merge_hi(r.q, 0x0f0f0f0fu, r.qh, 2 * j - 4, 0x10101010u);
+        const u32x4 hi = merge_hi(vmap(r.q, 0xffffffffu, 4), 0x0f0f0f0fu, r.qh, 2 * j - 3, 0x10101010u);
         const float SA = idot(lo, xa);
         const float SB = idot(hi, xb);
         return (d * static_cast<float>(s1)) * SA - (dmin * static_cast<float>(m1)) * xa.X +
@@ -282,8 +293,9 @@ template <> struct Fmt<OURO_KIND_Q6K> {
 #pragma clang fp contract(off)
         const int s = u & 1;
         const float d = f16f(r.d0 | (r.d1 << 8));
-        const u32x4 lo = vmap(r.ql, 0x0f0f0f0fu, 0) | (vmap(r.qh, 0x03030303u, 2 * s) << 4);
-        const u32x4 hi = vmap(r.ql, 0x0f0f0f0fu, 4) | (vmap(r.qh, 0x03030303u, 4 + 2 * s) << 4);
+        // bits 2s, 2s + 1 / 4 + 2s, 5 + 2s of qh to bits 4, 5 of each byte
+        const u32x4 lo = merge_hi(r.ql, 0x0f0f0f0fu, r.qh, 2 * s - 4, 0x30303030u);
+        const u32x4 hi = merge_hi(vmap(r.ql, 0xffffffffu, 4), 0x0f0f0f0fu, r.qh, 2 * s, 0x30303030u);
         const float SA = idot(lo, xa) - 32.f * xa.X;
         const float SB = idot(hi, xb) - 32.f * xb.X;
         const float ca = d * static_cast<float>(static_cast<int8_t>(r.sa));
@@ -329,10 +341,14 @@ template <> struct Fmt<OURO_KIND_Q3K> {
         const float d = f16f(r.d0 | (r.d1 << 8));
         const uint32_t sa = bfe(r.la, 4 * (ka >> 3), 4) | (bfe(r.ha, 2 * (ka >> 2), 2) << 4);
         const uint32_t sb = bfe(r.lb, 4 * (kb >> 3), 4) | (bfe(r.hb, 2 * (kb >> 2), 2) << 4);
-        const u32x4 ca = vmap(r.q, 0x03030303u, 2 * j0) | (vmap(r.hm, 0x01010101u, 4 * n + j0) << 2);
-        const u32x4 cb = vmap(r.q, 0x03030303u, 2 * j0 + 2) | (vmap(r.hm, 0x01010101u, 4 * n + j0 + 1) << 2);
+        // fields j0 and j0 + 1 at bits 0-1 and 2-3 of each byte; hmask bit
+        // 4n + j0 to bit 2 (code + 4 hbit) and bit 4n + j0 + 1 to bit 4 (four
+        // times code + 4 hbit: the sum is scaled by 1/4, exactly)
+        const u32x4 qs = vmap(r.q, 0xffffffffu, 2 * j0);
+        const u32x4 ca = merge_hi(qs, 0x03030303u, r.hm, 4 * n + j0 - 2, 0x04040404u);
+        const u32x4 cb = merge_hi(qs, 0x0c0c0c0cu, r.hm, 4 * n + j0 - 3, 0x10101010u);
         const float SA = idot(ca, xa) - 4.f * xa.X;
-        const float SB = idot(cb, xb) - 4.f * xb.X;
+        const float SB = 0.25f * idot(cb, xb) - 4.f * xb.X;
         const float fa = d * (static_cast<float>(sa) - 32.f);
         const float fb = d * (static_cast<float>(sb) - 32.f);
         return fa * SA + fb * SB;
