@@ -838,7 +838,7 @@ def main() -> int:
                     help="run one workload (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
               "(the workloads would shard by output rows / heads with no exchange).", file=sys.stderr)
         return 2
 
