@@ -294,7 +294,7 @@ private:
         const uint32_t n_tensors = le<uint32_t>(8);
         const uint32_t meta_len = le<uint32_t>(12);
         if (size_ < kHeaderLen + meta_len) bail("BMTS meta truncated: " + path_);
-        if (version == kVersionV2) bail("BMTS v2 (Cap'n Proto meta) is not read by this build: " + path_);
+        if (version == kVersionV2) bail("BMTS v2 (Cap'n Proto meta) is not read by this library: " + path_);
         if (version != kVersion) bail("unsupported BMTS version " + std::to_string(version) + " in " + path_);
         const std::string meta(reinterpret_cast<const char *>(map_ + kHeaderLen), meta_len);
         tensors_ = TableReader(meta).read();

@@ -48,7 +48,7 @@ enum {
     /* GGML_TYPE_I2_S of BitNet's ggml fork: bitnet.cpp's 2-bit ternary
      * tensor (codes + one fp32 per-tensor scale) */
     ORC_KIND_I2_S = 36,
-    /* this build's canonical row-major 2-bit codes (no reference kind) */
+    /* the library's canonical row-major 2-bit codes (no reference kind) */
     ORC_KIND_I2 = 0x4932,
 };
 
@@ -163,7 +163,7 @@ void orc_gemm_i2s(const uint8_t *i2s, size_t out_len, size_t in_len,
                   const int8_t *xq, const float *act_scale, size_t ncols,
                   int32_t *acc, float *y, int nthreads);
 
-/* ---- this build's I2 layouts (device repacks of I2_S) -------------------
+/* ---- the library's I2 layouts (device repacks of I2_S) -------------------
  *
  * Canonical I2 packing: row r is in_len/4 bytes; element k sits in byte k/4
  * at bits 2*(k%4)..2*(k%4)+1 as code = w + 1.  w in {-1,0,1}.

@@ -68,7 +68,7 @@ class BmtsShard:
             except (ValueError, KeyError, TypeError) as e:
                 raise ShardError(f"BMTS tensor table unreadable in {path}: {e}") from e
         elif version == BMTS_VERSION_V2:
-            raise ShardError(f"BMTS v{BMTS_VERSION_V2} (Cap'n Proto meta) is not read by this build: {path}")
+            raise ShardError(f"BMTS v{BMTS_VERSION_V2} (Cap'n Proto meta) is not read by this library: {path}")
         else:
             raise ShardError(f"unsupported BMTS version {version} in {path}")
         if len(tensors) != n_tensors:

@@ -1,5 +1,5 @@
 """The committed golden fixtures still come out of the oracle bit for bit
-(guards the checker against drift)."""
+(guards the oracle against drift)."""
 from pathlib import Path
 
 import numpy as np
