@@ -439,6 +439,93 @@ void i2_gemm_big_kernel(GemmArgs a) {
     const float wscale = *a.w_scale;
     const bool quad = (a.M % 4) == 0 && !a.acc && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
                       (a.epi.op != EPI_RESID || (reinterpret_cast<uintptr_t>(a.epi.b) & 15) == 0);
+    if (quad && a.swiglu && a.M % 8 == 0) {
+        // SwiGLU: the wavefront's 64 rows are 32 (up, gate) pairs, so its
+        // outputs are 32 rows of each column: one pass through LDS (output
+        // chunk 4 r + q of column n, at chunk (4 r + q) ^ (n % 8)) and 8
+        // lanes to a 128-byte line on the way out, as above.
+        float *tw = reinterpret_cast<float *>(&xs[0][0]) + wave * (kBigCols * 32);
+#pragma unroll
+        for (int r = 0; r < kBigTM; ++r)
+#pragma unroll
+            for (int c = 0; c < kBigTN; ++c) {
+                const int nl = c * 32 + (lane & 31);
+                const I8sInv ds = i8s_inv(as[c]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float2 v;  // outputs 16 r + 4 q + 2 g + {0, 1} of the wavefront
+                    v.x = swiglu_pair(i8s_out_inv(-(acc[r][c][4 * q] >> 6), ds, wscale),
+                                      i8s_out_inv(-(acc[r][c][4 * q + 1] >> 6), ds, wscale));
+                    v.y = swiglu_pair(i8s_out_inv(-(acc[r][c][4 * q + 2] >> 6), ds, wscale),
+                                      i8s_out_inv(-(acc[r][c][4 * q + 3] >> 6), ds, wscale));
+                    *reinterpret_cast<float2 *>(tw + nl * 32 + 4 * ((4 * r + q) ^ (nl & 7)) + 2 * g) = v;
+                }
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int col = lane >> 3, j = lane & 7, mh = a.M / 2;
+        const int o0 = RT0 * 16;  // the wavefront's first output row
+#pragma unroll
+        for (int i = 0; i < kBigCols / 8; ++i) {
+            const int nl = 8 * i + col, n = n0 + nl, orow = o0 + 4 * j;
+            const float4 v = *reinterpret_cast<const float4 *>(tw + nl * 32 + 4 * (j ^ (nl & 7)));
+            if (n < a.N && orow < mh)  // mh % 4 == 0: a chunk of 4 outputs is all in or all out
+                *reinterpret_cast<float4 *>(a.y + static_cast<long long>(n) * mh + orow) = v;
+        }
+        return;
+    }
+    if (quad && !a.swiglu && (a.epi.op == EPI_NONE || a.epi.op == EPI_RESID)) {
+        // Through LDS, one 32-row tile at a time: the wavefront writes its
+        // 32 x 128 outputs column by column into its own 16 KiB of the
+        // (now idle) activation buffers, 16-byte chunk j of column n at
+        // chunk j ^ (n % 8), then reads them back so that 8 lanes hold one
+        // column's 32 rows and each store instruction writes 8 whole
+        // 128-byte lines (the register layout gives 32 partial lines).
+        float *tw = reinterpret_cast<float *>(&xs[0][0]) + wave * (kBigCols * 32);
+        const int col = lane >> 3, j = lane & 7;  // read back: column 8 i + col, rows 4 j .. 4 j + 3
+#pragma unroll
+        for (int r = 0; r < kBigTM; ++r) {
+            const int r0 = (RT0 + r) * 32;
+#pragma unroll
+            for (int c = 0; c < kBigTN; ++c) {
+                const int nl = c * 32 + (lane & 31);  // the lane's column in the tile
+                const I8sInv ds = i8s_inv(as[c]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float4 v;
+                    v.x = i8s_out_inv(-(acc[r][c][4 * q] >> 6), ds, wscale);
+                    v.y = i8s_out_inv(-(acc[r][c][4 * q + 1] >> 6), ds, wscale);
+                    v.z = i8s_out_inv(-(acc[r][c][4 * q + 2] >> 6), ds, wscale);
+                    v.w = i8s_out_inv(-(acc[r][c][4 * q + 3] >> 6), ds, wscale);
+                    *reinterpret_cast<float4 *>(tw + nl * 32 + 4 * ((2 * q + g) ^ (nl & 7))) = v;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int i = 0; i < kBigCols / 8; ++i) {
+                const int nl = 8 * i + col, n = n0 + nl, row = r0 + 4 * j;
+                float4 v = *reinterpret_cast<const float4 *>(tw + nl * 32 + 4 * (j ^ (nl & 7)));
+                if (n < a.N && row + 3 < a.M) {
+                    const long long o = static_cast<long long>(n) * a.M + row;
+                    if (a.epi.op == EPI_RESID) {
+                        const float4 res = *reinterpret_cast<const float4 *>(a.epi.b + o);
+                        v.x = res.x + v.x;
+                        v.y = res.y + v.y;
+                        v.z = res.z + v.z;
+                        v.w = res.w + v.w;
+                    }
+                    *reinterpret_cast<float4 *>(a.y + o) = v;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();  // the reads are done before the next tile's writes
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < kBigTN; ++c) {
         const int n = n0 + c * 32 + (lane & 31);

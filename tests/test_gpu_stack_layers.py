@@ -46,9 +46,9 @@ def rel(a, b):
     return float(np.abs(a - b).max() / np.abs(b).max())
 
 
-def gpu_run(card, ps, feed):
+def gpu_run(card, ps, feed, max_ctx=32):
     N = len(ps)
-    st = Stack(card, 7, max_seqs=N, max_tokens=int(sum(len(p) for p in ps)), max_ctx=32)
+    st = Stack(card, 7, max_seqs=N, max_tokens=int(sum(len(p) for p in ps)), max_ctx=max_ctx)
     try:
         cu = np.concatenate([[0], np.cumsum([len(p) for p in ps])]).astype(np.int32)
         toks = DeviceBuffer.from_host(np.concatenate(ps).astype(np.int32))
@@ -99,3 +99,33 @@ def test_full_width_delta_layer(gpu, margin):
     print("delta-net layer vs bf16-prefill oracle:", e16, "vs fp32 oracle:", e32)
     assert max(e16) < 5e-2, e16
     assert max(e32) < 0.1, e32
+
+
+def long_prompts():
+    rng = np.random.default_rng(5)
+    return [rng.integers(0, VOCAB, n).astype(np.int32) for n in (300, 131)]
+
+
+def test_full_width_layers_long_prefill(gpu, margin):
+    """The same layers over 431 prompt tokens: enough columns that the
+    projections run on the 32x32x32 ternary GEMM (its row-major and SwiGLU
+    epilogues) and the attention covers five 64-key pages of one prompt,
+    against the same oracles at the same bars (one decode step after)."""
+    from oracle.stack_oracle import StackOracle
+
+    ps = long_prompts()
+    want, wtok = StackOracle(ATTN1, seed=7).run(ps, 1)
+    got, _ = gpu_run(ATTN1, ps, wtok[:-1], max_ctx=320)
+    ea = [rel(g, w) for g, w in zip(got, want)]
+    for i, (g, w) in enumerate(zip(got, want)):
+        margin(f"attention layer, 431 tokens, step {i}", g, w, 5e-2)
+    l32, t32 = StackOracle(DELTA1, seed=7).run(ps, 1)
+    l16, _ = StackOracle(DELTA1, seed=7, bf16_prefill=True).run(ps, 1, feed=t32[:-1])
+    gd, _ = gpu_run(DELTA1, ps, t32[:-1], max_ctx=320)
+    e16 = [rel(g, w) for g, w in zip(gd, l16)]
+    for i, (g, w) in enumerate(zip(gd, l16)):
+        margin(f"delta-net layer, 431 tokens, step {i}", g, w, 5e-2)
+    print("431-token prefill: attention", ea, "delta-net vs bf16 oracle", e16)
+    assert max(ea) < 5e-2, ea
+    assert max(e16) < 5e-2, e16
+
