@@ -29,6 +29,12 @@ HIPCC_FLAGS = [
     "-Wall",
 ]
 
+# Flags for one source file only.  kquant.hip: MFMA results in ordinary
+# VGPRs (the accumulator-register form would add a copy per result read).
+FILE_FLAGS = {
+    "kquant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -39,7 +45,7 @@ def _hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature name; that warning
     # is expected and filtered out.

@@ -34,6 +34,9 @@
 // and Q6_K (34, 110, 210 bytes) are only 2-byte aligned: their 16-byte pieces
 // are read as the aligned dwords that cover them and shifted into place with
 // v_alignbyte.  Scale bytes are read as bytes.
+//
+// Q3_K rows of up to 64 blocks go to kq3_mfma_kernel instead: the same digit
+// planes, but the products on the int8 matrix cores (see that kernel).
 #include "common.hpp"
 
 #include <algorithm>
@@ -601,6 +604,268 @@ __global__ __launch_bounds__(256) void kq_row_kernel(KqArgs a) {
     if (lane == 0) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
 }
 
+// ---- Q3_K on the int8 matrix cores ----
+//
+// v_mfma_i32_16x16x64_i8 with x's digit planes as the A operand and the
+// codes as B, so the products leave the vector ALU, which is left with the
+// decode and the scales.  A wavefront takes 16 rows (the columns of D) a
+// step.  Lane l = 16 g + c loads, for row c of the step, piece g of each
+// block: half n = g / 2, bytes l0 = 16 (g % 2) .. l0 + 15 of qs and of
+// hmask, and the scale bytes.  For run j (elements 128 n + 32 j + l0 + i,
+// code bits 2j of qs, hmask bit 4n + j) its 16-byte B slice holds 32 code as
+// int8: the two code bits at bits 5-6 and the inverted hmask bit at bit 7,
+// whose int8 value is 32 (lo2 + 4 hbit - 4).  A row 4 g' + p holds digit
+// plane p (p < 3) of run (g', j)'s 16 x values in k-slot group g' and zeros
+// elsewhere, so D row 4 g + p, column c is run (g, j) of row c summed against
+// plane p: lane l receives the three plane sums of its own run, adds them
+// exactly in int32 (65536 S0 + 256 S1 + S2, each a multiple of 32) and
+// applies the run's scale, the x exponent and, per block, d in fp32.  The
+// four pieces' partial sums of a row meet by two lane swaps at the end.
+//
+// The x planes of a column are built once per workgroup into LDS (896 bytes
+// a block: for each j the planes [g][p][16] and a 16-byte zero slot, which
+// the A lanes outside their group read, then the exponents [g][j]).  When the payload and its rows
+// are dword-aligned (Q3K_AL), even blocks start on a dword and odd blocks two
+// bytes past one: an even block's pieces are single aligned loads, an odd
+// block's qs and hmask pieces are read as the five dwords that cover them
+// and passed to the MFMA with their first dword's two leading bytes replaced
+// by the last two bytes (elements 14, 15, 0, .., 13), the order its x planes
+// are stored in.  Otherwise every piece is shifted into place per lane.
+constexpr int kQ3Waves = 4;          // wavefronts per workgroup, 16 rows each
+constexpr int kQ3Threads = 64 * kQ3Waves;
+constexpr int kQ3Rows = 16 * kQ3Waves;
+constexpr int kQ3MaxBlocks = 64;     // longer rows take the task kernel
+constexpr int kQ3Run = 208;          // LDS bytes of a block's run j: planes [g][p][16], then 16 zero bytes
+constexpr int kQ3Unit = 4 * kQ3Run + 64;  // a block: its four runs' planes, then the exponents [g][j]
+enum { Q3K_ANY = 0, Q3K_AL = 1 };
+
+typedef int q3v4i __attribute__((ext_vector_type(4)));
+
+// One block's loads for one lane: the qs and hmask pieces (q4 / h4: the
+// fifth dword of an odd block's pieces), the scale piece P and d.
+struct Q3Raw {
+    u32x4 q, h, P;
+    uint32_t q4, h4, d;
+};
+
+// PAR: 0 an aligned (even) block, 1 an odd block two bytes past a dword,
+// 2 any phase (per-lane shifts).  P holds the scale bytes from byte PO on
+// (PO = 4 for PAR 0: bytes 92..107, d loaded on its own; PO = 2 otherwise:
+// bytes 94..109, d in P's last two bytes).
+template <int PAR>
+__device__ __forceinline__ void q3_load(Q3Raw &r, const uint8_t *bp, int g) {
+    if constexpr (PAR == 0) {
+        r.q = *reinterpret_cast<const u32x4_a4 *>(bp + 32 + 16 * g);
+        r.h = *reinterpret_cast<const u32x4_a4 *>(bp + 16 * (g & 1));
+        r.P = *reinterpret_cast<const u32x4_a4 *>(bp + 92);
+        r.d = *reinterpret_cast<const uint16_t *>(bp + 108);
+    } else if constexpr (PAR == 1) {
+        r.q = *reinterpret_cast<const u32x4_a4 *>(bp + 30 + 16 * g);
+        r.q4 = *reinterpret_cast<const uint32_t *>(bp + 46 + 16 * g);
+        r.h = *reinterpret_cast<const u32x4_a4 *>(bp - 2 + 16 * (g & 1));
+        r.h4 = *reinterpret_cast<const uint32_t *>(bp + 14 + 16 * (g & 1));
+        r.P = *reinterpret_cast<const u32x4_a4 *>(bp + 94);
+    } else {
+        r.q = load16_any(bp + 32 + 16 * g);
+        r.h = load16_any(bp + 16 * (g & 1));
+        r.P = load16_any(bp + 94);
+    }
+}
+
+// Scale k = 8 n + 2 j + g % 2 of the lane's piece, minus 32: low four bits
+// nibble n of scale byte 2 j + g % 2, high two bits field 2 n + j / 2 of
+// byte 8 + 2 (j % 2) + g % 2 (dequant.rs:398-451).  L = 8 (g % 2) + 4 n.
+// P's high-bit bytes come with the top bit of every two-bit field flipped
+// (q3_flip), so the field read as a signed value is hi - 2 and the scale
+// minus 32 is lo + 16 (hi - 2).
+template <int PO, int J>
+__device__ __forceinline__ int q3_scale(const u32x4 &P, uint32_t L) {
+    constexpr int blo = PO + 2 * J, bhi = PO + 8 + 2 * (J & 1);
+    const uint32_t lo = bfe(P[blo >> 2], 8 * (blo & 3) + L, 4);
+    const int hi = __builtin_amdgcn_sbfe(static_cast<int>(P[bhi >> 2]), 8 * (bhi & 3) + 2 * (J >> 1) + L, 2);
+    return static_cast<int>(lo) + hi * 16;
+}
+
+// P with bit 1 of every two-bit field of the high-bit bytes (scale bytes
+// 8..11, P bytes PO + 8 .. PO + 11) flipped.
+template <int PO>
+__device__ __forceinline__ u32x4 q3_flip(u32x4 P) {
+    if constexpr (PO == 4) {
+        P.w ^= 0xaaaaaaaau;
+    } else {
+        P.z ^= 0xaaaa0000u;
+        P.w ^= 0x0000aaaau;
+    }
+    return P;
+}
+
+// One block of the lane's row: the four runs' MFMAs, then d.  aoff: the
+// lane's A slot within a run's planes; hr[j]: the rotation that brings
+// hmask bit 4n + j to bit 7.
+template <int PAR>
+__device__ __forceinline__ float q3_block(const Q3Raw &r, const uint8_t *xlds, int b, int aoff,
+                                          const uint32_t (&hr)[4], uint32_t L, int g) {
+#pragma clang fp contract(off)
+    constexpr int PO = PAR == 0 ? 4 : 2;
+    u32x4 q = r.q, h = r.h;
+    if constexpr (PAR == 1) {
+        q.x = (q.x & 0xffff0000u) | (r.q4 & 0xffffu);
+        h.x = (h.x & 0xffff0000u) | (r.h4 & 0xffffu);
+    }
+    const u32x4 hn = ~h;
+    const u32x4 P = q3_flip<PO>(r.P);
+    const uint8_t *xb = xlds + b * kQ3Unit;
+    const float4 xs = *reinterpret_cast<const float4 *>(xb + 4 * kQ3Run + 16 * g);
+    float blk = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const q3v4i A = *reinterpret_cast<const q3v4i *>(xb + kQ3Run * j + aoff);
+        q3v4i B;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t qv = __builtin_amdgcn_alignbit(q[d], q[d], (2 * j - 5) & 31) & 0x60606060u;
+            B[d] = static_cast<int>(qv | (__builtin_amdgcn_alignbit(hn[d], hn[d], hr[j]) & 0x80808080u));
+        }
+        const q3v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, q3v4i{0, 0, 0, 0}, 0, 0, 0);
+        const int t = (D[1] << 3) + (D[2] >> 5);
+        const int U = (D[0] << 11) + t;
+        int s;
+        if (j == 0) s = q3_scale<PO, 0>(P, L);
+        else if (j == 1) s = q3_scale<PO, 1>(P, L);
+        else if (j == 2) s = q3_scale<PO, 2>(P, L);
+        else s = q3_scale<PO, 3>(P, L);
+        const float xsj = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
+        blk = __builtin_fmaf(static_cast<float>(s), xsj * static_cast<float>(U), blk);
+    }
+    const uint32_t dbits = PAR == 0 ? r.d : (r.P.w >> 16);
+    return f16f(dbits) * blk;
+}
+
+// x's digit planes of every run into LDS; rot_odd: the element order of the
+// odd blocks' B slices (14: elements 14, 15, 0, .., 13).
+__device__ __forceinline__ void q3_prep(const float *xc, int nb, uint8_t *xlds, int rot_odd) {
+    for (int run = threadIdx.x; run < nb * 16; run += blockDim.x) {
+        const int b = run >> 4, g = (run >> 2) & 3, j = run & 3;
+        const float *src = xc + 256 * b + 128 * (g >> 1) + 32 * j + 16 * (g & 1);
+        const int rot = (b & 1) ? rot_odd : 0;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = src[(i + rot) & 15];
+        XRun xr;
+        make_run(v, xr);
+        uint8_t *xb = xlds + b * kQ3Unit;
+        u32x4 *dst = reinterpret_cast<u32x4 *>(xb + kQ3Run * j + 48 * g);
+        dst[0] = xr.p0;
+        dst[1] = xr.p1;
+        dst[2] = xr.p2;
+        if (g == 0) *reinterpret_cast<u32x4 *>(xb + kQ3Run * j + 192) = u32x4{0u, 0u, 0u, 0u};
+        reinterpret_cast<float *>(xb + 4 * kQ3Run)[4 * g + j] = xr.s;
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
+    const int nb = a.in_len / 256;
+    const int col = blockIdx.y;
+    q3_prep(a.x + static_cast<long long>(col) * a.in_len, nb, xlds, MODE == Q3K_AL ? 14 : 0);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4, n = g >> 1;
+    // A slot: row c = 4 g' + p holds plane p of run (g', j) in k-slot group
+    // g, zeros (the run's zero slot) unless g' = g and p < 3
+    const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
+    uint32_t hr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hr[j] = static_cast<uint32_t>(4 * n + j - 7) & 31u;
+    const uint32_t L = 8u * (g & 1) + 4u * n;
+    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    int tile = blockIdx.x;
+    if (tile >= tiles) return;  // no barrier follows
+    const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
+    auto row_ptr = [&](int t) {
+        const int row = min(min(t, tiles - 1) * kQ3Rows + 16 * wave + c, a.out_len - 1);  // clamped rows are dropped
+        return a.w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32;
+    };
+    // a row's partial sums over the four pieces, added by two lane swaps;
+    // lanes 0..15 store
+    auto finish = [&](float acc, int t) {
+        auto q1 = __builtin_amdgcn_permlane32_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q1[0]) + fbits(q1[1]);
+        auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q2[0]) + fbits(q2[1]);
+        const int row = t * kQ3Rows + 16 * wave + c;
+        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+    };
+    const int g8 = gridDim.x;
+    if constexpr (MODE == Q3K_AL) {
+        // steps of two blocks (an even and an odd one); nb is even here
+        const int steps = nb / 2;
+        Q3Raw e0, o0, e1, o1;
+        auto issue = [&](Q3Raw &e, Q3Raw &o, int t, int s) {
+            const uint8_t *bp = row_ptr(t) + 220 * s;
+            q3_load<0>(e, bp, g);
+            q3_load<1>(o, bp + 110, g);
+        };
+        int s = 0;
+        float acc = 0.f;
+        issue(e0, o0, tile, 0);
+        vm_drain();
+        auto step = [&](const Q3Raw &e, const Q3Raw &o) {
+            acc += q3_block<0>(e, xlds, 2 * s, aoff, hr, L, g);
+            acc += q3_block<1>(o, xlds, 2 * s + 1, aoff, hr, L, g);
+            if (++s == steps) {
+                finish(acc, tile);
+                acc = 0.f;
+                s = 0;
+                tile += g8;
+            }
+        };
+        for (;;) {
+            {
+                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
+                issue(e1, o1, nt, ns);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            step(e0, o0);
+            if (tile >= tiles) break;
+            {
+                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
+                issue(e0, o0, nt, ns);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            step(e1, o1);
+            if (tile >= tiles) break;
+        }
+    } else {
+        Q3Raw r0, r1;
+        auto issue = [&](Q3Raw &r, int t, int b) { q3_load<2>(r, row_ptr(t) + 110 * b, g); };
+        int b = 0;
+        float acc = 0.f;
+        issue(r0, tile, 0);
+        vm_drain();
+        auto step = [&](const Q3Raw &r) {
+            acc += q3_block<2>(r, xlds, b, aoff, hr, L, g);
+            if (++b == nb) {
+                finish(acc, tile);
+                acc = 0.f;
+                b = 0;
+                tile += g8;
+            }
+        };
+        for (;;) {
+            issue(r1, b + 1 == nb ? tile + g8 : tile, b + 1 == nb ? 0 : b + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            step(r0);
+            if (tile >= tiles) break;
+            issue(r0, b + 1 == nb ? tile + g8 : tile, b + 1 == nb ? 0 : b + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            step(r1);
+            if (tile >= tiles) break;
+        }
+    }
+}
+
 // Rows per slot per tile (two tiles' loads in flight): measured best over
 // 248320x5120 and 6912x2560 (R = 1, 2, 4), with workgroups of at most 256
 // threads (384- and 512-thread caps were 10-60 % slower).
@@ -646,6 +911,19 @@ template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     const bool ph = a.row_bytes % 4 == 0;
     using F = Fmt<KIND>;
+    if constexpr (KIND == OURO_KIND_Q3K) {
+        const int nb = a.in_len / 256;
+        if (nb <= kQ3MaxBlocks) {
+            // dword-aligned payload and rows (so nb is even): blocks alternate phase 0 / 2
+            const bool al = reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph;
+            const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+            const dim3 grid(std::min(tiles, cu_count() * 4), k);
+            const size_t lds = static_cast<size_t>(nb) * kQ3Unit;
+            if (al) hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_AL>, grid, dim3(kQ3Threads), lds, s, a);
+            else hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ANY>, grid, dim3(kQ3Threads), lds, s, a);
+            return check_launch("kq3_mfma_kernel");
+        }
+    }
     a.tpr = a.in_len / F::EPB * F::TPB;
     const KqPlan pl = kq_plan(a.tpr);
     if (!pl.slots) {
