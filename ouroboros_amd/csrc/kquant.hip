@@ -624,52 +624,48 @@ __global__ __launch_bounds__(256) void kq_row_kernel(KqArgs a) {
 //
 // The x planes of a column are built once per workgroup into LDS (896 bytes
 // a block: for each j the planes [g][p][16] and a 16-byte zero slot, which
-// the A lanes outside their group read, then the exponents [g][j]).  When the payload and its rows
-// are dword-aligned (Q3K_AL), even blocks start on a dword and odd blocks two
-// bytes past one: an even block's pieces are single aligned loads, an odd
-// block's qs and hmask pieces are read as the five dwords that cover them
-// and passed to the MFMA with their first dword's two leading bytes replaced
-// by the last two bytes (elements 14, 15, 0, .., 13), the order its x planes
-// are stored in.  Otherwise every piece is shifted into place per lane.
+// the A lanes outside their group read, then the exponents [g][j]).
+//
+// Loads.  When the payload and its rows are dword-aligned (Q3K_ST), a step
+// is two blocks (220 bytes of each of the 16 rows) and each wavefront stages
+// its rows' step segments through its own LDS area with contiguous 16-byte
+// loads (a load's 16-lane quarters read 256 consecutive bytes instead of
+// 16 bytes from each of 16 rows).  The even block of a segment sits on a
+// 16-byte boundary in LDS, so its pieces are single 16-byte reads; the odd
+// block starts 2 bytes before one, so its qs and hmask pieces are read as
+// bytes 2..15 (one 16-byte read) plus bytes 0..1 (from the dword before),
+// in the element order 2, .., 15, 0, 1, which is the order the odd blocks'
+// x planes are stored in.  Otherwise (Q3K_ANY) each lane loads its pieces
+// from global memory and shifts them into place.
 constexpr int kQ3Waves = 4;          // wavefronts per workgroup, 16 rows each
 constexpr int kQ3Threads = 64 * kQ3Waves;
 constexpr int kQ3Rows = 16 * kQ3Waves;
 constexpr int kQ3MaxBlocks = 64;     // longer rows take the task kernel
 constexpr int kQ3Run = 208;          // LDS bytes of a block's run j: planes [g][p][16], then 16 zero bytes
 constexpr int kQ3Unit = 4 * kQ3Run + 64;  // a block: its four runs' planes, then the exponents [g][j]
-enum { Q3K_ANY = 0, Q3K_AL = 1 };
+enum { Q3K_ANY = 0, Q3K_ST = 1 };
+constexpr int kQ3Pitch = 224;        // staged (Q3K_ST): LDS bytes of a row's step segment (220 used)
+constexpr int kQ3Stage = 16 * kQ3Pitch;  // a wavefront's staging area
 
 typedef int q3v4i __attribute__((ext_vector_type(4)));
 
-// One block's loads for one lane: the qs and hmask pieces (q4 / h4: the
-// fifth dword of an odd block's pieces), the scale piece P and d.
+// One block's pieces for one lane: qs and hmask (q4 / h4: bytes 0..1 of a
+// staged odd block's pieces, in their upper halves) and the scale piece P.
 struct Q3Raw {
     u32x4 q, h, P;
-    uint32_t q4, h4, d;
+    uint32_t q4, h4;
 };
 
-// PAR: 0 an aligned (even) block, 1 an odd block two bytes past a dword,
-// 2 any phase (per-lane shifts).  P holds the scale bytes from byte PO on
-// (PO = 4 for PAR 0: bytes 92..107, d loaded on its own; PO = 2 otherwise:
-// bytes 94..109, d in P's last two bytes).
-template <int PAR>
-__device__ __forceinline__ void q3_load(Q3Raw &r, const uint8_t *bp, int g) {
-    if constexpr (PAR == 0) {
-        r.q = *reinterpret_cast<const u32x4_a4 *>(bp + 32 + 16 * g);
-        r.h = *reinterpret_cast<const u32x4_a4 *>(bp + 16 * (g & 1));
-        r.P = *reinterpret_cast<const u32x4_a4 *>(bp + 92);
-        r.d = *reinterpret_cast<const uint16_t *>(bp + 108);
-    } else if constexpr (PAR == 1) {
-        r.q = *reinterpret_cast<const u32x4_a4 *>(bp + 30 + 16 * g);
-        r.q4 = *reinterpret_cast<const uint32_t *>(bp + 46 + 16 * g);
-        r.h = *reinterpret_cast<const u32x4_a4 *>(bp - 2 + 16 * (g & 1));
-        r.h4 = *reinterpret_cast<const uint32_t *>(bp + 14 + 16 * (g & 1));
-        r.P = *reinterpret_cast<const u32x4_a4 *>(bp + 94);
-    } else {
-        r.q = load16_any(bp + 32 + 16 * g);
-        r.h = load16_any(bp + 16 * (g & 1));
-        r.P = load16_any(bp + 94);
-    }
+// PAR: 0 a staged even block (P = block bytes 96..111: the scale bytes from
+// P byte 0, d at 12), 1 a staged odd block (q, h = piece bytes 2..15 and two
+// more; P = block bytes 94..109: the scale bytes from byte 2, d at 14), 2 a
+// block loaded per lane (as 1, in natural order).
+template <int PAR> constexpr int kQ3PO = PAR == 0 ? 0 : 2;
+
+__device__ __forceinline__ void q3_load_any(Q3Raw &r, const uint8_t *bp, int g) {
+    r.q = load16_any(bp + 32 + 16 * g);
+    r.h = load16_any(bp + 16 * (g & 1));
+    r.P = load16_any(bp + 94);
 }
 
 // Scale k = 8 n + 2 j + g % 2 of the lane's piece, minus 32: low four bits
@@ -690,8 +686,8 @@ __device__ __forceinline__ int q3_scale(const u32x4 &P, uint32_t L) {
 // 8..11, P bytes PO + 8 .. PO + 11) flipped.
 template <int PO>
 __device__ __forceinline__ u32x4 q3_flip(u32x4 P) {
-    if constexpr (PO == 4) {
-        P.w ^= 0xaaaaaaaau;
+    if constexpr (PO == 0) {
+        P.z ^= 0xaaaaaaaau;
     } else {
         P.z ^= 0xaaaa0000u;
         P.w ^= 0x0000aaaau;
@@ -706,11 +702,11 @@ template <int PAR>
 __device__ __forceinline__ float q3_block(const Q3Raw &r, const uint8_t *xlds, int b, int aoff,
                                           const uint32_t (&hr)[4], uint32_t L, int g) {
 #pragma clang fp contract(off)
-    constexpr int PO = PAR == 0 ? 4 : 2;
+    constexpr int PO = kQ3PO<PAR>;
     u32x4 q = r.q, h = r.h;
-    if constexpr (PAR == 1) {
-        q.x = (q.x & 0xffff0000u) | (r.q4 & 0xffffu);
-        h.x = (h.x & 0xffff0000u) | (r.h4 & 0xffffu);
+    if constexpr (PAR == 1) {  // bytes 14, 15, 0, 1 in the last dword
+        q.w = (q.w & 0xffffu) | (r.q4 & 0xffff0000u);
+        h.w = (h.w & 0xffffu) | (r.h4 & 0xffff0000u);
     }
     const u32x4 hn = ~h;
     const u32x4 P = q3_flip<PO>(r.P);
@@ -737,12 +733,12 @@ __device__ __forceinline__ float q3_block(const Q3Raw &r, const uint8_t *xlds, i
         const float xsj = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
         blk = __builtin_fmaf(static_cast<float>(s), xsj * static_cast<float>(U), blk);
     }
-    const uint32_t dbits = PAR == 0 ? r.d : (r.P.w >> 16);
+    const uint32_t dbits = PAR == 0 ? (r.P.w & 0xffffu) : (r.P.w >> 16);
     return f16f(dbits) * blk;
 }
 
 // x's digit planes of every run into LDS; rot_odd: the element order of the
-// odd blocks' B slices (14: elements 14, 15, 0, .., 13).
+// odd blocks' B slices (2: elements 2, .., 15, 0, 1).
 __device__ __forceinline__ void q3_prep(const float *xc, int nb, uint8_t *xlds, int rot_odd) {
     for (int run = threadIdx.x; run < nb * 16; run += blockDim.x) {
         const int b = run >> 4, g = (run >> 2) & 3, j = run & 3;
@@ -768,8 +764,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
     const int nb = a.in_len / 256;
     const int col = blockIdx.y;
-    q3_prep(a.x + static_cast<long long>(col) * a.in_len, nb, xlds, MODE == Q3K_AL ? 14 : 0);
-    __syncthreads();
+    const float *xc = a.x + static_cast<long long>(col) * a.in_len;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4, n = g >> 1;
     // A slot: row c = 4 g' + p holds plane p of run (g', j) in k-slot group
@@ -781,7 +776,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
     const uint32_t L = 8u * (g & 1) + 4u * n;
     const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
     int tile = blockIdx.x;
-    if (tile >= tiles) return;  // no barrier follows
+    if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
     const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
     auto row_ptr = [&](int t) {
         const int row = min(min(t, tiles - 1) * kQ3Rows + 16 * wave + c, a.out_len - 1);  // clamped rows are dropped
@@ -798,20 +793,66 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
         if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
     };
     const int g8 = gridDim.x;
-    if constexpr (MODE == Q3K_AL) {
-        // steps of two blocks (an even and an odd one); nb is even here
+    if constexpr (MODE == Q3K_ST) {
+        // steps of two blocks (nb is even).  Each wavefront stages its 16
+        // rows' 220-byte step segments through its own LDS area with
+        // contiguous 16-byte loads: 14 units a row, unit 13 read from byte
+        // 204 (overlapping unit 12, so no read passes the segment) and stored
+        // at 208, so segment bytes from 208 on sit 4 bytes later in LDS.
         const int steps = nb / 2;
-        Q3Raw e0, o0, e1, o1;
-        auto issue = [&](Q3Raw &e, Q3Raw &o, int t, int s) {
-            const uint8_t *bp = row_ptr(t) + 220 * s;
-            q3_load<0>(e, bp, g);
-            q3_load<1>(o, bp + 110, g);
+        uint8_t *wl = xlds + nb * kQ3Unit + wave * kQ3Stage;
+        int urow[4], uoff[4], ulds[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int id = min(64 * i + lane, 223), un = id % 14;
+            urow[i] = id / 14;
+            uoff[i] = un < 13 ? 16 * un : 204;
+            ulds[i] = kQ3Pitch * (id / 14) + 16 * un;
+        }
+        u32x4 st[4];
+        auto issue = [&](int t, int s) {
+            const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
+                st[i] = *reinterpret_cast<const u32x4_a4 *>(a.w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32 +
+                                                           220 * s + uoff[i]);
+            }
         };
+        auto stage = [&]() {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < 3 || lane < 32) *reinterpret_cast<u32x4 *>(wl + ulds[i]) = st[i];
+        };
+        const uint8_t *rl = wl + kQ3Pitch * c;
         int s = 0;
         float acc = 0.f;
-        issue(e0, o0, tile, 0);
-        vm_drain();
-        auto step = [&](const Q3Raw &e, const Q3Raw &o) {
+        issue(tile, 0);
+        q3_prep(xc, nb, xlds, 2);  // the first loads are in flight meanwhile
+        __syncthreads();
+        for (;;) {
+            stage();
+            {
+                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
+                issue(nt, ns);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // even block: segment bytes 0..109 (scale bytes from P byte 0, d at 12)
+            Q3Raw e, o;
+            e.q = *reinterpret_cast<const u32x4 *>(rl + 32 + 16 * g);
+            e.h = *reinterpret_cast<const u32x4 *>(rl + 16 * (g & 1));
+            e.P = *reinterpret_cast<const u32x4 *>(rl + 96);
+            // odd block: segment bytes 110..219; a piece's bytes 2..15 and 0..1
+            // (elements 2, .., 15, 0, 1); scale bytes from P byte 2, d at 14
+            o.q = *reinterpret_cast<const u32x4 *>(rl + 144 + 16 * g);
+            o.q4 = *reinterpret_cast<const uint32_t *>(rl + 140 + 16 * g);
+            o.h = *reinterpret_cast<const u32x4 *>(rl + 112 + 16 * (g & 1));
+            o.h4 = *reinterpret_cast<const uint32_t *>(rl + 108 + 16 * (g & 1));
+            o.P.x = *reinterpret_cast<const uint32_t *>(rl + 204);
+            o.P.y = *reinterpret_cast<const uint32_t *>(rl + 212);
+            const uint2 zw = *reinterpret_cast<const uint2 *>(rl + 216);
+            o.P.z = zw.x;
+            o.P.w = zw.y;
             acc += q3_block<0>(e, xlds, 2 * s, aoff, hr, L, g);
             acc += q3_block<1>(o, xlds, 2 * s + 1, aoff, hr, L, g);
             if (++s == steps) {
@@ -820,30 +861,16 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
                 s = 0;
                 tile += g8;
             }
-        };
-        for (;;) {
-            {
-                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
-                issue(e1, o1, nt, ns);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            step(e0, o0);
-            if (tile >= tiles) break;
-            {
-                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
-                issue(e0, o0, nt, ns);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            step(e1, o1);
             if (tile >= tiles) break;
         }
     } else {
         Q3Raw r0, r1;
-        auto issue = [&](Q3Raw &r, int t, int b) { q3_load<2>(r, row_ptr(t) + 110 * b, g); };
+        auto issue = [&](Q3Raw &r, int t, int b) { q3_load_any(r, row_ptr(t) + 110 * b, g); };
         int b = 0;
         float acc = 0.f;
         issue(r0, tile, 0);
-        vm_drain();
+        q3_prep(xc, nb, xlds, 0);
+        __syncthreads();
         auto step = [&](const Q3Raw &r) {
             acc += q3_block<2>(r, xlds, b, aoff, hr, L, g);
             if (++b == nb) {
@@ -914,12 +941,14 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     if constexpr (KIND == OURO_KIND_Q3K) {
         const int nb = a.in_len / 256;
         if (nb <= kQ3MaxBlocks) {
-            // dword-aligned payload and rows (so nb is even): blocks alternate phase 0 / 2
+            // dword-aligned payload and rows (so nb is even): the staged loads
             const bool al = reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph;
             const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
             const dim3 grid(std::min(tiles, cu_count() * 4), k);
             const size_t lds = static_cast<size_t>(nb) * kQ3Unit;
-            if (al) hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_AL>, grid, dim3(kQ3Threads), lds, s, a);
+            const size_t lds_st = lds + kQ3Waves * kQ3Stage;
+            if (al && lds_st <= 65536)
+                hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ST>, grid, dim3(kQ3Threads), lds_st, s, a);
             else hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ANY>, grid, dim3(kQ3Threads), lds, s, a);
             return check_launch("kq3_mfma_kernel");
         }
