@@ -29,10 +29,12 @@ HIPCC_FLAGS = [
     "-Wall",
 ]
 
-# Flags for one source file only.  kquant.hip: MFMA results in ordinary
-# VGPRs (the accumulator-register form would add a copy per result read).
+# Flags for one source file only.  kquant.hip, tl1_mfma.hip: MFMA results
+# in ordinary VGPRs (the accumulator-register form adds a copy per result
+# read; measured faster in both).
 FILE_FLAGS = {
     "kquant.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "tl1_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -13,18 +13,20 @@
 // Activations.  Column c of x, group g (128 elements): with E the binary
 // exponent of the group's largest |x| (|x| < 2^E), x_int = rint(x 2^(22-E)),
 // |x_int| <= 2^22, split into balanced base-256 digits x_int = 65536 p0 +
-// 256 p1 + p2 (each int8).  The three digit planes of every column are the
-// columns 3c + p of the MFMA B operand, laid out in its fragment order (one
-// 1 KiB piece per k block, step and tile of 16 B columns: lane l holds B
-// column l%16, k = 64 s + 16 (l/16) .. +16).  Elements below 2^(E-23) of a
-// group lose their low bits (error <= 2^-23 of the group's largest |x|).
+// 256 p1 + p2 (each int8, |p0| <= 65).  The three digit planes of column c
+// are the rows 4c + p of the MFMA A operand (row 4c + 3 is zero), laid out
+// in its fragment order (one 1 KiB piece per k block, step and tile of 16
+// rows: lane l holds A row l%16, k = 64 s + 16 (l/16) .. +16).  Elements
+// below 2^(E-23) of a group lose their low bits (error <= 2^-23 of the
+// group's largest |x|).
 //
-// Product.  Per group, two 16x16x64 int8 MFMA steps give the exact int32 sum
-// A = -64 sum_k trit x_int_p for every (row, plane column); the group's term
-// d(row, g) * w(g, column) * A, w = -2^(E - 28 + 8 (2 - p)) (the digit weight,
-// the exponent and the -64 of the A encoding), is added to an fp32
-// accumulator per (row, plane column); the three planes of a column are added
-// at the end.
+// Product.  The weights are the B operand, so D row 4c + p, column r is row
+// r's sum against plane p of column c, and lane l = 16 q + r of the D
+// fragment holds the three planes of column 4 t + q (tile t) for its own
+// weight row r.  Per group, two 16x16x64 int8 MFMA steps give exact int32
+// plane sums, which the lane combines exactly into T = sum_k trit x_int
+// (65536 S0 + 256 S1 + S2, scaled back from the encoding), and adds
+// d(r, g) 2^(E-22) T to an fp32 accumulator per (row, column).
 #include "common.hpp"
 
 #include <algorithm>
@@ -36,7 +38,7 @@ namespace {
 
 constexpr int kWave = 64;
 constexpr int kWaves = 4;  // wavefronts per workgroup, stacked along the rows
-constexpr int kPlanes = 3;
+constexpr int kRowsPerCol = 4;  // A rows of an x column: its three digit planes and a zero row
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
@@ -118,9 +120,9 @@ __global__ void tl1_scales_kernel(const uint8_t *__restrict__ raw, uint16_t *__r
 
 struct XprepArgs {
     const float *x;  // [ncols][K]
-    int8_t *xb;      // B fragments: [nkb][4 steps][tiles][64 lanes][16 bytes]
-    float *wt;       // [G][16 tiles] plane weights
-    int32_t *sx;     // [G][16 tiles] sums of each B column's digits over the group
+    int8_t *xb;      // A fragments: [nkb][4 steps][tiles][64 lanes][16 bytes]
+    float *wt;       // [G][4 tiles] 2^(E-22) of each column
+    int32_t *sx;     // [G][4 tiles] each column's sum of x_int over the group
     int K, G, tiles, ncols;
 };
 static_assert(sizeof(XprepArgs) == 48, "XprepArgs: kernel argument layout");
@@ -129,7 +131,7 @@ static_assert(sizeof(XprepArgs) == 48, "XprepArgs: kernel argument layout");
 // ncols (up to the last tile's end) and k past K write zero digits.
 __global__ __launch_bounds__(128) void tl1_xprep_kernel(XprepArgs a) {
     __shared__ float red[2];
-    __shared__ int dsum[2][kPlanes];
+    __shared__ int xsum[2];
     const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
     const int k = g * 128 + t;
     const float x = (c < a.ncols && k < a.K) ? a.x[static_cast<long long>(c) * a.K + k] : 0.f;
@@ -146,26 +148,22 @@ __global__ __launch_bounds__(128) void tl1_xprep_kernel(XprepArgs a) {
     const int r1 = (xi - p2) >> 8;  // exact: xi - p2 is a multiple of 256
     const int p1 = ((r1 + 128) & 255) - 128;
     const int p0 = (r1 - p1) >> 8;
-    const int dig[kPlanes] = {p0, p1, p2};
+    const int dig[kRowsPerCol] = {p0, p1, p2, 0};
     const int kb = k >> 8, s = (k & 255) >> 6, quarter = (k & 63) >> 4, byte = k & 15;
+    int v = xi;  // the group's sum of x_int (|sum| <= 2^29)
 #pragma unroll
-    for (int p = 0; p < kPlanes; ++p) {
-        int v = dig[p];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
-        if ((t & 63) == 0) dsum[t >> 6][p] = v;
-    }
+    for (int off = 32; off >= 1; off >>= 1) v += xor_shfl(v, off);
+    if ((t & 63) == 0) xsum[t >> 6] = v;
     __syncthreads();
 #pragma unroll
-    for (int p = 0; p < kPlanes; ++p) {
-        const int j = kPlanes * c + p;
-        if (j >= 16 * a.tiles) continue;
+    for (int p = 0; p < kRowsPerCol; ++p) {
+        const int j = kRowsPerCol * c + p;
         const int ct = j >> 4, lane = (j & 15) + 16 * quarter;
         a.xb[((static_cast<long long>(kb) * 4 + s) * a.tiles + ct) * 1024 + lane * 16 + byte] = static_cast<int8_t>(dig[p]);
-        if (t == 0) {
-            a.wt[static_cast<long long>(g) * 16 * a.tiles + j] = (c < a.ncols) ? -ldexpf(1.0f, E - 28 + 8 * (2 - p)) : 0.f;
-            a.sx[static_cast<long long>(g) * 16 * a.tiles + j] = dsum[0][p] + dsum[1][p];
-        }
+    }
+    if (t == 0) {
+        a.wt[static_cast<long long>(g) * 4 * a.tiles + c] = (c < a.ncols) ? ldexpf(1.0f, E - 22) : 0.f;
+        a.sx[static_cast<long long>(g) * 4 * a.tiles + c] = xsum[0] + xsum[1];
     }
 }
 
@@ -173,9 +171,9 @@ struct Tl1MmArgs {
     const v4u *w;        // unit layout [nrt][nkb][64] x 16 B (RAW: unused)
     const uint16_t *d;   // [M][G] f16 (RAW: unused)
     const uint8_t *raw;  // RAW: the reference's row-major groups of 28 bytes
-    const int8_t *xb;    // B fragments
-    const float *wt;     // [G][16 tiles]
-    const int32_t *sx;   // [G][16 tiles] digit sums (RAW)
+    const int8_t *xb;    // A fragments
+    const float *wt;     // [G][4 tiles]
+    const int32_t *sx;   // [G][4 tiles] sums of x_int (RAW)
     float *y;            // [ncols][M]
     int M, nkb, G, tiles, ncols, nrb, graw;  // graw: groups of a raw row (K / 128)
 };
@@ -204,31 +202,30 @@ __device__ __forceinline__ uint32_t digits4(uint32_t S, uint32_t me, uint32_t mo
 
 // Workgroup: 4 wavefronts along the rows, wavefront w owns row tiles
 // (4 rb + w) WR .. +WR-1 and all WC column tiles.  Per 256-deep k block the
-// workgroup stages the block's 4 WC B pieces in LDS (double-buffered,
+// workgroup stages the block's 4 WC A pieces of x in LDS (double-buffered,
 // prefetched a block ahead in registers) and each wavefront loads its WR
 // weight units and their scales a block ahead.  Indices are clamped, so
 // every load is unconditional.
 //
 // RAW: the weights are the reference's row-major payload.  Lane l loads the
 // 28 bytes of group g of row 16 rt + l%16 (one 16- and one 12-byte load) and
-// makes its A fragment of each step from them: the base-3 digit (0..2) of
+// makes its B fragment of each step from them: the base-3 digit (0..2) of
 // every element, elements 16 (l/16) .. +15 of the step's half group in the
 // payload's order (qs bytes 0..15 carry elements 16 n + m, bytes 16..23
 // elements 80 + 8 n + m, bytes 24, 25 elements 120 + 2 n + h).  The MFMA
-// then sums digit * x_p; the trit sum is that minus the group's digit sum of
-// the B column (exact integers), and the group scale d comes from bytes 26,
-// 27, moved to the lanes of the D rows by a lane shuffle.
+// then sums digit * x; the trit sum is that minus the group's sum of x_int
+// (exact integers), and the group scale d comes from bytes 26, 27 of the
+// lane's own row.
 template <int WR, int WC, bool RAW>
 __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     constexpr int kPiece = 1024;
     __shared__ __attribute__((aligned(16))) int8_t xs[2][4 * WC * kPiece];
-    __shared__ float comb[kWaves][16][16 * WC + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rt0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * WR;
     const int nrt = (a.M + 15) / 16;
     const int q = lane >> 4;
 
-    // RAW: per-lane digit multipliers of the odd steps' four A dwords (the
+    // RAW: per-lane digit multipliers of the odd steps' four B dwords (the
     // even steps take digit q of qs bytes 0..15: 3^q in both halves)
     uint32_t m_even = 0, me1[4] = {0, 0, 0, 0}, mo1[4] = {0, 0, 0, 0};
     if constexpr (RAW) {
@@ -261,17 +258,17 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
 #pragma unroll
         for (int i = 0; i < WC; ++i) *reinterpret_cast<v4u *>(&xs[buf][16 * (tid + kWave * kWaves * i)]) = xr[i];
     };
-    // unit layout: the lane's word of each step and the f16 scales of its 4 D
-    // rows for the block's two groups; RAW: the 7 dwords of its row's groups
+    // unit layout: the lane's word of each step and the f16 scales of its row
+    // for the block's two groups; RAW: the 7 dwords of its row's groups
     v4u wr[WR];
-    uint32_t dr[WR][4];
+    uint32_t dr[WR];
     uint32_t rr[WR][2][7];
     auto load_w = [&](int kb) {
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
             const int rt = min(rt0 + r, nrt - 1);
+            const long long row = min(rt * 16 + (lane & 15), a.M - 1);
             if constexpr (RAW) {
-                const long long row = min(rt * 16 + (lane & 15), a.M - 1);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int g = min(2 * kb + h, a.graw - 1);  // the padding group loads a real one, d = 0 below
@@ -283,22 +280,16 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
                 }
             } else {
                 wr[r] = a.w[(static_cast<long long>(rt) * a.nkb + kb) * kWave + lane];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int row = min(rt * 16 + 4 * (lane >> 4) + e, a.M - 1);
-                    dr[r][e] = *reinterpret_cast<const uint32_t *>(a.d + static_cast<long long>(row) * a.G + 2 * kb);
-                }
+                dr[r] = *reinterpret_cast<const uint32_t *>(a.d + row * a.G + 2 * kb);
             }
         }
     };
 
-    float yacc[WR][WC][4];
+    float yacc[WR][WC];
 #pragma unroll
     for (int r = 0; r < WR; ++r)
 #pragma unroll
-        for (int c = 0; c < WC; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) yacc[r][c][e] = 0.f;
+        for (int c = 0; c < WC; ++c) yacc[r][c] = 0.f;
 
     load_x(0);
     load_w(0);
@@ -306,7 +297,7 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     __syncthreads();
     for (int kb = 0; kb < a.nkb; ++kb) {
         v4u wc[WR];
-        uint32_t dc[WR][4];
+        uint32_t dc[WR];
         uint32_t rc[WR][2][7];
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
@@ -317,8 +308,7 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
                     for (int i = 0; i < 7; ++i) rc[r][h][i] = rr[r][h][i];
             } else {
                 wc[r] = wr[r];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dc[r][e] = dr[r][e];
+                dc[r] = dr[r];
             }
         }
         const bool more = kb + 1 < a.nkb;
@@ -338,7 +328,7 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
                 const int s = 2 * half + s2;
-                v4i A[WR];
+                v4i Bw[WR];
 #pragma unroll
                 for (int r = 0; r < WR; ++r) {
                     if constexpr (RAW) {
@@ -355,92 +345,75 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
 #pragma unroll
                             for (int dw = 0; dw < 4; ++dw) d4[dw] = digits4(src[dw], me1[dw], mo1[dw]);
                         }
-                        A[r] = v4i{static_cast<int>(d4[0]), static_cast<int>(d4[1]), static_cast<int>(d4[2]),
-                                   static_cast<int>(d4[3])};
+                        Bw[r] = v4i{static_cast<int>(d4[0]), static_cast<int>(d4[1]), static_cast<int>(d4[2]),
+                                    static_cast<int>(d4[3])};
                     } else {
                         const uint32_t wd = s == 0 ? wc[r][0] : s == 1 ? wc[r][1] : s == 2 ? wc[r][2] : wc[r][3];
-                        A[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
-                                   static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
+                        Bw[r] = v4i{static_cast<int>((wd << 6) & 0xC0C0C0C0u), static_cast<int>((wd << 4) & 0xC0C0C0C0u),
+                                    static_cast<int>((wd << 2) & 0xC0C0C0C0u), static_cast<int>(wd & 0xC0C0C0C0u)};
                     }
                 }
 #pragma unroll
                 for (int c = 0; c < WC; ++c) {
-                    const v4i B = *reinterpret_cast<const v4i *>(xbuf + (s * WC + c) * kPiece);
+                    const v4i Ax = *reinterpret_cast<const v4i *>(xbuf + (s * WC + c) * kPiece);
 #pragma unroll
                     for (int r = 0; r < WR; ++r)
-                        acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[r], B, acc[r][c], 0, 0, 0);
+                        acc[r][c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Ax, Bw[r], acc[r][c], 0, 0, 0);
                 }
             }
-            // the group's term: d(row) * w(g, column) * trit sum
+            // the group's term: d(row) 2^(E-22) T, T = sum_k trit x_int from the
+            // three plane sums (D rows 4 q + p of the lane)
 #pragma unroll
             for (int r = 0; r < WR; ++r) {
-                float dv[4];
+                float dv;
                 if constexpr (RAW) {
-                    // d of the lane's A row, then of its 4 D rows (lane 4 (l/16) + e holds row 4 (l/16) + e)
-                    const float own = 2 * kb + half < a.graw
+                    dv = g < a.graw
                         ? static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(rc[r][half][6] >> 16)))
                         : 0.f;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) dv[e] = __shfl(own, 4 * (lane >> 4) + e, 64);
                 } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint16_t db = static_cast<uint16_t>(half ? dc[r][e] >> 16 : dc[r][e] & 0xffffu);
-                        dv[e] = static_cast<float>(__builtin_bit_cast(_Float16, db));
-                    }
+                    dv = static_cast<float>(
+                        __builtin_bit_cast(_Float16, static_cast<uint16_t>(half ? dc[r] >> 16 : dc[r] & 0xffffu)));
                 }
 #pragma unroll
                 for (int c = 0; c < WC; ++c) {
-                    const long long wi = static_cast<long long>(g) * 16 * a.tiles + 16 * c + (lane & 15);
-                    const float wv = RAW ? -64.f * a.wt[wi] : a.wt[wi];
-                    const int corr = RAW ? a.sx[wi] : 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        yacc[r][c][e] = __builtin_fmaf(static_cast<float>(acc[r][c][e] - corr), dv[e] * wv, yacc[r][c][e]);
+                    const long long wi = static_cast<long long>(g) * 4 * a.tiles + 4 * c + q;
+                    int T;
+                    if constexpr (RAW)  // digit = trit + 1: the digit sum less the group's sum of x_int
+                        T = (acc[r][c][0] << 16) + (acc[r][c][1] << 8) + acc[r][c][2] - a.sx[wi];
+                    else  // the codes are -64 trit: every plane sum is a multiple of 64
+                        T = -((acc[r][c][0] << 10) + (acc[r][c][1] << 2) + (acc[r][c][2] >> 6));
+                    yacc[r][c] = __builtin_fmaf(static_cast<float>(T), dv * a.wt[wi], yacc[r][c]);
                 }
             }
         }
         if (more) store_x((kb + 1) & 1);
         __syncthreads();
     }
-    // the planes of a column lie in three B columns: add them through LDS,
-    // one row tile at a time (each wavefront its own region)
+    // lane 16 q + r holds row 16 rt + r of columns 4 c + q
 #pragma unroll
     for (int r = 0; r < WR; ++r) {
-        const int rt = rt0 + r;
+        const int rt = rt0 + r, row = rt * 16 + (lane & 15);
 #pragma unroll
-        for (int c = 0; c < WC; ++c)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) comb[wave][4 * (lane >> 4) + e][16 * c + (lane & 15)] = yacc[r][c][e];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        for (int idx = lane; idx < 16 * a.ncols; idx += kWave) {
-            const int rr2 = idx & 15, col = idx >> 4;
-            const float v = comb[wave][rr2][kPlanes * col] + comb[wave][rr2][kPlanes * col + 1] +
-                            comb[wave][rr2][kPlanes * col + 2];
-            const int row = rt * 16 + rr2;
-            if (rt < nrt && row < a.M) a.y[static_cast<long long>(col) * a.M + row] = v;
+        for (int c = 0; c < WC; ++c) {
+            const int col = 4 * c + q;
+            if (rt < nrt && row < a.M && col < a.ncols) a.y[static_cast<long long>(col) * a.M + row] = yacc[r][c];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
 }  // namespace
 
-// Columns one launch handles: 3 B columns each, up to 3 tiles of 16.
+// Columns one launch handles: 4 A rows each, up to 4 tiles of 16.
 constexpr int kTl1MmCols = 16;
 
 size_t tl1_mfma_code_bytes(size_t M, size_t K) { return (M + 15) / 16 * ((K + 255) / 256) * 1024; }
 size_t tl1_mfma_scale_bytes(size_t M, size_t K) { return M * ((K + 255) / 256 * 2) * sizeof(uint16_t); }
-// B fragments and plane weights for up to ncols columns (one launch's share).
+// A fragments and column weights for up to ncols columns (one launch's share).
 size_t tl1_xprep_bytes(size_t K, size_t ncols) {
     const size_t nc = std::min(ncols, static_cast<size_t>(kTl1MmCols));
-    const size_t tiles = (kPlanes * nc + 15) / 16;
+    const size_t tiles = (kRowsPerCol * nc + 15) / 16;
     const size_t nkb = (K + 255) / 256;
-    return nkb * 4 * tiles * 1024 + nkb * 2 * 16 * tiles * (sizeof(float) + sizeof(int32_t));
+    return nkb * 4 * tiles * 1024 + nkb * 2 * 4 * tiles * (sizeof(float) + sizeof(int32_t));
 }
 
 namespace {
@@ -488,29 +461,34 @@ int tl1_mfma_run(const uint8_t *codes, const uint16_t *scales, const uint8_t *ra
     const int nkb = static_cast<int>((K + 255) / 256);
     for (size_t c0 = 0; c0 < ncols; c0 += kTl1MmCols) {
         const int nc = static_cast<int>(std::min(ncols - c0, static_cast<size_t>(kTl1MmCols)));
-        const int tiles = (kPlanes * nc + 15) / 16;
+        const int tiles = (kRowsPerCol * nc + 15) / 16;
         int8_t *xb = static_cast<int8_t *>(scratch);
         float *wt = reinterpret_cast<float *>(xb + static_cast<size_t>(nkb) * 4 * tiles * 1024);
-        int32_t *sx = reinterpret_cast<int32_t *>(wt + static_cast<size_t>(nkb) * 2 * 16 * tiles);
+        int32_t *sx = reinterpret_cast<int32_t *>(wt + static_cast<size_t>(nkb) * 2 * 4 * tiles);
         XprepArgs xa{x + c0 * K, xb, wt, sx, static_cast<int>(K), 2 * nkb, tiles, nc};
-        const int vcols = (16 * tiles + kPlanes - 1) / kPlanes;  // virtual columns cover every B column
+        const int vcols = 4 * tiles;  // virtual columns cover every A row
         hipLaunchKernelGGL(tl1_xprep_kernel, dim3(2 * nkb, vcols), dim3(128), 0, s, xa);
         int st = check_launch("tl1_xprep_kernel");
         if (st) return st;
         Tl1MmArgs a{reinterpret_cast<const v4u *>(codes), scales, raw, xb, wt, sx, y + c0 * M, static_cast<int>(M), nkb,
                     2 * nkb, tiles, nc, 0, static_cast<int>(K / 128)};
         const int nrt = static_cast<int>((M + 15) / 16);
-        constexpr int WR = 2;
-        a.nrb = (nrt + kWaves * WR - 1) / (kWaves * WR);
+        // the raw payload's digit decode fills the registers: one row tile a
+        // wavefront there (184 against 219 us at 8 columns of 248320x5120),
+        // two on the unit layout (102 against 116 us)
+        const int wr = raw ? 1 : 2;
+        a.nrb = (nrt + kWaves * wr - 1) / (kWaves * wr);
         const dim3 grid(a.nrb), block(kWave * kWaves);
         if (raw) {
-            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 1, true>), grid, block, 0, s, a);
-            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 2, true>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((tl1_mfma_kernel<WR, 3, true>), grid, block, 0, s, a);
+            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<1, 1, true>), grid, block, 0, s, a);
+            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<1, 2, true>), grid, block, 0, s, a);
+            else if (tiles == 3) hipLaunchKernelGGL((tl1_mfma_kernel<1, 3, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((tl1_mfma_kernel<1, 4, true>), grid, block, 0, s, a);
         } else {
-            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 1, false>), grid, block, 0, s, a);
-            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<WR, 2, false>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((tl1_mfma_kernel<WR, 3, false>), grid, block, 0, s, a);
+            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<2, 1, false>), grid, block, 0, s, a);
+            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<2, 2, false>), grid, block, 0, s, a);
+            else if (tiles == 3) hipLaunchKernelGGL((tl1_mfma_kernel<2, 3, false>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((tl1_mfma_kernel<2, 4, false>), grid, block, 0, s, a);
         }
         st = check_launch("tl1_mfma_kernel");
         if (st) return st;
