@@ -958,8 +958,11 @@ def main() -> int:
         rows = res["kquant"]
         big = [r for r in rows if r["out_len"] == TL1_OUT]
         kind_id = {name: kind for name, kind, _bb, _be in KQ_KINDS}
-        for r in big:  # the lm_head launch of each kind's GEMV (one grid for every kind)
-            r["traffic"] = traffic_of(traffic, f"kq_gemv_kernel<{kind_id[r['kind']]},", 491520)
+        for r in big:  # the lm_head launch of each kind's GEMV
+            if r["kind"] == "Q3_K":  # the matrix-core kernel, 4 workgroups of 256 threads a CU
+                r["traffic"] = traffic_of(traffic, "kq3_mfma_kernel<1>", 262144)
+            else:
+                r["traffic"] = traffic_of(traffic, f"kq_gemv_kernel<{kind_id[r['kind']]},", 491520)
         slow = min(big, key=lambda r: r["GBs"])
         sec["kquant_matvec"] = {
             "value": slow["GBs"], "unit": "GB/s",
