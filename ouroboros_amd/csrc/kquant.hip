@@ -35,8 +35,9 @@
 // are read as the aligned dwords that cover them and shifted into place with
 // v_alignbyte.  Scale bytes are read as bytes.
 //
-// Q3_K rows of up to 64 blocks go to kq3_mfma_kernel instead: the same digit
-// planes, but the products on the int8 matrix cores (see that kernel).
+// Q3_K rows of up to 64 blocks, and Q4_K / Q5_K payloads on a 16-byte
+// boundary, go to kq3_mfma_kernel / kq45_mfma_kernel instead: the same digit
+// planes, but the products on the int8 matrix cores (see those kernels).
 #include "common.hpp"
 
 #include <algorithm>
@@ -893,6 +894,144 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
     }
 }
 
+// ---- Q4_K and Q5_K on the int8 matrix cores ----
+//
+// The scheme of kq3_mfma_kernel with 16-byte-aligned blocks (144 and 176
+// bytes): a step is one block of the wavefront's 16 rows, staged through
+// its LDS area with contiguous 16-byte loads, and every piece is one
+// 16-byte LDS read.  Lane l = 16 g + c takes pair g of row c's block (qs
+// bytes 32 g .. 32 g + 31; Q5_K also the 32 qh bytes), whose runs j are
+// elements 64 g + 16 j: the low nibbles of the pair's first and second 16
+// bytes (sub-block 2 g), then their high nibbles (2 g + 1); Q5_K adds 16
+// for bit 2 g (low) / 2 g + 1 (high) of the run's qh byte.  The codes (0..15
+// or 0..31) are the B operand as they are; with |p0| <= 64 the plane sums
+// combine exactly in int32, and the run adds d s 2^(E-22) U - dmin m X
+// (scale_min_k4, X the run's float sum of x).
+constexpr int kQ45Unit = 4 * kQ3Run + 128;  // a block's planes, then the exponents and the x sums [g][j]
+
+// x's digit planes, exponents and sums of every run (elements 256 b + 64 g + 16 j ..)
+__device__ __forceinline__ void q45_prep(const float *xc, int nb, uint8_t *xlds) {
+    for (int run = threadIdx.x; run < nb * 16; run += blockDim.x) {
+        const int b = run >> 4, g = (run >> 2) & 3, j = run & 3;
+        XRun xr;
+        make_run(xc + 256 * b + 64 * g + 16 * j, xr);
+        uint8_t *xb = xlds + b * kQ45Unit;
+        u32x4 *dst = reinterpret_cast<u32x4 *>(xb + kQ3Run * j + 48 * g);
+        dst[0] = xr.p0;
+        dst[1] = xr.p1;
+        dst[2] = xr.p2;
+        if (g == 0) *reinterpret_cast<u32x4 *>(xb + kQ3Run * j + 192) = u32x4{0u, 0u, 0u, 0u};
+        reinterpret_cast<float *>(xb + 4 * kQ3Run)[4 * g + j] = xr.s;
+        reinterpret_cast<float *>(xb + 4 * kQ3Run + 64)[4 * g + j] = xr.X;
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
+#pragma clang fp contract(off)
+    constexpr bool Q5 = KIND == OURO_KIND_Q5K;
+    constexpr int BB = Q5 ? 176 : 144, NU = BB / 16;  // 16-byte units of a block
+    constexpr int kUnits = 16 * NU, kIns = (kUnits + 63) / 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
+    const int nb = a.in_len / 256;
+    const int col = blockIdx.y;
+    const float *xc = a.x + static_cast<long long>(col) * a.in_len;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
+    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    int tile = blockIdx.x;
+    if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
+    const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
+    const int g8 = gridDim.x;
+    uint8_t *wl = xlds + nb * kQ45Unit + wave * (16 * BB);
+    int urow[kIns], uoff[kIns];
+#pragma unroll
+    for (int i = 0; i < kIns; ++i) {
+        const int id = min(64 * i + lane, kUnits - 1);
+        urow[i] = id / NU;
+        uoff[i] = 16 * (id % NU);
+    }
+    u32x4 st[kIns];
+    auto issue = [&](int t, int b) {
+        const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+#pragma unroll
+        for (int i = 0; i < kIns; ++i) {
+            const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
+            st[i] = *reinterpret_cast<const u32x4 *>(a.w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32 +
+                                                     BB * b + uoff[i]);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < kIns; ++i)
+            if (64 * i + lane < kUnits) *reinterpret_cast<u32x4 *>(wl + BB * urow[i] + uoff[i]) = st[i];
+    };
+    auto finish = [&](float acc, int t) {
+        auto q1 = __builtin_amdgcn_permlane32_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q1[0]) + fbits(q1[1]);
+        auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q2[0]) + fbits(q2[1]);
+        const int row = t * kQ3Rows + 16 * wave + c;
+        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+    };
+    const uint8_t *rl = wl + BB * c;
+    int b = 0;
+    float acc = 0.f;
+    issue(tile, 0);
+    q45_prep(xc, nb, xlds);  // the first loads are in flight meanwhile
+    __syncthreads();
+    for (;;) {
+        stage();
+        issue(b + 1 == nb ? tile + g8 : tile, b + 1 == nb ? 0 : b + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        const u32x4 P = *reinterpret_cast<const u32x4 *>(rl);  // d, dmin, scales[12]
+        const u32x4 q0 = *reinterpret_cast<const u32x4 *>(rl + (Q5 ? 48 : 16) + 32 * g);
+        const u32x4 q1 = *reinterpret_cast<const u32x4 *>(rl + (Q5 ? 64 : 32) + 32 * g);
+        u32x4 h0{}, h1{};
+        if constexpr (Q5) {
+            h0 = *reinterpret_cast<const u32x4 *>(rl + 16);
+            h1 = *reinterpret_cast<const u32x4 *>(rl + 32);
+        }
+        uint32_t s0, m0, s1, m1;
+        scale_min_k4(2 * g, P.y, P.z, P.w, s0, m0);
+        scale_min_k4(2 * g + 1, P.y, P.z, P.w, s1, m1);
+        const uint8_t *xb = xlds + b * kQ45Unit;
+        const float4 xs = *reinterpret_cast<const float4 *>(xb + 4 * kQ3Run + 16 * g);
+        const float4 xx = *reinterpret_cast<const float4 *>(xb + 4 * kQ3Run + 64 + 16 * g);
+        float ad = 0.f, am = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const q3v4i A = *reinterpret_cast<const q3v4i *>(xb + kQ3Run * j + aoff);
+            const u32x4 &q = (j & 1) ? q1 : q0;
+            q3v4i Bc;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t v = (j < 2 ? q[d] : q[d] >> 4) & 0x0f0f0f0fu;
+                if constexpr (Q5) {
+                    const uint32_t hv = (j & 1) ? h1[d] : h0[d];
+                    v |= __builtin_amdgcn_alignbit(hv, hv, static_cast<uint32_t>(2 * g + (j >> 1) - 4) & 31u) & 0x10101010u;
+                }
+                Bc[d] = static_cast<int>(v);
+            }
+            const q3v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bc, q3v4i{0, 0, 0, 0}, 0, 0, 0);
+            const int U = (D[0] << 16) + (D[1] << 8) + D[2];
+            const float xsj = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
+            const float xxj = j == 0 ? xx.x : j == 1 ? xx.y : j == 2 ? xx.z : xx.w;
+            ad = __builtin_fmaf(static_cast<float>(j < 2 ? s0 : s1), xsj * static_cast<float>(U), ad);
+            am = __builtin_fmaf(static_cast<float>(j < 2 ? m0 : m1), xxj, am);
+        }
+        acc += f16f(P.x & 0xffffu) * ad - f16f(P.x >> 16) * am;
+        if (++b == nb) {
+            finish(acc, tile);
+            acc = 0.f;
+            b = 0;
+            tile += g8;
+        }
+        if (tile >= tiles) break;
+    }
+}
+
 // Rows per slot per tile (two tiles' loads in flight): measured best over
 // 248320x5120 and 6912x2560 (R = 1, 2, 4), with workgroups of at most 256
 // threads (384- and 512-thread caps were 10-60 % slower).
@@ -938,6 +1077,17 @@ template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     const bool ph = a.row_bytes % 4 == 0;
     using F = Fmt<KIND>;
+    if constexpr (KIND == OURO_KIND_Q4K || KIND == OURO_KIND_Q5K) {
+        // the matrix-core kernel on a 16-byte-aligned payload (every block and row then is)
+        const int nb = a.in_len / 256;
+        const size_t lds = static_cast<size_t>(nb) * kQ45Unit + kQ3Waves * 16 * F::BB;
+        if (al16 && lds <= 65536) {
+            const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+            const dim3 grid(std::min(tiles, cu_count() * 4), k);
+            hipLaunchKernelGGL(kq45_mfma_kernel<KIND>, grid, dim3(kQ3Threads), lds, s, a);
+            return check_launch("kq45_mfma_kernel");
+        }
+    }
     if constexpr (KIND == OURO_KIND_Q3K) {
         const int nb = a.in_len / 256;
         if (nb <= kQ3MaxBlocks) {
