@@ -216,10 +216,18 @@ __device__ __forceinline__ uint32_t digits4(uint32_t S, uint32_t me, uint32_t mo
 // then sums digit * x; the trit sum is that minus the group's sum of x_int
 // (exact integers), and the group scale d comes from bytes 26, 27 of the
 // lane's own row.
-template <int WR, int WC, bool RAW>
+template <int WR, int WC, bool RAW, bool STG = false>
 __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
     constexpr int kPiece = 1024;
     __shared__ __attribute__((aligned(16))) int8_t xs[2][4 * WC * kPiece];
+    // STG (RAW, one row tile a wavefront, groups a row a multiple of 4, the
+    // payload 16-byte aligned): each wavefront copies its 16 rows' 112
+    // contiguous bytes of two k blocks (four groups) into its own LDS rows
+    // with contiguous 16-byte loads, instead of each lane loading its row's
+    // groups (a 16-lane quarter of a load then reads 16 rows).  Rows lie 144
+    // bytes apart, so a dword read of the 16 rows hits each bank at most twice
+    // (128 bytes apart they all fell in one bank: twice as slow).
+    __shared__ __attribute__((aligned(16))) uint8_t wst[STG ? kWaves : 1][STG ? 16 * 144 : 16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rt0 = (static_cast<int>(blockIdx.x) * kWaves + wave) * WR;
     const int nrt = (a.M + 15) / 16;
@@ -291,17 +299,50 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
 #pragma unroll
         for (int c = 0; c < WC; ++c) yacc[r][c] = 0.f;
 
+    v4u sg[2];
+    const int rowt = min(rt0, nrt - 1) * 16;
+    auto issue_seg = [&](int pair) {
+        const int pc = min(pair, a.nkb / 2 - 1);  // past the last pair: loaded again, never staged
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int id = min(64 * i + lane, 111);
+            const long long row = min(rowt + id / 7, a.M - 1);
+            sg[i] = *reinterpret_cast<const v4u *>(a.raw + row * (static_cast<long long>(a.graw) * 28) + 112LL * pc +
+                                                   16 * (id % 7));
+        }
+    };
+    auto stage_seg = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int id = 64 * i + lane;
+            if (id < 112) *reinterpret_cast<v4u *>(&wst[wave][144 * (id / 7) + 16 * (id % 7)]) = sg[i];
+        }
+    };
+
     load_x(0);
-    load_w(0);
+    if constexpr (STG) issue_seg(0);
+    else load_w(0);
     store_x(0);
     __syncthreads();
     for (int kb = 0; kb < a.nkb; ++kb) {
         v4u wc[WR];
         uint32_t dc[WR];
         uint32_t rc[WR][2][7];
+        if constexpr (STG) {
+            if ((kb & 1) == 0) {  // uniform
+                stage_seg();
+                issue_seg(kb / 2 + 1);
+            }
+            const uint8_t *gp = &wst[wave][144 * (lane & 15) + 56 * (kb & 1)];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 7; ++i) rc[0][h][i] = *reinterpret_cast<const uint32_t *>(gp + 28 * h + 4 * i);
+        }
 #pragma unroll
         for (int r = 0; r < WR; ++r) {
-            if constexpr (RAW) {
+            if constexpr (STG) {
+            } else if constexpr (RAW) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -314,7 +355,7 @@ __global__ __launch_bounds__(kWave *kWaves) void tl1_mfma_kernel(Tl1MmArgs a) {
         const bool more = kb + 1 < a.nkb;
         if (more) {
             load_x(kb + 1);
-            load_w(kb + 1);
+            if constexpr (!STG) load_w(kb + 1);
         }
         const int8_t *xbuf = xs[kb & 1] + 16 * lane;
 #pragma unroll
@@ -479,7 +520,12 @@ int tl1_mfma_run(const uint8_t *codes, const uint16_t *scales, const uint8_t *ra
         const int wr = raw ? 1 : 2;
         a.nrb = (nrt + kWaves * wr - 1) / (kWaves * wr);
         const dim3 grid(a.nrb), block(kWave * kWaves);
-        if (raw) {
+        if (raw && a.graw % 4 == 0 && reinterpret_cast<uintptr_t>(raw) % 16 == 0) {
+            if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<1, 1, true, true>), grid, block, 0, s, a);
+            else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<1, 2, true, true>), grid, block, 0, s, a);
+            else if (tiles == 3) hipLaunchKernelGGL((tl1_mfma_kernel<1, 3, true, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((tl1_mfma_kernel<1, 4, true, true>), grid, block, 0, s, a);
+        } else if (raw) {
             if (tiles == 1) hipLaunchKernelGGL((tl1_mfma_kernel<1, 1, true>), grid, block, 0, s, a);
             else if (tiles == 2) hipLaunchKernelGGL((tl1_mfma_kernel<1, 2, true>), grid, block, 0, s, a);
             else if (tiles == 3) hipLaunchKernelGGL((tl1_mfma_kernel<1, 3, true>), grid, block, 0, s, a);
