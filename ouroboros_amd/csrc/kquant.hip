@@ -1035,6 +1035,156 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
     }
 }
 
+// ---- Q6_K on the int8 matrix cores ----
+//
+// ql[128], qh[64], scales int8[16], d (dequant.rs:484-510).  Lane l = 16 g + c
+// takes half n = g / 2, bytes l0 = 16 (g % 2) .. l0 + 15 of row c's block: ql
+// at 64 n + l0 and 64 n + 32 + l0, qh at 128 + 32 n + l0; its run j is
+// elements 128 n + 32 j + l0 (the places of Q3_K's runs): the low nibbles of
+// the first / second ql piece (j = 0, 1), then their high nibbles, with bits
+// 2j, 2j + 1 of the qh byte below them, scale 8 n + g % 2 + 2 j.  The B slice
+// holds 4 (code - 32) as int8: the nibble at bits 2-5, the high bits at 6-7
+// with the top one inverted; the plane sums are combined in fp32 (in int32
+// they could reach 2^31).  With the payload and rows dword-aligned a step is
+// two blocks (an even block on a dword, an odd one 2 bytes past one): each
+// wavefront stages its 16 rows' 420-byte step segments at their natural
+// offsets in its LDS rows (26 sixteen-byte units and one dword a row, rows 432
+// bytes apart: 16-byte reads of 8 consecutive rows fall in distinct banks).
+// The even block's pieces are single 16-byte reads; an odd block's piece
+// starts 2 bytes past a 16-byte boundary: its bytes 0..13 are bytes 2..15 of
+// the 16-byte read there, its bytes 14, 15 come from the dword that follows
+// and replace the low half of the first dword (elements 14, 15, 0, .., 13,
+// the order the odd blocks' x planes are stored in).
+constexpr int kQ6Pitch = 432;  // LDS bytes of a staged row (420 used)
+
+template <int PAR>  // 0: the step's even block, 1: its odd block
+__device__ __forceinline__ float q6_block(const uint8_t *rl, const uint8_t *xb, int aoff, int n, int h, int g) {
+#pragma clang fp contract(off)
+    constexpr int B0 = PAR ? 210 : 0;  // the block's first byte in the LDS row
+    u32x4 l0v, l1v, qh;
+    uint2 sc;
+    float d;
+    if constexpr (PAR == 0) {
+        l0v = *reinterpret_cast<const u32x4 *>(rl + 64 * n + 16 * h);
+        l1v = *reinterpret_cast<const u32x4 *>(rl + 64 * n + 32 + 16 * h);
+        qh = *reinterpret_cast<const u32x4 *>(rl + 128 + 32 * n + 16 * h);
+        sc = *reinterpret_cast<const uint2 *>(rl + 192 + 8 * n);
+        d = f16f(*reinterpret_cast<const uint16_t *>(rl + 208));
+    } else {
+        // a piece at block offset o (LDS 210 + o): bytes 0..13 from the 16-byte
+        // read at 208 + o, bytes 14, 15 from the low half of the dword at 224 + o
+        auto piece = [&](int o) {
+            u32x4 r = *reinterpret_cast<const u32x4 *>(rl + 208 + o);
+            const uint32_t nx = *reinterpret_cast<const uint32_t *>(rl + 224 + o);
+            r.x = (r.x & 0xffff0000u) | (nx & 0xffffu);  // [. . b0 b1] -> [b14 b15 b0 b1]
+            return r;
+        };
+        l0v = piece(64 * n + 16 * h);
+        l1v = piece(64 * n + 32 + 16 * h);
+        qh = piece(128 + 32 * n + 16 * h);
+        // scale bytes 8n .. 8n + 7: block 192 + 8n .., LDS 402 + 8n .. (2 bytes past a dword)
+        const uint32_t s0 = *reinterpret_cast<const uint32_t *>(rl + 400 + 8 * n);
+        const uint32_t s1 = *reinterpret_cast<const uint32_t *>(rl + 404 + 8 * n);
+        const uint32_t s2 = *reinterpret_cast<const uint32_t *>(rl + 408 + 8 * n);
+        sc.x = __builtin_amdgcn_alignbyte(s1, s0, 2);
+        sc.y = __builtin_amdgcn_alignbyte(s2, s1, 2);
+        d = f16f(*reinterpret_cast<const uint16_t *>(rl + B0 + 208));
+    }
+    const float4 xs = *reinterpret_cast<const float4 *>(xb + 4 * kQ3Run + 16 * g);
+    float blk = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const q3v4i A = *reinterpret_cast<const q3v4i *>(xb + kQ3Run * j + aoff);
+        const u32x4 &ql = (j & 1) ? l1v : l0v;
+        q3v4i Bc;
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            const uint32_t lo = (j < 2 ? ql[dw] << 2 : ql[dw] >> 2) & 0x3c3c3c3cu;
+            const uint32_t hi = __builtin_amdgcn_alignbit(qh[dw], qh[dw], static_cast<uint32_t>(2 * j - 6) & 31u) & 0xc0c0c0c0u;
+            Bc[dw] = static_cast<int>((lo | hi) ^ 0x80808080u);
+        }
+        const q3v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bc, q3v4i{0, 0, 0, 0}, 0, 0, 0);
+        // 4 (65536 S0 + 256 S1 + S2): each plane sum a multiple of 4
+        const float U = __builtin_fmaf(static_cast<float>(D[0]), 16384.f, static_cast<float>((D[1] << 6) + (D[2] >> 2)));
+        const int scj = __builtin_amdgcn_sbfe(static_cast<int>(j < 2 ? sc.x : sc.y), 8 * h + 16 * (j & 1), 8);
+        const float xsj = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
+        blk = __builtin_fmaf(static_cast<float>(scj), xsj * U, blk);
+    }
+    return d * blk;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
+    constexpr int kUnits = 16 * 26, kIns = (kUnits + 63) / 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
+    const int nb = a.in_len / 256, steps = nb / 2;
+    const int col = blockIdx.y;
+    const float *xc = a.x + static_cast<long long>(col) * a.in_len;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4, n = g >> 1, h = g & 1;
+    const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
+    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    int tile = blockIdx.x;
+    if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
+    const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
+    const int g8 = gridDim.x;
+    uint8_t *wl = xlds + nb * kQ3Unit + wave * (16 * kQ6Pitch);
+    int urow[kIns], uoff[kIns];
+#pragma unroll
+    for (int i = 0; i < kIns; ++i) {
+        const int id = min(64 * i + lane, kUnits - 1);
+        urow[i] = id / 26;
+        uoff[i] = 16 * (id % 26);
+    }
+    u32x4 st[kIns];
+    uint32_t tail = 0;  // lanes 0..15: segment bytes 416..419 of row lane
+    auto issue = [&](int t, int s) {
+        const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+        const uint8_t *seg = a.w + 420 * s;
+#pragma unroll
+        for (int i = 0; i < kIns; ++i) {
+            const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
+            st[i] = *reinterpret_cast<const u32x4_a4 *>(seg + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32 + uoff[i]);
+        }
+        const int trow = min(r0 + (lane & 15), a.out_len - 1);
+        tail = *reinterpret_cast<const uint32_t *>(seg + static_cast<uint64_t>(static_cast<uint32_t>(trow)) * rb32 + 416);
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < kIns; ++i)
+            if (64 * i + lane < kUnits) *reinterpret_cast<u32x4 *>(wl + kQ6Pitch * urow[i] + uoff[i]) = st[i];
+        if (lane < 16) *reinterpret_cast<uint32_t *>(wl + kQ6Pitch * lane + 416) = tail;
+    };
+    auto finish = [&](float acc, int t) {
+        auto q1 = __builtin_amdgcn_permlane32_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q1[0]) + fbits(q1[1]);
+        auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q2[0]) + fbits(q2[1]);
+        const int row = t * kQ3Rows + 16 * wave + c;
+        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+    };
+    const uint8_t *rl = wl + kQ6Pitch * c;
+    int s = 0;
+    float acc = 0.f;
+    issue(tile, 0);
+    q3_prep(xc, nb, xlds, 14);  // the first loads are in flight meanwhile
+    __syncthreads();
+    for (;;) {
+        stage();
+        issue(s + 1 == steps ? tile + g8 : tile, s + 1 == steps ? 0 : s + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        acc += q6_block<0>(rl, xlds + 2 * s * kQ3Unit, aoff, n, h, g);
+        acc += q6_block<1>(rl, xlds + (2 * s + 1) * kQ3Unit, aoff, n, h, g);
+        if (++s == steps) {
+            finish(acc, tile);
+            acc = 0.f;
+            s = 0;
+            tile += g8;
+        }
+        if (tile >= tiles) break;
+    }
+}
+
 // Rows per slot per tile (two tiles' loads in flight): measured best over
 // 248320x5120 and 6912x2560 (R = 1, 2, 4), with workgroups of at most 256
 // threads (384- and 512-thread caps were 10-60 % slower).
@@ -1080,6 +1230,17 @@ template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     const bool ph = a.row_bytes % 4 == 0;
     using F = Fmt<KIND>;
+    if constexpr (KIND == OURO_KIND_Q6K) {
+        // dword-aligned payload and rows (nb even): steps of an even and an odd block
+        const int nb = a.in_len / 256;
+        const size_t lds = static_cast<size_t>(nb) * kQ3Unit + kQ3Waves * 16 * kQ6Pitch;
+        if (reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph && lds <= 65536) {
+            const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+            const dim3 grid(std::min(tiles, cu_count() * 3), k);
+            hipLaunchKernelGGL(kq6_mfma_kernel<KIND>, grid, dim3(kQ3Threads), lds, s, a);
+            return check_launch("kq6_mfma_kernel");
+        }
+    }
     if constexpr (KIND == OURO_KIND_Q4K || KIND == OURO_KIND_Q5K) {
         // the matrix-core kernel on a 16-byte-aligned payload (every block and row then is)
         const int nb = a.in_len / 256;

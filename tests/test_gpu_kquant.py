@@ -86,11 +86,14 @@ def test_kquant_lm_head_shape(gpu, orc, margin, kind):
 
 
 @pytest.mark.parametrize("kind", KINDS, ids=lambda k: k.name)
-@pytest.mark.parametrize("offset", [1, 2, 3, 6, 16])
-def test_kquant_misaligned_payload(gpu, orc, margin, kind, offset):
-    """The payload at any byte offset (the reference takes &[u8])."""
-    out_len, in_len = 97, 768
-    rng = np.random.default_rng(offset)
+@pytest.mark.parametrize("offset", [1, 2, 3, 4, 6, 16])
+@pytest.mark.parametrize("in_len", [768, 1024])
+def test_kquant_misaligned_payload(gpu, orc, margin, kind, offset, in_len):
+    """The payload at any byte offset (the reference takes &[u8]); rows of
+    an odd and an even number of blocks (Q6_K rows of an even number of
+    blocks are dword-aligned when the payload is)."""
+    out_len = 97
+    rng = np.random.default_rng(offset + in_len)
     p = kq_payload(rng, kind, out_len, in_len)
     x = rng.standard_normal(in_len).astype(np.float32)
     want = orc.matvec_q(p, int(kind), out_len, in_len, x)
