@@ -35,9 +35,11 @@
 // are read as the aligned dwords that cover them and shifted into place with
 // v_alignbyte.  Scale bytes are read as bytes.
 //
-// Q3_K rows of up to 64 blocks, and Q4_K / Q5_K payloads on a 16-byte
-// boundary, go to kq3_mfma_kernel / kq45_mfma_kernel instead: the same digit
-// planes, but the products on the int8 matrix cores (see those kernels).
+// Q3_K rows of up to 64 blocks, Q4_K / Q5_K payloads on a 16-byte boundary
+// and dword-aligned Q6_K rows of an even number of blocks (up to 42) go to
+// kq3_mfma_kernel / kq45_mfma_kernel / kq6_mfma_kernel instead: the same
+// digit planes, but the products on the int8 matrix cores (see those
+// kernels).
 #include "common.hpp"
 
 #include <algorithm>
