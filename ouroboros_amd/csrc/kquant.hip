@@ -646,7 +646,7 @@ constexpr int kQ3Rows = 16 * kQ3Waves;
 constexpr int kQ3MaxBlocks = 64;     // longer rows take the task kernel
 constexpr int kQ3Run = 208;          // LDS bytes of a block's run j: planes [g][p][16], then 16 zero bytes
 constexpr int kQ3Unit = 4 * kQ3Run + 64;  // a block: its four runs' planes, then the exponents [g][j]
-enum { Q3K_ANY = 0, Q3K_ST = 1 };
+enum { Q3K_ANY = 0, Q3K_ST = 1, Q3K_STS = 2 };  // STS: staged, shared 16-row tiles (kq45_mfma_kernel's SH)
 // staged (Q3K_ST): LDS bytes of a row's step segment (220 used); at 240 the
 // 16-byte reads of 8 consecutive lanes (rows c .. c + 7) fall in distinct
 // banks (224, rows 4 apart share them: 2-way conflicts, 2.5 % slower)
@@ -767,6 +767,8 @@ __device__ __forceinline__ void q3_prep(const float *xc, int nb, uint8_t *xlds, 
 
 template <int MODE>
 __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
+    constexpr bool SH = MODE == Q3K_STS;
+    constexpr int RT = SH ? 16 : kQ3Rows;  // rows a tile
     extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
     const int nb = a.in_len / 256;
     const int col = blockIdx.y;
@@ -780,12 +782,13 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) hr[j] = static_cast<uint32_t>(4 * n + j - 7) & 31u;
     const uint32_t L = 8u * (g & 1) + 4u * n;
-    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    const int tiles = (a.out_len + RT - 1) / RT;
+    const int rw = SH ? 0 : 16 * wave;  // the wavefront's first row in a tile
     int tile = blockIdx.x;
     if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
     const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
     auto row_ptr = [&](int t) {
-        const int row = min(min(t, tiles - 1) * kQ3Rows + 16 * wave + c, a.out_len - 1);  // clamped rows are dropped
+        const int row = min(min(t, tiles - 1) * RT + rw + c, a.out_len - 1);  // clamped rows are dropped
         return a.w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32;
     };
     // a row's partial sums over the four pieces, added by two lane swaps;
@@ -795,11 +798,22 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
         acc = fbits(q1[0]) + fbits(q1[1]);
         auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
         acc = fbits(q2[0]) + fbits(q2[1]);
-        const int row = t * kQ3Rows + 16 * wave + c;
-        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        if constexpr (SH) {  // every wavefront, once a tile
+            float(*red)[4][16] = reinterpret_cast<float(*)[4][16]>(xlds + nb * kQ3Unit + kQ3Waves * kQ3Stage);
+            const int par = (t / static_cast<int>(gridDim.x)) & 1;
+            if (g == 0) red[par][wave][c] = acc;
+            __syncthreads();
+            const int row = t * RT + c;
+            if (wave == 0 && g == 0 && row < a.out_len)
+                a.y[static_cast<long long>(col) * a.out_len + row] =
+                    ((red[par][0][c] + red[par][1][c]) + red[par][2][c]) + red[par][3][c];
+        } else {
+            const int row = t * RT + rw + c;
+            if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        }
     };
     const int g8 = gridDim.x;
-    if constexpr (MODE == Q3K_ST) {
+    if constexpr (MODE != Q3K_ANY) {
         // steps of two blocks (nb is even).  Each wavefront stages its 16
         // rows' 220-byte step segments through its own LDS area with
         // contiguous 16-byte loads: 14 units a row, unit 13 read from byte
@@ -817,7 +831,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
         }
         u32x4 st[4];
         auto issue = [&](int t, int s) {
-            const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+            const int r0 = min(t, tiles - 1) * RT + rw;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
@@ -831,17 +845,25 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
                 if (i < 3 || lane < 32) *reinterpret_cast<u32x4 *>(wl + ulds[i]) = st[i];
         };
         const uint8_t *rl = wl + kQ3Pitch * c;
-        int s = 0;
+        // the wavefront's steps of a tile: s0, s0 + ss, .. (STS: wavefronts
+        // with s0 >= steps have none, and only meet the others at the tile's end)
+        const int s0 = SH ? wave : 0, ss = SH ? 4 : 1;
+        const bool any = s0 < steps;
+        int s = s0;
         float acc = 0.f;
-        issue(tile, 0);
+        if (any) issue(tile, s0);
         q3_prep(xc, nb, xlds, 2);  // the first loads are in flight meanwhile
         __syncthreads();
         for (;;) {
-            stage();
-            {
-                const int ns = s + 1 == steps ? 0 : s + 1, nt = s + 1 == steps ? tile + g8 : tile;
-                issue(nt, ns);
+            if (!any) {  // STS only
+                finish(0.f, tile);
+                tile += g8;
+                if (tile >= tiles) break;
+                continue;
             }
+            stage();
+            const bool last = s + ss >= steps;
+            issue(last ? tile + g8 : tile, last ? s0 : s + ss);
             __builtin_amdgcn_sched_barrier(0);
             // even block: segment bytes 0..109 (scale bytes from P byte 0, d at 12)
             Q3Raw e, o;
@@ -861,11 +883,13 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
             o.P.w = zw.y;
             acc += q3_block<0>(e, xlds, 2 * s, aoff, hr, L, g);
             acc += q3_block<1>(o, xlds, 2 * s + 1, aoff, hr, L, g);
-            if (++s == steps) {
+            if (last) {
                 finish(acc, tile);
                 acc = 0.f;
-                s = 0;
+                s = s0;
                 tile += g8;
+            } else {
+                s += ss;
             }
             if (tile >= tiles) break;
         }
@@ -912,6 +936,12 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
 // or 0..31) are the B operand as they are; with |p0| <= 64 the plane sums
 // combine exactly in int32, and the run adds d s 2^(E-22) U - dmin m X
 // (scale_min_k4, X the run's float sum of x).
+//
+// SH (for matrices of few rows): a tile is 16 rows shared by the four
+// wavefronts, wavefront w taking blocks w, w + 4, ..; their partial sums
+// meet in LDS (double-buffered by tile, one barrier a tile) and are added in
+// wavefront order.  Four times the workgroups and a quarter of the serial
+// steps per tile of the 64-row tiles.
 constexpr int kQ45Unit = 4 * kQ3Run + 128;  // a block's planes, then the exponents and the x sums [g][j]
 
 // x's digit planes, exponents and sums of every run (elements 256 b + 64 g + 16 j ..)
@@ -931,10 +961,11 @@ __device__ __forceinline__ void q45_prep(const float *xc, int nb, uint8_t *xlds)
     }
 }
 
-template <int KIND>
+template <int KIND, bool SH>
 __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
 #pragma clang fp contract(off)
     constexpr bool Q5 = KIND == OURO_KIND_Q5K;
+    constexpr int RT = SH ? 16 : kQ3Rows;  // rows a tile
     constexpr int BB = Q5 ? 176 : 144, NU = BB / 16;  // 16-byte units of a block
     constexpr int kUnits = 16 * NU, kIns = (kUnits + 63) / 64;
     extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
@@ -944,12 +975,15 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
     const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
-    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    const int tiles = (a.out_len + RT - 1) / RT;
+    const int rw = SH ? 0 : 16 * wave;  // the wavefront's first row in a tile
     int tile = blockIdx.x;
     if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
     const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
     const int g8 = gridDim.x;
     uint8_t *wl = xlds + nb * kQ45Unit + wave * (16 * BB);
+    // SH: the wavefronts' row sums [tile parity][wavefront][row], after the staging areas
+    float(*red)[4][16] = reinterpret_cast<float(*)[4][16]>(xlds + nb * kQ45Unit + 4 * 16 * BB);
     int urow[kIns], uoff[kIns];
 #pragma unroll
     for (int i = 0; i < kIns; ++i) {
@@ -959,7 +993,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
     }
     u32x4 st[kIns];
     auto issue = [&](int t, int b) {
-        const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+        const int r0 = min(t, tiles - 1) * RT + rw;
 #pragma unroll
         for (int i = 0; i < kIns; ++i) {
             const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
@@ -977,18 +1011,39 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
         acc = fbits(q1[0]) + fbits(q1[1]);
         auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
         acc = fbits(q2[0]) + fbits(q2[1]);
-        const int row = t * kQ3Rows + 16 * wave + c;
-        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        if constexpr (SH) {  // every wavefront, once a tile
+            const int par = (t / g8) & 1;
+            if (g == 0) red[par][wave][c] = acc;
+            __syncthreads();
+            const int row = t * RT + c;
+            if (wave == 0 && g == 0 && row < a.out_len)
+                a.y[static_cast<long long>(col) * a.out_len + row] =
+                    ((red[par][0][c] + red[par][1][c]) + red[par][2][c]) + red[par][3][c];
+        } else {
+            const int row = t * RT + rw + c;
+            if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        }
     };
     const uint8_t *rl = wl + BB * c;
-    int b = 0;
+    // the wavefront's blocks of a tile: b0, b0 + bs, .. (SH: wavefronts with
+    // b0 >= nb have none, and only meet the others at the tile's end)
+    const int b0 = SH ? wave : 0, bs = SH ? 4 : 1;
+    const bool any = b0 < nb;
+    int b = b0;
     float acc = 0.f;
-    issue(tile, 0);
+    if (any) issue(tile, b0);
     q45_prep(xc, nb, xlds);  // the first loads are in flight meanwhile
     __syncthreads();
     for (;;) {
+        if (!any) {  // SH only
+            finish(0.f, tile);
+            tile += g8;
+            if (tile >= tiles) break;
+            continue;
+        }
         stage();
-        issue(b + 1 == nb ? tile + g8 : tile, b + 1 == nb ? 0 : b + 1);
+        const bool last = b + bs >= nb;
+        issue(last ? tile + g8 : tile, last ? b0 : b + bs);
         __builtin_amdgcn_sched_barrier(0);
         const u32x4 P = *reinterpret_cast<const u32x4 *>(rl);  // d, dmin, scales[12]
         const u32x4 q0 = *reinterpret_cast<const u32x4 *>(rl + (Q5 ? 48 : 16) + 32 * g);
@@ -1027,11 +1082,13 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
             am = __builtin_fmaf(static_cast<float>(j < 2 ? m0 : m1), xxj, am);
         }
         acc += f16f(P.x & 0xffffu) * ad - f16f(P.x >> 16) * am;
-        if (++b == nb) {
+        if (last) {
             finish(acc, tile);
             acc = 0.f;
-            b = 0;
+            b = b0;
             tile += g8;
+        } else {
+            b += bs;
         }
         if (tile >= tiles) break;
     }
@@ -1115,9 +1172,10 @@ __device__ __forceinline__ float q6_block(const uint8_t *rl, const uint8_t *xb, 
     return d * blk;
 }
 
-template <int KIND>
+template <int KIND, bool SH>  // SH: the shared 16-row tiles of kq45_mfma_kernel
 __global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
     constexpr int kUnits = 16 * 26, kIns = (kUnits + 63) / 64;
+    constexpr int RT = SH ? 16 : kQ3Rows;  // rows a tile
     extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
     const int nb = a.in_len / 256, steps = nb / 2;
     const int col = blockIdx.y;
@@ -1125,12 +1183,14 @@ __global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4, n = g >> 1, h = g & 1;
     const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
-    const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
+    const int tiles = (a.out_len + RT - 1) / RT;
+    const int rw = SH ? 0 : 16 * wave;  // the wavefront's first row in a tile
     int tile = blockIdx.x;
     if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
     const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
     const int g8 = gridDim.x;
     uint8_t *wl = xlds + nb * kQ3Unit + wave * (16 * kQ6Pitch);
+    float(*red)[4][16] = reinterpret_cast<float(*)[4][16]>(xlds + nb * kQ3Unit + 4 * 16 * kQ6Pitch);
     int urow[kIns], uoff[kIns];
 #pragma unroll
     for (int i = 0; i < kIns; ++i) {
@@ -1141,7 +1201,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
     u32x4 st[kIns];
     uint32_t tail = 0;  // lanes 0..15: segment bytes 416..419 of row lane
     auto issue = [&](int t, int s) {
-        const int r0 = min(t, tiles - 1) * kQ3Rows + 16 * wave;
+        const int r0 = min(t, tiles - 1) * RT + rw;
         const uint8_t *seg = a.w + 420 * s;
 #pragma unroll
         for (int i = 0; i < kIns; ++i) {
@@ -1162,26 +1222,49 @@ __global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
         acc = fbits(q1[0]) + fbits(q1[1]);
         auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
         acc = fbits(q2[0]) + fbits(q2[1]);
-        const int row = t * kQ3Rows + 16 * wave + c;
-        if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        if constexpr (SH) {  // every wavefront, once a tile
+            const int par = (t / g8) & 1;
+            if (g == 0) red[par][wave][c] = acc;
+            __syncthreads();
+            const int row = t * RT + c;
+            if (wave == 0 && g == 0 && row < a.out_len)
+                a.y[static_cast<long long>(col) * a.out_len + row] =
+                    ((red[par][0][c] + red[par][1][c]) + red[par][2][c]) + red[par][3][c];
+        } else {
+            const int row = t * RT + rw + c;
+            if (g == 0 && row < a.out_len) a.y[static_cast<long long>(col) * a.out_len + row] = acc;
+        }
     };
     const uint8_t *rl = wl + kQ6Pitch * c;
-    int s = 0;
+    // the wavefront's steps of a tile: s0, s0 + ss, .. (SH: wavefronts with
+    // s0 >= steps have none, and only meet the others at the tile's end)
+    const int s0 = SH ? wave : 0, ss = SH ? 4 : 1;
+    const bool any = s0 < steps;
+    int s = s0;
     float acc = 0.f;
-    issue(tile, 0);
+    if (any) issue(tile, s0);
     q3_prep(xc, nb, xlds, 14);  // the first loads are in flight meanwhile
     __syncthreads();
     for (;;) {
+        if (!any) {  // SH only
+            finish(0.f, tile);
+            tile += g8;
+            if (tile >= tiles) break;
+            continue;
+        }
         stage();
-        issue(s + 1 == steps ? tile + g8 : tile, s + 1 == steps ? 0 : s + 1);
+        const bool last = s + ss >= steps;
+        issue(last ? tile + g8 : tile, last ? s0 : s + ss);
         __builtin_amdgcn_sched_barrier(0);
         acc += q6_block<0>(rl, xlds + 2 * s * kQ3Unit, aoff, n, h, g);
         acc += q6_block<1>(rl, xlds + (2 * s + 1) * kQ3Unit, aoff, n, h, g);
-        if (++s == steps) {
+        if (last) {
             finish(acc, tile);
             acc = 0.f;
-            s = 0;
+            s = s0;
             tile += g8;
+        } else {
+            s += ss;
         }
         if (tile >= tiles) break;
     }
@@ -1228,6 +1311,27 @@ KqPlan kq_plan(int tpr) {
     return KqPlan{best, (best * tpr + 63) / 64 * 64};
 }
 
+// Tiling of the matrix-core kernels for a matrix of out_len rows whose x
+// planes and staging areas take lds bytes of LDS and whose rows take steps
+// serial steps: 0 the 64-row tiles, 1 the shared 16-row tiles (SH), -1 the
+// task kernel.  With fewer 64-row tiles than CUs each workgroup walks its
+// rows' whole length alone; SH then pays when the 64-row grid would leave
+// over half the CUs idle or a tile is 12 steps or more (else its per-
+// workgroup x planes and barriers cost more than it gains), and where it
+// does not fit in LDS, or below 2048 rows, the task kernel is faster.
+// Measured (us, 64-row tiles -> SH): Q4_K 8192x8192 23.4 -> 11.8,
+// 4096x14336 38.1 -> 15.5, 14336x4096 13.8 -> 10.0, 6912x2560 9.1 -> 6.0;
+// Q3_K / Q6_K 4096x4096 9.0 -> 5.3 / 11.8 -> 7.3, 14336x4096 (8 steps)
+// 10.4 -> 11.1 / 13.5 -> 14.3; 1024x5120 on the task kernel 4.2-5.2.
+constexpr int kShRed = 2 * 4 * 16 * 4;  // LDS bytes of SH's row sums
+int kq_tiling(int out_len, size_t lds, int steps) {
+    if (lds > 65536) return -1;
+    const int t64 = (out_len + kQ3Rows - 1) / kQ3Rows, cus = cu_count();
+    if (t64 >= cus) return 0;
+    if (2 * t64 <= cus || steps >= 12) return out_len >= 2048 && lds + kShRed <= 65536 ? 1 : -1;
+    return 0;
+}
+
 template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     const bool ph = a.row_bytes % 4 == 0;
@@ -1236,10 +1340,15 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         // dword-aligned payload and rows (nb even): steps of an even and an odd block
         const int nb = a.in_len / 256;
         const size_t lds = static_cast<size_t>(nb) * kQ3Unit + kQ3Waves * 16 * kQ6Pitch;
-        if (reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph && lds <= 65536) {
-            const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
-            const dim3 grid(std::min(tiles, cu_count() * 3), k);
-            hipLaunchKernelGGL(kq6_mfma_kernel<KIND>, grid, dim3(kQ3Threads), lds, s, a);
+        const int til = kq_tiling(a.out_len, lds, nb / 2);
+        if (reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph && til >= 0) {
+            if (til == 1) {
+                const dim3 grid(std::min((a.out_len + 15) / 16, cu_count() * 3), k);
+                hipLaunchKernelGGL((kq6_mfma_kernel<KIND, true>), grid, dim3(kQ3Threads), lds + kShRed, s, a);
+            } else {
+                const dim3 grid(std::min((a.out_len + kQ3Rows - 1) / kQ3Rows, cu_count() * 3), k);
+                hipLaunchKernelGGL((kq6_mfma_kernel<KIND, false>), grid, dim3(kQ3Threads), lds, s, a);
+            }
             return check_launch("kq6_mfma_kernel");
         }
     }
@@ -1247,10 +1356,15 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         // the matrix-core kernel on a 16-byte-aligned payload (every block and row then is)
         const int nb = a.in_len / 256;
         const size_t lds = static_cast<size_t>(nb) * kQ45Unit + kQ3Waves * 16 * F::BB;
-        if (al16 && lds <= 65536) {
-            const int tiles = (a.out_len + kQ3Rows - 1) / kQ3Rows;
-            const dim3 grid(std::min(tiles, cu_count() * 4), k);
-            hipLaunchKernelGGL(kq45_mfma_kernel<KIND>, grid, dim3(kQ3Threads), lds, s, a);
+        const int til = kq_tiling(a.out_len, lds, nb);
+        if (al16 && til >= 0) {
+            if (til == 1) {
+                const dim3 grid(std::min((a.out_len + 15) / 16, cu_count() * 4), k);
+                hipLaunchKernelGGL((kq45_mfma_kernel<KIND, true>), grid, dim3(kQ3Threads), lds + kShRed, s, a);
+            } else {
+                const dim3 grid(std::min((a.out_len + kQ3Rows - 1) / kQ3Rows, cu_count() * 4), k);
+                hipLaunchKernelGGL((kq45_mfma_kernel<KIND, false>), grid, dim3(kQ3Threads), lds, s, a);
+            }
             return check_launch("kq45_mfma_kernel");
         }
     }
@@ -1263,10 +1377,20 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
             const dim3 grid(std::min(tiles, cu_count() * 4), k);
             const size_t lds = static_cast<size_t>(nb) * kQ3Unit;
             const size_t lds_st = lds + kQ3Waves * kQ3Stage;
-            if (al && lds_st <= 65536)
+            const int til = al ? kq_tiling(a.out_len, lds_st, nb / 2) : -1;
+            if (til == 1) {
+                const dim3 gs(std::min((a.out_len + 15) / 16, cu_count() * 4), k);
+                hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_STS>, gs, dim3(kQ3Threads), lds_st + kShRed, s, a);
+                return check_launch("kq3_mfma_kernel");
+            }
+            if (til == 0) {
                 hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ST>, grid, dim3(kQ3Threads), lds_st, s, a);
-            else hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ANY>, grid, dim3(kQ3Threads), lds, s, a);
-            return check_launch("kq3_mfma_kernel");
+                return check_launch("kq3_mfma_kernel");
+            }
+            if (!al && kq_tiling(a.out_len, lds, nb) == 0) {  // unstaged: each lane loads its own pieces
+                hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ANY>, grid, dim3(kQ3Threads), lds, s, a);
+                return check_launch("kq3_mfma_kernel");
+            }
         }
     }
     a.tpr = a.in_len / F::EPB * F::TPB;

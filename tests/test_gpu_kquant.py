@@ -5,7 +5,7 @@ max|y| <= 1e-5 (the reference's fused-vs-scalar rel 1e-5, ops.rs:800-838;
 rel 1e-3 for matmul, ops.rs:720-750), and per row
 |err| <= 1e-5 |y| + 2e-6 sum_i |w_i x_i| (see close()).  Shapes: the ternary
 layer 6912x2560 and the lm_head probe 248320x5120; misaligned payloads; the
->512-task and >1024-task rows."""
+>512-task and >1024-task rows; each tiling of the matrix-core kernels."""
 import ctypes as C
 
 import numpy as np
@@ -121,8 +121,47 @@ def test_kquant_long_rows(gpu, orc, margin, kind, in_len):
 
 
 @pytest.mark.parametrize("kind", KINDS, ids=lambda k: k.name)
-def test_kquant_matmul_columns(gpu, orc, kind):
-    out_len, in_len, k = 300, 1024, 5
+@pytest.mark.parametrize("out_len,in_len", [(2049, 512), (2100, 768), (3001, 1280), (4100, 4096), (8200, 8192),
+                                             (16399, 512), (16399, 768)])
+def test_kquant_tilings(gpu, orc, margin, kind, out_len, in_len):
+    """Each tiling of the matrix-core kernels: the shared 16-row tiles
+    (2048 <= rows < 64 per CU) with ragged last tiles and rows of 2, 3, 5
+    and 16 blocks (with fewer than four steps some wavefronts have none;
+    5 splits unevenly; 8192-element rows of 16 and 32 steps), and the
+    64-row tiles (16399 rows; Q3_K rows of 3 blocks are not dword-aligned:
+    the unstaged kernel)."""
+    rng = np.random.default_rng(out_len * 7 + in_len + int(kind))
+    p = kq_payload(rng, kind, out_len, in_len)
+    x = rng.standard_normal(in_len).astype(np.float32)
+    want = orc.matvec_q(p, int(kind), out_len, in_len, x)
+    got = ops.matvec_q(p, kind, out_len, in_len, x)
+    check(orc, margin, f"{kind.name} {out_len}x{in_len}", got, want, p, kind, out_len, in_len, x, 1e-5)
+
+
+@pytest.mark.parametrize("kind", KINDS, ids=lambda k: k.name)
+@pytest.mark.parametrize("offset", [2, 4])
+def test_kquant_misaligned_tall(gpu, orc, margin, kind, offset):
+    """Payload offsets on a matrix of the shared 16-row tiles: 4 keeps Q3_K
+    and Q6_K rows dword-aligned (staged), 2 does not."""
+    out_len, in_len = 2100, 1024
+    rng = np.random.default_rng(offset + 99)
+    p = kq_payload(rng, kind, out_len, in_len)
+    x = rng.standard_normal(in_len).astype(np.float32)
+    want = orc.matvec_q(p, int(kind), out_len, in_len, x)
+    buf = DeviceBuffer((p.size + 32,), np.uint8)
+    host = np.zeros(p.size + 32, np.uint8)
+    host[offset:offset + p.size] = p
+    buf.upload(host)
+    xb = DeviceBuffer.from_host(x)
+    y = DeviceBuffer((out_len,), np.float32)
+    call("ouro_matvec_q", buf.ptr + offset, int(kind), out_len, in_len, xb.ptr, y.ptr, None)
+    check(orc, margin, f"{kind.name} tall +{offset}", y.download(), want, p, kind, out_len, in_len, x, 1e-5)
+
+
+@pytest.mark.parametrize("kind", KINDS, ids=lambda k: k.name)
+@pytest.mark.parametrize("out_len", [300, 2100])
+def test_kquant_matmul_columns(gpu, orc, kind, out_len):
+    in_len, k = 1024, 5
     rng = np.random.default_rng(7)
     p = kq_payload(rng, kind, out_len, in_len)
     x = rng.standard_normal((k, in_len)).astype(np.float32)
