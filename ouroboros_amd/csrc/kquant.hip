@@ -848,7 +848,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq3_mfma_kernel(KqArgs a) {
         // the wavefront's steps of a tile: s0, s0 + ss, .. (STS: wavefronts
         // with s0 >= steps have none, and only meet the others at the tile's end)
         const int s0 = SH ? wave : 0, ss = SH ? 4 : 1;
-        const bool any = s0 < steps;
+        const bool any = !SH || s0 < steps;
         int s = s0;
         float acc = 0.f;
         if (any) issue(tile, s0);
@@ -1028,7 +1028,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
     // the wavefront's blocks of a tile: b0, b0 + bs, .. (SH: wavefronts with
     // b0 >= nb have none, and only meet the others at the tile's end)
     const int b0 = SH ? wave : 0, bs = SH ? 4 : 1;
-    const bool any = b0 < nb;
+    const bool any = !SH || b0 < nb;
     int b = b0;
     float acc = 0.f;
     if (any) issue(tile, b0);
@@ -1239,7 +1239,7 @@ __global__ __launch_bounds__(kQ3Threads) void kq6_mfma_kernel(KqArgs a) {
     // the wavefront's steps of a tile: s0, s0 + ss, .. (SH: wavefronts with
     // s0 >= steps have none, and only meet the others at the tile's end)
     const int s0 = SH ? wave : 0, ss = SH ? 4 : 1;
-    const bool any = s0 < steps;
+    const bool any = !SH || s0 < steps;
     int s = s0;
     float acc = 0.f;
     if (any) issue(tile, s0);
