@@ -36,10 +36,11 @@
 // v_alignbyte.  Scale bytes are read as bytes.
 //
 // Q3_K rows of up to 64 blocks, Q4_K / Q5_K payloads on a 16-byte boundary
-// and dword-aligned Q6_K rows of an even number of blocks (up to 42) go to
-// kq3_mfma_kernel / kq45_mfma_kernel / kq6_mfma_kernel instead: the same
-// digit planes, but the products on the int8 matrix cores (see those
-// kernels).
+// and dword-aligned Q6_K rows of an even number of blocks (up to 42), in
+// matrices of 2048 rows or more, go to kq3_mfma_kernel / kq45_mfma_kernel /
+// kq6_mfma_kernel instead: the same digit planes, but the products on the
+// int8 matrix cores, in 64-row tiles or, for matrices of few rows, 16-row
+// tiles shared by a workgroup's wavefronts (kq_tiling).
 #include "common.hpp"
 
 #include <algorithm>
