@@ -961,10 +961,10 @@ def main() -> int:
         for r in big:  # the lm_head launch of each kind's GEMV
             if r["kind"] == "Q3_K":  # the matrix-core kernels: workgroups of 256 threads, 4 a CU
                 r["traffic"] = traffic_of(traffic, "kq3_mfma_kernel<1>", 262144)
-            elif r["kind"] in ("Q4_K", "Q5_K"):  # the 64-row tiles at this shape
-                r["traffic"] = traffic_of(traffic, f"kq45_mfma_kernel<{kind_id[r['kind']]}, false>", 262144)
+            elif r["kind"] in ("Q4_K", "Q5_K"):  # the shared 16-row tiles
+                r["traffic"] = traffic_of(traffic, f"kq45_mfma_kernel<{kind_id[r['kind']]}, true>", 262144)
             elif r["kind"] == "Q6_K":  # 3 workgroups a CU
-                r["traffic"] = traffic_of(traffic, "kq6_mfma_kernel<14, false>", 196608)
+                r["traffic"] = traffic_of(traffic, "kq6_mfma_kernel<14, true>", 196608)
             else:
                 r["traffic"] = traffic_of(traffic, f"kq_gemv_kernel<{kind_id[r['kind']]},", 491520)
         slow = min(big, key=lambda r: r["GBs"])

@@ -1315,21 +1315,26 @@ KqPlan kq_plan(int tpr) {
 // Tiling of the matrix-core kernels for a matrix of out_len rows whose x
 // planes and staging areas take lds bytes of LDS and whose rows take steps
 // serial steps: 0 the 64-row tiles, 1 the shared 16-row tiles (SH), -1 the
-// task kernel.  With fewer 64-row tiles than CUs each workgroup walks its
-// rows' whole length alone; SH then pays when the 64-row grid would leave
-// over half the CUs idle or a tile is 12 steps or more (else its per-
-// workgroup x planes and barriers cost more than it gains), and where it
-// does not fit in LDS, or below 2048 rows, the task kernel is faster.
-// Measured (us, 64-row tiles -> SH): Q4_K 8192x8192 23.4 -> 11.8,
-// 4096x14336 38.1 -> 15.5, 14336x4096 13.8 -> 10.0, 6912x2560 9.1 -> 6.0;
-// Q3_K / Q6_K 4096x4096 9.0 -> 5.3 / 11.8 -> 7.3, 14336x4096 (8 steps)
-// 10.4 -> 11.1 / 13.5 -> 14.3; 1024x5120 on the task kernel 4.2-5.2.
+// task kernel.  Q4_K, Q5_K and Q6_K (any_sh) take SH wherever it fits, tall
+// matrices included (248320x5120: 133.1 -> 121.6, 160.6 -> 147.1, 182.7 ->
+// 176.1 us; 16384x5120 Q4_K 17.7 -> 12.6 us).  Q3_K keeps the 64-row tiles
+// (248320x5120 109.7 against 116.4 us with SH) unless they number fewer
+// than the CUs, where each workgroup walks its rows' whole length alone: SH
+// then pays when the 64-row grid would leave over half the CUs idle or a
+// tile is 12 steps or more (14336x4096, 8 steps: 10.4 against 11.1 us with
+// SH; 8192x8192 16.5 -> 11.4; 4096x4096 9.0 -> 5.3).  Where SH does not fit
+// in LDS on a matrix of few rows, and below 2048 rows, the task kernel is
+// faster (Q3_K 4096x14336 20.3 against 26.4 us; 1024x5120 4.2-5.2 against
+// 12.0-13.2 us).  Other Q4_K measurements: 8192x8192 23.4 -> 11.8,
+// 4096x14336 38.1 -> 15.5, 6912x2560 9.1 -> 6.0 us with SH.
 constexpr int kShRed = 2 * 4 * 16 * 4;  // LDS bytes of SH's row sums
-int kq_tiling(int out_len, size_t lds, int steps) {
+int kq_tiling(int out_len, size_t lds, int steps, bool any_sh) {
     if (lds > 65536) return -1;
     const int t64 = (out_len + kQ3Rows - 1) / kQ3Rows, cus = cu_count();
+    const bool sh = out_len >= 2048 && lds + kShRed <= 65536;
+    if (any_sh && sh) return 1;
     if (t64 >= cus) return 0;
-    if (2 * t64 <= cus || steps >= 12) return out_len >= 2048 && lds + kShRed <= 65536 ? 1 : -1;
+    if (any_sh || 2 * t64 <= cus || steps >= 12) return sh ? 1 : -1;
     return 0;
 }
 
@@ -1341,7 +1346,7 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         // dword-aligned payload and rows (nb even): steps of an even and an odd block
         const int nb = a.in_len / 256;
         const size_t lds = static_cast<size_t>(nb) * kQ3Unit + kQ3Waves * 16 * kQ6Pitch;
-        const int til = kq_tiling(a.out_len, lds, nb / 2);
+        const int til = kq_tiling(a.out_len, lds, nb / 2, true);
         if (reinterpret_cast<uintptr_t>(a.w) % 4 == 0 && ph && til >= 0) {
             if (til == 1) {
                 const dim3 grid(std::min((a.out_len + 15) / 16, cu_count() * 3), k);
@@ -1357,7 +1362,7 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
         // the matrix-core kernel on a 16-byte-aligned payload (every block and row then is)
         const int nb = a.in_len / 256;
         const size_t lds = static_cast<size_t>(nb) * kQ45Unit + kQ3Waves * 16 * F::BB;
-        const int til = kq_tiling(a.out_len, lds, nb);
+        const int til = kq_tiling(a.out_len, lds, nb, true);
         if (al16 && til >= 0) {
             if (til == 1) {
                 const dim3 grid(std::min((a.out_len + 15) / 16, cu_count() * 4), k);
@@ -1378,7 +1383,7 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
             const dim3 grid(std::min(tiles, cu_count() * 4), k);
             const size_t lds = static_cast<size_t>(nb) * kQ3Unit;
             const size_t lds_st = lds + kQ3Waves * kQ3Stage;
-            const int til = al ? kq_tiling(a.out_len, lds_st, nb / 2) : -1;
+            const int til = al ? kq_tiling(a.out_len, lds_st, nb / 2, false) : -1;
             if (til == 1) {
                 const dim3 gs(std::min((a.out_len + 15) / 16, cu_count() * 4), k);
                 hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_STS>, gs, dim3(kQ3Threads), lds_st + kShRed, s, a);
@@ -1388,7 +1393,7 @@ int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
                 hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ST>, grid, dim3(kQ3Threads), lds_st, s, a);
                 return check_launch("kq3_mfma_kernel");
             }
-            if (!al && kq_tiling(a.out_len, lds, nb) == 0) {  // unstaged: each lane loads its own pieces
+            if (!al && kq_tiling(a.out_len, lds, nb, false) == 0) {  // unstaged: each lane loads its own pieces
                 hipLaunchKernelGGL(kq3_mfma_kernel<Q3K_ANY>, grid, dim3(kQ3Threads), lds, s, a);
                 return check_launch("kq3_mfma_kernel");
             }

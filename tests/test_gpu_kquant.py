@@ -127,10 +127,23 @@ def test_kquant_tilings(gpu, orc, margin, kind, out_len, in_len):
     """Each tiling of the matrix-core kernels: the shared 16-row tiles
     (2048 <= rows < 64 per CU) with ragged last tiles and rows of 2, 3, 5
     and 16 blocks (with fewer than four steps some wavefronts have none;
-    5 splits unevenly; 8192-element rows of 16 and 32 steps), and the
-    64-row tiles (16399 rows; Q3_K rows of 3 blocks are not dword-aligned:
-    the unstaged kernel)."""
+    5 splits unevenly; 8192-element rows of 16 and 32 steps), and Q3_K's
+    64-row tiles (16399 rows; rows of 3 blocks are not dword-aligned: the
+    unstaged kernel)."""
     rng = np.random.default_rng(out_len * 7 + in_len + int(kind))
+    p = kq_payload(rng, kind, out_len, in_len)
+    x = rng.standard_normal(in_len).astype(np.float32)
+    want = orc.matvec_q(p, int(kind), out_len, in_len, x)
+    got = ops.matvec_q(p, kind, out_len, in_len, x)
+    check(orc, margin, f"{kind.name} {out_len}x{in_len}", got, want, p, kind, out_len, in_len, x, 1e-5)
+
+
+def test_kquant_64_row_tiles(gpu, orc, margin):
+    """Q6_K rows of 42 blocks on a tall matrix: the shared 16-row tiles do
+    not fit in LDS there, the 64-row tiles do (for Q4_K and Q5_K no row
+    length fits the one and not the other)."""
+    kind, out_len, in_len = QuantKind.Q6K, 16399, 10752
+    rng = np.random.default_rng(in_len)
     p = kq_payload(rng, kind, out_len, in_len)
     x = rng.standard_normal(in_len).astype(np.float32)
     want = orc.matvec_q(p, int(kind), out_len, in_len, x)
