@@ -965,6 +965,8 @@ def main() -> int:
                 r["traffic"] = traffic_of(traffic, f"kq45_mfma_kernel<{kind_id[r['kind']]}, true>", 262144)
             elif r["kind"] == "Q6_K":  # 3 workgroups a CU
                 r["traffic"] = traffic_of(traffic, "kq6_mfma_kernel<14, true>", 196608)
+            elif r["kind"] == "Q8_0":
+                r["traffic"] = traffic_of(traffic, "kq8_mfma_kernel", 262144)
             else:
                 r["traffic"] = traffic_of(traffic, f"kq_gemv_kernel<{kind_id[r['kind']]},", 491520)
         slow = min(big, key=lambda r: r["GBs"])

@@ -35,12 +35,13 @@
 // are read as the aligned dwords that cover them and shifted into place with
 // v_alignbyte.  Scale bytes are read as bytes.
 //
-// Q3_K rows of up to 64 blocks, Q4_K / Q5_K payloads on a 16-byte boundary
-// and dword-aligned Q6_K rows of an even number of blocks (up to 42), in
-// matrices of 2048 rows or more, go to kq3_mfma_kernel / kq45_mfma_kernel /
-// kq6_mfma_kernel instead: the same digit planes, but the products on the
-// int8 matrix cores, in 64-row tiles or, for matrices of few rows, 16-row
-// tiles shared by a workgroup's wavefronts (kq_tiling).
+// Q3_K rows of up to 64 blocks, Q4_K / Q5_K payloads on a 16-byte boundary,
+// dword-aligned Q6_K rows of an even number of blocks (up to 42) and Q8_0
+// rows of a multiple of 8 blocks on a 16-byte boundary, in matrices of 2048
+// rows or more, go to kq3_mfma_kernel / kq45_mfma_kernel / kq6_mfma_kernel /
+// kq8_mfma_kernel instead: the same digit planes, but the products on the
+// int8 matrix cores, in 64-row tiles or 16-row tiles shared by a
+// workgroup's wavefronts (kq_tiling).
 #include "common.hpp"
 
 #include <algorithm>
@@ -1095,6 +1096,132 @@ __global__ __launch_bounds__(kQ3Threads) void kq45_mfma_kernel(KqArgs a) {
     }
 }
 
+// ---- Q8_0 on the int8 matrix cores ----
+//
+// d f16, then 32 int8 codes (dequant.rs:225-231).  With the payload on a
+// 16-byte boundary and rows of a multiple of 8 blocks (272 bytes, so every
+// row is on one too) a step is one 256-element chunk, 8 blocks of each of
+// the tile's 16 rows, staged through LDS like kq45_mfma_kernel's blocks, in
+// the shared 16-row tiles.  With q45_prep's x planes, MFMA j gives lane
+// 16 g + c the run of elements 64 g + 16 j: half j % 2 of block
+// 2 g + j / 2 of row c.  Block b of a segment starts at 34 b: the even
+// block of a lane's pair has its codes 2 bytes past a dword (read as the
+// dwords around them and shifted), the odd one on a dword (its d the upper
+// half of the dword before).  The codes are the B operand as they are; the
+// plane sums can pass 2^31 combined, so U is combined in fp32.
+constexpr int kQ8Seg = 272;  // segment bytes of a row (8 blocks)
+
+__global__ __launch_bounds__(kQ3Threads) void kq8_mfma_kernel(KqArgs a) {
+#pragma clang fp contract(off)
+    constexpr int NU = kQ8Seg / 16, kUnits = 16 * NU, kIns = (kUnits + 63) / 64;
+    extern __shared__ __attribute__((aligned(16))) uint8_t xlds[];
+    const int nb = a.in_len / 256;  // steps: 256-element chunks
+    const int col = blockIdx.y;
+    const float *xc = a.x + static_cast<long long>(col) * a.in_len;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int aoff = (c >> 2) == g && (c & 3) < 3 ? 48 * g + 16 * (c & 3) : 192;
+    const int tiles = (a.out_len + 15) / 16;
+    int tile = blockIdx.x;
+    if (tile >= tiles) return;  // the whole workgroup (blockIdx.x is uniform)
+    const uint32_t rb32 = static_cast<uint32_t>(a.row_bytes);
+    const int g8 = gridDim.x;
+    uint8_t *wl = xlds + nb * kQ45Unit + wave * (16 * kQ8Seg);
+    // the wavefronts' row sums [tile parity][wavefront][row], after the staging areas
+    float(*red)[4][16] = reinterpret_cast<float(*)[4][16]>(xlds + nb * kQ45Unit + 4 * 16 * kQ8Seg);
+    int urow[kIns], uoff[kIns];
+#pragma unroll
+    for (int i = 0; i < kIns; ++i) {
+        const int id = min(64 * i + lane, kUnits - 1);
+        urow[i] = id / NU;
+        uoff[i] = 16 * (id % NU);
+    }
+    u32x4 st[kIns];
+    auto issue = [&](int t, int s) {
+        const int r0 = min(t, tiles - 1) * 16;
+#pragma unroll
+        for (int i = 0; i < kIns; ++i) {
+            const int row = min(r0 + urow[i], a.out_len - 1);  // clamped rows are dropped
+            st[i] = *reinterpret_cast<const u32x4 *>(a.w + static_cast<uint64_t>(static_cast<uint32_t>(row)) * rb32 +
+                                                     kQ8Seg * s + uoff[i]);
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < kIns; ++i)
+            if (64 * i + lane < kUnits) *reinterpret_cast<u32x4 *>(wl + kQ8Seg * urow[i] + uoff[i]) = st[i];
+    };
+    auto finish = [&](float acc, int t) {  // every wavefront, once a tile
+        auto q1 = __builtin_amdgcn_permlane32_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q1[0]) + fbits(q1[1]);
+        auto q2 = __builtin_amdgcn_permlane16_swap(ubits(acc), ubits(acc), false, false);
+        acc = fbits(q2[0]) + fbits(q2[1]);
+        const int par = (t / g8) & 1;
+        if (g == 0) red[par][wave][c] = acc;
+        __syncthreads();
+        const int row = t * 16 + c;
+        if (wave == 0 && g == 0 && row < a.out_len)
+            a.y[static_cast<long long>(col) * a.out_len + row] =
+                ((red[par][0][c] + red[par][1][c]) + red[par][2][c]) + red[par][3][c];
+    };
+    // the lane's blocks 2g (codes from segment byte 68 g + 2) and 2g + 1
+    // (d at 68 g + 34, codes from 68 g + 36)
+    const uint32_t *re = reinterpret_cast<const uint32_t *>(wl + kQ8Seg * c + 68 * g);
+    const int s0 = wave;
+    const bool any = s0 < nb;  // wavefronts without steps only meet the others at the tile's end
+    int s = s0;
+    float acc = 0.f;
+    if (any) issue(tile, s0);
+    q45_prep(xc, nb, xlds);  // the first loads are in flight meanwhile
+    __syncthreads();
+    for (;;) {
+        if (!any) {
+            finish(0.f, tile);
+            tile += g8;
+            if (tile >= tiles) break;
+            continue;
+        }
+        stage();
+        const bool last = s + 4 >= nb;
+        issue(last ? tile + g8 : tile, last ? s0 : s + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t w[17];  // the lane's 68 bytes (its two blocks)
+#pragma unroll
+        for (int i = 0; i < 17; ++i) w[i] = re[i];
+        u32x4 ce[2], co[2];  // the even and odd block's codes, halves 0 and 1
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            ce[k >> 2][k & 3] = __builtin_amdgcn_alignbyte(w[k + 1], w[k], 2);
+            co[k >> 2][k & 3] = w[9 + k];
+        }
+        const float de = f16f(w[0] & 0xffffu), dodd = f16f(w[8] >> 16);
+        const uint8_t *xb = xlds + s * kQ45Unit;
+        const float4 xs = *reinterpret_cast<const float4 *>(xb + 4 * kQ3Run + 16 * g);
+        float be = 0.f, bo = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const q3v4i A = *reinterpret_cast<const q3v4i *>(xb + kQ3Run * j + aoff);
+            const u32x4 &q = j < 2 ? ce[j & 1] : co[j & 1];
+            const q3v4i Bc{static_cast<int>(q.x), static_cast<int>(q.y), static_cast<int>(q.z), static_cast<int>(q.w)};
+            const q3v4i D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, Bc, q3v4i{0, 0, 0, 0}, 0, 0, 0);
+            const float U = __builtin_fmaf(static_cast<float>(D[0]), 65536.f, static_cast<float>((D[1] << 8) + D[2]));
+            const float xsj = j == 0 ? xs.x : j == 1 ? xs.y : j == 2 ? xs.z : xs.w;
+            if (j < 2) be = __builtin_fmaf(xsj, U, be);
+            else bo = __builtin_fmaf(xsj, U, bo);
+        }
+        acc += de * be + dodd * bo;
+        if (last) {
+            finish(acc, tile);
+            acc = 0.f;
+            s = s0;
+            tile += g8;
+        } else {
+            s += 4;
+        }
+        if (tile >= tiles) break;
+    }
+}
+
 // ---- Q6_K on the int8 matrix cores ----
 //
 // ql[128], qh[64], scales int8[16], d (dequant.rs:484-510).  Lane l = 16 g + c
@@ -1342,6 +1469,16 @@ template <int KIND>
 int launch_kind(KqArgs a, int k, bool al16, hipStream_t s) {
     const bool ph = a.row_bytes % 4 == 0;
     using F = Fmt<KIND>;
+    if constexpr (KIND == OURO_KIND_Q8_0) {
+        // a 16-byte-aligned payload with rows of a multiple of 8 blocks
+        const int nb = a.in_len / 256;
+        const size_t lds = static_cast<size_t>(nb) * kQ45Unit + kQ3Waves * 16 * kQ8Seg;
+        if (al16 && a.in_len % 256 == 0 && kq_tiling(a.out_len, lds, nb, true) == 1) {
+            const dim3 grid(std::min((a.out_len + 15) / 16, cu_count() * 4), k);
+            hipLaunchKernelGGL(kq8_mfma_kernel, grid, dim3(kQ3Threads), lds + kShRed, s, a);
+            return check_launch("kq8_mfma_kernel");
+        }
+    }
     if constexpr (KIND == OURO_KIND_Q6K) {
         // dword-aligned payload and rows (nb even): steps of an even and an odd block
         const int nb = a.in_len / 256;
@@ -1461,7 +1598,7 @@ int kq_matmul(const void *payload, int kind, size_t out_len, size_t in_len, cons
     const hipStream_t s = as_stream(stream);
     const int kk = static_cast<int>(k);
     switch (kind) {
-    case OURO_KIND_Q8_0: return launch_kind<OURO_KIND_Q8_0>(a, kk, false, s);
+    case OURO_KIND_Q8_0: return launch_kind<OURO_KIND_Q8_0>(a, kk, al16, s);
     case OURO_KIND_Q3K: return launch_kind<OURO_KIND_Q3K>(a, kk, false, s);
     case OURO_KIND_Q4K: return launch_kind<OURO_KIND_Q4K>(a, kk, al16, s);
     case OURO_KIND_Q5K: return launch_kind<OURO_KIND_Q5K>(a, kk, al16, s);
