@@ -138,6 +138,20 @@ def test_kquant_tilings(gpu, orc, margin, kind, out_len, in_len):
     check(orc, margin, f"{kind.name} {out_len}x{in_len}", got, want, p, kind, out_len, in_len, x, 1e-5)
 
 
+def test_q8_0_rows_not_whole_chunks(gpu, orc, margin):
+    """Q8_0 rows of 25 blocks (800 elements: not whole 256-element chunks)
+    on a matrix of the matrix-core row counts: the task kernel; and the same
+    rows with one chunk more (1056 elements: 33 blocks, still not 8k)."""
+    for in_len in (800, 1056):
+        out_len = 2100
+        rng = np.random.default_rng(in_len)
+        p = kq_payload(rng, QuantKind.Q8_0, out_len, in_len)
+        x = rng.standard_normal(in_len).astype(np.float32)
+        want = orc.matvec_q(p, int(QuantKind.Q8_0), out_len, in_len, x)
+        got = ops.matvec_q(p, QuantKind.Q8_0, out_len, in_len, x)
+        check(orc, margin, f"Q8_0 {out_len}x{in_len}", got, want, p, QuantKind.Q8_0, out_len, in_len, x, 1e-5)
+
+
 def test_kquant_64_row_tiles(gpu, orc, margin):
     """Q6_K rows of 42 blocks on a tall matrix: the shared 16-row tiles do
     not fit in LDS there, the 64-row tiles do (for Q4_K and Q5_K no row
